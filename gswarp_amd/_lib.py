@@ -1,0 +1,104 @@
+"""ctypes binding of ``libgswarp_hip.so`` (declared in include/gswarp_hip.h).
+
+The library is the only compute path: if it cannot be loaded, every
+rasterizer call raises ``RuntimeError`` — there is no CPU or eager fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libgswarp_hip.so"
+
+GS_OK = 0
+GS_RECORD_FLOATS = 12
+GS_GRAD_FLOATS = 10
+
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes); must match include/gswarp_hip.h
+SIGNATURES = {
+    "gs_version": (ctypes.c_int, []),
+    "gs_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "gs_preprocess_fwd": (
+        ctypes.c_int,
+        [_i32, _i32, _i32, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _f32, _f32, _f32, _i32, _i32,
+         _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    ),
+    "gs_mark_visible": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp]),
+    "gs_scan_scratch_bytes": (_sz, [_i32]),
+    "gs_scan_tiles": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "gs_num_rendered_readback": (ctypes.c_int, [_vp, _vp, _vp]),
+    "gs_duplicate_keys": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp]),
+    "gs_sort_num_passes": (ctypes.c_int, [_i32]),
+    "gs_sort_scratch_bytes": (_sz, [_i64]),
+    "gs_sort_pairs_u64": (ctypes.c_int, [_i64, _i32, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "gs_tile_ranges": (ctypes.c_int, [_i64, _vp, _i32, _vp, _vp]),
+    "gs_render_fwd": (ctypes.c_int, [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "gs_render_fwd_flow": (
+        ctypes.c_int,
+        [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    ),
+    "gs_render_bwd": (
+        ctypes.c_int, [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp],
+    ),
+    "gs_preprocess_bwd": (
+        ctypes.c_int,
+        [_i32, _i32, _i32, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _f32, _f32, _f32, _f32, _vp, _vp, _vp, _vp, _vp,
+         _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    ),
+}
+
+_lock = threading.Lock()
+_handle = None
+
+
+class _Lib:
+    """Loaded library whose gs_* calls raise RuntimeError on a non-zero status."""
+
+    def __init__(self, handle: ctypes.CDLL):
+        self.handle = handle
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+
+    def status_string(self, status: int) -> str:
+        return self.handle.gs_status_string(int(status)).decode()
+
+    def call(self, name: str, *args):
+        status = getattr(self.handle, name)(*args)
+        if status != GS_OK:
+            raise RuntimeError(f"{name} failed with status {status}: {self.status_string(status)}")
+        return status
+
+    def __getattr__(self, name: str):
+        return getattr(self.handle, name)
+
+
+def load() -> _Lib:
+    """Load the HIP library; raises RuntimeError when it is not built."""
+    global _handle
+    if _handle is None:
+        with _lock:
+            if _handle is None:
+                if not LIB_PATH.exists():
+                    raise RuntimeError(
+                        f"{LIB_PATH.name} is not built; run `python -m gswarp_amd._build` "
+                        "(hipcc, gfx950) before using the rasterizer"
+                    )
+                _handle = _Lib(ctypes.CDLL(str(LIB_PATH)))
+    return _handle
+
+
+def ptr(tensor) -> int | None:
+    """Raw device address of a tensor (None for an absent optional input)."""
+    if tensor is None:
+        return None
+    return tensor.data_ptr()

@@ -1,0 +1,388 @@
+"""Host orchestration of the rasterizer stages on the current HIP stream.
+
+Stage order and semantics follow the reference pipeline
+(gswarp/_internal/methods/pipeline.py:11-45): empty scene -> preprocess ->
+binning -> features -> render -> state, and the manual backward of
+gswarp/_internal/backends/warp/backward_ops.py:376-746 (flow variant:
+flow_ops.py:196-512).  Every stage allocates its tensors with torch on the
+input's device and enqueues the gfx950 kernels through the C ABI on
+``torch.cuda.current_stream(device)``; the only host synchronisation is the
+pair-count readback of the binning stage.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib, _workspace
+from ._coverage import tile_coverage_mode_id
+from ._runtime import BINNING_SORT_MODES, ExecutionOptions
+from ._state import BinningState, ForwardResult, ForwardState, PreprocessOutputs, RenderStageResult
+
+BLOCK_X = 16
+BLOCK_Y = 16
+NUM_CHANNELS = 3
+MAX_BINNING_PAIRS = (1 << 31) - 1
+
+
+@dataclass(slots=True)
+class RasterInputs:
+    """The 18-argument forward tuple of the reference raw ABI, typed."""
+
+    background: torch.Tensor
+    means3d: torch.Tensor
+    colors: torch.Tensor
+    opacities: torch.Tensor
+    scales: torch.Tensor
+    rotations: torch.Tensor
+    scale_modifier: float
+    cov3d_precomp: torch.Tensor
+    viewmatrix: torch.Tensor
+    projmatrix: torch.Tensor
+    tan_fovx: float
+    tan_fovy: float
+    image_height: int
+    image_width: int
+    sh: torch.Tensor
+    degree: int
+    campos: torch.Tensor
+    prefiltered: bool
+
+    @classmethod
+    def from_args(cls, args) -> "RasterInputs":
+        return cls(*args)
+
+
+def validate_pair_count(value: int) -> int:
+    """binning_ops.py:75-81."""
+    if value < 0 or value > MAX_BINNING_PAIRS:
+        raise OverflowError(
+            "binning tile-reference count exceeds signed int32; reduce Gaussian footprint or image size"
+        )
+    return value
+
+
+def grid_dims(width: int, height: int) -> tuple[int, int]:
+    return (width + BLOCK_X - 1) // BLOCK_X, (height + BLOCK_Y - 1) // BLOCK_Y
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _f32c(t: torch.Tensor, align16: bool = False) -> torch.Tensor:
+    t = t.detach()
+    if t.dtype != torch.float32:
+        t = t.to(torch.float32)
+    t = t.contiguous()
+    if align16 and t.numel() and t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+def _focal(size: int, tanfov: float) -> float:
+    return size / (2.0 * tanfov)
+
+
+def empty_forward(inputs: RasterInputs, flow_aux_k: int | None = None) -> ForwardResult:
+    """N == 0: background image and zeros (preprocess_ops.py:45-71, flow_ops.py:62-106)."""
+    device = inputs.means3d.device
+    H, W, n = inputs.image_height, inputs.image_width, inputs.means3d.shape[0]
+    bg = inputs.background.to(device=device, dtype=torch.float32).reshape(NUM_CHANNELS, 1, 1)
+    aux: tuple[torch.Tensor, ...] = ()
+    if flow_aux_k is not None:
+        aux = _empty_flow_aux(flow_aux_k, H, W, device)
+    return ForwardResult(
+        num_rendered=0,
+        color=bg.expand(NUM_CHANNELS, H, W).clone(),
+        depth=torch.zeros((1, H, W), dtype=torch.float32, device=device),
+        alpha=torch.zeros((1, H, W), dtype=torch.float32, device=device),
+        radii=torch.zeros((n,), dtype=torch.int32, device=device),
+        proj_2d=torch.zeros((n, 2), dtype=torch.float32, device=device),
+        conic_2d=torch.zeros((n, 3), dtype=torch.float32, device=device),
+        conic_2d_inv=torch.zeros((n, 3), dtype=torch.float32, device=device),
+        state=None,
+        aux=aux,
+    )
+
+
+def _empty_flow_aux(k: int, H: int, W: int, device) -> tuple[torch.Tensor, ...]:
+    if k <= 0:
+        return (
+            torch.empty((0,), dtype=torch.int32, device=device),
+            torch.empty((0,), dtype=torch.float32, device=device),
+            torch.empty((0,), dtype=torch.float32, device=device),
+        )
+    return (
+        torch.full((k, H, W), -1, dtype=torch.int32, device=device),
+        torch.zeros((k, H, W), dtype=torch.float32, device=device),
+        torch.zeros((2, k, H, W), dtype=torch.float32, device=device),
+    )
+
+
+def preprocess(inputs: RasterInputs, options: ExecutionOptions) -> PreprocessOutputs:
+    """Fused projection / covariance / coverage / SH colour (preprocess_ops.py:289-581)."""
+    if inputs.prefiltered:
+        raise NotImplementedError("prefiltered=True is not supported by the gfx950 preprocess path.")
+    has_cov = inputs.cov3d_precomp.numel() != 0
+    has_sr = inputs.scales.numel() != 0 and inputs.rotations.numel() != 0
+    if has_cov == has_sr:
+        raise ValueError("Provide exactly one of cov3D_precomp or scales/rotations")
+    if has_cov:
+        raise NotImplementedError("the cov3D_precomp input path is not implemented by the gfx950 backend yet")
+    lib = _lib.load()
+    means = inputs.means3d
+    if means.ndim != 2 or means.shape[1] != 3:
+        raise ValueError("means3D must have dimensions (num_points, 3)")
+    device = means.device
+    P = means.shape[0]
+    W, H = inputs.image_width, inputs.image_height
+    f = dict(dtype=torch.float32, device=device)
+    out = PreprocessOutputs(
+        radii=torch.empty((P,), dtype=torch.int32, device=device),
+        depths=torch.empty((P,), **f),
+        proj_2d=torch.empty((P, 2), **f),
+        conic_2d=torch.empty((P, 3), **f),
+        conic_2d_inv=torch.empty((P, 3), **f),
+        tiles_touched=torch.empty((P,), dtype=torch.int32, device=device),
+        records=torch.empty((P, _lib.GS_RECORD_FLOATS), **f),
+        clamped=torch.empty((P,), dtype=torch.uint8, device=device),
+        coverage_mode=tile_coverage_mode_id(options.tile_coverage_mode),
+    )
+    colors = _f32c(inputs.colors) if inputs.colors.numel() != 0 else None
+    shs = None
+    K = 0
+    if colors is None:
+        if inputs.sh.numel() == 0:
+            raise ValueError("provide exactly one of sh or colors_precomp")
+        shs = _f32c(inputs.sh).reshape(P, -1, NUM_CHANNELS)
+        K = shs.shape[1]
+    tanfovx, tanfovy = float(inputs.tan_fovx), float(inputs.tan_fovy)
+    # Locals keep every converted input alive until the launch is enqueued.
+    means_c = _f32c(means)
+    scales_c = _f32c(inputs.scales)
+    rot_c = _f32c(inputs.rotations, align16=True)
+    opac_c = _f32c(inputs.opacities)
+    view_c = _f32c(inputs.viewmatrix)
+    proj_c = _f32c(inputs.projmatrix)
+    campos_c = _f32c(inputs.campos)
+    lib.call(
+        "gs_preprocess_fwd", P, K, int(inputs.degree), means_c.data_ptr(), scales_c.data_ptr(), rot_c.data_ptr(),
+        float(inputs.scale_modifier), opac_c.data_ptr(), _lib.ptr(shs), _lib.ptr(colors), view_c.data_ptr(),
+        proj_c.data_ptr(), campos_c.data_ptr(), tanfovx, tanfovy, _focal(W, tanfovx), _focal(H, tanfovy), W, H,
+        out.coverage_mode, out.radii.data_ptr(), out.depths.data_ptr(), out.proj_2d.data_ptr(),
+        out.conic_2d.data_ptr(), out.conic_2d_inv.data_ptr(), out.tiles_touched.data_ptr(), out.records.data_ptr(),
+        out.clamped.data_ptr(), _stream(device))
+    return out
+
+
+def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options: ExecutionOptions,
+            keep_keys: bool = False) -> BinningState:
+    """Scan, pair-count readback, duplicate-with-keys, 64-bit sort, ranges (binning_ops.py:84-431)."""
+    if options.binning_sort_mode not in BINNING_SORT_MODES:
+        raise ValueError("sort_mode must be one of 'torch', 'warp_radix', or 'warp_depth_stable_tile'")
+    lib = _lib.load()
+    device = pre.radii.device
+    P = pre.radii.shape[0]
+    grid_x, grid_y = grid_dims(image_width, image_height)
+    T = grid_x * grid_y
+    stream = _stream(device)
+    offsets = torch.empty((P,), dtype=torch.int32, device=device)
+    total = torch.empty((1,), dtype=torch.int64, device=device)
+    scan_scratch = torch.empty((max(int(lib.gs_scan_scratch_bytes(P)), 1),), dtype=torch.uint8, device=device)
+    lib.call("gs_scan_tiles", P, pre.tiles_touched.data_ptr(), offsets.data_ptr(), total.data_ptr(),
+             scan_scratch.data_ptr(), scan_scratch.numel(), stream)
+    pinned = _workspace.readback_buffer(device, torch.cuda.current_stream(device))
+    lib.call("gs_num_rendered_readback", total.data_ptr(), pinned.data_ptr(), stream)
+    R = validate_pair_count(int(pinned[0]))
+    if R == 0:
+        return BinningState(grid_x, grid_y, torch.empty((0,), dtype=torch.int32, device=device),
+                            torch.zeros((T, 2), dtype=torch.int32, device=device), 0)
+    keys = torch.empty((R,), dtype=torch.int64, device=device)
+    vals = torch.empty((R,), dtype=torch.int32, device=device)
+    keys_alt = torch.empty((R,), dtype=torch.int64, device=device)
+    vals_alt = torch.empty((R,), dtype=torch.int32, device=device)
+    lib.call("gs_duplicate_keys", P, pre.radii.data_ptr(), pre.records.data_ptr(), pre.conic_2d_inv.data_ptr(),
+             offsets.data_ptr(), image_width, image_height, pre.coverage_mode, R, keys.data_ptr(), vals.data_ptr(),
+             stream)
+    key_bits = 32 + (T - 1).bit_length()
+    sort_scratch = torch.empty((max(int(lib.gs_sort_scratch_bytes(R)), 1),), dtype=torch.uint8, device=device)
+    lib.call("gs_sort_pairs_u64", R, key_bits, keys.data_ptr(), vals.data_ptr(), keys_alt.data_ptr(),
+             vals_alt.data_ptr(), sort_scratch.data_ptr(), sort_scratch.numel(), stream)
+    if lib.gs_sort_num_passes(key_bits) % 2:
+        keys, vals = keys_alt, vals_alt
+    ranges = torch.empty((T, 2), dtype=torch.int32, device=device)
+    lib.call("gs_tile_ranges", R, keys.data_ptr(), T, ranges.data_ptr(), stream)
+    return BinningState(grid_x, grid_y, vals, ranges, R, keys if keep_keys else None)
+
+
+def render(pre: PreprocessOutputs, bins: BinningState, background: torch.Tensor, image_height: int,
+           image_width: int, options: ExecutionOptions, *, flow: bool = False) -> RenderStageResult:
+    """Tile blend (render_ops.py:16-93; flow: flow_ops.py:109-193)."""
+    lib = _lib.load()
+    device = pre.radii.device
+    P = pre.radii.shape[0]
+    H, W = image_height, image_width
+    f = dict(dtype=torch.float32, device=device)
+    bg = _f32c(background.to(device))
+    color = torch.empty((NUM_CHANNELS, H, W), **f)
+    depth = torch.empty((1, H, W), **f)
+    alpha = torch.empty((1, H, W), **f)
+    n_contrib = torch.empty((H * W,), dtype=torch.int32, device=device)
+    aux: tuple[torch.Tensor, ...] = ()
+    write_aux = bool(flow and options.compute_flow_aux)
+    k = int(options.flow_topk or 0) if write_aux else 0
+    if bins.num_rendered == 0:
+        color.copy_(bg.reshape(NUM_CHANNELS, 1, 1).expand_as(color))
+        depth.zero_()
+        alpha.zero_()
+        n_contrib.zero_()
+        if flow:
+            aux = _empty_flow_aux(k, H, W, device)
+        return RenderStageResult(color, depth, alpha, n_contrib, aux)
+    compute_depth = int(bool(options.compute_depth))
+    stream = _stream(device)
+    if flow:
+        if write_aux:
+            aux = (torch.empty((k, H, W), dtype=torch.int32, device=device), torch.empty((k, H, W), **f),
+                   torch.empty((2, k, H, W), **f))
+        else:
+            aux = _empty_flow_aux(0, H, W, device)
+        lib.call("gs_render_fwd_flow", W, H, P, bins.num_rendered, bins.ranges.data_ptr(), bins.point_list.data_ptr(),
+                 pre.records.data_ptr(), bg.data_ptr(), compute_depth, int(write_aux), k, color.data_ptr(),
+                 depth.data_ptr(), alpha.data_ptr(), n_contrib.data_ptr(),
+                 aux[0].data_ptr() if write_aux else None, aux[1].data_ptr() if write_aux else None,
+                 aux[2].data_ptr() if write_aux else None, stream)
+    else:
+        lib.call("gs_render_fwd", W, H, P, bins.num_rendered, bins.ranges.data_ptr(), bins.point_list.data_ptr(), pre.records.data_ptr(),
+                 bg.data_ptr(), compute_depth, color.data_ptr(), depth.data_ptr(), alpha.data_ptr(),
+                 n_contrib.data_ptr(), stream)
+    return RenderStageResult(color, depth, alpha, n_contrib, aux)
+
+
+def forward(inputs: RasterInputs, options: ExecutionOptions, *, flow: bool = False) -> ForwardResult:
+    """One typed forward: the reference's execute_typed_forward (pipeline.py:11-45)."""
+    means = inputs.means3d
+    if means.ndim != 2 or means.shape[1] != 3:
+        raise ValueError("means3D must have dimensions (num_points, 3)")
+    device = means.device
+    with torch.cuda.device(device), _workspace.device_lock(device):
+        if means.shape[0] == 0:
+            k = (options.flow_topk if options.compute_flow_aux else 0) if flow else None
+            return empty_forward(inputs, k)
+        pre = preprocess(inputs, options)
+        bins = binning(pre, inputs.image_height, inputs.image_width, options)
+        res = render(pre, bins, inputs.background, inputs.image_height, inputs.image_width, options, flow=flow)
+    return ForwardResult(
+        num_rendered=bins.num_rendered,
+        color=res.color,
+        depth=res.depth,
+        alpha=res.alpha,
+        radii=pre.radii,
+        proj_2d=pre.proj_2d,
+        conic_2d=pre.conic_2d,
+        conic_2d_inv=pre.conic_2d_inv,
+        state=ForwardState(pre, bins, res.n_contrib),
+        aux=res.aux,
+    )
+
+
+def _zeros_if_none(t: torch.Tensor | None, shape, device) -> torch.Tensor:
+    if t is None:
+        return torch.zeros(shape, dtype=torch.float32, device=device)
+    return _f32c(t)
+
+
+def backward(inputs: RasterInputs, radii: torch.Tensor, alpha: torch.Tensor, grad_color, grad_depth, grad_alpha,
+             grad_proj_2d, grad_conic_2d, grad_conic_2d_inv, options: ExecutionOptions,
+             forward_state: ForwardState | None, *, flow_double: bool = False):
+    """Manual backward -> (grad_means2D, grad_colors, grad_opacities, grad_means3D, grad_cov3D,
+    grad_sh, grad_scales, grad_rotations), the order of backward_ops.py:746."""
+    lib = _lib.load()
+    means = inputs.means3d
+    device = means.device
+    P = means.shape[0]
+    H, W = inputs.image_height, inputs.image_width
+    grad_colors = torch.empty_like(inputs.colors)
+    grad_cov3d = torch.empty_like(inputs.cov3d_precomp)
+    if P == 0:
+        return (torch.zeros((0, 3), dtype=torch.float32, device=device), grad_colors,
+                torch.empty_like(inputs.opacities), torch.zeros_like(means), grad_cov3d,
+                torch.empty_like(inputs.sh), torch.zeros_like(inputs.scales), torch.zeros_like(inputs.rotations))
+    with torch.cuda.device(device), _workspace.device_lock(device):
+        if forward_state is None:
+            # Second backward of a retained graph: rebuild the forward state.
+            pre = preprocess(inputs, options)
+            bins = binning(pre, H, W, options)
+            n_contrib = render(pre, bins, inputs.background, H, W, options).n_contrib
+        else:
+            pre, bins, n_contrib = forward_state.preprocess, forward_state.binning, forward_state.n_contrib
+        stream = _stream(device)
+        grad_gauss = torch.zeros((P, _lib.GS_GRAD_FLOATS), dtype=torch.float32, device=device)
+        if bins.num_rendered != 0:
+            bg = _f32c(inputs.background.to(device))
+            gc = _zeros_if_none(grad_color, (NUM_CHANNELS, H, W), device)
+            gd = _zeros_if_none(grad_depth, (1, H, W), device)
+            ga = _zeros_if_none(grad_alpha, (1, H, W), device)
+            alpha_c = _f32c(alpha)
+            lib.call("gs_render_bwd", W, H, P, bins.num_rendered, bins.ranges.data_ptr(), bins.point_list.data_ptr(),
+                     pre.records.data_ptr(), bg.data_ptr(), alpha_c.data_ptr(), n_contrib.data_ptr(),
+                     gc.data_ptr(), gd.data_ptr(), ga.data_ptr(), int(bool(options.compute_depth)),
+                     grad_gauss.data_ptr(), stream)
+        has_sh = inputs.sh.numel() != 0
+        shs = _f32c(inputs.sh).reshape(P, -1, NUM_CHANNELS) if has_sh else None
+        K = shs.shape[1] if has_sh else 0
+        grad_sh = torch.empty((P, K, NUM_CHANNELS), dtype=torch.float32, device=device) if has_sh else \
+            torch.empty_like(inputs.sh)
+        f = dict(dtype=torch.float32, device=device)
+        grad_means3d = torch.empty((P, 3), **f)
+        grad_means2d = torch.empty((P, 3), **f)
+        grad_scales = torch.empty((P, 3), **f)
+        grad_rotations = torch.empty((P, 4), **f)
+        tanfovx, tanfovy = float(inputs.tan_fovx), float(inputs.tan_fovy)
+        means_c = _f32c(means)
+        scales_c = _f32c(inputs.scales)
+        rot_c = _f32c(inputs.rotations, align16=True)
+        campos_c = _f32c(inputs.campos)
+        view_c = _f32c(inputs.viewmatrix)
+        proj_c = _f32c(inputs.projmatrix)
+        radii_c = radii.contiguous()
+        gp2 = _zeros_if_none(grad_proj_2d, (P, 2), device)
+        gcon = _zeros_if_none(grad_conic_2d, (P, 3), device)
+        gcov = _zeros_if_none(grad_conic_2d_inv, (P, 3), device)
+        lib.call(
+            "gs_preprocess_bwd", P, K, int(inputs.degree), means_c.data_ptr(), scales_c.data_ptr(), rot_c.data_ptr(),
+            float(inputs.scale_modifier), _lib.ptr(shs), campos_c.data_ptr(), view_c.data_ptr(), proj_c.data_ptr(),
+            tanfovx, tanfovy, _focal(W, tanfovx), _focal(H, tanfovy), radii_c.data_ptr(), pre.clamped.data_ptr(),
+            grad_gauss.data_ptr(), gp2.data_ptr(), gcon.data_ptr(), gcov.data_ptr(), int(bool(flow_double)),
+            grad_means3d.data_ptr(), grad_means2d.data_ptr(), grad_scales.data_ptr(), grad_rotations.data_ptr(),
+            grad_sh.data_ptr() if has_sh else None, None, None, stream)
+    grad_opacities = grad_gauss[:, 5:6]
+    if grad_opacities.shape != inputs.opacities.shape:
+        grad_opacities = grad_opacities.reshape(inputs.opacities.shape)
+    if inputs.colors.numel() != 0:
+        grad_colors = grad_gauss[:, 6:9].reshape(inputs.colors.shape)
+    if has_sh:
+        grad_sh = grad_sh.reshape(inputs.sh.shape)
+    return (grad_means2d, grad_colors, grad_opacities, grad_means3d, grad_cov3d, grad_sh,
+            grad_scales.reshape(inputs.scales.shape), grad_rotations.reshape(inputs.rotations.shape))
+
+
+def mark_visible(positions: torch.Tensor, viewmatrix: torch.Tensor) -> torch.Tensor:
+    """view-space z > 0.2 as bool (preprocess_ops.py:584-595)."""
+    points = positions.contiguous()
+    if points.ndim != 2 or points.shape[1] != 3:
+        raise ValueError("means3D must have dimensions (num_points, 3)")
+    device = points.device
+    if points.shape[0] == 0:
+        return torch.empty((0,), dtype=torch.bool, device=device)
+    lib = _lib.load()
+    out = torch.empty((points.shape[0],), dtype=torch.uint8, device=device)
+    points_c = _f32c(points)
+    view_c = _f32c(viewmatrix)
+    with torch.cuda.device(device), _workspace.device_lock(device):
+        lib.call("gs_mark_visible", points.shape[0], points_c.data_ptr(), view_c.data_ptr(), out.data_ptr(),
+                 _stream(device))
+    return out.view(torch.bool)

@@ -1,0 +1,79 @@
+"""Per-(device, stream) host workspaces and submission locks.
+
+The forward pass performs one device-to-host read (the pair count), which
+needs page-locked host memory to be asynchronous on the stream.  Allocating
+pinned memory is slow, so one small pinned buffer is kept per (device,
+stream), at most ``MAX_WORKSPACE_STREAMS`` per device with least-recently
+used eviction; an evicted or cleared entry's stream is synchronised first so
+no copy into it can still be in flight (the contract of the reference's
+workspace cache, gswarp/_internal/backends/warp/memory.py:20-22 and
+340-393).  Device scratch (scan and sort tables) comes from torch's
+stream-ordered caching allocator per call.
+
+Submission from several host threads is serialised per device with an
+RLock, as gswarp/_stream.py:128-151 does; calls on different streams still
+overlap on the GPU.
+"""
+
+from __future__ import annotations
+
+import threading
+from collections import OrderedDict
+
+import torch
+
+MAX_WORKSPACE_STREAMS = 4
+
+_lock = threading.Lock()
+_device_locks: dict[int, threading.RLock] = {}
+_entries: "OrderedDict[tuple[int, int], dict]" = OrderedDict()
+_evictions = 0
+
+
+def device_lock(device: torch.device) -> threading.RLock:
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    with _lock:
+        lock = _device_locks.get(index)
+        if lock is None:
+            lock = _device_locks[index] = threading.RLock()
+        return lock
+
+
+def readback_buffer(device: torch.device, stream: torch.cuda.Stream) -> torch.Tensor:
+    """Pinned int64[2] host buffer owned by (device, stream)."""
+    global _evictions
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, stream.cuda_stream)
+    with _lock:
+        entry = _entries.get(key)
+        if entry is not None:
+            _entries.move_to_end(key)
+            return entry["pinned"]
+        per_device = [k for k in _entries if k[0] == index]
+        while len(per_device) >= MAX_WORKSPACE_STREAMS:
+            victim = per_device.pop(0)
+            old = _entries.pop(victim)
+            old["stream"].synchronize()
+            _evictions += 1
+        entry = {"pinned": torch.zeros(2, dtype=torch.int64, pin_memory=True), "stream": stream}
+        _entries[key] = entry
+        return entry["pinned"]
+
+
+def clear_caches() -> None:
+    """Drop every workspace after synchronising the streams that use them."""
+    with _lock:
+        for entry in _entries.values():
+            entry["stream"].synchronize()
+        _entries.clear()
+
+
+def cache_report() -> dict:
+    with _lock:
+        return {
+            "workspace_entries": len(_entries),
+            "workspace_evictions": _evictions,
+            "workspace_limit_per_device": MAX_WORKSPACE_STREAMS,
+            "retained_host_bytes": sum(e["pinned"].numel() * e["pinned"].element_size() for e in _entries.values()),
+            "retained_device_bytes": 0,
+        }

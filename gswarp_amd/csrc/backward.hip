@@ -1,0 +1,668 @@
+// Manual backward for gfx950.
+//
+// render_bwd: one 256-thread workgroup per tile walks the tile's list back to
+// front from the largest n_contrib of its pixels (backward_kernels.py:539-707
+// semantics: T starts at 1 - alpha_out, is divided by max(1-alpha, 1e-5) per
+// blended Gaussian, reverse recurrences for colour, depth and alpha, the
+// background term, xy gradients scaled by W/2 and H/2, conic gradients with
+// the -1/2 factor).  Per Gaussian, each wave sums its 64 pixels' ten gradient
+// components with DPP row operations (skipped when no lane of the wave
+// blended it), the four waves combine through LDS float atomics, and after
+// each 256-Gaussian batch one lane per Gaussian issues a single global atomic
+// per non-zero component.
+//
+// preprocess_bwd: one thread per Gaussian fusing the SH colour backward
+// (backward_kernels.py:298-536), the projected-mean / depth backward
+// (backward_kernels.py:89-112), the cov2D -> cov3D -> scale/rotation backward
+// (backward_kernels.py:114-287) and the accumulation (backward_kernels.py:289-295).
+// cov3D is recomputed from scale and rotation with the forward's exact
+// expression instead of being stored by the forward pass.
+#include "gs_common.h"
+#include "gs_capi.h"
+
+namespace gs {
+
+constexpr int kGradFloats = 10;  // dx, dy, conic a, b, c, opacity, r, g, b, depth
+
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ float dpp_mov(float src) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(src), kCtrl, kRowMask, 0xF, false));
+}
+
+// Sum over the 64 lanes of a fully active wave; the total lands in lane 63.
+__device__ __forceinline__ float wave_sum_lane63(float v) {
+  v = v + dpp_mov<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  v = v + dpp_mov<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+  v = v + dpp_mov<0x141, 0xF>(v);  // row_half_mirror
+  v = v + dpp_mov<0x140, 0xF>(v);  // row_mirror
+  v = v + dpp_mov<0x142, 0xA>(v);  // row_bcast:15 -> rows 1, 3
+  v = v + dpp_mov<0x143, 0xC>(v);  // row_bcast:31 -> rows 2, 3
+  return v;
+}
+
+__device__ __forceinline__ int wave_max_i32(int v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const int o = __shfl_xor(v, off, 64);
+    v = v > o ? v : o;
+  }
+  return v;
+}
+
+struct RenderBwdParams {
+  int W, H, grid_x, num_tiles;
+  int num_points;
+  int num_rendered;
+  const int2* ranges;
+  const int* point_list;
+  const float4* records;
+  const float* bg;
+  const float* out_alpha;
+  const int* n_contrib;
+  const float* grad_color;
+  const float* grad_depth;
+  const float* grad_alpha;
+  int compute_depth;
+  float* grad_gauss;
+};
+
+__global__ __launch_bounds__(kTilePixels) void render_bwd_kernel(RenderBwdParams p) {
+  __shared__ float4 s_r0[kTilePixels];
+  __shared__ float4 s_r1[kTilePixels];
+  __shared__ float4 s_r2[kTilePixels];
+  __shared__ int s_id[kTilePixels];
+  __shared__ float s_acc[kTilePixels * kGradFloats];
+  __shared__ int s_any[kTilePixels];
+  __shared__ int s_wmax[kTilePixels / 64];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int tile = blockIdx.x;
+  const int tx = tile % p.grid_x;
+  const int ty = tile / p.grid_x;
+  const int px = tx * kBlockX + (threadIdx.x % kBlockX);
+  const int py = ty * kBlockY + (threadIdx.x / kBlockX);
+  const bool inside = px < p.W && py < p.H;
+  const int P = p.W * p.H;
+  const int pix = py * p.W + px;
+  int2 rg = p.ranges[tile];
+  rg.x = imax(0, imin(rg.x, p.num_rendered));
+  rg.y = imax(rg.x, imin(rg.y, p.num_rendered));
+  const int n = rg.y - rg.x;
+
+  int last = 0;
+  if (inside && n > 0) last = imax(0, imin(p.n_contrib[pix], n));
+  const int wmax = wave_max_i32(last);
+  if (lane == 0) s_wmax[wave] = wmax;
+  __syncthreads();
+  int max_lc = s_wmax[0];
+#pragma unroll
+  for (int w = 1; w < kTilePixels / 64; ++w) max_lc = max_lc > s_wmax[w] ? max_lc : s_wmax[w];
+  if (max_lc == 0) return;  // uniform across the workgroup
+
+  const float ddelx_dx = 0.5f * (float)p.W;
+  const float ddely_dy = 0.5f * (float)p.H;
+  const float pfx = (float)px;
+  const float pfy = (float)py;
+  float T_final = 0.0f, T = 0.0f;
+  float gp0 = 0.0f, gp1 = 0.0f, gp2 = 0.0f, gpd = 0.0f, gpa = 0.0f, bg_dot = 0.0f;
+  if (inside && n > 0) {
+    T_final = 1.0f - p.out_alpha[pix];
+    T = T_final;
+    gp0 = p.grad_color[pix];
+    gp1 = p.grad_color[P + pix];
+    gp2 = p.grad_color[2 * P + pix];
+    if (p.compute_depth) gpd = p.grad_depth[pix];
+    gpa = p.grad_alpha[pix];
+    bg_dot = p.bg[0] * gp0 + p.bg[1] * gp1 + p.bg[2] * gp2;
+  }
+  float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f, acc_d = 0.0f, acc_a = 0.0f;
+  float last_alpha = 0.0f, lc0 = 0.0f, lc1 = 0.0f, lc2 = 0.0f, last_depth = 0.0f;
+
+  for (int batch_end = max_lc; batch_end > 0; batch_end -= kTilePixels) {
+    const int batch_start = batch_end > kTilePixels ? batch_end - kTilePixels : 0;
+    const int cnt = batch_end - batch_start;
+    __syncthreads();
+    if (threadIdx.x < cnt) {
+      int id = p.point_list[rg.x + batch_start + threadIdx.x];
+      if ((unsigned)id >= (unsigned)p.num_points) id = 0;
+      const float4* rec = p.records + 3 * (size_t)id;
+      s_r0[threadIdx.x] = rec[0];
+      s_r1[threadIdx.x] = rec[1];
+      s_r2[threadIdx.x] = rec[2];
+      s_id[threadIdx.x] = id;
+      s_any[threadIdx.x] = 0;
+    }
+#pragma unroll
+    for (int i = threadIdx.x; i < kTilePixels * kGradFloats; i += kTilePixels) s_acc[i] = 0.0f;
+    __syncthreads();
+
+    for (int jj = cnt - 1; jj >= 0; --jj) {
+      const int pos = batch_start + jj;
+      float g[kGradFloats];
+#pragma unroll
+      for (int c = 0; c < kGradFloats; ++c) g[c] = 0.0f;
+      bool has = false;
+      if (inside && pos < last) {
+        const float4 a = s_r0[jj];
+        const float4 b = s_r1[jj];
+        const float dx = a.x - pfx;
+        const float dy = a.y - pfy;
+        const float power = -0.5f * (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
+        if (power <= 0.0f && power >= b.w) {
+          const float G = exp_sw(power);
+          const float alpha = fminr(kAlphaMax, b.y * G);
+          if (alpha >= kAlphaMin) {
+            has = true;
+            const float4 f = s_r2[jj];
+            const float oma = fmaxr(1.0f - alpha, kOneMinusAlphaMin);
+            T = T / oma;
+            const float dchannel = alpha * T;
+            const float om_last = 1.0f - last_alpha;
+            acc0 = last_alpha * lc0 + om_last * acc0;
+            acc1 = last_alpha * lc1 + om_last * acc1;
+            acc2 = last_alpha * lc2 + om_last * acc2;
+            lc0 = f.x;
+            lc1 = f.y;
+            lc2 = f.z;
+            float dL_dopa = (f.x - acc0) * gp0 + (f.y - acc1) * gp1 + (f.z - acc2) * gp2;
+            g[6] = dchannel * gp0;
+            g[7] = dchannel * gp1;
+            g[8] = dchannel * gp2;
+            if (p.compute_depth) {
+              acc_d = last_alpha * last_depth + om_last * acc_d;
+              last_depth = b.z;
+              dL_dopa = dL_dopa + (b.z - acc_d) * gpd;
+              g[9] = dchannel * gpd;
+            }
+            acc_a = last_alpha + om_last * acc_a;
+            dL_dopa = dL_dopa + (1.0f - acc_a) * gpa;
+            dL_dopa = dL_dopa * T;
+            last_alpha = alpha;
+            dL_dopa = dL_dopa + (-T_final / oma) * bg_dot;
+            const float dL_dG = b.y * dL_dopa;
+            const float gdx = G * dx;
+            const float gdy = G * dy;
+            const float dG_ddelx = -gdx * a.z - gdy * a.w;
+            const float dG_ddely = -gdy * b.x - gdx * a.w;
+            g[0] = dL_dG * dG_ddelx * ddelx_dx;
+            g[1] = dL_dG * dG_ddely * ddely_dy;
+            g[2] = -0.5f * gdx * dx * dL_dG;
+            g[3] = -0.5f * gdx * dy * dL_dG;
+            g[4] = -0.5f * gdy * dy * dL_dG;
+            g[5] = G * dL_dopa;
+          }
+        }
+      }
+      if (__ballot(has) != 0) {
+#pragma unroll
+        for (int c = 0; c < kGradFloats; ++c) g[c] = wave_sum_lane63(g[c]);
+        if (lane == 63) {
+#pragma unroll
+          for (int c = 0; c < kGradFloats; ++c) atomicAdd(&s_acc[jj * kGradFloats + c], g[c]);
+          s_any[jj] = 1;
+        }
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < cnt && s_any[threadIdx.x]) {
+      float* dst = p.grad_gauss + (size_t)s_id[threadIdx.x] * kGradFloats;
+#pragma unroll
+      for (int c = 0; c < kGradFloats; ++c) {
+        const float v = s_acc[threadIdx.x * kGradFloats + c];
+        if (v != 0.0f) unsafeAtomicAdd(dst + c, v);
+      }
+    }
+  }
+}
+
+struct PreprocessBwdParams {
+  int P, K, degree;
+  const float* means3d;
+  const float* scales;
+  const float* rotations;
+  float scale_modifier;
+  const float* shs;
+  const float* campos;
+  const float* view;
+  const float* proj;
+  float tanfovx, tanfovy, focal_x, focal_y;
+  const int* radii;
+  const uint8_t* clamped;
+  const float* grad_gauss;
+  const float* grad_proj_2d;
+  const float* grad_conic_2d;
+  const float* grad_conic_2d_inv;
+  int flow_double;
+  float* grad_means3d;
+  float* grad_means2d;
+  float* grad_scales;
+  float* grad_rotations;
+  float* grad_sh;
+  float* grad_opacity;
+  float* grad_colors;
+};
+
+struct V3 {
+  float x, y, z;
+};
+
+__device__ __forceinline__ float dot3(V3 a, float b0, float b1, float b2) { return a.x * b0 + a.y * b1 + a.z * b2; }
+
+// SH colour backward for one Gaussian: writes its K x 3 block of grad_sh and
+// returns dL/dmean through the direction normalisation.
+__device__ __forceinline__ V3 sh_backward(const float* __restrict__ sh, float* __restrict__ gsh, int K, int degree,
+                                          float dirx, float diry, float dirz, float g0, float g1, float g2) {
+  const float len_sq = dirx * dirx + diry * diry + dirz * dirz;
+  const float inv_len = 1.0f / sqrtf(fmaxr(len_sq, 1.0e-20f));
+  const float x = dirx * inv_len, y = diry * inv_len, z = dirz * inv_len;
+  V3 dx = {0.0f, 0.0f, 0.0f}, dy = {0.0f, 0.0f, 0.0f}, dz = {0.0f, 0.0f, 0.0f};
+  int written = 0;
+  if (K > 0) {
+    gsh[0] = kShC0 * g0;
+    gsh[1] = kShC0 * g1;
+    gsh[2] = kShC0 * g2;
+    written = 1;
+  }
+  if (degree > 0 && K > 3) {
+    const float w1 = -kShC1 * y, w2 = kShC1 * z, w3 = -kShC1 * x;
+    gsh[3] = w1 * g0; gsh[4] = w1 * g1; gsh[5] = w1 * g2;
+    gsh[6] = w2 * g0; gsh[7] = w2 * g1; gsh[8] = w2 * g2;
+    gsh[9] = w3 * g0; gsh[10] = w3 * g1; gsh[11] = w3 * g2;
+    written = 4;
+    dx = {-kShC1 * sh[9], -kShC1 * sh[10], -kShC1 * sh[11]};
+    dy = {-kShC1 * sh[3], -kShC1 * sh[4], -kShC1 * sh[5]};
+    dz = {kShC1 * sh[6], kShC1 * sh[7], kShC1 * sh[8]};
+    if (degree > 1 && K > 8) {
+      const float xx = x * x, yy = y * y, zz = z * z;
+      const float xy = x * y, yz = y * z, xz = x * z;
+      const float w4 = kShC2_0 * xy, w5 = kShC2_1 * yz, w6 = kShC2_2 * (2.0f * zz - xx - yy);
+      const float w7 = kShC2_3 * xz, w8 = kShC2_4 * (xx - yy);
+      gsh[12] = w4 * g0; gsh[13] = w4 * g1; gsh[14] = w4 * g2;
+      gsh[15] = w5 * g0; gsh[16] = w5 * g1; gsh[17] = w5 * g2;
+      gsh[18] = w6 * g0; gsh[19] = w6 * g1; gsh[20] = w6 * g2;
+      gsh[21] = w7 * g0; gsh[22] = w7 * g1; gsh[23] = w7 * g2;
+      gsh[24] = w8 * g0; gsh[25] = w8 * g1; gsh[26] = w8 * g2;
+      written = 9;
+      const float ex4 = kShC2_0 * y, ex6 = kShC2_2 * (-2.0f * x), ex7 = kShC2_3 * z, ex8 = kShC2_4 * (2.0f * x);
+      const float ey4 = kShC2_0 * x, ey5 = kShC2_1 * z, ey6 = kShC2_2 * (-2.0f * y), ey8 = kShC2_4 * (-2.0f * y);
+      const float ez5 = kShC2_1 * y, ez6 = kShC2_2 * (4.0f * z), ez7 = kShC2_3 * x;
+#define GS_C(k, c) sh[3 * (k) + (c)]
+      dx.x = dx.x + ex4 * GS_C(4, 0) + ex6 * GS_C(6, 0) + ex7 * GS_C(7, 0) + ex8 * GS_C(8, 0);
+      dx.y = dx.y + ex4 * GS_C(4, 1) + ex6 * GS_C(6, 1) + ex7 * GS_C(7, 1) + ex8 * GS_C(8, 1);
+      dx.z = dx.z + ex4 * GS_C(4, 2) + ex6 * GS_C(6, 2) + ex7 * GS_C(7, 2) + ex8 * GS_C(8, 2);
+      dy.x = dy.x + ey4 * GS_C(4, 0) + ey5 * GS_C(5, 0) + ey6 * GS_C(6, 0) + ey8 * GS_C(8, 0);
+      dy.y = dy.y + ey4 * GS_C(4, 1) + ey5 * GS_C(5, 1) + ey6 * GS_C(6, 1) + ey8 * GS_C(8, 1);
+      dy.z = dy.z + ey4 * GS_C(4, 2) + ey5 * GS_C(5, 2) + ey6 * GS_C(6, 2) + ey8 * GS_C(8, 2);
+      dz.x = dz.x + ez5 * GS_C(5, 0) + ez6 * GS_C(6, 0) + ez7 * GS_C(7, 0);
+      dz.y = dz.y + ez5 * GS_C(5, 1) + ez6 * GS_C(6, 1) + ez7 * GS_C(7, 1);
+      dz.z = dz.z + ez5 * GS_C(5, 2) + ez6 * GS_C(6, 2) + ez7 * GS_C(7, 2);
+      if (degree > 2 && K > 15) {
+        const float w9 = kShC3_0 * y * (3.0f * xx - yy);
+        const float w10 = kShC3_1 * xy * z;
+        const float w11 = kShC3_2 * y * (4.0f * zz - xx - yy);
+        const float w12 = kShC3_3 * z * (2.0f * zz - 3.0f * xx - 3.0f * yy);
+        const float w13 = kShC3_4 * x * (4.0f * zz - xx - yy);
+        const float w14 = kShC3_5 * z * (xx - yy);
+        const float w15 = kShC3_6 * x * (xx - 3.0f * yy);
+        gsh[27] = w9 * g0; gsh[28] = w9 * g1; gsh[29] = w9 * g2;
+        gsh[30] = w10 * g0; gsh[31] = w10 * g1; gsh[32] = w10 * g2;
+        gsh[33] = w11 * g0; gsh[34] = w11 * g1; gsh[35] = w11 * g2;
+        gsh[36] = w12 * g0; gsh[37] = w12 * g1; gsh[38] = w12 * g2;
+        gsh[39] = w13 * g0; gsh[40] = w13 * g1; gsh[41] = w13 * g2;
+        gsh[42] = w14 * g0; gsh[43] = w14 * g1; gsh[44] = w14 * g2;
+        gsh[45] = w15 * g0; gsh[46] = w15 * g1; gsh[47] = w15 * g2;
+        written = 16;
+        const float ex9 = kShC3_0 * (6.0f * xy), ex10 = kShC3_1 * yz, ex11 = kShC3_2 * (-2.0f * xy);
+        const float ex12 = kShC3_3 * (-6.0f * xz), ex13 = kShC3_4 * (-3.0f * xx + 4.0f * zz - yy);
+        const float ex14 = kShC3_5 * (2.0f * xz), ex15 = kShC3_6 * (3.0f * (xx - yy));
+        const float ey9 = kShC3_0 * (3.0f * (xx - yy)), ey10 = kShC3_1 * xz;
+        const float ey11 = kShC3_2 * (-3.0f * yy + 4.0f * zz - xx), ey12 = kShC3_3 * (-6.0f * yz);
+        const float ey13 = kShC3_4 * (-2.0f * xy), ey14 = kShC3_5 * (-2.0f * yz), ey15 = kShC3_6 * (-6.0f * xy);
+        const float ez10 = kShC3_1 * xy, ez11 = kShC3_2 * (8.0f * yz);
+        const float ez12 = kShC3_3 * (3.0f * (2.0f * zz - xx - yy)), ez13 = kShC3_4 * (8.0f * xz);
+        const float ez14 = kShC3_5 * (xx - yy);
+#define GS_DX(acc, c)                                                                                      \
+  acc = acc + ex9 * GS_C(9, c) + ex10 * GS_C(10, c) + ex11 * GS_C(11, c) + ex12 * GS_C(12, c) +           \
+        ex13 * GS_C(13, c) + ex14 * GS_C(14, c) + ex15 * GS_C(15, c)
+#define GS_DY(acc, c)                                                                                      \
+  acc = acc + ey9 * GS_C(9, c) + ey10 * GS_C(10, c) + ey11 * GS_C(11, c) + ey12 * GS_C(12, c) +           \
+        ey13 * GS_C(13, c) + ey14 * GS_C(14, c) + ey15 * GS_C(15, c)
+#define GS_DZ(acc, c)                                                                                      \
+  acc = acc + ez10 * GS_C(10, c) + ez11 * GS_C(11, c) + ez12 * GS_C(12, c) + ez13 * GS_C(13, c) +         \
+        ez14 * GS_C(14, c)
+        GS_DX(dx.x, 0); GS_DX(dx.y, 1); GS_DX(dx.z, 2);
+        GS_DY(dy.x, 0); GS_DY(dy.y, 1); GS_DY(dy.z, 2);
+        GS_DZ(dz.x, 0); GS_DZ(dz.y, 1); GS_DZ(dz.z, 2);
+#undef GS_DX
+#undef GS_DY
+#undef GS_DZ
+#undef GS_C
+      }
+    }
+  }
+  for (int k = written; k < K; ++k) {
+    gsh[3 * k + 0] = 0.0f;
+    gsh[3 * k + 1] = 0.0f;
+    gsh[3 * k + 2] = 0.0f;
+  }
+  const float ddir0 = dot3(dx, g0, g1, g2);
+  const float ddir1 = dot3(dy, g0, g1, g2);
+  const float ddir2 = dot3(dz, g0, g1, g2);
+  // d normalize(v) / dv applied to dL/ddir (math_kernels.py:90-97).
+  const float sum2 = dirx * dirx + diry * diry + dirz * dirz;
+  const float invsum32 = 1.0f / sqrtf(fmaxr(sum2 * sum2 * sum2, 1.0e-20f));
+  V3 r;
+  r.x = ((sum2 - dirx * dirx) * ddir0 - diry * dirx * ddir1 - dirz * dirx * ddir2) * invsum32;
+  r.y = (-dirx * diry * ddir0 + (sum2 - diry * diry) * ddir1 - dirz * diry * ddir2) * invsum32;
+  r.z = (-dirx * dirz * ddir0 - diry * dirz * ddir1 + (sum2 - dirz * dirz) * ddir2) * invsum32;
+  return r;
+}
+
+__global__ __launch_bounds__(256) void preprocess_bwd_kernel(PreprocessBwdParams p) {
+  const int tid = blockIdx.x * blockDim.x + threadIdx.x;
+  if (tid >= p.P) return;
+  const float* __restrict__ V = p.view;
+  const float* __restrict__ Pm = p.proj;
+  const float mx = p.means3d[3 * tid + 0];
+  const float my = p.means3d[3 * tid + 1];
+  const float mz = p.means3d[3 * tid + 2];
+  const int rad = p.radii[tid];
+  const float* gg = p.grad_gauss + (size_t)tid * kGradFloats;
+  const float rpx = gg[0], rpy = gg[1];
+  const float rc0 = gg[2], rc1 = gg[3], rc2 = gg[4];
+  const float ropa = gg[5];
+  const float rcol0 = gg[6], rcol1 = gg[7], rcol2 = gg[8];
+  const float rdepth = gg[9];
+
+  // Part A: projected mean and depth.
+  const float hom_x = Pm[0] * mx + Pm[4] * my + Pm[8] * mz + Pm[12];
+  const float hom_y = Pm[1] * mx + Pm[5] * my + Pm[9] * mz + Pm[13];
+  const float hom_w = Pm[3] * mx + Pm[7] * my + Pm[11] * mz + Pm[15];
+  const float inv_w = 1.0f / (hom_w + 0.0000001f);
+  float gx = rpx, gy = rpy;
+  const float inv_w2 = inv_w * inv_w;
+  if (rad > 0) {
+    float ax = p.grad_proj_2d[2 * tid + 0];
+    float ay = p.grad_proj_2d[2 * tid + 1];
+    if (p.flow_double) {
+      ax = ax + rpx;
+      ay = ay + rpy;
+    }
+    gx = gx + ax;
+    gy = gy + ay;
+  }
+  const float gh = hom_x * gx + hom_y * gy;
+  float pm_x = inv_w * (Pm[0] * gx + Pm[1] * gy) - Pm[3] * inv_w2 * gh;
+  float pm_y = inv_w * (Pm[4] * gx + Pm[5] * gy) - Pm[7] * inv_w2 * gh;
+  float pm_z = inv_w * (Pm[8] * gx + Pm[9] * gy) - Pm[11] * inv_w2 * gh;
+  const float zv = V[2] * mx + V[6] * my + V[10] * mz + V[14];
+  pm_x = pm_x + (V[2] - V[3] * zv) * rdepth;
+  pm_y = pm_y + (V[6] - V[7] * zv) * rdepth;
+  pm_z = pm_z + (V[10] - V[11] * zv) * rdepth;
+
+  // Part B: cov2D -> cov3D -> scale / rotation, and the mean through the
+  // EWA Jacobian.
+  float gcm_x = 0.0f, gcm_y = 0.0f, gcm_z = 0.0f;
+  float gs0 = 0.0f, gs1 = 0.0f, gs2 = 0.0f;
+  float gq0 = 0.0f, gq1 = 0.0f, gq2 = 0.0f, gq3 = 0.0f;
+  if (rad > 0) {
+    const float x = V[0] * mx + V[4] * my + V[8] * mz + V[12];
+    const float y = V[1] * mx + V[5] * my + V[9] * mz + V[13];
+    const float z = V[2] * mx + V[6] * my + V[10] * mz + V[14];
+    const float tz_inv = 1.0f / (z + 1.0e-7f);
+    const float limx = kFovClamp * p.tanfovx;
+    const float limy = kFovClamp * p.tanfovy;
+    const float txtz = x * tz_inv;
+    const float tytz = y * tz_inv;
+    const float x_grad_mul = (txtz < -limx || txtz > limx) ? 0.0f : 1.0f;
+    const float y_grad_mul = (tytz < -limy || tytz > limy) ? 0.0f : 1.0f;
+    const float tx = clampr(txtz, -limx, limx);
+    const float ty = clampr(tytz, -limy, limy);
+    const float j00 = p.focal_x * tz_inv;
+    const float j02 = -j00 * tx;
+    const float j11 = p.focal_y * tz_inv;
+    const float j12 = -j11 * ty;
+    const float w00 = V[0], w01 = V[1], w02 = V[2];
+    const float w10 = V[4], w11 = V[5], w12 = V[6];
+    const float w20 = V[8], w21 = V[9], w22 = V[10];
+    const float t00 = w00 * j00 + w02 * j02;
+    const float t10 = w10 * j00 + w12 * j02;
+    const float t20 = w20 * j00 + w22 * j02;
+    const float t01 = w01 * j11 + w02 * j12;
+    const float t11 = w11 * j11 + w12 * j12;
+    const float t21 = w21 * j11 + w22 * j12;
+
+    const float ss0 = p.scales[3 * tid + 0] * p.scale_modifier;
+    const float ss1 = p.scales[3 * tid + 1] * p.scale_modifier;
+    const float ss2 = p.scales[3 * tid + 2] * p.scale_modifier;
+    const float4 q = reinterpret_cast<const float4*>(p.rotations)[tid];
+    const float rr = q.x, xq = q.y, yq = q.z, zq = q.w;
+    const float r00 = 1.0f - 2.0f * (yq * yq + zq * zq);
+    const float r01 = 2.0f * (xq * yq + rr * zq);
+    const float r02 = 2.0f * (xq * zq - rr * yq);
+    const float r10 = 2.0f * (xq * yq - rr * zq);
+    const float r11 = 1.0f - 2.0f * (xq * xq + zq * zq);
+    const float r12 = 2.0f * (yq * zq + rr * xq);
+    const float r20 = 2.0f * (xq * zq + rr * yq);
+    const float r21 = 2.0f * (yq * zq - rr * xq);
+    const float r22 = 1.0f - 2.0f * (xq * xq + yq * yq);
+    const float mm00 = ss0 * r00, mm01 = ss0 * r01, mm02 = ss0 * r02;
+    const float mm10 = ss1 * r10, mm11 = ss1 * r11, mm12 = ss1 * r12;
+    const float mm20 = ss2 * r20, mm21 = ss2 * r21, mm22 = ss2 * r22;
+    // cov3D = M^T M, the forward's expression (preprocess_kernels.py:177-182).
+    const float v00 = mm00 * mm00 + mm10 * mm10 + mm20 * mm20;
+    const float v01 = mm00 * mm01 + mm10 * mm11 + mm20 * mm21;
+    const float v02 = mm00 * mm02 + mm10 * mm12 + mm20 * mm22;
+    const float v11 = mm01 * mm01 + mm11 * mm11 + mm21 * mm21;
+    const float v12 = mm01 * mm02 + mm11 * mm12 + mm21 * mm22;
+    const float v22 = mm02 * mm02 + mm12 * mm12 + mm22 * mm22;
+
+    const float vt0x = v00 * t00 + v01 * t10 + v02 * t20;
+    const float vt0y = v01 * t00 + v11 * t10 + v12 * t20;
+    const float vt0z = v02 * t00 + v12 * t10 + v22 * t20;
+    const float vt1x = v00 * t01 + v01 * t11 + v02 * t21;
+    const float vt1y = v01 * t01 + v11 * t11 + v12 * t21;
+    const float vt1z = v02 * t01 + v12 * t11 + v22 * t21;
+    const float aa = t00 * vt0x + t10 * vt0y + t20 * vt0z + 0.3f + 0.0f;
+    const float bb = t00 * vt1x + t10 * vt1y + t20 * vt1z;
+    const float cc = t01 * vt1x + t11 * vt1y + t21 * vt1z + 0.3f + 0.0f;
+    const float denom = aa * cc - bb * bb;
+    const float denom2inv = 1.0f / (denom * denom + 1.0e-7f);
+
+    float uc0 = p.grad_conic_2d[3 * tid + 0];
+    float uc1 = p.grad_conic_2d[3 * tid + 1];
+    float uc2 = p.grad_conic_2d[3 * tid + 2];
+    if (p.flow_double) {
+      uc0 = uc0 + rc0;
+      uc1 = uc1 + rc1;
+      uc2 = uc2 + rc2;
+    }
+    const float tc0 = rc0 + uc0;
+    const float tc1 = rc1 + uc1;
+    const float tc2 = rc2 + uc2;
+    float dL_da = denom2inv * (-cc * cc * tc0 + 2.0f * bb * cc * tc1 - bb * bb * tc2);
+    float dL_dc = denom2inv * (-aa * aa * tc2 + 2.0f * aa * bb * tc1 - bb * bb * tc0);
+    float dL_db = denom2inv * 2.0f * (bb * cc * tc0 - (aa * cc + bb * bb) * tc1 + aa * bb * tc2);
+    dL_da = dL_da + p.grad_conic_2d_inv[3 * tid + 0];
+    dL_db = dL_db + p.grad_conic_2d_inv[3 * tid + 1];
+    dL_dc = dL_dc + p.grad_conic_2d_inv[3 * tid + 2];
+
+    const float gc0 = t00 * t00 * dL_da + t00 * t01 * dL_db + t01 * t01 * dL_dc;
+    const float gc3 = t10 * t10 * dL_da + t10 * t11 * dL_db + t11 * t11 * dL_dc;
+    const float gc5 = t20 * t20 * dL_da + t20 * t21 * dL_db + t21 * t21 * dL_dc;
+    const float gc1 = 2.0f * t00 * t10 * dL_da + (t00 * t11 + t01 * t10) * dL_db + 2.0f * t01 * t11 * dL_dc;
+    const float gc2 = 2.0f * t00 * t20 * dL_da + (t00 * t21 + t01 * t20) * dL_db + 2.0f * t01 * t21 * dL_dc;
+    const float gc4 = 2.0f * t10 * t20 * dL_da + (t10 * t21 + t11 * t20) * dL_db + 2.0f * t11 * t21 * dL_dc;
+
+    const float dL_dT00 = 2.0f * vt0x * dL_da + vt1x * dL_db;
+    const float dL_dT01 = 2.0f * vt0y * dL_da + vt1y * dL_db;
+    const float dL_dT02 = 2.0f * vt0z * dL_da + vt1z * dL_db;
+    const float dL_dT10 = vt0x * dL_db + 2.0f * vt1x * dL_dc;
+    const float dL_dT11 = vt0y * dL_db + 2.0f * vt1y * dL_dc;
+    const float dL_dT12 = vt0z * dL_db + 2.0f * vt1z * dL_dc;
+    const float dL_dJ00 = w00 * dL_dT00 + w10 * dL_dT01 + w20 * dL_dT02;
+    const float dL_dJ02 = w02 * dL_dT00 + w12 * dL_dT01 + w22 * dL_dT02;
+    const float dL_dJ11 = w01 * dL_dT10 + w11 * dL_dT11 + w21 * dL_dT12;
+    const float dL_dJ12 = w02 * dL_dT10 + w12 * dL_dT11 + w22 * dL_dT12;
+    const float dL_dtx = x_grad_mul * -j00 * tz_inv * dL_dJ02;
+    const float dL_dty = y_grad_mul * -j11 * tz_inv * dL_dJ12;
+    const float dL_dtz = -(j00 * dL_dJ00 + j11 * dL_dJ11 + 2.0f * j02 * dL_dJ02 + 2.0f * j12 * dL_dJ12) * tz_inv;
+    gcm_x = w00 * dL_dtx + w01 * dL_dty + w02 * dL_dtz;
+    gcm_y = w10 * dL_dtx + w11 * dL_dty + w12 * dL_dtz;
+    gcm_z = w20 * dL_dtx + w21 * dL_dty + w22 * dL_dtz;
+
+    const float sg00 = gc0, sg01 = 0.5f * gc1, sg02 = 0.5f * gc2;
+    const float sg11 = gc3, sg12 = 0.5f * gc4, sg22 = gc5;
+    const float dM00 = 2.0f * (mm00 * sg00 + mm01 * sg01 + mm02 * sg02);
+    const float dM01 = 2.0f * (mm00 * sg01 + mm01 * sg11 + mm02 * sg12);
+    const float dM02 = 2.0f * (mm00 * sg02 + mm01 * sg12 + mm02 * sg22);
+    const float dM10 = 2.0f * (mm10 * sg00 + mm11 * sg01 + mm12 * sg02);
+    const float dM11 = 2.0f * (mm10 * sg01 + mm11 * sg11 + mm12 * sg12);
+    const float dM12 = 2.0f * (mm10 * sg02 + mm11 * sg12 + mm12 * sg22);
+    const float dM20 = 2.0f * (mm20 * sg00 + mm21 * sg01 + mm22 * sg02);
+    const float dM21 = 2.0f * (mm20 * sg01 + mm21 * sg11 + mm22 * sg12);
+    const float dM22 = 2.0f * (mm20 * sg02 + mm21 * sg12 + mm22 * sg22);
+    gs0 = p.scale_modifier * (dM00 * r00 + dM01 * r01 + dM02 * r02);
+    gs1 = p.scale_modifier * (dM10 * r10 + dM11 * r11 + dM12 * r12);
+    gs2 = p.scale_modifier * (dM20 * r20 + dM21 * r21 + dM22 * r22);
+    const float dR00 = dM00 * ss0, dR01 = dM01 * ss0, dR02 = dM02 * ss0;
+    const float dR10 = dM10 * ss1, dR11 = dM11 * ss1, dR12 = dM12 * ss1;
+    const float dR20 = dM20 * ss2, dR21 = dM21 * ss2, dR22 = dM22 * ss2;
+    gq0 = 2.0f * zq * (dR01 - dR10) + 2.0f * yq * (dR20 - dR02) + 2.0f * xq * (dR12 - dR21);
+    gq1 = 2.0f * yq * (dR10 + dR01) + 2.0f * zq * (dR20 + dR02) + 2.0f * rr * (dR12 - dR21) -
+          4.0f * xq * (dR22 + dR11);
+    gq2 = 2.0f * xq * (dR10 + dR01) + 2.0f * rr * (dR20 - dR02) + 2.0f * zq * (dR12 + dR21) -
+          4.0f * yq * (dR22 + dR00);
+    gq3 = 2.0f * rr * (dR01 - dR10) + 2.0f * xq * (dR20 + dR02) + 2.0f * yq * (dR12 + dR21) -
+          4.0f * zq * (dR11 + dR00);
+  }
+
+  // SH colour backward (its colour gradient is identically zero for culled
+  // Gaussians, so their coefficient gradients are plain zeros).
+  float gsh_x = 0.0f, gsh_y = 0.0f, gsh_z = 0.0f;
+  if (p.shs != nullptr) {
+    float* gsh = p.grad_sh + (size_t)tid * (size_t)(3 * p.K);
+    if (rad > 0) {
+      const uint8_t cl = p.clamped != nullptr ? p.clamped[tid] : 0;
+      const float g0 = rcol0 * (1.0f - (float)(cl & 1));
+      const float g1 = rcol1 * (1.0f - (float)((cl >> 1) & 1));
+      const float g2 = rcol2 * (1.0f - (float)((cl >> 2) & 1));
+      const float* sh = p.shs + (size_t)tid * (size_t)(3 * p.K);
+      const V3 gm = sh_backward(sh, gsh, p.K, p.degree, mx - p.campos[0], my - p.campos[1], mz - p.campos[2], g0,
+                                g1, g2);
+      gsh_x = gm.x;
+      gsh_y = gm.y;
+      gsh_z = gm.z;
+    } else {
+      for (int k = 0; k < 3 * p.K; ++k) gsh[k] = 0.0f;
+    }
+  }
+
+  // Part C: accumulate.
+  p.grad_means3d[3 * tid + 0] = pm_x + gcm_x + gsh_x;
+  p.grad_means3d[3 * tid + 1] = pm_y + gcm_y + gsh_y;
+  p.grad_means3d[3 * tid + 2] = pm_z + gcm_z + gsh_z;
+  p.grad_means2d[3 * tid + 0] = rpx;
+  p.grad_means2d[3 * tid + 1] = rpy;
+  p.grad_means2d[3 * tid + 2] = 0.0f;
+  p.grad_scales[3 * tid + 0] = gs0;
+  p.grad_scales[3 * tid + 1] = gs1;
+  p.grad_scales[3 * tid + 2] = gs2;
+  reinterpret_cast<float4*>(p.grad_rotations)[tid] = make_float4(gq0, gq1, gq2, gq3);
+  if (p.grad_opacity != nullptr) p.grad_opacity[tid] = ropa;
+  if (p.grad_colors != nullptr) {
+    p.grad_colors[3 * tid + 0] = rcol0;
+    p.grad_colors[3 * tid + 1] = rcol1;
+    p.grad_colors[3 * tid + 2] = rcol2;
+  }
+}
+
+}  // namespace gs
+
+extern "C" int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t num_points,
+                             int64_t num_rendered, const int32_t* ranges,
+                             const int32_t* point_list, const float* records, const float* background,
+                             const float* out_alpha, const int32_t* n_contrib, const float* grad_color,
+                             const float* grad_depth, const float* grad_alpha, int32_t compute_depth,
+                             float* grad_gauss, void* stream) {
+  if (image_width <= 0 || image_height <= 0 || (long long)image_width * image_height > 0x7fffffffLL)
+    return GS_ERR_INVALID_ARGUMENT;
+  if (num_points <= 0 || num_rendered < 0) return GS_ERR_INVALID_ARGUMENT;
+  if (num_rendered > 0x7fffffffLL) return GS_ERR_OVERFLOW;
+  if (!ranges || !point_list || !records || !background || !out_alpha || !n_contrib || !grad_color ||
+      !grad_alpha || !grad_gauss || (compute_depth && !grad_depth))
+    return GS_ERR_INVALID_ARGUMENT;
+  if (reinterpret_cast<uintptr_t>(records) & 15) return GS_ERR_MISALIGNED;
+  gs::RenderBwdParams p;
+  p.W = image_width;
+  p.H = image_height;
+  p.grid_x = (image_width + gs::kBlockX - 1) / gs::kBlockX;
+  p.num_tiles = p.grid_x * ((image_height + gs::kBlockY - 1) / gs::kBlockY);
+  p.num_points = num_points;
+  p.num_rendered = (int)num_rendered;
+  p.ranges = reinterpret_cast<const int2*>(ranges);
+  p.point_list = point_list;
+  p.records = reinterpret_cast<const float4*>(records);
+  p.bg = background;
+  p.out_alpha = out_alpha;
+  p.n_contrib = n_contrib;
+  p.grad_color = grad_color;
+  p.grad_depth = grad_depth;
+  p.grad_alpha = grad_alpha;
+  p.compute_depth = compute_depth;
+  p.grad_gauss = grad_gauss;
+  hipLaunchKernelGGL(gs::render_bwd_kernel, dim3(p.num_tiles), dim3(gs::kTilePixels), 0, (hipStream_t)stream, p);
+  return gs_status_from_hip(hipGetLastError());
+}
+
+extern "C" int gs_preprocess_bwd(int32_t P, int32_t sh_coeffs, int32_t degree, const float* means3d,
+                                 const float* scales, const float* rotations, float scale_modifier,
+                                 const float* shs, const float* campos, const float* viewmatrix,
+                                 const float* projmatrix, float tanfovx, float tanfovy, float focal_x,
+                                 float focal_y, const int32_t* radii, const uint8_t* clamped,
+                                 const float* grad_gauss, const float* grad_proj_2d, const float* grad_conic_2d,
+                                 const float* grad_conic_2d_inv, int32_t flow_double, float* grad_means3d,
+                                 float* grad_means2d, float* grad_scales, float* grad_rotations, float* grad_sh,
+                                 float* grad_opacity, float* grad_colors, void* stream) {
+  if (P < 0) return GS_ERR_INVALID_ARGUMENT;
+  if (P == 0) return GS_OK;
+  if (!means3d || !scales || !rotations || !viewmatrix || !projmatrix || !radii || !grad_gauss || !grad_proj_2d ||
+      !grad_conic_2d || !grad_conic_2d_inv || !grad_means3d || !grad_means2d || !grad_scales || !grad_rotations)
+    return GS_ERR_INVALID_ARGUMENT;
+  if (shs != nullptr && (grad_sh == nullptr || campos == nullptr || sh_coeffs <= 0)) return GS_ERR_INVALID_ARGUMENT;
+  if ((reinterpret_cast<uintptr_t>(rotations) & 15) || (reinterpret_cast<uintptr_t>(grad_rotations) & 15))
+    return GS_ERR_MISALIGNED;
+  gs::PreprocessBwdParams p;
+  p.P = P;
+  p.K = sh_coeffs;
+  p.degree = degree;
+  p.means3d = means3d;
+  p.scales = scales;
+  p.rotations = rotations;
+  p.scale_modifier = scale_modifier;
+  p.shs = shs;
+  p.campos = campos;
+  p.view = viewmatrix;
+  p.proj = projmatrix;
+  p.tanfovx = tanfovx;
+  p.tanfovy = tanfovy;
+  p.focal_x = focal_x;
+  p.focal_y = focal_y;
+  p.radii = radii;
+  p.clamped = clamped;
+  p.grad_gauss = grad_gauss;
+  p.grad_proj_2d = grad_proj_2d;
+  p.grad_conic_2d = grad_conic_2d;
+  p.grad_conic_2d_inv = grad_conic_2d_inv;
+  p.flow_double = flow_double;
+  p.grad_means3d = grad_means3d;
+  p.grad_means2d = grad_means2d;
+  p.grad_scales = grad_scales;
+  p.grad_rotations = grad_rotations;
+  p.grad_sh = grad_sh;
+  p.grad_opacity = grad_opacity;
+  p.grad_colors = grad_colors;
+  hipLaunchKernelGGL(gs::preprocess_bwd_kernel, dim3((P + 255) / 256), dim3(256), 0, (hipStream_t)stream, p);
+  return gs_status_from_hip(hipGetLastError());
+}

@@ -1,0 +1,284 @@
+// Shared device-side definitions for the gfx950 Gaussian-splatting rasterizer.
+//
+// Everything here that feeds an integer decision (radius, tile rectangle,
+// tile coverage, alpha >= 1/255, transmittance cut-off) is written as plain
+// IEEE-754 binary32 arithmetic in a fixed evaluation order.  The library is
+// compiled with -ffp-contract=off and correctly rounded fp32 divide/sqrt, so
+// every such decision is reproducible bit-for-bit by a host compiler that
+// evaluates the same expressions with the same flags.
+//
+// Reference semantics followed (file:line into fancifulland2718/gswarp 1.1.0):
+//   constants           gswarp/_internal/backends/warp/constants.py:5-45
+//   tile rect           gswarp/_internal/backends/warp/math_kernels.py:137-148
+//   SnugBox rect        gswarp/_internal/backends/warp/math_kernels.py:151-194
+//   conic-rect test     gswarp/_internal/backends/warp/math_kernels.py:197-240
+//   AccuTile band       gswarp/_internal/backends/warp/math_kernels.py:243-303
+//   tile count          gswarp/_internal/backends/warp/math_kernels.py:306-390
+//   NDC -> pixel        gswarp/_internal/backends/warp/math_kernels.py:86-87
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#pragma clang fp contract(off)
+
+namespace gs {
+
+constexpr int kBlockX = 16;
+constexpr int kBlockY = 16;
+constexpr int kTilePixels = kBlockX * kBlockY;
+constexpr int kChannels = 3;
+
+// Real spherical-harmonics constants of the 3DGS convention, rounded to fp32.
+constexpr float kShC0 = 0.28209479177387814f;
+constexpr float kShC1 = 0.4886025119029199f;
+constexpr float kShC2_0 = 1.0925484305920792f;
+constexpr float kShC2_1 = -1.0925484305920792f;
+constexpr float kShC2_2 = 0.31539156525252005f;
+constexpr float kShC2_3 = -1.0925484305920792f;
+constexpr float kShC2_4 = 0.5462742152960396f;
+constexpr float kShC3_0 = -0.5900435899266435f;
+constexpr float kShC3_1 = 2.890611442640554f;
+constexpr float kShC3_2 = -0.4570457994644658f;
+constexpr float kShC3_3 = 0.3731763325901154f;
+constexpr float kShC3_4 = -0.4570457994644658f;
+constexpr float kShC3_5 = 1.445305721320277f;
+constexpr float kShC3_6 = -0.5900435899266435f;
+
+constexpr float kNearPlane = 0.2f;
+constexpr float kFovClamp = 1.3f;
+constexpr float kDetEps = 1.0e-7f;
+constexpr float kOneMinusAlphaMin = 1.0e-5f;
+constexpr float kSnugPad = 1.0f;
+constexpr float kQEps = 1.0e-4f;
+constexpr float kFloatMax = 3.402823466e38f;
+constexpr float kAlphaMin = 1.0f / 255.0f;
+constexpr float kTransmittanceMin = 0.0001f;
+constexpr float kAlphaMax = 0.99f;
+
+constexpr int kCoverageSnugbox = 0;
+constexpr int kCoverageAccutile = 1;
+constexpr int kCoverageConicRect = 2;
+constexpr int kConicMaskMaxTiles = 64;
+
+// Per-Gaussian render record, 48 bytes = three float4:
+//   r0 = (x, y, conic_a, conic_b)
+//   r1 = (conic_c, opacity, depth, power_cutoff)
+//   r2 = (r, g, b, 0)
+// power_cutoff is the largest Gaussian exponent for which alpha is provably
+// below 1/255 (see power_cutoff()); the render loops skip the exponential
+// for smaller exponents without changing any decision.
+constexpr int kRecordFloats = 12;
+
+__host__ __device__ __forceinline__ float fminr(float a, float b) { return a < b ? a : b; }
+__host__ __device__ __forceinline__ float fmaxr(float a, float b) { return a > b ? a : b; }
+__host__ __device__ __forceinline__ int imin(int a, int b) { return a < b ? a : b; }
+__host__ __device__ __forceinline__ int imax(int a, int b) { return a > b ? a : b; }
+__host__ __device__ __forceinline__ float clampr(float x, float lo, float hi) {
+  return x < lo ? lo : (x > hi ? hi : x);
+}
+
+// Truncating float -> int32 conversion with defined results everywhere:
+// NaN -> 0, saturation at the int32 range (the semantics of the hardware
+// conversion instruction, made explicit so host code can reproduce it).
+__host__ __device__ __forceinline__ int f2i(float f) {
+  if (!(f == f)) return 0;
+  if (f >= 2147483648.0f) return 2147483647;
+  if (f <= -2147483648.0f) return (-2147483647 - 1);
+  return (int)f;
+}
+
+// exp(x) by Cody-Waite range reduction x = n*ln2 + r (|r| <= ln2/2, ln2 split
+// into an exact 9-bit head and a tail) followed by the degree-7 Taylor
+// polynomial of e^r in Horner form and an exact scaling by 2^n.  Results are
+// within 2 ulp of exp(x) for x in [-87, 88]; x < -87 returns 0 (the result
+// would be below 1.7e-38 and only ever feeds an alpha < 1/255 decision).
+__device__ __forceinline__ float exp_sw(float x) {
+  if (x < -87.0f) return 0.0f;
+  if (x > 88.0f) x = 88.0f;
+  const float n = rintf(x * 1.44269504088896341f);
+  float r = x - n * 0.693359375f;
+  r = r - n * (-2.12194440e-4f);
+  float p = 1.98412698e-4f;          // 1/5040
+  p = p * r + 1.38888889e-3f;        // 1/720
+  p = p * r + 8.33333333e-3f;        // 1/120
+  p = p * r + 4.16666667e-2f;        // 1/24
+  p = p * r + 1.66666667e-1f;        // 1/6
+  p = p * r + 0.5f;
+  p = p * r + 1.0f;
+  p = p * r + 1.0f;
+  return ldexpf(p, (int)n);
+}
+
+// ln(y) for finite y > 0: y = m * 2^e with m in [sqrt(1/2), sqrt(2)), then
+// ln(m) = 2*atanh(s), s = (m-1)/(m+1), |s| <= 0.1716, by its odd series to
+// s^11.  ln2 is split into a head with trailing zero bits and a tail so that
+// e*ln2_hi is exact.
+__device__ __forceinline__ float log_sw(float y) {
+  int e;
+  float m = frexpf(y, &e);
+  if (m < 0.70710678118654752f) {
+    m = m * 2.0f;
+    e = e - 1;
+  }
+  const float s = (m - 1.0f) / (m + 1.0f);
+  const float s2 = s * s;
+  float p = 0.0909090909f;           // 1/11
+  p = p * s2 + 0.111111111f;         // 1/9
+  p = p * s2 + 0.142857143f;         // 1/7
+  p = p * s2 + 0.2f;                 // 1/5
+  p = p * s2 + 0.333333333f;         // 1/3
+  const float lnm = 2.0f * s + (2.0f * s) * (s2 * p);
+  const float ef = (float)e;
+  return ef * 0.693145751953125f + (lnm + ef * 1.42860677e-6f);
+}
+
+// Largest exponent below which o*exp(power) < 1/255 holds for every power,
+// with a 1e-3 margin that covers exp_sw and product rounding (relative error
+// < 1e-6).  Returns +inf when the Gaussian can never reach the alpha cut-off.
+__device__ __forceinline__ float power_cutoff(float opacity) {
+  const float o255 = 255.0f * opacity;
+  if (!(o255 > 1.0f)) return kFloatMax;
+  return -log_sw(o255) - 1.0e-3f;
+}
+
+__device__ __forceinline__ float ndc_to_pix(float v, int size) {
+  return ((v + 1.0f) * (float)size - 1.0f) * 0.5f;
+}
+
+// Tile rectangle of the 3-sigma square (truncating casts, clamped to grid).
+__device__ __forceinline__ int4 tile_rect(float px, float py, int rx, int ry, int grid_x, int grid_y) {
+  int4 r;
+  r.x = imin(grid_x, imax(0, f2i((px - (float)rx) / (float)kBlockX)));
+  r.y = imin(grid_y, imax(0, f2i((py - (float)ry) / (float)kBlockY)));
+  r.z = imin(grid_x, imax(0, f2i((px + (float)rx + (float)(kBlockX - 1)) / (float)kBlockX)));
+  r.w = imin(grid_y, imax(0, f2i((py + (float)ry + (float)(kBlockY - 1)) / (float)kBlockY)));
+  return r;
+}
+
+// Alpha-cutoff threshold of the conic quadratic form: 2*ln(max(255*o, 1)).
+__device__ __forceinline__ float coverage_threshold(float opacity) {
+  return 2.0f * log_sw(fmaxr(255.0f * opacity, 1.0f));
+}
+
+// Padded SnugBox (1/255 cut-off + one pixel) intersected with the 3-sigma rect.
+__device__ __forceinline__ int4 snugbox_rect(float px, float py, float cov_aa, float cov_cc, float opacity,
+                                             int cuda_radius, int grid_x, int grid_y) {
+  const int4 c = tile_rect(px, py, cuda_radius, cuda_radius, grid_x, grid_y);
+  const float t = coverage_threshold(opacity);
+  if (t <= 0.0f) return make_int4(0, 0, 0, 0);
+  const int rx = f2i(ceilf(sqrtf(fmaxr(t * cov_aa, 0.0f)) + kSnugPad));
+  const int ry = f2i(ceilf(sqrtf(fmaxr(t * cov_cc, 0.0f)) + kSnugPad));
+  const int4 s = tile_rect(px, py, rx, ry, grid_x, grid_y);
+  return make_int4(imax(c.x, s.x), imax(c.y, s.y), imin(c.z, s.z), imin(c.w, s.w));
+}
+
+__device__ __forceinline__ float conic_q(float x, float y, float a, float b, float c) {
+  return a * x * x + 2.0f * b * x * y + c * y * y;
+}
+
+__device__ __forceinline__ bool conic_rect_intersects_tile(float px, float py, float a, float b, float c,
+                                                           float threshold, int tile_x, int tile_y) {
+  const float det = a * c - b * b;
+  if (a <= 0.0f || c <= 0.0f || det <= kDetEps) return true;
+  const float x0 = (float)(tile_x * kBlockX) - px;
+  const float x1 = (float)(tile_x * kBlockX + kBlockX - 1) - px;
+  const float y0 = (float)(tile_y * kBlockY) - py;
+  const float y1 = (float)(tile_y * kBlockY + kBlockY - 1) - py;
+  if (x0 <= 0.0f && x1 >= 0.0f && y0 <= 0.0f && y1 >= 0.0f) return true;
+  float qmin = kFloatMax;
+  float y = clampr(-b * x0 / c, y0, y1);
+  qmin = fminr(qmin, conic_q(x0, y, a, b, c));
+  y = clampr(-b * x1 / c, y0, y1);
+  qmin = fminr(qmin, conic_q(x1, y, a, b, c));
+  float x = clampr(-b * y0 / a, x0, x1);
+  qmin = fminr(qmin, conic_q(x, y0, a, b, c));
+  x = clampr(-b * y1 / a, x0, x1);
+  qmin = fminr(qmin, conic_q(x, y1, a, b, c));
+  return qmin <= threshold + kQEps;
+}
+
+// Exact conic-ellipse interval along the u axis for one band of tiles at
+// tile_v, returned as a half-open tile range clamped to [u_min, u_max].
+__device__ __forceinline__ int2 accutile_band(float pu, float pv, float cuu, float cuv, float cvv,
+                                              float threshold, int tile_v, int block_u, int block_v,
+                                              int rect_u_min, int rect_u_max) {
+  const float det = cuu * cvv - cuv * cuv;
+  if (cuu <= 0.0f || cvv <= 0.0f || det <= kDetEps) return make_int2(rect_u_min, rect_u_max);
+  const float ts = threshold + kQEps;
+  const float v0 = (float)(tile_v * block_v) - pv;
+  const float v1 = (float)(tile_v * block_v + block_v - 1) - pv;
+  float umin = kFloatMax;
+  float umax = -kFloatMax;
+  bool found = false;
+  float disc = cuu * ts - det * v0 * v0;
+  if (disc >= -kQEps) {
+    const float half = sqrtf(fmaxr(disc, 0.0f)) / cuu;
+    const float center = -cuv * v0 / cuu;
+    umin = fminr(umin, center - half);
+    umax = fmaxr(umax, center + half);
+    found = true;
+  }
+  disc = cuu * ts - det * v1 * v1;
+  if (disc >= -kQEps) {
+    const float half = sqrtf(fmaxr(disc, 0.0f)) / cuu;
+    const float center = -cuv * v1 / cuu;
+    umin = fminr(umin, center - half);
+    umax = fmaxr(umax, center + half);
+    found = true;
+  }
+  const float ext = sqrtf(fmaxr(ts * cvv / det, 0.0f));
+  const float v_at_min = cuv * ext / cvv;
+  if (v_at_min >= v0 - kQEps && v_at_min <= v1 + kQEps) {
+    umin = fminr(umin, -ext);
+    umax = fmaxr(umax, -ext);
+    found = true;
+  }
+  const float v_at_max = -cuv * ext / cvv;
+  if (v_at_max >= v0 - kQEps && v_at_max <= v1 + kQEps) {
+    umin = fminr(umin, ext);
+    umax = fmaxr(umax, ext);
+    found = true;
+  }
+  if (!found) return make_int2(rect_u_min, rect_u_min);
+  const int tmin = f2i(floorf((pu + umin) / (float)block_u));
+  const int tmax = f2i(floorf((pu + umax) / (float)block_u)) + 1;
+  return make_int2(imax(rect_u_min, imin(rect_u_max, tmin)), imax(rect_u_min, imin(rect_u_max, tmax)));
+}
+
+// Number of tiles a Gaussian is binned to under the given coverage mode.
+// Mode kCoverageConicRect counts tiles exactly only up to kConicMaskMaxTiles
+// candidate tiles and falls back to AccuTile beyond that, which is the
+// effective behaviour of the reference binning stage for that mode.
+__device__ __forceinline__ int count_covered_tiles(float px, float py, float cov_aa, float cov_cc, float ca,
+                                                   float cb, float cc, float opacity, int cuda_radius,
+                                                   int grid_x, int grid_y, int mode) {
+  const int4 rect = snugbox_rect(px, py, cov_aa, cov_cc, opacity, cuda_radius, grid_x, grid_y);
+  const int span_x = rect.z - rect.x;
+  const int span_y = rect.w - rect.y;
+  const int area = span_x * span_y;
+  if (area <= 1) return area;
+  if (mode == kCoverageSnugbox) return area;
+  const float threshold = coverage_threshold(opacity);
+  int count = 0;
+  if (mode == kCoverageConicRect && area <= kConicMaskMaxTiles) {
+    for (int ty = rect.y; ty < rect.w; ++ty)
+      for (int tx = rect.x; tx < rect.z; ++tx)
+        if (conic_rect_intersects_tile(px, py, ca, cb, cc, threshold, tx, ty)) ++count;
+    return count;
+  }
+  if (span_y <= span_x) {
+    for (int ty = rect.y; ty < rect.w; ++ty) {
+      const int2 iv = accutile_band(px, py, ca, cb, cc, threshold, ty, kBlockX, kBlockY, rect.x, rect.z);
+      count += imax(0, iv.y - iv.x);
+    }
+  } else {
+    for (int tx = rect.x; tx < rect.z; ++tx) {
+      const int2 iv = accutile_band(py, px, cc, cb, ca, threshold, tx, kBlockY, kBlockX, rect.y, rect.w);
+      count += imax(0, iv.y - iv.x);
+    }
+  }
+  return count;
+}
+
+}  // namespace gs

@@ -1,0 +1,208 @@
+/*
+ * gswarp_hip.h — C ABI of the gfx950 3D Gaussian Splatting rasterizer.
+ *
+ * Every entry point is extern "C", takes device pointers, explicit sizes and
+ * a HIP stream (passed as void*, i.e. hipStream_t), enqueues its kernels on
+ * that stream and returns an int status: GS_OK (0), a GS_ERR_* code, or a
+ * positive hipError_t value.  No entry point allocates device memory or keeps
+ * mutable global state; scratch is always caller-provided and sized by the
+ * matching *_scratch_bytes query.  Calls on different streams with disjoint
+ * buffers may run concurrently.
+ *
+ * Each function replaces one stage of the reference host pipeline
+ * (fancifulland2718/gswarp 1.1.0, Warp backend); the stage it replaces is
+ * cited above its declaration as file:line under
+ * gswarp/_internal/backends/warp/.
+ *
+ * Layouts (N = Gaussians, K = SH coefficients per Gaussian, P = W*H pixels,
+ * T = ceil(W/16)*ceil(H/16) tiles, R = Gaussian/tile pairs):
+ *   means3d (N,3), scales (N,3), rotations (N,4) [w,x,y,z], opacities (N),
+ *   shs (N,K,3), colors (N,3), view/proj (4,4) row-vector convention,
+ *   campos (3), background (3): all fp32, C-contiguous.
+ *   records (N,12) fp32, 16-byte aligned: per-Gaussian render record
+ *     (x, y, conic_a, conic_b | conic_c, opacity, depth, power_cutoff |
+ *      r, g, b, 0).
+ *   images: color (3,H,W), depth (1,H,W), alpha (1,H,W), n_contrib (H,W) int32.
+ *   ranges (T,2) int32 [start, end) into the sorted pair list.
+ *   grad_gauss (N,10) fp32, zero-initialised by the caller, accumulated by
+ *     gs_render_bwd: (dx, dy, conic_a, conic_b, conic_c, opacity, r, g, b, depth).
+ */
+#ifndef GSWARP_HIP_H
+#define GSWARP_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GS_OK 0
+#define GS_ERR_INVALID_ARGUMENT (-1)
+#define GS_ERR_MISALIGNED (-2)
+#define GS_ERR_SCRATCH_TOO_SMALL (-3)
+#define GS_ERR_OVERFLOW (-4)
+
+#define GS_COVERAGE_SNUGBOX 0
+#define GS_COVERAGE_ACCUTILE_SWEEP 1
+#define GS_COVERAGE_CONIC_RECT 2
+
+#define GS_RECORD_FLOATS 12
+#define GS_GRAD_FLOATS 10
+
+/* Library version as 10000*major + 100*minor + patch. */
+int gs_version(void);
+
+/* Human-readable text for a status returned by any gs_* call. */
+const char* gs_status_string(int status);
+
+/*
+ * Fused preprocess: projection, near-plane cull, EWA 2D covariance, conic,
+ * radius, tile-rect cull, tile-coverage count and (when colors_precomp is
+ * NULL) SH colour of degree `degree` from K = sh_coeffs coefficients.
+ * Culled Gaussians get radius 0 and zero outputs; records are written only
+ * for visible Gaussians.  clamped (N bytes, optional) receives the per-channel
+ * clamp flags of the SH colour as bits 0..2.
+ * Replaces: preprocess_ops.py:289-581 (preprocess_gaussians, scales/rotations
+ * path) with preprocess_kernels.py:83-269 and the SH kernel
+ * preprocess_kernels.py:272-342.
+ */
+int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, const float* means3d,
+                      const float* scales, const float* rotations, float scale_modifier,
+                      const float* opacities, const float* shs, const float* colors_precomp,
+                      const float* viewmatrix, const float* projmatrix, const float* campos,
+                      float tanfovx, float tanfovy, float focal_x, float focal_y,
+                      int32_t image_width, int32_t image_height, int32_t coverage_mode,
+                      int32_t* radii, float* depths, float* proj_2d, float* conic_2d,
+                      float* conic_2d_inv, int32_t* tiles_touched, float* records,
+                      uint8_t* clamped, void* stream);
+
+/*
+ * visible[i] = view-space z of means3d[i] > 0.2.
+ * Replaces: preprocess_ops.py:584-595 (mark_visible) with
+ * preprocess_kernels.py:604-624.
+ */
+int gs_mark_visible(int32_t P, const float* means3d, const float* viewmatrix, uint8_t* visible,
+                    void* stream);
+
+/*
+ * Inclusive prefix sum of tiles_touched (point order) into offsets, plus the
+ * exact int64 total into *total_dev (device pointer).  offsets are only
+ * meaningful when the total fits in int32.
+ * Replaces: memory.py:539-551 (_inclusive_scan_i32) and
+ * binning_ops.py:62-81 (_wide_pair_count_if_needed).
+ */
+size_t gs_scan_scratch_bytes(int32_t P);
+int gs_scan_tiles(int32_t P, const int32_t* tiles_touched, int32_t* offsets, int64_t* total_dev,
+                  void* scratch, size_t scratch_bytes, void* stream);
+
+/*
+ * Copies the int64 at total_dev into caller-provided pinned host memory and
+ * waits for the stream: the single device-to-host synchronisation of a
+ * forward pass.
+ * Replaces: binning_ops.py:243-252 (the num_rendered .item()).
+ */
+int gs_num_rendered_readback(const int64_t* total_dev, int64_t* total_host_pinned, void* stream);
+
+/*
+ * For every Gaussian with radius > 0, emits one (key, value) pair per covered
+ * tile at offsets[i-1] (0 for i == 0): key = tile_id << 32 | float bits of
+ * depth, value = i.  Pairs are produced in point-index order; a stable sort
+ * by the 64-bit key then yields the reference's (tile, depth, index) order.
+ * Replaces: binning_kernels.py:411-451 with binning_kernels.py:127-216 and
+ * the depth sort that precedes it (binning_ops.py:152-222).
+ */
+int gs_duplicate_keys(int32_t P, const int32_t* radii, const float* records, const float* conic_2d_inv,
+                      const int32_t* offsets, int32_t image_width, int32_t image_height,
+                      int32_t coverage_mode, int64_t num_rendered, uint64_t* keys_out, int32_t* values_out,
+                      void* stream);
+
+/*
+ * Stable LSD radix sort of n (uint64 key, int32 value) pairs on the low
+ * key_bits bits of the key, 8 bits per pass, ping-ponging between
+ * (keys, values) and (keys_alt, values_alt).  The result ends in the primary
+ * buffers when gs_sort_num_passes(key_bits) is even, else in the _alt ones.
+ * Replaces: binning_ops.py:337-343 and memory.py:586-600
+ * (wp.utils.radix_sort_pairs on tile ids).
+ */
+int gs_sort_num_passes(int32_t key_bits);
+size_t gs_sort_scratch_bytes(int64_t n);
+int gs_sort_pairs_u64(int64_t n, int32_t key_bits, uint64_t* keys, int32_t* values, uint64_t* keys_alt,
+                      int32_t* values_alt, void* scratch, size_t scratch_bytes, void* stream);
+
+/*
+ * ranges[t] = [start, end) of tile t in the sorted keys; empty tiles [0, 0].
+ * Replaces: binning_kernels.py:468-487 (_identify_tile_ranges) and the zero
+ * fill at binning_ops.py:233.
+ */
+int gs_tile_ranges(int64_t n, const uint64_t* sorted_keys, int32_t num_tiles, int32_t* ranges, void* stream);
+
+/*
+ * Per-tile front-to-back alpha blending (16x16 tiles, one workgroup each).
+ * num_points (N) and num_rendered (R) bound every index read from ranges and
+ * point_list.
+ * Writes color + T*bg, alpha = sum of weights, depth (zero unless
+ * compute_depth) and n_contrib (1-based index of the last blended Gaussian).
+ * Replaces: render_ops.py:16-93 with render_kernels.py:16-147.
+ */
+int gs_render_fwd(int32_t image_width, int32_t image_height, int32_t num_points, int64_t num_rendered,
+                  const int32_t* ranges,
+                  const int32_t* point_list, const float* records, const float* background,
+                  int32_t compute_depth, float* out_color, float* out_depth, float* out_alpha,
+                  int32_t* n_contrib, void* stream);
+
+/*
+ * gs_render_fwd plus the flow auxiliaries of the first top_k blended
+ * Gaussians per pixel, front to back: ids (top_k,H,W) int32 (-1 when fewer),
+ * weights alpha*T (top_k,H,W), and x_mu (2,top_k,H,W) = mean - pixel.
+ * Every slot of every pixel is written.  With write_aux == 0 the aux
+ * pointers may be NULL.
+ * Replaces: flow_ops.py:109-193 with flow_kernels.py:31-176.
+ */
+int gs_render_fwd_flow(int32_t image_width, int32_t image_height, int32_t num_points, int64_t num_rendered,
+                       const int32_t* ranges,
+                       const int32_t* point_list, const float* records, const float* background,
+                       int32_t compute_depth, int32_t write_aux, int32_t top_k, float* out_color,
+                       float* out_depth, float* out_alpha, int32_t* n_contrib, int32_t* gs_per_pixel,
+                       float* weight_per_gs_pixel, float* x_mu, void* stream);
+
+/*
+ * Reverse blend: accumulates per-Gaussian gradients of the pixel loss into
+ * grad_gauss (N,10), which the caller zero-initialises.
+ * Replaces: backward_ops.py:183-290 with backward_kernels.py:539-707.
+ */
+int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t num_points, int64_t num_rendered,
+                  const int32_t* ranges,
+                  const int32_t* point_list, const float* records, const float* background,
+                  const float* out_alpha, const int32_t* n_contrib, const float* grad_color,
+                  const float* grad_depth, const float* grad_alpha, int32_t compute_depth,
+                  float* grad_gauss, void* stream);
+
+/*
+ * Fused per-Gaussian backward: SH colour backward (when shs != NULL), the
+ * projected-mean and depth gradients, cov2D -> cov3D -> scale/rotation
+ * gradients, and the accumulation into grad_means3d / grad_means2d (z = 0).
+ * flow_double != 0 adds the render xy/conic gradients a second time into the
+ * projected-mean and conic chains, as the reference flow backward does with
+ * enable_flow_grad.  grad_sh (N,K,3) is fully written (zeros beyond the
+ * evaluated bands); grad_opacity (N) and grad_colors (N,3, when non-NULL)
+ * are copied out of grad_gauss.
+ * Replaces: backward_ops.py:376-746 (fused path) with
+ * backward_kernels.py:53-295, backward_kernels.py:298-536 and
+ * flow_kernels.py:14-28.
+ */
+int gs_preprocess_bwd(int32_t P, int32_t sh_coeffs, int32_t degree, const float* means3d,
+                      const float* scales, const float* rotations, float scale_modifier,
+                      const float* shs, const float* campos, const float* viewmatrix,
+                      const float* projmatrix, float tanfovx, float tanfovy, float focal_x, float focal_y,
+                      const int32_t* radii, const uint8_t* clamped, const float* grad_gauss,
+                      const float* grad_proj_2d, const float* grad_conic_2d, const float* grad_conic_2d_inv,
+                      int32_t flow_double, float* grad_means3d, float* grad_means2d, float* grad_scales,
+                      float* grad_rotations, float* grad_sh, float* grad_opacity, float* grad_colors,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GSWARP_HIP_H */

@@ -1,0 +1,329 @@
+"""CPU oracle for the rasterizer path — TEST INFRASTRUCTURE ONLY.
+
+This package restates the fancifulland2718/gswarp 1.1.0 rasterizer (Warp
+backend) in plain C (``gs_oracle.c``) and exposes it through ctypes/numpy.
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import it, and only as the checker or the timed CPU
+baseline.  The product package ``gswarp_amd`` never imports it.
+
+Every wrapper takes and returns numpy arrays (float32 / int32, C-contiguous).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent
+SOURCE = ORACLE_DIR / "gs_oracle.c"
+LIB_PATH = ORACLE_DIR / "libgs_oracle.so"
+
+CFLAGS = (
+    "-O2",
+    "-std=c11",
+    "-fPIC",
+    "-shared",
+    "-fopenmp",
+    "-ffp-contract=off",
+    "-fno-fast-math",
+    "-fno-finite-math-only",
+)
+
+BLOCK = 16
+
+_lib = None
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile gs_oracle.c with gcc into libgs_oracle.so next to it."""
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = ["gcc", *CFLAGS, str(SOURCE), "-o", str(tmp), "-lm"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+_F = ctypes.POINTER(ctypes.c_float)
+_I = ctypes.POINTER(ctypes.c_int)
+_c_int = ctypes.c_int
+_c_float = ctypes.c_float
+_c_ll = ctypes.c_longlong
+
+_SIGNATURES = {
+    "or_exp": (_c_float, [_c_float]),
+    "or_log": (_c_float, [_c_float]),
+    "or_count_covered_tiles": (None, [_c_int, _F, _F, _F, _I, _c_int, _c_int, _c_int, _I]),
+    "or_emit_covered_tiles": (None, [_c_int, _F, _F, _F, _I, _c_int, _c_int, _c_int, _I, _I, _I]),
+    "or_preprocess": (
+        None,
+        [_c_int, _c_int, _c_int, _F, _F, _F, _c_float, _F, _F, _F, _F, _F, _F, _c_float, _c_float, _c_float,
+         _c_float, _c_int, _c_int, _c_int, _I, _F, _F, _F, _F, _I, _F, _F, _I, _I],
+    ),
+    "or_mark_visible": (None, [_c_int, _F, _F, _I]),
+    "or_num_rendered": (_c_ll, [_c_int, _I]),
+    "or_binning": (None, [_c_int, _I, _F, _I, _F, _F, _F, _c_int, _c_int, _c_int, _c_ll, _I, _I, _I]),
+    "or_render_fwd": (
+        None,
+        [_c_int, _c_int, _I, _I, _F, _F, _F, _F, _F, _c_int, _c_int, _F, _F, _F, _I, _I, _F, _F],
+    ),
+    "or_render_bwd": (
+        None,
+        [_c_int, _c_int, _c_int, _I, _I, _F, _F, _F, _F, _F, _F, _I, _F, _F, _F, _c_int, _F],
+    ),
+    "or_preprocess_bwd": (
+        None,
+        [_c_int, _c_int, _c_int, _F, _F, _F, _c_float, _F, _F, _F, _I, _F, _F, _c_float, _c_float, _c_float,
+         _c_float, _I, _F, _F, _F, _F, _c_int, _F, _F, _F, _F, _F],
+    ),
+    "or_num_threads": (_c_int, []),
+    "or_set_num_threads": (None, [_c_int]),
+}
+
+
+def lib():
+    """Load (building first if absent) the oracle shared library."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = handle
+    return _lib
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+def _fp(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data_as(_F)
+
+
+def _ip(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data_as(_I)
+
+
+def exp(x: float) -> float:
+    return float(lib().or_exp(float(x)))
+
+
+def log(x: float) -> float:
+    return float(lib().or_log(float(x)))
+
+
+def grid_dims(width: int, height: int) -> tuple[int, int]:
+    return (width + BLOCK - 1) // BLOCK, (height + BLOCK - 1) // BLOCK
+
+
+def set_num_threads(n: int) -> None:
+    lib().or_set_num_threads(int(n))
+
+
+def num_threads() -> int:
+    return int(lib().or_num_threads())
+
+
+def count_covered_tiles(points_xy, cov2d, conic_opacity, radii, grid_x, grid_y, mode=1) -> np.ndarray:
+    points_xy, cov2d, conic_opacity, radii = _f32(points_xy), _f32(cov2d), _f32(conic_opacity), _i32(radii)
+    n = radii.shape[0]
+    out = np.zeros(n, dtype=np.int32)
+    lib().or_count_covered_tiles(n, _fp(points_xy), _fp(cov2d), _fp(conic_opacity), _ip(radii), grid_x, grid_y,
+                                 mode, _ip(out))
+    return out
+
+
+def emit_covered_tiles(points_xy, cov2d, conic_opacity, radii, grid_x, grid_y, mode=1):
+    """(tile_ids, point_list, inclusive offsets) in point order."""
+    points_xy, cov2d, conic_opacity, radii = _f32(points_xy), _f32(cov2d), _f32(conic_opacity), _i32(radii)
+    counts = count_covered_tiles(points_xy, cov2d, conic_opacity, radii, grid_x, grid_y, mode)
+    counts = np.where(radii > 0, counts, 0).astype(np.int32)
+    offsets = np.cumsum(counts, dtype=np.int64).astype(np.int32)
+    total = int(offsets[-1]) if offsets.size else 0
+    tiles = np.full(total, -1, dtype=np.int32)
+    points = np.full(total, -1, dtype=np.int32)
+    n = radii.shape[0]
+    lib().or_emit_covered_tiles(n, _fp(points_xy), _fp(cov2d), _fp(conic_opacity), _ip(radii), grid_x, grid_y,
+                                mode, _ip(offsets), _ip(tiles), _ip(points))
+    return tiles, points, offsets
+
+
+def preprocess(means3d, scales, rotations, opacities, view, proj, campos, *, tanfovx, tanfovy, width, height,
+               scale_modifier=1.0, shs=None, degree=0, colors=None, coverage_mode=1) -> dict:
+    """Reference preprocess + SH colour (scales/rotations path)."""
+    means3d, scales, rotations = _f32(means3d), _f32(scales), _f32(rotations)
+    opacities = _f32(opacities).reshape(-1)
+    view, proj, campos = _f32(view).reshape(16), _f32(proj).reshape(16), _f32(campos).reshape(3)
+    P = means3d.shape[0]
+    K = 0
+    if shs is not None:
+        shs = _f32(shs).reshape(P, -1, 3)
+        K = shs.shape[1]
+    if colors is not None:
+        colors = _f32(colors).reshape(P, 3)
+    focal_x = np.float32(width / (2.0 * tanfovx))
+    focal_y = np.float32(height / (2.0 * tanfovy))
+    out = {
+        "radii": np.zeros(P, np.int32),
+        "depths": np.zeros(P, np.float32),
+        "proj_2d": np.zeros((P, 2), np.float32),
+        "conic_2d": np.zeros((P, 3), np.float32),
+        "conic_2d_inv": np.zeros((P, 3), np.float32),
+        "tiles_touched": np.zeros(P, np.int32),
+        "cov3d": np.zeros((P, 6), np.float32),
+        "rgb": np.zeros((P, 3), np.float32),
+        "clamped": np.zeros((P, 3), np.int32),
+        "visible": np.zeros(P, np.int32),
+    }
+    lib().or_preprocess(
+        P, K, degree, _fp(means3d), _fp(scales), _fp(rotations), float(scale_modifier), _fp(opacities),
+        _fp(shs), _fp(colors), _fp(view), _fp(proj), _fp(campos), float(np.float32(tanfovx)),
+        float(np.float32(tanfovy)), float(focal_x), float(focal_y), width, height, coverage_mode,
+        _ip(out["radii"]), _fp(out["depths"]), _fp(out["proj_2d"]), _fp(out["conic_2d"]), _fp(out["conic_2d_inv"]),
+        _ip(out["tiles_touched"]), _fp(out["cov3d"]), _fp(out["rgb"]), _ip(out["clamped"]), _ip(out["visible"]))
+    out["conic_opacity"] = np.concatenate([out["conic_2d"], opacities.reshape(P, 1)], axis=1)
+    out["conic_opacity"][out["radii"] <= 0] = 0.0
+    return out
+
+
+def mark_visible(means3d, view) -> np.ndarray:
+    means3d, view = _f32(means3d), _f32(view).reshape(16)
+    out = np.zeros(means3d.shape[0], np.int32)
+    lib().or_mark_visible(means3d.shape[0], _fp(means3d), _fp(view), _ip(out))
+    return out.astype(bool)
+
+
+def binning(pre: dict, width: int, height: int, coverage_mode=1) -> dict:
+    """Reference binning (depth sort, scan, duplicate, tile sort, ranges)."""
+    radii = _i32(pre["radii"])
+    P = radii.shape[0]
+    tiles_touched = _i32(pre["tiles_touched"])
+    R = int(lib().or_num_rendered(P, _ip(tiles_touched)))
+    grid_x, grid_y = grid_dims(width, height)
+    point_list = np.zeros(max(R, 1), np.int32)
+    tile_ids = np.zeros(max(R, 1), np.int32)
+    ranges = np.zeros((grid_x * grid_y, 2), np.int32)
+    lib().or_binning(P, _ip(radii), _fp(_f32(pre["depths"])), _ip(tiles_touched), _fp(_f32(pre["proj_2d"])),
+                     _fp(_f32(pre["conic_2d_inv"])), _fp(_f32(pre["conic_opacity"])), width, height, coverage_mode,
+                     R, _ip(point_list), _ip(tile_ids), _ip(ranges))
+    return {"num_rendered": R, "point_list": point_list[:R], "tile_ids": tile_ids[:R], "ranges": ranges}
+
+
+def render_fwd(pre: dict, bins: dict, features, background, width, height, *, compute_depth=True, top_k=0) -> dict:
+    features = _f32(features).reshape(-1, 3)
+    bg = _f32(background).reshape(3)
+    P = width * height
+    out = {
+        "color": np.zeros((3, height, width), np.float32),
+        "depth": np.zeros((1, height, width), np.float32),
+        "alpha": np.zeros((1, height, width), np.float32),
+        "n_contrib": np.zeros((height, width), np.int32),
+    }
+    ids = weights = x_mu = None
+    if top_k > 0:
+        ids = np.zeros((top_k, height, width), np.int32)
+        weights = np.zeros((top_k, height, width), np.float32)
+        x_mu = np.zeros((2, top_k, height, width), np.float32)
+    point_list = _i32(bins["point_list"]) if bins["num_rendered"] > 0 else np.zeros(1, np.int32)
+    lib().or_render_fwd(width, height, _ip(_i32(bins["ranges"])), _ip(point_list), _fp(_f32(pre["proj_2d"])),
+                        _fp(features), _fp(_f32(pre["depths"])), _fp(_f32(pre["conic_opacity"])), _fp(bg),
+                        int(bool(compute_depth)), int(top_k), _fp(out["color"]), _fp(out["depth"]),
+                        _fp(out["alpha"]), _ip(out["n_contrib"]), _ip(ids), _fp(weights), _fp(x_mu))
+    del P
+    if top_k > 0:
+        out.update(gs_per_pixel=ids, weight_per_gs_pixel=weights, x_mu=x_mu)
+    return out
+
+
+def render_bwd(pre: dict, bins: dict, features, background, width, height, fwd: dict, grad_color, grad_depth,
+               grad_alpha, *, compute_depth=True) -> np.ndarray:
+    """Per-Gaussian (N, 10) render gradients: dx, dy, conic a, b, c, opacity, rgb, depth."""
+    features = _f32(features).reshape(-1, 3)
+    N = features.shape[0]
+    out = np.zeros((N, 10), np.float32)
+    point_list = _i32(bins["point_list"]) if bins["num_rendered"] > 0 else np.zeros(1, np.int32)
+    lib().or_render_bwd(width, height, N, _ip(_i32(bins["ranges"])), _ip(point_list), _fp(_f32(pre["proj_2d"])),
+                        _fp(features), _fp(_f32(pre["depths"])), _fp(_f32(pre["conic_opacity"])),
+                        _fp(_f32(background).reshape(3)), _fp(_f32(fwd["alpha"])), _ip(_i32(fwd["n_contrib"])),
+                        _fp(_f32(grad_color)), _fp(_f32(grad_depth)), _fp(_f32(grad_alpha)),
+                        int(bool(compute_depth)), _fp(out))
+    return out
+
+
+def preprocess_bwd(pre: dict, grad_gauss, means3d, scales, rotations, view, proj, campos, *, tanfovx, tanfovy,
+                   width, height, scale_modifier=1.0, shs=None, degree=0, grad_proj_2d=None, grad_conic_2d=None,
+                   grad_conic_2d_inv=None, flow_double=False) -> dict:
+    means3d, scales, rotations = _f32(means3d), _f32(scales), _f32(rotations)
+    P = means3d.shape[0]
+    K = 0
+    if shs is not None:
+        shs = _f32(shs).reshape(P, -1, 3)
+        K = shs.shape[1]
+    zeros = lambda *s: np.zeros(s, np.float32)  # noqa: E731
+    grad_proj_2d = zeros(P, 2) if grad_proj_2d is None else _f32(grad_proj_2d)
+    grad_conic_2d = zeros(P, 3) if grad_conic_2d is None else _f32(grad_conic_2d)
+    grad_conic_2d_inv = zeros(P, 3) if grad_conic_2d_inv is None else _f32(grad_conic_2d_inv)
+    focal_x = np.float32(width / (2.0 * tanfovx))
+    focal_y = np.float32(height / (2.0 * tanfovy))
+    out = {
+        "means3D": zeros(P, 3),
+        "means2D": zeros(P, 3),
+        "scales": zeros(P, 3),
+        "rotations": zeros(P, 4),
+        "sh": zeros(P, max(K, 1), 3)[:, :K],
+    }
+    out["sh"] = np.ascontiguousarray(out["sh"])
+    lib().or_preprocess_bwd(
+        P, K, degree, _fp(means3d), _fp(scales), _fp(rotations), float(scale_modifier), _fp(_f32(pre["cov3d"])),
+        _fp(shs), _fp(_f32(campos).reshape(3)), _ip(_i32(pre["clamped"])), _fp(_f32(view).reshape(16)),
+        _fp(_f32(proj).reshape(16)), float(np.float32(tanfovx)), float(np.float32(tanfovy)), float(focal_x),
+        float(focal_y), _ip(_i32(pre["radii"])), _fp(_f32(grad_gauss)), _fp(grad_proj_2d), _fp(grad_conic_2d),
+        _fp(grad_conic_2d_inv), int(bool(flow_double)), _fp(out["means3D"]), _fp(out["means2D"]),
+        _fp(out["scales"]), _fp(out["rotations"]), _fp(out["sh"]) if K > 0 else None)
+    gg = _f32(grad_gauss)
+    out["opacities"] = gg[:, 5:6].copy()
+    out["colors"] = gg[:, 6:9].copy()
+    return out
+
+
+def rasterize(scene: dict, *, coverage_mode=1, compute_depth=True, top_k=0) -> dict:
+    """Full forward on a scene dict (numpy arrays) as produced by gswarp_amd.configs."""
+    s = scene
+    pre = preprocess(s["means3D"], s["scales"], s["rotations"], s["opacities"], s["viewmatrix"], s["projmatrix"],
+                     s["campos"], tanfovx=s["tanfovx"], tanfovy=s["tanfovy"], width=s["width"], height=s["height"],
+                     scale_modifier=s.get("scale_modifier", 1.0), shs=s.get("shs"), degree=s.get("sh_degree", 0),
+                     colors=s.get("colors_precomp"), coverage_mode=coverage_mode)
+    bins = binning(pre, s["width"], s["height"], coverage_mode)
+    fwd = render_fwd(pre, bins, pre["rgb"], s["bg"], s["width"], s["height"], compute_depth=compute_depth,
+                     top_k=top_k)
+    return {"pre": pre, "bins": bins, "fwd": fwd}
+
+
+def rasterize_backward(scene: dict, result: dict, grad_color, grad_depth, grad_alpha, *, compute_depth=True,
+                       grad_proj_2d=None, grad_conic_2d=None, grad_conic_2d_inv=None, flow_double=False) -> dict:
+    """Full backward matching the reference's gradient tuple (as a dict)."""
+    s = scene
+    pre, bins, fwd = result["pre"], result["bins"], result["fwd"]
+    gg = render_bwd(pre, bins, pre["rgb"], s["bg"], s["width"], s["height"], fwd, grad_color,
+                    grad_depth if grad_depth is not None else np.zeros_like(fwd["depth"]), grad_alpha,
+                    compute_depth=compute_depth)
+    grads = preprocess_bwd(pre, gg, s["means3D"], s["scales"], s["rotations"], s["viewmatrix"], s["projmatrix"],
+                           s["campos"], tanfovx=s["tanfovx"], tanfovy=s["tanfovy"], width=s["width"],
+                           height=s["height"], scale_modifier=s.get("scale_modifier", 1.0), shs=s.get("shs"),
+                           degree=s.get("sh_degree", 0), grad_proj_2d=grad_proj_2d, grad_conic_2d=grad_conic_2d,
+                           grad_conic_2d_inv=grad_conic_2d_inv, flow_double=flow_double)
+    grads["grad_gauss"] = gg
+    return grads

@@ -1,0 +1,158 @@
+"""Parity of every gfx950 stage with the CPU oracle on seeded scenes.
+
+Bar (from the build's north star): radii, tile counts, sorted keys, point
+lists and tile ranges bit-exact; colour / depth / alpha within 1e-4
+absolute; flow top-K ids exact; gradients within 1e-3 relative with the
+floor documented in helpers.grad_mismatch.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gswarp_amd import _pipeline, configs
+from helpers import gpu_forward, grad_mismatch, options, oracle_forward, to_np
+
+pytestmark = pytest.mark.gpu
+
+CASES = {
+    "c0_full": dict(config=0),
+    "c1_full": dict(config=1),
+    "c2_small": dict(config=2, count=60_000, width=480, height=270),
+    "c3_small": dict(config=3, count=60_000, width=480, height=270),
+    "c4_small": dict(config=4, count=40_000, width=320, height=180),
+    "c1_ragged": dict(config=1, count=5_000, width=203, height=117),
+}
+
+COLOR_ATOL = 1e-4
+
+
+def _scene(name, device, seed=0):
+    kw = dict(CASES[name])
+    cfg = kw.pop("config")
+    return configs.make_scene(cfg, seed=seed, device=device, **kw)
+
+
+def _check_forward(scene, opts, *, coverage_mode=1, flow=False, top_k=0, colors=False):
+    print(f"[parity] N={scene['means3D'].shape[0]} {scene['width']}x{scene['height']} cov={coverage_mode} "
+          f"flow={flow} colors={colors}", flush=True)
+    out = gpu_forward(scene, opts, flow=flow, colors=colors)
+    host, ref = oracle_forward(scene, coverage_mode=coverage_mode, compute_depth=opts.compute_depth,
+                               top_k=top_k, colors=colors)
+    pre, bins, res = out["pre"], out["bins"], out["res"]
+    rp, rb, rf = ref["pre"], ref["bins"], ref["fwd"]
+    # preprocess: integer outputs bit-exact, float outputs bit-exact too
+    assert np.array_equal(to_np(pre.radii), rp["radii"])
+    assert np.array_equal(to_np(pre.tiles_touched), rp["tiles_touched"])
+    for key in ("proj_2d", "conic_2d", "conic_2d_inv", "depths"):
+        assert np.array_equal(to_np(getattr(pre, key)), rp[key]), key
+    vis = rp["radii"] > 0
+    rgb = to_np(pre.records)[:, 8:11]
+    assert np.array_equal(rgb[vis], rp["rgb"][vis])
+    # binning
+    assert bins.num_rendered == rb["num_rendered"]
+    if bins.num_rendered:
+        assert np.array_equal(to_np(bins.point_list), rb["point_list"])
+        keys = to_np(bins.sorted_keys).view(np.uint64)
+        assert np.array_equal((keys >> np.uint64(32)).astype(np.int64), rb["tile_ids"].astype(np.int64))
+        depth_bits = (keys & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+        assert np.array_equal(depth_bits, rp["depths"].view(np.uint32)[rb["point_list"]])
+    assert np.array_equal(to_np(bins.ranges), rb["ranges"])
+    # render
+    assert np.array_equal(to_np(res.n_contrib).reshape(rf["n_contrib"].shape), rf["n_contrib"])
+    for key, t in (("color", res.color), ("depth", res.depth), ("alpha", res.alpha)):
+        err = float(np.abs(to_np(t) - rf[key]).max())
+        assert err <= COLOR_ATOL, (key, err)
+    if flow and top_k:
+        assert np.array_equal(to_np(res.aux[0]), rf["gs_per_pixel"])
+        assert float(np.abs(to_np(res.aux[1]) - rf["weight_per_gs_pixel"]).max()) <= COLOR_ATOL
+        assert float(np.abs(to_np(res.aux[2]) - rf["x_mu"]).max()) <= COLOR_ATOL
+    return out, host, ref
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_forward_stages_match_oracle(case, device):
+    scene = _scene(case, device)
+    flow = CASES[case]["config"] == 4
+    _check_forward(scene, options(flow=flow), flow=flow, top_k=20 if flow else 0)
+
+
+@pytest.mark.parametrize("coverage_mode", [0, 2])
+def test_alternative_coverage_modes_match_oracle(coverage_mode, device):
+    scene = configs.make_scene(1, count=20_000, width=320, height=256, device=device)
+    _check_forward(scene, options(coverage_mode=coverage_mode), coverage_mode=coverage_mode)
+
+
+def test_depth_off_matches_oracle(device):
+    scene = configs.make_scene(2, count=20_000, width=320, height=200, device=device)
+    _check_forward(scene, options(compute_depth=False))
+
+
+def test_colors_precomp_matches_oracle(device):
+    scene = configs.make_scene(1, count=20_000, width=256, height=256, device=device)
+    _check_forward(scene, options(), colors=True)
+
+
+def _upstream(scene, seed, with_meta=True):
+    H, W, N = scene["height"], scene["width"], scene["means3D"].shape[0]
+    g = torch.Generator().manual_seed(seed)
+    dev = scene["means3D"].device
+    grads = {
+        "color": torch.randn(3, H, W, generator=g),
+        "depth": torch.randn(1, H, W, generator=g),
+        "alpha": torch.randn(1, H, W, generator=g),
+        "proj_2d": torch.randn(N, 2, generator=g) * (1e-2 if with_meta else 0.0),
+        "conic_2d": torch.randn(N, 3, generator=g) * (1e-2 if with_meta else 0.0),
+        "conic_2d_inv": torch.randn(N, 3, generator=g) * (1e-2 if with_meta else 0.0),
+    }
+    return {k: v.to(dev) for k, v in grads.items()}
+
+
+def _check_backward(scene, *, flow_double=False, compute_depth=True, colors=False, seed=3):
+    opts = options(compute_depth=compute_depth)
+    out = gpu_forward(scene, opts, colors=colors)
+    host, ref = oracle_forward(scene, compute_depth=compute_depth, colors=colors)
+    up = _upstream(scene, seed)
+    with torch.cuda.device(scene["means3D"].device):
+        grads = _pipeline.backward(out["inputs"], out["pre"].radii, out["res"].alpha, up["color"], up["depth"],
+                                   up["alpha"], up["proj_2d"], up["conic_2d"], up["conic_2d_inv"], opts,
+                                   _pipeline.ForwardState(out["pre"], out["bins"], out["res"].n_contrib),
+                                   flow_double=flow_double)
+    torch.cuda.synchronize()
+    g_means2d, g_colors, g_opac, g_means3d, _g_cov, g_sh, g_scales, g_rot = grads
+    ref_g = __import__("oracle").rasterize_backward(
+        host, ref, to_np(up["color"]), to_np(up["depth"]), to_np(up["alpha"]), compute_depth=compute_depth,
+        grad_proj_2d=to_np(up["proj_2d"]), grad_conic_2d=to_np(up["conic_2d"]),
+        grad_conic_2d_inv=to_np(up["conic_2d_inv"]), flow_double=flow_double)
+    checks = [("means2D", g_means2d, ref_g["means2D"]), ("opacities", g_opac, ref_g["opacities"]),
+              ("means3D", g_means3d, ref_g["means3D"]), ("scales", g_scales, ref_g["scales"]),
+              ("rotations", g_rot, ref_g["rotations"])]
+    if colors:
+        checks.append(("colors", g_colors, ref_g["colors"]))
+    else:
+        checks.append(("sh", g_sh, ref_g["sh"]))
+    failures = []
+    for name, actual, expected in checks:
+        a = to_np(actual).reshape(expected.shape)
+        bad, worst = grad_mismatch(a, expected)
+        print(f"[grad] {name}: mismatches={bad} worst_ratio={worst:.3f} max|e|={np.abs(expected).max():.3e}",
+              flush=True)
+        if bad:
+            failures.append((name, bad, worst))
+    assert not failures, failures
+
+
+@pytest.mark.parametrize("case", ["c1_full", "c2_small", "c3_small", "c1_ragged"])
+def test_backward_matches_oracle(case, device):
+    _check_backward(_scene(case, device))
+
+
+def test_flow_backward_doubling_matches_oracle(device):
+    _check_backward(_scene("c4_small", device), flow_double=True)
+
+
+def test_backward_depth_off_and_colors_precomp(device):
+    scene = configs.make_scene(2, count=20_000, width=320, height=200, device=device)
+    _check_backward(scene, compute_depth=False, colors=True)
