@@ -1,0 +1,289 @@
+#!/usr/bin/env python
+"""Benchmark of the gfx950 rasterizer: forward + backward on one MI355X.
+
+Workload: 1,000,000 fp32 Gaussians, 1920x1080, SH degree
+3, forward with depth and alpha outputs plus the manual backward, upstream
+gradients ~N(0,1) on colour, depth and alpha, camera direction re-drawn per
+iteration from the seed.  One step = one forward + backward through the
+public ``GaussianRasterizer`` and ``torch.autograd.backward``.
+
+Prints ONE JSON line on stdout (everything else goes to stderr) with the
+metric Gaussians/s = N / t(fwd+bwd), the per-stage times measured live with
+HIP events on the launch stream, the HBM-roofline fraction of the dominant
+kernel and of the whole iteration, and the CPU baseline (the C oracle on
+this host's cores, one fwd+bwd of the same scene).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from collections import defaultdict
+from contextlib import contextmanager
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, GB/s
+METRIC = "fwd+bwd ms/iter & Gaussians/s @1M Gaussians 1080p SH3; % HBM roofline"
+
+
+def log(*args):
+    print(*args, file=sys.stderr, flush=True)
+
+
+class StageTimer:
+    """Records a pair of HIP events around each pipeline stage on the current stream."""
+
+    def __init__(self):
+        import torch
+
+        self.torch = torch
+        self.enabled = False
+        self.events = defaultdict(list)
+        self.notes = defaultdict(list)
+
+    @contextmanager
+    def __call__(self, name):
+        if not self.enabled:
+            yield
+            return
+        torch = self.torch
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        try:
+            yield
+        finally:
+            end.record()
+            self.events[name].append((start, end))
+
+    def note(self, key, value):
+        if self.enabled:
+            self.notes[key].append(value)
+
+    def mean_ms(self) -> dict:
+        return {name: sum(s.elapsed_time(e) for s, e in pairs) / len(pairs) for name, pairs in self.events.items()}
+
+
+def sort_passes(tiles: int) -> int:
+    return math.ceil((32 + math.ceil(math.log2(tiles))) / 8)
+
+
+def algorithmic_bytes(N: int, R: float, P: int, T: int) -> dict:
+    """Bytes crossing each stage boundary once (the SH3, depth-on accounting of the
+    reference dataflow): preprocess 112N + SH 228N, scan 8N, duplicate 44N + 12R,
+    sort passes*24R, ranges 8R + 8T, render 44R + 24P + 8T, render backward
+    44R + 28P + 40N + 8T, SH + preprocess backward 624N."""
+    return {
+        "preprocess": 340.0 * N,
+        "scan": 8.0 * N,
+        "duplicate": 44.0 * N + 12.0 * R,
+        "sort": sort_passes(T) * 24.0 * R,
+        "ranges": 8.0 * R + 8.0 * T,
+        "render": 44.0 * R + 24.0 * P + 8.0 * T,
+        "render_bwd": 44.0 * R + 28.0 * P + 40.0 * N + 8.0 * T,
+        "preprocess_bwd": 624.0 * N,
+    }
+
+
+def read_traffic(stage: str):
+    """HBM bytes per launch of a stage from the committed rocprofv3 PMC summary, if present."""
+    path = ROOT / "profiles" / "traffic_config2.txt"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        parts = line.split()
+        if len(parts) >= 2 and parts[0] == f"{stage}:":
+            try:
+                return float(parts[1])
+            except ValueError:
+                return None
+    return None
+
+
+def cpu_baseline(scene, grads) -> dict:
+    """One fwd+bwd of the same scene with the C oracle on this host's cores."""
+    import oracle
+    from gswarp_amd import configs
+
+    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16")), 16)
+    oracle.set_num_threads(threads)
+    host = configs.scene_to_numpy(scene)
+    g = {k: v.detach().cpu().numpy() for k, v in grads.items()}
+    t0 = time.perf_counter()
+    res = oracle.rasterize(host)
+    oracle.rasterize_backward(host, res, g["color"], g["depth"], g["alpha"])
+    dt = time.perf_counter() - t0
+    n = host["means3D"].shape[0]
+    return {
+        "value": n / dt,
+        "unit": "Gaussians/s",
+        "cores": oracle.num_threads(),
+        "kind": "port",
+        "sample": f"one fwd+bwd of the iteration-0 view of this workload ({n} Gaussians) by the C oracle "
+                  f"(oracle/gs_oracle.c, OpenMP), {dt:.2f} s",
+        "seconds": dt,
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4))
+    parser.add_argument("--count", type=int, default=None, help="override the Gaussian count")
+    parser.add_argument("--seed", type=int, default=0)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-stage-timing", action="store_true")
+    args = parser.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(view-parallel sharding is a design note). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from gswarp_amd import _pipeline, configs
+    from gswarp_amd.rasterizer import GaussianRasterizationSettings, GaussianRasterizer
+    from gswarp_amd.rasterizer_flow import GaussianRasterizationSettings as FlowSettings
+    from gswarp_amd.rasterizer_flow import GaussianRasterizer as FlowRasterizer
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    spec = configs.CONFIGS[args.config]
+    t0 = time.perf_counter()
+    scene = configs.make_scene(args.config, seed=args.seed, count=args.count, device=device)
+    N = scene["means3D"].shape[0]
+    W, H = scene["width"], scene["height"]
+    P = W * H
+    T = ((W + 15) // 16) * ((H + 15) // 16)
+    grads = configs.upstream_gradients(args.config, W, H, seed=args.seed, device=device)
+    total_steps = args.warmup + args.steps
+    if args.config in (2, 3, 4):  # view direction re-drawn per iteration
+        cams = [configs.orbit_camera(spec, args.seed, it) for it in range(total_steps)]
+    else:
+        cams = [scene] * total_steps
+    flow = spec.flow
+    settings = []
+    for cam in cams:
+        common = dict(image_height=H, image_width=W, tanfovx=cam["tanfovx"], tanfovy=cam["tanfovy"],
+                      bg=scene["bg"], scale_modifier=1.0, viewmatrix=cam["viewmatrix"].to(device),
+                      projmatrix=cam["projmatrix"].to(device), sh_degree=spec.sh_degree,
+                      campos=cam["campos"].to(device), prefiltered=False, auto_tune=False, auto_tune_verbose=False)
+        settings.append(FlowSettings(**common, enable_flow_grad=True, compute_flow_aux=True) if flow
+                        else GaussianRasterizationSettings(**common))
+    leaves = {k: scene[k].clone().requires_grad_(True) for k in ("means3D", "scales", "rotations", "opacities", "shs")}
+    means2D = torch.zeros_like(leaves["means3D"], requires_grad=True)
+    log(f"[bench] config {args.config}: N={N} {W}x{H} SH{spec.sh_degree} setup {time.perf_counter() - t0:.1f}s")
+
+    timer = StageTimer()
+    _pipeline.STAGE_TIMER = timer
+    step_events = []
+
+    def step(i: int, timed: bool):
+        for t in (*leaves.values(), means2D):
+            t.grad = None
+        rast = (FlowRasterizer if flow else GaussianRasterizer)(settings[i])
+        e0 = e1 = e2 = None
+        if timed:
+            e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+            e0.record()
+        out = rast(leaves["means3D"], means2D, leaves["opacities"], shs=leaves["shs"], scales=leaves["scales"],
+                   rotations=leaves["rotations"])
+        if timed:
+            e1.record()
+        if flow:
+            outputs, upstream = [out[0], out[9]], [grads["color"], grads["x_mu"]]
+        else:
+            color, _radii, meta = out
+            outputs, upstream = [color, meta.depth, meta.alpha], [grads["color"], grads["depth"], grads["alpha"]]
+        torch.autograd.backward(outputs, upstream)
+        if timed:
+            e2.record()
+            step_events.append((e0, e1, e2))
+
+    for i in range(args.warmup):
+        step(i, False)
+    torch.cuda.synchronize()
+    timer.enabled = not args.no_stage_timing
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for i in range(args.warmup, total_steps):
+        step(i, True)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    timer.enabled = False
+    _pipeline.STAGE_TIMER = None
+
+    ms_per_step = 1000.0 * elapsed / args.steps
+    fwd_ms = sum(a.elapsed_time(b) for a, b, _ in step_events) / len(step_events)
+    bwd_ms = sum(b.elapsed_time(c) for _, b, c in step_events) / len(step_events)
+    stage_ms = timer.mean_ms() if not args.no_stage_timing else {}
+    Rs = timer.notes.get("num_rendered", [])
+    R = sum(Rs) / len(Rs) if Rs else float("nan")
+    log(f"[bench] {ms_per_step:.3f} ms/step (fwd {fwd_ms:.3f} ms, bwd {bwd_ms:.3f} ms), mean R={R:.0f}")
+
+    roofline = None
+    stages = {}
+    if stage_ms and Rs:
+        algo = algorithmic_bytes(N, R, P, T)
+        for name, ms in sorted(stage_ms.items(), key=lambda kv: -kv[1]):
+            gbps = algo[name] / (ms * 1e-3) / 1e9 if name in algo else None
+            stages[name] = {"ms": round(ms, 4), "algorithmic_bytes": algo.get(name),
+                            "achieved_GBps": None if gbps is None else round(gbps, 1),
+                            "hbm_frac": None if gbps is None else round(gbps / HBM_PEAK_GBPS, 4)}
+            log(f"[bench]   {name:15s} {ms:8.4f} ms" + ("" if gbps is None else f"  {gbps:8.1f} GB/s"))
+        dominant = max((n for n in stage_ms if n in algo), key=lambda n: stage_ms[n])
+        achieved = algo[dominant] / (stage_ms[dominant] * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 5),
+                    "traffic": read_traffic(dominant),
+                    "algorithmic_bytes_per_launch": algo[dominant]}
+    iteration_bytes = 1056.0 * N + 252.0 * R + 52.0 * P + 24.0 * T if Rs else None
+
+    result = {
+        "metric": METRIC,
+        "value": N / (ms_per_step * 1e-3),
+        "unit": "Gaussians/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded Gaussians and cameras, BASELINE config distributions)",
+        "config": {"workload": f"config{args.config}: {spec.description}", "gaussians": N, "width": W,
+                   "height": H, "sh_degree": spec.sh_degree, "tiles": T, "mean_num_rendered": R,
+                   "parallelism": "single GPU"},
+        "fwd_ms": fwd_ms,
+        "bwd_ms": bwd_ms,
+        "fwd_bwd_ms": ms_per_step,
+        "iteration_hbm_frac": None if iteration_bytes is None else
+        round(iteration_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 5),
+        "stages": stages,
+        "roofline": roofline,
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline (oracle) ...")
+        result["cpu_baseline"] = cpu_baseline(scene, grads)  # the scene carries the iteration-0 camera
+        log(f"[bench] CPU baseline {result['cpu_baseline']['seconds']:.2f} s on "
+            f"{result['cpu_baseline']['cores']} threads")
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

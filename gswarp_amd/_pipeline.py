@@ -12,6 +12,7 @@ pair-count readback of the binning stage.
 
 from __future__ import annotations
 
+import contextlib
 from dataclasses import dataclass
 
 import torch
@@ -25,6 +26,16 @@ BLOCK_X = 16
 BLOCK_Y = 16
 NUM_CHANNELS = 3
 MAX_BINNING_PAIRS = (1 << 31) - 1
+
+# Optional per-stage timer: a callable(stage_name) returning a context
+# manager that brackets the stage's launches (used by bench.py to record
+# HIP events on the launch stream).  None disables it.
+STAGE_TIMER = None
+
+
+def _stage(name: str):
+    timer = STAGE_TIMER
+    return timer(name) if timer is not None else contextlib.nullcontext()
 
 
 @dataclass(slots=True)
@@ -168,13 +179,14 @@ def preprocess(inputs: RasterInputs, options: ExecutionOptions) -> PreprocessOut
     view_c = _f32c(inputs.viewmatrix)
     proj_c = _f32c(inputs.projmatrix)
     campos_c = _f32c(inputs.campos)
-    lib.call(
-        "gs_preprocess_fwd", P, K, int(inputs.degree), means_c.data_ptr(), scales_c.data_ptr(), rot_c.data_ptr(),
-        float(inputs.scale_modifier), opac_c.data_ptr(), _lib.ptr(shs), _lib.ptr(colors), view_c.data_ptr(),
-        proj_c.data_ptr(), campos_c.data_ptr(), tanfovx, tanfovy, _focal(W, tanfovx), _focal(H, tanfovy), W, H,
-        out.coverage_mode, out.radii.data_ptr(), out.depths.data_ptr(), out.proj_2d.data_ptr(),
-        out.conic_2d.data_ptr(), out.conic_2d_inv.data_ptr(), out.tiles_touched.data_ptr(), out.records.data_ptr(),
-        out.clamped.data_ptr(), _stream(device))
+    with _stage("preprocess"):
+        lib.call(
+            "gs_preprocess_fwd", P, K, int(inputs.degree), means_c.data_ptr(), scales_c.data_ptr(),
+            rot_c.data_ptr(), float(inputs.scale_modifier), opac_c.data_ptr(), _lib.ptr(shs), _lib.ptr(colors),
+            view_c.data_ptr(), proj_c.data_ptr(), campos_c.data_ptr(), tanfovx, tanfovy, _focal(W, tanfovx),
+            _focal(H, tanfovy), W, H, out.coverage_mode, out.radii.data_ptr(), out.depths.data_ptr(),
+            out.proj_2d.data_ptr(), out.conic_2d.data_ptr(), out.conic_2d_inv.data_ptr(),
+            out.tiles_touched.data_ptr(), out.records.data_ptr(), out.clamped.data_ptr(), _stream(device))
     return out
 
 
@@ -192,11 +204,14 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
     offsets = torch.empty((P,), dtype=torch.int32, device=device)
     total = torch.empty((1,), dtype=torch.int64, device=device)
     scan_scratch = torch.empty((max(int(lib.gs_scan_scratch_bytes(P)), 1),), dtype=torch.uint8, device=device)
-    lib.call("gs_scan_tiles", P, pre.tiles_touched.data_ptr(), offsets.data_ptr(), total.data_ptr(),
-             scan_scratch.data_ptr(), scan_scratch.numel(), stream)
+    with _stage("scan"):
+        lib.call("gs_scan_tiles", P, pre.tiles_touched.data_ptr(), offsets.data_ptr(), total.data_ptr(),
+                 scan_scratch.data_ptr(), scan_scratch.numel(), stream)
     pinned = _workspace.readback_buffer(device, torch.cuda.current_stream(device))
     lib.call("gs_num_rendered_readback", total.data_ptr(), pinned.data_ptr(), stream)
     R = validate_pair_count(int(pinned[0]))
+    if STAGE_TIMER is not None and hasattr(STAGE_TIMER, "note"):
+        STAGE_TIMER.note("num_rendered", R)
     if R == 0:
         return BinningState(grid_x, grid_y, torch.empty((0,), dtype=torch.int32, device=device),
                             torch.zeros((T, 2), dtype=torch.int32, device=device), 0)
@@ -204,17 +219,20 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
     vals = torch.empty((R,), dtype=torch.int32, device=device)
     keys_alt = torch.empty((R,), dtype=torch.int64, device=device)
     vals_alt = torch.empty((R,), dtype=torch.int32, device=device)
-    lib.call("gs_duplicate_keys", P, pre.radii.data_ptr(), pre.records.data_ptr(), pre.conic_2d_inv.data_ptr(),
-             offsets.data_ptr(), image_width, image_height, pre.coverage_mode, R, keys.data_ptr(), vals.data_ptr(),
-             stream)
+    with _stage("duplicate"):
+        lib.call("gs_duplicate_keys", P, pre.radii.data_ptr(), pre.records.data_ptr(),
+                 pre.conic_2d_inv.data_ptr(), offsets.data_ptr(), image_width, image_height, pre.coverage_mode, R,
+                 keys.data_ptr(), vals.data_ptr(), stream)
     key_bits = 32 + (T - 1).bit_length()
     sort_scratch = torch.empty((max(int(lib.gs_sort_scratch_bytes(R)), 1),), dtype=torch.uint8, device=device)
-    lib.call("gs_sort_pairs_u64", R, key_bits, keys.data_ptr(), vals.data_ptr(), keys_alt.data_ptr(),
-             vals_alt.data_ptr(), sort_scratch.data_ptr(), sort_scratch.numel(), stream)
+    with _stage("sort"):
+        lib.call("gs_sort_pairs_u64", R, key_bits, keys.data_ptr(), vals.data_ptr(), keys_alt.data_ptr(),
+                 vals_alt.data_ptr(), sort_scratch.data_ptr(), sort_scratch.numel(), stream)
     if lib.gs_sort_num_passes(key_bits) % 2:
         keys, vals = keys_alt, vals_alt
     ranges = torch.empty((T, 2), dtype=torch.int32, device=device)
-    lib.call("gs_tile_ranges", R, keys.data_ptr(), T, ranges.data_ptr(), stream)
+    with _stage("ranges"):
+        lib.call("gs_tile_ranges", R, keys.data_ptr(), T, ranges.data_ptr(), stream)
     return BinningState(grid_x, grid_y, vals, ranges, R, keys if keep_keys else None)
 
 
@@ -250,15 +268,17 @@ def render(pre: PreprocessOutputs, bins: BinningState, background: torch.Tensor,
                    torch.empty((2, k, H, W), **f))
         else:
             aux = _empty_flow_aux(0, H, W, device)
-        lib.call("gs_render_fwd_flow", W, H, P, bins.num_rendered, bins.ranges.data_ptr(), bins.point_list.data_ptr(),
-                 pre.records.data_ptr(), bg.data_ptr(), compute_depth, int(write_aux), k, color.data_ptr(),
-                 depth.data_ptr(), alpha.data_ptr(), n_contrib.data_ptr(),
-                 aux[0].data_ptr() if write_aux else None, aux[1].data_ptr() if write_aux else None,
-                 aux[2].data_ptr() if write_aux else None, stream)
+        with _stage("render"):
+            lib.call("gs_render_fwd_flow", W, H, P, bins.num_rendered, bins.ranges.data_ptr(),
+                     bins.point_list.data_ptr(), pre.records.data_ptr(), bg.data_ptr(), compute_depth,
+                     int(write_aux), k, color.data_ptr(), depth.data_ptr(), alpha.data_ptr(), n_contrib.data_ptr(),
+                     aux[0].data_ptr() if write_aux else None, aux[1].data_ptr() if write_aux else None,
+                     aux[2].data_ptr() if write_aux else None, stream)
     else:
-        lib.call("gs_render_fwd", W, H, P, bins.num_rendered, bins.ranges.data_ptr(), bins.point_list.data_ptr(), pre.records.data_ptr(),
-                 bg.data_ptr(), compute_depth, color.data_ptr(), depth.data_ptr(), alpha.data_ptr(),
-                 n_contrib.data_ptr(), stream)
+        with _stage("render"):
+            lib.call("gs_render_fwd", W, H, P, bins.num_rendered, bins.ranges.data_ptr(),
+                     bins.point_list.data_ptr(), pre.records.data_ptr(), bg.data_ptr(), compute_depth,
+                     color.data_ptr(), depth.data_ptr(), alpha.data_ptr(), n_contrib.data_ptr(), stream)
     return RenderStageResult(color, depth, alpha, n_contrib, aux)
 
 
@@ -327,10 +347,11 @@ def backward(inputs: RasterInputs, radii: torch.Tensor, alpha: torch.Tensor, gra
             gd = _zeros_if_none(grad_depth, (1, H, W), device)
             ga = _zeros_if_none(grad_alpha, (1, H, W), device)
             alpha_c = _f32c(alpha)
-            lib.call("gs_render_bwd", W, H, P, bins.num_rendered, bins.ranges.data_ptr(), bins.point_list.data_ptr(),
-                     pre.records.data_ptr(), bg.data_ptr(), alpha_c.data_ptr(), n_contrib.data_ptr(),
-                     gc.data_ptr(), gd.data_ptr(), ga.data_ptr(), int(bool(options.compute_depth)),
-                     grad_gauss.data_ptr(), stream)
+            with _stage("render_bwd"):
+                lib.call("gs_render_bwd", W, H, P, bins.num_rendered, bins.ranges.data_ptr(),
+                         bins.point_list.data_ptr(), pre.records.data_ptr(), bg.data_ptr(), alpha_c.data_ptr(),
+                         n_contrib.data_ptr(), gc.data_ptr(), gd.data_ptr(), ga.data_ptr(),
+                         int(bool(options.compute_depth)), grad_gauss.data_ptr(), stream)
         has_sh = inputs.sh.numel() != 0
         shs = _f32c(inputs.sh).reshape(P, -1, NUM_CHANNELS) if has_sh else None
         K = shs.shape[1] if has_sh else 0
@@ -352,13 +373,15 @@ def backward(inputs: RasterInputs, radii: torch.Tensor, alpha: torch.Tensor, gra
         gp2 = _zeros_if_none(grad_proj_2d, (P, 2), device)
         gcon = _zeros_if_none(grad_conic_2d, (P, 3), device)
         gcov = _zeros_if_none(grad_conic_2d_inv, (P, 3), device)
-        lib.call(
-            "gs_preprocess_bwd", P, K, int(inputs.degree), means_c.data_ptr(), scales_c.data_ptr(), rot_c.data_ptr(),
-            float(inputs.scale_modifier), _lib.ptr(shs), campos_c.data_ptr(), view_c.data_ptr(), proj_c.data_ptr(),
-            tanfovx, tanfovy, _focal(W, tanfovx), _focal(H, tanfovy), radii_c.data_ptr(), pre.clamped.data_ptr(),
-            grad_gauss.data_ptr(), gp2.data_ptr(), gcon.data_ptr(), gcov.data_ptr(), int(bool(flow_double)),
-            grad_means3d.data_ptr(), grad_means2d.data_ptr(), grad_scales.data_ptr(), grad_rotations.data_ptr(),
-            grad_sh.data_ptr() if has_sh else None, None, None, stream)
+        with _stage("preprocess_bwd"):
+            lib.call(
+                "gs_preprocess_bwd", P, K, int(inputs.degree), means_c.data_ptr(), scales_c.data_ptr(),
+                rot_c.data_ptr(), float(inputs.scale_modifier), _lib.ptr(shs), campos_c.data_ptr(),
+                view_c.data_ptr(), proj_c.data_ptr(), tanfovx, tanfovy, _focal(W, tanfovx), _focal(H, tanfovy),
+                radii_c.data_ptr(), pre.clamped.data_ptr(), grad_gauss.data_ptr(), gp2.data_ptr(), gcon.data_ptr(),
+                gcov.data_ptr(), int(bool(flow_double)), grad_means3d.data_ptr(), grad_means2d.data_ptr(),
+                grad_scales.data_ptr(), grad_rotations.data_ptr(), grad_sh.data_ptr() if has_sh else None, None,
+                None, stream)
     grad_opacities = grad_gauss[:, 5:6]
     if grad_opacities.shape != inputs.opacities.shape:
         grad_opacities = grad_opacities.reshape(inputs.opacities.shape)
