@@ -7,10 +7,13 @@ rasterizer call raises ``RuntimeError`` — there is no CPU or eager fallback.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libgswarp_hip.so"
+# GSWARP_AMD_LIB selects another build of the same library (e.g. one compiled
+# with different pixels-per-lane settings).
+LIB_PATH = Path(os.environ.get("GSWARP_AMD_LIB", Path(__file__).resolve().parent / "libgswarp_hip.so"))
 
 GS_OK = 0
 GS_RECORD_FLOATS = 12

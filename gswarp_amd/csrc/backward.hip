@@ -1,15 +1,16 @@
 // Manual backward for gfx950.
 //
-// render_bwd: one 256-thread workgroup per tile walks the tile's list back to
-// front from the largest n_contrib of its pixels (backward_kernels.py:539-707
-// semantics: T starts at 1 - alpha_out, is divided by max(1-alpha, 1e-5) per
-// blended Gaussian, reverse recurrences for colour, depth and alpha, the
-// background term, xy gradients scaled by W/2 and H/2, conic gradients with
-// the -1/2 factor).  Per Gaussian, each wave sums its 64 pixels' ten gradient
-// components with DPP row operations (skipped when no lane of the wave
-// blended it), the four waves combine through LDS float atomics, and after
-// each 256-Gaussian batch one lane per Gaussian issues a single global atomic
-// per non-zero component.
+// render_bwd: wave64 workgroups each own a slice of a tile and walk the
+// tile's list back to front from the largest n_contrib of their pixels
+// (backward_kernels.py:539-707 semantics: T starts at 1 - alpha_out and is
+// divided by max(1-alpha, 1e-5) per blended Gaussian, reverse recurrences for
+// colour, depth and alpha, the background term, xy gradients scaled by W/2
+// and H/2, conic gradients with the -1/2 factor).  Per Gaussian each lane
+// sums its pixels' terms, the wave sums the ten components with a transposed
+// lane-swap/DPP reduction (skipped when no pixel of the wave blended it), and
+// one lane per row issues the global float atomics of its row's components.
+// The blend decisions use the forward's exact arithmetic; T uses the
+// hardware reciprocal (gradients only).
 //
 // preprocess_bwd: one thread per Gaussian fusing the SH colour backward
 // (backward_kernels.py:298-536), the projected-mean / depth backward
@@ -23,21 +24,55 @@
 namespace gs {
 
 constexpr int kGradFloats = 10;  // dx, dy, conic a, b, c, opacity, r, g, b, depth
+#ifndef GS_BWD_PIX
+#define GS_BWD_PIX 2
+#endif
+constexpr int kBwdPix = GS_BWD_PIX;  // pixels per lane: 1, 2 or 4
 
 template <int kCtrl, int kRowMask>
 __device__ __forceinline__ float dpp_mov(float src) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(src), kCtrl, kRowMask, 0xF, false));
 }
 
-// Sum over the 64 lanes of a fully active wave; the total lands in lane 63.
-__device__ __forceinline__ float wave_sum_lane63(float v) {
+// Sum over the 16 lanes of each row; every lane of the row receives the total.
+__device__ __forceinline__ float row_sum16(float v) {
   v = v + dpp_mov<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
   v = v + dpp_mov<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
   v = v + dpp_mov<0x141, 0xF>(v);  // row_half_mirror
   v = v + dpp_mov<0x140, 0xF>(v);  // row_mirror
-  v = v + dpp_mov<0x142, 0xA>(v);  // row_bcast:15 -> rows 1, 3
-  v = v + dpp_mov<0x143, 0xC>(v);  // row_bcast:31 -> rows 2, 3
   return v;
+}
+
+// v_permlane32_swap exchanges lanes 32-63 of a with lanes 0-31 of b, so the
+// sum of the two results holds a[l] + a[l+32] in lanes 0-31 and
+// b[l-32] + b[l] in lanes 32-63: two half-wave partial sums for one add.
+__device__ __forceinline__ float fold32(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// v_permlane16_swap exchanges the odd rows of a with the even rows of b: the
+// sum holds a folded over row pairs (0,1) and (2,3) in rows 0 and 2 and b
+// folded the same way in rows 1 and 3.
+__device__ __forceinline__ float fold16(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Transposed wave reduction of ten per-lane values: two lane-swap folds
+// leave three registers whose four rows each carry one component, then one
+// row reduction per register (28 VALU operations instead of 60 for ten
+// separate wave sums).  Row r of m[0] holds component {0,1,5,6}[r], of m[1]
+// {2,3,7,8}[r], of m[2] {4,4,9,9}[r].
+__device__ __forceinline__ void wave_sum10(const float (&g)[10], float (&m)[3]) {
+  const float h0 = fold32(g[0], g[5]);
+  const float h1 = fold32(g[1], g[6]);
+  const float h2 = fold32(g[2], g[7]);
+  const float h3 = fold32(g[3], g[8]);
+  const float h4 = fold32(g[4], g[9]);
+  m[0] = row_sum16(fold16(h0, h1));
+  m[1] = row_sum16(fold16(h2, h3));
+  m[2] = row_sum16(fold16(h4, h4));
 }
 
 __device__ __forceinline__ int wave_max_i32(int v) {
@@ -66,151 +101,193 @@ struct RenderBwdParams {
   float* grad_gauss;
 };
 
-__global__ __launch_bounds__(kTilePixels) void render_bwd_kernel(RenderBwdParams p) {
-  __shared__ float4 s_r0[kTilePixels];
-  __shared__ float4 s_r1[kTilePixels];
-  __shared__ float4 s_r2[kTilePixels];
-  __shared__ int s_id[kTilePixels];
-  __shared__ float s_acc[kTilePixels * kGradFloats];
-  __shared__ int s_any[kTilePixels];
-  __shared__ int s_wmax[kTilePixels / 64];
+struct BwdBatch {
+  float4 r0, r1, r2;
+  int id;
+};
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int tile = blockIdx.x;
+__device__ __forceinline__ BwdBatch load_bwd_batch(const RenderBwdParams& p, int first, int cnt, int lane) {
+  BwdBatch b;
+  b.id = 0;
+  b.r0 = b.r1 = b.r2 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (lane < cnt) {
+    int id = p.point_list[first + lane];
+    if ((unsigned)id >= (unsigned)p.num_points) id = 0;  // guards inconsistent caller input only
+    const float4* rec = p.records + 3 * (size_t)id;
+    b.r0 = rec[0];
+    b.r1 = rec[1];
+    b.r2 = rec[2];
+    b.id = id;
+  }
+  return b;
+}
+
+// 4/kPix independent wave64 workgroups per tile, lane l owning the kPix
+// pixels of column l % 16 in rows l / 16 + 4k (k < kPix) of its slice (the
+// forward's layout).  Per Gaussian, each
+// lane first sums its pixels' contributions, using the factorisation
+//   v = G * dL/dalpha_hat per pixel,
+//   dL/dxy    = -(W/2, H/2) * o * (a dx sum(v) + b sum(v dy), c sum(v dy) + b dx sum(v)),
+//   dL/dconic = -1/2 * o * (dx^2 sum(v), dx sum(v dy), sum(v dy^2)),
+//   dL/dopacity = sum(v),
+// which is the reference's per-pixel expression summed over pixels sharing
+// dx; then the ten per-lane components are summed over the wave.
+template <bool kDepth, int kPix>
+__global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
+  constexpr int kSubs = 4 / kPix;
+  __shared__ float4 s_r0[64], s_r1[64], s_r2[64];
+  __shared__ int s_id[64];
+  const int lane = threadIdx.x;
+  const int2 ts = xcd_tile_sub(blockIdx.x, p.num_tiles, kSubs);
+  const int tile = ts.x;
   const int tx = tile % p.grid_x;
   const int ty = tile / p.grid_x;
-  const int px = tx * kBlockX + (threadIdx.x % kBlockX);
-  const int py = ty * kBlockY + (threadIdx.x / kBlockX);
-  const bool inside = px < p.W && py < p.H;
+  const int px = tx * kBlockX + (lane & 15);
+  const int py0 = ty * kBlockY + ts.y * 4 * kPix + (lane >> 4);
   const int P = p.W * p.H;
-  const int pix = py * p.W + px;
+  const float pfx = (float)px;
   int2 rg = p.ranges[tile];
   rg.x = imax(0, imin(rg.x, p.num_rendered));
   rg.y = imax(rg.x, imin(rg.y, p.num_rendered));
   const int n = rg.y - rg.x;
 
-  int last = 0;
-  if (inside && n > 0) last = imax(0, imin(p.n_contrib[pix], n));
-  const int wmax = wave_max_i32(last);
-  if (lane == 0) s_wmax[wave] = wmax;
-  __syncthreads();
-  int max_lc = s_wmax[0];
+  float pfy[kPix], T[kPix], Tf[kPix], gp0[kPix], gp1[kPix], gp2[kPix], gpd[kPix], gpa[kPix], bgd[kPix];
+  float acc0[kPix], acc1[kPix], acc2[kPix], accd[kPix], acca[kPix];
+  float la[kPix], lc0[kPix], lc1[kPix], lc2[kPix], ld[kPix];
+  int last[kPix];
+  int lmax = 0;
 #pragma unroll
-  for (int w = 1; w < kTilePixels / 64; ++w) max_lc = max_lc > s_wmax[w] ? max_lc : s_wmax[w];
-  if (max_lc == 0) return;  // uniform across the workgroup
-
-  const float ddelx_dx = 0.5f * (float)p.W;
-  const float ddely_dy = 0.5f * (float)p.H;
-  const float pfx = (float)px;
-  const float pfy = (float)py;
-  float T_final = 0.0f, T = 0.0f;
-  float gp0 = 0.0f, gp1 = 0.0f, gp2 = 0.0f, gpd = 0.0f, gpa = 0.0f, bg_dot = 0.0f;
-  if (inside && n > 0) {
-    T_final = 1.0f - p.out_alpha[pix];
-    T = T_final;
-    gp0 = p.grad_color[pix];
-    gp1 = p.grad_color[P + pix];
-    gp2 = p.grad_color[2 * P + pix];
-    if (p.compute_depth) gpd = p.grad_depth[pix];
-    gpa = p.grad_alpha[pix];
-    bg_dot = p.bg[0] * gp0 + p.bg[1] * gp1 + p.bg[2] * gp2;
+  for (int k = 0; k < kPix; ++k) {
+    const int py = py0 + 4 * k;
+    pfy[k] = (float)py;
+    last[k] = 0;
+    T[k] = Tf[k] = gp0[k] = gp1[k] = gp2[k] = gpd[k] = gpa[k] = bgd[k] = 0.0f;
+    acc0[k] = acc1[k] = acc2[k] = accd[k] = acca[k] = 0.0f;
+    la[k] = lc0[k] = lc1[k] = lc2[k] = ld[k] = 0.0f;
+    if (px < p.W && py < p.H && n > 0) {
+      const int pix = py * p.W + px;
+      last[k] = imax(0, imin(p.n_contrib[pix], n));
+      Tf[k] = 1.0f - p.out_alpha[pix];
+      T[k] = Tf[k];
+      gp0[k] = p.grad_color[pix];
+      gp1[k] = p.grad_color[P + pix];
+      gp2[k] = p.grad_color[2 * P + pix];
+      if (kDepth) gpd[k] = p.grad_depth[pix];
+      gpa[k] = p.grad_alpha[pix];
+      bgd[k] = p.bg[0] * gp0[k] + p.bg[1] * gp1[k] + p.bg[2] * gp2[k];
+    }
+    lmax = imax(lmax, last[k]);
   }
-  float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f, acc_d = 0.0f, acc_a = 0.0f;
-  float last_alpha = 0.0f, lc0 = 0.0f, lc1 = 0.0f, lc2 = 0.0f, last_depth = 0.0f;
+  const int max_lc = __builtin_amdgcn_readfirstlane(wave_max_i32(lmax));
+  if (max_lc == 0) return;
+  const float half_w = 0.5f * (float)p.W;
+  const float half_h = 0.5f * (float)p.H;
 
-  for (int batch_end = max_lc; batch_end > 0; batch_end -= kTilePixels) {
-    const int batch_start = batch_end > kTilePixels ? batch_end - kTilePixels : 0;
-    const int cnt = batch_end - batch_start;
-    __syncthreads();
-    if (threadIdx.x < cnt) {
-      int id = p.point_list[rg.x + batch_start + threadIdx.x];
-      if ((unsigned)id >= (unsigned)p.num_points) id = 0;
-      const float4* rec = p.records + 3 * (size_t)id;
-      s_r0[threadIdx.x] = rec[0];
-      s_r1[threadIdx.x] = rec[1];
-      s_r2[threadIdx.x] = rec[2];
-      s_id[threadIdx.x] = id;
-      s_any[threadIdx.x] = 0;
+  int bs = imax(0, max_lc - 64);
+  BwdBatch next = load_bwd_batch(p, rg.x + bs, max_lc - bs, lane);
+  for (int batch_end = max_lc; batch_end > 0; batch_end = bs, bs = imax(0, bs - 64)) {
+    const int cnt = batch_end - bs;
+    // One wave per workgroup: its LDS queue orders these writes before the
+    // broadcast reads below.
+    s_r0[lane] = next.r0;
+    s_r1[lane] = next.r1;
+    s_r2[lane] = next.r2;
+    s_id[lane] = next.id;
+    if (bs > 0) {
+      const int nbs = imax(0, bs - 64);
+      next = load_bwd_batch(p, rg.x + nbs, bs - nbs, lane);
     }
-#pragma unroll
-    for (int i = threadIdx.x; i < kTilePixels * kGradFloats; i += kTilePixels) s_acc[i] = 0.0f;
-    __syncthreads();
-
     for (int jj = cnt - 1; jj >= 0; --jj) {
-      const int pos = batch_start + jj;
+      const int pos = bs + jj;
+      const float4 a = s_r0[jj];
+      const float4 b = s_r1[jj];
+      const float dx = a.x - pfx;
+      const float adxx = a.z * dx * dx;
+      const float bdx = a.w * dx;
+      float pw[kPix], dy[kPix];
+      bool cand[kPix];
+      bool any = false;
+#pragma unroll
+      for (int k = 0; k < kPix; ++k) {
+        dy[k] = a.y - pfy[k];
+        pw[k] = -0.5f * (adxx + b.x * dy[k] * dy[k]) - bdx * dy[k];
+        cand[k] = pos < last[k] && pw[k] <= 0.0f && pw[k] >= b.w;
+        any = any || cand[k];
+      }
+      if (__ballot(any) == 0) continue;
+      const float4 f = s_r2[jj];
+      float G[kPix], alpha[kPix];
+      bool ok[kPix];
+      bool any_ok = false;
+#pragma unroll
+      for (int k = 0; k < kPix; ++k) {
+        G[k] = exp_sw_nonpos(cand[k] ? pw[k] : 0.0f);
+        alpha[k] = fminr(kAlphaMax, b.y * G[k]);
+        ok[k] = cand[k] && alpha[k] >= kAlphaMin;
+        any_ok = any_ok || ok[k];
+      }
+      if (__ballot(any_ok) == 0) continue;
+      float sv = 0.0f, svy = 0.0f, svyy = 0.0f, sr = 0.0f, sg = 0.0f, sb = 0.0f, sd = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kPix; ++k) {
+        const float inv = __builtin_amdgcn_rcpf(fmaxr(1.0f - alpha[k], kOneMinusAlphaMin));
+        const float Tn = T[k] * inv;
+        const float dch = ok[k] ? alpha[k] * Tn : 0.0f;
+        const float oml = 1.0f - la[k];
+        const float a0 = fmaf(la[k], lc0[k], oml * acc0[k]);
+        const float a1 = fmaf(la[k], lc1[k], oml * acc1[k]);
+        const float a2 = fmaf(la[k], lc2[k], oml * acc2[k]);
+        float dL_dopa = fmaf(f.x - a0, gp0[k], fmaf(f.y - a1, gp1[k], (f.z - a2) * gp2[k]));
+        if (kDepth) {
+          const float ad = fmaf(la[k], ld[k], oml * accd[k]);
+          dL_dopa = fmaf(b.z - ad, gpd[k], dL_dopa);
+          accd[k] = ok[k] ? ad : accd[k];
+          ld[k] = ok[k] ? b.z : ld[k];
+          sd = fmaf(dch, gpd[k], sd);
+        }
+        const float aa = fmaf(oml, acca[k], la[k]);
+        dL_dopa = fmaf(1.0f - aa, gpa[k], dL_dopa);
+        dL_dopa = fmaf(dL_dopa, Tn, -Tf[k] * inv * bgd[k]);
+        const float v = ok[k] ? G[k] * dL_dopa : 0.0f;
+        sv += v;
+        svy = fmaf(v, dy[k], svy);
+        svyy = fmaf(v * dy[k], dy[k], svyy);
+        sr = fmaf(dch, gp0[k], sr);
+        sg = fmaf(dch, gp1[k], sg);
+        sb = fmaf(dch, gp2[k], sb);
+        T[k] = ok[k] ? Tn : T[k];
+        acc0[k] = ok[k] ? a0 : acc0[k];
+        acc1[k] = ok[k] ? a1 : acc1[k];
+        acc2[k] = ok[k] ? a2 : acc2[k];
+        acca[k] = ok[k] ? aa : acca[k];
+        lc0[k] = ok[k] ? f.x : lc0[k];
+        lc1[k] = ok[k] ? f.y : lc1[k];
+        lc2[k] = ok[k] ? f.z : lc2[k];
+        la[k] = ok[k] ? alpha[k] : la[k];
+      }
+      const float s = b.y * sv, sy = b.y * svy, syy = b.y * svyy;
       float g[kGradFloats];
-#pragma unroll
-      for (int c = 0; c < kGradFloats; ++c) g[c] = 0.0f;
-      bool has = false;
-      if (inside && pos < last) {
-        const float4 a = s_r0[jj];
-        const float4 b = s_r1[jj];
-        const float dx = a.x - pfx;
-        const float dy = a.y - pfy;
-        const float power = -0.5f * (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
-        if (power <= 0.0f && power >= b.w) {
-          const float G = exp_sw(power);
-          const float alpha = fminr(kAlphaMax, b.y * G);
-          if (alpha >= kAlphaMin) {
-            has = true;
-            const float4 f = s_r2[jj];
-            const float oma = fmaxr(1.0f - alpha, kOneMinusAlphaMin);
-            T = T / oma;
-            const float dchannel = alpha * T;
-            const float om_last = 1.0f - last_alpha;
-            acc0 = last_alpha * lc0 + om_last * acc0;
-            acc1 = last_alpha * lc1 + om_last * acc1;
-            acc2 = last_alpha * lc2 + om_last * acc2;
-            lc0 = f.x;
-            lc1 = f.y;
-            lc2 = f.z;
-            float dL_dopa = (f.x - acc0) * gp0 + (f.y - acc1) * gp1 + (f.z - acc2) * gp2;
-            g[6] = dchannel * gp0;
-            g[7] = dchannel * gp1;
-            g[8] = dchannel * gp2;
-            if (p.compute_depth) {
-              acc_d = last_alpha * last_depth + om_last * acc_d;
-              last_depth = b.z;
-              dL_dopa = dL_dopa + (b.z - acc_d) * gpd;
-              g[9] = dchannel * gpd;
-            }
-            acc_a = last_alpha + om_last * acc_a;
-            dL_dopa = dL_dopa + (1.0f - acc_a) * gpa;
-            dL_dopa = dL_dopa * T;
-            last_alpha = alpha;
-            dL_dopa = dL_dopa + (-T_final / oma) * bg_dot;
-            const float dL_dG = b.y * dL_dopa;
-            const float gdx = G * dx;
-            const float gdy = G * dy;
-            const float dG_ddelx = -gdx * a.z - gdy * a.w;
-            const float dG_ddely = -gdy * b.x - gdx * a.w;
-            g[0] = dL_dG * dG_ddelx * ddelx_dx;
-            g[1] = dL_dG * dG_ddely * ddely_dy;
-            g[2] = -0.5f * gdx * dx * dL_dG;
-            g[3] = -0.5f * gdx * dy * dL_dG;
-            g[4] = -0.5f * gdy * dy * dL_dG;
-            g[5] = G * dL_dopa;
-          }
-        }
-      }
-      if (__ballot(has) != 0) {
-#pragma unroll
-        for (int c = 0; c < kGradFloats; ++c) g[c] = wave_sum_lane63(g[c]);
-        if (lane == 63) {
-#pragma unroll
-          for (int c = 0; c < kGradFloats; ++c) atomicAdd(&s_acc[jj * kGradFloats + c], g[c]);
-          s_any[jj] = 1;
-        }
-      }
-    }
-    __syncthreads();
-    if (threadIdx.x < cnt && s_any[threadIdx.x]) {
-      float* dst = p.grad_gauss + (size_t)s_id[threadIdx.x] * kGradFloats;
-#pragma unroll
-      for (int c = 0; c < kGradFloats; ++c) {
-        const float v = s_acc[threadIdx.x * kGradFloats + c];
-        if (v != 0.0f) unsafeAtomicAdd(dst + c, v);
+      g[0] = -half_w * fmaf(a.z * dx, s, a.w * sy);
+      g[1] = -half_h * fmaf(b.x, sy, a.w * dx * s);
+      g[2] = -0.5f * dx * dx * s;
+      g[3] = -0.5f * dx * sy;
+      g[4] = -0.5f * syy;
+      g[5] = sv;
+      g[6] = sr;
+      g[7] = sg;
+      g[8] = sb;
+      g[9] = sd;
+      float m[3];
+      wave_sum10(g, m);
+      if ((lane & 15) == 0) {
+        // Lane 16 r adds row r's three components (zeros are skipped; the
+        // depth component is zero when depth is off).
+        float* dst = p.grad_gauss + (size_t)s_id[jj] * kGradFloats;
+        const int r = lane >> 4;
+        const int c0 = (r & 1) + 5 * (r >> 1);
+        if (m[0] != 0.0f) unsafeAtomicAdd(dst + c0, m[0]);
+        if (m[1] != 0.0f) unsafeAtomicAdd(dst + c0 + 2, m[1]);
+        if ((r & 1) == 0 && m[2] != 0.0f) unsafeAtomicAdd(dst + 4 + 5 * (r >> 1), m[2]);
       }
     }
   }
@@ -612,7 +689,11 @@ extern "C" int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t 
   p.grad_alpha = grad_alpha;
   p.compute_depth = compute_depth;
   p.grad_gauss = grad_gauss;
-  hipLaunchKernelGGL(gs::render_bwd_kernel, dim3(p.num_tiles), dim3(gs::kTilePixels), 0, (hipStream_t)stream, p);
+  const dim3 grid(p.num_tiles * (4 / gs::kBwdPix));
+  if (compute_depth)
+    hipLaunchKernelGGL((gs::render_bwd_kernel<true, gs::kBwdPix>), grid, dim3(64), 0, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL((gs::render_bwd_kernel<false, gs::kBwdPix>), grid, dim3(64), 0, (hipStream_t)stream, p);
   return gs_status_from_hip(hipGetLastError());
 }
 

@@ -90,23 +90,44 @@ __host__ __device__ __forceinline__ int f2i(float f) {
 
 // exp(x) by Cody-Waite range reduction x = n*ln2 + r (|r| <= ln2/2, ln2 split
 // into an exact 9-bit head and a tail) followed by the degree-7 Taylor
-// polynomial of e^r in Horner form and an exact scaling by 2^n.  Results are
-// within 2 ulp of exp(x) for x in [-87, 88]; x < -87 returns 0 (the result
-// would be below 1.7e-38 and only ever feeds an alpha < 1/255 decision).
+// polynomial of e^r in Horner form and an exact scaling by 2^n.  Every step
+// is a single correctly rounded fused multiply-add, so a host evaluating the
+// same fmaf sequence reproduces the result bit for bit.  Results are within
+// 2 ulp of exp(x) for x in [-87, 88]; x < -87 returns 0 (the result would be
+// below 1.7e-38 and only ever feeds an alpha < 1/255 decision).
 __device__ __forceinline__ float exp_sw(float x) {
   if (x < -87.0f) return 0.0f;
   if (x > 88.0f) x = 88.0f;
   const float n = rintf(x * 1.44269504088896341f);
-  float r = x - n * 0.693359375f;
-  r = r - n * (-2.12194440e-4f);
+  float r = fmaf(n, -0.693359375f, x);
+  r = fmaf(n, 2.12194440e-4f, r);
   float p = 1.98412698e-4f;          // 1/5040
-  p = p * r + 1.38888889e-3f;        // 1/720
-  p = p * r + 8.33333333e-3f;        // 1/120
-  p = p * r + 4.16666667e-2f;        // 1/24
-  p = p * r + 1.66666667e-1f;        // 1/6
-  p = p * r + 0.5f;
-  p = p * r + 1.0f;
-  p = p * r + 1.0f;
+  p = fmaf(p, r, 1.38888889e-3f);    // 1/720
+  p = fmaf(p, r, 8.33333333e-3f);    // 1/120
+  p = fmaf(p, r, 4.16666667e-2f);    // 1/24
+  p = fmaf(p, r, 1.66666667e-1f);    // 1/6
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return ldexpf(p, (int)n);
+}
+
+// exp_sw restricted to x in [-87, 0], where its two range guards are no-ops:
+// the same fmaf sequence, so the result is bit-identical to exp_sw(x).  The
+// render loops only evaluate exponents in [power_cutoff, 0] and power_cutoff
+// is never below -87.
+__device__ __forceinline__ float exp_sw_nonpos(float x) {
+  const float n = rintf(x * 1.44269504088896341f);
+  float r = fmaf(n, -0.693359375f, x);
+  r = fmaf(n, 2.12194440e-4f, r);
+  float p = 1.98412698e-4f;
+  p = fmaf(p, r, 1.38888889e-3f);
+  p = fmaf(p, r, 8.33333333e-3f);
+  p = fmaf(p, r, 4.16666667e-2f);
+  p = fmaf(p, r, 1.66666667e-1f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
   return ldexpf(p, (int)n);
 }
 
@@ -135,12 +156,39 @@ __device__ __forceinline__ float log_sw(float y) {
 
 // Largest exponent below which o*exp(power) < 1/255 holds for every power,
 // with a 1e-3 margin that covers exp_sw and product rounding (relative error
-// < 1e-6).  Returns +inf when the Gaussian can never reach the alpha cut-off.
+// < 1e-6).  Returns FLT_MAX when the Gaussian can never reach the alpha
+// cut-off.  Never below -87: exp_sw is 0 there, so alpha is 0 and skipping
+// those exponents changes no decision either.
 __device__ __forceinline__ float power_cutoff(float opacity) {
   const float o255 = 255.0f * opacity;
   if (!(o255 > 1.0f)) return kFloatMax;
-  return -log_sw(o255) - 1.0e-3f;
+  if (o255 > 1.0e37f) return -87.0f;
+  return fmaxr(-log_sw(o255) - 1.0e-3f, -87.0f);
 }
+
+// Workgroups are dispatched round-robin over the eight XCDs (each with its
+// own L2).  Mapping workgroup b to tile start(b % 8) + b / 8 gives every XCD
+// one contiguous band of tiles, so neighbouring tiles, which share most of
+// their Gaussians, hit the same L2.  Bijective on [0, num_tiles).
+__device__ __forceinline__ int xcd_tile(int b, int num_tiles) {
+  const int q = num_tiles >> 3;
+  const int r = num_tiles & 7;
+  const int xcd = b & 7;
+  return xcd * q + (xcd < r ? xcd : r) + (b >> 3);
+}
+
+// Same XCD banding for `subs` independent waves per tile: consecutive
+// workgroups on one XCD are the sub-waves of one tile, then the next tile.
+__device__ __forceinline__ int2 xcd_tile_sub(int b, int num_tiles, int subs) {
+  const int unit = xcd_tile(b, num_tiles * subs);
+  return make_int2(unit / subs, unit % subs);
+}
+
+__device__ __forceinline__ float lane_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+__device__ __forceinline__ int lane_i(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
 
 __device__ __forceinline__ float ndc_to_pix(float v, int size) {
   return ((v + 1.0f) * (float)size - 1.0f) * 0.5f;

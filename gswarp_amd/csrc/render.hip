@@ -1,7 +1,16 @@
-// Forward render: one 256-thread workgroup (4 wave64) per 16x16 tile, one
-// pixel per lane.  Gaussians of the tile's sorted list are staged 256 at a
-// time in LDS (three float4 per Gaussian from the packed render record); a
-// workgroup-wide vote ends the tile once every pixel's transmittance is done.
+// Forward render: each 16x16 tile is covered by 4/kPix independent wave64
+// workgroups, each owning a 16 x 4*kPix slice; lane l owns the kPix pixels
+// of column l % 16 in rows l / 16 + 4k (k < kPix) of its slice.  Pixels of a
+// lane share dx to a Gaussian, so a*dx*dx and b*dx are evaluated once per
+// lane, exactly as the per-pixel expression would round them.  The tile's
+// sorted Gaussians are fetched 64 at a time, one packed 48-byte record per
+// lane, with the next batch prefetched into registers while the current one
+// is blended from a per-wave LDS slot (one broadcast ds_read_b128 per record
+// quarter; no barriers since each workgroup is one wave).  Per Gaussian the
+// per-pixel work is branch-free (select-based updates inside one wave-uniform
+// "any candidate" branch) so the pixels' exponential chains interleave.  A
+// wave-wide ballot ends the slice once every one of its pixels is done.
+//
 // Semantics follow render_kernels.py:16-147 (and flow_kernels.py:31-176 for
 // the flow variant):
 //   power > 0 skipped; alpha = min(0.99, o*exp(power)); alpha < 1/255 skipped;
@@ -14,6 +23,11 @@
 #include "gs_capi.h"
 
 namespace gs {
+
+#ifndef GS_FWD_PIX
+#define GS_FWD_PIX 1
+#endif
+constexpr int kFwdPix = GS_FWD_PIX;  // pixels per lane: 1, 2 or 4
 
 struct RenderFwdParams {
   int W, H, grid_x, num_tiles;
@@ -34,123 +48,164 @@ struct RenderFwdParams {
   float* x_mu;
 };
 
-template <bool kFlow>
-__global__ __launch_bounds__(kTilePixels) void render_fwd_kernel(RenderFwdParams p) {
-  __shared__ float4 s_r0[kTilePixels];
-  __shared__ float4 s_r1[kTilePixels];
-  __shared__ float4 s_r2[kTilePixels];
-  __shared__ int s_id[kFlow ? kTilePixels : 1];
+struct Batch {
+  float4 r0, r1, r2;
+  int id;
+};
 
-  const int tile = blockIdx.x;
+__device__ __forceinline__ Batch load_batch(const RenderFwdParams& p, int first, int cnt, int lane) {
+  Batch b;
+  b.id = 0;
+  b.r0 = b.r1 = b.r2 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (lane < cnt) {
+    int id = p.point_list[first + lane];
+    if ((unsigned)id >= (unsigned)p.num_points) id = 0;  // guards inconsistent caller input only
+    const float4* rec = p.records + 3 * (size_t)id;
+    b.r0 = rec[0];
+    b.r1 = rec[1];
+    b.r2 = rec[2];
+    b.id = id;
+  }
+  return b;
+}
+
+template <bool kFlow, int kPixPerLane>
+__global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
+  constexpr int kSubs = 4 / kPixPerLane;
+  __shared__ float4 s_r0[64], s_r1[64], s_r2[64];
+  __shared__ int s_id[kFlow ? 64 : 1];
+  const int lane = threadIdx.x;
+  const int2 ts = xcd_tile_sub(blockIdx.x, p.num_tiles, kSubs);
+  const int tile = ts.x;
   const int tx = tile % p.grid_x;
   const int ty = tile / p.grid_x;
-  const int px = tx * kBlockX + (threadIdx.x % kBlockX);
-  const int py = ty * kBlockY + (threadIdx.x / kBlockX);
-  const bool inside = px < p.W && py < p.H;
+  const int px = tx * kBlockX + (lane & 15);
+  const int py0 = ty * kBlockY + ts.y * 4 * kPixPerLane + (lane >> 4);
   const int P = p.W * p.H;
-  const int pix = py * p.W + px;
+  const float pfx = (float)px;
   int2 rg = p.ranges[tile];
-  // Ranges come from gs_tile_ranges over num_rendered sorted pairs; the clamp
-  // only guards against inconsistent caller input.
   rg.x = imax(0, imin(rg.x, p.num_rendered));
   rg.y = imax(rg.x, imin(rg.y, p.num_rendered));
   const int n = rg.y - rg.x;
-  const float pfx = (float)px;
-  const float pfy = (float)py;
-
-  float T = 1.0f;
-  int last = 0;
-  float c0 = 0.0f, c1 = 0.0f, c2 = 0.0f, wsum = 0.0f, dacc = 0.0f;
-  int done = inside ? 0 : 1;
-  int n_success = 0;
   const bool aux = kFlow && p.write_aux != 0;
 
-  const int rounds = (n + kTilePixels - 1) / kTilePixels;
-  for (int r = 0; r < rounds; ++r) {
-    if (__syncthreads_count(done) == kTilePixels) break;
-    const int progress = r * kTilePixels + threadIdx.x;
-    if (progress < n) {
-      int id = p.point_list[rg.x + progress];
-      if ((unsigned)id >= (unsigned)p.num_points) id = 0;
-      const float4* rec = p.records + 3 * (size_t)id;
-      s_r0[threadIdx.x] = rec[0];
-      s_r1[threadIdx.x] = rec[1];
-      s_r2[threadIdx.x] = rec[2];
-      if (kFlow) s_id[threadIdx.x] = id;
-    }
-    __syncthreads();
-    const int batch = imin(kTilePixels, n - r * kTilePixels);
-    if (!done) {
-      for (int j = 0; j < batch; ++j) {
-        const float4 a = s_r0[j];
-        const float4 b = s_r1[j];
-        const float dx = a.x - pfx;
-        const float dy = a.y - pfy;
-        const float power = -0.5f * (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
-        if (!(power <= 0.0f) || power < b.w) continue;
-        const float alpha = fminr(kAlphaMax, b.y * exp_sw(power));
-        if (alpha < kAlphaMin) continue;
-        const float test_T = T * (1.0f - alpha);
-        if (test_T < kTransmittanceMin) {
-          done = 1;
-          break;
+  // T > 0: transmittance of a live pixel; T < 0: -T of a finished pixel
+  // (transmittance never drops below 1e-4 while live); pixels outside the
+  // image start finished.
+  float T[kPixPerLane], c0[kPixPerLane], c1[kPixPerLane], c2[kPixPerLane], ws[kPixPerLane], da[kPixPerLane];
+  float pfy[kPixPerLane];
+  int last[kPixPerLane], nsucc[kPixPerLane];
+#pragma unroll
+  for (int k = 0; k < kPixPerLane; ++k) {
+    const int py = py0 + 4 * k;
+    pfy[k] = (float)py;
+    T[k] = (px < p.W && py < p.H) ? 1.0f : -1.0f;
+    c0[k] = c1[k] = c2[k] = ws[k] = da[k] = 0.0f;
+    last[k] = 0;
+    nsucc[k] = 0;
+  }
+
+  Batch next = load_batch(p, rg.x, imin(64, n), lane);
+  for (int base = 0; base < n; base += 64) {
+    bool live = false;
+#pragma unroll
+    for (int k = 0; k < kPixPerLane; ++k) live = live || T[k] > 0.0f;
+    if (__ballot(live) == 0) break;
+    const int cnt = imin(64, n - base);
+    // One wave per workgroup: LDS writes and the broadcast reads below are
+    // ordered by the wave's own in-order LDS queue, no barrier needed.
+    s_r0[lane] = next.r0;
+    s_r1[lane] = next.r1;
+    s_r2[lane] = next.r2;
+    if (kFlow) s_id[lane] = next.id;
+    if (base + 64 < n) next = load_batch(p, rg.x + base + 64, imin(64, n - base - 64), lane);
+    for (int j = 0; j < cnt; ++j) {
+      const float4 a = s_r0[j];
+      const float4 b = s_r1[j];
+      const float dx = a.x - pfx;
+      const float adxx = a.z * dx * dx;
+      const float bdx = a.w * dx;
+      float pw[kPixPerLane], dy[kPixPerLane];
+      bool cand[kPixPerLane];
+      bool any = false;
+#pragma unroll
+      for (int k = 0; k < kPixPerLane; ++k) {
+        dy[k] = a.y - pfy[k];
+        pw[k] = -0.5f * (adxx + b.x * dy[k] * dy[k]) - bdx * dy[k];
+        cand[k] = T[k] > 0.0f && pw[k] <= 0.0f && pw[k] >= b.w;
+        any = any || cand[k];
+      }
+      if (__ballot(any) == 0) continue;
+      const float4 f = s_r2[j];
+#pragma unroll
+      for (int k = 0; k < kPixPerLane; ++k) {
+        const float alpha = fminr(kAlphaMax, b.y * exp_sw_nonpos(cand[k] ? pw[k] : 0.0f));
+        const bool ok = cand[k] && alpha >= kAlphaMin;
+        const float test_T = T[k] * (1.0f - alpha);
+        const bool fin = ok && test_T < kTransmittanceMin;
+        const bool blend = ok && !fin;
+        const float contribution = alpha * T[k];
+        c0[k] = blend ? c0[k] + f.x * contribution : c0[k];
+        c1[k] = blend ? c1[k] + f.y * contribution : c1[k];
+        c2[k] = blend ? c2[k] + f.z * contribution : c2[k];
+        ws[k] = blend ? ws[k] + contribution : ws[k];
+        if (p.compute_depth) da[k] = blend ? da[k] + b.z * contribution : da[k];
+        if (aux && blend && nsucc[k] < p.top_k) {
+          const size_t pix = (size_t)(py0 + 4 * k) * p.W + px;
+          const size_t ai = (size_t)nsucc[k] * P + pix;
+          p.gs_per_pixel[ai] = s_id[j];
+          p.weight[ai] = contribution;
+          p.x_mu[ai] = dx;
+          p.x_mu[(size_t)p.top_k * P + ai] = dy[k];
         }
-        const float contribution = alpha * T;
-        const float4 f = s_r2[j];
-        c0 = c0 + f.x * contribution;
-        c1 = c1 + f.y * contribution;
-        c2 = c2 + f.z * contribution;
-        wsum = wsum + contribution;
-        if (p.compute_depth) dacc = dacc + b.z * contribution;
-        if (aux && n_success < p.top_k) {
-          const size_t aux_idx = (size_t)n_success * P + pix;
-          p.gs_per_pixel[aux_idx] = s_id[j];
-          p.weight[aux_idx] = contribution;
-          p.x_mu[aux_idx] = dx;
-          p.x_mu[(size_t)p.top_k * P + aux_idx] = dy;
-        }
-        if (kFlow) ++n_success;
-        T = test_T;
-        last = r * kTilePixels + j + 1;
+        if (kFlow) nsucc[k] += blend ? 1 : 0;
+        T[k] = fin ? -T[k] : (blend ? test_T : T[k]);
+        last[k] = blend ? base + j + 1 : last[k];
       }
     }
   }
 
-  if (inside) {
-    p.n_contrib[pix] = last;
-    p.out_color[pix] = c0 + T * p.bg[0];
-    p.out_color[P + pix] = c1 + T * p.bg[1];
-    p.out_color[2 * P + pix] = c2 + T * p.bg[2];
-    p.out_alpha[pix] = wsum;
-    p.out_depth[pix] = dacc;
-    if (aux) {
-      for (int k = n_success; k < p.top_k; ++k) {
-        const size_t aux_idx = (size_t)k * P + pix;
-        p.gs_per_pixel[aux_idx] = -1;
-        p.weight[aux_idx] = 0.0f;
-        p.x_mu[aux_idx] = 0.0f;
-        p.x_mu[(size_t)p.top_k * P + aux_idx] = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kPixPerLane; ++k) {
+    const int py = py0 + 4 * k;
+    if (px < p.W && py < p.H) {
+      const int pix = py * p.W + px;
+      const float Tk = fabsf(T[k]);
+      p.n_contrib[pix] = last[k];
+      p.out_color[pix] = c0[k] + Tk * p.bg[0];
+      p.out_color[P + pix] = c1[k] + Tk * p.bg[1];
+      p.out_color[2 * P + pix] = c2[k] + Tk * p.bg[2];
+      p.out_alpha[pix] = ws[k];
+      p.out_depth[pix] = da[k];
+      if (aux) {
+        for (int s = nsucc[k]; s < p.top_k; ++s) {
+          const size_t ai = (size_t)s * P + pix;
+          p.gs_per_pixel[ai] = -1;
+          p.weight[ai] = 0.0f;
+          p.x_mu[ai] = 0.0f;
+          p.x_mu[(size_t)p.top_k * P + ai] = 0.0f;
+        }
       }
     }
   }
 }
 
 static int launch_render_fwd(const RenderFwdParams& p, bool flow, hipStream_t s) {
+  const dim3 grid(p.num_tiles * (4 / kFwdPix));
   if (flow)
-    hipLaunchKernelGGL(render_fwd_kernel<true>, dim3(p.num_tiles), dim3(kTilePixels), 0, s, p);
+    hipLaunchKernelGGL((render_fwd_kernel<true, kFwdPix>), grid, dim3(64), 0, s, p);
   else
-    hipLaunchKernelGGL(render_fwd_kernel<false>, dim3(p.num_tiles), dim3(kTilePixels), 0, s, p);
+    hipLaunchKernelGGL((render_fwd_kernel<false, kFwdPix>), grid, dim3(64), 0, s, p);
   return gs_status_from_hip(hipGetLastError());
 }
 
 }  // namespace gs
 
 static int gs_render_fwd_common(int32_t W, int32_t H, int32_t num_points, int64_t num_rendered,
-                                const int32_t* ranges, const int32_t* point_list,
-                                const float* records, const float* background, int32_t compute_depth,
-                                int32_t write_aux, int32_t top_k, float* out_color, float* out_depth,
-                                float* out_alpha, int32_t* n_contrib, int32_t* gs_per_pixel, float* weight,
-                                float* x_mu, bool flow, void* stream) {
+                                const int32_t* ranges, const int32_t* point_list, const float* records,
+                                const float* background, int32_t compute_depth, int32_t write_aux, int32_t top_k,
+                                float* out_color, float* out_depth, float* out_alpha, int32_t* n_contrib,
+                                int32_t* gs_per_pixel, float* weight, float* x_mu, bool flow, void* stream) {
   if (W <= 0 || H <= 0 || (long long)W * H > 0x7fffffffLL) return GS_ERR_INVALID_ARGUMENT;
   if (num_points <= 0 || num_rendered < 0) return GS_ERR_INVALID_ARGUMENT;
   if (num_rendered > 0x7fffffffLL) return GS_ERR_OVERFLOW;
@@ -182,24 +237,22 @@ static int gs_render_fwd_common(int32_t W, int32_t H, int32_t num_points, int64_
   return gs::launch_render_fwd(p, flow, (hipStream_t)stream);
 }
 
-extern "C" int gs_render_fwd(int32_t image_width, int32_t image_height, int32_t num_points,
-                             int64_t num_rendered, const int32_t* ranges,
-                             const int32_t* point_list, const float* records, const float* background,
-                             int32_t compute_depth, float* out_color, float* out_depth, float* out_alpha,
-                             int32_t* n_contrib, void* stream) {
+extern "C" int gs_render_fwd(int32_t image_width, int32_t image_height, int32_t num_points, int64_t num_rendered,
+                             const int32_t* ranges, const int32_t* point_list, const float* records,
+                             const float* background, int32_t compute_depth, float* out_color, float* out_depth,
+                             float* out_alpha, int32_t* n_contrib, void* stream) {
   return gs_render_fwd_common(image_width, image_height, num_points, num_rendered, ranges, point_list, records,
-                              background, compute_depth, 0,
-                              0, out_color, out_depth, out_alpha, n_contrib, nullptr, nullptr, nullptr, false,
-                              stream);
+                              background, compute_depth, 0, 0, out_color, out_depth, out_alpha, n_contrib, nullptr,
+                              nullptr, nullptr, false, stream);
 }
 
 extern "C" int gs_render_fwd_flow(int32_t image_width, int32_t image_height, int32_t num_points,
-                                  int64_t num_rendered, const int32_t* ranges,
-                                  const int32_t* point_list, const float* records, const float* background,
-                                  int32_t compute_depth, int32_t write_aux, int32_t top_k, float* out_color,
-                                  float* out_depth, float* out_alpha, int32_t* n_contrib, int32_t* gs_per_pixel,
+                                  int64_t num_rendered, const int32_t* ranges, const int32_t* point_list,
+                                  const float* records, const float* background, int32_t compute_depth,
+                                  int32_t write_aux, int32_t top_k, float* out_color, float* out_depth,
+                                  float* out_alpha, int32_t* n_contrib, int32_t* gs_per_pixel,
                                   float* weight_per_gs_pixel, float* x_mu, void* stream) {
   return gs_render_fwd_common(image_width, image_height, num_points, num_rendered, ranges, point_list, records,
-                              background, compute_depth, write_aux, top_k, out_color, out_depth, out_alpha, n_contrib, gs_per_pixel,
-                              weight_per_gs_pixel, x_mu, true, stream);
+                              background, compute_depth, write_aux, top_k, out_color, out_depth, out_alpha,
+                              n_contrib, gs_per_pixel, weight_per_gs_pixel, x_mu, true, stream);
 }

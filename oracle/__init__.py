@@ -29,6 +29,7 @@ CFLAGS = (
     "-shared",
     "-fopenmp",
     "-ffp-contract=off",
+    "-mfma",
     "-fno-fast-math",
     "-fno-finite-math-only",
 )

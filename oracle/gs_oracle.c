@@ -78,21 +78,22 @@ static inline int f2i(float f) {
 }
 
 /* exp: Cody–Waite reduction x = n ln2 + r, ln2 = 0.693359375 - 2.12194440e-4,
- * degree-7 Taylor polynomial of e^r, exact 2^n scaling. */
+ * degree-7 Taylor polynomial of e^r, exact 2^n scaling; every step one fused
+ * multiply-add (fmaf, correctly rounded). */
 float or_exp(float x) {
   if (x < -87.0f) return 0.0f;
   if (x > 88.0f) x = 88.0f;
   const float n = rintf(x * 1.44269504088896341f);
-  float r = x - n * 0.693359375f;
-  r = r - n * (-2.12194440e-4f);
+  float r = fmaf(n, -0.693359375f, x);
+  r = fmaf(n, 2.12194440e-4f, r);
   float p = 1.98412698e-4f;
-  p = p * r + 1.38888889e-3f;
-  p = p * r + 8.33333333e-3f;
-  p = p * r + 4.16666667e-2f;
-  p = p * r + 1.66666667e-1f;
-  p = p * r + 0.5f;
-  p = p * r + 1.0f;
-  p = p * r + 1.0f;
+  p = fmaf(p, r, 1.38888889e-3f);
+  p = fmaf(p, r, 8.33333333e-3f);
+  p = fmaf(p, r, 4.16666667e-2f);
+  p = fmaf(p, r, 1.66666667e-1f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
   return ldexpf(p, (int)n);
 }
 
