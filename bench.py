@@ -108,6 +108,90 @@ def read_traffic(stage: str):
     return None
 
 
+def measure_copy_bandwidth(device, nbytes: int = 1 << 30, reps: int = 5) -> float:
+    """Achievable HBM bandwidth (GB/s, read + write bytes) of a plain device copy of
+    nbytes, timed with HIP events on the current stream."""
+    import torch
+
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device=device).fill_(1.0)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    end.record()
+    end.synchronize()
+    seconds = start.elapsed_time(end) * 1e-3 / reps
+    del src, dst
+    return 2.0 * nbytes / seconds / 1e9
+
+
+# Kernel-name prefix -> pipeline stage, for the rocprofv3 PMC summary.
+STAGE_OF_KERNEL = (
+    ("gs::preprocess_fwd_kernel", "preprocess"),
+    ("gs::scan_", "scan"),
+    ("gs::zero_i64_kernel", "scan"),
+    ("gs::duplicate_keys_kernel", "duplicate"),
+    ("gs_sort::", "sort"),
+    ("gs::zero_ranges_kernel", "ranges"),
+    ("gs::tile_ranges_kernel", "ranges"),
+    ("gs::render_fwd_kernel", "render"),
+    ("gs::render_bwd_kernel", "render_bwd"),
+    ("gs::preprocess_bwd_kernel", "preprocess_bwd"),
+)
+
+
+def _stage_of(kernel_name: str):
+    name = kernel_name.replace("void ", "", 1)
+    for prefix, stage in STAGE_OF_KERNEL:
+        if name.startswith(prefix):
+            return stage
+    return None
+
+
+def summarize_pmc(fetch_csv: str, write_csv: str, out_path: str, copy_bytes: int = 1 << 30) -> None:
+    """Turn two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE, then WRITE_SIZE,
+    both in KiB per dispatch) into per-stage HBM bytes per launch.  Each counter is
+    scaled by what it reads for the calibration copy (the largest device copy, of
+    copy_bytes read and copy_bytes written), so the figures are in true bytes."""
+    import csv
+
+    def load(path, counter):
+        rows = [r for r in csv.DictReader(open(path)) if r["Counter_Name"] == counter]
+        per_stage = defaultdict(float)
+        copies = []
+        renders = 0
+        for r in rows:
+            value = float(r["Counter_Value"])
+            stage = _stage_of(r["Kernel_Name"])
+            if stage is not None:
+                per_stage[stage] += value
+            if "copyBuffer" in r["Kernel_Name"]:
+                copies.append(value)
+            if stage == "render":
+                renders += 1
+        return per_stage, max(copies), renders
+
+    fetch, fetch_copy, iters = load(fetch_csv, "FETCH_SIZE")
+    write, write_copy, iters_w = load(write_csv, "WRITE_SIZE")
+    f_scale = copy_bytes / fetch_copy
+    w_scale = copy_bytes / write_copy
+    lines = [
+        "# HBM traffic per launch of each stage (bytes), config 2, from rocprofv3 --pmc",
+        f"# FETCH_SIZE scale {f_scale:.2f} B/unit, WRITE_SIZE scale {w_scale:.2f} B/unit "
+        f"(calibration copy of {copy_bytes} B read + {copy_bytes} B written read "
+        f"{fetch_copy:.0f} / {write_copy:.0f} units)",
+        f"# iterations averaged: {iters} (fetch run), {iters_w} (write run)",
+    ]
+    for stage in sorted(set(fetch) | set(write)):
+        fb = fetch.get(stage, 0.0) * f_scale / max(iters, 1)
+        wb = write.get(stage, 0.0) * w_scale / max(iters_w, 1)
+        lines.append(f"{stage}: {fb + wb:.0f} fetch {fb:.0f} write {wb:.0f}")
+    Path(out_path).write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def cpu_baseline(scene, grads) -> dict:
     """One fwd+bwd of the same scene with the C oracle on this host's cores."""
     import oracle
@@ -143,7 +227,12 @@ def main() -> int:
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-stage-timing", action="store_true")
+    parser.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OUT"),
+                        help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) into OUT and exit")
     args = parser.parse_args()
+    if args.pmc_summary:
+        summarize_pmc(*args.pmc_summary)
+        return 0
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -249,6 +338,10 @@ def main() -> int:
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 5),
                     "traffic": read_traffic(dominant),
                     "algorithmic_bytes_per_launch": algo[dominant]}
+    copy_gbps = measure_copy_bandwidth(device)
+    log(f"[bench] device copy bandwidth {copy_gbps:.0f} GB/s")
+    if roofline is not None:
+        roofline["copy_GBps"] = round(copy_gbps, 1)
     iteration_bytes = 1056.0 * N + 252.0 * R + 52.0 * P + 24.0 * T if Rs else None
 
     result = {
@@ -270,6 +363,7 @@ def main() -> int:
         "fwd_ms": fwd_ms,
         "bwd_ms": bwd_ms,
         "fwd_bwd_ms": ms_per_step,
+        "hbm_copy_GBps": round(copy_gbps, 1),
         "iteration_hbm_frac": None if iteration_bytes is None else
         round(iteration_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 5),
         "stages": stages,
