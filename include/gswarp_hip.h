@@ -138,7 +138,8 @@ int gs_sort_pairs_u64(int64_t n, int32_t key_bits, uint64_t* keys, int32_t* valu
 int gs_tile_ranges(int64_t n, const uint64_t* sorted_keys, int32_t num_tiles, int32_t* ranges, void* stream);
 
 /*
- * Per-tile front-to-back alpha blending (16x16 tiles, one workgroup each).
+ * Per-tile front-to-back alpha blending of 16x16 tiles, each covered by
+ * independent wave64 workgroups that own a slice of its rows.
  * num_points (N) and num_rendered (R) bound every index read from ranges and
  * point_list.
  * Writes color + T*bg, alpha = sum of weights, depth (zero unless
