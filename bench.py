@@ -192,6 +192,37 @@ def summarize_pmc(fetch_csv: str, write_csv: str, out_path: str, copy_bytes: int
     print("\n".join(lines))
 
 
+def summarize_sq(counter_csv: str, out_path: str) -> None:
+    """Per-kernel means per dispatch of the SQ counters in one rocprofv3 --pmc
+    counter_collection.csv, with the LDS bank-conflict rate
+    (SQ_LDS_BANK_CONFLICT / SQ_ACTIVE_INST_LDS, both in cycles) and VALU
+    instructions per wave."""
+    import csv
+
+    per = defaultdict(lambda: defaultdict(float))
+    dispatches = defaultdict(set)
+    for r in csv.DictReader(open(counter_csv)):
+        name = r["Kernel_Name"]
+        short = name.replace("void ", "", 1).split("(")[0]
+        if _stage_of(name) is None:
+            continue
+        per[short][r["Counter_Name"]] += float(r["Counter_Value"])
+        dispatches[short].add(r["Dispatch_Id"])
+    counters = sorted({c for d in per.values() for c in d})
+    lines = ["# SQ counters per dispatch (mean), one MI355X; columns: kernel, dispatches, "
+             + ", ".join(counters) + ", lds_conflict_rate, valu_insts_per_wave"]
+    for k in sorted(per):
+        n = len(dispatches[k])
+        d = {c: per[k][c] / n for c in counters}
+        lds = d.get("SQ_ACTIVE_INST_LDS", 0.0)
+        rate = d.get("SQ_LDS_BANK_CONFLICT", 0.0) / lds if lds else 0.0
+        waves = d.get("SQ_WAVES", 0.0)
+        vpw = d.get("SQ_INSTS_VALU", 0.0) / waves if waves else 0.0
+        lines.append(f"{k} {n} " + " ".join(f"{d[c]:.4g}" for c in counters) + f" {rate:.4f} {vpw:.1f}")
+    Path(out_path).write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def cpu_baseline(scene, grads) -> dict:
     """One fwd+bwd of the same scene with the C oracle on this host's cores."""
     import oracle
@@ -229,7 +260,12 @@ def main() -> int:
     parser.add_argument("--no-stage-timing", action="store_true")
     parser.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OUT"),
                         help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) into OUT and exit")
+    parser.add_argument("--sq-summary", nargs=2, metavar=("COUNTER_CSV", "OUT"),
+                        help="summarise one rocprofv3 --pmc run of SQ counters into OUT and exit")
     args = parser.parse_args()
+    if args.sq_summary:
+        summarize_sq(*args.sq_summary)
+        return 0
     if args.pmc_summary:
         summarize_pmc(*args.pmc_summary)
         return 0
