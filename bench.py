@@ -73,24 +73,35 @@ class StageTimer:
 
 
 def sort_passes(tiles: int) -> int:
+    """Passes of the 64-bit (tile << 32 | depth) key sort, 8 bits each."""
     return math.ceil((32 + math.ceil(math.log2(tiles))) / 8)
 
 
-def algorithmic_bytes(N: int, R: float, P: int, T: int) -> dict:
+def algorithmic_bytes(N: int, R: float, P: int, T: int, sort_mode: str) -> dict:
     """Bytes crossing each stage boundary once (the SH3, depth-on accounting of the
-    reference dataflow): preprocess 112N + SH 228N, scan 8N, duplicate 44N + 12R,
-    sort passes*24R, ranges 8R + 8T, render 44R + 24P + 8T, render backward
-    44R + 28P + 40N + 8T, SH + preprocess backward 624N."""
-    return {
+    reference dataflow): preprocess 112N + SH 228N, scan 8N, duplicate 44N + 12R
+    (64-bit key + value) or 44N + 8R (tile id + value), ranges 8R + 8T, render
+    44R + 24P + 8T, render backward 44R + 28P + 40N + 8T, SH + preprocess
+    backward 624N.  Sorts: the one 64-bit key sort moves 24R per pass over
+    ceil((32 + ceil(log2 T)) / 8) passes; the depth-then-tile dataflow moves 16N
+    per pass over 4 passes for the depth sort and 16R per pass over
+    ceil(log2 T / 8) passes for the tile sort."""
+    out = {
         "preprocess": 340.0 * N,
         "scan": 8.0 * N,
-        "duplicate": 44.0 * N + 12.0 * R,
-        "sort": sort_passes(T) * 24.0 * R,
         "ranges": 8.0 * R + 8.0 * T,
         "render": 44.0 * R + 24.0 * P + 8.0 * T,
         "render_bwd": 44.0 * R + 28.0 * P + 40.0 * N + 8.0 * T,
         "preprocess_bwd": 624.0 * N,
     }
+    if sort_mode == "warp_radix":
+        out["duplicate"] = 44.0 * N + 12.0 * R
+        out["sort"] = sort_passes(T) * 24.0 * R
+    else:
+        out["duplicate"] = 44.0 * N + 8.0 * R
+        out["depth_sort"] = 4 * 16.0 * N
+        out["sort"] = math.ceil((T - 1).bit_length() / 8) * 16.0 * R
+    return out
 
 
 def read_traffic(stage: str):
@@ -132,10 +143,13 @@ STAGE_OF_KERNEL = (
     ("gs::preprocess_fwd_kernel", "preprocess"),
     ("gs::scan_", "scan"),
     ("gs::zero_i64_kernel", "scan"),
+    ("gs::depth_keys_kernel", "depth_sort"),
     ("gs::duplicate_keys_kernel", "duplicate"),
+    ("gs::duplicate_tiles_kernel", "duplicate"),
     ("gs_sort::", "sort"),
     ("gs::zero_ranges_kernel", "ranges"),
     ("gs::tile_ranges_kernel", "ranges"),
+    ("gs::tile_ranges_u32_kernel", "ranges"),
     ("gs::render_fwd_kernel", "render"),
     ("gs::render_bwd_kernel", "render_bwd"),
     ("gs::preprocess_bwd_kernel", "preprocess_bwd"),
@@ -258,6 +272,8 @@ def main() -> int:
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-stage-timing", action="store_true")
+    parser.add_argument("--sort-mode", default=None, choices=("warp_depth_stable_tile", "warp_radix", "torch"),
+                        help="binning sort mode (default: the API default, warp_depth_stable_tile)")
     parser.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OUT"),
                         help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) into OUT and exit")
     parser.add_argument("--sq-summary", nargs=2, metavar=("COUNTER_CSV", "OUT"),
@@ -278,13 +294,16 @@ def main() -> int:
 
     import torch
 
-    from gswarp_amd import _pipeline, configs
+    from gswarp_amd import _pipeline, _runtime, configs
     from gswarp_amd.rasterizer import GaussianRasterizationSettings, GaussianRasterizer
     from gswarp_amd.rasterizer_flow import GaussianRasterizationSettings as FlowSettings
     from gswarp_amd.rasterizer_flow import GaussianRasterizer as FlowRasterizer
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.sort_mode:
+        _runtime.set_binning_sort_mode(args.sort_mode)
+    sort_mode = _runtime.get_binning_sort_mode()
     spec = configs.CONFIGS[args.config]
     t0 = time.perf_counter()
     scene = configs.make_scene(args.config, seed=args.seed, count=args.count, device=device)
@@ -354,20 +373,29 @@ def main() -> int:
     fwd_ms = sum(a.elapsed_time(b) for a, b, _ in step_events) / len(step_events)
     bwd_ms = sum(b.elapsed_time(c) for _, b, c in step_events) / len(step_events)
     stage_ms = timer.mean_ms() if not args.no_stage_timing else {}
+    passes = timer.notes.get("sort_passes", [])
     Rs = timer.notes.get("num_rendered", [])
     R = sum(Rs) / len(Rs) if Rs else float("nan")
     log(f"[bench] {ms_per_step:.3f} ms/step (fwd {fwd_ms:.3f} ms, bwd {bwd_ms:.3f} ms), mean R={R:.0f}")
 
     roofline = None
+    binning_sort = None
     stages = {}
     if stage_ms and Rs:
-        algo = algorithmic_bytes(N, R, P, T)
+        algo = algorithmic_bytes(N, R, P, T, sort_mode)
         for name, ms in sorted(stage_ms.items(), key=lambda kv: -kv[1]):
             gbps = algo[name] / (ms * 1e-3) / 1e9 if name in algo else None
             stages[name] = {"ms": round(ms, 4), "algorithmic_bytes": algo.get(name),
                             "achieved_GBps": None if gbps is None else round(gbps, 1),
                             "hbm_frac": None if gbps is None else round(gbps / HBM_PEAK_GBPS, 4)}
             log(f"[bench]   {name:15s} {ms:8.4f} ms" + ("" if gbps is None else f"  {gbps:8.1f} GB/s"))
+        sort_names = [n for n in ("depth_sort", "sort") if n in stage_ms]
+        sort_ms = sum(stage_ms[n] for n in sort_names)
+        sort_bytes = sum(algo[n] for n in sort_names)
+        binning_sort = {"mode": sort_mode, "stages": sort_names, "ms": round(sort_ms, 4),
+                        "algorithmic_bytes": sort_bytes,
+                        "hbm_frac": round(sort_bytes / (sort_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+        log(f"[bench]   binning sort ({sort_mode}) {sort_ms:.4f} ms  {binning_sort['hbm_frac'] * 100:.1f}% of HBM peak")
         dominant = max((n for n in stage_ms if n in algo), key=lambda n: stage_ms[n])
         achieved = algo[dominant] / (stage_ms[dominant] * 1e-3) / 1e9
         roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
@@ -395,6 +423,7 @@ def main() -> int:
         "data": "synthetic (seeded Gaussians and cameras, BASELINE config distributions)",
         "config": {"workload": f"config{args.config}: {spec.description}", "gaussians": N, "width": W,
                    "height": H, "sh_degree": spec.sh_degree, "tiles": T, "mean_num_rendered": R,
+                   "mean_sort_passes": (sum(passes) / len(passes)) if passes else None,
                    "parallelism": "single GPU"},
         "fwd_ms": fwd_ms,
         "bwd_ms": bwd_ms,
@@ -403,6 +432,7 @@ def main() -> int:
         "iteration_hbm_frac": None if iteration_bytes is None else
         round(iteration_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 5),
         "stages": stages,
+        "binning_sort": binning_sort,
         "roofline": roofline,
         "cpu_baseline": None,
     }

@@ -36,13 +36,22 @@ SIGNATURES = {
     ),
     "gs_mark_visible": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp]),
     "gs_scan_scratch_bytes": (_sz, [_i32]),
-    "gs_scan_tiles": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "gs_depth_keys": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp]),
+    "gs_scan_tiles": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "gs_num_rendered_readback": (ctypes.c_int, [_vp, _vp, _vp]),
-    "gs_duplicate_keys": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp]),
+    "gs_duplicate_keys": (
+        ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, ctypes.c_uint32, _i32, _i32, _vp, _vp, _vp],
+    ),
+    "gs_duplicate_tiles": (
+        ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp],
+    ),
     "gs_sort_num_passes": (ctypes.c_int, [_i32]),
     "gs_sort_scratch_bytes": (_sz, [_i64]),
     "gs_sort_pairs_u64": (ctypes.c_int, [_i64, _i32, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
-    "gs_tile_ranges": (ctypes.c_int, [_i64, _vp, _i32, _vp, _vp]),
+    "gs_sort_keys_u64": (ctypes.c_int, [_i64, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
+    "gs_sort_pairs_u32": (ctypes.c_int, [_i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "gs_tile_ranges": (ctypes.c_int, [_i64, _vp, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "gs_tile_ranges_u32": (ctypes.c_int, [_i64, _vp, _i32, _vp, _vp]),
     "gs_render_fwd": (ctypes.c_int, [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
     "gs_render_fwd_flow": (
         ctypes.c_int,

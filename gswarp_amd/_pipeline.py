@@ -20,7 +20,7 @@ import torch
 from . import _lib, _workspace
 from ._coverage import tile_coverage_mode_id
 from ._runtime import BINNING_SORT_MODES, ExecutionOptions
-from ._state import BinningState, ForwardResult, ForwardState, PreprocessOutputs, RenderStageResult
+from ._state import BinningState, ForwardResult, ForwardState, KeyLayout, PreprocessOutputs, RenderStageResult
 
 BLOCK_X = 16
 BLOCK_Y = 16
@@ -190,11 +190,126 @@ def preprocess(inputs: RasterInputs, options: ExecutionOptions) -> PreprocessOut
     return out
 
 
+def key_layout(P: int, T: int, depth_min: int, depth_max: int) -> KeyLayout:
+    """Binning key fields: tile id above the visible depth range's bits above the
+    packed point index; the index is carried separately when the three do not fit."""
+    tile_bits = (T - 1).bit_length()
+    depth_bits = (depth_max - depth_min).bit_length() if depth_max >= depth_min else 0
+    value_bits = max(1, (P - 1).bit_length())
+    if tile_bits + depth_bits + value_bits > 64:
+        value_bits = 0
+    return KeyLayout(depth_min=depth_min, depth_bits=depth_bits, value_bits=value_bits)
+
+
 def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options: ExecutionOptions,
             keep_keys: bool = False) -> BinningState:
-    """Scan, pair-count readback, duplicate-with-keys, 64-bit sort, ranges (binning_ops.py:84-431)."""
-    if options.binning_sort_mode not in BINNING_SORT_MODES:
+    """Per-tile Gaussian lists (binning_ops.py:84-431) in the requested sort mode.
+
+    All three modes give identical point lists and ranges:
+    ``warp_depth_stable_tile`` (default) sorts the Gaussians by depth and then
+    the emitted (tile, point) pairs stably by tile with the HIP radix sort;
+    ``warp_radix`` sorts one packed 64-bit (tile, depth, point) key per pair
+    with the HIP radix sort; ``torch`` is the depth-then-tile dataflow with
+    ``torch.sort`` (stable) in place of the HIP radix sort.
+    """
+    mode = options.binning_sort_mode
+    if mode not in BINNING_SORT_MODES:
         raise ValueError("sort_mode must be one of 'torch', 'warp_radix', or 'warp_depth_stable_tile'")
+    if mode == "warp_radix":
+        return _binning_packed(pre, image_height, image_width, keep_keys)
+    return _binning_depth_tile(pre, image_height, image_width, keep_keys, use_torch=(mode == "torch"))
+
+
+def _note(key: str, value) -> None:
+    if STAGE_TIMER is not None and hasattr(STAGE_TIMER, "note"):
+        STAGE_TIMER.note(key, value)
+
+
+def _readback(lib, info: torch.Tensor, device: torch.device, stream: int) -> tuple[int, int]:
+    """(pair count, packed visible depth-bit range) after the scan: the forward's one host sync."""
+    pinned = _workspace.readback_buffer(device, torch.cuda.current_stream(device))
+    lib.call("gs_num_rendered_readback", info.data_ptr(), pinned.data_ptr(), stream)
+    R = validate_pair_count(int(pinned[0]))
+    _note("num_rendered", R)
+    return R, int(pinned[1]) & 0xFFFFFFFFFFFFFFFF
+
+
+def _empty_binning(grid_x: int, grid_y: int, device: torch.device) -> BinningState:
+    return BinningState(grid_x, grid_y, torch.empty((0,), dtype=torch.int32, device=device),
+                        torch.zeros((grid_x * grid_y, 2), dtype=torch.int32, device=device), 0)
+
+
+def _binning_depth_tile(pre: PreprocessOutputs, image_height: int, image_width: int, keep_keys: bool,
+                        use_torch: bool) -> BinningState:
+    lib = _lib.load()
+    device = pre.radii.device
+    P = pre.radii.shape[0]
+    grid_x, grid_y = grid_dims(image_width, image_height)
+    T = grid_x * grid_y
+    stream = _stream(device)
+    if P == 0:
+        return _empty_binning(grid_x, grid_y, device)
+    # 1. stable depth sort of the Gaussians (culled ones first with key 0)
+    dkeys = torch.empty((P,), dtype=torch.int32, device=device)
+    order = torch.empty((P,), dtype=torch.int32, device=device)
+    with _stage("depth_sort"):
+        lib.call("gs_depth_keys", P, pre.radii.data_ptr(), pre.depths.data_ptr(), dkeys.data_ptr(),
+                 order.data_ptr(), stream)
+        if use_torch:
+            dkeys, perm = torch.sort(dkeys, stable=True)
+            order = order[perm]
+        else:
+            dkeys_alt = torch.empty_like(dkeys)
+            order_alt = torch.empty_like(order)
+            scratch = torch.empty((max(int(lib.gs_sort_scratch_bytes(P)), 1),), dtype=torch.uint8, device=device)
+            lib.call("gs_sort_pairs_u32", P, 0, 32, dkeys.data_ptr(), order.data_ptr(), dkeys_alt.data_ptr(),
+                     order_alt.data_ptr(), scratch.data_ptr(), scratch.numel(), stream)
+            if lib.gs_sort_num_passes(32) % 2:
+                dkeys, order = dkeys_alt, order_alt
+    # 2. tile counts scanned in depth order, pair count to the host
+    offsets = torch.empty((P,), dtype=torch.int32, device=device)
+    info = torch.empty((2,), dtype=torch.int64, device=device)
+    scan_scratch = torch.empty((max(int(lib.gs_scan_scratch_bytes(P)), 1),), dtype=torch.uint8, device=device)
+    with _stage("scan"):
+        lib.call("gs_scan_tiles", P, pre.tiles_touched.data_ptr(), order.data_ptr(), pre.radii.data_ptr(),
+                 pre.depths.data_ptr(), offsets.data_ptr(), info.data_ptr(), scan_scratch.data_ptr(),
+                 scan_scratch.numel(), stream)
+    R, _ = _readback(lib, info, device, stream)
+    if R == 0:
+        return _empty_binning(grid_x, grid_y, device)
+    # 3. (tile, point) pairs in depth order, then a stable sort by tile
+    tiles = torch.empty((R,), dtype=torch.int32, device=device)
+    vals = torch.empty((R,), dtype=torch.int32, device=device)
+    with _stage("duplicate"):
+        lib.call("gs_duplicate_tiles", P, order.data_ptr(), pre.radii.data_ptr(), pre.records.data_ptr(),
+                 pre.conic_2d_inv.data_ptr(), offsets.data_ptr(), image_width, image_height, pre.coverage_mode, R,
+                 tiles.data_ptr(), vals.data_ptr(), stream)
+    tile_bits = (T - 1).bit_length()
+    _note("sort_passes", int(lib.gs_sort_num_passes(tile_bits)))
+    with _stage("sort"):
+        if use_torch:
+            tiles, perm = torch.sort(tiles, stable=True)
+            vals = vals[perm]
+        elif tile_bits > 0:
+            tiles_alt = torch.empty_like(tiles)
+            vals_alt = torch.empty_like(vals)
+            scratch = torch.empty((max(int(lib.gs_sort_scratch_bytes(R)), 1),), dtype=torch.uint8, device=device)
+            lib.call("gs_sort_pairs_u32", R, 0, tile_bits, tiles.data_ptr(), vals.data_ptr(), tiles_alt.data_ptr(),
+                     vals_alt.data_ptr(), scratch.data_ptr(), scratch.numel(), stream)
+            if lib.gs_sort_num_passes(tile_bits) % 2:
+                tiles, vals = tiles_alt, vals_alt
+    ranges = torch.empty((T, 2), dtype=torch.int32, device=device)
+    with _stage("ranges"):
+        lib.call("gs_tile_ranges_u32", R, tiles.data_ptr(), T, ranges.data_ptr(), stream)
+    keys = None
+    layout = KeyLayout(depth_min=0, depth_bits=32, value_bits=0)
+    if keep_keys:  # tile << 32 | depth bits, for tests
+        keys = (tiles.to(torch.int64) << 32) | (pre.depths.view(torch.int32)[vals.long()].to(torch.int64)
+                                                & 0xFFFFFFFF)
+    return BinningState(grid_x, grid_y, vals, ranges, R, keys, layout)
+
+
+def _binning_packed(pre: PreprocessOutputs, image_height: int, image_width: int, keep_keys: bool) -> BinningState:
     lib = _lib.load()
     device = pre.radii.device
     P = pre.radii.shape[0]
@@ -202,38 +317,44 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
     T = grid_x * grid_y
     stream = _stream(device)
     offsets = torch.empty((P,), dtype=torch.int32, device=device)
-    total = torch.empty((1,), dtype=torch.int64, device=device)
+    info = torch.empty((2,), dtype=torch.int64, device=device)
     scan_scratch = torch.empty((max(int(lib.gs_scan_scratch_bytes(P)), 1),), dtype=torch.uint8, device=device)
     with _stage("scan"):
-        lib.call("gs_scan_tiles", P, pre.tiles_touched.data_ptr(), offsets.data_ptr(), total.data_ptr(),
-                 scan_scratch.data_ptr(), scan_scratch.numel(), stream)
-    pinned = _workspace.readback_buffer(device, torch.cuda.current_stream(device))
-    lib.call("gs_num_rendered_readback", total.data_ptr(), pinned.data_ptr(), stream)
-    R = validate_pair_count(int(pinned[0]))
-    if STAGE_TIMER is not None and hasattr(STAGE_TIMER, "note"):
-        STAGE_TIMER.note("num_rendered", R)
+        lib.call("gs_scan_tiles", P, pre.tiles_touched.data_ptr(), None, pre.radii.data_ptr(), pre.depths.data_ptr(),
+                 offsets.data_ptr(), info.data_ptr(), scan_scratch.data_ptr(), scan_scratch.numel(), stream)
+    R, depth_range = _readback(lib, info, device, stream)
     if R == 0:
-        return BinningState(grid_x, grid_y, torch.empty((0,), dtype=torch.int32, device=device),
-                            torch.zeros((T, 2), dtype=torch.int32, device=device), 0)
+        return _empty_binning(grid_x, grid_y, device)
+    layout = key_layout(P, T, depth_range & 0xFFFFFFFF, depth_range >> 32)
+    packed = layout.value_bits > 0
     keys = torch.empty((R,), dtype=torch.int64, device=device)
-    vals = torch.empty((R,), dtype=torch.int32, device=device)
     keys_alt = torch.empty((R,), dtype=torch.int64, device=device)
-    vals_alt = torch.empty((R,), dtype=torch.int32, device=device)
+    vals = vals_alt = None
+    if not packed:
+        vals = torch.empty((R,), dtype=torch.int32, device=device)
+        vals_alt = torch.empty((R,), dtype=torch.int32, device=device)
     with _stage("duplicate"):
         lib.call("gs_duplicate_keys", P, pre.radii.data_ptr(), pre.records.data_ptr(),
                  pre.conic_2d_inv.data_ptr(), offsets.data_ptr(), image_width, image_height, pre.coverage_mode, R,
-                 keys.data_ptr(), vals.data_ptr(), stream)
-    key_bits = 32 + (T - 1).bit_length()
+                 layout.depth_min, layout.depth_bits, layout.value_bits, keys.data_ptr(), _lib.ptr(vals), stream)
+    sort_bits = (T - 1).bit_length() + layout.depth_bits
     sort_scratch = torch.empty((max(int(lib.gs_sort_scratch_bytes(R)), 1),), dtype=torch.uint8, device=device)
+    _note("sort_passes", int(lib.gs_sort_num_passes(sort_bits)))
     with _stage("sort"):
-        lib.call("gs_sort_pairs_u64", R, key_bits, keys.data_ptr(), vals.data_ptr(), keys_alt.data_ptr(),
-                 vals_alt.data_ptr(), sort_scratch.data_ptr(), sort_scratch.numel(), stream)
-    if lib.gs_sort_num_passes(key_bits) % 2:
+        if packed:
+            lib.call("gs_sort_keys_u64", R, layout.value_bits, sort_bits, keys.data_ptr(), keys_alt.data_ptr(),
+                     sort_scratch.data_ptr(), sort_scratch.numel(), stream)
+        else:
+            lib.call("gs_sort_pairs_u64", R, sort_bits, keys.data_ptr(), vals.data_ptr(), keys_alt.data_ptr(),
+                     vals_alt.data_ptr(), sort_scratch.data_ptr(), sort_scratch.numel(), stream)
+    if lib.gs_sort_num_passes(sort_bits) % 2:
         keys, vals = keys_alt, vals_alt
+    point_list = torch.empty((R,), dtype=torch.int32, device=device) if packed else vals
     ranges = torch.empty((T, 2), dtype=torch.int32, device=device)
     with _stage("ranges"):
-        lib.call("gs_tile_ranges", R, keys.data_ptr(), T, ranges.data_ptr(), stream)
-    return BinningState(grid_x, grid_y, vals, ranges, R, keys if keep_keys else None)
+        lib.call("gs_tile_ranges", R, keys.data_ptr(), layout.tile_shift, layout.value_bits, T, ranges.data_ptr(),
+                 point_list.data_ptr() if packed else None, stream)
+    return BinningState(grid_x, grid_y, point_list, ranges, R, keys if keep_keys else None, layout)
 
 
 def render(pre: PreprocessOutputs, bins: BinningState, background: torch.Tensor, image_height: int,

@@ -26,13 +26,38 @@ class PreprocessOutputs:
 
 
 @dataclass(slots=True)
+class KeyLayout:
+    """Fields of the 64-bit binning key, from high to low:
+    tile | float_bits(depth) - depth_min (depth_bits wide) | point index (value_bits wide, 0 = not packed)."""
+
+    depth_min: int = 0
+    depth_bits: int = 32
+    value_bits: int = 0
+
+    @property
+    def tile_shift(self) -> int:
+        return self.depth_bits + self.value_bits
+
+
+@dataclass(slots=True)
 class BinningState:
     grid_x: int
     grid_y: int
     point_list: torch.Tensor  # (R,) int32
     ranges: torch.Tensor  # (T, 2) int32
     num_rendered: int
-    sorted_keys: torch.Tensor | None = None  # (R,) int64: tile << 32 | depth bits
+    sorted_keys: torch.Tensor | None = None  # (R,) int64 sorted binning keys (see KeyLayout)
+    key_layout: KeyLayout = field(default_factory=KeyLayout)
+
+    def decode_keys(self) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """(tile id, depth float bits, sort field = tile and depth fields as one
+        non-negative int64) of every sorted pair, from sorted_keys."""
+        k = self.sorted_keys
+        lay = self.key_layout
+        field_ = (k >> lay.value_bits) & ((1 << (64 - lay.value_bits)) - 1) if lay.value_bits else k
+        tile = (k >> lay.tile_shift) & ((1 << (64 - lay.tile_shift)) - 1)
+        depth = (field_ & ((1 << lay.depth_bits) - 1)) + lay.depth_min
+        return tile, depth, field_
 
 
 @dataclass(slots=True)

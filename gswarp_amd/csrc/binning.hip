@@ -1,13 +1,20 @@
-// Tile binning: tile-count prefix sum, duplicate-with-keys, tile ranges.
+// Tile binning: depth sort keys, tile-count prefix sum, duplicate-with-keys,
+// tile ranges.  Two dataflows produce identical per-tile lists:
 //
-// The reference builds its per-tile lists with two stable sorts: all N
-// Gaussians by depth (binning_ops.py:152-222), then the R emitted
-// (tile, point) pairs by tile (binning_ops.py:297-343).  Here the pairs are
-// emitted once in point-index order with a 64-bit key tile<<32 | depth bits
-// and sorted once (sort.hip).  A stable sort of that key orders pairs by
-// (tile, depth bits, point index), which is exactly the order the
-// reference's depth-then-tile sorts produce, so point lists and tile ranges
-// are identical.
+// * depth then tile (the reference's default, binning_ops.py:152-222 and
+//   297-343): the N Gaussians are sorted stably by depth bits (culled ones
+//   first with key 0), the tile counts are scanned in that order, each
+//   Gaussian emits (tile id, index) pairs at its offset, and a stable sort of
+//   the R tile ids (ceil(log2 T) bits) orders pairs by (tile, depth, index).
+// * one 64-bit key (the reference's packed "warp_radix" mode): pairs are
+//   emitted in point-index order as
+//     key = ((tile << depth_bits) | (float_bits(depth) - depth_min)) << value_bits | point
+//   and sorted once on the tile and depth fields.  Subtracting the smallest
+//   visible depth's bits keeps the order and drops the bits all depths share;
+//   the point index rides in the low value_bits bits when the fields fit in
+//   64 bits, so the sort moves 8 bytes per pair.
+// Depths of binned Gaussians are positive, so their float bits order like the
+// depths; both stable sorts therefore give (tile, depth, point index) order.
 #include "gs_common.h"
 #include "gs_capi.h"
 
@@ -48,38 +55,127 @@ __device__ __forceinline__ long long block_exclusive_scan_i64(long long v, long 
   return wave_off + inc - v;
 }
 
+__device__ __forceinline__ unsigned wave_min_u32(unsigned v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned o = __shfl_xor(v, off, 64);
+    v = o < v ? o : v;
+  }
+  return v;
+}
+
+__device__ __forceinline__ unsigned wave_max_u32(unsigned v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned o = __shfl_xor(v, off, 64);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// Per block of kScanTile Gaussians: the tile-count sum, and the smallest and
+// largest depth bits of the Gaussians with radius > 0 (min ~0u / max 0 when
+// there are none), packed as max << 32 | min.
 __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(int n, const int* __restrict__ in,
-                                                                  long long* __restrict__ block_sums) {
+                                                                  const int* __restrict__ order,
+                                                                  const int* __restrict__ radii,
+                                                                  const float* __restrict__ depths,
+                                                                  long long* __restrict__ block_sums,
+                                                                  unsigned long long* __restrict__ block_range) {
   __shared__ long long lds4[kScanThreads / 64];
+  __shared__ unsigned s_min[kScanThreads / 64], s_max[kScanThreads / 64];
   const long long base = (long long)blockIdx.x * kScanTile;
   long long s = 0;
+  unsigned dmin = ~0u, dmax = 0u;
+  int cnt[kScanItems], rad[kScanItems];
+  unsigned bits[kScanItems];
 #pragma unroll
   for (int i = 0; i < kScanItems; ++i) {
     const long long idx = base + (long long)i * kScanThreads + threadIdx.x;
-    if (idx < n) s += in[idx];
+    cnt[i] = rad[i] = 0;
+    bits[i] = 0u;
+    if (idx < n) {
+      const int src = order ? order[idx] : (int)idx;
+      cnt[i] = in[src];
+      rad[i] = radii[src];
+      bits[i] = __float_as_uint(depths[src]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kScanItems; ++i) {
+    s += cnt[i];
+    if (rad[i] > 0) {
+      dmin = bits[i] < dmin ? bits[i] : dmin;
+      dmax = bits[i] > dmax ? bits[i] : dmax;
+    }
+  }
+  dmin = wave_min_u32(dmin);
+  dmax = wave_max_u32(dmax);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    s_min[wave] = dmin;
+    s_max[wave] = dmax;
   }
   long long total;
-  block_exclusive_scan_i64(s, lds4, &total);
-  if (threadIdx.x == 0) block_sums[blockIdx.x] = total;
+  block_exclusive_scan_i64(s, lds4, &total);  // its barriers also order s_min / s_max
+  if (threadIdx.x == 0) {
+    block_sums[blockIdx.x] = total;
+    unsigned mn = ~0u, mx = 0u;
+#pragma unroll
+    for (int w = 0; w < kScanThreads / 64; ++w) {
+      mn = s_min[w] < mn ? s_min[w] : mn;
+      mx = s_max[w] > mx ? s_max[w] : mx;
+    }
+    block_range[blockIdx.x] = ((unsigned long long)mx << 32) | mn;
+  }
 }
 
-// Single-workgroup exclusive scan of the block sums; also stores the total.
+// Single-workgroup exclusive scan of the block sums; stores the total pair
+// count in info[0] and the visible depth-bit range (max << 32 | min, or 0
+// when nothing is visible) in info[1].
 __global__ __launch_bounds__(kScanThreads) void scan_blocks_kernel(int nb, long long* __restrict__ block_sums,
-                                                                  long long* __restrict__ total_out) {
+                                                                  const unsigned long long* __restrict__ block_range,
+                                                                  long long* __restrict__ info) {
   __shared__ long long lds4[kScanThreads / 64];
+  __shared__ unsigned s_min[kScanThreads / 64], s_max[kScanThreads / 64];
   long long carry = 0;
+  unsigned dmin = ~0u, dmax = 0u;
   for (int base = 0; base < nb; base += kScanThreads) {
     const int i = base + threadIdx.x;
     const long long v = i < nb ? block_sums[i] : 0;
+    if (i < nb) {
+      const unsigned long long r = block_range[i];
+      const unsigned mn = (unsigned)r, mx = (unsigned)(r >> 32);
+      dmin = mn < dmin ? mn : dmin;
+      dmax = mx > dmax ? mx : dmax;
+    }
     long long tot;
     const long long ex = block_exclusive_scan_i64(v, lds4, &tot);
     if (i < nb) block_sums[i] = carry + ex;
     carry += tot;
   }
-  if (threadIdx.x == 0) *total_out = carry;
+  dmin = wave_min_u32(dmin);
+  dmax = wave_max_u32(dmax);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    s_min[wave] = dmin;
+    s_max[wave] = dmax;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned mn = ~0u, mx = 0u;
+#pragma unroll
+    for (int w = 0; w < kScanThreads / 64; ++w) {
+      mn = s_min[w] < mn ? s_min[w] : mn;
+      mx = s_max[w] > mx ? s_max[w] : mx;
+    }
+    info[0] = carry;
+    info[1] = mx >= mn ? (long long)(((unsigned long long)mx << 32) | mn) : 0;
+  }
 }
 
 __global__ __launch_bounds__(kScanThreads) void scan_apply_kernel(int n, const int* __restrict__ in,
+                                                                 const int* __restrict__ order,
                                                                  const long long* __restrict__ block_offsets,
                                                                  int* __restrict__ out) {
   __shared__ long long lds4[kScanThreads / 64];
@@ -89,9 +185,10 @@ __global__ __launch_bounds__(kScanThreads) void scan_apply_kernel(int n, const i
 #pragma unroll
   for (int i = 0; i < kScanItems; ++i) {
     const long long idx = base + i;
-    v[i] = idx < n ? in[idx] : 0;
-    s += v[i];
+    v[i] = idx < n ? in[order ? order[idx] : (int)idx] : 0;
   }
+#pragma unroll
+  for (int i = 0; i < kScanItems; ++i) s += v[i];
   long long total;
   long long run = block_offsets[blockIdx.x] + block_exclusive_scan_i64(s, lds4, &total);
 #pragma unroll
@@ -102,65 +199,71 @@ __global__ __launch_bounds__(kScanThreads) void scan_apply_kernel(int n, const i
   }
 }
 
-// Emission of one Gaussian's covered tiles, in the same enumeration as
-// count_covered_tiles (binning_kernels.py:127-216 semantics).
-__device__ __forceinline__ void emit_tiles(float px, float py, float ca, float cb, float cc, float opacity,
-                                           float cov_aa, float cov_cc, int radius, int grid_x, int grid_y,
-                                           int mode, uint32_t depth_bits, int point_id, long long off,
-                                           long long limit, unsigned long long* __restrict__ keys,
-                                           int* __restrict__ values) {
+// Visits one Gaussian's covered tiles in the enumeration order of
+// count_covered_tiles (binning_kernels.py:127-216 semantics), calling
+// f(tile_id) for each.
+template <typename F>
+__device__ __forceinline__ void for_each_covered_tile(float px, float py, float ca, float cb, float cc,
+                                                      float opacity, float cov_aa, float cov_cc, int radius,
+                                                      int grid_x, int grid_y, int mode, F&& f) {
   const int4 rect = snugbox_rect(px, py, cov_aa, cov_cc, opacity, radius, grid_x, grid_y);
   const int span_x = rect.z - rect.x;
   const int span_y = rect.w - rect.y;
   const int area = span_x * span_y;
-  const unsigned long long dk = (unsigned long long)depth_bits;
   if (area <= 1 || mode == kCoverageSnugbox) {
     for (int ty = rect.y; ty < rect.w; ++ty)
-      for (int tx = rect.x; tx < rect.z; ++tx) {
-        if (off < limit) {
-          keys[off] = ((unsigned long long)(ty * grid_x + tx) << 32) | dk;
-          values[off] = point_id;
-        }
-        ++off;
-      }
+      for (int tx = rect.x; tx < rect.z; ++tx) f(ty * grid_x + tx);
     return;
   }
   const float threshold = coverage_threshold(opacity);
   if (mode == kCoverageConicRect && area <= kConicMaskMaxTiles) {
     for (int ty = rect.y; ty < rect.w; ++ty)
       for (int tx = rect.x; tx < rect.z; ++tx)
-        if (conic_rect_intersects_tile(px, py, ca, cb, cc, threshold, tx, ty)) {
-          if (off < limit) {
-            keys[off] = ((unsigned long long)(ty * grid_x + tx) << 32) | dk;
-            values[off] = point_id;
-          }
-          ++off;
-        }
+        if (conic_rect_intersects_tile(px, py, ca, cb, cc, threshold, tx, ty)) f(ty * grid_x + tx);
     return;
   }
   if (span_y <= span_x) {
     for (int ty = rect.y; ty < rect.w; ++ty) {
       const int2 iv = accutile_band(px, py, ca, cb, cc, threshold, ty, kBlockX, kBlockY, rect.x, rect.z);
-      for (int tx = iv.x; tx < iv.y; ++tx) {
-        if (off < limit) {
-          keys[off] = ((unsigned long long)(ty * grid_x + tx) << 32) | dk;
-          values[off] = point_id;
-        }
-        ++off;
-      }
+      for (int tx = iv.x; tx < iv.y; ++tx) f(ty * grid_x + tx);
     }
   } else {
     for (int tx = rect.x; tx < rect.z; ++tx) {
       const int2 iv = accutile_band(py, px, cc, cb, ca, threshold, tx, kBlockY, kBlockX, rect.y, rect.w);
-      for (int ty = iv.x; ty < iv.y; ++ty) {
-        if (off < limit) {
-          keys[off] = ((unsigned long long)(ty * grid_x + tx) << 32) | dk;
-          values[off] = point_id;
-        }
-        ++off;
-      }
+      for (int ty = iv.x; ty < iv.y; ++ty) f(ty * grid_x + tx);
     }
   }
+}
+
+// 64-bit keys: key = tile << tile_shift | depth_field, where depth_field
+// already holds the depth offset (and the packed point index when values is
+// null).  Writes stop at `limit` (the pair count the scan reported).
+__device__ __forceinline__ void emit_tiles(float px, float py, float ca, float cb, float cc, float opacity,
+                                           float cov_aa, float cov_cc, int radius, int grid_x, int grid_y,
+                                           int mode, unsigned long long depth_field, int tile_shift,
+                                           int point_id, long long off, long long limit,
+                                           unsigned long long* __restrict__ keys, int* __restrict__ values) {
+  for_each_covered_tile(px, py, ca, cb, cc, opacity, cov_aa, cov_cc, radius, grid_x, grid_y, mode, [&](int tile) {
+    if (off < limit) {
+      keys[off] = ((unsigned long long)tile << tile_shift) | depth_field;
+      if (values) values[off] = point_id;
+    }
+    ++off;
+  });
+}
+
+// (tile id, point index) pairs for the stable tile sort.
+__device__ __forceinline__ void emit_tile_ids(float px, float py, float ca, float cb, float cc, float opacity,
+                                              float cov_aa, float cov_cc, int radius, int grid_x, int grid_y,
+                                              int mode, int point_id, long long off, long long limit,
+                                              unsigned* __restrict__ tiles, int* __restrict__ values) {
+  for_each_covered_tile(px, py, ca, cb, cc, opacity, cov_aa, cov_cc, radius, grid_x, grid_y, mode, [&](int tile) {
+    if (off < limit) {
+      tiles[off] = (unsigned)tile;
+      values[off] = point_id;
+    }
+    ++off;
+  });
 }
 
 __global__ __launch_bounds__(256) void duplicate_keys_kernel(int P, const int* __restrict__ radii,
@@ -168,6 +271,7 @@ __global__ __launch_bounds__(256) void duplicate_keys_kernel(int P, const int* _
                                                             const float* __restrict__ cov2d,
                                                             const int* __restrict__ offsets, int grid_x,
                                                             int grid_y, int mode, long long limit,
+                                                            unsigned depth_min, int depth_bits, int value_bits,
                                                             unsigned long long* __restrict__ keys,
                                                             int* __restrict__ values) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
@@ -179,12 +283,69 @@ __global__ __launch_bounds__(256) void duplicate_keys_kernel(int P, const int* _
   const float4 r1 = records[3 * (size_t)idx + 1];
   const float cov_aa = cov2d[3 * idx + 0];
   const float cov_cc = cov2d[3 * idx + 2];
-  emit_tiles(r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, cov_aa, cov_cc, radius, grid_x, grid_y, mode,
-             __float_as_uint(r1.z), idx, off, limit, keys, values);
+  const unsigned long long doff = (unsigned long long)(__float_as_uint(r1.z) - depth_min);
+  const unsigned long long field = (doff << value_bits) | (value_bits > 0 ? (unsigned long long)idx : 0ull);
+  emit_tiles(r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, cov_aa, cov_cc, radius, grid_x, grid_y, mode, field,
+             depth_bits + value_bits, idx, off, limit, keys, value_bits > 0 ? nullptr : values);
 }
 
-__global__ void zero_i64_kernel(long long* p) {
-  if (threadIdx.x == 0) *p = 0;
+// Depth-sort input (binning_kernels.py:27-40 semantics): key = float bits of
+// the depth for Gaussians with radius > 0 (positive floats order like their
+// bits), 0 for culled ones; value = point index.
+__global__ __launch_bounds__(256) void depth_keys_kernel(int P, const int* __restrict__ radii,
+                                                        const float* __restrict__ depths,
+                                                        unsigned* __restrict__ keys, int* __restrict__ values) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= P) return;
+  keys[i] = radii[i] > 0 ? __float_as_uint(depths[i]) : 0u;
+  values[i] = i;
+}
+
+// Emission in depth order: thread j emits the tiles of Gaussian order[j] at
+// offsets[j-1] as (tile id, point index) pairs (binning_kernels.py:411-451).
+__global__ __launch_bounds__(256) void duplicate_tiles_kernel(int P, const int* __restrict__ order,
+                                                             const int* __restrict__ radii,
+                                                             const float4* __restrict__ records,
+                                                             const float* __restrict__ cov2d,
+                                                             const int* __restrict__ offsets, int grid_x,
+                                                             int grid_y, int mode, long long limit,
+                                                             unsigned* __restrict__ tiles,
+                                                             int* __restrict__ values) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= P) return;
+  const int idx = order[j];
+  if ((unsigned)idx >= (unsigned)P) return;  // never taken for a permutation
+  const int radius = radii[idx];
+  if (radius <= 0) return;
+  const long long off = j > 0 ? (long long)offsets[j - 1] : 0;
+  const float4 r0 = records[3 * (size_t)idx + 0];
+  const float4 r1 = records[3 * (size_t)idx + 1];
+  const float cov_aa = cov2d[3 * idx + 0];
+  const float cov_cc = cov2d[3 * idx + 2];
+  emit_tile_ids(r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, cov_aa, cov_cc, radius, grid_x, grid_y, mode, idx, off, limit,
+                tiles, values);
+}
+
+__global__ __launch_bounds__(256) void tile_ranges_u32_kernel(long long n, const unsigned* __restrict__ tiles,
+                                                             int num_tiles, int2* __restrict__ ranges) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const unsigned tile = tiles[i];
+  if (tile >= (unsigned)num_tiles) return;  // never taken for ids from duplicate_tiles_kernel
+  if (i == 0) {
+    ranges[tile].x = 0;
+  } else {
+    const unsigned prev = tiles[i - 1];
+    if (tile != prev) {
+      if (prev < (unsigned)num_tiles) ranges[prev].y = (int)i;
+      ranges[tile].x = (int)i;
+    }
+  }
+  if (i == n - 1) ranges[tile].y = (int)n;
+}
+
+__global__ void zero_info_kernel(long long* p) {
+  if (threadIdx.x < 2) p[threadIdx.x] = 0;
 }
 
 __global__ __launch_bounds__(256) void zero_ranges_kernel(int n2, int* __restrict__ ranges) {
@@ -192,18 +353,23 @@ __global__ __launch_bounds__(256) void zero_ranges_kernel(int n2, int* __restric
   if (i < n2) ranges[i] = 0;
 }
 
+// ranges[t] = [start, end) of tile t in the sorted keys (tile = key >> tile_shift);
+// with value_bits > 0 also unpacks point_list[i] = low value_bits of key i.
 __global__ __launch_bounds__(256) void tile_ranges_kernel(long long n, const unsigned long long* __restrict__ keys,
-                                                         int num_tiles, int2* __restrict__ ranges) {
+                                                         int tile_shift, int value_bits, int num_tiles,
+                                                         int2* __restrict__ ranges, int* __restrict__ point_list) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const unsigned tile = (unsigned)(keys[i] >> 32);
-  if (tile >= (unsigned)num_tiles) return;  // never taken for keys from gs_duplicate_keys
+  const unsigned long long k = keys[i];
+  if (value_bits > 0) point_list[i] = (int)(k & ((1ull << value_bits) - 1ull));
+  const unsigned long long tile = k >> tile_shift;
+  if (tile >= (unsigned long long)num_tiles) return;  // never taken for keys from gs_duplicate_keys
   if (i == 0) {
     ranges[tile].x = 0;
   } else {
-    const unsigned prev = (unsigned)(keys[i - 1] >> 32);
+    const unsigned long long prev = keys[i - 1] >> tile_shift;
     if (tile != prev) {
-      if (prev < (unsigned)num_tiles) ranges[prev].y = (int)i;
+      if (prev < (unsigned long long)num_tiles) ranges[prev].y = (int)i;
       ranges[tile].x = (int)i;
     }
   }
@@ -235,34 +401,36 @@ static inline int gs_scan_blocks(int32_t P) { return (P + gs::kScanTile - 1) / g
 
 extern "C" size_t gs_scan_scratch_bytes(int32_t P) {
   if (P <= 0) return 0;
-  return ((size_t)gs_scan_blocks(P) * sizeof(long long) + 255) & ~(size_t)255;
+  return ((size_t)gs_scan_blocks(P) * 2 * sizeof(long long) + 255) & ~(size_t)255;
 }
 
-extern "C" int gs_scan_tiles(int32_t P, const int32_t* tiles_touched, int32_t* offsets, int64_t* total_dev,
-                             void* scratch, size_t scratch_bytes, void* stream) {
-  if (P < 0 || !total_dev) return GS_ERR_INVALID_ARGUMENT;
+extern "C" int gs_scan_tiles(int32_t P, const int32_t* tiles_touched, const int32_t* order, const int32_t* radii,
+                             const float* depths, int32_t* offsets, int64_t* info_dev, void* scratch,
+                             size_t scratch_bytes, void* stream) {
+  if (P < 0 || !info_dev) return GS_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
   if (P == 0) {
-    hipLaunchKernelGGL(gs::zero_i64_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<long long*>(total_dev));
+    hipLaunchKernelGGL(gs::zero_info_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<long long*>(info_dev));
     return gs_status_from_hip(hipGetLastError());
   }
-  if (!tiles_touched || !offsets || !scratch) return GS_ERR_INVALID_ARGUMENT;
+  if (!tiles_touched || !radii || !depths || !offsets || !scratch) return GS_ERR_INVALID_ARGUMENT;
   if (scratch_bytes < gs_scan_scratch_bytes(P)) return GS_ERR_SCRATCH_TOO_SMALL;
   const int nb = gs_scan_blocks(P);
   long long* block_sums = reinterpret_cast<long long*>(scratch);
-  hipLaunchKernelGGL(gs::scan_reduce_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, tiles_touched,
-                     block_sums);
-  hipLaunchKernelGGL(gs::scan_blocks_kernel, dim3(1), dim3(gs::kScanThreads), 0, s, nb, block_sums,
-                     reinterpret_cast<long long*>(total_dev));
-  hipLaunchKernelGGL(gs::scan_apply_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, tiles_touched,
+  unsigned long long* block_range = reinterpret_cast<unsigned long long*>(block_sums + nb);
+  hipLaunchKernelGGL(gs::scan_reduce_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, tiles_touched, order,
+                     radii, depths, block_sums, block_range);
+  hipLaunchKernelGGL(gs::scan_blocks_kernel, dim3(1), dim3(gs::kScanThreads), 0, s, nb, block_sums, block_range,
+                     reinterpret_cast<long long*>(info_dev));
+  hipLaunchKernelGGL(gs::scan_apply_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, tiles_touched, order,
                      block_sums, offsets);
   return gs_status_from_hip(hipGetLastError());
 }
 
-extern "C" int gs_num_rendered_readback(const int64_t* total_dev, int64_t* total_host_pinned, void* stream) {
-  if (!total_dev || !total_host_pinned) return GS_ERR_INVALID_ARGUMENT;
+extern "C" int gs_num_rendered_readback(const int64_t* info_dev, int64_t* info_host_pinned, void* stream) {
+  if (!info_dev || !info_host_pinned) return GS_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
-  hipError_t e = hipMemcpyAsync(total_host_pinned, total_dev, sizeof(int64_t), hipMemcpyDeviceToHost, s);
+  hipError_t e = hipMemcpyAsync(info_host_pinned, info_dev, 2 * sizeof(int64_t), hipMemcpyDeviceToHost, s);
   if (e != hipSuccess) return (int)e;
   return gs_status_from_hip(hipStreamSynchronize(s));
 }
@@ -270,34 +438,84 @@ extern "C" int gs_num_rendered_readback(const int64_t* total_dev, int64_t* total
 extern "C" int gs_duplicate_keys(int32_t P, const int32_t* radii, const float* records,
                                  const float* conic_2d_inv, const int32_t* offsets, int32_t image_width,
                                  int32_t image_height, int32_t coverage_mode, int64_t num_rendered,
-                                 uint64_t* keys_out, int32_t* values_out, void* stream) {
+                                 uint32_t depth_min, int32_t depth_bits, int32_t value_bits, uint64_t* keys_out,
+                                 int32_t* values_out, void* stream) {
+  if (P < 0 || image_width <= 0 || image_height <= 0 || coverage_mode < 0 || coverage_mode > 2)
+    return GS_ERR_INVALID_ARGUMENT;
+  if (depth_bits < 0 || depth_bits > 32 || value_bits < 0 || value_bits > 31) return GS_ERR_INVALID_ARGUMENT;
+  const int grid_x = (image_width + gs::kBlockX - 1) / gs::kBlockX;
+  const int grid_y = (image_height + gs::kBlockY - 1) / gs::kBlockY;
+  const int tile_bits = gs_bit_length(grid_x * grid_y - 1);
+  if (tile_bits + depth_bits + value_bits > 64) return GS_ERR_INVALID_ARGUMENT;
+  if (value_bits > 0 && gs_bit_length(P - 1) > value_bits) return GS_ERR_INVALID_ARGUMENT;
+  if (P == 0 || num_rendered <= 0) return GS_OK;
+  if (!radii || !records || !conic_2d_inv || !offsets || !keys_out || (value_bits == 0 && !values_out))
+    return GS_ERR_INVALID_ARGUMENT;
+  if (reinterpret_cast<uintptr_t>(records) & 15) return GS_ERR_MISALIGNED;
+  hipLaunchKernelGGL(gs::duplicate_keys_kernel, dim3((P + 255) / 256), dim3(256), 0, (hipStream_t)stream, P,
+                     radii, reinterpret_cast<const float4*>(records), conic_2d_inv, offsets, grid_x, grid_y,
+                     coverage_mode, (long long)num_rendered, depth_min, depth_bits, value_bits,
+                     reinterpret_cast<unsigned long long*>(keys_out), values_out);
+  return gs_status_from_hip(hipGetLastError());
+}
+
+extern "C" int gs_tile_ranges(int64_t n, const uint64_t* sorted_keys, int32_t tile_shift, int32_t value_bits,
+                              int32_t num_tiles, int32_t* ranges, int32_t* point_list, void* stream) {
+  if (n < 0 || num_tiles <= 0 || !ranges) return GS_ERR_INVALID_ARGUMENT;
+  if (tile_shift < 0 || tile_shift > 63 || value_bits < 0 || value_bits > 31 || value_bits > tile_shift)
+    return GS_ERR_INVALID_ARGUMENT;
+  if (n > 0x7fffffffLL) return GS_ERR_OVERFLOW;
+  hipStream_t s = (hipStream_t)stream;
+  const int n2 = 2 * num_tiles;
+  hipLaunchKernelGGL(gs::zero_ranges_kernel, dim3((n2 + 255) / 256), dim3(256), 0, s, n2, ranges);
+  if (n > 0) {
+    if (!sorted_keys || (value_bits > 0 && !point_list)) return GS_ERR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(gs::tile_ranges_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (long long)n,
+                       reinterpret_cast<const unsigned long long*>(sorted_keys), tile_shift, value_bits, num_tiles,
+                       reinterpret_cast<int2*>(ranges), point_list);
+  }
+  return gs_status_from_hip(hipGetLastError());
+}
+
+extern "C" int gs_depth_keys(int32_t P, const int32_t* radii, const float* depths, uint32_t* keys_out,
+                             int32_t* values_out, void* stream) {
+  if (P < 0) return GS_ERR_INVALID_ARGUMENT;
+  if (P == 0) return GS_OK;
+  if (!radii || !depths || !keys_out || !values_out) return GS_ERR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(gs::depth_keys_kernel, dim3((P + 255) / 256), dim3(256), 0, (hipStream_t)stream, P, radii,
+                     depths, keys_out, values_out);
+  return gs_status_from_hip(hipGetLastError());
+}
+
+extern "C" int gs_duplicate_tiles(int32_t P, const int32_t* order, const int32_t* radii, const float* records,
+                                  const float* conic_2d_inv, const int32_t* offsets, int32_t image_width,
+                                  int32_t image_height, int32_t coverage_mode, int64_t num_rendered,
+                                  uint32_t* tiles_out, int32_t* values_out, void* stream) {
   if (P < 0 || image_width <= 0 || image_height <= 0 || coverage_mode < 0 || coverage_mode > 2)
     return GS_ERR_INVALID_ARGUMENT;
   if (P == 0 || num_rendered <= 0) return GS_OK;
-  if (!radii || !records || !conic_2d_inv || !offsets || !keys_out || !values_out)
+  if (!order || !radii || !records || !conic_2d_inv || !offsets || !tiles_out || !values_out)
     return GS_ERR_INVALID_ARGUMENT;
   if (reinterpret_cast<uintptr_t>(records) & 15) return GS_ERR_MISALIGNED;
   const int grid_x = (image_width + gs::kBlockX - 1) / gs::kBlockX;
   const int grid_y = (image_height + gs::kBlockY - 1) / gs::kBlockY;
-  hipLaunchKernelGGL(gs::duplicate_keys_kernel, dim3((P + 255) / 256), dim3(256), 0, (hipStream_t)stream, P,
+  hipLaunchKernelGGL(gs::duplicate_tiles_kernel, dim3((P + 255) / 256), dim3(256), 0, (hipStream_t)stream, P, order,
                      radii, reinterpret_cast<const float4*>(records), conic_2d_inv, offsets, grid_x, grid_y,
-                     coverage_mode, (long long)num_rendered, reinterpret_cast<unsigned long long*>(keys_out),
-                     values_out);
+                     coverage_mode, (long long)num_rendered, tiles_out, values_out);
   return gs_status_from_hip(hipGetLastError());
 }
 
-extern "C" int gs_tile_ranges(int64_t n, const uint64_t* sorted_keys, int32_t num_tiles, int32_t* ranges,
-                              void* stream) {
+extern "C" int gs_tile_ranges_u32(int64_t n, const uint32_t* sorted_tiles, int32_t num_tiles, int32_t* ranges,
+                                  void* stream) {
   if (n < 0 || num_tiles <= 0 || !ranges) return GS_ERR_INVALID_ARGUMENT;
   if (n > 0x7fffffffLL) return GS_ERR_OVERFLOW;
   hipStream_t s = (hipStream_t)stream;
   const int n2 = 2 * num_tiles;
   hipLaunchKernelGGL(gs::zero_ranges_kernel, dim3((n2 + 255) / 256), dim3(256), 0, s, n2, ranges);
   if (n > 0) {
-    if (!sorted_keys) return GS_ERR_INVALID_ARGUMENT;
-    hipLaunchKernelGGL(gs::tile_ranges_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (long long)n,
-                       reinterpret_cast<const unsigned long long*>(sorted_keys), num_tiles,
-                       reinterpret_cast<int2*>(ranges));
+    if (!sorted_tiles) return GS_ERR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(gs::tile_ranges_u32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                       (long long)n, sorted_tiles, num_tiles, reinterpret_cast<int2*>(ranges));
   }
   return gs_status_from_hip(hipGetLastError());
 }

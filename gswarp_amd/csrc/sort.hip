@@ -1,15 +1,18 @@
-// Stable LSD radix sort of (uint64 key, int32 value) pairs for gfx950.
+// Stable LSD radix sort of uint32 or uint64 keys (optionally with int32
+// values) for gfx950, on a bit field [lo_bit, lo_bit + key_bits) of the key.
 //
 // Per 8-bit digit pass (reduce-then-scan):
-//   1. upsweep:   each 4096-element block histograms its digits in LDS
-//                 (one 256-bin histogram per wave) -> hist[digit][block].
-//   2. rowscan:   one workgroup per digit scans hist[digit][*] across blocks
+//   1. upsweep:   each 4096-element block counts its digits -> hist[digit][block].
+//   2. rowscan:   one wave per digit scans hist[digit][*] across blocks
 //                 (exclusive) and records the digit total.
-//   3. downsweep: each block ranks its elements stably with 64-lane ballot
-//                 matching (8 ballots per item give the set of lanes holding
-//                 the same digit), stages them in LDS in digit order, and
-//                 writes them out so that consecutive lanes store consecutive
-//                 addresses within each digit run.
+//   3. downsweep: each block ranks its elements stably, stages them in LDS in
+//                 digit order, and writes them out so that consecutive lanes
+//                 store consecutive addresses within each digit run.
+// The downsweep ranks with ballot matching: 8 ballots give each lane the set
+// of lanes holding its digit, the lane's rank among them is a popcount, and
+// only the lowest such lane updates the wave's counter, so ranks are stable
+// and keys whose digits take few values (the exponent bits of depths, the
+// high bits of tile ids) cause no LDS serialisation.
 // Element e of block b is handled by wave w = (e / 1024), item slot
 // i = (e % 1024) / 64, lane = e % 64, so processing slots in order with a
 // per-wave running counter preserves the input order among equal digits.
@@ -48,53 +51,108 @@ __device__ __forceinline__ unsigned block_exclusive_scan_u32(unsigned v, unsigne
   return wave_off + inc - v;
 }
 
-__global__ __launch_bounds__(kThreads) void upsweep_kernel(const u64* __restrict__ keys, long long n, int shift,
+template <typename K>
+__device__ __forceinline__ unsigned digit_of(K key, int shift) { return (unsigned)(key >> shift) & (kRadix - 1); }
+
+// Lanes of the wave holding the same digit d as this lane (among valid lanes).
+// Per bit b: s = bit b of d sign-extended (0 or ~0, one v_bfe_i32), m = ballot
+// of that bit, and the lanes agreeing with this lane's bit are ~(m ^ s).  The
+// update peers &= ~(m ^ s) is one v_bitop3_b32 per 32-bit half with truth
+// table 0x84 = S1 & ~(S0 ^ S2) (peers as S1; symmetric in S0 and S2).
+__device__ __forceinline__ u64 match_digit(unsigned d, bool valid) {
+  const u64 v = __ballot(valid);
+  unsigned lo = (unsigned)v, hi = (unsigned)(v >> 32);
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const unsigned s = (unsigned)__builtin_amdgcn_sbfe((int)d, b, 1);
+    const u64 m = __ballot(s != 0u);
+    lo = __builtin_amdgcn_bitop3_b32((unsigned)m, lo, s, 0x84);
+    hi = __builtin_amdgcn_bitop3_b32((unsigned)(m >> 32), hi, s, 0x84);
+  }
+  return ((u64)hi << 32) | lo;
+}
+
+// Digit counts of one block.  Counting needs no stable order, so lanes add
+// into one of kCopies histogram copies chosen by lane % kCopies with LDS
+// atomics; copies sit kRadix + 1 words apart, so equal digits in different
+// copies fall in different banks and a wave whose lanes share one digit
+// serialises 64 / kCopies deep instead of 64.
+constexpr int kCopies = 8;
+constexpr int kCopyStride = kRadix + 1;
+
+template <typename K>
+__global__ __launch_bounds__(kThreads) void upsweep_kernel(const K* __restrict__ keys, long long n, int shift,
                                                           int nb, unsigned* __restrict__ hist) {
-  __shared__ unsigned wh[kWaves][kRadix];
+  __shared__ unsigned h[kCopies * kCopyStride];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int i = threadIdx.x; i < kWaves * kRadix; i += kThreads) (&wh[0][0])[i] = 0;
-  __syncthreads();
+  for (int i = threadIdx.x; i < kCopies * kCopyStride; i += kThreads) h[i] = 0;
   const long long base = (long long)blockIdx.x * kTile + wave * (64 * kItems) + lane;
+  K key[kItems];
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     const long long idx = base + i * 64;
-    if (idx < n) {
-      const unsigned d = (unsigned)(keys[idx] >> shift) & (kRadix - 1);
-      atomicAdd(&wh[wave][d], 1u);
-    }
+    key[i] = idx < n ? keys[idx] : K(0);
   }
   __syncthreads();
+  unsigned* mine = h + (lane & (kCopies - 1)) * kCopyStride;
+#pragma unroll
+  for (int i = 0; i < kItems; ++i)
+    if (base + i * 64 < n) atomicAdd(mine + digit_of(key[i], shift), 1u);
+  __syncthreads();
   const int d = threadIdx.x;
-  const unsigned c = wh[0][d] + wh[1][d] + wh[2][d] + wh[3][d];
+  unsigned c = 0;
+#pragma unroll
+  for (int k = 0; k < kCopies; ++k) c += h[k * kCopyStride + d];
   hist[(size_t)d * nb + blockIdx.x] = c;
 }
 
+// One wave per digit row: hist[d][*] becomes its exclusive prefix over blocks
+// and digit_totals[d] the row total.  Lanes take 16 consecutive entries each,
+// so a row of up to 1024 blocks is one round of loads.
 __global__ __launch_bounds__(kThreads) void rowscan_kernel(int nb, unsigned* __restrict__ hist,
                                                           unsigned* __restrict__ digit_totals) {
-  __shared__ unsigned lds_w[kWaves];
-  unsigned* row = hist + (size_t)blockIdx.x * nb;
+  constexpr int kPer = 16;
+  const int lane = threadIdx.x & 63;
+  const int d = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  unsigned* row = hist + (size_t)d * nb;
   unsigned carry = 0;
-  for (int base = 0; base < nb; base += kThreads) {
-    const int i = base + threadIdx.x;
-    const unsigned v = i < nb ? row[i] : 0u;
-    unsigned tot;
-    const unsigned ex = block_exclusive_scan_u32(v, lds_w, &tot);
-    if (i < nb) row[i] = carry + ex;
-    carry += tot;
+  for (int base = 0; base < nb; base += 64 * kPer) {
+    unsigned v[kPer];
+    unsigned sum = 0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int idx = base + lane * kPer + i;
+      v[i] = idx < nb ? row[idx] : 0u;
+      sum += v[i];
+    }
+    unsigned inc = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const unsigned t = __shfl_up(inc, off, 64);
+      if (lane >= off) inc += t;
+    }
+    unsigned run = carry + inc - sum;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int idx = base + lane * kPer + i;
+      if (idx < nb) row[idx] = run;
+      run += v[i];
+    }
+    carry += __shfl(inc, 63, 64);
   }
-  if (threadIdx.x == 0) digit_totals[blockIdx.x] = carry;
+  if (lane == 0) digit_totals[d] = carry;
 }
 
-__global__ __launch_bounds__(kThreads) void downsweep_kernel(const u64* __restrict__ keys_in,
+template <typename K, bool kValues>
+__global__ __launch_bounds__(kThreads) void downsweep_kernel(const K* __restrict__ keys_in,
                                                             const int* __restrict__ vals_in,
-                                                            u64* __restrict__ keys_out, int* __restrict__ vals_out,
+                                                            K* __restrict__ keys_out, int* __restrict__ vals_out,
                                                             long long n, int shift, int nb,
                                                             const unsigned* __restrict__ hist,
                                                             const unsigned* __restrict__ digit_totals) {
-  __shared__ u64 s_keys[kTile];
-  __shared__ int s_vals[kTile];
+  __shared__ K s_keys[kTile];
+  __shared__ int s_vals[kValues ? kTile : 1];
   __shared__ unsigned s_wcount[kWaves][kRadix];
   __shared__ unsigned s_dstart[kRadix];
   __shared__ long long s_gbase[kRadix];
@@ -109,18 +167,14 @@ __global__ __launch_bounds__(kThreads) void downsweep_kernel(const u64* __restri
 #pragma unroll
   for (int i = threadIdx.x; i < kWaves * kRadix; i += kThreads) (&s_wcount[0][0])[i] = 0;
 
-  u64 key[kItems];
+  K key[kItems];
   int val[kItems];
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     const long long idx = wave_base + i * 64;
-    if (idx < n) {
-      key[i] = keys_in[idx];
-      val[i] = vals_in[idx];
-    } else {
-      key[i] = 0;
-      val[i] = 0;
-    }
+    const bool in = idx < n;
+    key[i] = in ? keys_in[idx] : K(0);
+    if (kValues) val[i] = in ? vals_in[idx] : 0;
   }
   __syncthreads();
 
@@ -129,20 +183,13 @@ __global__ __launch_bounds__(kThreads) void downsweep_kernel(const u64* __restri
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     const bool valid = (wave_base + i * 64) < n;
-    const unsigned d = (unsigned)(key[i] >> shift) & (kRadix - 1);
-    u64 peers = __ballot(valid);
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      const bool bit = (d >> b) & 1u;
-      const u64 m = __ballot(bit);
-      peers &= bit ? m : ~m;
-    }
+    const unsigned d = digit_of(key[i], shift);
+    const u64 peers = match_digit(d, valid);
     unsigned before = 0;
     if (valid) before = s_wcount[wave][d];
     __builtin_amdgcn_wave_barrier();
     const unsigned below = (unsigned)__popcll(peers & lt_mask);
-    const bool leader = valid && below == 0;
-    if (leader) s_wcount[wave][d] = before + (unsigned)__popcll(peers);
+    if (valid && below == 0) s_wcount[wave][d] = before + (unsigned)__popcll(peers);
     __builtin_amdgcn_wave_barrier();
     rank[i] = before + below;
   }
@@ -172,10 +219,10 @@ __global__ __launch_bounds__(kThreads) void downsweep_kernel(const u64* __restri
   for (int i = 0; i < kItems; ++i) {
     const bool valid = (wave_base + i * 64) < n;
     if (valid) {
-      const unsigned d = (unsigned)(key[i] >> shift) & (kRadix - 1);
+      const unsigned d = digit_of(key[i], shift);
       const unsigned lp = s_dstart[d] + s_wcount[wave][d] + rank[i];
       s_keys[lp] = key[i];
-      s_vals[lp] = val[i];
+      if (kValues) s_vals[lp] = val[i];
     }
   }
   __syncthreads();
@@ -184,18 +231,21 @@ __global__ __launch_bounds__(kThreads) void downsweep_kernel(const u64* __restri
   for (int j = 0; j < kItems; ++j) {
     const int p = j * kThreads + threadIdx.x;
     if (p < block_count) {
-      const u64 k = s_keys[p];
-      const unsigned d = (unsigned)(k >> shift) & (kRadix - 1);
-      const long long gp = s_gbase[d] + p;
+      const K k = s_keys[p];
+      const long long gp = s_gbase[digit_of(k, shift)] + p;
       if (gp >= 0 && gp < n) {  // always true for a consistent histogram
         keys_out[gp] = k;
-        vals_out[gp] = s_vals[p];
+        if (kValues) vals_out[gp] = s_vals[p];
       }
     }
   }
 }
 
 static inline int num_blocks(long long n) { return (int)((n + kTile - 1) / kTile); }
+
+template <typename K, bool kValues>
+static int sort_impl(int64_t n, int32_t lo_bit, int32_t key_bits, K* kin, K* kout, int* vin, int* vout,
+                     void* scratch, size_t scratch_bytes, hipStream_t s);
 
 }  // namespace gs_sort
 
@@ -208,32 +258,26 @@ extern "C" size_t gs_sort_scratch_bytes(int64_t n) {
   return (bytes + 255) & ~(size_t)255;
 }
 
-extern "C" int gs_sort_pairs_u64(int64_t n, int32_t key_bits, uint64_t* keys, int32_t* values,
-                                 uint64_t* keys_alt, int32_t* values_alt, void* scratch, size_t scratch_bytes,
-                                 void* stream) {
-  if (n < 0 || key_bits < 0 || key_bits > 64) return GS_ERR_INVALID_ARGUMENT;
+template <typename K, bool kValues>
+static int gs_sort::sort_impl(int64_t n, int32_t lo_bit, int32_t key_bits, K* kin, K* kout, int* vin,
+                              int* vout, void* scratch, size_t scratch_bytes, hipStream_t s) {
+  if (n < 0 || lo_bit < 0 || key_bits < 0 || lo_bit + key_bits > (int)(8 * sizeof(K)))
+    return GS_ERR_INVALID_ARGUMENT;
   if (n > 0x7fffffffLL) return GS_ERR_OVERFLOW;
   if (n == 0 || key_bits == 0) return GS_OK;
-  if (!keys || !values || !keys_alt || !values_alt || !scratch) return GS_ERR_INVALID_ARGUMENT;
+  if (!kin || !kout || !scratch || (kValues && (!vin || !vout))) return GS_ERR_INVALID_ARGUMENT;
   if (scratch_bytes < gs_sort_scratch_bytes(n)) return GS_ERR_SCRATCH_TOO_SMALL;
-  hipStream_t s = (hipStream_t)stream;
-  const int nb = gs_sort::num_blocks(n);
+  const int nb = num_blocks(n);
   unsigned* hist = reinterpret_cast<unsigned*>(scratch);
-  unsigned* digit_totals = hist + (size_t)nb * gs_sort::kRadix;
+  unsigned* digit_totals = hist + (size_t)nb * kRadix;
   const int passes = gs_passes_for_bits(key_bits);
-  gs_sort::u64* kin = reinterpret_cast<gs_sort::u64*>(keys);
-  gs_sort::u64* kout = reinterpret_cast<gs_sort::u64*>(keys_alt);
-  int* vin = values;
-  int* vout = values_alt;
   for (int pass = 0; pass < passes; ++pass) {
-    const int shift = pass * 8;
-    hipLaunchKernelGGL(gs_sort::upsweep_kernel, dim3(nb), dim3(gs_sort::kThreads), 0, s, kin, (long long)n, shift,
-                       nb, hist);
-    hipLaunchKernelGGL(gs_sort::rowscan_kernel, dim3(gs_sort::kRadix), dim3(gs_sort::kThreads), 0, s, nb, hist,
-                       digit_totals);
-    hipLaunchKernelGGL(gs_sort::downsweep_kernel, dim3(nb), dim3(gs_sort::kThreads), 0, s, kin, vin, kout, vout,
+    const int shift = lo_bit + pass * 8;
+    hipLaunchKernelGGL((upsweep_kernel<K>), dim3(nb), dim3(kThreads), 0, s, kin, (long long)n, shift, nb, hist);
+    hipLaunchKernelGGL(rowscan_kernel, dim3(kRadix / kWaves), dim3(kThreads), 0, s, nb, hist, digit_totals);
+    hipLaunchKernelGGL((downsweep_kernel<K, kValues>), dim3(nb), dim3(kThreads), 0, s, kin, vin, kout, vout,
                        (long long)n, shift, nb, hist, digit_totals);
-    gs_sort::u64* tk = kin;
+    K* tk = kin;
     kin = kout;
     kout = tk;
     int* tv = vin;
@@ -241,4 +285,26 @@ extern "C" int gs_sort_pairs_u64(int64_t n, int32_t key_bits, uint64_t* keys, in
     vout = tv;
   }
   return gs_status_from_hip(hipGetLastError());
+}
+
+extern "C" int gs_sort_pairs_u64(int64_t n, int32_t key_bits, uint64_t* keys, int32_t* values,
+                                 uint64_t* keys_alt, int32_t* values_alt, void* scratch, size_t scratch_bytes,
+                                 void* stream) {
+  return gs_sort::sort_impl<gs_sort::u64, true>(n, 0, key_bits, reinterpret_cast<gs_sort::u64*>(keys),
+                                  reinterpret_cast<gs_sort::u64*>(keys_alt), values, values_alt, scratch,
+                                  scratch_bytes, (hipStream_t)stream);
+}
+
+extern "C" int gs_sort_keys_u64(int64_t n, int32_t lo_bit, int32_t key_bits, uint64_t* keys, uint64_t* keys_alt,
+                                void* scratch, size_t scratch_bytes, void* stream) {
+  return gs_sort::sort_impl<gs_sort::u64, false>(n, lo_bit, key_bits, reinterpret_cast<gs_sort::u64*>(keys),
+                                   reinterpret_cast<gs_sort::u64*>(keys_alt), nullptr, nullptr, scratch,
+                                   scratch_bytes, (hipStream_t)stream);
+}
+
+extern "C" int gs_sort_pairs_u32(int64_t n, int32_t lo_bit, int32_t key_bits, uint32_t* keys, int32_t* values,
+                                 uint32_t* keys_alt, int32_t* values_alt, void* scratch, size_t scratch_bytes,
+                                 void* stream) {
+  return gs_sort::sort_impl<unsigned, true>(n, lo_bit, key_bits, keys, keys_alt, values, values_alt, scratch,
+                                            scratch_bytes, (hipStream_t)stream);
 }

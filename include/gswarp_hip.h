@@ -86,42 +86,77 @@ int gs_mark_visible(int32_t P, const float* means3d, const float* viewmatrix, ui
                     void* stream);
 
 /*
- * Inclusive prefix sum of tiles_touched (point order) into offsets, plus the
- * exact int64 total into *total_dev (device pointer).  offsets are only
- * meaningful when the total fits in int32.
+ * Depth-sort input of the depth-then-tile binning: keys_out[i] = float bits
+ * of depths[i] when radii[i] > 0, else 0; values_out[i] = i.  Sorted stably
+ * (gs_sort_pairs_u32 on 32 bits) they give the reference's depth order with
+ * culled Gaussians first.
+ * Replaces: binning_kernels.py:27-40 (_prepare_depth_sort_payload, unpacked
+ * layout) before the depth sort at binning_ops.py:152-222.
+ */
+int gs_depth_keys(int32_t P, const int32_t* radii, const float* depths, uint32_t* keys_out, int32_t* values_out,
+                  void* stream);
+
+/*
+ * Inclusive prefix sum of tiles_touched[order[j]] (order == NULL: point
+ * order) into offsets, plus, in the two int64 at info_dev (device memory):
+ * info[0] = the exact total pair count, info[1] = (max << 32 | min) of the
+ * float bits of depths[i] over the Gaussians with radii[i] > 0 (0 when there
+ * are none).  offsets are only meaningful when the total fits in int32.
  * Replaces: memory.py:539-551 (_inclusive_scan_i32) and
  * binning_ops.py:62-81 (_wide_pair_count_if_needed).
  */
 size_t gs_scan_scratch_bytes(int32_t P);
-int gs_scan_tiles(int32_t P, const int32_t* tiles_touched, int32_t* offsets, int64_t* total_dev,
-                  void* scratch, size_t scratch_bytes, void* stream);
+int gs_scan_tiles(int32_t P, const int32_t* tiles_touched, const int32_t* order, const int32_t* radii,
+                  const float* depths, int32_t* offsets, int64_t* info_dev, void* scratch, size_t scratch_bytes,
+                  void* stream);
 
 /*
- * Copies the int64 at total_dev into caller-provided pinned host memory and
- * waits for the stream: the single device-to-host synchronisation of a
+ * Copies the two int64 at info_dev into caller-provided pinned host memory
+ * and waits for the stream: the single device-to-host synchronisation of a
  * forward pass.
  * Replaces: binning_ops.py:243-252 (the num_rendered .item()).
  */
-int gs_num_rendered_readback(const int64_t* total_dev, int64_t* total_host_pinned, void* stream);
+int gs_num_rendered_readback(const int64_t* info_dev, int64_t* info_host_pinned, void* stream);
 
 /*
- * For every Gaussian with radius > 0, emits one (key, value) pair per covered
- * tile at offsets[i-1] (0 for i == 0): key = tile_id << 32 | float bits of
- * depth, value = i.  Pairs are produced in point-index order; a stable sort
- * by the 64-bit key then yields the reference's (tile, depth, index) order.
+ * For every Gaussian i with radius > 0, emits one key per covered tile at
+ * offsets[i-1] (0 for i == 0):
+ *   key = ((tile_id << depth_bits) | (float_bits(depth_i) - depth_min)) << value_bits | v
+ * with v = i when value_bits > 0 (values_out unused, may be NULL), else
+ * v = 0 and values_out[pair] = i.  depth_min / depth_bits come from the
+ * range gs_scan_tiles reports (depth_bits = bit length of max - min); the
+ * tile, depth and value fields must fit in 64 bits and i in value_bits.
+ * Pairs are produced in point-index order; a stable sort on the tile and
+ * depth fields then yields the reference's (tile, depth, index) order.
  * Replaces: binning_kernels.py:411-451 with binning_kernels.py:127-216 and
  * the depth sort that precedes it (binning_ops.py:152-222).
  */
 int gs_duplicate_keys(int32_t P, const int32_t* radii, const float* records, const float* conic_2d_inv,
                       const int32_t* offsets, int32_t image_width, int32_t image_height,
-                      int32_t coverage_mode, int64_t num_rendered, uint64_t* keys_out, int32_t* values_out,
-                      void* stream);
+                      int32_t coverage_mode, int64_t num_rendered, uint32_t depth_min, int32_t depth_bits,
+                      int32_t value_bits, uint64_t* keys_out, int32_t* values_out, void* stream);
 
 /*
- * Stable LSD radix sort of n (uint64 key, int32 value) pairs on the low
- * key_bits bits of the key, 8 bits per pass, ping-ponging between
- * (keys, values) and (keys_alt, values_alt).  The result ends in the primary
- * buffers when gs_sort_num_passes(key_bits) is even, else in the _alt ones.
+ * Depth-then-tile binning emission: thread j emits the covered tiles of
+ * Gaussian order[j] (radius > 0) at offsets[j-1] (0 for j == 0) as
+ * (tile id, point index) pairs.  With order the depth-sorted point list, a
+ * stable sort of the tile ids then yields the reference's per-tile lists.
+ * Replaces: binning_kernels.py:411-451 (_duplicate_with_keys_from_order)
+ * with binning_kernels.py:127-216.
+ */
+int gs_duplicate_tiles(int32_t P, const int32_t* order, const int32_t* radii, const float* records,
+                       const float* conic_2d_inv, const int32_t* offsets, int32_t image_width,
+                       int32_t image_height, int32_t coverage_mode, int64_t num_rendered, uint32_t* tiles_out,
+                       int32_t* values_out, void* stream);
+
+/*
+ * Stable LSD radix sorts, 8 bits per pass, ping-ponging between the primary
+ * and the _alt buffers: the result ends in the primary buffers when
+ * gs_sort_num_passes(key_bits) is even, else in the _alt ones.
+ * gs_sort_pairs_u64 sorts (uint64 key, int32 value) pairs on the low
+ * key_bits bits; gs_sort_keys_u64 sorts keys alone and gs_sort_pairs_u32
+ * (uint32 key, int32 value) pairs, both on bits [lo_bit, lo_bit + key_bits)
+ * (bits below lo_bit ride along).
  * Replaces: binning_ops.py:337-343 and memory.py:586-600
  * (wp.utils.radix_sort_pairs on tile ids).
  */
@@ -129,13 +164,22 @@ int gs_sort_num_passes(int32_t key_bits);
 size_t gs_sort_scratch_bytes(int64_t n);
 int gs_sort_pairs_u64(int64_t n, int32_t key_bits, uint64_t* keys, int32_t* values, uint64_t* keys_alt,
                       int32_t* values_alt, void* scratch, size_t scratch_bytes, void* stream);
+int gs_sort_keys_u64(int64_t n, int32_t lo_bit, int32_t key_bits, uint64_t* keys, uint64_t* keys_alt,
+                     void* scratch, size_t scratch_bytes, void* stream);
+int gs_sort_pairs_u32(int64_t n, int32_t lo_bit, int32_t key_bits, uint32_t* keys, int32_t* values,
+                      uint32_t* keys_alt, int32_t* values_alt, void* scratch, size_t scratch_bytes, void* stream);
 
 /*
- * ranges[t] = [start, end) of tile t in the sorted keys; empty tiles [0, 0].
+ * ranges[t] = [start, end) of tile t = key >> tile_shift in the sorted keys;
+ * empty tiles [0, 0].  With value_bits > 0 also writes
+ * point_list[i] = key_i & (2^value_bits - 1).
  * Replaces: binning_kernels.py:468-487 (_identify_tile_ranges) and the zero
  * fill at binning_ops.py:233.
  */
-int gs_tile_ranges(int64_t n, const uint64_t* sorted_keys, int32_t num_tiles, int32_t* ranges, void* stream);
+int gs_tile_ranges(int64_t n, const uint64_t* sorted_keys, int32_t tile_shift, int32_t value_bits,
+                   int32_t num_tiles, int32_t* ranges, int32_t* point_list, void* stream);
+/* The same for sorted uint32 tile ids (depth-then-tile binning). */
+int gs_tile_ranges_u32(int64_t n, const uint32_t* sorted_tiles, int32_t num_tiles, int32_t* ranges, void* stream);
 
 /*
  * Per-tile front-to-back alpha blending of 16x16 tiles, each covered by

@@ -13,10 +13,10 @@ COVERAGE_NAMES = {0: "snugbox", 1: "accutile_sweep", 2: "conic_rect"}
 
 
 def options(coverage_mode: int = 1, compute_depth: bool = True, flow: bool = False, top_k: int = 20,
-            compute_flow_aux: bool = True) -> ExecutionOptions:
+            compute_flow_aux: bool = True, sort_mode: str = "warp_depth_stable_tile") -> ExecutionOptions:
     return ExecutionOptions(
         backward_mode="manual",
-        binning_sort_mode="warp_depth_stable_tile",
+        binning_sort_mode=sort_mode,
         tile_coverage_mode=COVERAGE_NAMES[coverage_mode],
         compute_depth=compute_depth,
         auto_tune=False,

@@ -415,21 +415,21 @@ def test_invalid_settings_raise_before_launch(device):
         _std(device, bad, _settings(device, bg))
 
 
-def test_full_size_config2_binning_structure(device):
+@pytest.mark.parametrize("sort_mode", ["warp_depth_stable_tile", "warp_radix"])
+def test_full_size_config2_binning_structure(sort_mode, device):
     """Config 2 at full size (1M Gaussians, 1920x1080): the sorted keys are
     non-decreasing, every key's tile matches its range, the ranges partition
     [0, R), R equals the sum of visible tile counts, and each tile's depths are
     non-decreasing with index order among equal depths."""
     scene = configs.make_scene(2, seed=0, device=device)
-    out = gpu_forward(scene, options())
+    out = gpu_forward(scene, options(sort_mode=sort_mode))
     pre, bins = out["pre"], out["bins"]
     R = bins.num_rendered
     assert R > 1_000_000
     vis = pre.radii > 0
     assert int(pre.tiles_touched[vis].sum().item()) == R
-    keys = bins.sorted_keys
-    assert bool((keys[1:] >= keys[:-1]).all())
-    tiles = (keys >> 32).to(torch.int64)
+    tiles, depth, field_ = bins.decode_keys()
+    assert bool((field_[1:] >= field_[:-1]).all())
     T = bins.ranges.shape[0]
     assert int(tiles.min()) >= 0 and int(tiles.max()) < T
     counts = torch.bincount(tiles, minlength=T)
@@ -438,10 +438,13 @@ def test_full_size_config2_binning_structure(device):
     assert torch.equal(bins.ranges[nonempty, 0].long(), starts[nonempty])
     assert torch.equal(bins.ranges[nonempty, 1].long(), (starts + counts)[nonempty])
     assert int(bins.ranges[~nonempty].abs().sum()) == 0
-    # the key's low word is the depth of the listed Gaussian, and equal-key runs keep index order
-    depth_bits = (keys & 0xFFFFFFFF).to(torch.int64)
+    # the depth field is the depth of the listed Gaussian, and equal-field runs keep index order
     pts = bins.point_list.long()
-    assert torch.equal(depth_bits, pre.depths.view(torch.int32)[pts].to(torch.int64) & 0xFFFFFFFF)
-    same = keys[1:] == keys[:-1]
+    assert torch.equal(depth, pre.depths.view(torch.int32)[pts].to(torch.int64) & 0xFFFFFFFF)
+    same = field_[1:] == field_[:-1]
     assert bool((pts[1:][same] > pts[:-1][same]).all())
+    if sort_mode == "warp_radix":
+        # this workload packs the point index into the key and sorts fewer than 6 passes of bits
+        lay = bins.key_layout
+        assert lay.value_bits == 20 and (T - 1).bit_length() + lay.depth_bits <= 40
     torch.cuda.synchronize()

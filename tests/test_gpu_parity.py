@@ -55,10 +55,13 @@ def _check_forward(scene, opts, *, coverage_mode=1, flow=False, top_k=0, colors=
     assert bins.num_rendered == rb["num_rendered"]
     if bins.num_rendered:
         assert np.array_equal(to_np(bins.point_list), rb["point_list"])
-        keys = to_np(bins.sorted_keys).view(np.uint64)
-        assert np.array_equal((keys >> np.uint64(32)).astype(np.int64), rb["tile_ids"].astype(np.int64))
-        depth_bits = (keys & np.uint64(0xFFFFFFFF)).astype(np.uint32)
-        assert np.array_equal(depth_bits, rp["depths"].view(np.uint32)[rb["point_list"]])
+        tile, depth, _ = bins.decode_keys()
+        assert np.array_equal(to_np(tile), rb["tile_ids"].astype(np.int64))
+        assert np.array_equal(to_np(depth).astype(np.uint32), rp["depths"].view(np.uint32)[rb["point_list"]])
+        lay = bins.key_layout
+        if lay.value_bits:  # the packed low bits are the point list itself
+            low = to_np(bins.sorted_keys) & ((1 << lay.value_bits) - 1)
+            assert np.array_equal(low, rb["point_list"].astype(np.int64))
     assert np.array_equal(to_np(bins.ranges), rb["ranges"])
     # render
     assert np.array_equal(to_np(res.n_contrib).reshape(rf["n_contrib"].shape), rf["n_contrib"])
@@ -77,6 +80,15 @@ def test_forward_stages_match_oracle(case, device):
     scene = _scene(case, device)
     flow = CASES[case]["config"] == 4
     _check_forward(scene, options(flow=flow), flow=flow, top_k=20 if flow else 0)
+
+
+@pytest.mark.parametrize("sort_mode", ["warp_radix", "torch"])
+@pytest.mark.parametrize("case", ["c0_full", "c2_small", "c3_small", "c1_ragged"])
+def test_other_sort_modes_match_oracle(case, sort_mode, device):
+    """The packed 64-bit key sort and the torch.sort dataflow give the same
+    bit-exact lists as the default depth-then-tile HIP sort."""
+    scene = _scene(case, device)
+    _check_forward(scene, options(sort_mode=sort_mode))
 
 
 @pytest.mark.parametrize("coverage_mode", [0, 2])
