@@ -68,8 +68,9 @@ class StageTimer:
         if self.enabled:
             self.notes[key].append(value)
 
-    def mean_ms(self) -> dict:
-        return {name: sum(s.elapsed_time(e) for s, e in pairs) / len(pairs) for name, pairs in self.events.items()}
+    def mean_ms(self, steps: int) -> dict:
+        """Mean time per step of each stage (a stage that runs twice in a step counts twice)."""
+        return {name: sum(s.elapsed_time(e) for s, e in pairs) / steps for name, pairs in self.events.items()}
 
 
 def sort_passes(tiles: int) -> int:
@@ -77,7 +78,7 @@ def sort_passes(tiles: int) -> int:
     return math.ceil((32 + math.ceil(math.log2(tiles))) / 8)
 
 
-def algorithmic_bytes(N: int, R: float, P: int, T: int, sort_mode: str) -> dict:
+def algorithmic_bytes(N: int, R: float, P: int, T: int, dataflow: str) -> dict:
     """Bytes crossing each stage boundary once (the SH3, depth-on accounting of the
     reference dataflow): preprocess 112N + SH 228N, scan 8N, duplicate 44N + 12R
     (64-bit key + value) or 44N + 8R (tile id + value), ranges 8R + 8T, render
@@ -94,7 +95,7 @@ def algorithmic_bytes(N: int, R: float, P: int, T: int, sort_mode: str) -> dict:
         "render_bwd": 44.0 * R + 28.0 * P + 40.0 * N + 8.0 * T,
         "preprocess_bwd": 624.0 * N,
     }
-    if sort_mode == "warp_radix":
+    if dataflow == "warp_radix":
         out["duplicate"] = 44.0 * N + 12.0 * R
         out["sort"] = sort_passes(T) * 24.0 * R
     else:
@@ -372,7 +373,7 @@ def main() -> int:
     ms_per_step = 1000.0 * elapsed / args.steps
     fwd_ms = sum(a.elapsed_time(b) for a, b, _ in step_events) / len(step_events)
     bwd_ms = sum(b.elapsed_time(c) for _, b, c in step_events) / len(step_events)
-    stage_ms = timer.mean_ms() if not args.no_stage_timing else {}
+    stage_ms = timer.mean_ms(args.steps) if not args.no_stage_timing else {}
     passes = timer.notes.get("sort_passes", [])
     Rs = timer.notes.get("num_rendered", [])
     R = sum(Rs) / len(Rs) if Rs else float("nan")
@@ -382,7 +383,8 @@ def main() -> int:
     binning_sort = None
     stages = {}
     if stage_ms and Rs:
-        algo = algorithmic_bytes(N, R, P, T, sort_mode)
+        dataflows = set(timer.notes.get("binning_dataflow", []))
+        algo = algorithmic_bytes(N, R, P, T, "warp_radix" if dataflows == {"packed_key"} else sort_mode)
         for name, ms in sorted(stage_ms.items(), key=lambda kv: -kv[1]):
             gbps = algo[name] / (ms * 1e-3) / 1e9 if name in algo else None
             stages[name] = {"ms": round(ms, 4), "algorithmic_bytes": algo.get(name),
@@ -395,7 +397,9 @@ def main() -> int:
         binning_sort = {"mode": sort_mode, "stages": sort_names, "ms": round(sort_ms, 4),
                         "algorithmic_bytes": sort_bytes,
                         "hbm_frac": round(sort_bytes / (sort_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
-        log(f"[bench]   binning sort ({sort_mode}) {sort_ms:.4f} ms  {binning_sort['hbm_frac'] * 100:.1f}% of HBM peak")
+        binning_sort["dataflow"] = sorted(dataflows)
+        log(f"[bench]   binning sort ({sort_mode}, {'/'.join(sorted(dataflows))}) {sort_ms:.4f} ms  "
+            f"{binning_sort['hbm_frac'] * 100:.1f}% of HBM peak")
         dominant = max((n for n in stage_ms if n in algo), key=lambda n: stage_ms[n])
         achieved = algo[dominant] / (stage_ms[dominant] * 1e-3) / 1e9
         roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
@@ -424,6 +428,7 @@ def main() -> int:
         "config": {"workload": f"config{args.config}: {spec.description}", "gaussians": N, "width": W,
                    "height": H, "sh_degree": spec.sh_degree, "tiles": T, "mean_num_rendered": R,
                    "mean_sort_passes": (sum(passes) / len(passes)) if passes else None,
+                   "binning_dataflow": sorted(set(timer.notes.get("binning_dataflow", []))),
                    "parallelism": "single GPU"},
         "fwd_ms": fwd_ms,
         "bwd_ms": bwd_ms,

@@ -201,23 +201,57 @@ def key_layout(P: int, T: int, depth_min: int, depth_max: int) -> KeyLayout:
     return KeyLayout(depth_min=depth_min, depth_bits=depth_bits, value_bits=value_bits)
 
 
+# Above this many pairs per Gaussian the default mode sorts Gaussians by depth
+# and then pairs by tile (two short sorts) instead of one 64-bit key per pair.
+DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN = 4
+
+
 def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options: ExecutionOptions,
             keep_keys: bool = False) -> BinningState:
     """Per-tile Gaussian lists (binning_ops.py:84-431) in the requested sort mode.
 
-    All three modes give identical point lists and ranges:
-    ``warp_depth_stable_tile`` (default) sorts the Gaussians by depth and then
-    the emitted (tile, point) pairs stably by tile with the HIP radix sort;
-    ``warp_radix`` sorts one packed 64-bit (tile, depth, point) key per pair
-    with the HIP radix sort; ``torch`` is the depth-then-tile dataflow with
-    ``torch.sort`` (stable) in place of the HIP radix sort.
+    Every mode yields the same lists: per tile, the Gaussians in (depth, index)
+    order.  A point-order scan of the tile counts always runs first; it gives
+    the pair count (the forward's one host sync) and the visible depth range.
+    ``warp_radix`` then sorts one packed 64-bit (tile, depth, point) key per
+    pair with the HIP radix sort.  ``torch`` sorts the Gaussians by depth and
+    the (tile, point) pairs by tile with ``torch.sort`` (stable), as the
+    reference's torch mode does.  ``warp_depth_stable_tile`` (the default)
+    runs the reference's depth-then-tile dataflow with the HIP radix sort when
+    there are more than DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN pairs per Gaussian,
+    and the single packed-key sort otherwise, where one sort of the pairs is
+    cheaper than two sorts and the extra gathers.
     """
     mode = options.binning_sort_mode
     if mode not in BINNING_SORT_MODES:
         raise ValueError("sort_mode must be one of 'torch', 'warp_radix', or 'warp_depth_stable_tile'")
-    if mode == "warp_radix":
-        return _binning_packed(pre, image_height, image_width, keep_keys)
-    return _binning_depth_tile(pre, image_height, image_width, keep_keys, use_torch=(mode == "torch"))
+    lib = _lib.load()
+    device = pre.radii.device
+    P = pre.radii.shape[0]
+    grid_x, grid_y = grid_dims(image_width, image_height)
+    T = grid_x * grid_y
+    stream = _stream(device)
+    offsets = torch.empty((P,), dtype=torch.int32, device=device)
+    info = torch.empty((2,), dtype=torch.int64, device=device)
+    scan_scratch = torch.empty((max(int(lib.gs_scan_scratch_bytes(P)), 1),), dtype=torch.uint8, device=device)
+    with _stage("scan"):
+        lib.call("gs_scan_tiles", P, pre.tiles_touched.data_ptr(), None, pre.radii.data_ptr(), pre.depths.data_ptr(),
+                 offsets.data_ptr(), info.data_ptr(), scan_scratch.data_ptr(), scan_scratch.numel(), stream)
+    pinned = _workspace.readback_buffer(device, torch.cuda.current_stream(device))
+    lib.call("gs_num_rendered_readback", info.data_ptr(), pinned.data_ptr(), stream)
+    R = validate_pair_count(int(pinned[0]))
+    depth_range = int(pinned[1]) & 0xFFFFFFFFFFFFFFFF
+    _note("num_rendered", R)
+    if R == 0:
+        return BinningState(grid_x, grid_y, torch.empty((0,), dtype=torch.int32, device=device),
+                            torch.zeros((T, 2), dtype=torch.int32, device=device), 0)
+    layout = key_layout(P, T, depth_range & 0xFFFFFFFF, depth_range >> 32)
+    if mode == "warp_radix" or (mode == "warp_depth_stable_tile" and layout.value_bits > 0
+                                and R <= DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN * P):
+        _note("binning_dataflow", "packed_key")
+        return _binning_packed(pre, image_width, image_height, offsets, R, layout, keep_keys)
+    _note("binning_dataflow", "depth_then_tile")
+    return _binning_depth_tile(pre, image_width, image_height, R, keep_keys, use_torch=(mode == "torch"))
 
 
 def _note(key: str, value) -> None:
@@ -225,31 +259,16 @@ def _note(key: str, value) -> None:
         STAGE_TIMER.note(key, value)
 
 
-def _readback(lib, info: torch.Tensor, device: torch.device, stream: int) -> tuple[int, int]:
-    """(pair count, packed visible depth-bit range) after the scan: the forward's one host sync."""
-    pinned = _workspace.readback_buffer(device, torch.cuda.current_stream(device))
-    lib.call("gs_num_rendered_readback", info.data_ptr(), pinned.data_ptr(), stream)
-    R = validate_pair_count(int(pinned[0]))
-    _note("num_rendered", R)
-    return R, int(pinned[1]) & 0xFFFFFFFFFFFFFFFF
-
-
-def _empty_binning(grid_x: int, grid_y: int, device: torch.device) -> BinningState:
-    return BinningState(grid_x, grid_y, torch.empty((0,), dtype=torch.int32, device=device),
-                        torch.zeros((grid_x * grid_y, 2), dtype=torch.int32, device=device), 0)
-
-
-def _binning_depth_tile(pre: PreprocessOutputs, image_height: int, image_width: int, keep_keys: bool,
+def _binning_depth_tile(pre: PreprocessOutputs, image_width: int, image_height: int, R: int, keep_keys: bool,
                         use_torch: bool) -> BinningState:
+    """Depth sort of the Gaussians, tile counts scanned in depth order, (tile, point)
+    pairs emitted in that order and sorted stably by tile (binning_ops.py:152-343)."""
     lib = _lib.load()
     device = pre.radii.device
     P = pre.radii.shape[0]
     grid_x, grid_y = grid_dims(image_width, image_height)
     T = grid_x * grid_y
     stream = _stream(device)
-    if P == 0:
-        return _empty_binning(grid_x, grid_y, device)
-    # 1. stable depth sort of the Gaussians (culled ones first with key 0)
     dkeys = torch.empty((P,), dtype=torch.int32, device=device)
     order = torch.empty((P,), dtype=torch.int32, device=device)
     with _stage("depth_sort"):
@@ -266,18 +285,13 @@ def _binning_depth_tile(pre: PreprocessOutputs, image_height: int, image_width: 
                      order_alt.data_ptr(), scratch.data_ptr(), scratch.numel(), stream)
             if lib.gs_sort_num_passes(32) % 2:
                 dkeys, order = dkeys_alt, order_alt
-    # 2. tile counts scanned in depth order, pair count to the host
+    # depth-order offsets; the total is the R already read back
     offsets = torch.empty((P,), dtype=torch.int32, device=device)
     info = torch.empty((2,), dtype=torch.int64, device=device)
     scan_scratch = torch.empty((max(int(lib.gs_scan_scratch_bytes(P)), 1),), dtype=torch.uint8, device=device)
     with _stage("scan"):
-        lib.call("gs_scan_tiles", P, pre.tiles_touched.data_ptr(), order.data_ptr(), pre.radii.data_ptr(),
-                 pre.depths.data_ptr(), offsets.data_ptr(), info.data_ptr(), scan_scratch.data_ptr(),
-                 scan_scratch.numel(), stream)
-    R, _ = _readback(lib, info, device, stream)
-    if R == 0:
-        return _empty_binning(grid_x, grid_y, device)
-    # 3. (tile, point) pairs in depth order, then a stable sort by tile
+        lib.call("gs_scan_tiles", P, pre.tiles_touched.data_ptr(), order.data_ptr(), None, None, offsets.data_ptr(),
+                 info.data_ptr(), scan_scratch.data_ptr(), scan_scratch.numel(), stream)
     tiles = torch.empty((R,), dtype=torch.int32, device=device)
     vals = torch.empty((R,), dtype=torch.int32, device=device)
     with _stage("duplicate"):
@@ -302,30 +316,21 @@ def _binning_depth_tile(pre: PreprocessOutputs, image_height: int, image_width: 
     with _stage("ranges"):
         lib.call("gs_tile_ranges_u32", R, tiles.data_ptr(), T, ranges.data_ptr(), stream)
     keys = None
-    layout = KeyLayout(depth_min=0, depth_bits=32, value_bits=0)
     if keep_keys:  # tile << 32 | depth bits, for tests
         keys = (tiles.to(torch.int64) << 32) | (pre.depths.view(torch.int32)[vals.long()].to(torch.int64)
                                                 & 0xFFFFFFFF)
-    return BinningState(grid_x, grid_y, vals, ranges, R, keys, layout)
+    return BinningState(grid_x, grid_y, vals, ranges, R, keys, KeyLayout(depth_min=0, depth_bits=32, value_bits=0))
 
 
-def _binning_packed(pre: PreprocessOutputs, image_height: int, image_width: int, keep_keys: bool) -> BinningState:
+def _binning_packed(pre: PreprocessOutputs, image_width: int, image_height: int, offsets: torch.Tensor, R: int,
+                    layout: KeyLayout, keep_keys: bool) -> BinningState:
+    """One packed 64-bit key per pair, emitted in point order and sorted once."""
     lib = _lib.load()
     device = pre.radii.device
     P = pre.radii.shape[0]
     grid_x, grid_y = grid_dims(image_width, image_height)
     T = grid_x * grid_y
     stream = _stream(device)
-    offsets = torch.empty((P,), dtype=torch.int32, device=device)
-    info = torch.empty((2,), dtype=torch.int64, device=device)
-    scan_scratch = torch.empty((max(int(lib.gs_scan_scratch_bytes(P)), 1),), dtype=torch.uint8, device=device)
-    with _stage("scan"):
-        lib.call("gs_scan_tiles", P, pre.tiles_touched.data_ptr(), None, pre.radii.data_ptr(), pre.depths.data_ptr(),
-                 offsets.data_ptr(), info.data_ptr(), scan_scratch.data_ptr(), scan_scratch.numel(), stream)
-    R, depth_range = _readback(lib, info, device, stream)
-    if R == 0:
-        return _empty_binning(grid_x, grid_y, device)
-    layout = key_layout(P, T, depth_range & 0xFFFFFFFF, depth_range >> 32)
     packed = layout.value_bits > 0
     keys = torch.empty((R,), dtype=torch.int64, device=device)
     keys_alt = torch.empty((R,), dtype=torch.int64, device=device)

@@ -97,8 +97,10 @@ __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(int n, const 
     if (idx < n) {
       const int src = order ? order[idx] : (int)idx;
       cnt[i] = in[src];
-      rad[i] = radii[src];
-      bits[i] = __float_as_uint(depths[src]);
+      if (radii) {
+        rad[i] = radii[src];
+        bits[i] = __float_as_uint(depths[src]);
+      }
     }
   }
 #pragma unroll
@@ -413,7 +415,8 @@ extern "C" int gs_scan_tiles(int32_t P, const int32_t* tiles_touched, const int3
     hipLaunchKernelGGL(gs::zero_info_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<long long*>(info_dev));
     return gs_status_from_hip(hipGetLastError());
   }
-  if (!tiles_touched || !radii || !depths || !offsets || !scratch) return GS_ERR_INVALID_ARGUMENT;
+  if (!tiles_touched || !offsets || !scratch || (radii == nullptr) != (depths == nullptr))
+    return GS_ERR_INVALID_ARGUMENT;
   if (scratch_bytes < gs_scan_scratch_bytes(P)) return GS_ERR_SCRATCH_TOO_SMALL;
   const int nb = gs_scan_blocks(P);
   long long* block_sums = reinterpret_cast<long long*>(scratch);

@@ -101,7 +101,8 @@ int gs_depth_keys(int32_t P, const int32_t* radii, const float* depths, uint32_t
  * order) into offsets, plus, in the two int64 at info_dev (device memory):
  * info[0] = the exact total pair count, info[1] = (max << 32 | min) of the
  * float bits of depths[i] over the Gaussians with radii[i] > 0 (0 when there
- * are none).  offsets are only meaningful when the total fits in int32.
+ * are none, or when radii and depths are both NULL, which skips the range).
+ * offsets are only meaningful when the total fits in int32.
  * Replaces: memory.py:539-551 (_inclusive_scan_i32) and
  * binning_ops.py:62-81 (_wide_pair_count_if_needed).
  */
