@@ -9,8 +9,9 @@
 // sums its pixels' terms, the wave sums the ten components with a transposed
 // lane-swap/DPP reduction (skipped when no pixel of the wave blended it), and
 // one lane per row issues the global float atomics of its row's components.
-// The blend decisions use the forward's exact arithmetic; T uses the
-// hardware reciprocal (gradients only).
+// The blend decisions are exactly the forward's (exp_sw is evaluated only in
+// a thin band above the record's power cutoff where the decision needs it);
+// gradient values use the hardware exponential and reciprocal.
 //
 // preprocess_bwd: one thread per Gaussian fusing the SH colour backward
 // (backward_kernels.py:298-536), the projected-mean / depth backward
@@ -24,6 +25,8 @@
 namespace gs {
 
 constexpr int kGradFloats = 10;  // dx, dy, conic a, b, c, opacity, r, g, b, depth
+constexpr float kSureMargin = 2.0e-3f;  // exponents this far above the cutoff always blend
+constexpr float kLog2e = 1.44269504088896341f;
 #ifndef GS_BWD_PIX
 #define GS_BWD_PIX 2
 #endif
@@ -151,9 +154,11 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
   rg.y = imax(rg.x, imin(rg.y, p.num_rendered));
   const int n = rg.y - rg.x;
 
-  float pfy[kPix], T[kPix], Tf[kPix], gp0[kPix], gp1[kPix], gp2[kPix], gpd[kPix], gpa[kPix], bgd[kPix];
+  // Per pixel: T (reconstructed transmittance), the forward's final T, the
+  // upstream gradients, and the colour / depth / alpha accumulated behind
+  // the current Gaussian (acc*, updated as soon as a Gaussian is blended).
+  float pfy[kPix], T[kPix], tfb[kPix], gp0[kPix], gp1[kPix], gp2[kPix], gpd[kPix], gpa[kPix];
   float acc0[kPix], acc1[kPix], acc2[kPix], accd[kPix], acca[kPix];
-  float la[kPix], lc0[kPix], lc1[kPix], lc2[kPix], ld[kPix];
   int last[kPix];
   int lmax = 0;
 #pragma unroll
@@ -161,20 +166,20 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
     const int py = py0 + 4 * k;
     pfy[k] = (float)py;
     last[k] = 0;
-    T[k] = Tf[k] = gp0[k] = gp1[k] = gp2[k] = gpd[k] = gpa[k] = bgd[k] = 0.0f;
+    T[k] = tfb[k] = gp0[k] = gp1[k] = gp2[k] = gpd[k] = gpa[k] = 0.0f;
     acc0[k] = acc1[k] = acc2[k] = accd[k] = acca[k] = 0.0f;
-    la[k] = lc0[k] = lc1[k] = lc2[k] = ld[k] = 0.0f;
     if (px < p.W && py < p.H && n > 0) {
       const int pix = py * p.W + px;
       last[k] = imax(0, imin(p.n_contrib[pix], n));
-      Tf[k] = 1.0f - p.out_alpha[pix];
-      T[k] = Tf[k];
+      const float Tf = 1.0f - p.out_alpha[pix];
+      T[k] = Tf;
       gp0[k] = p.grad_color[pix];
       gp1[k] = p.grad_color[P + pix];
       gp2[k] = p.grad_color[2 * P + pix];
       if (kDepth) gpd[k] = p.grad_depth[pix];
       gpa[k] = p.grad_alpha[pix];
-      bgd[k] = p.bg[0] * gp0[k] + p.bg[1] * gp1[k] + p.bg[2] * gp2[k];
+      // background term of dL/dalpha: -T_final / (1 - alpha) * (bg . dL/dcolor)
+      tfb[k] = -Tf * (p.bg[0] * gp0[k] + p.bg[1] * gp1[k] + p.bg[2] * gp2[k]);
     }
     lmax = imax(lmax, last[k]);
   }
@@ -215,55 +220,65 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
         any = any || cand[k];
       }
       if (__ballot(any) == 0) continue;
-      const float4 f = s_r2[jj];
-      float G[kPix], alpha[kPix];
+      // Blend decisions, identical to the forward's: above cutoff + 2e-3 the
+      // forward's alpha is provably >= 1/255 (the cutoff sits 1e-3 below
+      // -ln(255 o) and exp_sw / log_sw err by < 1e-6 relative), below the
+      // cutoff provably < 1/255; only the thin band between needs exp_sw.
       bool ok[kPix];
-      bool any_ok = false;
+      bool band_any = false;
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
-        G[k] = exp_sw_nonpos(cand[k] ? pw[k] : 0.0f);
-        alpha[k] = fminr(kAlphaMax, b.y * G[k]);
-        ok[k] = cand[k] && alpha[k] >= kAlphaMin;
-        any_ok = any_ok || ok[k];
+        ok[k] = cand[k] && pw[k] >= b.w + kSureMargin;
+        band_any = band_any || (cand[k] && !ok[k]);
       }
+      if (__ballot(band_any) != 0) {
+#pragma unroll
+        for (int k = 0; k < kPix; ++k) {
+          const bool band = cand[k] && !ok[k];
+          const float a_sw = fminr(kAlphaMax, b.y * exp_sw_nonpos(band ? pw[k] : 0.0f));
+          ok[k] = ok[k] || (band && a_sw >= kAlphaMin);
+        }
+      }
+      bool any_ok = false;
+#pragma unroll
+      for (int k = 0; k < kPix; ++k) any_ok = any_ok || ok[k];
       if (__ballot(any_ok) == 0) continue;
+      const float4 f = s_r2[jj];
       float sv = 0.0f, svy = 0.0f, svyy = 0.0f, sr = 0.0f, sg = 0.0f, sb = 0.0f, sd = 0.0f;
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
-        const float inv = __builtin_amdgcn_rcpf(fmaxr(1.0f - alpha[k], kOneMinusAlphaMin));
+        // Gradient values use the hardware exponential (v_exp_f32): they only
+        // need the 1e-3 gradient tolerance, the decisions above are exact.
+        // A pixel that does not blend this Gaussian gets G = 2^-inf = 0, so
+        // alpha = 0, T * rcp(1) = T and every update below leaves its state
+        // unchanged, with no per-pixel selects.
+        const float G = __builtin_amdgcn_exp2f(ok[k] ? pw[k] * kLog2e : -__builtin_inff());
+        const float alpha = fminr(kAlphaMax, b.y * G);
+        const float inv = __builtin_amdgcn_rcpf(fmaxr(1.0f - alpha, kOneMinusAlphaMin));
         const float Tn = T[k] * inv;
-        const float dch = ok[k] ? alpha[k] * Tn : 0.0f;
-        const float oml = 1.0f - la[k];
-        const float a0 = fmaf(la[k], lc0[k], oml * acc0[k]);
-        const float a1 = fmaf(la[k], lc1[k], oml * acc1[k]);
-        const float a2 = fmaf(la[k], lc2[k], oml * acc2[k]);
-        float dL_dopa = fmaf(f.x - a0, gp0[k], fmaf(f.y - a1, gp1[k], (f.z - a2) * gp2[k]));
+        const float dch = alpha * Tn;
+        float dL_dopa = fmaf(f.x - acc0[k], gp0[k], fmaf(f.y - acc1[k], gp1[k], (f.z - acc2[k]) * gp2[k]));
+        const float oma = 1.0f - alpha;
         if (kDepth) {
-          const float ad = fmaf(la[k], ld[k], oml * accd[k]);
-          dL_dopa = fmaf(b.z - ad, gpd[k], dL_dopa);
-          accd[k] = ok[k] ? ad : accd[k];
-          ld[k] = ok[k] ? b.z : ld[k];
+          dL_dopa = fmaf(b.z - accd[k], gpd[k], dL_dopa);
+          accd[k] = fmaf(alpha, b.z, oma * accd[k]);
           sd = fmaf(dch, gpd[k], sd);
         }
-        const float aa = fmaf(oml, acca[k], la[k]);
-        dL_dopa = fmaf(1.0f - aa, gpa[k], dL_dopa);
-        dL_dopa = fmaf(dL_dopa, Tn, -Tf[k] * inv * bgd[k]);
-        const float v = ok[k] ? G[k] * dL_dopa : 0.0f;
+        dL_dopa = fmaf(1.0f - acca[k], gpa[k], dL_dopa);
+        dL_dopa = fmaf(dL_dopa, Tn, tfb[k] * inv);
+        const float v = G * dL_dopa;
         sv += v;
         svy = fmaf(v, dy[k], svy);
         svyy = fmaf(v * dy[k], dy[k], svyy);
         sr = fmaf(dch, gp0[k], sr);
         sg = fmaf(dch, gp1[k], sg);
         sb = fmaf(dch, gp2[k], sb);
-        T[k] = ok[k] ? Tn : T[k];
-        acc0[k] = ok[k] ? a0 : acc0[k];
-        acc1[k] = ok[k] ? a1 : acc1[k];
-        acc2[k] = ok[k] ? a2 : acc2[k];
-        acca[k] = ok[k] ? aa : acca[k];
-        lc0[k] = ok[k] ? f.x : lc0[k];
-        lc1[k] = ok[k] ? f.y : lc1[k];
-        lc2[k] = ok[k] ? f.z : lc2[k];
-        la[k] = ok[k] ? alpha[k] : la[k];
+        // this Gaussian joins what lies behind the next (nearer) one
+        T[k] = Tn;
+        acc0[k] = fmaf(alpha, f.x, oma * acc0[k]);
+        acc1[k] = fmaf(alpha, f.y, oma * acc1[k]);
+        acc2[k] = fmaf(alpha, f.z, oma * acc2[k]);
+        acca[k] = fmaf(oma, acca[k], alpha);
       }
       const float s = b.y * sv, sy = b.y * svy, syy = b.y * svyy;
       float g[kGradFloats];

@@ -144,12 +144,14 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
         const float test_T = T[k] * (1.0f - alpha);
         const bool fin = ok && test_T < kTransmittanceMin;
         const bool blend = ok && !fin;
-        const float contribution = alpha * T[k];
-        c0[k] = blend ? c0[k] + f.x * contribution : c0[k];
-        c1[k] = blend ? c1[k] + f.y * contribution : c1[k];
-        c2[k] = blend ? c2[k] + f.z * contribution : c2[k];
-        ws[k] = blend ? ws[k] + contribution : ws[k];
-        if (p.compute_depth) da[k] = blend ? da[k] + b.z * contribution : da[k];
+        // A pixel that does not blend adds a contribution of exactly +0 (the
+        // sums are unchanged bit for bit), which replaces per-output selects.
+        const float contribution = blend ? alpha * T[k] : 0.0f;
+        c0[k] = c0[k] + f.x * contribution;
+        c1[k] = c1[k] + f.y * contribution;
+        c2[k] = c2[k] + f.z * contribution;
+        ws[k] = ws[k] + contribution;
+        if (p.compute_depth) da[k] = da[k] + b.z * contribution;
         if (aux && blend && nsucc[k] < p.top_k) {
           const size_t pix = (size_t)(py0 + 4 * k) * p.W + px;
           const size_t ai = (size_t)nsucc[k] * P + pix;
