@@ -133,6 +133,17 @@ def _empty_flow_aux(k: int, H: int, W: int, device) -> tuple[torch.Tensor, ...]:
     )
 
 
+def _covariance_inputs(inputs: RasterInputs, P: int):
+    """(scales, rotations, None) or (None, None, cov3D (P, 6)) as contiguous fp32, the
+    two covariance sources of preprocess_ops.py:289-581."""
+    if inputs.cov3d_precomp.numel() != 0:
+        cov = _f32c(inputs.cov3d_precomp).reshape(-1)
+        if cov.numel() != 6 * P:
+            raise ValueError("cov3D_precomp must hold 6 values per Gaussian")
+        return None, None, cov
+    return _f32c(inputs.scales), _f32c(inputs.rotations, align16=True), None
+
+
 def preprocess(inputs: RasterInputs, options: ExecutionOptions) -> PreprocessOutputs:
     """Fused projection / covariance / coverage / SH colour (preprocess_ops.py:289-581)."""
     if inputs.prefiltered:
@@ -141,8 +152,6 @@ def preprocess(inputs: RasterInputs, options: ExecutionOptions) -> PreprocessOut
     has_sr = inputs.scales.numel() != 0 and inputs.rotations.numel() != 0
     if has_cov == has_sr:
         raise ValueError("Provide exactly one of cov3D_precomp or scales/rotations")
-    if has_cov:
-        raise NotImplementedError("the cov3D_precomp input path is not implemented by the gfx950 backend yet")
     lib = _lib.load()
     means = inputs.means3d
     if means.ndim != 2 or means.shape[1] != 3:
@@ -173,16 +182,16 @@ def preprocess(inputs: RasterInputs, options: ExecutionOptions) -> PreprocessOut
     tanfovx, tanfovy = float(inputs.tan_fovx), float(inputs.tan_fovy)
     # Locals keep every converted input alive until the launch is enqueued.
     means_c = _f32c(means)
-    scales_c = _f32c(inputs.scales)
-    rot_c = _f32c(inputs.rotations, align16=True)
+    scales_c, rot_c, cov_c = _covariance_inputs(inputs, P)
     opac_c = _f32c(inputs.opacities)
     view_c = _f32c(inputs.viewmatrix)
     proj_c = _f32c(inputs.projmatrix)
     campos_c = _f32c(inputs.campos)
     with _stage("preprocess"):
         lib.call(
-            "gs_preprocess_fwd", P, K, int(inputs.degree), means_c.data_ptr(), scales_c.data_ptr(),
-            rot_c.data_ptr(), float(inputs.scale_modifier), opac_c.data_ptr(), _lib.ptr(shs), _lib.ptr(colors),
+            "gs_preprocess_fwd", P, K, int(inputs.degree), means_c.data_ptr(), _lib.ptr(scales_c),
+            _lib.ptr(rot_c), _lib.ptr(cov_c), float(inputs.scale_modifier), opac_c.data_ptr(), _lib.ptr(shs),
+            _lib.ptr(colors),
             view_c.data_ptr(), proj_c.data_ptr(), campos_c.data_ptr(), tanfovx, tanfovy, _focal(W, tanfovx),
             _focal(H, tanfovy), W, H, out.coverage_mode, out.radii.data_ptr(), out.depths.data_ptr(),
             out.proj_2d.data_ptr(), out.conic_2d.data_ptr(), out.conic_2d_inv.data_ptr(),
@@ -486,12 +495,17 @@ def backward(inputs: RasterInputs, radii: torch.Tensor, alpha: torch.Tensor, gra
         f = dict(dtype=torch.float32, device=device)
         grad_means3d = torch.empty((P, 3), **f)
         grad_means2d = torch.empty((P, 3), **f)
-        grad_scales = torch.empty((P, 3), **f)
-        grad_rotations = torch.empty((P, 4), **f)
+        scales_c, rot_c, cov_c = _covariance_inputs(inputs, P)
+        if cov_c is None:
+            grad_scales = torch.empty((P, 3), **f)
+            grad_rotations = torch.empty((P, 4), **f)
+        else:
+            # The precomputed-covariance branch of backward_ops.py:733-737.
+            grad_scales = torch.zeros_like(inputs.scales)
+            grad_rotations = torch.zeros_like(inputs.rotations)
+            grad_cov3d = torch.empty((P, 6), **f)
         tanfovx, tanfovy = float(inputs.tan_fovx), float(inputs.tan_fovy)
         means_c = _f32c(means)
-        scales_c = _f32c(inputs.scales)
-        rot_c = _f32c(inputs.rotations, align16=True)
         campos_c = _f32c(inputs.campos)
         view_c = _f32c(inputs.viewmatrix)
         proj_c = _f32c(inputs.projmatrix)
@@ -501,13 +515,15 @@ def backward(inputs: RasterInputs, radii: torch.Tensor, alpha: torch.Tensor, gra
         gcov = _zeros_if_none(grad_conic_2d_inv, (P, 3), device)
         with _stage("preprocess_bwd"):
             lib.call(
-                "gs_preprocess_bwd", P, K, int(inputs.degree), means_c.data_ptr(), scales_c.data_ptr(),
-                rot_c.data_ptr(), float(inputs.scale_modifier), _lib.ptr(shs), campos_c.data_ptr(),
+                "gs_preprocess_bwd", P, K, int(inputs.degree), means_c.data_ptr(), _lib.ptr(scales_c),
+                _lib.ptr(rot_c), _lib.ptr(cov_c), float(inputs.scale_modifier), _lib.ptr(shs), campos_c.data_ptr(),
                 view_c.data_ptr(), proj_c.data_ptr(), tanfovx, tanfovy, _focal(W, tanfovx), _focal(H, tanfovy),
                 radii_c.data_ptr(), pre.clamped.data_ptr(), grad_gauss.data_ptr(), gp2.data_ptr(), gcon.data_ptr(),
                 gcov.data_ptr(), int(bool(flow_double)), grad_means3d.data_ptr(), grad_means2d.data_ptr(),
-                grad_scales.data_ptr(), grad_rotations.data_ptr(), grad_sh.data_ptr() if has_sh else None, None,
-                None, stream)
+                _lib.ptr(grad_scales) if cov_c is None else None,
+                _lib.ptr(grad_rotations) if cov_c is None else None,
+                _lib.ptr(grad_cov3d) if cov_c is not None else None,
+                grad_sh.data_ptr() if has_sh else None, None, None, stream)
     grad_opacities = grad_gauss[:, 5:6]
     if grad_opacities.shape != inputs.opacities.shape:
         grad_opacities = grad_opacities.reshape(inputs.opacities.shape)
@@ -515,6 +531,8 @@ def backward(inputs: RasterInputs, radii: torch.Tensor, alpha: torch.Tensor, gra
         grad_colors = grad_gauss[:, 6:9].reshape(inputs.colors.shape)
     if has_sh:
         grad_sh = grad_sh.reshape(inputs.sh.shape)
+    if grad_cov3d.numel() != 0:
+        grad_cov3d = grad_cov3d.reshape(inputs.cov3d_precomp.shape)
     return (grad_means2d, grad_colors, grad_opacities, grad_means3d, grad_cov3d, grad_sh,
             grad_scales.reshape(inputs.scales.shape), grad_rotations.reshape(inputs.rotations.shape))
 

@@ -313,6 +313,7 @@ struct PreprocessBwdParams {
   const float* means3d;
   const float* scales;
   const float* rotations;
+  const float* cov3d;  // precomputed (N, 6) 3D covariances, or null
   float scale_modifier;
   const float* shs;
   const float* campos;
@@ -330,6 +331,7 @@ struct PreprocessBwdParams {
   float* grad_means2d;
   float* grad_scales;
   float* grad_rotations;
+  float* grad_cov3d;
   float* grad_sh;
   float* grad_opacity;
   float* grad_colors;
@@ -525,30 +527,42 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(PreprocessBwdParams
     const float t11 = w11 * j11 + w12 * j12;
     const float t21 = w21 * j11 + w22 * j12;
 
-    const float ss0 = p.scales[3 * tid + 0] * p.scale_modifier;
-    const float ss1 = p.scales[3 * tid + 1] * p.scale_modifier;
-    const float ss2 = p.scales[3 * tid + 2] * p.scale_modifier;
-    const float4 q = reinterpret_cast<const float4*>(p.rotations)[tid];
-    const float rr = q.x, xq = q.y, yq = q.z, zq = q.w;
-    const float r00 = 1.0f - 2.0f * (yq * yq + zq * zq);
-    const float r01 = 2.0f * (xq * yq + rr * zq);
-    const float r02 = 2.0f * (xq * zq - rr * yq);
-    const float r10 = 2.0f * (xq * yq - rr * zq);
-    const float r11 = 1.0f - 2.0f * (xq * xq + zq * zq);
-    const float r12 = 2.0f * (yq * zq + rr * xq);
-    const float r20 = 2.0f * (xq * zq + rr * yq);
-    const float r21 = 2.0f * (yq * zq - rr * xq);
-    const float r22 = 1.0f - 2.0f * (xq * xq + yq * yq);
-    const float mm00 = ss0 * r00, mm01 = ss0 * r01, mm02 = ss0 * r02;
-    const float mm10 = ss1 * r10, mm11 = ss1 * r11, mm12 = ss1 * r12;
-    const float mm20 = ss2 * r20, mm21 = ss2 * r21, mm22 = ss2 * r22;
-    // cov3D = M^T M, the forward's expression (preprocess_kernels.py:177-182).
-    const float v00 = mm00 * mm00 + mm10 * mm10 + mm20 * mm20;
-    const float v01 = mm00 * mm01 + mm10 * mm11 + mm20 * mm21;
-    const float v02 = mm00 * mm02 + mm10 * mm12 + mm20 * mm22;
-    const float v11 = mm01 * mm01 + mm11 * mm11 + mm21 * mm21;
-    const float v12 = mm01 * mm02 + mm11 * mm12 + mm21 * mm22;
-    const float v22 = mm02 * mm02 + mm12 * mm12 + mm22 * mm22;
+    const bool precomp = p.cov3d != nullptr;
+    float ss0 = 0.0f, ss1 = 0.0f, ss2 = 0.0f, rr = 0.0f, xq = 0.0f, yq = 0.0f, zq = 0.0f;
+    float r00 = 0.0f, r01 = 0.0f, r02 = 0.0f, r10 = 0.0f, r11 = 0.0f, r12 = 0.0f, r20 = 0.0f, r21 = 0.0f,
+          r22 = 0.0f;
+    float mm00 = 0.0f, mm01 = 0.0f, mm02 = 0.0f, mm10 = 0.0f, mm11 = 0.0f, mm12 = 0.0f, mm20 = 0.0f, mm21 = 0.0f,
+          mm22 = 0.0f;
+    float v00, v01, v02, v11, v12, v22;
+    if (precomp) {
+      const float* cv = p.cov3d + 6 * (size_t)tid;
+      v00 = cv[0]; v01 = cv[1]; v02 = cv[2]; v11 = cv[3]; v12 = cv[4]; v22 = cv[5];
+    } else {
+      ss0 = p.scales[3 * tid + 0] * p.scale_modifier;
+      ss1 = p.scales[3 * tid + 1] * p.scale_modifier;
+      ss2 = p.scales[3 * tid + 2] * p.scale_modifier;
+      const float4 q = reinterpret_cast<const float4*>(p.rotations)[tid];
+      rr = q.x; xq = q.y; yq = q.z; zq = q.w;
+      r00 = 1.0f - 2.0f * (yq * yq + zq * zq);
+      r01 = 2.0f * (xq * yq + rr * zq);
+      r02 = 2.0f * (xq * zq - rr * yq);
+      r10 = 2.0f * (xq * yq - rr * zq);
+      r11 = 1.0f - 2.0f * (xq * xq + zq * zq);
+      r12 = 2.0f * (yq * zq + rr * xq);
+      r20 = 2.0f * (xq * zq + rr * yq);
+      r21 = 2.0f * (yq * zq - rr * xq);
+      r22 = 1.0f - 2.0f * (xq * xq + yq * yq);
+      mm00 = ss0 * r00; mm01 = ss0 * r01; mm02 = ss0 * r02;
+      mm10 = ss1 * r10; mm11 = ss1 * r11; mm12 = ss1 * r12;
+      mm20 = ss2 * r20; mm21 = ss2 * r21; mm22 = ss2 * r22;
+      // cov3D = M^T M, the forward's expression (preprocess_kernels.py:177-182).
+      v00 = mm00 * mm00 + mm10 * mm10 + mm20 * mm20;
+      v01 = mm00 * mm01 + mm10 * mm11 + mm20 * mm21;
+      v02 = mm00 * mm02 + mm10 * mm12 + mm20 * mm22;
+      v11 = mm01 * mm01 + mm11 * mm11 + mm21 * mm21;
+      v12 = mm01 * mm02 + mm11 * mm12 + mm21 * mm22;
+      v22 = mm02 * mm02 + mm12 * mm12 + mm22 * mm22;
+    }
 
     const float vt0x = v00 * t00 + v01 * t10 + v02 * t20;
     const float vt0y = v01 * t00 + v11 * t10 + v12 * t20;
@@ -604,30 +618,39 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(PreprocessBwdParams
     gcm_y = w10 * dL_dtx + w11 * dL_dty + w12 * dL_dtz;
     gcm_z = w20 * dL_dtx + w21 * dL_dty + w22 * dL_dtz;
 
-    const float sg00 = gc0, sg01 = 0.5f * gc1, sg02 = 0.5f * gc2;
-    const float sg11 = gc3, sg12 = 0.5f * gc4, sg22 = gc5;
-    const float dM00 = 2.0f * (mm00 * sg00 + mm01 * sg01 + mm02 * sg02);
-    const float dM01 = 2.0f * (mm00 * sg01 + mm01 * sg11 + mm02 * sg12);
-    const float dM02 = 2.0f * (mm00 * sg02 + mm01 * sg12 + mm02 * sg22);
-    const float dM10 = 2.0f * (mm10 * sg00 + mm11 * sg01 + mm12 * sg02);
-    const float dM11 = 2.0f * (mm10 * sg01 + mm11 * sg11 + mm12 * sg12);
-    const float dM12 = 2.0f * (mm10 * sg02 + mm11 * sg12 + mm12 * sg22);
-    const float dM20 = 2.0f * (mm20 * sg00 + mm21 * sg01 + mm22 * sg02);
-    const float dM21 = 2.0f * (mm20 * sg01 + mm21 * sg11 + mm22 * sg12);
-    const float dM22 = 2.0f * (mm20 * sg02 + mm21 * sg12 + mm22 * sg22);
-    gs0 = p.scale_modifier * (dM00 * r00 + dM01 * r01 + dM02 * r02);
-    gs1 = p.scale_modifier * (dM10 * r10 + dM11 * r11 + dM12 * r12);
-    gs2 = p.scale_modifier * (dM20 * r20 + dM21 * r21 + dM22 * r22);
-    const float dR00 = dM00 * ss0, dR01 = dM01 * ss0, dR02 = dM02 * ss0;
-    const float dR10 = dM10 * ss1, dR11 = dM11 * ss1, dR12 = dM12 * ss1;
-    const float dR20 = dM20 * ss2, dR21 = dM21 * ss2, dR22 = dM22 * ss2;
-    gq0 = 2.0f * zq * (dR01 - dR10) + 2.0f * yq * (dR20 - dR02) + 2.0f * xq * (dR12 - dR21);
-    gq1 = 2.0f * yq * (dR10 + dR01) + 2.0f * zq * (dR20 + dR02) + 2.0f * rr * (dR12 - dR21) -
-          4.0f * xq * (dR22 + dR11);
-    gq2 = 2.0f * xq * (dR10 + dR01) + 2.0f * rr * (dR20 - dR02) + 2.0f * zq * (dR12 + dR21) -
-          4.0f * yq * (dR22 + dR00);
-    gq3 = 2.0f * rr * (dR01 - dR10) + 2.0f * xq * (dR20 + dR02) + 2.0f * yq * (dR12 + dR21) -
-          4.0f * zq * (dR11 + dR00);
+    if (precomp) {
+      // dL/dcov3D is the output (backward_ops.py:734-737); no scale / rotation chain.
+      float* gcv = p.grad_cov3d + 6 * (size_t)tid;
+      gcv[0] = gc0; gcv[1] = gc1; gcv[2] = gc2; gcv[3] = gc3; gcv[4] = gc4; gcv[5] = gc5;
+    } else {
+      const float sg00 = gc0, sg01 = 0.5f * gc1, sg02 = 0.5f * gc2;
+      const float sg11 = gc3, sg12 = 0.5f * gc4, sg22 = gc5;
+      const float dM00 = 2.0f * (mm00 * sg00 + mm01 * sg01 + mm02 * sg02);
+      const float dM01 = 2.0f * (mm00 * sg01 + mm01 * sg11 + mm02 * sg12);
+      const float dM02 = 2.0f * (mm00 * sg02 + mm01 * sg12 + mm02 * sg22);
+      const float dM10 = 2.0f * (mm10 * sg00 + mm11 * sg01 + mm12 * sg02);
+      const float dM11 = 2.0f * (mm10 * sg01 + mm11 * sg11 + mm12 * sg12);
+      const float dM12 = 2.0f * (mm10 * sg02 + mm11 * sg12 + mm12 * sg22);
+      const float dM20 = 2.0f * (mm20 * sg00 + mm21 * sg01 + mm22 * sg02);
+      const float dM21 = 2.0f * (mm20 * sg01 + mm21 * sg11 + mm22 * sg12);
+      const float dM22 = 2.0f * (mm20 * sg02 + mm21 * sg12 + mm22 * sg22);
+      gs0 = p.scale_modifier * (dM00 * r00 + dM01 * r01 + dM02 * r02);
+      gs1 = p.scale_modifier * (dM10 * r10 + dM11 * r11 + dM12 * r12);
+      gs2 = p.scale_modifier * (dM20 * r20 + dM21 * r21 + dM22 * r22);
+      const float dR00 = dM00 * ss0, dR01 = dM01 * ss0, dR02 = dM02 * ss0;
+      const float dR10 = dM10 * ss1, dR11 = dM11 * ss1, dR12 = dM12 * ss1;
+      const float dR20 = dM20 * ss2, dR21 = dM21 * ss2, dR22 = dM22 * ss2;
+      gq0 = 2.0f * zq * (dR01 - dR10) + 2.0f * yq * (dR20 - dR02) + 2.0f * xq * (dR12 - dR21);
+      gq1 = 2.0f * yq * (dR10 + dR01) + 2.0f * zq * (dR20 + dR02) + 2.0f * rr * (dR12 - dR21) -
+            4.0f * xq * (dR22 + dR11);
+      gq2 = 2.0f * xq * (dR10 + dR01) + 2.0f * rr * (dR20 - dR02) + 2.0f * zq * (dR12 + dR21) -
+            4.0f * yq * (dR22 + dR00);
+      gq3 = 2.0f * rr * (dR01 - dR10) + 2.0f * xq * (dR20 + dR02) + 2.0f * yq * (dR12 + dR21) -
+            4.0f * zq * (dR11 + dR00);
+    }
+  } else if (p.grad_cov3d != nullptr) {
+    float* gcv = p.grad_cov3d + 6 * (size_t)tid;
+    for (int k = 0; k < 6; ++k) gcv[k] = 0.0f;
   }
 
   // SH colour backward (its colour gradient is identically zero for culled
@@ -658,10 +681,12 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(PreprocessBwdParams
   p.grad_means2d[3 * tid + 0] = rpx;
   p.grad_means2d[3 * tid + 1] = rpy;
   p.grad_means2d[3 * tid + 2] = 0.0f;
-  p.grad_scales[3 * tid + 0] = gs0;
-  p.grad_scales[3 * tid + 1] = gs1;
-  p.grad_scales[3 * tid + 2] = gs2;
-  reinterpret_cast<float4*>(p.grad_rotations)[tid] = make_float4(gq0, gq1, gq2, gq3);
+  if (p.cov3d == nullptr) {
+    p.grad_scales[3 * tid + 0] = gs0;
+    p.grad_scales[3 * tid + 1] = gs1;
+    p.grad_scales[3 * tid + 2] = gs2;
+    reinterpret_cast<float4*>(p.grad_rotations)[tid] = make_float4(gq0, gq1, gq2, gq3);
+  }
   if (p.grad_opacity != nullptr) p.grad_opacity[tid] = ropa;
   if (p.grad_colors != nullptr) {
     p.grad_colors[3 * tid + 0] = rcol0;
@@ -713,21 +738,27 @@ extern "C" int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t 
 }
 
 extern "C" int gs_preprocess_bwd(int32_t P, int32_t sh_coeffs, int32_t degree, const float* means3d,
-                                 const float* scales, const float* rotations, float scale_modifier,
+                                 const float* scales, const float* rotations, const float* cov3d_precomp,
+                                 float scale_modifier,
                                  const float* shs, const float* campos, const float* viewmatrix,
                                  const float* projmatrix, float tanfovx, float tanfovy, float focal_x,
                                  float focal_y, const int32_t* radii, const uint8_t* clamped,
                                  const float* grad_gauss, const float* grad_proj_2d, const float* grad_conic_2d,
                                  const float* grad_conic_2d_inv, int32_t flow_double, float* grad_means3d,
-                                 float* grad_means2d, float* grad_scales, float* grad_rotations, float* grad_sh,
-                                 float* grad_opacity, float* grad_colors, void* stream) {
+                                 float* grad_means2d, float* grad_scales, float* grad_rotations,
+                                 float* grad_cov3d, float* grad_sh, float* grad_opacity, float* grad_colors,
+                                 void* stream) {
   if (P < 0) return GS_ERR_INVALID_ARGUMENT;
   if (P == 0) return GS_OK;
-  if (!means3d || !scales || !rotations || !viewmatrix || !projmatrix || !radii || !grad_gauss || !grad_proj_2d ||
-      !grad_conic_2d || !grad_conic_2d_inv || !grad_means3d || !grad_means2d || !grad_scales || !grad_rotations)
+  if (!means3d || !viewmatrix || !projmatrix || !radii || !grad_gauss || !grad_proj_2d || !grad_conic_2d ||
+      !grad_conic_2d_inv || !grad_means3d || !grad_means2d)
     return GS_ERR_INVALID_ARGUMENT;
+  if (cov3d_precomp == nullptr && (!scales || !rotations || !grad_scales || !grad_rotations))
+    return GS_ERR_INVALID_ARGUMENT;
+  if (cov3d_precomp != nullptr && !grad_cov3d) return GS_ERR_INVALID_ARGUMENT;
   if (shs != nullptr && (grad_sh == nullptr || campos == nullptr || sh_coeffs <= 0)) return GS_ERR_INVALID_ARGUMENT;
-  if ((reinterpret_cast<uintptr_t>(rotations) & 15) || (reinterpret_cast<uintptr_t>(grad_rotations) & 15))
+  if (cov3d_precomp == nullptr &&
+      ((reinterpret_cast<uintptr_t>(rotations) & 15) || (reinterpret_cast<uintptr_t>(grad_rotations) & 15)))
     return GS_ERR_MISALIGNED;
   gs::PreprocessBwdParams p;
   p.P = P;
@@ -736,6 +767,7 @@ extern "C" int gs_preprocess_bwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
   p.means3d = means3d;
   p.scales = scales;
   p.rotations = rotations;
+  p.cov3d = cov3d_precomp;
   p.scale_modifier = scale_modifier;
   p.shs = shs;
   p.campos = campos;
@@ -756,6 +788,7 @@ extern "C" int gs_preprocess_bwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
   p.grad_means2d = grad_means2d;
   p.grad_scales = grad_scales;
   p.grad_rotations = grad_rotations;
+  p.grad_cov3d = grad_cov3d;
   p.grad_sh = grad_sh;
   p.grad_opacity = grad_opacity;
   p.grad_colors = grad_colors;

@@ -2,6 +2,8 @@
 //   projection + near-plane cull          preprocess_kernels.py:131-146
 //   cov3D = M^T M, M = diag(s) R(q)        preprocess_kernels.py:148-182
 //   EWA cov2D = (M T)^T (M T) + 0.3 I      preprocess_kernels.py:184-219
+//   or, for precomputed cov3D V, cov2D = T^T (V T) + 0.3 I with |det| < 1e-7
+//   culled                                 preprocess_kernels.py:345-477
 //   conic, radius, tile-rect cull          preprocess_kernels.py:221-244
 //   outputs + tile coverage count          preprocess_kernels.py:246-269
 //   SH degree 0..3 colour, +0.5, clamp     preprocess_kernels.py:272-342
@@ -22,6 +24,7 @@ struct PreprocessParams {
   const float* means3d;
   const float* scales;
   const float* rotations;
+  const float* cov3d;  // precomputed (N, 6) 3D covariances, or null
   float scale_modifier;
   const float* opacities;
   const float* shs;
@@ -111,24 +114,6 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p)
     const float p_proj_x = hom_x * inv_w;
     const float p_proj_y = hom_y * inv_w;
 
-    const float s0 = p.scales[3 * idx + 0] * p.scale_modifier;
-    const float s1 = p.scales[3 * idx + 1] * p.scale_modifier;
-    const float s2 = p.scales[3 * idx + 2] * p.scale_modifier;
-    const float4 q = reinterpret_cast<const float4*>(p.rotations)[idx];
-    const float rr = q.x, xq = q.y, yq = q.z, zq = q.w;
-    const float r00 = 1.0f - 2.0f * (yq * yq + zq * zq);
-    const float r01 = 2.0f * (xq * yq + rr * zq);
-    const float r02 = 2.0f * (xq * zq - rr * yq);
-    const float r10 = 2.0f * (xq * yq - rr * zq);
-    const float r11 = 1.0f - 2.0f * (xq * xq + zq * zq);
-    const float r12 = 2.0f * (yq * zq + rr * xq);
-    const float r20 = 2.0f * (xq * zq + rr * yq);
-    const float r21 = 2.0f * (yq * zq - rr * xq);
-    const float r22 = 1.0f - 2.0f * (xq * xq + yq * yq);
-    const float m00 = s0 * r00, m01 = s0 * r01, m02 = s0 * r02;
-    const float m10 = s1 * r10, m11 = s1 * r11, m12 = s1 * r12;
-    const float m20 = s2 * r20, m21 = s2 * r21, m22 = s2 * r22;
-
     float vx = V[0] * mx + V[4] * my + V[8] * mz + V[12];
     float vy = V[1] * mx + V[5] * my + V[9] * mz + V[13];
     const float vz = p_view_z;
@@ -148,17 +133,51 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p)
     const float t01 = V[1] * b_j + V[2] * d_j;
     const float t11 = V[5] * b_j + V[6] * d_j;
     const float t21 = V[9] * b_j + V[10] * d_j;
-    const float a00 = m00 * t00 + m01 * t10 + m02 * t20;
-    const float a10 = m10 * t00 + m11 * t10 + m12 * t20;
-    const float a20 = m20 * t00 + m21 * t10 + m22 * t20;
-    const float a01 = m00 * t01 + m01 * t11 + m02 * t21;
-    const float a11 = m10 * t01 + m11 * t11 + m12 * t21;
-    const float a21 = m20 * t01 + m21 * t11 + m22 * t21;
-    const float ca = a00 * a00 + a10 * a10 + a20 * a20 + 0.3f;
-    const float cb = a00 * a01 + a10 * a11 + a20 * a21;
-    const float cc = a01 * a01 + a11 * a11 + a21 * a21 + 0.3f;
+    float ca, cb, cc;
+    if (p.cov3d == nullptr) {
+      // M = diag(s) R(q) with the reference's (transposed) rotation layout.
+      const float s0 = p.scales[3 * idx + 0] * p.scale_modifier;
+      const float s1 = p.scales[3 * idx + 1] * p.scale_modifier;
+      const float s2 = p.scales[3 * idx + 2] * p.scale_modifier;
+      const float4 q = reinterpret_cast<const float4*>(p.rotations)[idx];
+      const float rr = q.x, xq = q.y, yq = q.z, zq = q.w;
+      const float r00 = 1.0f - 2.0f * (yq * yq + zq * zq);
+      const float r01 = 2.0f * (xq * yq + rr * zq);
+      const float r02 = 2.0f * (xq * zq - rr * yq);
+      const float r10 = 2.0f * (xq * yq - rr * zq);
+      const float r11 = 1.0f - 2.0f * (xq * xq + zq * zq);
+      const float r12 = 2.0f * (yq * zq + rr * xq);
+      const float r20 = 2.0f * (xq * zq + rr * yq);
+      const float r21 = 2.0f * (yq * zq - rr * xq);
+      const float r22 = 1.0f - 2.0f * (xq * xq + yq * yq);
+      const float m00 = s0 * r00, m01 = s0 * r01, m02 = s0 * r02;
+      const float m10 = s1 * r10, m11 = s1 * r11, m12 = s1 * r12;
+      const float m20 = s2 * r20, m21 = s2 * r21, m22 = s2 * r22;
+      const float a00 = m00 * t00 + m01 * t10 + m02 * t20;
+      const float a10 = m10 * t00 + m11 * t10 + m12 * t20;
+      const float a20 = m20 * t00 + m21 * t10 + m22 * t20;
+      const float a01 = m00 * t01 + m01 * t11 + m02 * t21;
+      const float a11 = m10 * t01 + m11 * t11 + m12 * t21;
+      const float a21 = m20 * t01 + m21 * t11 + m22 * t21;
+      ca = a00 * a00 + a10 * a10 + a20 * a20 + 0.3f;
+      cb = a00 * a01 + a10 * a11 + a20 * a21;
+      cc = a01 * a01 + a11 * a11 + a21 * a21 + 0.3f;
+    } else {
+      const float* cv = p.cov3d + 6 * (size_t)idx;
+      const float v00 = cv[0], v01 = cv[1], v02 = cv[2], v11 = cv[3], v12 = cv[4], v22 = cv[5];
+      const float vt0x = v00 * t00 + v01 * t10 + v02 * t20;
+      const float vt0y = v01 * t00 + v11 * t10 + v12 * t20;
+      const float vt0z = v02 * t00 + v12 * t10 + v22 * t20;
+      const float vt1x = v00 * t01 + v01 * t11 + v02 * t21;
+      const float vt1y = v01 * t01 + v11 * t11 + v12 * t21;
+      const float vt1z = v02 * t01 + v12 * t11 + v22 * t21;
+      ca = t00 * vt0x + t10 * vt0y + t20 * vt0z + 0.3f;
+      cb = t00 * vt1x + t10 * vt1y + t20 * vt1z;
+      cc = t01 * vt1x + t11 * vt1y + t21 * vt1z + 0.3f;
+    }
     const float det = ca * cc - cb * cb;
-    visible = fabsf(det) > kDetEps;
+    // the fused kernel culls |det| <= 1e-7, the precomputed-covariance kernel |det| < 1e-7
+    visible = p.cov3d == nullptr ? fabsf(det) > kDetEps : !(fabsf(det) < kDetEps);
     if (visible) {
       const float det_inv = 1.0f / det;
       const float k0 = cc * det_inv, k1 = -cb * det_inv, k2 = ca * det_inv;
@@ -240,7 +259,8 @@ __global__ __launch_bounds__(256) void mark_visible_kernel(int P, const float* _
 }  // namespace gs
 
 extern "C" int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, const float* means3d,
-                                 const float* scales, const float* rotations, float scale_modifier,
+                                 const float* scales, const float* rotations, const float* cov3d_precomp,
+                                 float scale_modifier,
                                  const float* opacities, const float* shs, const float* colors_precomp,
                                  const float* viewmatrix, const float* projmatrix, const float* campos,
                                  float tanfovx, float tanfovy, float focal_x, float focal_y,
@@ -251,12 +271,14 @@ extern "C" int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
   if (P < 0 || image_width <= 0 || image_height <= 0) return GS_ERR_INVALID_ARGUMENT;
   if (coverage_mode < 0 || coverage_mode > 2) return GS_ERR_INVALID_ARGUMENT;
   if (P == 0) return GS_OK;
-  if (!means3d || !scales || !rotations || !opacities || !viewmatrix || !projmatrix || !radii || !depths ||
-      !proj_2d || !conic_2d || !conic_2d_inv || !tiles_touched || !records)
+  if (!means3d || !opacities || !viewmatrix || !projmatrix || !radii || !depths || !proj_2d || !conic_2d ||
+      !conic_2d_inv || !tiles_touched || !records)
     return GS_ERR_INVALID_ARGUMENT;
+  if (cov3d_precomp == nullptr && (!scales || !rotations)) return GS_ERR_INVALID_ARGUMENT;
   if (colors_precomp == nullptr && (shs == nullptr || campos == nullptr || sh_coeffs <= 0))
     return GS_ERR_INVALID_ARGUMENT;
-  if ((reinterpret_cast<uintptr_t>(rotations) & 15) || (reinterpret_cast<uintptr_t>(records) & 15))
+  if ((cov3d_precomp == nullptr && (reinterpret_cast<uintptr_t>(rotations) & 15)) ||
+      (reinterpret_cast<uintptr_t>(records) & 15))
     return GS_ERR_MISALIGNED;
   gs::PreprocessParams p;
   p.P = P;
@@ -265,6 +287,7 @@ extern "C" int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
   p.means3d = means3d;
   p.scales = scales;
   p.rotations = rotations;
+  p.cov3d = cov3d_precomp;
   p.scale_modifier = scale_modifier;
   p.opacities = opacities;
   p.shs = shs;

@@ -59,16 +59,20 @@ const char* gs_status_string(int status);
 /*
  * Fused preprocess: projection, near-plane cull, EWA 2D covariance, conic,
  * radius, tile-rect cull, tile-coverage count and (when colors_precomp is
- * NULL) SH colour of degree `degree` from K = sh_coeffs coefficients.
+ * NULL) SH colour of degree `degree` from K = sh_coeffs coefficients.  The 3D
+ * covariance comes from scales and rotations, or, when cov3d_precomp (N, 6:
+ * xx, xy, xz, yy, yz, zz) is non-NULL, is taken as given (scales / rotations
+ * may then be NULL), with the reference's masked-kernel arithmetic.
  * Culled Gaussians get radius 0 and zero outputs; records are written only
  * for visible Gaussians.  clamped (N bytes, optional) receives the per-channel
  * clamp flags of the SH colour as bits 0..2.
- * Replaces: preprocess_ops.py:289-581 (preprocess_gaussians, scales/rotations
- * path) with preprocess_kernels.py:83-269 and the SH kernel
+ * Replaces: preprocess_ops.py:289-581 (preprocess_gaussians) with
+ * preprocess_kernels.py:83-269 (scales/rotations), preprocess_kernels.py:345-477
+ * and 604-624 (precomputed covariances) and the SH kernel
  * preprocess_kernels.py:272-342.
  */
 int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, const float* means3d,
-                      const float* scales, const float* rotations, float scale_modifier,
+                      const float* scales, const float* rotations, const float* cov3d_precomp, float scale_modifier,
                       const float* opacities, const float* shs, const float* colors_precomp,
                       const float* viewmatrix, const float* projmatrix, const float* campos,
                       float tanfovx, float tanfovy, float focal_x, float focal_y,
@@ -232,20 +236,22 @@ int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t num_points,
  * projected-mean and conic chains, as the reference flow backward does with
  * enable_flow_grad.  grad_sh (N,K,3) is fully written (zeros beyond the
  * evaluated bands); grad_opacity (N) and grad_colors (N,3, when non-NULL)
- * are copied out of grad_gauss.
- * Replaces: backward_ops.py:376-746 (fused path) with
- * backward_kernels.py:53-295, backward_kernels.py:298-536 and
- * flow_kernels.py:14-28.
+ * are copied out of grad_gauss.  With cov3d_precomp non-NULL the cov2D
+ * gradient is returned as grad_cov3d (N, 6) instead of being chained into
+ * grad_scales / grad_rotations (which may then be NULL).
+ * Replaces: backward_ops.py:376-746 with backward_kernels.py:53-295 (fused),
+ * backward_kernels.py:710-870 (precomputed covariances),
+ * backward_kernels.py:298-536 and flow_kernels.py:14-28.
  */
 int gs_preprocess_bwd(int32_t P, int32_t sh_coeffs, int32_t degree, const float* means3d,
-                      const float* scales, const float* rotations, float scale_modifier,
+                      const float* scales, const float* rotations, const float* cov3d_precomp, float scale_modifier,
                       const float* shs, const float* campos, const float* viewmatrix,
                       const float* projmatrix, float tanfovx, float tanfovy, float focal_x, float focal_y,
                       const int32_t* radii, const uint8_t* clamped, const float* grad_gauss,
                       const float* grad_proj_2d, const float* grad_conic_2d, const float* grad_conic_2d_inv,
                       int32_t flow_double, float* grad_means3d, float* grad_means2d, float* grad_scales,
-                      float* grad_rotations, float* grad_sh, float* grad_opacity, float* grad_colors,
-                      void* stream);
+                      float* grad_rotations, float* grad_cov3d, float* grad_sh, float* grad_opacity,
+                      float* grad_colors, void* stream);
 
 #ifdef __cplusplus
 }

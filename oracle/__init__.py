@@ -63,7 +63,7 @@ _SIGNATURES = {
     "or_emit_covered_tiles": (None, [_c_int, _F, _F, _F, _I, _c_int, _c_int, _c_int, _I, _I, _I]),
     "or_preprocess": (
         None,
-        [_c_int, _c_int, _c_int, _F, _F, _F, _c_float, _F, _F, _F, _F, _F, _F, _c_float, _c_float, _c_float,
+        [_c_int, _c_int, _c_int, _F, _F, _F, _F, _c_float, _F, _F, _F, _F, _F, _F, _c_float, _c_float, _c_float,
          _c_float, _c_int, _c_int, _c_int, _I, _F, _F, _F, _F, _I, _F, _F, _I, _I],
     ),
     "or_mark_visible": (None, [_c_int, _F, _F, _I]),
@@ -80,7 +80,7 @@ _SIGNATURES = {
     "or_preprocess_bwd": (
         None,
         [_c_int, _c_int, _c_int, _F, _F, _F, _c_float, _F, _F, _F, _I, _F, _F, _c_float, _c_float, _c_float,
-         _c_float, _I, _F, _F, _F, _F, _c_int, _F, _F, _F, _F, _F],
+         _c_float, _I, _F, _F, _F, _F, _c_int, _c_int, _F, _F, _F, _F, _F, _F],
     ),
     "or_num_threads": (_c_int, []),
     "or_set_num_threads": (None, [_c_int]),
@@ -163,9 +163,15 @@ def emit_covered_tiles(points_xy, cov2d, conic_opacity, radii, grid_x, grid_y, m
 
 
 def preprocess(means3d, scales, rotations, opacities, view, proj, campos, *, tanfovx, tanfovy, width, height,
-               scale_modifier=1.0, shs=None, degree=0, colors=None, coverage_mode=1) -> dict:
-    """Reference preprocess + SH colour (scales/rotations path)."""
-    means3d, scales, rotations = _f32(means3d), _f32(scales), _f32(rotations)
+               scale_modifier=1.0, shs=None, degree=0, colors=None, coverage_mode=1, cov3d_precomp=None) -> dict:
+    """Reference preprocess + SH colour: the fused scales/rotations path, or the
+    masked path for precomputed 3D covariances (cov3d_precomp (N, 6))."""
+    means3d = _f32(means3d)
+    if cov3d_precomp is not None:
+        cov3d_precomp = _f32(cov3d_precomp).reshape(-1, 6)
+        scales = rotations = None
+    else:
+        scales, rotations = _f32(scales), _f32(rotations)
     opacities = _f32(opacities).reshape(-1)
     view, proj, campos = _f32(view).reshape(16), _f32(proj).reshape(16), _f32(campos).reshape(3)
     P = means3d.shape[0]
@@ -190,7 +196,8 @@ def preprocess(means3d, scales, rotations, opacities, view, proj, campos, *, tan
         "visible": np.zeros(P, np.int32),
     }
     lib().or_preprocess(
-        P, K, degree, _fp(means3d), _fp(scales), _fp(rotations), float(scale_modifier), _fp(opacities),
+        P, K, degree, _fp(means3d), _fp(scales), _fp(rotations), _fp(cov3d_precomp), float(scale_modifier),
+        _fp(opacities),
         _fp(shs), _fp(colors), _fp(view), _fp(proj), _fp(campos), float(np.float32(tanfovx)),
         float(np.float32(tanfovy)), float(focal_x), float(focal_y), width, height, coverage_mode,
         _ip(out["radii"]), _fp(out["depths"]), _fp(out["proj_2d"]), _fp(out["conic_2d"]), _fp(out["conic_2d_inv"]),
@@ -266,8 +273,13 @@ def render_bwd(pre: dict, bins: dict, features, background, width, height, fwd: 
 
 def preprocess_bwd(pre: dict, grad_gauss, means3d, scales, rotations, view, proj, campos, *, tanfovx, tanfovy,
                    width, height, scale_modifier=1.0, shs=None, degree=0, grad_proj_2d=None, grad_conic_2d=None,
-                   grad_conic_2d_inv=None, flow_double=False) -> dict:
-    means3d, scales, rotations = _f32(means3d), _f32(scales), _f32(rotations)
+                   grad_conic_2d_inv=None, flow_double=False, cov3d_precomp=None) -> dict:
+    means3d = _f32(means3d)
+    precomp = cov3d_precomp is not None
+    if not precomp:
+        scales, rotations = _f32(scales), _f32(rotations)
+    else:
+        scales = rotations = None
     P = means3d.shape[0]
     K = 0
     if shs is not None:
@@ -284,6 +296,7 @@ def preprocess_bwd(pre: dict, grad_gauss, means3d, scales, rotations, view, proj
         "means2D": zeros(P, 3),
         "scales": zeros(P, 3),
         "rotations": zeros(P, 4),
+        "cov3D": zeros(P, 6),
         "sh": zeros(P, max(K, 1), 3)[:, :K],
     }
     out["sh"] = np.ascontiguousarray(out["sh"])
@@ -292,8 +305,8 @@ def preprocess_bwd(pre: dict, grad_gauss, means3d, scales, rotations, view, proj
         _fp(shs), _fp(_f32(campos).reshape(3)), _ip(_i32(pre["clamped"])), _fp(_f32(view).reshape(16)),
         _fp(_f32(proj).reshape(16)), float(np.float32(tanfovx)), float(np.float32(tanfovy)), float(focal_x),
         float(focal_y), _ip(_i32(pre["radii"])), _fp(_f32(grad_gauss)), _fp(grad_proj_2d), _fp(grad_conic_2d),
-        _fp(grad_conic_2d_inv), int(bool(flow_double)), _fp(out["means3D"]), _fp(out["means2D"]),
-        _fp(out["scales"]), _fp(out["rotations"]), _fp(out["sh"]) if K > 0 else None)
+        _fp(grad_conic_2d_inv), int(bool(flow_double)), int(precomp), _fp(out["means3D"]), _fp(out["means2D"]),
+        _fp(out["scales"]), _fp(out["rotations"]), _fp(out["cov3D"]), _fp(out["sh"]) if K > 0 else None)
     gg = _f32(grad_gauss)
     out["opacities"] = gg[:, 5:6].copy()
     out["colors"] = gg[:, 6:9].copy()
@@ -303,10 +316,11 @@ def preprocess_bwd(pre: dict, grad_gauss, means3d, scales, rotations, view, proj
 def rasterize(scene: dict, *, coverage_mode=1, compute_depth=True, top_k=0) -> dict:
     """Full forward on a scene dict (numpy arrays) as produced by gswarp_amd.configs."""
     s = scene
-    pre = preprocess(s["means3D"], s["scales"], s["rotations"], s["opacities"], s["viewmatrix"], s["projmatrix"],
-                     s["campos"], tanfovx=s["tanfovx"], tanfovy=s["tanfovy"], width=s["width"], height=s["height"],
-                     scale_modifier=s.get("scale_modifier", 1.0), shs=s.get("shs"), degree=s.get("sh_degree", 0),
-                     colors=s.get("colors_precomp"), coverage_mode=coverage_mode)
+    pre = preprocess(s["means3D"], s.get("scales"), s.get("rotations"), s["opacities"], s["viewmatrix"],
+                     s["projmatrix"], s["campos"], tanfovx=s["tanfovx"], tanfovy=s["tanfovy"], width=s["width"],
+                     height=s["height"], scale_modifier=s.get("scale_modifier", 1.0), shs=s.get("shs"),
+                     degree=s.get("sh_degree", 0), colors=s.get("colors_precomp"), coverage_mode=coverage_mode,
+                     cov3d_precomp=s.get("cov3D_precomp"))
     bins = binning(pre, s["width"], s["height"], coverage_mode)
     fwd = render_fwd(pre, bins, pre["rgb"], s["bg"], s["width"], s["height"], compute_depth=compute_depth,
                      top_k=top_k)
@@ -321,10 +335,12 @@ def rasterize_backward(scene: dict, result: dict, grad_color, grad_depth, grad_a
     gg = render_bwd(pre, bins, pre["rgb"], s["bg"], s["width"], s["height"], fwd, grad_color,
                     grad_depth if grad_depth is not None else np.zeros_like(fwd["depth"]), grad_alpha,
                     compute_depth=compute_depth)
-    grads = preprocess_bwd(pre, gg, s["means3D"], s["scales"], s["rotations"], s["viewmatrix"], s["projmatrix"],
+    grads = preprocess_bwd(pre, gg, s["means3D"], s.get("scales"), s.get("rotations"), s["viewmatrix"],
+                           s["projmatrix"],
                            s["campos"], tanfovx=s["tanfovx"], tanfovy=s["tanfovy"], width=s["width"],
                            height=s["height"], scale_modifier=s.get("scale_modifier", 1.0), shs=s.get("shs"),
                            degree=s.get("sh_degree", 0), grad_proj_2d=grad_proj_2d, grad_conic_2d=grad_conic_2d,
-                           grad_conic_2d_inv=grad_conic_2d_inv, flow_double=flow_double)
+                           grad_conic_2d_inv=grad_conic_2d_inv, flow_double=flow_double,
+                           cov3d_precomp=s.get("cov3D_precomp"))
     grads["grad_gauss"] = gg
     return grads

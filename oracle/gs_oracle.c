@@ -379,7 +379,8 @@ static void sh_forward_one(const float* mean, const float* campos, const float* 
  * (preprocess_ops.py:548-549).  focal_x/y are the host's W/(2 tanfovx) rounded to fp32.
  */
 void or_preprocess(int P, int K, int degree, const float* means3d, const float* scales, const float* rotations,
-                   float scale_modifier, const float* opacities, const float* shs, const float* colors,
+                   const float* cov3d_precomp, float scale_modifier, const float* opacities, const float* shs,
+                   const float* colors,
                    const float* V, const float* Pm, const float* campos, float tanfovx, float tanfovy,
                    float focal_x, float focal_y, int W, int H, int coverage_mode, int* radii, float* depths,
                    float* proj_2d, float* conic_2d, float* conic_2d_inv, int* tiles_touched, float* cov3d,
@@ -408,6 +409,57 @@ void or_preprocess(int P, int K, int degree, const float* means3d, const float* 
       const float inv_w = 1.0f / (hom_w + 0.0000001f);
       const float p_proj_x = hom_x * inv_w;
       const float p_proj_y = hom_y * inv_w;
+      if (cov3d_precomp != NULL) {
+        /* masked path for precomputed 3D covariances: preprocess_kernels.py:345-477 (cov2D as t^T (V t),
+         * culled when |det| < 1e-7) after the projection of preprocess_kernels.py:604-624 */
+        const float* cv = cov3d_precomp + 6 * idx;
+        for (int k = 0; k < 6; ++k) cov3d[6 * idx + k] = cv[k];
+        float x = V[0] * p[0] + V[4] * p[1] + V[8] * p[2] + V[12];
+        float y = V[1] * p[0] + V[5] * p[1] + V[9] * p[2] + V[13];
+        const float z = p_view_z;
+        const float limx = 1.3f * tanfovx, limy = 1.3f * tanfovy;
+        const float txtz = x / z, tytz = y / z;
+        x = clamp_(txtz, -limx, limx) * z;
+        y = clamp_(tytz, -limy, limy) * z;
+        const float a = focal_x / z, b = focal_y / z;
+        const float c = -(focal_x * x) / (z * z), d = -(focal_y * y) / (z * z);
+        const float t00 = V[0] * a + V[2] * c, t10 = V[4] * a + V[6] * c, t20 = V[8] * a + V[10] * c;
+        const float t01 = V[1] * b + V[2] * d, t11 = V[5] * b + V[6] * d, t21 = V[9] * b + V[10] * d;
+        const float v00 = cv[0], v01 = cv[1], v02 = cv[2], v11 = cv[3], v12 = cv[4], v22 = cv[5];
+        const float vt0x = v00 * t00 + v01 * t10 + v02 * t20;
+        const float vt0y = v01 * t00 + v11 * t10 + v12 * t20;
+        const float vt0z = v02 * t00 + v12 * t10 + v22 * t20;
+        const float vt1x = v00 * t01 + v01 * t11 + v02 * t21;
+        const float vt1y = v01 * t01 + v11 * t11 + v12 * t21;
+        const float vt1z = v02 * t01 + v12 * t11 + v22 * t21;
+        const float cov_a = t00 * vt0x + t10 * vt0y + t20 * vt0z + 0.3f;
+        const float cov_b = t00 * vt1x + t10 * vt1y + t20 * vt1z;
+        const float cov_c = t01 * vt1x + t11 * vt1y + t21 * vt1z + 0.3f;
+        const float det = cov_a * cov_c - cov_b * cov_b;
+        if (fabsf(det) < DET_EPSILON) goto sh;
+        const float det_inv = 1.0f / det;
+        const float con0 = cov_c * det_inv, con1 = -cov_b * det_inv, con2 = cov_a * det_inv;
+        const float mid = 0.5f * (cov_a + cov_c);
+        const float root = sqrtf(fmax_(0.1f, mid * mid - det));
+        const int radius = f2i(ceilf(3.0f * sqrtf(fmax_(mid + root, mid - root))));
+        const float point_x = ndc_to_pix(p_proj_x, W);
+        const float point_y = ndc_to_pix(p_proj_y, H);
+        const rect4 cr = compute_tile_rect(point_x, point_y, radius, radius, grid_x, grid_y);
+        if ((cr.x1 - cr.x0) * (cr.y1 - cr.y0) == 0) goto sh;
+        depths[idx] = p_view_z;
+        radii[idx] = radius;
+        proj_2d[2 * idx] = point_x;
+        proj_2d[2 * idx + 1] = point_y;
+        conic_2d[3 * idx] = con0;
+        conic_2d[3 * idx + 1] = con1;
+        conic_2d[3 * idx + 2] = con2;
+        conic_2d_inv[3 * idx] = cov_a;
+        conic_2d_inv[3 * idx + 1] = cov_b;
+        conic_2d_inv[3 * idx + 2] = cov_c;
+        tiles_touched[idx] = visit_covered_tiles(point_x, point_y, cov_a, cov_c, con0, con1, con2, opacities[idx],
+                                                 radius, grid_x, grid_y, coverage_mode, NULL, NULL);
+        goto sh;
+      }
       const float s0 = scales[3 * idx] * scale_modifier;
       const float s1 = scales[3 * idx + 1] * scale_modifier;
       const float s2 = scales[3 * idx + 2] * scale_modifier;
@@ -781,8 +833,8 @@ void or_preprocess_bwd(int P, int K, int degree, const float* means3d, const flo
                        const int* clamped, const float* V, const float* Pm, float tanfovx, float tanfovy,
                        float focal_x, float focal_y, const int* radii, const float* grad_gauss,
                        const float* grad_proj_2d, const float* grad_conic_2d, const float* grad_conic_2d_inv,
-                       int flow_double, float* grad_means3d, float* grad_means2d, float* grad_scales,
-                       float* grad_rotations, float* grad_sh) {
+                       int flow_double, int cov3d_is_precomp, float* grad_means3d, float* grad_means2d,
+                       float* grad_scales, float* grad_rotations, float* grad_cov3d, float* grad_sh) {
 #pragma omp parallel for schedule(static)
   for (int tid = 0; tid < P; ++tid) {
     const float* mean = means3d + 3 * tid;
@@ -864,6 +916,116 @@ void or_preprocess_bwd(int P, int K, int degree, const float* means3d, const flo
       gsm0 = ((sum2 - d0 * d0) * dd0 - d1 * d0 * dd1 - d2 * d0 * dd2) * invsum32;
       gsm1 = (-d0 * d1 * dd0 + (sum2 - d1 * d1) * dd1 - d2 * d1 * dd2) * invsum32;
       gsm2 = (-d0 * d2 * dd0 - d1 * d2 * dd1 + (sum2 - d2 * d2) * dd2) * invsum32;
+    }
+    if (cov3d_is_precomp) {
+      /* non-fused chain for precomputed covariances (backward_ops.py:679-744):
+       * projected means (backward_kernels.py:838-870), cov2D -> cov3D (backward_kernels.py:710-836) */
+      const float hx = Pm[0] * mean[0] + Pm[4] * mean[1] + Pm[8] * mean[2] + Pm[12];
+      const float hy = Pm[1] * mean[0] + Pm[5] * mean[1] + Pm[9] * mean[2] + Pm[13];
+      const float hw = Pm[3] * mean[0] + Pm[7] * mean[1] + Pm[11] * mean[2] + Pm[15];
+      const float iw = 1.0f / (hw + 0.0000001f);
+      const float mul1 = hx * iw * iw, mul2 = hy * iw * iw;
+      float gxy0 = gg[0], gxy1 = gg[1];
+      if (rad > 0) {
+        float ax = grad_proj_2d[2 * tid], ay = grad_proj_2d[2 * tid + 1];
+        if (flow_double) {
+          ax = ax + gg[0];
+          ay = ay + gg[1];
+        }
+        gxy0 = gxy0 + ax;
+        gxy1 = gxy1 + ay;
+      }
+      float ox = (Pm[0] * iw - Pm[3] * mul1) * gxy0 + (Pm[1] * iw - Pm[3] * mul2) * gxy1;
+      float oy = (Pm[4] * iw - Pm[7] * mul1) * gxy0 + (Pm[5] * iw - Pm[7] * mul2) * gxy1;
+      float oz = (Pm[8] * iw - Pm[11] * mul1) * gxy0 + (Pm[9] * iw - Pm[11] * mul2) * gxy1;
+      const float mul3 = V[2] * mean[0] + V[6] * mean[1] + V[10] * mean[2] + V[14];
+      ox = ox + (V[2] - V[3] * mul3) * gg[9];
+      oy = oy + (V[6] - V[7] * mul3) * gg[9];
+      oz = oz + (V[10] - V[11] * mul3) * gg[9];
+      float cm0 = 0.0f, cm1 = 0.0f, cm2 = 0.0f;
+      float* gcv = grad_cov3d + 6 * tid;
+      for (int k = 0; k < 6; ++k) gcv[k] = 0.0f;
+      if (rad > 0) {
+        float x = V[0] * mean[0] + V[4] * mean[1] + V[8] * mean[2] + V[12];
+        float y = V[1] * mean[0] + V[5] * mean[1] + V[9] * mean[2] + V[13];
+        const float z = V[2] * mean[0] + V[6] * mean[1] + V[10] * mean[2] + V[14];
+        const float limx = 1.3f * tanfovx, limy = 1.3f * tanfovy;
+        const float txtz = x / z, tytz = y / z;
+        const float tx = clamp_(txtz, -limx, limx) * z, ty = clamp_(tytz, -limy, limy) * z;
+        const float xm = (txtz < -limx || txtz > limx) ? 0.0f : 1.0f;
+        const float ym = (tytz < -limy || tytz > limy) ? 0.0f : 1.0f;
+        const float j00 = focal_x / z, j02 = -(focal_x * tx) / (z * z);
+        const float j11 = focal_y / z, j12 = -(focal_y * ty) / (z * z);
+        const float w00 = V[0], w01 = V[1], w02 = V[2], w10 = V[4], w11 = V[5], w12 = V[6], w20 = V[8],
+                    w21 = V[9], w22 = V[10];
+        const float t00 = w00 * j00 + w02 * j02, t10 = w10 * j00 + w12 * j02, t20 = w20 * j00 + w22 * j02;
+        const float t01 = w01 * j11 + w02 * j12, t11 = w11 * j11 + w12 * j12, t21 = w21 * j11 + w22 * j12;
+        const float* cv = cov3d + 6 * tid;
+        const float v00 = cv[0], v01 = cv[1], v02 = cv[2], v11 = cv[3], v12 = cv[4], v22 = cv[5];
+        const float vt0x = v00 * t00 + v01 * t10 + v02 * t20;
+        const float vt0y = v01 * t00 + v11 * t10 + v12 * t20;
+        const float vt0z = v02 * t00 + v12 * t10 + v22 * t20;
+        const float vt1x = v00 * t01 + v01 * t11 + v02 * t21;
+        const float vt1y = v01 * t01 + v11 * t11 + v12 * t21;
+        const float vt1z = v02 * t01 + v12 * t11 + v22 * t21;
+        const float a = t00 * vt0x + t10 * vt0y + t20 * vt0z + 0.3f + 0.0f;
+        const float b = t00 * vt1x + t10 * vt1y + t20 * vt1z;
+        const float c = t01 * vt1x + t11 * vt1y + t21 * vt1z + 0.3f + 0.0f;
+        const float denom = a * c - b * b;
+        const float denom2inv = 1.0f / (denom * denom + 1.0e-7f);
+        float u0 = grad_conic_2d[3 * tid], u1 = grad_conic_2d[3 * tid + 1], u2 = grad_conic_2d[3 * tid + 2];
+        if (flow_double) {
+          u0 = u0 + gg[2];
+          u1 = u1 + gg[3];
+          u2 = u2 + gg[4];
+        }
+        const float tc0 = gg[2] + u0, tc1 = gg[3] + u1, tc2 = gg[4] + u2;
+        float dL_da = denom2inv * (-c * c * tc0 + 2.0f * b * c * tc1 + (denom - a * c) * tc2);
+        float dL_dc = denom2inv * (-a * a * tc2 + 2.0f * a * b * tc1 + (denom - a * c) * tc0);
+        float dL_db = denom2inv * 2.0f * (b * c * tc0 - (denom + 2.0f * b * b) * tc1 + a * b * tc2);
+        dL_da = dL_da + grad_conic_2d_inv[3 * tid];
+        dL_db = dL_db + grad_conic_2d_inv[3 * tid + 1];
+        dL_dc = dL_dc + grad_conic_2d_inv[3 * tid + 2];
+        gcv[0] = t00 * t00 * dL_da + t00 * t01 * dL_db + t01 * t01 * dL_dc;
+        gcv[3] = t10 * t10 * dL_da + t10 * t11 * dL_db + t11 * t11 * dL_dc;
+        gcv[5] = t20 * t20 * dL_da + t20 * t21 * dL_db + t21 * t21 * dL_dc;
+        gcv[1] = 2.0f * t00 * t10 * dL_da + (t00 * t11 + t01 * t10) * dL_db + 2.0f * t01 * t11 * dL_dc;
+        gcv[2] = 2.0f * t00 * t20 * dL_da + (t00 * t21 + t01 * t20) * dL_db + 2.0f * t01 * t21 * dL_dc;
+        gcv[4] = 2.0f * t10 * t20 * dL_da + (t10 * t21 + t11 * t20) * dL_db + 2.0f * t11 * t21 * dL_dc;
+        const float dT00 = 2.0f * (t00 * v00 + t10 * v01 + t20 * v02) * dL_da + (t01 * v00 + t11 * v01 + t21 * v02) * dL_db;
+        const float dT01 = 2.0f * (t00 * v01 + t10 * v11 + t20 * v12) * dL_da + (t01 * v01 + t11 * v11 + t21 * v12) * dL_db;
+        const float dT02 = 2.0f * (t00 * v02 + t10 * v12 + t20 * v22) * dL_da + (t01 * v02 + t11 * v12 + t21 * v22) * dL_db;
+        const float dT10 = 2.0f * (t01 * v00 + t11 * v01 + t21 * v02) * dL_dc + (t00 * v00 + t10 * v01 + t20 * v02) * dL_db;
+        const float dT11 = 2.0f * (t01 * v01 + t11 * v11 + t21 * v12) * dL_dc + (t00 * v01 + t10 * v11 + t20 * v12) * dL_db;
+        const float dT12 = 2.0f * (t01 * v02 + t11 * v12 + t21 * v22) * dL_dc + (t00 * v02 + t10 * v12 + t20 * v22) * dL_db;
+        const float dJ00 = w00 * dT00 + w10 * dT01 + w20 * dT02;
+        const float dJ02 = w02 * dT00 + w12 * dT01 + w22 * dT02;
+        const float dJ11 = w01 * dT10 + w11 * dT11 + w21 * dT12;
+        const float dJ12 = w02 * dT10 + w12 * dT11 + w22 * dT12;
+        const float tz_inv = 1.0f / z;
+        const float tz2 = tz_inv * tz_inv, tz3 = tz2 * tz_inv;
+        const float dtx = xm * -focal_x * tz2 * dJ02;
+        const float dty = ym * -focal_y * tz2 * dJ12;
+        const float dtz = -focal_x * tz2 * dJ00 - focal_y * tz2 * dJ11 + (2.0f * focal_x * tx) * tz3 * dJ02 +
+                          (2.0f * focal_y * ty) * tz3 * dJ12;
+        cm0 = V[0] * dtx + V[1] * dty + V[2] * dtz;
+        cm1 = V[4] * dtx + V[5] * dty + V[6] * dtz;
+        cm2 = V[8] * dtx + V[9] * dty + V[10] * dtz;
+      }
+      /* accumulation (backward_kernels.py:289-295 order: projected + cov + sh) */
+      float a0 = ox + cm0, a1 = oy + cm1, a2 = oz + cm2;
+      if (has_sh) {
+        a0 = a0 + gsm0;
+        a1 = a1 + gsm1;
+        a2 = a2 + gsm2;
+      }
+      grad_means3d[3 * tid] = a0;
+      grad_means3d[3 * tid + 1] = a1;
+      grad_means3d[3 * tid + 2] = a2;
+      grad_means2d[3 * tid] = gg[0];
+      grad_means2d[3 * tid + 1] = gg[1];
+      grad_means2d[3 * tid + 2] = 0.0f;
+      continue;
     }
     /* Part A */
     const float hom_x = Pm[0] * mean[0] + Pm[4] * mean[1] + Pm[8] * mean[2] + Pm[12];

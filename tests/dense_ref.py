@@ -44,6 +44,14 @@ def quat_to_rot(q: torch.Tensor) -> torch.Tensor:
     ], -2)
 
 
+def covariance_upper(scales: np.ndarray, rotations: np.ndarray, scale_modifier: float = 1.0) -> np.ndarray:
+    """(N, 6) upper triangle (xx, xy, xz, yy, yz, zz) of R diag(s^2) R^T in float64."""
+    R = quat_to_rot(torch.tensor(np.asarray(rotations), dtype=torch.float64))
+    S2 = torch.diag_embed((torch.tensor(np.asarray(scales), dtype=torch.float64) * scale_modifier) ** 2)
+    sig = (R @ S2 @ R.transpose(1, 2)).numpy()
+    return np.stack([sig[:, 0, 0], sig[:, 0, 1], sig[:, 0, 2], sig[:, 1, 1], sig[:, 1, 2], sig[:, 2, 2]], 1)
+
+
 def sh_basis(d: torch.Tensor, degree: int) -> torch.Tensor:
     """(N, (degree+1)^2) real SH basis values in the 3DGS sign convention."""
     x, y, z = d.unbind(-1)
@@ -69,8 +77,9 @@ def tile_rect(px: float, py: float, r: int, gx: int, gy: int):
 
 
 def preprocess(means, scales, rots, view, proj, campos, tanfovx, tanfovy, W, H, shs=None, degree=0,
-               colors=None, scale_modifier=1.0) -> dict:
-    """float64 preprocess + colour; tensors keep their autograd history."""
+               colors=None, scale_modifier=1.0, cov3d=None) -> dict:
+    """float64 preprocess + colour; tensors keep their autograd history.  With
+    cov3d (N, 6: xx, xy, xz, yy, yz, zz) the 3D covariance is taken as given."""
     V = view.reshape(16)
     P = proj.reshape(16)
     x, y, z = means.unbind(1)
@@ -82,9 +91,15 @@ def preprocess(means, scales, rots, view, proj, campos, tanfovx, tanfovy, W, H, 
     ndc = torch.stack([hom_x * inv_w, hom_y * inv_w], 1)
 
     Wrot = torch.stack([torch.stack([V[c * 4 + r] for c in range(3)]) for r in range(3)])
-    Rm = quat_to_rot(rots)
-    S2 = torch.diag_embed((scales * scale_modifier) ** 2)
-    sigma = Rm @ S2 @ Rm.transpose(1, 2)
+    if cov3d is not None:
+        c = cov3d
+        sigma = torch.stack([torch.stack([c[:, 0], c[:, 1], c[:, 2]], -1),
+                             torch.stack([c[:, 1], c[:, 3], c[:, 4]], -1),
+                             torch.stack([c[:, 2], c[:, 4], c[:, 5]], -1)], -2)
+    else:
+        Rm = quat_to_rot(rots)
+        S2 = torch.diag_embed((scales * scale_modifier) ** 2)
+        sigma = Rm @ S2 @ Rm.transpose(1, 2)
     pv = means @ Wrot.T + torch.stack([V[12], V[13], V[14]])
     fx = W / (2.0 * tanfovx)
     fy = H / (2.0 * tanfovy)

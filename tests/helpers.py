@@ -5,6 +5,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 
+import dense_ref
 import oracle
 from gswarp_amd import _pipeline, configs
 from gswarp_amd._runtime import ExecutionOptions
@@ -35,11 +36,27 @@ def raster_inputs(scene: dict, *, colors: bool = False) -> _pipeline.RasterInput
             g = torch.Generator().manual_seed(11)
             rgb = torch.rand(scene["means3D"].shape[0], 3, generator=g).to(dev)
             scene["colors_precomp"] = rgb
+    cov = scene.get("cov3D_precomp")
     return _pipeline.RasterInputs(
         scene["bg"], scene["means3D"], scene["colors_precomp"] if colors else empty, scene["opacities"],
-        scene["scales"], scene["rotations"], float(scene.get("scale_modifier", 1.0)), empty, scene["viewmatrix"],
+        scene["scales"] if cov is None else empty, scene["rotations"] if cov is None else empty,
+        float(scene.get("scale_modifier", 1.0)), empty if cov is None else cov, scene["viewmatrix"],
         scene["projmatrix"], scene["tanfovx"], scene["tanfovy"], scene["height"], scene["width"],
         empty if colors else scene["shs"], scene["sh_degree"], scene["campos"], False)
+
+
+def with_precomputed_covariance(scene: dict, seed: int = 5) -> dict:
+    """The scene with cov3D_precomp = R diag(s^2) R^T (float64, rounded to
+    float32) whose off-diagonals are shrunk toward zero by a random factor per
+    Gaussian, a convex mix of two PSD matrices, so covariances are not all of
+    the scale/rotation form.  scales / rotations are dropped."""
+    host = {k: scene[k].detach().cpu().numpy() for k in ("scales", "rotations")}
+    cov = dense_ref.covariance_upper(host["scales"], host["rotations"], float(scene.get("scale_modifier", 1.0)))
+    t = np.random.default_rng(seed).uniform(0.0, 0.6, size=(cov.shape[0], 1))
+    cov[:, [1, 2, 4]] *= 1.0 - t
+    out = {k: v for k, v in scene.items() if k not in ("scales", "rotations")}
+    out["cov3D_precomp"] = torch.from_numpy(cov.astype(np.float32)).to(scene["means3D"].device)
+    return out
 
 
 def gpu_forward(scene: dict, opts: ExecutionOptions, *, flow: bool = False, colors: bool = False) -> dict:

@@ -38,9 +38,9 @@ def _settings(device, bg, *, flow=False, size=16, **extra):
     return Settings(**common)
 
 
-def _inputs(device, means, *, scales=None, sh=None):
+def _inputs(device, means, *, scales=None, sh=None, covariances=None):
     n = means.shape[0]
-    if scales is None:
+    if scales is None and covariances is None:
         scales = torch.full((n, 3), 0.5, device=device)
     return dict(
         means3D=means,
@@ -48,9 +48,10 @@ def _inputs(device, means, *, scales=None, sh=None):
         sh=_empty(device) if sh is None else sh,
         colors_precomp=torch.full((n, 3), 0.2, device=device) if sh is None else _empty(device),
         opacities=torch.full((n, 1), 0.8, device=device),
-        scales=scales,
-        rotations=torch.tensor([[1.0, 0.0, 0.0, 0.0]], device=device).expand(n, -1).clone(),
-        cov3Ds_precomp=_empty(device),
+        scales=_empty(device) if covariances is not None else scales,
+        rotations=_empty(device) if covariances is not None else
+        torch.tensor([[1.0, 0.0, 0.0, 0.0]], device=device).expand(n, -1).clone(),
+        cov3Ds_precomp=_empty(device) if covariances is None else covariances,
     )
 
 
@@ -209,6 +210,99 @@ def test_conic_inverse_gradient_matches_finite_difference(device):
     numeric = (loss_for(0.5 + eps, False)[0].item() - loss_for(0.5 - eps, False)[0].item()) / (2 * eps)
     assert analytic != 0.0
     assert abs(analytic - numeric) <= max(1e-2, abs(numeric) * 5e-2)
+
+
+def _iso_cov(device, var=0.25, grad=False):
+    return torch.tensor([[var, 0.0, 0.0, var, 0.0, var]], device=device, requires_grad=grad)
+
+
+def test_precomputed_covariance_preprocess_avoids_host_scalar_readback(device):
+    """test_rasterizer_cuda_contracts.py:368-395: a culled cov3D_precomp point
+    preprocesses with no Tensor.item() and leaves zero radii and conics."""
+    from unittest.mock import patch
+
+    from gswarp_amd import _pipeline
+    from helpers import raster_inputs
+    scene = dict(means3D=torch.tensor([[0.0, 0.0, -2.0]], device=device), cov3D_precomp=_iso_cov(device),
+                 opacities=torch.full((1, 1), 0.8, device=device), bg=torch.zeros(3, device=device),
+                 viewmatrix=torch.eye(4, device=device), projmatrix=torch.eye(4, device=device),
+                 tanfovx=1.0, tanfovy=1.0, height=16, width=16, campos=torch.zeros(3, device=device),
+                 sh_degree=0, colors_precomp=torch.full((1, 3), 0.2, device=device))
+    inputs = raster_inputs(scene, colors=True)
+    with patch.object(torch.Tensor, "item", side_effect=AssertionError):
+        pre = _pipeline.preprocess(inputs, options())
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(pre.radii) == 0
+    assert torch.count_nonzero(pre.conic_2d) == 0 and torch.count_nonzero(pre.tiles_touched) == 0
+
+
+def test_all_culled_precomputed_covariance_has_zero_gradients(device):
+    """test_rasterizer_cuda_contracts.py:397-433."""
+    bg = torch.tensor([0.2, 0.6, 0.3], device=device)
+    means = torch.tensor([[0.0, 0.0, -2.0]], device=device, requires_grad=True)
+    cov = _iso_cov(device, grad=True)
+    inputs = _inputs(device, means, covariances=cov)
+    inputs["colors_precomp"] = torch.full((1, 3), 0.2, device=device, requires_grad=True)
+    inputs["opacities"] = torch.full((1, 1), 0.8, device=device, requires_grad=True)
+    color, radii, meta = _std(device, inputs, _settings(device, bg))
+    color.sum().backward()
+    torch.testing.assert_close(color, bg[:, None, None].expand(3, 16, 16))
+    assert torch.count_nonzero(radii) == 0
+    assert torch.count_nonzero(meta.proj_2D) == 0 and torch.count_nonzero(meta.conic_2D) == 0
+    for t in (means, cov, inputs["colors_precomp"], inputs["opacities"]):
+        assert t.grad is not None and t.grad.shape == t.shape
+        assert torch.count_nonzero(t.grad) == 0
+
+
+def test_conic_inverse_gradient_reaches_precomputed_covariance_path(device):
+    """test_rasterizer_cuda_contracts.py:609-623, with a central-difference check
+    of each of the six covariance entries added."""
+    bg = torch.zeros(3, device=device)
+    means = torch.tensor([[0.0, 0.0, 2.0]], device=device)
+    base = torch.tensor([[0.25, 0.03, -0.02, 0.2, 0.04, 0.3]], device=device)
+
+    def loss_for(cov, grad):
+        cov = cov.clone().requires_grad_(grad)
+        _, _, meta = _std(device, _inputs(device, means, covariances=cov), _settings(device, bg))
+        return meta.conic_2D_inv.sum(), cov
+
+    loss, cov = loss_for(base, True)
+    loss.backward()
+    assert torch.isfinite(cov.grad).all() and cov.grad.abs().sum().item() > 0
+    eps = 1e-3
+    for j in range(6):
+        step = torch.zeros_like(base)
+        step[0, j] = eps
+        numeric = (loss_for(base + step, False)[0].item() - loss_for(base - step, False)[0].item()) / (2 * eps)
+        assert abs(cov.grad[0, j].item() - numeric) <= max(1e-2, abs(numeric) * 5e-2), (j, cov.grad, numeric)
+
+
+def test_rotated_precomputed_covariance_matches_per_pixel_compositing(device):
+    """The rotated-Gaussian compositing contract (test_rasterizer_cuda_contracts.py:482-505)
+    fed the same Gaussian as a precomputed covariance."""
+    import numpy as np
+
+    import dense_ref
+    size = 64
+    bg = torch.tensor([0.1, 0.2, 0.3], device=device)
+    opacity = 0.2
+    rgb = torch.tensor([[0.7, 0.4, 0.2]], device=device)
+    cov = dense_ref.covariance_upper(np.array([[0.25, 0.03, 0.1]]), np.array([[0.92, 0.0, 0.0, 0.39]]))
+    inputs = _inputs(device, torch.tensor([[-0.5, -0.5, 2.0]], device=device),
+                     covariances=torch.tensor(cov, dtype=torch.float32, device=device))
+    inputs["colors_precomp"] = rgb
+    inputs["opacities"] = torch.full((1, 1), opacity, device=device)
+    rendered, _, meta = _std(device, inputs, _settings(device, bg, size=size))
+    point, conic = meta.proj_2D[0], meta.conic_2D[0]
+    pix = torch.arange(size, dtype=torch.float32, device=device)
+    py, px = torch.meshgrid(pix, pix, indexing="ij")
+    dx, dy = point[0] - px, point[1] - py
+    power = -0.5 * (conic[0] * dx * dx + conic[2] * dy * dy) - conic[1] * dx * dy
+    alpha = torch.clamp(opacity * torch.exp(power), max=0.99)
+    alpha = torch.where(alpha >= 1.0 / 255.0, alpha, 0.0)
+    expected = rgb[0, :, None, None] * alpha[None] + bg[:, None, None] * (1.0 - alpha[None])
+    torch.testing.assert_close(rendered, expected, atol=2e-5, rtol=2e-4)
+    assert alpha.max() > 0.15
 
 
 def test_colour_gradient_matches_finite_difference(device):

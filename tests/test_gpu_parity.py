@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from gswarp_amd import _pipeline, configs
-from helpers import gpu_forward, grad_mismatch, options, oracle_forward, to_np
+from helpers import gpu_forward, grad_mismatch, options, oracle_forward, to_np, with_precomputed_covariance
 
 pytestmark = pytest.mark.gpu
 
@@ -137,14 +137,18 @@ def _check_backward(scene, *, flow_double=False, compute_depth=True, colors=Fals
                                    _pipeline.ForwardState(out["pre"], out["bins"], out["res"].n_contrib),
                                    flow_double=flow_double)
     torch.cuda.synchronize()
-    g_means2d, g_colors, g_opac, g_means3d, _g_cov, g_sh, g_scales, g_rot = grads
+    g_means2d, g_colors, g_opac, g_means3d, g_cov, g_sh, g_scales, g_rot = grads
     ref_g = __import__("oracle").rasterize_backward(
         host, ref, to_np(up["color"]), to_np(up["depth"]), to_np(up["alpha"]), compute_depth=compute_depth,
         grad_proj_2d=to_np(up["proj_2d"]), grad_conic_2d=to_np(up["conic_2d"]),
         grad_conic_2d_inv=to_np(up["conic_2d_inv"]), flow_double=flow_double)
     checks = [("means2D", g_means2d, ref_g["means2D"]), ("opacities", g_opac, ref_g["opacities"]),
-              ("means3D", g_means3d, ref_g["means3D"]), ("scales", g_scales, ref_g["scales"]),
-              ("rotations", g_rot, ref_g["rotations"])]
+              ("means3D", g_means3d, ref_g["means3D"])]
+    if "cov3D_precomp" in scene:
+        checks.append(("cov3D", g_cov, ref_g["cov3D"]))
+        assert g_scales.numel() == 0 and g_rot.numel() == 0
+    else:
+        checks += [("scales", g_scales, ref_g["scales"]), ("rotations", g_rot, ref_g["rotations"])]
     if colors:
         checks.append(("colors", g_colors, ref_g["colors"]))
     else:
@@ -172,3 +176,22 @@ def test_flow_backward_doubling_matches_oracle(device):
 def test_backward_depth_off_and_colors_precomp(device):
     scene = configs.make_scene(2, count=20_000, width=320, height=200, device=device)
     _check_backward(scene, compute_depth=False, colors=True)
+
+
+@pytest.mark.parametrize("case", ["c1_full", "c2_small", "c1_ragged"])
+def test_precomputed_covariance_forward_matches_oracle(case, device):
+    """cov3D_precomp input (preprocess_kernels.py:345-477): every stage bit-exact."""
+    scene = with_precomputed_covariance(_scene(case, device))
+    _check_forward(scene, options())
+
+
+@pytest.mark.parametrize("coverage_mode", [0, 2])
+def test_precomputed_covariance_coverage_modes_match_oracle(coverage_mode, device):
+    scene = with_precomputed_covariance(configs.make_scene(1, count=20_000, width=320, height=256, device=device))
+    _check_forward(scene, options(coverage_mode=coverage_mode), coverage_mode=coverage_mode)
+
+
+@pytest.mark.parametrize("case,flow_double", [("c1_full", False), ("c2_small", False), ("c4_small", True)])
+def test_precomputed_covariance_backward_matches_oracle(case, flow_double, device):
+    """dL/dcov3D from the chain of backward_ops.py:679-744 instead of scale / rotation."""
+    _check_backward(with_precomputed_covariance(_scene(case, device)), flow_double=flow_double)

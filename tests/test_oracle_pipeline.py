@@ -431,3 +431,68 @@ def test_flow_doubling_adds_render_grads_once_more():
         assert not np.allclose(doubled[name], single[name])
     np.testing.assert_array_equal(doubled["opacities"], single["opacities"])
     np.testing.assert_array_equal(doubled["sh"], single["sh"])
+
+
+# ---------------------------------------------------------------- precomputed 3D covariances
+
+def cov3d_of(s: dict) -> np.ndarray:
+    """Upper triangle (xx, xy, xz, yy, yz, zz) of R diag(s^2) R^T in float64."""
+    return dense_ref.covariance_upper(s["scales"], s["rotations"])
+
+
+def precomp_scene(seed: int, n: int = 50) -> dict:
+    s = tiny_scene(seed, n=n)
+    s["cov3D_precomp"] = cov3d_of(s).astype(np.float32)
+    return s
+
+
+def test_precomputed_covariance_matches_scale_rotation_path():
+    """The masked path fed R diag(s^2) R^T reproduces the fused path's outputs
+    (same mathematics, different float evaluation order)."""
+    s = precomp_scene(4, n=200)
+    ref = oracle.rasterize({k: v for k, v in s.items() if k != "cov3D_precomp"})
+    got = oracle.rasterize({k: v for k, v in s.items() if k not in ("scales", "rotations")})
+    assert np.mean(got["pre"]["radii"] == ref["pre"]["radii"]) > 0.98
+    vis = (got["pre"]["radii"] > 0) & (ref["pre"]["radii"] > 0)
+    np.testing.assert_allclose(got["pre"]["conic_2d_inv"][vis], ref["pre"]["conic_2d_inv"][vis], rtol=1e-4, atol=1e-6)
+    np.testing.assert_allclose(got["fwd"]["color"], ref["fwd"]["color"], atol=2e-3)
+
+
+def test_precomputed_covariance_masked_path_details():
+    """The masked kernel culls |det| < 1e-7 (strict) and stores the given
+    covariance for the backward (preprocess_kernels.py:420-422)."""
+    s = precomp_scene(5, n=20)
+    s.pop("scales")
+    s.pop("rotations")
+    res = oracle.rasterize(s)
+    np.testing.assert_array_equal(res["pre"]["cov3d"], s["cov3D_precomp"])
+    assert (res["pre"]["radii"] > 0).sum() > 5
+
+
+@pytest.mark.parametrize("seed", [0, 3])
+def test_precomputed_covariance_backward_matches_float64_autograd(seed):
+    s = precomp_scene(seed)
+    s.pop("scales")
+    s.pop("rotations")
+    res = oracle.rasterize(s)
+    g = torch.Generator().manual_seed(200 + seed)
+    H, W = s["height"], s["width"]
+    gc = torch.randn(3, H, W, generator=g, dtype=torch.float64)
+    gd = torch.randn(1, H, W, generator=g, dtype=torch.float64)
+    ga = torch.randn(1, H, W, generator=g, dtype=torch.float64)
+    grads = oracle.rasterize_backward(s, res, gc.numpy().astype(np.float32), gd.numpy().astype(np.float32),
+                                      ga.numpy().astype(np.float32))
+    leaves = {k: t64(s[k]).requires_grad_(True) for k in ("means3D", "opacities", "shs", "cov3D_precomp")}
+    pre = dense_ref.preprocess(leaves["means3D"], None, None, t64(s["viewmatrix"]), t64(s["projmatrix"]),
+                               t64(s["campos"]), s["tanfovx"], s["tanfovy"], W, H, shs=leaves["shs"],
+                               degree=s["sh_degree"], cov3d=leaves["cov3D_precomp"])
+    n = s["means3D"].shape[0]
+    out = dense_ref.render(pre["pix"], pre["conic"], leaves["opacities"][:, 0], pre["rgb"], pre["depth"],
+                           res["pre"]["radii"], tile_sets_of(res, n, W), W, H, t64(s["bg"]))
+    ((out["color"] * gc).sum() + (out["alpha"] * ga).sum() + (out["depth"] * gd).sum()).backward()
+    for name, key in (("means3D", "means3D"), ("cov3D", "cov3D_precomp"), ("opacities", "opacities"),
+                      ("sh", "shs")):
+        expected = leaves[key].grad.numpy()
+        bad, worst = grad_mismatch(grads[name], expected)
+        assert bad == 0, (name, worst)
+        assert np.abs(expected).max() > 0
