@@ -17,7 +17,7 @@ from dataclasses import dataclass
 
 import torch
 
-from . import _lib, _workspace
+from . import _lib, _packing, _workspace
 from ._coverage import tile_coverage_mode_id
 from ._runtime import BINNING_SORT_MODES, ExecutionOptions
 from ._state import BinningState, ForwardResult, ForwardState, KeyLayout, PreprocessOutputs, RenderStageResult
@@ -144,8 +144,9 @@ def _covariance_inputs(inputs: RasterInputs, P: int):
     return _f32c(inputs.scales), _f32c(inputs.rotations, align16=True), None
 
 
-def preprocess(inputs: RasterInputs, options: ExecutionOptions) -> PreprocessOutputs:
-    """Fused projection / covariance / coverage / SH colour (preprocess_ops.py:289-581)."""
+def preprocess(inputs: RasterInputs, options: ExecutionOptions, *, pack: bool = False) -> PreprocessOutputs:
+    """Fused projection / covariance / coverage / SH colour (preprocess_ops.py:289-581).
+    With ``pack`` the records and clamp bits live in one raw-ABI geom buffer."""
     if inputs.prefiltered:
         raise NotImplementedError("prefiltered=True is not supported by the gfx950 preprocess path.")
     has_cov = inputs.cov3d_precomp.numel() != 0
@@ -160,6 +161,12 @@ def preprocess(inputs: RasterInputs, options: ExecutionOptions) -> PreprocessOut
     P = means.shape[0]
     W, H = inputs.image_width, inputs.image_height
     f = dict(dtype=torch.float32, device=device)
+    if pack:
+        geom, records, clamped = _packing.allocate_geom(P, device)
+    else:
+        geom = None
+        records = torch.empty((P, _lib.GS_RECORD_FLOATS), **f)
+        clamped = torch.empty((P,), dtype=torch.uint8, device=device)
     out = PreprocessOutputs(
         radii=torch.empty((P,), dtype=torch.int32, device=device),
         depths=torch.empty((P,), **f),
@@ -167,9 +174,10 @@ def preprocess(inputs: RasterInputs, options: ExecutionOptions) -> PreprocessOut
         conic_2d=torch.empty((P, 3), **f),
         conic_2d_inv=torch.empty((P, 3), **f),
         tiles_touched=torch.empty((P,), dtype=torch.int32, device=device),
-        records=torch.empty((P, _lib.GS_RECORD_FLOATS), **f),
-        clamped=torch.empty((P,), dtype=torch.uint8, device=device),
+        records=records,
+        clamped=clamped,
         coverage_mode=tile_coverage_mode_id(options.tile_coverage_mode),
+        geom=geom,
     )
     colors = _f32c(inputs.colors) if inputs.colors.numel() != 0 else None
     shs = None
@@ -216,7 +224,7 @@ DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN = 4
 
 
 def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options: ExecutionOptions,
-            keep_keys: bool = False) -> BinningState:
+            keep_keys: bool = False, pack: bool = False) -> BinningState:
     """Per-tile Gaussian lists (binning_ops.py:84-431) in the requested sort mode.
 
     Every mode yields the same lists: per tile, the Gaussians in (depth, index)
@@ -229,7 +237,8 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
     runs the reference's depth-then-tile dataflow with the HIP radix sort when
     there are more than DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN pairs per Gaussian,
     and the single packed-key sort otherwise, where one sort of the pairs is
-    cheaper than two sorts and the extra gathers.
+    cheaper than two sorts and the extra gathers.  With ``pack`` point_list and
+    ranges are views of one raw-ABI binning buffer.
     """
     mode = options.binning_sort_mode
     if mode not in BINNING_SORT_MODES:
@@ -251,16 +260,29 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
     R = validate_pair_count(int(pinned[0]))
     depth_range = int(pinned[1]) & 0xFFFFFFFFFFFFFFFF
     _note("num_rendered", R)
+    buffer = point_list = ranges = None
+    if pack:
+        buffer, point_list, ranges = _packing.allocate_binning(R, T, device)
     if R == 0:
-        return BinningState(grid_x, grid_y, torch.empty((0,), dtype=torch.int32, device=device),
-                            torch.zeros((T, 2), dtype=torch.int32, device=device), 0)
+        if ranges is None:
+            ranges = torch.empty((T, 2), dtype=torch.int32, device=device)
+        ranges.zero_()
+        return BinningState(grid_x, grid_y, torch.empty((0,), dtype=torch.int32, device=device), ranges, 0,
+                            buffer=buffer)
     layout = key_layout(P, T, depth_range & 0xFFFFFFFF, depth_range >> 32)
     if mode == "warp_radix" or (mode == "warp_depth_stable_tile" and layout.value_bits > 0
                                 and R <= DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN * P):
         _note("binning_dataflow", "packed_key")
-        return _binning_packed(pre, image_width, image_height, offsets, R, layout, keep_keys)
-    _note("binning_dataflow", "depth_then_tile")
-    return _binning_depth_tile(pre, image_width, image_height, R, keep_keys, use_torch=(mode == "torch"))
+        bins = _binning_packed(pre, image_width, image_height, offsets, R, layout, keep_keys, point_list, ranges)
+    else:
+        _note("binning_dataflow", "depth_then_tile")
+        bins = _binning_depth_tile(pre, image_width, image_height, R, keep_keys, mode == "torch", ranges)
+    if buffer is not None:
+        if bins.point_list.data_ptr() != point_list.data_ptr():
+            point_list.copy_(bins.point_list)
+            bins.point_list = point_list
+        bins.buffer = buffer
+    return bins
 
 
 def _note(key: str, value) -> None:
@@ -269,7 +291,7 @@ def _note(key: str, value) -> None:
 
 
 def _binning_depth_tile(pre: PreprocessOutputs, image_width: int, image_height: int, R: int, keep_keys: bool,
-                        use_torch: bool) -> BinningState:
+                        use_torch: bool, ranges: torch.Tensor | None = None) -> BinningState:
     """Depth sort of the Gaussians, tile counts scanned in depth order, (tile, point)
     pairs emitted in that order and sorted stably by tile (binning_ops.py:152-343)."""
     lib = _lib.load()
@@ -321,7 +343,8 @@ def _binning_depth_tile(pre: PreprocessOutputs, image_width: int, image_height: 
                      vals_alt.data_ptr(), scratch.data_ptr(), scratch.numel(), stream)
             if lib.gs_sort_num_passes(tile_bits) % 2:
                 tiles, vals = tiles_alt, vals_alt
-    ranges = torch.empty((T, 2), dtype=torch.int32, device=device)
+    if ranges is None:
+        ranges = torch.empty((T, 2), dtype=torch.int32, device=device)
     with _stage("ranges"):
         lib.call("gs_tile_ranges_u32", R, tiles.data_ptr(), T, ranges.data_ptr(), stream)
     keys = None
@@ -332,7 +355,8 @@ def _binning_depth_tile(pre: PreprocessOutputs, image_width: int, image_height: 
 
 
 def _binning_packed(pre: PreprocessOutputs, image_width: int, image_height: int, offsets: torch.Tensor, R: int,
-                    layout: KeyLayout, keep_keys: bool) -> BinningState:
+                    layout: KeyLayout, keep_keys: bool, point_list: torch.Tensor | None = None,
+                    ranges: torch.Tensor | None = None) -> BinningState:
     """One packed 64-bit key per pair, emitted in point order and sorted once."""
     lib = _lib.load()
     device = pre.radii.device
@@ -363,8 +387,12 @@ def _binning_packed(pre: PreprocessOutputs, image_width: int, image_height: int,
                      vals_alt.data_ptr(), sort_scratch.data_ptr(), sort_scratch.numel(), stream)
     if lib.gs_sort_num_passes(sort_bits) % 2:
         keys, vals = keys_alt, vals_alt
-    point_list = torch.empty((R,), dtype=torch.int32, device=device) if packed else vals
-    ranges = torch.empty((T, 2), dtype=torch.int32, device=device)
+    if not packed:
+        point_list = vals
+    elif point_list is None:
+        point_list = torch.empty((R,), dtype=torch.int32, device=device)
+    if ranges is None:
+        ranges = torch.empty((T, 2), dtype=torch.int32, device=device)
     with _stage("ranges"):
         lib.call("gs_tile_ranges", R, keys.data_ptr(), layout.tile_shift, layout.value_bits, T, ranges.data_ptr(),
                  point_list.data_ptr() if packed else None, stream)
@@ -417,8 +445,10 @@ def render(pre: PreprocessOutputs, bins: BinningState, background: torch.Tensor,
     return RenderStageResult(color, depth, alpha, n_contrib, aux)
 
 
-def forward(inputs: RasterInputs, options: ExecutionOptions, *, flow: bool = False) -> ForwardResult:
-    """One typed forward: the reference's execute_typed_forward (pipeline.py:11-45)."""
+def forward(inputs: RasterInputs, options: ExecutionOptions, *, flow: bool = False,
+            pack: bool = False) -> ForwardResult:
+    """One typed forward: the reference's execute_typed_forward (pipeline.py:11-45).
+    ``pack`` lays the state out in the raw ABI's geom / binning buffers."""
     means = inputs.means3d
     if means.ndim != 2 or means.shape[1] != 3:
         raise ValueError("means3D must have dimensions (num_points, 3)")
@@ -427,8 +457,8 @@ def forward(inputs: RasterInputs, options: ExecutionOptions, *, flow: bool = Fal
         if means.shape[0] == 0:
             k = (options.flow_topk if options.compute_flow_aux else 0) if flow else None
             return empty_forward(inputs, k)
-        pre = preprocess(inputs, options)
-        bins = binning(pre, inputs.image_height, inputs.image_width, options)
+        pre = preprocess(inputs, options, pack=pack)
+        bins = binning(pre, inputs.image_height, inputs.image_width, options, pack=pack)
         res = render(pre, bins, inputs.background, inputs.image_height, inputs.image_width, options, flow=flow)
     return ForwardResult(
         num_rendered=bins.num_rendered,

@@ -23,6 +23,7 @@ class PreprocessOutputs:
     records: torch.Tensor  # (N, 12) fp32 render records
     clamped: torch.Tensor  # (N,) uint8 SH clamp bits
     coverage_mode: int = 1
+    geom: torch.Tensor | None = None  # raw-ABI byte buffer that records and clamped are views of
 
 
 @dataclass(slots=True)
@@ -48,6 +49,7 @@ class BinningState:
     num_rendered: int
     sorted_keys: torch.Tensor | None = None  # (R,) int64 sorted binning keys (see KeyLayout)
     key_layout: KeyLayout = field(default_factory=KeyLayout)
+    buffer: torch.Tensor | None = None  # raw-ABI (R + 2T) int32 buffer that point_list and ranges are views of
 
     def decode_keys(self) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         """(tile id, depth float bits, sort field = tile and depth fields as one

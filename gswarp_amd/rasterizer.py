@@ -125,6 +125,21 @@ def get_runtime_auto_tuning_config():
     return False, False
 
 
+def set_runtime_auto_tuning(enabled: bool | None = None, verbose: bool | None = None) -> None:
+    """Accepted for compatibility (runtime.py:162-167); launch shapes are fixed."""
+
+
+def is_available() -> bool:
+    """True when the gfx950 HIP library loads (runtime.py:439-440 asks the same of Warp)."""
+    from . import _lib
+
+    try:
+        _lib.load()
+    except (OSError, RuntimeError):
+        return False
+    return True
+
+
 def clear_warp_caches():
     """Release the per-stream host workspaces (the name is kept for compatibility)."""
     _workspace.clear_caches()
