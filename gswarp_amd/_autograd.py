@@ -21,7 +21,8 @@ def _forward_args(means3D, sh, colors_precomp, opacities, scales, rotations, cov
         raster_settings.bg, means3D, colors_precomp, opacities, scales, rotations, raster_settings.scale_modifier,
         cov3Ds_precomp, raster_settings.viewmatrix, raster_settings.projmatrix, raster_settings.tanfovx,
         raster_settings.tanfovy, raster_settings.image_height, raster_settings.image_width, sh,
-        raster_settings.sh_degree, raster_settings.campos, raster_settings.prefiltered)
+        raster_settings.sh_degree, raster_settings.campos, raster_settings.prefiltered,
+        float(getattr(raster_settings, "filter_variance", 0.0)))
 
 
 def _run_forward(ctx, means3D, sh, colors_precomp, opacities, scales, rotations, cov3Ds_precomp, raster_settings,

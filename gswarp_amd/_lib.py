@@ -32,7 +32,7 @@ SIGNATURES = {
     "gs_preprocess_fwd": (
         ctypes.c_int,
         [_i32, _i32, _i32, _vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _f32, _f32, _f32, _i32,
-         _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+         _i32, _i32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     ),
     "gs_mark_visible": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp]),
     "gs_scan_scratch_bytes": (_sz, [_i32]),
@@ -63,7 +63,7 @@ SIGNATURES = {
     "gs_preprocess_bwd": (
         ctypes.c_int,
         [_i32, _i32, _i32, _vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _f32, _f32, _f32, _f32, _vp, _vp, _vp, _vp,
-         _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+         _vp, _vp, _i32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     ),
 }
 

@@ -60,6 +60,9 @@ class RasterInputs:
     degree: int
     campos: torch.Tensor
     prefiltered: bool
+    # Mip-Splatting screen-space variance, the Mip method's 19th forward
+    # argument (mip_autograd.py:51-71); 0 for the standard rasterizer.
+    filter_variance: float = 0.0
 
     @classmethod
     def from_args(cls, args) -> "RasterInputs":
@@ -201,7 +204,8 @@ def preprocess(inputs: RasterInputs, options: ExecutionOptions, *, pack: bool = 
             _lib.ptr(rot_c), _lib.ptr(cov_c), float(inputs.scale_modifier), opac_c.data_ptr(), _lib.ptr(shs),
             _lib.ptr(colors),
             view_c.data_ptr(), proj_c.data_ptr(), campos_c.data_ptr(), tanfovx, tanfovy, _focal(W, tanfovx),
-            _focal(H, tanfovy), W, H, out.coverage_mode, out.radii.data_ptr(), out.depths.data_ptr(),
+            _focal(H, tanfovy), W, H, out.coverage_mode, float(inputs.filter_variance), out.radii.data_ptr(),
+            out.depths.data_ptr(),
             out.proj_2d.data_ptr(), out.conic_2d.data_ptr(), out.conic_2d_inv.data_ptr(),
             out.tiles_touched.data_ptr(), out.records.data_ptr(), out.clamped.data_ptr(), _stream(device))
     return out
@@ -549,7 +553,8 @@ def backward(inputs: RasterInputs, radii: torch.Tensor, alpha: torch.Tensor, gra
                 _lib.ptr(rot_c), _lib.ptr(cov_c), float(inputs.scale_modifier), _lib.ptr(shs), campos_c.data_ptr(),
                 view_c.data_ptr(), proj_c.data_ptr(), tanfovx, tanfovy, _focal(W, tanfovx), _focal(H, tanfovy),
                 radii_c.data_ptr(), pre.clamped.data_ptr(), grad_gauss.data_ptr(), gp2.data_ptr(), gcon.data_ptr(),
-                gcov.data_ptr(), int(bool(flow_double)), grad_means3d.data_ptr(), grad_means2d.data_ptr(),
+                gcov.data_ptr(), int(bool(flow_double)), float(inputs.filter_variance), grad_means3d.data_ptr(),
+                grad_means2d.data_ptr(),
                 _lib.ptr(grad_scales) if cov_c is None else None,
                 _lib.ptr(grad_rotations) if cov_c is None else None,
                 _lib.ptr(grad_cov3d) if cov_c is not None else None,

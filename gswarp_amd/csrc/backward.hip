@@ -327,6 +327,7 @@ struct PreprocessBwdParams {
   const float* grad_conic_2d;
   const float* grad_conic_2d_inv;
   int flow_double;
+  float filter_variance;  // Mip-Splatting screen-space variance added to cov2D; 0 = none
   float* grad_means3d;
   float* grad_means2d;
   float* grad_scales;
@@ -570,9 +571,9 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(PreprocessBwdParams
     const float vt1x = v00 * t01 + v01 * t11 + v02 * t21;
     const float vt1y = v01 * t01 + v11 * t11 + v12 * t21;
     const float vt1z = v02 * t01 + v12 * t11 + v22 * t21;
-    const float aa = t00 * vt0x + t10 * vt0y + t20 * vt0z + 0.3f + 0.0f;
+    const float aa = t00 * vt0x + t10 * vt0y + t20 * vt0z + 0.3f + p.filter_variance;
     const float bb = t00 * vt1x + t10 * vt1y + t20 * vt1z;
-    const float cc = t01 * vt1x + t11 * vt1y + t21 * vt1z + 0.3f + 0.0f;
+    const float cc = t01 * vt1x + t11 * vt1y + t21 * vt1z + 0.3f + p.filter_variance;
     const float denom = aa * cc - bb * bb;
     const float denom2inv = 1.0f / (denom * denom + 1.0e-7f);
 
@@ -744,11 +745,13 @@ extern "C" int gs_preprocess_bwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
                                  const float* projmatrix, float tanfovx, float tanfovy, float focal_x,
                                  float focal_y, const int32_t* radii, const uint8_t* clamped,
                                  const float* grad_gauss, const float* grad_proj_2d, const float* grad_conic_2d,
-                                 const float* grad_conic_2d_inv, int32_t flow_double, float* grad_means3d,
-                                 float* grad_means2d, float* grad_scales, float* grad_rotations,
+                                 const float* grad_conic_2d_inv, int32_t flow_double, float filter_variance,
+                                 float* grad_means3d, float* grad_means2d, float* grad_scales,
+                                 float* grad_rotations,
                                  float* grad_cov3d, float* grad_sh, float* grad_opacity, float* grad_colors,
                                  void* stream) {
   if (P < 0) return GS_ERR_INVALID_ARGUMENT;
+  if (!(filter_variance >= 0.0f) || !__builtin_isfinite(filter_variance)) return GS_ERR_INVALID_ARGUMENT;
   if (P == 0) return GS_OK;
   if (!means3d || !viewmatrix || !projmatrix || !radii || !grad_gauss || !grad_proj_2d || !grad_conic_2d ||
       !grad_conic_2d_inv || !grad_means3d || !grad_means2d)
@@ -784,6 +787,7 @@ extern "C" int gs_preprocess_bwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
   p.grad_conic_2d = grad_conic_2d;
   p.grad_conic_2d_inv = grad_conic_2d_inv;
   p.flow_double = flow_double;
+  p.filter_variance = filter_variance;
   p.grad_means3d = grad_means3d;
   p.grad_means2d = grad_means2d;
   p.grad_scales = grad_scales;

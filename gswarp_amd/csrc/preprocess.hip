@@ -7,6 +7,8 @@
 //   conic, radius, tile-rect cull          preprocess_kernels.py:221-244
 //   outputs + tile coverage count          preprocess_kernels.py:246-269
 //   SH degree 0..3 colour, +0.5, clamp     preprocess_kernels.py:272-342
+//   optional Mip-Splatting filter: cov2D + f I, its conic, radius and tile
+//   count for Gaussians the base cull keeps     backend_mip_3dgs.py:63-102
 // The colour is written into a packed 48-byte render record together with
 // the screen position, conic, opacity and depth, so the render kernels fetch
 // one Gaussian with three 16-byte loads.  SH colour is evaluated for visible
@@ -34,6 +36,7 @@ struct PreprocessParams {
   const float* campos;
   float tanfovx, tanfovy, focal_x, focal_y;
   int W, H, grid_x, grid_y, coverage_mode;
+  float filter_variance;  // Mip-Splatting screen-space variance; 0 = none
   int* radii;
   float* depths;
   float* proj_2d;
@@ -190,15 +193,36 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p)
       const float pty = ndc_to_pix(p_proj_y, p.H);
       const int4 rect = tile_rect(ptx, pty, rad, rad, p.grid_x, p.grid_y);
       visible = (rect.z - rect.x) * (rect.w - rect.y) != 0;
-      if (visible) {
-        const float op = p.opacities[idx];
-        radius = rad;
+      float fa = ca, fc = cc, q0 = k0, q1 = k1, q2 = k2;
+      int frad = rad;
+      if (visible && p.filter_variance != 0.0f) {
+        // Mip filter on a kept Gaussian: culled unless the filtered
+        // determinant exceeds 1e-12; depth and position stay.
+        fa = ca + p.filter_variance;
+        fc = cc + p.filter_variance;
+        const float fdet = fa * fc - cb * cb;
         depth = p_view_z;
         pxo = ptx;
         pyo = pty;
-        con0 = k0; con1 = k1; con2 = k2;
-        cov_a = ca; cov_b = cb; cov_c = cc;
-        touched = count_covered_tiles(ptx, pty, ca, cc, k0, k1, k2, op, rad, p.grid_x, p.grid_y,
+        visible = fdet > 1.0e-12f;
+        const float inv = 1.0f / fdet;
+        q0 = fc * inv; q1 = -cb * inv; q2 = fa * inv;
+        const float d = fa - fc;
+        float disc = 0.25f * (d * d) + cb * cb;
+        disc = disc < 0.0f ? 0.0f : disc;
+        float lam = 0.5f * (fa + fc) + sqrtf(disc);
+        lam = lam < 0.1f ? 0.1f : lam;
+        frad = f2i(ceilf(3.0f * sqrtf(lam)));
+      }
+      if (visible) {
+        const float op = p.opacities[idx];
+        radius = frad;
+        depth = p_view_z;
+        pxo = ptx;
+        pyo = pty;
+        con0 = q0; con1 = q1; con2 = q2;
+        cov_a = fa; cov_b = cb; cov_c = fc;
+        touched = count_covered_tiles(ptx, pty, fa, fc, q0, q1, q2, op, frad, p.grid_x, p.grid_y,
                                       p.coverage_mode);
 
         float3 col;
@@ -223,8 +247,8 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p)
           if (col.z < 0.0f) { col.z = 0.0f; clamp_bits |= 4; }
         }
         float4* rec = p.records + 3 * (size_t)idx;
-        rec[0] = make_float4(ptx, pty, k0, k1);
-        rec[1] = make_float4(k2, op, p_view_z, power_cutoff(op));
+        rec[0] = make_float4(ptx, pty, q0, q1);
+        rec[1] = make_float4(q2, op, p_view_z, power_cutoff(op));
         rec[2] = make_float4(col.x, col.y, col.z, 0.0f);
         if (p.clamped != nullptr) p.clamped[idx] = clamp_bits;
       }
@@ -265,11 +289,13 @@ extern "C" int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
                                  const float* viewmatrix, const float* projmatrix, const float* campos,
                                  float tanfovx, float tanfovy, float focal_x, float focal_y,
                                  int32_t image_width, int32_t image_height, int32_t coverage_mode,
-                                 int32_t* radii, float* depths, float* proj_2d, float* conic_2d,
+                                 float filter_variance, int32_t* radii, float* depths, float* proj_2d,
+                                 float* conic_2d,
                                  float* conic_2d_inv, int32_t* tiles_touched, float* records,
                                  uint8_t* clamped, void* stream) {
   if (P < 0 || image_width <= 0 || image_height <= 0) return GS_ERR_INVALID_ARGUMENT;
   if (coverage_mode < 0 || coverage_mode > 2) return GS_ERR_INVALID_ARGUMENT;
+  if (!(filter_variance >= 0.0f) || !__builtin_isfinite(filter_variance)) return GS_ERR_INVALID_ARGUMENT;
   if (P == 0) return GS_OK;
   if (!means3d || !opacities || !viewmatrix || !projmatrix || !radii || !depths || !proj_2d || !conic_2d ||
       !conic_2d_inv || !tiles_touched || !records)
@@ -304,6 +330,7 @@ extern "C" int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
   p.grid_x = (image_width + gs::kBlockX - 1) / gs::kBlockX;
   p.grid_y = (image_height + gs::kBlockY - 1) / gs::kBlockY;
   p.coverage_mode = coverage_mode;
+  p.filter_variance = filter_variance;
   p.radii = radii;
   p.depths = depths;
   p.proj_2d = proj_2d;

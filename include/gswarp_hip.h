@@ -65,11 +65,16 @@ const char* gs_status_string(int status);
  * may then be NULL), with the reference's masked-kernel arithmetic.
  * Culled Gaussians get radius 0 and zero outputs; records are written only
  * for visible Gaussians.  clamped (N bytes, optional) receives the per-channel
- * clamp flags of the SH colour as bits 0..2.
+ * clamp flags of the SH colour as bits 0..2.  A non-zero filter_variance
+ * (finite, >= 0) applies the Mip-Splatting screen-space filter to the kept
+ * Gaussians: cov2D + f I, its conic, the radius ceil(3 sqrt(max(lambda_max,
+ * 0.1))) and the tile count are recomputed; a filtered determinant <= 1e-12
+ * culls (depth and position are kept).
  * Replaces: preprocess_ops.py:289-581 (preprocess_gaussians) with
  * preprocess_kernels.py:83-269 (scales/rotations), preprocess_kernels.py:345-477
- * and 604-624 (precomputed covariances) and the SH kernel
- * preprocess_kernels.py:272-342.
+ * and 604-624 (precomputed covariances), the SH kernel
+ * preprocess_kernels.py:272-342, and the Mip filter of backend_mip_3dgs.py:63-102
+ * (whose tile recount is binning_kernels.py:56-123).
  */
 int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, const float* means3d,
                       const float* scales, const float* rotations, const float* cov3d_precomp, float scale_modifier,
@@ -77,7 +82,7 @@ int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, const float*
                       const float* viewmatrix, const float* projmatrix, const float* campos,
                       float tanfovx, float tanfovy, float focal_x, float focal_y,
                       int32_t image_width, int32_t image_height, int32_t coverage_mode,
-                      int32_t* radii, float* depths, float* proj_2d, float* conic_2d,
+                      float filter_variance, int32_t* radii, float* depths, float* proj_2d, float* conic_2d,
                       float* conic_2d_inv, int32_t* tiles_touched, float* records,
                       uint8_t* clamped, void* stream);
 
@@ -238,7 +243,9 @@ int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t num_points,
  * evaluated bands); grad_opacity (N) and grad_colors (N,3, when non-NULL)
  * are copied out of grad_gauss.  With cov3d_precomp non-NULL the cov2D
  * gradient is returned as grad_cov3d (N, 6) instead of being chained into
- * grad_scales / grad_rotations (which may then be NULL).
+ * grad_scales / grad_rotations (which may then be NULL).  filter_variance is
+ * the forward's Mip-Splatting variance (0 without the filter), added to the
+ * recomputed cov2D as in backward_kernels.py:176-178.
  * Replaces: backward_ops.py:376-746 with backward_kernels.py:53-295 (fused),
  * backward_kernels.py:710-870 (precomputed covariances),
  * backward_kernels.py:298-536 and flow_kernels.py:14-28.
@@ -249,9 +256,9 @@ int gs_preprocess_bwd(int32_t P, int32_t sh_coeffs, int32_t degree, const float*
                       const float* projmatrix, float tanfovx, float tanfovy, float focal_x, float focal_y,
                       const int32_t* radii, const uint8_t* clamped, const float* grad_gauss,
                       const float* grad_proj_2d, const float* grad_conic_2d, const float* grad_conic_2d_inv,
-                      int32_t flow_double, float* grad_means3d, float* grad_means2d, float* grad_scales,
-                      float* grad_rotations, float* grad_cov3d, float* grad_sh, float* grad_opacity,
-                      float* grad_colors, void* stream);
+                      int32_t flow_double, float filter_variance, float* grad_means3d, float* grad_means2d,
+                      float* grad_scales, float* grad_rotations, float* grad_cov3d, float* grad_sh,
+                      float* grad_opacity, float* grad_colors, void* stream);
 
 #ifdef __cplusplus
 }

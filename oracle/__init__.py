@@ -64,7 +64,7 @@ _SIGNATURES = {
     "or_preprocess": (
         None,
         [_c_int, _c_int, _c_int, _F, _F, _F, _F, _c_float, _F, _F, _F, _F, _F, _F, _c_float, _c_float, _c_float,
-         _c_float, _c_int, _c_int, _c_int, _I, _F, _F, _F, _F, _I, _F, _F, _I, _I],
+         _c_float, _c_int, _c_int, _c_int, _c_float, _I, _F, _F, _F, _F, _I, _F, _F, _I, _I],
     ),
     "or_mark_visible": (None, [_c_int, _F, _F, _I]),
     "or_num_rendered": (_c_ll, [_c_int, _I]),
@@ -80,7 +80,7 @@ _SIGNATURES = {
     "or_preprocess_bwd": (
         None,
         [_c_int, _c_int, _c_int, _F, _F, _F, _c_float, _F, _F, _F, _I, _F, _F, _c_float, _c_float, _c_float,
-         _c_float, _I, _F, _F, _F, _F, _c_int, _c_int, _F, _F, _F, _F, _F, _F],
+         _c_float, _I, _F, _F, _F, _F, _c_int, _c_int, _c_float, _F, _F, _F, _F, _F, _F],
     ),
     "or_num_threads": (_c_int, []),
     "or_set_num_threads": (None, [_c_int]),
@@ -163,9 +163,11 @@ def emit_covered_tiles(points_xy, cov2d, conic_opacity, radii, grid_x, grid_y, m
 
 
 def preprocess(means3d, scales, rotations, opacities, view, proj, campos, *, tanfovx, tanfovy, width, height,
-               scale_modifier=1.0, shs=None, degree=0, colors=None, coverage_mode=1, cov3d_precomp=None) -> dict:
+               scale_modifier=1.0, shs=None, degree=0, colors=None, coverage_mode=1, cov3d_precomp=None,
+               filter_variance=0.0) -> dict:
     """Reference preprocess + SH colour: the fused scales/rotations path, or the
-    masked path for precomputed 3D covariances (cov3d_precomp (N, 6))."""
+    masked path for precomputed 3D covariances (cov3d_precomp (N, 6)); a
+    non-zero filter_variance applies the Mip-Splatting screen-space filter."""
     means3d = _f32(means3d)
     if cov3d_precomp is not None:
         cov3d_precomp = _f32(cov3d_precomp).reshape(-1, 6)
@@ -200,7 +202,7 @@ def preprocess(means3d, scales, rotations, opacities, view, proj, campos, *, tan
         _fp(opacities),
         _fp(shs), _fp(colors), _fp(view), _fp(proj), _fp(campos), float(np.float32(tanfovx)),
         float(np.float32(tanfovy)), float(focal_x), float(focal_y), width, height, coverage_mode,
-        _ip(out["radii"]), _fp(out["depths"]), _fp(out["proj_2d"]), _fp(out["conic_2d"]), _fp(out["conic_2d_inv"]),
+        float(np.float32(filter_variance)), _ip(out["radii"]), _fp(out["depths"]), _fp(out["proj_2d"]), _fp(out["conic_2d"]), _fp(out["conic_2d_inv"]),
         _ip(out["tiles_touched"]), _fp(out["cov3d"]), _fp(out["rgb"]), _ip(out["clamped"]), _ip(out["visible"]))
     out["conic_opacity"] = np.concatenate([out["conic_2d"], opacities.reshape(P, 1)], axis=1)
     out["conic_opacity"][out["radii"] <= 0] = 0.0
@@ -273,7 +275,7 @@ def render_bwd(pre: dict, bins: dict, features, background, width, height, fwd: 
 
 def preprocess_bwd(pre: dict, grad_gauss, means3d, scales, rotations, view, proj, campos, *, tanfovx, tanfovy,
                    width, height, scale_modifier=1.0, shs=None, degree=0, grad_proj_2d=None, grad_conic_2d=None,
-                   grad_conic_2d_inv=None, flow_double=False, cov3d_precomp=None) -> dict:
+                   grad_conic_2d_inv=None, flow_double=False, cov3d_precomp=None, filter_variance=0.0) -> dict:
     means3d = _f32(means3d)
     precomp = cov3d_precomp is not None
     if not precomp:
@@ -305,7 +307,8 @@ def preprocess_bwd(pre: dict, grad_gauss, means3d, scales, rotations, view, proj
         _fp(shs), _fp(_f32(campos).reshape(3)), _ip(_i32(pre["clamped"])), _fp(_f32(view).reshape(16)),
         _fp(_f32(proj).reshape(16)), float(np.float32(tanfovx)), float(np.float32(tanfovy)), float(focal_x),
         float(focal_y), _ip(_i32(pre["radii"])), _fp(_f32(grad_gauss)), _fp(grad_proj_2d), _fp(grad_conic_2d),
-        _fp(grad_conic_2d_inv), int(bool(flow_double)), int(precomp), _fp(out["means3D"]), _fp(out["means2D"]),
+        _fp(grad_conic_2d_inv), int(bool(flow_double)), int(precomp), float(np.float32(filter_variance)),
+        _fp(out["means3D"]), _fp(out["means2D"]),
         _fp(out["scales"]), _fp(out["rotations"]), _fp(out["cov3D"]), _fp(out["sh"]) if K > 0 else None)
     gg = _f32(grad_gauss)
     out["opacities"] = gg[:, 5:6].copy()
@@ -320,7 +323,7 @@ def rasterize(scene: dict, *, coverage_mode=1, compute_depth=True, top_k=0) -> d
                      s["projmatrix"], s["campos"], tanfovx=s["tanfovx"], tanfovy=s["tanfovy"], width=s["width"],
                      height=s["height"], scale_modifier=s.get("scale_modifier", 1.0), shs=s.get("shs"),
                      degree=s.get("sh_degree", 0), colors=s.get("colors_precomp"), coverage_mode=coverage_mode,
-                     cov3d_precomp=s.get("cov3D_precomp"))
+                     cov3d_precomp=s.get("cov3D_precomp"), filter_variance=s.get("filter_variance", 0.0))
     bins = binning(pre, s["width"], s["height"], coverage_mode)
     fwd = render_fwd(pre, bins, pre["rgb"], s["bg"], s["width"], s["height"], compute_depth=compute_depth,
                      top_k=top_k)
@@ -341,6 +344,6 @@ def rasterize_backward(scene: dict, result: dict, grad_color, grad_depth, grad_a
                            height=s["height"], scale_modifier=s.get("scale_modifier", 1.0), shs=s.get("shs"),
                            degree=s.get("sh_degree", 0), grad_proj_2d=grad_proj_2d, grad_conic_2d=grad_conic_2d,
                            grad_conic_2d_inv=grad_conic_2d_inv, flow_double=flow_double,
-                           cov3d_precomp=s.get("cov3D_precomp"))
+                           cov3d_precomp=s.get("cov3D_precomp"), filter_variance=s.get("filter_variance", 0.0))
     grads["grad_gauss"] = gg
     return grads

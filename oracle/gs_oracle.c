@@ -378,11 +378,52 @@ static void sh_forward_one(const float* mean, const float* campos, const float* 
  * preprocess_ops.py:548-565); colors_precomp replaces the SH colour
  * (preprocess_ops.py:548-549).  focal_x/y are the host's W/(2 tanfovx) rounded to fp32.
  */
+/* Mip-Splatting screen-space low-pass filter of one Gaussian, applied after the base preprocess
+ * (backend_mip_3dgs.py:63-102): for radius > 0, cov2D += f I; culled (radius, conic, cov2D and tile
+ * count zero) unless the filtered determinant exceeds 1e-12; otherwise conic = filtered inverse,
+ * radius = ceil(3 sqrt(max(tr/2 + sqrt(max(((a-c)^2)/4 + b^2, 0)), 0.1))) and the tiles recounted
+ * with the filtered values (binning_kernels.py:56-123, the same count as the base preprocess).
+ * Depth and screen position keep their base values. */
+static void mip_filter_one(int idx, float f, const float* opacities, int grid_x, int grid_y, int coverage_mode,
+                           int* radii, const float* proj_2d, float* conic_2d, float* conic_2d_inv,
+                           int* tiles_touched) {
+  if (radii[idx] <= 0) return;
+  const float a = conic_2d_inv[3 * idx] + f;
+  const float b = conic_2d_inv[3 * idx + 1];
+  const float c = conic_2d_inv[3 * idx + 2] + f;
+  const float det = a * c - b * b;
+  if (!(det > 1.0e-12f)) {
+    radii[idx] = 0;
+    tiles_touched[idx] = 0;
+    for (int k = 0; k < 3; ++k) conic_2d[3 * idx + k] = conic_2d_inv[3 * idx + k] = 0.0f;
+    return;
+  }
+  const float inv_det = 1.0f / det;
+  const float con0 = c * inv_det, con1 = -b * inv_det, con2 = a * inv_det;
+  const float trace = a + c;
+  const float d = a - c;
+  float disc = 0.25f * (d * d) + b * b;
+  if (disc < 0.0f) disc = 0.0f;
+  float lam = 0.5f * trace + sqrtf(disc);
+  if (lam < 0.1f) lam = 0.1f;
+  const int radius = f2i(ceilf(3.0f * sqrtf(lam)));
+  radii[idx] = radius;
+  conic_2d[3 * idx] = con0;
+  conic_2d[3 * idx + 1] = con1;
+  conic_2d[3 * idx + 2] = con2;
+  conic_2d_inv[3 * idx] = a;
+  conic_2d_inv[3 * idx + 1] = b;
+  conic_2d_inv[3 * idx + 2] = c;
+  tiles_touched[idx] = visit_covered_tiles(proj_2d[2 * idx], proj_2d[2 * idx + 1], a, c, con0, con1, con2,
+                                           opacities[idx], radius, grid_x, grid_y, coverage_mode, NULL, NULL);
+}
+
 void or_preprocess(int P, int K, int degree, const float* means3d, const float* scales, const float* rotations,
                    const float* cov3d_precomp, float scale_modifier, const float* opacities, const float* shs,
                    const float* colors,
                    const float* V, const float* Pm, const float* campos, float tanfovx, float tanfovy,
-                   float focal_x, float focal_y, int W, int H, int coverage_mode, int* radii, float* depths,
+                   float focal_x, float focal_y, int W, int H, int coverage_mode, float filter_variance,
+                   int* radii, float* depths,
                    float* proj_2d, float* conic_2d, float* conic_2d_inv, int* tiles_touched, float* cov3d,
                    float* rgb, int* clamped, int* visible_mask) {
   const int grid_x = (W + BLOCK_X - 1) / BLOCK_X;
@@ -538,6 +579,9 @@ void or_preprocess(int P, int K, int degree, const float* means3d, const float* 
                                                radius, grid_x, grid_y, coverage_mode, NULL, NULL);
     }
   sh:
+    if (filter_variance != 0.0f)
+      mip_filter_one(idx, filter_variance, opacities, grid_x, grid_y, coverage_mode, radii, proj_2d, conic_2d,
+                     conic_2d_inv, tiles_touched);
     if (colors != NULL) {
       for (int ch = 0; ch < 3; ++ch) {
         rgb[3 * idx + ch] = colors[3 * idx + ch];
@@ -833,7 +877,8 @@ void or_preprocess_bwd(int P, int K, int degree, const float* means3d, const flo
                        const int* clamped, const float* V, const float* Pm, float tanfovx, float tanfovy,
                        float focal_x, float focal_y, const int* radii, const float* grad_gauss,
                        const float* grad_proj_2d, const float* grad_conic_2d, const float* grad_conic_2d_inv,
-                       int flow_double, int cov3d_is_precomp, float* grad_means3d, float* grad_means2d,
+                       int flow_double, int cov3d_is_precomp, float filter_variance, float* grad_means3d,
+                       float* grad_means2d,
                        float* grad_scales, float* grad_rotations, float* grad_cov3d, float* grad_sh) {
 #pragma omp parallel for schedule(static)
   for (int tid = 0; tid < P; ++tid) {
@@ -968,9 +1013,9 @@ void or_preprocess_bwd(int P, int K, int degree, const float* means3d, const flo
         const float vt1x = v00 * t01 + v01 * t11 + v02 * t21;
         const float vt1y = v01 * t01 + v11 * t11 + v12 * t21;
         const float vt1z = v02 * t01 + v12 * t11 + v22 * t21;
-        const float a = t00 * vt0x + t10 * vt0y + t20 * vt0z + 0.3f + 0.0f;
+        const float a = t00 * vt0x + t10 * vt0y + t20 * vt0z + 0.3f + filter_variance;
         const float b = t00 * vt1x + t10 * vt1y + t20 * vt1z;
-        const float c = t01 * vt1x + t11 * vt1y + t21 * vt1z + 0.3f + 0.0f;
+        const float c = t01 * vt1x + t11 * vt1y + t21 * vt1z + 0.3f + filter_variance;
         const float denom = a * c - b * b;
         const float denom2inv = 1.0f / (denom * denom + 1.0e-7f);
         float u0 = grad_conic_2d[3 * tid], u1 = grad_conic_2d[3 * tid + 1], u2 = grad_conic_2d[3 * tid + 2];
@@ -1082,9 +1127,9 @@ void or_preprocess_bwd(int P, int K, int degree, const float* means3d, const flo
       const float vt1x = v00 * t01 + v01 * t11 + v02 * t21;
       const float vt1y = v01 * t01 + v11 * t11 + v12 * t21;
       const float vt1z = v02 * t01 + v12 * t11 + v22 * t21;
-      const float aa = t00 * vt0x + t10 * vt0y + t20 * vt0z + 0.3f + 0.0f;
+      const float aa = t00 * vt0x + t10 * vt0y + t20 * vt0z + 0.3f + filter_variance;
       const float bb = t00 * vt1x + t10 * vt1y + t20 * vt1z;
-      const float cc = t01 * vt1x + t11 * vt1y + t21 * vt1z + 0.3f + 0.0f;
+      const float cc = t01 * vt1x + t11 * vt1y + t21 * vt1z + 0.3f + filter_variance;
       const float denom = aa * cc - bb * bb;
       const float denom2inv = 1.0f / (denom * denom + 1.0e-7f);
       float u0 = grad_conic_2d[3 * tid], u1 = grad_conic_2d[3 * tid + 1], u2 = grad_conic_2d[3 * tid + 2];

@@ -7,7 +7,8 @@ Each step follows the reference's stated semantics:
 * projection and EWA covariance (preprocess_kernels.py:133-269): view depth
   from the row-vector view matrix, homogeneous divide by w + 1e-7, Sigma =
   R diag(s^2) R^T from the unnormalised quaternion (w, x, y, z), camera-space
-  x/z and y/z clamped to 1.3 tan(fov), cov2D = J W Sigma W^T J^T + 0.3 I,
+  x/z and y/z clamped to 1.3 tan(fov) (a clamped coordinate held constant
+  in the gradient, as the reference's backward does), cov2D = J W Sigma W^T J^T + 0.3 I,
   conic = cov2D^-1, radius = ceil(3 sqrt(mid + sqrt(max(0.1, mid^2 - det)))),
   pixel = ((ndc + 1) S - 1) / 2, culled when z <= 0.2, |det| <= 1e-7 or the
   3-sigma tile rectangle is empty;
@@ -77,9 +78,13 @@ def tile_rect(px: float, py: float, r: int, gx: int, gy: int):
 
 
 def preprocess(means, scales, rots, view, proj, campos, tanfovx, tanfovy, W, H, shs=None, degree=0,
-               colors=None, scale_modifier=1.0, cov3d=None) -> dict:
+               colors=None, scale_modifier=1.0, cov3d=None, filter_variance=0.0) -> dict:
     """float64 preprocess + colour; tensors keep their autograd history.  With
-    cov3d (N, 6: xx, xy, xz, yy, yz, zz) the 3D covariance is taken as given."""
+    cov3d (N, 6: xx, xy, xz, yy, yz, zz) the 3D covariance is taken as given.
+    A non-zero filter_variance f is the Mip-Splatting screen-space filter
+    (backend_mip_3dgs.py:63-102): Gaussians kept by the base cull get
+    cov2D + f I, their conic is its inverse and their radius
+    ceil(3 sqrt(lambda_max)) of the filtered covariance (floored at 0.1)."""
     V = view.reshape(16)
     P = proj.reshape(16)
     x, y, z = means.unbind(1)
@@ -104,8 +109,14 @@ def preprocess(means, scales, rots, view, proj, campos, tanfovx, tanfovy, W, H, 
     fx = W / (2.0 * tanfovx)
     fy = H / (2.0 * tanfovy)
     limx, limy = 1.3 * tanfovx, 1.3 * tanfovy
-    tx = torch.clamp(pv[:, 0] / vz, -limx, limx) * vz
-    ty = torch.clamp(pv[:, 1] / vz, -limy, limy) * vz
+    # A clamped camera-space coordinate is a constant for the gradient: the
+    # reference masks its gradient and differentiates the Jacobian in z as if
+    # it were fixed (backward_kernels.py:134-137, 212-214; 827-829).
+    rx, ry = pv[:, 0] / vz, pv[:, 1] / vz
+    tx = torch.clamp(rx, -limx, limx) * vz
+    ty = torch.clamp(ry, -limy, limy) * vz
+    tx = torch.where((rx < -limx) | (rx > limx), tx.detach(), tx)
+    ty = torch.where((ry < -limy) | (ry > limy), ty.detach(), ty)
     zero = torch.zeros_like(vz)
     J = torch.stack([torch.stack([fx / vz, zero, -fx * tx / (vz * vz)], -1),
                      torch.stack([zero, fy / vz, -fy * ty / (vz * vz)], -1)], -2)
@@ -132,6 +143,20 @@ def preprocess(means, scales, rots, view, proj, campos, tanfovx, tanfovy, W, H, 
         x0, y0, x1, y1 = tile_rect(pixd[i, 0], pixd[i, 1], r, gx, gy)
         if (x1 - x0) * (y1 - y0) > 0:
             radii[i] = r
+    if filter_variance != 0.0:
+        a = a + filter_variance
+        c = c + filter_variance
+        det = a * c - b * b
+        conic = torch.stack([c / det, -b / det, a / det], 1)
+        ad, cd, dd, bd = a.detach().numpy(), c.detach().numpy(), det.detach().numpy(), b.detach().numpy()
+        for i in range(n):
+            if radii[i] == 0:
+                continue
+            if not dd[i] > 1e-12:
+                radii[i] = 0
+                continue
+            lam = 0.5 * (ad[i] + cd[i]) + math.sqrt(max(0.25 * (ad[i] - cd[i]) ** 2 + bd[i] ** 2, 0.0))
+            radii[i] = int(math.ceil(3.0 * math.sqrt(max(lam, 0.1))))
 
     if colors is None:
         d = means - campos.reshape(1, 3)

@@ -42,7 +42,8 @@ def raster_inputs(scene: dict, *, colors: bool = False) -> _pipeline.RasterInput
         scene["scales"] if cov is None else empty, scene["rotations"] if cov is None else empty,
         float(scene.get("scale_modifier", 1.0)), empty if cov is None else cov, scene["viewmatrix"],
         scene["projmatrix"], scene["tanfovx"], scene["tanfovy"], scene["height"], scene["width"],
-        empty if colors else scene["shs"], scene["sh_degree"], scene["campos"], False)
+        empty if colors else scene["shs"], scene["sh_degree"], scene["campos"], False,
+        float(scene.get("filter_variance", 0.0)))
 
 
 def with_precomputed_covariance(scene: dict, seed: int = 5) -> dict:

@@ -305,6 +305,86 @@ def test_rotated_precomputed_covariance_matches_per_pixel_compositing(device):
     assert alpha.max() > 0.15
 
 
+def _mip_settings(device, bg, f, **extra):
+    from gswarp_amd.methods.mip_3dgs import MipGaussianRasterizationSettings
+    common = _settings(device, bg)._asdict()
+    common.update(extra)
+    return MipGaussianRasterizationSettings(**common, filter_variance=f)
+
+
+def _two_gaussian_inputs(device):
+    means = torch.tensor([[-0.15, 0.05, 2.0], [0.2, -0.1, 2.4]], device=device, requires_grad=True)
+    inputs = _inputs(device, means, scales=torch.tensor([[0.25, 0.1, 0.05], [0.12, 0.3, 0.2]], device=device))
+    inputs["rotations"] = torch.tensor([[0.9, 0.1, 0.0, 0.4], [1.0, 0.0, 0.2, 0.0]], device=device)
+    for key in ("colors_precomp", "opacities", "scales", "rotations"):
+        inputs[key] = inputs[key].clone().requires_grad_(True)
+    return inputs
+
+
+def test_mip_zero_filter_matches_baseline_and_filtered_gradients_are_finite(device):
+    """test_classic_variant_methods_cuda.py:144-162."""
+    from gswarp_amd.methods.mip_3dgs import rasterize_gaussians as rasterize_mip
+    bg = torch.tensor([0.05, 0.15, 0.25], device=device)
+
+    def loss(out):
+        return out[0].square().mean() + out[2].alpha.mean() + out[2].depth.mean()
+
+    base_in = _two_gaussian_inputs(device)
+    base = _std(device, base_in, _settings(device, bg))
+    loss(base).backward()
+    zero_in = _two_gaussian_inputs(device)
+    zero = rasterize_mip(*(zero_in[k] for k in ("means3D", "means2D", "sh", "colors_precomp", "opacities", "scales",
+                                                "rotations", "cov3Ds_precomp")), _mip_settings(device, bg, 0.0))
+    torch.testing.assert_close(zero[0], base[0], rtol=2e-5, atol=2e-5)
+    torch.testing.assert_close(zero[2].alpha, base[2].alpha, rtol=2e-5, atol=2e-5)
+    loss(zero).backward()
+    torch.testing.assert_close(zero_in["means3D"].grad, base_in["means3D"].grad, rtol=3e-4, atol=3e-5)
+    filt_in = _two_gaussian_inputs(device)
+    filt = rasterize_mip(*(filt_in[k] for k in ("means3D", "means2D", "sh", "colors_precomp", "opacities", "scales",
+                                                "rotations", "cov3Ds_precomp")), _mip_settings(device, bg, 0.25))
+    loss(filt).backward()
+    for name in ("means3D", "means2D", "colors_precomp", "opacities", "scales", "rotations"):
+        assert torch.isfinite(filt_in[name].grad).all(), name
+    # the filter only widens each footprint (every conic shrinks), so the
+    # accumulated alpha grows
+    assert float(filt[2].alpha.detach().sum()) > float(base[2].alpha.detach().sum())
+
+
+def test_mip_settings_are_validated(device):
+    from gswarp_amd.methods.mip_3dgs import MipGaussianRasterizer
+    bg = torch.zeros(3, device=device)
+    inputs = _inputs(device, torch.tensor([[0.0, 0.0, 2.0]], device=device))
+    for bad in (dict(f=-0.1), dict(f=float("inf")), dict(f=0.3, antialiasing=True)):
+        f = bad.pop("f")
+        rast = MipGaussianRasterizer(_mip_settings(device, bg, f, **bad))
+        with pytest.raises(ValueError):
+            rast(inputs["means3D"], inputs["means2D"], inputs["opacities"], colors_precomp=inputs["colors_precomp"],
+                 scales=inputs["scales"], rotations=inputs["rotations"])
+
+
+def test_mip_filter_conic_inverse_gradient_matches_finite_difference(device):
+    """The filter variance enters the backward's recomputed cov2D: the analytic
+    dL/dscale of sum(conic_2D_inv) under the filter matches central differences."""
+    from gswarp_amd.methods.mip_3dgs import rasterize_gaussians as rasterize_mip
+    bg = torch.zeros(3, device=device)
+    means = torch.tensor([[0.1, 0.0, 2.0]], device=device)
+
+    def loss_for(value, grad):
+        scales = torch.tensor([[value, 0.3, 0.2]], device=device, requires_grad=grad)
+        inp = _inputs(device, means, scales=scales)
+        out = rasterize_mip(*(inp[k] for k in ("means3D", "means2D", "sh", "colors_precomp", "opacities", "scales",
+                                               "rotations", "cov3Ds_precomp")), _mip_settings(device, bg, 0.5))
+        return out[2].conic_2D.sum(), scales
+
+    loss, scales = loss_for(0.5, True)
+    loss.backward()
+    analytic = scales.grad[0, 0].item()
+    eps = 1e-3
+    numeric = (loss_for(0.5 + eps, False)[0].item() - loss_for(0.5 - eps, False)[0].item()) / (2 * eps)
+    assert analytic != 0.0
+    assert abs(analytic - numeric) <= max(1e-4, abs(numeric) * 2e-2), (analytic, numeric)
+
+
 def test_colour_gradient_matches_finite_difference(device):
     """Central differences of sum(colour * W) through the GPU forward against
     the GPU backward, for the mean, scales and rotation of one Gaussian.  W is

@@ -195,3 +195,23 @@ def test_precomputed_covariance_coverage_modes_match_oracle(coverage_mode, devic
 def test_precomputed_covariance_backward_matches_oracle(case, flow_double, device):
     """dL/dcov3D from the chain of backward_ops.py:679-744 instead of scale / rotation."""
     _check_backward(with_precomputed_covariance(_scene(case, device)), flow_double=flow_double)
+
+
+@pytest.mark.parametrize("case,f,coverage_mode", [("c1_full", 0.3, 1), ("c2_small", 0.1, 1), ("c1_ragged", 2.0, 1),
+                                                   ("c1_full", 0.3, 0), ("c1_full", 0.3, 2)])
+def test_mip_filter_forward_matches_oracle(case, f, coverage_mode, device):
+    """Mip-Splatting filter variance (backend_mip_3dgs.py:63-102): filtered
+    conics, radii and recounted tiles, then every later stage, bit-exact."""
+    scene = dict(_scene(case, device), filter_variance=f)
+    _check_forward(scene, options(coverage_mode=coverage_mode), coverage_mode=coverage_mode)
+
+
+def test_mip_filter_with_precomputed_covariance_matches_oracle(device):
+    scene = dict(with_precomputed_covariance(_scene("c1_full", device)), filter_variance=0.3)
+    _check_forward(scene, options())
+    _check_backward(scene)
+
+
+@pytest.mark.parametrize("case", ["c1_full", "c2_small"])
+def test_mip_filter_backward_matches_oracle(case, device):
+    _check_backward(dict(_scene(case, device), filter_variance=0.3))

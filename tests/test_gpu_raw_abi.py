@@ -27,7 +27,7 @@ GRAD_NAMES = ("means2D", "colors", "opacities", "means3D", "cov3D", "sh", "scale
 
 def _raw_args(scene, colors=False):
     inputs = raster_inputs(scene, colors=colors)
-    return [getattr(inputs, f.name) for f in fields(_pipeline.RasterInputs)]
+    return [getattr(inputs, f.name) for f in fields(_pipeline.RasterInputs)][:18]
 
 
 def _upstream(scene, seed=3):

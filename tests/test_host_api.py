@@ -275,3 +275,22 @@ def test_bench_refuses_more_than_one_gpu():
     out = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
                          timeout=120)
     assert out.returncode == 2 and "one GPU" in out.stderr
+
+
+def test_mip_settings_defaults_and_filter_checks():
+    """gswarp/methods/mip_3dgs.py:29-48 defaults; the filter checks of
+    mip_3dgs.py:83-87 (antialiasing off, finite non-negative variance)."""
+    import math
+
+    from gswarp_amd.methods import mip_3dgs
+    import gswarp.methods.mip_3dgs as alias
+    assert alias.MipGaussianRasterizationSettings is mip_3dgs.MipGaussianRasterizationSettings
+    fields = mip_3dgs.MipGaussianRasterizationSettings._fields
+    assert fields[-1] == "filter_variance"
+    assert mip_3dgs.MipGaussianRasterizationSettings._field_defaults["filter_variance"] == 0.3
+    ok = mip_3dgs.MipGaussianRasterizationSettings(16, 16, 1.0, 1.0, None, 1.0, None, None, 0, None, False)
+    mip_3dgs._check_filter(ok)
+    for bad in (ok._replace(filter_variance=-1e-3), ok._replace(filter_variance=math.inf),
+                ok._replace(filter_variance=math.nan), ok._replace(antialiasing=True)):
+        with pytest.raises(ValueError):
+            mip_3dgs._check_filter(bad)

@@ -496,3 +496,114 @@ def test_precomputed_covariance_backward_matches_float64_autograd(seed):
         bad, worst = grad_mismatch(grads[name], expected)
         assert bad == 0, (name, worst)
         assert np.abs(expected).max() > 0
+
+
+# ---------------------------------------------------------------- Mip-Splatting filter variance
+
+def mip_scene(seed: int, f: float, n: int = 120, precomp: bool = False) -> dict:
+    s = tiny_scene(seed, n=n, spread=0.8)
+    s["filter_variance"] = f
+    if precomp:
+        s["cov3D_precomp"] = cov3d_of(s).astype(np.float32)
+        s.pop("scales")
+        s.pop("rotations")
+    return s
+
+
+def test_mip_filter_closed_form_on_axis():
+    """Identity camera and rotation, on-axis point: filtered cov2D =
+    (f/z)^2 s^2 + 0.3 + v on the diagonal, conic its inverse, and with the
+    discriminant zero the radius is ceil(3 sqrt(cov2D))."""
+    cam = identity_camera()
+    z, s, v = 2.0, 0.05, 1.0
+    means = np.array([[0.0, 0.0, z]], np.float32)
+    kw = dict(tanfovx=cam["tanfovx"], tanfovy=cam["tanfovy"], width=64, height=64,
+              colors=np.full((1, 3), 0.2, np.float32))
+    args = (means, np.full((1, 3), s, np.float32), np.array([[1, 0, 0, 0]], np.float32),
+            np.full((1, 1), 0.8, np.float32), cam["view"], cam["proj"], cam["campos"])
+    base = oracle.preprocess(*args, **kw)
+    pre = oracle.preprocess(*args, filter_variance=v, **kw)
+    var = (64 / 2.0 / z) ** 2 * s * s + 0.3 + v
+    np.testing.assert_allclose(pre["conic_2d_inv"][0], [var, 0.0, var], rtol=1e-5)
+    np.testing.assert_allclose(pre["conic_2d"][0], [1 / var, 0.0, 1 / var], rtol=1e-5)
+    assert pre["radii"][0] == math.ceil(3.0 * math.sqrt(var))
+    assert pre["radii"][0] > base["radii"][0]
+    assert pre["depths"][0] == base["depths"][0] and np.array_equal(pre["proj_2d"], base["proj_2d"])
+    # a point-like Gaussian: cov2D ~ 0.3 + v, radius ceil(3 sqrt(0.4)) = 2
+    tiny = oracle.preprocess(means, np.full((1, 3), 1e-4, np.float32), *args[2:], filter_variance=0.1, **kw)
+    assert tiny["radii"][0] == 2
+    # the 0.1 eigenvalue floor: precomputed cov3D with cov2D = -0.15 I before
+    # and -0.1 I after the filter (determinant 0.01, kept) gives radius
+    # ceil(3 sqrt(0.1)) = 1
+    v = -0.45 / (64 / 2.0 / z) ** 2
+    cov = np.array([[v, 0.0, 0.0, v, 0.0, v]], np.float32)
+    neg = oracle.preprocess(means, None, None, *args[3:], cov3d_precomp=cov, filter_variance=0.05, **kw)
+    np.testing.assert_allclose(neg["conic_2d_inv"][0], [-0.1, 0.0, -0.1], atol=1e-6)
+    assert neg["radii"][0] == 1
+
+
+def test_mip_zero_filter_is_the_base_path():
+    s = tiny_scene(3, n=80)
+    base = oracle.rasterize(s)
+    zero = oracle.rasterize({**s, "filter_variance": 0.0})
+    for key in ("radii", "conic_2d", "conic_2d_inv", "tiles_touched"):
+        assert np.array_equal(base["pre"][key], zero["pre"][key])
+    assert np.array_equal(base["fwd"]["color"], zero["fwd"]["color"])
+
+
+@pytest.mark.parametrize("seed,f", [(0, 0.3), (1, 0.1), (2, 2.0)])
+def test_mip_filter_matches_float64_restatement(seed, f):
+    s = mip_scene(seed, f, n=200)
+    res = oracle.rasterize(s)
+    op = res["pre"]
+    leaves = {k: t64(s[k]) for k in ("means3D", "scales", "rotations", "shs")}
+    pre = dense_ref.preprocess(leaves["means3D"], leaves["scales"], leaves["rotations"], t64(s["viewmatrix"]),
+                               t64(s["projmatrix"]), t64(s["campos"]), s["tanfovx"], s["tanfovy"], s["width"],
+                               s["height"], shs=leaves["shs"], degree=s["sh_degree"], filter_variance=f)
+    a, b, c = (pre["cov2d"][:, i].numpy() for i in range(3))
+    lam = 0.5 * (a + c) + np.sqrt(np.maximum(0.25 * (a - c) ** 2 + b * b, 0.0))
+    r3 = 3.0 * np.sqrt(np.maximum(lam, 0.1))
+    near_int = np.abs(r3 - np.round(r3)) < 1e-4
+    assert np.array_equal(op["radii"][~near_int], pre["radii"][~near_int])
+    v = (op["radii"] > 0) & (pre["radii"] > 0)
+    assert v.sum() > 50
+    np.testing.assert_allclose(op["conic_2d_inv"][v], pre["cov2d"].numpy()[v], rtol=2e-5, atol=1e-6)
+    np.testing.assert_allclose(op["conic_2d"][v], pre["conic"].numpy()[v], rtol=1e-4, atol=1e-7)
+    # tile counts are recounted from the filtered values
+    gx, gy = oracle.grid_dims(s["width"], s["height"])
+    recount = oracle.count_covered_tiles(op["proj_2d"], op["conic_2d_inv"], op["conic_opacity"], op["radii"],
+                                         gx, gy, 1)
+    assert np.array_equal(recount, op["tiles_touched"])
+    base = oracle.rasterize({k: val for k, val in s.items() if k != "filter_variance"})
+    assert (op["tiles_touched"] > base["pre"]["tiles_touched"]).sum() > 5
+
+
+@pytest.mark.parametrize("seed,precomp", [(0, False), (5, False), (1, True)])
+def test_mip_filter_backward_matches_float64_autograd(seed, precomp):
+    f = 0.3
+    s = mip_scene(seed, f, n=50, precomp=precomp)
+    res = oracle.rasterize(s)
+    g = torch.Generator().manual_seed(300 + seed)
+    H, W = s["height"], s["width"]
+    gc = torch.randn(3, H, W, generator=g, dtype=torch.float64)
+    gd = torch.randn(1, H, W, generator=g, dtype=torch.float64)
+    ga = torch.randn(1, H, W, generator=g, dtype=torch.float64)
+    grads = oracle.rasterize_backward(s, res, gc.numpy().astype(np.float32), gd.numpy().astype(np.float32),
+                                      ga.numpy().astype(np.float32))
+    names = ("means3D", "opacities", "shs") + (("cov3D_precomp",) if precomp else ("scales", "rotations"))
+    leaves = {k: t64(s[k]).requires_grad_(True) for k in names}
+    pre = dense_ref.preprocess(leaves["means3D"], leaves.get("scales"), leaves.get("rotations"),
+                               t64(s["viewmatrix"]), t64(s["projmatrix"]), t64(s["campos"]), s["tanfovx"],
+                               s["tanfovy"], W, H, shs=leaves["shs"], degree=s["sh_degree"],
+                               cov3d=leaves.get("cov3D_precomp"), filter_variance=f)
+    n = s["means3D"].shape[0]
+    out = dense_ref.render(pre["pix"], pre["conic"], leaves["opacities"][:, 0], pre["rgb"], pre["depth"],
+                           res["pre"]["radii"], tile_sets_of(res, n, W), W, H, t64(s["bg"]))
+    np.testing.assert_allclose(res["fwd"]["color"], out["color"].detach().numpy(), atol=2e-4)
+    ((out["color"] * gc).sum() + (out["alpha"] * ga).sum() + (out["depth"] * gd).sum()).backward()
+    key_of = {"cov3D_precomp": "cov3D", "shs": "sh"}
+    for name in names:
+        expected = leaves[name].grad.numpy()
+        bad, worst = grad_mismatch(grads[key_of.get(name, name)], expected)
+        assert bad == 0, (name, worst)
+        assert np.abs(expected).max() > 0
