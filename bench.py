@@ -143,7 +143,7 @@ def measure_copy_bandwidth(device, nbytes: int = 1 << 30, reps: int = 5) -> floa
 STAGE_OF_KERNEL = (
     ("gs::preprocess_fwd_kernel", "preprocess"),
     ("gs::scan_", "scan"),
-    ("gs::zero_i64_kernel", "scan"),
+    ("gs::zero_info_kernel", "scan"),
     ("gs::depth_keys_kernel", "depth_sort"),
     ("gs::duplicate_keys_kernel", "duplicate"),
     ("gs::duplicate_tiles_kernel", "duplicate"),
@@ -238,6 +238,22 @@ def summarize_sq(counter_csv: str, out_path: str) -> None:
     print("\n".join(lines))
 
 
+def summarize_stats(stats_csv: str, out_path: str, header: str = "") -> None:
+    """rocprofv3 --kernel-trace --stats kernel_stats.csv -> calls, average / min /
+    max duration (us), share of GPU time and name of each kernel, longest first."""
+    import csv
+
+    rows = list(csv.DictReader(open(stats_csv)))
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    lines = [line for line in header.split("\n") if line] if header else []
+    lines.append("# columns: calls, average us, min us, max us, share of GPU time, kernel")
+    for r in rows:
+        lines.append(f"{int(r['Calls']):5d} {float(r['AverageNs']) / 1e3:10.1f} {float(r['MinNs']) / 1e3:10.1f} "
+                     f"{float(r['MaxNs']) / 1e3:10.1f} {float(r['Percentage']):6.2f}%  {r['Name'][:110]}")
+    Path(out_path).write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def cpu_baseline(scene, grads) -> dict:
     """One fwd+bwd of the same scene with the C oracle on this host's cores."""
     import oracle
@@ -279,7 +295,12 @@ def main() -> int:
                         help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) into OUT and exit")
     parser.add_argument("--sq-summary", nargs=2, metavar=("COUNTER_CSV", "OUT"),
                         help="summarise one rocprofv3 --pmc run of SQ counters into OUT and exit")
+    parser.add_argument("--stats-summary", nargs=2, metavar=("KERNEL_STATS_CSV", "OUT"),
+                        help="summarise one rocprofv3 --kernel-trace --stats run into OUT and exit")
     args = parser.parse_args()
+    if args.stats_summary:
+        summarize_stats(*args.stats_summary)
+        return 0
     if args.sq_summary:
         summarize_sq(*args.sq_summary)
         return 0

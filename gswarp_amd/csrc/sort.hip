@@ -51,8 +51,17 @@ __device__ __forceinline__ unsigned block_exclusive_scan_u32(unsigned v, unsigne
   return wave_off + inc - v;
 }
 
+// Digit of a pass: bits [shift, shift + 8) of the key, restricted by dmask to
+// the sorted field in the last pass (bits above the field take no part).
 template <typename K>
-__device__ __forceinline__ unsigned digit_of(K key, int shift) { return (unsigned)(key >> shift) & (kRadix - 1); }
+__device__ __forceinline__ unsigned digit_of(K key, int shift, unsigned dmask) {
+  return (unsigned)(key >> shift) & dmask;
+}
+
+static inline unsigned pass_digit_mask(int key_bits, int pass) {
+  const int bits = key_bits - 8 * pass;
+  return bits >= 8 ? 0xFFu : ((1u << bits) - 1u);
+}
 
 // Lanes of the wave holding the same digit d as this lane (among valid lanes).
 // Per bit b: s = bit b of d sign-extended (0 or ~0, one v_bfe_i32), m = ballot
@@ -82,7 +91,7 @@ constexpr int kCopyStride = kRadix + 1;
 
 template <typename K>
 __global__ __launch_bounds__(kThreads) void upsweep_kernel(const K* __restrict__ keys, long long n, int shift,
-                                                          int nb, unsigned* __restrict__ hist) {
+                                                          unsigned dmask, int nb, unsigned* __restrict__ hist) {
   __shared__ unsigned h[kCopies * kCopyStride];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -98,7 +107,7 @@ __global__ __launch_bounds__(kThreads) void upsweep_kernel(const K* __restrict__
   unsigned* mine = h + (lane & (kCopies - 1)) * kCopyStride;
 #pragma unroll
   for (int i = 0; i < kItems; ++i)
-    if (base + i * 64 < n) atomicAdd(mine + digit_of(key[i], shift), 1u);
+    if (base + i * 64 < n) atomicAdd(mine + digit_of(key[i], shift, dmask), 1u);
   __syncthreads();
   const int d = threadIdx.x;
   unsigned c = 0;
@@ -148,7 +157,7 @@ template <typename K, bool kValues>
 __global__ __launch_bounds__(kThreads) void downsweep_kernel(const K* __restrict__ keys_in,
                                                             const int* __restrict__ vals_in,
                                                             K* __restrict__ keys_out, int* __restrict__ vals_out,
-                                                            long long n, int shift, int nb,
+                                                            long long n, int shift, unsigned dmask, int nb,
                                                             const unsigned* __restrict__ hist,
                                                             const unsigned* __restrict__ digit_totals) {
   __shared__ K s_keys[kTile];
@@ -183,7 +192,7 @@ __global__ __launch_bounds__(kThreads) void downsweep_kernel(const K* __restrict
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     const bool valid = (wave_base + i * 64) < n;
-    const unsigned d = digit_of(key[i], shift);
+    const unsigned d = digit_of(key[i], shift, dmask);
     const u64 peers = match_digit(d, valid);
     unsigned before = 0;
     if (valid) before = s_wcount[wave][d];
@@ -219,7 +228,7 @@ __global__ __launch_bounds__(kThreads) void downsweep_kernel(const K* __restrict
   for (int i = 0; i < kItems; ++i) {
     const bool valid = (wave_base + i * 64) < n;
     if (valid) {
-      const unsigned d = digit_of(key[i], shift);
+      const unsigned d = digit_of(key[i], shift, dmask);
       const unsigned lp = s_dstart[d] + s_wcount[wave][d] + rank[i];
       s_keys[lp] = key[i];
       if (kValues) s_vals[lp] = val[i];
@@ -232,7 +241,7 @@ __global__ __launch_bounds__(kThreads) void downsweep_kernel(const K* __restrict
     const int p = j * kThreads + threadIdx.x;
     if (p < block_count) {
       const K k = s_keys[p];
-      const long long gp = s_gbase[digit_of(k, shift)] + p;
+      const long long gp = s_gbase[digit_of(k, shift, dmask)] + p;
       if (gp >= 0 && gp < n) {  // always true for a consistent histogram
         keys_out[gp] = k;
         if (kValues) vals_out[gp] = s_vals[p];
@@ -273,10 +282,12 @@ static int gs_sort::sort_impl(int64_t n, int32_t lo_bit, int32_t key_bits, K* ki
   const int passes = gs_passes_for_bits(key_bits);
   for (int pass = 0; pass < passes; ++pass) {
     const int shift = lo_bit + pass * 8;
-    hipLaunchKernelGGL((upsweep_kernel<K>), dim3(nb), dim3(kThreads), 0, s, kin, (long long)n, shift, nb, hist);
+    const unsigned dmask = pass_digit_mask(key_bits, pass);
+    hipLaunchKernelGGL((upsweep_kernel<K>), dim3(nb), dim3(kThreads), 0, s, kin, (long long)n, shift, dmask, nb,
+                       hist);
     hipLaunchKernelGGL(rowscan_kernel, dim3(kRadix / kWaves), dim3(kThreads), 0, s, nb, hist, digit_totals);
     hipLaunchKernelGGL((downsweep_kernel<K, kValues>), dim3(nb), dim3(kThreads), 0, s, kin, vin, kout, vout,
-                       (long long)n, shift, nb, hist, digit_totals);
+                       (long long)n, shift, dmask, nb, hist, digit_totals);
     K* tk = kin;
     kin = kout;
     kout = tk;
