@@ -127,14 +127,28 @@ __device__ __forceinline__ BwdBatch load_bwd_batch(const RenderBwdParams& p, int
 
 // 4/kPix independent wave64 workgroups per tile, lane l owning the kPix
 // pixels of column l % 16 in rows l / 16 + 4k (k < kPix) of its slice (the
-// forward's layout).  Per Gaussian, each
-// lane first sums its pixels' contributions, using the factorisation
+// forward's layout).
+//
+// Per pixel the reverse blend keeps two running values: T, the transmittance
+// in front of the current Gaussian, and S = U . acc, the upstream gradient
+// U = (dL/dr, dL/dg, dL/db, dL/ddepth, dL/dalpha) dotted with the
+// accumulated features behind it, acc = (colour, depth, alpha) of everything
+// behind, each Gaussian adding F = (r, g, b, depth, 1) as
+//   acc <- alpha F + (1 - alpha) acc   =>   S <- alpha (F.U) + (1 - alpha) S.
+// The reference's per-channel sum  sum_ch (F_ch - acc_ch) U_ch  is F.U - S,
+// and its background term -T_final / (1 - alpha) (bg . dL/dcolour) is the
+// same recurrence started from S = bg . dL/dcolour instead of 0 (the
+// background is an opaque layer behind the last Gaussian; 1 - alpha >= 0.01
+// since alpha <= 0.99, so the 1e-5 floor never applies to it).  Per
+// Gaussian each lane then sums its pixels' contributions, using
 //   v = G * dL/dalpha_hat per pixel,
 //   dL/dxy    = -(W/2, H/2) * o * (a dx sum(v) + b sum(v dy), c sum(v dy) + b dx sum(v)),
 //   dL/dconic = -1/2 * o * (dx^2 sum(v), dx sum(v dy), sum(v dy^2)),
 //   dL/dopacity = sum(v),
-// which is the reference's per-pixel expression summed over pixels sharing
-// dx; then the ten per-lane components are summed over the wave.
+// the reference's per-pixel expressions summed over pixels sharing dx; then
+// the ten per-lane components are summed over the wave.  Each batch of 64
+// records is first tested lane-parallel against the slice rectangle
+// (record_may_touch) and only records that may touch it are visited.
 template <bool kDepth, int kPix>
 __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
   constexpr int kSubs = 4 / kPix;
@@ -145,8 +159,10 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
   const int tile = ts.x;
   const int tx = tile % p.grid_x;
   const int ty = tile / p.grid_x;
-  const int px = tx * kBlockX + (lane & 15);
-  const int py0 = ty * kBlockY + ts.y * 4 * kPix + (lane >> 4);
+  const int sx0 = tx * kBlockX;
+  const int sy0 = ty * kBlockY + ts.y * 4 * kPix;
+  const int px = sx0 + (lane & 15);
+  const int py0 = sy0 + (lane >> 4);
   const int P = p.W * p.H;
   const float pfx = (float)px;
   int2 rg = p.ranges[tile];
@@ -154,11 +170,7 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
   rg.y = imax(rg.x, imin(rg.y, p.num_rendered));
   const int n = rg.y - rg.x;
 
-  // Per pixel: T (reconstructed transmittance), the forward's final T, the
-  // upstream gradients, and the colour / depth / alpha accumulated behind
-  // the current Gaussian (acc*, updated as soon as a Gaussian is blended).
-  float pfy[kPix], T[kPix], tfb[kPix], gp0[kPix], gp1[kPix], gp2[kPix], gpd[kPix], gpa[kPix];
-  float acc0[kPix], acc1[kPix], acc2[kPix], accd[kPix], acca[kPix];
+  float pfy[kPix], T[kPix], S[kPix], gp0[kPix], gp1[kPix], gp2[kPix], gpd[kPix], gpa[kPix];
   int last[kPix];
   int lmax = 0;
 #pragma unroll
@@ -166,20 +178,17 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
     const int py = py0 + 4 * k;
     pfy[k] = (float)py;
     last[k] = 0;
-    T[k] = tfb[k] = gp0[k] = gp1[k] = gp2[k] = gpd[k] = gpa[k] = 0.0f;
-    acc0[k] = acc1[k] = acc2[k] = accd[k] = acca[k] = 0.0f;
+    T[k] = S[k] = gp0[k] = gp1[k] = gp2[k] = gpd[k] = gpa[k] = 0.0f;
     if (px < p.W && py < p.H && n > 0) {
       const int pix = py * p.W + px;
       last[k] = imax(0, imin(p.n_contrib[pix], n));
-      const float Tf = 1.0f - p.out_alpha[pix];
-      T[k] = Tf;
+      T[k] = 1.0f - p.out_alpha[pix];
       gp0[k] = p.grad_color[pix];
       gp1[k] = p.grad_color[P + pix];
       gp2[k] = p.grad_color[2 * P + pix];
       if (kDepth) gpd[k] = p.grad_depth[pix];
       gpa[k] = p.grad_alpha[pix];
-      // background term of dL/dalpha: -T_final / (1 - alpha) * (bg . dL/dcolor)
-      tfb[k] = -Tf * (p.bg[0] * gp0[k] + p.bg[1] * gp1[k] + p.bg[2] * gp2[k]);
+      S[k] = fmaf(p.bg[2], gp2[k], fmaf(p.bg[1], gp1[k], p.bg[0] * gp0[k]));
     }
     lmax = imax(lmax, last[k]);
   }
@@ -187,6 +196,8 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
   if (max_lc == 0) return;
   const float half_w = 0.5f * (float)p.W;
   const float half_h = 0.5f * (float)p.H;
+  const float rx0 = (float)sx0, rx1 = (float)(sx0 + kBlockX - 1);
+  const float ry0 = (float)sy0, ry1 = (float)(sy0 + 4 * kPix - 1);
 
   int bs = imax(0, max_lc - 64);
   BwdBatch next = load_bwd_batch(p, rg.x + bs, max_lc - bs, lane);
@@ -198,11 +209,14 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
     s_r1[lane] = next.r1;
     s_r2[lane] = next.r2;
     s_id[lane] = next.id;
+    uint64_t todo = __ballot(lane < cnt && record_may_touch(next.r0, next.r1, rx0, rx1, ry0, ry1));
     if (bs > 0) {
       const int nbs = imax(0, bs - 64);
       next = load_bwd_batch(p, rg.x + nbs, bs - nbs, lane);
     }
-    for (int jj = cnt - 1; jj >= 0; --jj) {
+    while (todo != 0) {
+      const int jj = 63 - __builtin_clzll(todo);
+      todo ^= 1ull << jj;
       const int pos = bs + jj;
       const float4 a = s_r0[jj];
       const float4 b = s_r1[jj];
@@ -217,68 +231,68 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
         dy[k] = a.y - pfy[k];
         pw[k] = -0.5f * (adxx + b.x * dy[k] * dy[k]) - bdx * dy[k];
         cand[k] = pos < last[k] && pw[k] <= 0.0f && pw[k] >= b.w;
-        any = any || cand[k];
+        any |= cand[k];
       }
       if (__ballot(any) == 0) continue;
       // Blend decisions, identical to the forward's: above cutoff + 2e-3 the
       // forward's alpha is provably >= 1/255 (the cutoff sits 1e-3 below
       // -ln(255 o) and exp_sw / log_sw err by < 1e-6 relative), below the
       // cutoff provably < 1/255; only the thin band between needs exp_sw.
-      bool ok[kPix];
+      // e = log2 of the Gaussian value G for pixels that blend, -inf (G = 0)
+      // for the others.
+      const float sure = b.w + kSureMargin;
+      float e[kPix];
       bool band_any = false;
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
-        ok[k] = cand[k] && pw[k] >= b.w + kSureMargin;
-        band_any = band_any || (cand[k] && !ok[k]);
+        e[k] = (cand[k] && pw[k] >= sure) ? pw[k] * kLog2e : -__builtin_inff();
+        band_any |= cand[k] && pw[k] < sure;
       }
       if (__ballot(band_any) != 0) {
 #pragma unroll
         for (int k = 0; k < kPix; ++k) {
-          const bool band = cand[k] && !ok[k];
+          const bool band = cand[k] && pw[k] < sure;
           const float a_sw = fminr(kAlphaMax, b.y * exp_sw_nonpos(band ? pw[k] : 0.0f));
-          ok[k] = ok[k] || (band && a_sw >= kAlphaMin);
+          e[k] = (band && a_sw >= kAlphaMin) ? pw[k] * kLog2e : e[k];
         }
       }
-      bool any_ok = false;
-#pragma unroll
-      for (int k = 0; k < kPix; ++k) any_ok = any_ok || ok[k];
-      if (__ballot(any_ok) == 0) continue;
       const float4 f = s_r2[jj];
-      float sv = 0.0f, svy = 0.0f, svyy = 0.0f, sr = 0.0f, sg = 0.0f, sb = 0.0f, sd = 0.0f;
+      float sv, svy, svyy, sr, sg, sb, sd;
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
         // Gradient values use the hardware exponential (v_exp_f32): they only
         // need the 1e-3 gradient tolerance, the decisions above are exact.
         // A pixel that does not blend this Gaussian gets G = 2^-inf = 0, so
-        // alpha = 0, T * rcp(1) = T and every update below leaves its state
-        // unchanged, with no per-pixel selects.
-        const float G = __builtin_amdgcn_exp2f(ok[k] ? pw[k] * kLog2e : -__builtin_inff());
-        const float alpha = fminr(kAlphaMax, b.y * G);
-        const float inv = __builtin_amdgcn_rcpf(fmaxr(1.0f - alpha, kOneMinusAlphaMin));
-        const float Tn = T[k] * inv;
-        const float dch = alpha * Tn;
-        float dL_dopa = fmaf(f.x - acc0[k], gp0[k], fmaf(f.y - acc1[k], gp1[k], (f.z - acc2[k]) * gp2[k]));
+        // alpha = 0, T * rcp(1) = T, S is unchanged and it adds exact zeros.
+        const float G = __builtin_amdgcn_exp2f(e[k]);
+        const float alpha = fminf(kAlphaMax, b.y * G);
         const float oma = 1.0f - alpha;
-        if (kDepth) {
-          dL_dopa = fmaf(b.z - accd[k], gpd[k], dL_dopa);
-          accd[k] = fmaf(alpha, b.z, oma * accd[k]);
-          sd = fmaf(dch, gpd[k], sd);
+        const float Tn = T[k] * __builtin_amdgcn_rcpf(fmaxr(oma, kOneMinusAlphaMin));
+        float fu = fmaf(f.z, gp2[k], fmaf(f.y, gp1[k], fmaf(f.x, gp0[k], gpa[k])));
+        if (kDepth) fu = fmaf(b.z, gpd[k], fu);
+        const float v = G * (Tn * (fu - S[k]));
+        const float dch = alpha * Tn;
+        const float vdy = v * dy[k];
+        if (k == 0) {
+          sv = v;
+          svy = vdy;
+          svyy = vdy * dy[k];
+          sr = dch * gp0[k];
+          sg = dch * gp1[k];
+          sb = dch * gp2[k];
+          sd = kDepth ? dch * gpd[k] : 0.0f;
+        } else {
+          sv += v;
+          svy += vdy;
+          svyy = fmaf(vdy, dy[k], svyy);
+          sr = fmaf(dch, gp0[k], sr);
+          sg = fmaf(dch, gp1[k], sg);
+          sb = fmaf(dch, gp2[k], sb);
+          if (kDepth) sd = fmaf(dch, gpd[k], sd);
         }
-        dL_dopa = fmaf(1.0f - acca[k], gpa[k], dL_dopa);
-        dL_dopa = fmaf(dL_dopa, Tn, tfb[k] * inv);
-        const float v = G * dL_dopa;
-        sv += v;
-        svy = fmaf(v, dy[k], svy);
-        svyy = fmaf(v * dy[k], dy[k], svyy);
-        sr = fmaf(dch, gp0[k], sr);
-        sg = fmaf(dch, gp1[k], sg);
-        sb = fmaf(dch, gp2[k], sb);
         // this Gaussian joins what lies behind the next (nearer) one
+        S[k] = fmaf(alpha, fu, oma * S[k]);
         T[k] = Tn;
-        acc0[k] = fmaf(alpha, f.x, oma * acc0[k]);
-        acc1[k] = fmaf(alpha, f.y, oma * acc1[k]);
-        acc2[k] = fmaf(alpha, f.z, oma * acc2[k]);
-        acca[k] = fmaf(oma, acca[k], alpha);
       }
       const float s = b.y * sv, sy = b.y * svy, syy = b.y * svyy;
       float g[kGradFloats];

@@ -166,6 +166,33 @@ __device__ __forceinline__ float power_cutoff(float opacity) {
   return fmaxr(-log_sw(o255) - 1.0e-3f, -87.0f);
 }
 
+// Whether a render record can pass the blend loops' candidate test
+// power_cutoff <= power <= 0 at any pixel centre of the rectangle
+// [x0, x1] x [y0, y1].  The candidate set is the ellipse
+//   Q(d) = a dx^2 + 2 b dx dy + c dy^2 <= q,  q = -2 * power_cutoff,
+// whose bounding box has half-widths sqrt(q c / det) and sqrt(q a / det),
+// det = a c - b^2.  The loops evaluate the exponent in fp32: each of its
+// three terms carries a few ulp of relative error, and inside the box every
+// term is at most q * (a c / det), so the fp32 exponent can pass the test
+// only where the exact Q <= q (1 + 4 * 2^-24 * 3 * ac/det).  The box below
+// is computed in double (a c and b^2 are exact there) for q inflated ten
+// times that bound, plus 0.02 px; conics that are not positive definite or
+// so elongated (ac/det >= 1e5) that the bound is weak are never culled.
+// Returning true is always safe: it only costs the per-pixel test.
+__device__ __forceinline__ bool record_may_touch(float4 r0, float4 r1, float x0, float x1, float y0, float y1) {
+  const float cutoff = r1.w;
+  if (cutoff > 0.0f) return false;  // alpha < 1/255 at every exponent <= 0
+  const double a = r0.z, b = r0.w, c = r1.x;
+  const double ac = a * c;
+  const double det = ac - b * b;
+  if (!(a > 0.0 && c > 0.0 && det > 0.0 && ac < 1.0e5 * det)) return true;
+  const double q = -2.0 * (double)cutoff * (1.0 + 8.0e-6 * (ac / det)) + 1.0e-6;
+  const double ex = sqrt(q * c / det) + 0.02;
+  const double ey = sqrt(q * a / det) + 0.02;
+  const double gx = r0.x, gy = r0.y;
+  return !(gx + ex < (double)x0 || gx - ex > (double)x1 || gy + ey < (double)y0 || gy - ey > (double)y1);
+}
+
 // Workgroups are dispatched round-robin over the eight XCDs (each with its
 // own L2).  Mapping workgroup b to tile start(b % 8) + b / 8 gives every XCD
 // one contiguous band of tiles, so neighbouring tiles, which share most of

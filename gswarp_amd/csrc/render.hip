@@ -6,7 +6,9 @@
 // sorted Gaussians are fetched 64 at a time, one packed 48-byte record per
 // lane, with the next batch prefetched into registers while the current one
 // is blended from a per-wave LDS slot (one broadcast ds_read_b128 per record
-// quarter; no barriers since each workgroup is one wave).  Per Gaussian the
+// quarter; no barriers since each workgroup is one wave).  Each batch is
+// first tested lane-parallel against the slice rectangle (record_may_touch)
+// and only records that may touch the slice are visited.  Per Gaussian the
 // per-pixel work is branch-free (select-based updates inside one wave-uniform
 // "any candidate" branch) so the pixels' exponential chains interleave.  A
 // wave-wide ballot ends the slice once every one of its pixels is done.
@@ -79,10 +81,14 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
   const int tile = ts.x;
   const int tx = tile % p.grid_x;
   const int ty = tile / p.grid_x;
-  const int px = tx * kBlockX + (lane & 15);
-  const int py0 = ty * kBlockY + ts.y * 4 * kPixPerLane + (lane >> 4);
+  const int sx0 = tx * kBlockX;
+  const int sy0 = ty * kBlockY + ts.y * 4 * kPixPerLane;
+  const int px = sx0 + (lane & 15);
+  const int py0 = sy0 + (lane >> 4);
   const int P = p.W * p.H;
   const float pfx = (float)px;
+  const float rx0 = (float)sx0, rx1 = (float)(sx0 + kBlockX - 1);
+  const float ry0 = (float)sy0, ry1 = (float)(sy0 + 4 * kPixPerLane - 1);
   int2 rg = p.ranges[tile];
   rg.x = imax(0, imin(rg.x, p.num_rendered));
   rg.y = imax(rg.x, imin(rg.y, p.num_rendered));
@@ -118,8 +124,11 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
     s_r1[lane] = next.r1;
     s_r2[lane] = next.r2;
     if (kFlow) s_id[lane] = next.id;
+    uint64_t todo = __ballot(lane < cnt && record_may_touch(next.r0, next.r1, rx0, rx1, ry0, ry1));
     if (base + 64 < n) next = load_batch(p, rg.x + base + 64, imin(64, n - base - 64), lane);
-    for (int j = 0; j < cnt; ++j) {
+    while (todo != 0) {
+      const int j = __builtin_ctzll(todo);
+      todo &= todo - 1;
       const float4 a = s_r0[j];
       const float4 b = s_r1[j];
       const float dx = a.x - pfx;
@@ -133,7 +142,7 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
         dy[k] = a.y - pfy[k];
         pw[k] = -0.5f * (adxx + b.x * dy[k] * dy[k]) - bdx * dy[k];
         cand[k] = T[k] > 0.0f && pw[k] <= 0.0f && pw[k] >= b.w;
-        any = any || cand[k];
+        any |= cand[k];
       }
       if (__ballot(any) == 0) continue;
       const float4 f = s_r2[j];
