@@ -52,6 +52,7 @@ SIGNATURES = {
     "gs_sort_pairs_u32": (ctypes.c_int, [_i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "gs_tile_ranges": (ctypes.c_int, [_i64, _vp, _i32, _i32, _i32, _vp, _vp, _vp]),
     "gs_tile_ranges_u32": (ctypes.c_int, [_i64, _vp, _i32, _vp, _vp]),
+    "gs_sort_tile_segments": (ctypes.c_int, [_i64, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _i32, _vp]),
     "gs_render_fwd": (ctypes.c_int, [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
     "gs_render_fwd_flow": (
         ctypes.c_int,

@@ -222,6 +222,11 @@ def key_layout(P: int, T: int, depth_min: int, depth_max: int) -> KeyLayout:
     return KeyLayout(depth_min=depth_min, depth_bits=depth_bits, value_bits=value_bits)
 
 
+# How the packed-key dataflow orders its pairs: "segmented" sorts the keys
+# stably by the tile field only and then each tile's segment by depth on chip
+# (gs_sort_tile_segments); "full" runs the radix sort over tile and depth bits.
+PACKED_SORT = "segmented"
+
 # Above this many pairs per Gaussian the default mode sorts Gaussians by depth
 # and then pairs by tile (two short sorts) instead of one 64-bit key per pair.
 DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN = 4
@@ -379,8 +384,30 @@ def _binning_packed(pre: PreprocessOutputs, image_width: int, image_height: int,
         lib.call("gs_duplicate_keys", P, pre.radii.data_ptr(), pre.records.data_ptr(),
                  pre.conic_2d_inv.data_ptr(), offsets.data_ptr(), image_width, image_height, pre.coverage_mode, R,
                  layout.depth_min, layout.depth_bits, layout.value_bits, keys.data_ptr(), _lib.ptr(vals), stream)
-    sort_bits = (T - 1).bit_length() + layout.depth_bits
+    tile_bits = (T - 1).bit_length()
     sort_scratch = torch.empty((max(int(lib.gs_sort_scratch_bytes(R)), 1),), dtype=torch.uint8, device=device)
+    if ranges is None:
+        ranges = torch.empty((T, 2), dtype=torch.int32, device=device)
+    if packed and PACKED_SORT == "segmented":
+        # Stable sort on the tile field only, then each tile's segment (in point
+        # order) sorted stably by its depth field on chip.
+        passes = int(lib.gs_sort_num_passes(tile_bits))
+        _note("sort_passes", passes)
+        with _stage("sort"):
+            lib.call("gs_sort_keys_u64", R, layout.tile_shift, tile_bits, keys.data_ptr(), keys_alt.data_ptr(),
+                     sort_scratch.data_ptr(), sort_scratch.numel(), stream)
+        if passes % 2:
+            keys, keys_alt = keys_alt, keys
+        with _stage("ranges"):
+            lib.call("gs_tile_ranges", R, keys.data_ptr(), layout.tile_shift, 0, T, ranges.data_ptr(), None, stream)
+        if point_list is None:
+            point_list = torch.empty((R,), dtype=torch.int32, device=device)
+        with _stage("sort"):
+            lib.call("gs_sort_tile_segments", R, keys.data_ptr(), keys_alt.data_ptr(), T, ranges.data_ptr(),
+                     layout.value_bits, layout.depth_bits, layout.value_bits, point_list.data_ptr(),
+                     int(bool(keep_keys)), stream)
+        return BinningState(grid_x, grid_y, point_list, ranges, R, keys if keep_keys else None, layout)
+    sort_bits = tile_bits + layout.depth_bits
     _note("sort_passes", int(lib.gs_sort_num_passes(sort_bits)))
     with _stage("sort"):
         if packed:
@@ -395,8 +422,6 @@ def _binning_packed(pre: PreprocessOutputs, image_width: int, image_height: int,
         point_list = vals
     elif point_list is None:
         point_list = torch.empty((R,), dtype=torch.int32, device=device)
-    if ranges is None:
-        ranges = torch.empty((T, 2), dtype=torch.int32, device=device)
     with _stage("ranges"):
         lib.call("gs_tile_ranges", R, keys.data_ptr(), layout.tile_shift, layout.value_bits, T, ranges.data_ptr(),
                  point_list.data_ptr() if packed else None, stream)

@@ -319,3 +319,360 @@ extern "C" int gs_sort_pairs_u32(int64_t n, int32_t lo_bit, int32_t key_bits, ui
   return gs_sort::sort_impl<unsigned, true>(n, lo_bit, key_bits, keys, keys_alt, values, values_alt, scratch,
                                             scratch_bytes, (hipStream_t)stream);
 }
+
+// ---------------------------------------------------------------------------
+// Per-tile segment sort.  After the packed (tile, depth, point) keys have been
+// sorted stably by their tile field alone, each tile's keys are contiguous and
+// still in point order.  One 256-thread workgroup per tile then sorts its
+// segment stably by the depth field [lo_bit, lo_bit + key_bits) with 8-bit LSD
+// passes, which yields the (depth, point) order of a full key sort, and writes
+// point_list = the low value_bits of each key (and, on request, the sorted keys
+// back in place).
+//
+// Segments of up to kSmallCap keys are sorted by one wave each
+// (segment_sort_small_kernel); longer ones by a 256-thread workgroup
+// (segment_sort_kernel).  There, segments of up to kCap keys are sorted on
+// chip: each thread holds up to
+// kSlots keys in registers, ranks them with the same ballot-matched stable
+// ranking as the downsweep above, scatters them into one LDS buffer and
+// reloads them in element order for the next pass.  Longer segments are
+// sorted through global memory, ping-ponging between their ranges of keys and
+// keys_alt: a counting pass per digit, then chunks of kCap keys ranked on chip
+// and scattered behind the running digit offsets.
+namespace gs_seg {
+
+using gs_sort::u64;
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kSlots = 8;
+constexpr int kCap = kThreads * kSlots;  // 2048 keys
+constexpr int kRadix = 256;
+
+struct Shared {
+  u64 buf[kCap];
+  unsigned wc[2][kWaves][kRadix];
+  unsigned base[kRadix];
+  unsigned lds_w[kWaves];
+};
+
+// Stable ranks of this wave's keys among the keys of equal digit: slot by
+// slot, lanes in order, continuing this wave's per-digit counters wc.
+__device__ __forceinline__ void rank_slots(const u64 (&key)[kSlots], const bool (&valid)[kSlots], int nslots,
+                                           int shift, unsigned dmask, unsigned* wc, unsigned (&rank)[kSlots]) {
+  const int lane = threadIdx.x & 63;
+  const u64 lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+  for (int i = 0; i < kSlots; ++i) {
+    rank[i] = 0;
+    if (i < nslots) {
+      const unsigned d = gs_sort::digit_of(key[i], shift, dmask);
+      const u64 peers = gs_sort::match_digit(d, valid[i]);
+      unsigned before = 0;
+      if (valid[i]) before = wc[d];
+      __builtin_amdgcn_wave_barrier();
+      const unsigned below = (unsigned)__popcll(peers & lt_mask);
+      if (valid[i] && below == 0) wc[d] = before + (unsigned)__popcll(peers);
+      __builtin_amdgcn_wave_barrier();
+      rank[i] = before + below;
+    }
+  }
+}
+
+// Element e of a chunk of cnt keys belongs to wave e / cw, slot (e % cw) / 64,
+// lane e % 64, with cw = 64 * ceil(cnt / 256): waves take contiguous runs, so
+// processing waves, slots and lanes in order is processing elements in order.
+__device__ __forceinline__ int chunk_wave_span(int cnt) { return 64 * ((cnt + kThreads - 1) / kThreads); }
+
+// Segments of up to kSmallCap keys: one wave per tile, no workgroup barriers.
+// Lane l holds keys 64 i + l (i < kSmallSlots) in registers; 9-bit digits
+// (three passes over a 26-bit depth field) with 512 per-digit counters in LDS,
+// scanned by the wave with lane l owning counters 8 l .. 8 l + 7.  The wave's
+// LDS accesses execute in issue order, so the wave_barrier() compiler fences
+// are all the ordering the counter and buffer updates need.
+constexpr int kSmallSlots = 16;
+constexpr int kSmallCap = 64 * kSmallSlots;  // 1024 keys
+constexpr int kSmallDigitBits = 9;
+constexpr int kSmallRadix = 1 << kSmallDigitBits;
+
+// Lanes of the wave holding the same kBits-bit digit d (among valid lanes);
+// the same per-bit ballot filtering as gs_sort::match_digit.
+template <int kBits>
+__device__ __forceinline__ u64 match_bits(unsigned d, bool valid) {
+  const u64 v = __ballot(valid);
+  unsigned lo = (unsigned)v, hi = (unsigned)(v >> 32);
+#pragma unroll
+  for (int b = 0; b < kBits; ++b) {
+    const unsigned sb = (unsigned)__builtin_amdgcn_sbfe((int)d, b, 1);
+    const u64 m = __ballot(sb != 0u);
+    lo = __builtin_amdgcn_bitop3_b32((unsigned)m, lo, sb, 0x84);
+    hi = __builtin_amdgcn_bitop3_b32((unsigned)(m >> 32), hi, sb, 0x84);
+  }
+  return ((u64)hi << 32) | lo;
+}
+
+// Inclusive prefix sum over the 64 lanes: Hillis-Steele within each row of
+// 16 lanes by DPP row shifts (lanes shifted in from outside the row read 0),
+// then the totals of the rows below added from three lane reads.
+__device__ __forceinline__ unsigned wave_inclusive_scan_u32(unsigned x) {
+  x += (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xF, 0xF, true);  // row_shr:1
+  x += (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xF, 0xF, true);  // row_shr:2
+  x += (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xF, 0xF, true);  // row_shr:4
+  x += (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xF, 0xF, true);  // row_shr:8
+  const unsigned r0 = (unsigned)__builtin_amdgcn_readlane((int)x, 15);
+  const unsigned r1 = (unsigned)__builtin_amdgcn_readlane((int)x, 31);
+  const unsigned r2 = (unsigned)__builtin_amdgcn_readlane((int)x, 47);
+  const int row = (threadIdx.x & 63) >> 4;
+  return x + (row >= 1 ? r0 : 0u) + (row >= 2 ? r1 : 0u) + (row >= 3 ? r2 : 0u);
+}
+
+__global__ __launch_bounds__(64) void segment_sort_small_kernel(long long n, u64* __restrict__ keys,
+                                                               const int2* __restrict__ ranges, int lo_bit,
+                                                               int key_bits, int value_bits,
+                                                               int* __restrict__ point_list, int write_keys) {
+  __shared__ u64 s_buf[kSmallCap];
+  __shared__ uint4 s_wc4[kSmallRadix / 4];
+  unsigned* s_wc = reinterpret_cast<unsigned*>(s_wc4);
+  const int lane = threadIdx.x;
+  int2 rg = ranges[blockIdx.x];
+  const long long start = rg.x < 0 ? 0 : (rg.x > n ? n : rg.x);
+  const long long end = rg.y < start ? start : (rg.y > n ? n : rg.y);
+  const int cnt = (int)(end - start);
+  if (cnt <= 0 || cnt > kSmallCap) return;
+  const int nslots = (cnt + 63) >> 6;
+  const u64 vmask = (1ull << value_bits) - 1ull;
+  const u64 lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  u64 key[kSmallSlots];
+  bool valid[kSmallSlots];
+#pragma unroll
+  for (int i = 0; i < kSmallSlots; ++i) {
+    valid[i] = i < nslots && 64 * i + lane < cnt;
+    key[i] = valid[i] ? keys[start + 64 * i + lane] : 0ull;
+  }
+  const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
+  s_wc4[2 * lane] = zero4;
+  s_wc4[2 * lane + 1] = zero4;
+  __builtin_amdgcn_wave_barrier();
+  const int passes = (key_bits + kSmallDigitBits - 1) / kSmallDigitBits;
+  for (int pass = 0; pass < passes; ++pass) {
+    const int shift = lo_bit + kSmallDigitBits * pass;
+    const int bits = key_bits - kSmallDigitBits * pass < kSmallDigitBits ? key_bits - kSmallDigitBits * pass
+                                                                         : kSmallDigitBits;
+    const unsigned dmask = (1u << bits) - 1u;
+    unsigned rank[kSmallSlots];
+#pragma unroll
+    for (int i = 0; i < kSmallSlots; ++i) {
+      rank[i] = 0;
+      if (i < nslots) {
+        const unsigned d = (unsigned)(key[i] >> shift) & dmask;
+        const u64 peers = match_bits<kSmallDigitBits>(d, valid[i]);
+        unsigned before = 0;
+        if (valid[i]) before = s_wc[d];
+        __builtin_amdgcn_wave_barrier();
+        const unsigned below = (unsigned)__popcll(peers & lt_mask);
+        if (valid[i] && below == 0) s_wc[d] = before + (unsigned)__popcll(peers);
+        __builtin_amdgcn_wave_barrier();
+        rank[i] = before + below;
+      }
+    }
+    // counters -> exclusive digit starts
+    {
+      const uint4 a = s_wc4[2 * lane];
+      const uint4 b = s_wc4[2 * lane + 1];
+      const unsigned t = a.x + a.y + a.z + a.w + b.x + b.y + b.z + b.w;
+      unsigned e = wave_inclusive_scan_u32(t) - t;
+      uint4 ea, eb;
+      ea.x = e; e += a.x;
+      ea.y = e; e += a.y;
+      ea.z = e; e += a.z;
+      ea.w = e; e += a.w;
+      eb.x = e; e += b.x;
+      eb.y = e; e += b.y;
+      eb.z = e; e += b.z;
+      eb.w = e;
+      s_wc4[2 * lane] = ea;
+      s_wc4[2 * lane + 1] = eb;
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < kSmallSlots; ++i) {
+      if (valid[i]) s_buf[s_wc[(unsigned)(key[i] >> shift) & dmask] + rank[i]] = key[i];
+    }
+    __builtin_amdgcn_wave_barrier();
+    s_wc4[2 * lane] = zero4;
+    s_wc4[2 * lane + 1] = zero4;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < kSmallSlots; ++i)
+      if (valid[i]) key[i] = s_buf[64 * i + lane];
+    __builtin_amdgcn_wave_barrier();
+  }
+#pragma unroll
+  for (int i = 0; i < kSmallSlots; ++i) {
+    if (valid[i]) {
+      point_list[start + 64 * i + lane] = (int)(key[i] & vmask);
+      if (write_keys) keys[start + 64 * i + lane] = key[i];
+    }
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void segment_sort_kernel(long long n, u64* __restrict__ keys,
+                                                               u64* __restrict__ keys_alt, int num_tiles,
+                                                               const int2* __restrict__ ranges, int lo_bit,
+                                                               int key_bits, int value_bits,
+                                                               int* __restrict__ point_list, int write_keys) {
+  __shared__ Shared s;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int tile = blockIdx.x;
+  int2 rg = ranges[tile];
+  const long long start = rg.x < 0 ? 0 : (rg.x > n ? n : rg.x);
+  const long long end = rg.y < start ? start : (rg.y > n ? n : rg.y);
+  const int cnt_all = (int)(end - start);
+  if (cnt_all <= kSmallCap) return;  // segment_sort_small_kernel's
+  const u64 vmask = (1ull << value_bits) - 1ull;
+  const int passes = (key_bits + 7) / 8;
+
+  if (cnt_all <= kCap) {
+    const int cw = chunk_wave_span(cnt_all);
+    const int nslots = cw / 64;
+    u64 key[kSlots];
+    bool valid[kSlots];
+    int elem[kSlots];
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+      elem[i] = wave * cw + 64 * i + lane;
+      valid[i] = i < nslots && elem[i] < cnt_all;
+      key[i] = valid[i] ? keys[start + elem[i]] : 0ull;
+    }
+    for (int i = tid; i < kWaves * kRadix; i += kThreads) (&s.wc[0][0][0])[i] = 0;
+    __syncthreads();
+    for (int pass = 0; pass < passes; ++pass) {
+      const int b = pass & 1;
+      const int shift = lo_bit + 8 * pass;
+      const unsigned dmask = key_bits - 8 * pass >= 8 ? 0xFFu : ((1u << (key_bits - 8 * pass)) - 1u);
+      unsigned rank[kSlots];
+      rank_slots(key, valid, nslots, shift, dmask, s.wc[b][wave], rank);
+      __syncthreads();
+      {
+        const int d = tid;
+        unsigned run = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          const unsigned c = s.wc[b][w][d];
+          s.wc[b][w][d] = run;
+          s.wc[b ^ 1][w][d] = 0;
+          run += c;
+        }
+        unsigned tot;
+        s.base[d] = gs_sort::block_exclusive_scan_u32(run, s.lds_w, &tot);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < kSlots; ++i) {
+        if (valid[i]) {
+          const unsigned d = gs_sort::digit_of(key[i], shift, dmask);
+          s.buf[s.base[d] + s.wc[b][wave][d] + rank[i]] = key[i];
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < kSlots; ++i)
+        if (valid[i]) key[i] = s.buf[elem[i]];
+    }
+    // key[i] is now sorted element elem[i]; waves cover contiguous runs.
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+      if (valid[i]) {
+        point_list[start + elem[i]] = (int)(key[i] & vmask);
+        if (write_keys) keys[start + elem[i]] = key[i];
+      }
+    }
+    return;
+  }
+
+  // Long segment: ping-pong through global memory.
+  u64* src = keys + start;
+  u64* dst = keys_alt + start;
+  unsigned* cnt = &s.wc[1][0][0];
+  for (int pass = 0; pass < passes; ++pass) {
+    const int shift = lo_bit + 8 * pass;
+    const unsigned dmask = key_bits - 8 * pass >= 8 ? 0xFFu : ((1u << (key_bits - 8 * pass)) - 1u);
+    cnt[tid] = 0;
+    for (int w = 0; w < kWaves; ++w) s.wc[0][w][tid] = 0;
+    __syncthreads();
+    for (int e = tid; e < cnt_all; e += kThreads) atomicAdd(&cnt[gs_sort::digit_of(src[e], shift, dmask)], 1u);
+    __syncthreads();
+    {
+      unsigned tot;
+      s.base[tid] = gs_sort::block_exclusive_scan_u32(cnt[tid], s.lds_w, &tot);
+    }
+    __syncthreads();
+    for (int c0 = 0; c0 < cnt_all; c0 += kCap) {
+      const int ccnt = cnt_all - c0 < kCap ? cnt_all - c0 : kCap;
+      const int cw = chunk_wave_span(ccnt);
+      const int nslots = cw / 64;
+      u64 key[kSlots];
+      bool valid[kSlots];
+#pragma unroll
+      for (int i = 0; i < kSlots; ++i) {
+        const int e = wave * cw + 64 * i + lane;
+        valid[i] = i < nslots && e < ccnt;
+        key[i] = valid[i] ? src[c0 + e] : 0ull;
+      }
+      unsigned rank[kSlots];
+      rank_slots(key, valid, nslots, shift, dmask, s.wc[0][wave], rank);
+      __syncthreads();
+      unsigned run = 0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const unsigned c = s.wc[0][w][tid];
+        s.wc[0][w][tid] = run;
+        run += c;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < kSlots; ++i) {
+        if (valid[i]) {
+          const unsigned d = gs_sort::digit_of(key[i], shift, dmask);
+          dst[s.base[d] + s.wc[0][wave][d] + rank[i]] = key[i];
+        }
+      }
+      __syncthreads();
+      s.base[tid] += run;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) s.wc[0][w][tid] = 0;
+      __threadfence_block();
+      __syncthreads();
+    }
+    u64* t = src;
+    src = dst;
+    dst = t;
+  }
+  for (int e = tid; e < cnt_all; e += kThreads) {
+    const u64 k = src[e];
+    point_list[start + e] = (int)(k & vmask);
+    if (write_keys && src != keys + start) keys[start + e] = k;
+  }
+}
+
+}  // namespace gs_seg
+
+extern "C" int gs_sort_tile_segments(int64_t n, uint64_t* keys, uint64_t* keys_alt, int32_t num_tiles,
+                                     const int32_t* ranges, int32_t lo_bit, int32_t key_bits, int32_t value_bits,
+                                     int32_t* point_list, int32_t write_keys, void* stream) {
+  if (n < 0 || num_tiles < 0 || key_bits < 0 || value_bits < 1 || value_bits > 31 || lo_bit < value_bits ||
+      lo_bit + key_bits > 64)
+    return GS_ERR_INVALID_ARGUMENT;
+  if (n > 0x7fffffffLL) return GS_ERR_OVERFLOW;
+  if (n == 0 || num_tiles == 0) return GS_OK;
+  if (!keys || !keys_alt || !ranges || !point_list) return GS_ERR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(gs_seg::segment_sort_small_kernel, dim3(num_tiles), dim3(64), 0, (hipStream_t)stream,
+                     (long long)n, reinterpret_cast<gs_sort::u64*>(keys), reinterpret_cast<const int2*>(ranges),
+                     lo_bit, key_bits, value_bits, point_list, write_keys);
+  hipLaunchKernelGGL(gs_seg::segment_sort_kernel, dim3(num_tiles), dim3(gs_seg::kThreads), 0, (hipStream_t)stream,
+                     (long long)n, reinterpret_cast<gs_sort::u64*>(keys), reinterpret_cast<gs_sort::u64*>(keys_alt),
+                     num_tiles, reinterpret_cast<const int2*>(ranges), lo_bit, key_bits, value_bits, point_list,
+                     write_keys);
+  return gs_status_from_hip(hipGetLastError());
+}

@@ -192,6 +192,25 @@ int gs_tile_ranges(int64_t n, const uint64_t* sorted_keys, int32_t tile_shift, i
 int gs_tile_ranges_u32(int64_t n, const uint32_t* sorted_tiles, int32_t num_tiles, int32_t* ranges, void* stream);
 
 /*
+ * Second half of the packed-key binning sort.  keys holds the packed
+ * (tile, depth field, point) keys already sorted stably by their tile field,
+ * so each tile's keys are contiguous and in point order, and ranges holds
+ * their [start, end) (gs_tile_ranges).  Each tile's segment is sorted stably
+ * by bits [lo_bit, lo_bit + key_bits) (the depth field), which gives the
+ * order of a full (tile, depth, point) key sort, and
+ * point_list[i] = key_i & (2^value_bits - 1) is written.  With write_keys the
+ * sorted keys are also written back to keys; without it the keys of tiles
+ * longer than 2048 are left permuted within their segment.  keys_alt
+ * (n keys) is scratch for those tiles.  Allocates nothing.
+ * Replaces: binning_ops.py:337-343 (the stable tile sort of the
+ * depth-ordered pairs) together with the depth order of
+ * binning_ops.py:152-222, i.e. the final per-tile (depth, point) order.
+ */
+int gs_sort_tile_segments(int64_t n, uint64_t* keys, uint64_t* keys_alt, int32_t num_tiles, const int32_t* ranges,
+                          int32_t lo_bit, int32_t key_bits, int32_t value_bits, int32_t* point_list,
+                          int32_t write_keys, void* stream);
+
+/*
  * Per-tile front-to-back alpha blending of 16x16 tiles, each covered by
  * independent wave64 workgroups that own a slice of its rows.
  * num_points (N) and num_rendered (R) bound every index read from ranges and

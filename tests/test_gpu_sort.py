@@ -122,3 +122,64 @@ def test_sort_repeated_calls_reuse_scratch(device):
         torch.cuda.synchronize()
         res = (alt if lib.gs_sort_num_passes(45) % 2 else kt).cpu().numpy().view(np.uint64)
         assert np.array_equal(res, keys[np.argsort(_field(keys, 0, 45), kind="stable")])
+
+
+def _tile_sorted_keys(rng, sizes, depth_bits, value_bits, dup):
+    """Packed (tile, depth field, point) keys grouped by tile, in point order
+    within each tile (the state after the stable tile-field sort)."""
+    chunks = []
+    for t, c in enumerate(sizes):
+        if c == 0:
+            continue
+        idx = np.sort(rng.choice(1 << value_bits, size=c, replace=False)).astype(np.uint64)
+        hi = max(1, (1 << depth_bits) if not dup else min(1 << depth_bits, 7))
+        depth = rng.integers(0, hi, size=c, dtype=np.uint64) if depth_bits > 0 else np.zeros(c, np.uint64)
+        chunks.append((np.uint64(t) << np.uint64(depth_bits + value_bits)) | (depth << np.uint64(value_bits)) | idx)
+    keys = np.concatenate(chunks) if chunks else np.zeros(0, np.uint64)
+    ends = np.cumsum(sizes)
+    ranges = np.stack([ends - np.asarray(sizes), ends], axis=1).astype(np.int32)
+    ranges[np.asarray(sizes) == 0] = 0
+    return keys, ranges
+
+
+SEGMENT_CASES = [
+    # tile sizes, depth_bits, value_bits, duplicate-heavy depths, write_keys
+    ([0, 1, 2, 63, 64, 65, 0, 300, 1013, 2047, 2048, 0], 26, 20, False, True),
+    ([2049, 5000, 0, 17, 20000, 4097], 26, 20, False, True),
+    ([2049, 5000, 17, 9000], 26, 20, True, False),
+    ([350] * 40 + [1400] * 3, 9, 20, True, True),
+    ([500, 3000, 1], 0, 20, False, True),
+    ([777, 2500, 64], 1, 31, True, True),
+    ([1024, 6000, 2000], 32, 20, False, False),
+]
+
+
+@pytest.mark.parametrize("sizes,depth_bits,value_bits,dup,write_keys", SEGMENT_CASES)
+def test_tile_segment_sort_matches_full_key_sort(sizes, depth_bits, value_bits, dup, write_keys, device):
+    """gs_sort_tile_segments on tile-grouped keys gives the full (tile, depth,
+    point) key order: tiles empty, tiny, ragged, exactly at and above the
+    2048-key on-chip capacity (the chunked global path), partial last digits,
+    no depth bits, and duplicate-heavy depths (stability)."""
+    lib = _lib.load()
+    rng = np.random.default_rng(sum(sizes) * 7 + depth_bits)
+    keys, ranges = _tile_sorted_keys(rng, sizes, depth_bits, value_bits, dup)
+    n = keys.size
+    kt = torch.from_numpy(keys.view(np.int64).copy()).to(device)
+    alt = torch.full_like(kt, -1)
+    rt = torch.from_numpy(ranges).to(device)
+    pl = torch.full((n,), -7, dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    print(f"[segsort] n={n} tiles={len(sizes)} depth_bits={depth_bits} write_keys={write_keys}", flush=True)
+    lib.call("gs_sort_tile_segments", n, kt.data_ptr(), alt.data_ptr(), len(sizes), rt.data_ptr(), value_bits,
+             depth_bits, value_bits, pl.data_ptr(), int(write_keys), stream)
+    torch.cuda.synchronize()
+    expect = np.sort(keys)
+    vmask = np.uint64((1 << value_bits) - 1)
+    assert np.array_equal(pl.cpu().numpy(), (expect & vmask).astype(np.int32))
+    got_keys = kt.cpu().numpy().view(np.uint64)
+    if write_keys:
+        assert np.array_equal(got_keys, expect)
+    else:  # left in place, or (tiles above 2048 keys) permuted within their segment
+        assert np.array_equal(np.sort(got_keys), expect)
+        for (a, b) in ranges:
+            assert np.array_equal(np.sort(got_keys[a:b]), expect[a:b])
