@@ -38,6 +38,9 @@ def _run_forward(ctx, means3D, sh, colors_precomp, opacities, scales, rotations,
     ctx.save_for_backward(colors_precomp, opacities, means3D, scales, rotations, cov3Ds_precomp, result.radii, sh,
                           result.alpha)
     ctx.mark_non_differentiable(result.radii)
+    # Outputs the loss does not use reach backward as None, which the kernels
+    # read as zero gradients, instead of as materialised zero tensors.
+    ctx.set_materialize_grads(False)
     return result
 
 

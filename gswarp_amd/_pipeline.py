@@ -13,6 +13,7 @@ pair-count readback of the binning stage.
 from __future__ import annotations
 
 import contextlib
+import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -20,7 +21,8 @@ import torch
 from . import _lib, _packing, _workspace
 from ._coverage import tile_coverage_mode_id
 from ._runtime import BINNING_SORT_MODES, ExecutionOptions
-from ._state import BinningState, ForwardResult, ForwardState, KeyLayout, PreprocessOutputs, RenderStageResult
+from ._state import (BinningState, ForwardResult, ForwardState, KeyLayout, PreprocessOutputs, RenderImages,
+                     RenderStageResult)
 
 BLOCK_X = 16
 BLOCK_Y = 16
@@ -36,6 +38,15 @@ STAGE_TIMER = None
 def _stage(name: str):
     timer = STAGE_TIMER
     return timer(name) if timer is not None else contextlib.nullcontext()
+
+
+def _stage_chain(names):
+    """Raw event handles (a ctypes array) bracketing consecutive stages inside
+    one C call, when the stage timer offers them; None otherwise."""
+    timer = STAGE_TIMER
+    if timer is None or not hasattr(timer, "chain"):
+        return None
+    return timer.chain(names)
 
 
 @dataclass(slots=True)
@@ -233,7 +244,7 @@ DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN = 4
 
 
 def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options: ExecutionOptions,
-            keep_keys: bool = False, pack: bool = False) -> BinningState:
+            keep_keys: bool = False, pack: bool = False, images: RenderImages | None = None) -> BinningState:
     """Per-tile Gaussian lists (binning_ops.py:84-431) in the requested sort mode.
 
     Every mode yields the same lists: per tile, the Gaussians in (depth, index)
@@ -247,7 +258,9 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
     there are more than DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN pairs per Gaussian,
     and the single packed-key sort otherwise, where one sort of the pairs is
     cheaper than two sorts and the extra gathers.  With ``pack`` point_list and
-    ranges are views of one raw-ABI binning buffer.
+    ranges are views of one raw-ABI binning buffer.  With ``images`` the
+    packed path may launch the standard forward render into them right after
+    the binning (then the returned state has ``rendered`` set).
     """
     mode = options.binning_sort_mode
     if mode not in BINNING_SORT_MODES:
@@ -265,11 +278,45 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
         lib.call("gs_scan_tiles", P, pre.tiles_touched.data_ptr(), None, pre.radii.data_ptr(), pre.depths.data_ptr(),
                  offsets.data_ptr(), info.data_ptr(), scan_scratch.data_ptr(), scan_scratch.numel(), stream)
     pinned = _workspace.readback_buffer(device, torch.cuda.current_stream(device))
-    lib.call("gs_num_rendered_readback", info.data_ptr(), pinned.data_ptr(), stream)
-    R = validate_pair_count(int(pinned[0]))
-    depth_range = int(pinned[1]) & 0xFFFFFFFFFFFFFFFF
-    _note("num_rendered", R)
-    buffer = point_list = ranges = None
+    capacity = _workspace.pair_capacity(device) if (not pack and not keep_keys and mode != "torch"
+                                                    and PACKED_SORT == "segmented" and P > 0) else 0
+    if capacity > 0:
+        # Buffers for the expected pair count are allocated before the count
+        # is read back, so that one C call reads it and launches the whole
+        # packed binning; it declines (result[4] == 0) when the count does not
+        # fit or the default mode picks the depth-then-tile dataflow.
+        point_list = torch.empty((capacity,), dtype=torch.int32, device=device)
+        ranges = torch.empty((T, 2), dtype=torch.int32, device=device)
+        ws = torch.empty((int(lib.gs_bin_packed_workspace_bytes(capacity)),), dtype=torch.uint8, device=device)
+        result = (ctypes.c_int64 * 6)()
+        events = _stage_chain(("duplicate", "sort", "ranges", "sort") + (("render",) if images is not None else ()))
+        img = images
+        lib.call("gs_readback_bin_packed", info.data_ptr(), pinned.data_ptr(), P, pre.radii.data_ptr(),
+                 pre.records.data_ptr(), pre.conic_2d_inv.data_ptr(), offsets.data_ptr(), image_width, image_height,
+                 pre.coverage_mode, DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN if mode == "warp_depth_stable_tile" else 0,
+                 capacity, ws.data_ptr(), ws.numel(), ranges.data_ptr(), point_list.data_ptr(),
+                 None if img is None else img.background.data_ptr(), int(img is not None and img.compute_depth),
+                 None if img is None else img.color.data_ptr(), None if img is None else img.depth.data_ptr(),
+                 None if img is None else img.alpha.data_ptr(), None if img is None else img.n_contrib.data_ptr(),
+                 events, result, stream)
+        R = validate_pair_count(int(result[0]))
+        _workspace.note_pairs(device, R)
+        _note("num_rendered", R)
+        if result[4]:
+            _note("binning_dataflow", "packed_key")
+            _note("sort_passes", int(lib.gs_sort_num_passes((T - 1).bit_length())))
+            layout = KeyLayout(depth_min=int(result[1]), depth_bits=int(result[2]), value_bits=int(result[3]))
+            return BinningState(grid_x, grid_y, point_list[:R], ranges, R, None, layout, rendered=bool(result[5]))
+        depth_range = int(pinned[1]) & 0xFFFFFFFFFFFFFFFF
+        point_list = ranges = None
+    else:
+        point_list = ranges = None
+        lib.call("gs_num_rendered_readback", info.data_ptr(), pinned.data_ptr(), stream)
+        R = validate_pair_count(int(pinned[0]))
+        depth_range = int(pinned[1]) & 0xFFFFFFFFFFFFFFFF
+        _workspace.note_pairs(device, R)
+        _note("num_rendered", R)
+    buffer = None
     if pack:
         buffer, point_list, ranges = _packing.allocate_binning(R, T, device)
     if R == 0:
@@ -366,7 +413,7 @@ def _binning_depth_tile(pre: PreprocessOutputs, image_width: int, image_height: 
 def _binning_packed(pre: PreprocessOutputs, image_width: int, image_height: int, offsets: torch.Tensor, R: int,
                     layout: KeyLayout, keep_keys: bool, point_list: torch.Tensor | None = None,
                     ranges: torch.Tensor | None = None) -> BinningState:
-    """One packed 64-bit key per pair, emitted in point order and sorted once."""
+    """One packed 64-bit key per pair, emitted in point order and sorted."""
     lib = _lib.load()
     device = pre.radii.device
     P = pre.radii.shape[0]
@@ -374,6 +421,23 @@ def _binning_packed(pre: PreprocessOutputs, image_width: int, image_height: int,
     T = grid_x * grid_y
     stream = _stream(device)
     packed = layout.value_bits > 0
+    tile_bits = (T - 1).bit_length()
+    if ranges is None:
+        ranges = torch.empty((T, 2), dtype=torch.int32, device=device)
+    if packed and PACKED_SORT == "segmented":
+        # One host call launches emission, the stable sort on the tile field,
+        # the tile ranges and each tile's on-chip depth sort back to back.
+        _note("sort_passes", int(lib.gs_sort_num_passes(tile_bits)))
+        if point_list is None:
+            point_list = torch.empty((R,), dtype=torch.int32, device=device)
+        ws = torch.empty((max(int(lib.gs_bin_packed_workspace_bytes(R)), 1),), dtype=torch.uint8, device=device)
+        keys_out = torch.empty((R,), dtype=torch.int64, device=device) if keep_keys else None
+        events = _stage_chain(("duplicate", "sort", "ranges", "sort"))
+        lib.call("gs_bin_packed", P, pre.radii.data_ptr(), pre.records.data_ptr(), pre.conic_2d_inv.data_ptr(),
+                 offsets.data_ptr(), image_width, image_height, pre.coverage_mode, R, layout.depth_min,
+                 layout.depth_bits, layout.value_bits, ws.data_ptr(), ws.numel(), ranges.data_ptr(),
+                 point_list.data_ptr(), _lib.ptr(keys_out), events, stream)
+        return BinningState(grid_x, grid_y, point_list, ranges, R, keys_out, layout)
     keys = torch.empty((R,), dtype=torch.int64, device=device)
     keys_alt = torch.empty((R,), dtype=torch.int64, device=device)
     vals = vals_alt = None
@@ -384,30 +448,8 @@ def _binning_packed(pre: PreprocessOutputs, image_width: int, image_height: int,
         lib.call("gs_duplicate_keys", P, pre.radii.data_ptr(), pre.records.data_ptr(),
                  pre.conic_2d_inv.data_ptr(), offsets.data_ptr(), image_width, image_height, pre.coverage_mode, R,
                  layout.depth_min, layout.depth_bits, layout.value_bits, keys.data_ptr(), _lib.ptr(vals), stream)
-    tile_bits = (T - 1).bit_length()
-    sort_scratch = torch.empty((max(int(lib.gs_sort_scratch_bytes(R)), 1),), dtype=torch.uint8, device=device)
-    if ranges is None:
-        ranges = torch.empty((T, 2), dtype=torch.int32, device=device)
-    if packed and PACKED_SORT == "segmented":
-        # Stable sort on the tile field only, then each tile's segment (in point
-        # order) sorted stably by its depth field on chip.
-        passes = int(lib.gs_sort_num_passes(tile_bits))
-        _note("sort_passes", passes)
-        with _stage("sort"):
-            lib.call("gs_sort_keys_u64", R, layout.tile_shift, tile_bits, keys.data_ptr(), keys_alt.data_ptr(),
-                     sort_scratch.data_ptr(), sort_scratch.numel(), stream)
-        if passes % 2:
-            keys, keys_alt = keys_alt, keys
-        with _stage("ranges"):
-            lib.call("gs_tile_ranges", R, keys.data_ptr(), layout.tile_shift, 0, T, ranges.data_ptr(), None, stream)
-        if point_list is None:
-            point_list = torch.empty((R,), dtype=torch.int32, device=device)
-        with _stage("sort"):
-            lib.call("gs_sort_tile_segments", R, keys.data_ptr(), keys_alt.data_ptr(), T, ranges.data_ptr(),
-                     layout.value_bits, layout.depth_bits, layout.value_bits, point_list.data_ptr(),
-                     int(bool(keep_keys)), stream)
-        return BinningState(grid_x, grid_y, point_list, ranges, R, keys if keep_keys else None, layout)
     sort_bits = tile_bits + layout.depth_bits
+    sort_scratch = torch.empty((max(int(lib.gs_sort_scratch_bytes(R)), 1),), dtype=torch.uint8, device=device)
     _note("sort_passes", int(lib.gs_sort_num_passes(sort_bits)))
     with _stage("sort"):
         if packed:
@@ -428,20 +470,33 @@ def _binning_packed(pre: PreprocessOutputs, image_width: int, image_height: int,
     return BinningState(grid_x, grid_y, point_list, ranges, R, keys if keep_keys else None, layout)
 
 
+def render_images(background: torch.Tensor, image_height: int, image_width: int, options: ExecutionOptions,
+                  device: torch.device) -> RenderImages:
+    """The forward render's outputs, allocated ahead of the binning."""
+    f = dict(dtype=torch.float32, device=device)
+    H, W = image_height, image_width
+    return RenderImages(_f32c(background.to(device)), torch.empty((NUM_CHANNELS, H, W), **f),
+                        torch.empty((1, H, W), **f), torch.empty((1, H, W), **f),
+                        torch.empty((H * W,), dtype=torch.int32, device=device), bool(options.compute_depth))
+
+
 def render(pre: PreprocessOutputs, bins: BinningState, background: torch.Tensor, image_height: int,
-           image_width: int, options: ExecutionOptions, *, flow: bool = False) -> RenderStageResult:
-    """Tile blend (render_ops.py:16-93; flow: flow_ops.py:109-193)."""
+           image_width: int, options: ExecutionOptions, *, flow: bool = False,
+           images: RenderImages | None = None) -> RenderStageResult:
+    """Tile blend (render_ops.py:16-93; flow: flow_ops.py:109-193).  ``images``
+    are preallocated outputs; when the binning already launched the render into
+    them (``bins.rendered``) nothing more is launched."""
     lib = _lib.load()
     device = pre.radii.device
     P = pre.radii.shape[0]
     H, W = image_height, image_width
     f = dict(dtype=torch.float32, device=device)
-    bg = _f32c(background.to(device))
-    color = torch.empty((NUM_CHANNELS, H, W), **f)
-    depth = torch.empty((1, H, W), **f)
-    alpha = torch.empty((1, H, W), **f)
-    n_contrib = torch.empty((H * W,), dtype=torch.int32, device=device)
+    if images is None:
+        images = render_images(background, H, W, options, device)
+    bg, color, depth, alpha, n_contrib = images.background, images.color, images.depth, images.alpha, images.n_contrib
     aux: tuple[torch.Tensor, ...] = ()
+    if bins.rendered and not flow:
+        return RenderStageResult(color, depth, alpha, n_contrib, aux)
     write_aux = bool(flow and options.compute_flow_aux)
     k = int(options.flow_topk or 0) if write_aux else 0
     if bins.num_rendered == 0:
@@ -487,8 +542,11 @@ def forward(inputs: RasterInputs, options: ExecutionOptions, *, flow: bool = Fal
             k = (options.flow_topk if options.compute_flow_aux else 0) if flow else None
             return empty_forward(inputs, k)
         pre = preprocess(inputs, options, pack=pack)
-        bins = binning(pre, inputs.image_height, inputs.image_width, options, pack=pack)
-        res = render(pre, bins, inputs.background, inputs.image_height, inputs.image_width, options, flow=flow)
+        images = render_images(inputs.background, inputs.image_height, inputs.image_width, options, device)
+        bins = binning(pre, inputs.image_height, inputs.image_width, options, pack=pack,
+                       images=None if flow else images)
+        res = render(pre, bins, inputs.background, inputs.image_height, inputs.image_width, options, flow=flow,
+                     images=images)
     return ForwardResult(
         num_rendered=bins.num_rendered,
         color=res.color,
@@ -503,10 +561,10 @@ def forward(inputs: RasterInputs, options: ExecutionOptions, *, flow: bool = Fal
     )
 
 
-def _zeros_if_none(t: torch.Tensor | None, shape, device) -> torch.Tensor:
-    if t is None:
-        return torch.zeros(shape, dtype=torch.float32, device=device)
-    return _f32c(t)
+def _f32c_or_none(t: torch.Tensor | None) -> torch.Tensor | None:
+    """Contiguous fp32 upstream gradient, or None (the kernels read an absent
+    gradient as zero)."""
+    return None if t is None else _f32c(t)
 
 
 def backward(inputs: RasterInputs, radii: torch.Tensor, alpha: torch.Tensor, grad_color, grad_depth, grad_alpha,
@@ -537,14 +595,14 @@ def backward(inputs: RasterInputs, radii: torch.Tensor, alpha: torch.Tensor, gra
         grad_gauss = torch.zeros((P, _lib.GS_GRAD_FLOATS), dtype=torch.float32, device=device)
         if bins.num_rendered != 0:
             bg = _f32c(inputs.background.to(device))
-            gc = _zeros_if_none(grad_color, (NUM_CHANNELS, H, W), device)
-            gd = _zeros_if_none(grad_depth, (1, H, W), device)
-            ga = _zeros_if_none(grad_alpha, (1, H, W), device)
+            gc = _f32c_or_none(grad_color)
+            gd = _f32c_or_none(grad_depth)
+            ga = _f32c_or_none(grad_alpha)
             alpha_c = _f32c(alpha)
             with _stage("render_bwd"):
                 lib.call("gs_render_bwd", W, H, P, bins.num_rendered, bins.ranges.data_ptr(),
                          bins.point_list.data_ptr(), pre.records.data_ptr(), bg.data_ptr(), alpha_c.data_ptr(),
-                         n_contrib.data_ptr(), gc.data_ptr(), gd.data_ptr(), ga.data_ptr(),
+                         n_contrib.data_ptr(), _lib.ptr(gc), _lib.ptr(gd), _lib.ptr(ga),
                          int(bool(options.compute_depth)), grad_gauss.data_ptr(), stream)
         has_sh = inputs.sh.numel() != 0
         shs = _f32c(inputs.sh).reshape(P, -1, NUM_CHANNELS) if has_sh else None
@@ -569,16 +627,16 @@ def backward(inputs: RasterInputs, radii: torch.Tensor, alpha: torch.Tensor, gra
         view_c = _f32c(inputs.viewmatrix)
         proj_c = _f32c(inputs.projmatrix)
         radii_c = radii.contiguous()
-        gp2 = _zeros_if_none(grad_proj_2d, (P, 2), device)
-        gcon = _zeros_if_none(grad_conic_2d, (P, 3), device)
-        gcov = _zeros_if_none(grad_conic_2d_inv, (P, 3), device)
+        gp2 = _f32c_or_none(grad_proj_2d)
+        gcon = _f32c_or_none(grad_conic_2d)
+        gcov = _f32c_or_none(grad_conic_2d_inv)
         with _stage("preprocess_bwd"):
             lib.call(
                 "gs_preprocess_bwd", P, K, int(inputs.degree), means_c.data_ptr(), _lib.ptr(scales_c),
                 _lib.ptr(rot_c), _lib.ptr(cov_c), float(inputs.scale_modifier), _lib.ptr(shs), campos_c.data_ptr(),
                 view_c.data_ptr(), proj_c.data_ptr(), tanfovx, tanfovy, _focal(W, tanfovx), _focal(H, tanfovy),
-                radii_c.data_ptr(), pre.clamped.data_ptr(), grad_gauss.data_ptr(), gp2.data_ptr(), gcon.data_ptr(),
-                gcov.data_ptr(), int(bool(flow_double)), float(inputs.filter_variance), grad_means3d.data_ptr(),
+                radii_c.data_ptr(), pre.clamped.data_ptr(), grad_gauss.data_ptr(), _lib.ptr(gp2), _lib.ptr(gcon),
+                _lib.ptr(gcov), int(bool(flow_double)), float(inputs.filter_variance), grad_means3d.data_ptr(),
                 grad_means2d.data_ptr(),
                 _lib.ptr(grad_scales) if cov_c is None else None,
                 _lib.ptr(grad_rotations) if cov_c is None else None,

@@ -41,6 +41,19 @@ class KeyLayout:
 
 
 @dataclass(slots=True)
+class RenderImages:
+    """Forward render outputs allocated before the binning, so that the binning
+    call can launch the render into them."""
+
+    background: torch.Tensor  # (3,) fp32, contiguous
+    color: torch.Tensor  # (3, H, W)
+    depth: torch.Tensor  # (1, H, W)
+    alpha: torch.Tensor  # (1, H, W)
+    n_contrib: torch.Tensor  # (H*W,) int32
+    compute_depth: bool = True
+
+
+@dataclass(slots=True)
 class BinningState:
     grid_x: int
     grid_y: int
@@ -50,6 +63,7 @@ class BinningState:
     sorted_keys: torch.Tensor | None = None  # (R,) int64 sorted binning keys (see KeyLayout)
     key_layout: KeyLayout = field(default_factory=KeyLayout)
     buffer: torch.Tensor | None = None  # raw-ABI (R + 2T) int32 buffer that point_list and ranges are views of
+    rendered: bool = False  # the standard forward render was launched with the binning (RenderImages)
 
     def decode_keys(self) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         """(tile id, depth float bits, sort field = tile and depth fields as one

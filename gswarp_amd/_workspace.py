@@ -60,12 +60,31 @@ def readback_buffer(device: torch.device, stream: torch.cuda.Stream) -> torch.Te
         return entry["pinned"]
 
 
+# Pair count of the last forward per device: the next forward allocates its
+# binning buffers for 1.25x that many pairs before its own count is known.
+_pair_hint: dict[int, int] = {}
+PAIR_HEADROOM = 1.25
+
+
+def pair_capacity(device: torch.device) -> int:
+    """Pairs to provision before the count is read back (0: no estimate yet)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    last = _pair_hint.get(index, 0)
+    return int(last * PAIR_HEADROOM) + 1024 if last > 0 else 0
+
+
+def note_pairs(device: torch.device, count: int) -> None:
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    _pair_hint[index] = int(count)
+
+
 def clear_caches() -> None:
     """Drop every workspace after synchronising the streams that use them."""
     with _lock:
         for entry in _entries.values():
             entry["stream"].synchronize()
         _entries.clear()
+        _pair_hint.clear()
 
 
 def cache_report() -> dict:

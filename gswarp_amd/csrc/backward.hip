@@ -183,11 +183,14 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
       const int pix = py * p.W + px;
       last[k] = imax(0, imin(p.n_contrib[pix], n));
       T[k] = 1.0f - p.out_alpha[pix];
-      gp0[k] = p.grad_color[pix];
-      gp1[k] = p.grad_color[P + pix];
-      gp2[k] = p.grad_color[2 * P + pix];
-      if (kDepth) gpd[k] = p.grad_depth[pix];
-      gpa[k] = p.grad_alpha[pix];
+      // absent upstream gradients (null) are zero
+      if (p.grad_color) {
+        gp0[k] = p.grad_color[pix];
+        gp1[k] = p.grad_color[P + pix];
+        gp2[k] = p.grad_color[2 * P + pix];
+      }
+      if (kDepth && p.grad_depth) gpd[k] = p.grad_depth[pix];
+      if (p.grad_alpha) gpa[k] = p.grad_alpha[pix];
       S[k] = fmaf(p.bg[2], gp2[k], fmaf(p.bg[1], gp1[k], p.bg[0] * gp0[k]));
     }
     lmax = imax(lmax, last[k]);
@@ -492,8 +495,9 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(PreprocessBwdParams
   float gx = rpx, gy = rpy;
   const float inv_w2 = inv_w * inv_w;
   if (rad > 0) {
-    float ax = p.grad_proj_2d[2 * tid + 0];
-    float ay = p.grad_proj_2d[2 * tid + 1];
+    // absent upstream gradients (null) are zero
+    float ax = p.grad_proj_2d ? p.grad_proj_2d[2 * tid + 0] : 0.0f;
+    float ay = p.grad_proj_2d ? p.grad_proj_2d[2 * tid + 1] : 0.0f;
     if (p.flow_double) {
       ax = ax + rpx;
       ay = ay + rpy;
@@ -591,9 +595,9 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(PreprocessBwdParams
     const float denom = aa * cc - bb * bb;
     const float denom2inv = 1.0f / (denom * denom + 1.0e-7f);
 
-    float uc0 = p.grad_conic_2d[3 * tid + 0];
-    float uc1 = p.grad_conic_2d[3 * tid + 1];
-    float uc2 = p.grad_conic_2d[3 * tid + 2];
+    float uc0 = p.grad_conic_2d ? p.grad_conic_2d[3 * tid + 0] : 0.0f;
+    float uc1 = p.grad_conic_2d ? p.grad_conic_2d[3 * tid + 1] : 0.0f;
+    float uc2 = p.grad_conic_2d ? p.grad_conic_2d[3 * tid + 2] : 0.0f;
     if (p.flow_double) {
       uc0 = uc0 + rc0;
       uc1 = uc1 + rc1;
@@ -605,9 +609,11 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(PreprocessBwdParams
     float dL_da = denom2inv * (-cc * cc * tc0 + 2.0f * bb * cc * tc1 - bb * bb * tc2);
     float dL_dc = denom2inv * (-aa * aa * tc2 + 2.0f * aa * bb * tc1 - bb * bb * tc0);
     float dL_db = denom2inv * 2.0f * (bb * cc * tc0 - (aa * cc + bb * bb) * tc1 + aa * bb * tc2);
-    dL_da = dL_da + p.grad_conic_2d_inv[3 * tid + 0];
-    dL_db = dL_db + p.grad_conic_2d_inv[3 * tid + 1];
-    dL_dc = dL_dc + p.grad_conic_2d_inv[3 * tid + 2];
+    if (p.grad_conic_2d_inv) {
+      dL_da = dL_da + p.grad_conic_2d_inv[3 * tid + 0];
+      dL_db = dL_db + p.grad_conic_2d_inv[3 * tid + 1];
+      dL_dc = dL_dc + p.grad_conic_2d_inv[3 * tid + 2];
+    }
 
     const float gc0 = t00 * t00 * dL_da + t00 * t01 * dL_db + t01 * t01 * dL_dc;
     const float gc3 = t10 * t10 * dL_da + t10 * t11 * dL_db + t11 * t11 * dL_dc;
@@ -722,8 +728,7 @@ extern "C" int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t 
     return GS_ERR_INVALID_ARGUMENT;
   if (num_points <= 0 || num_rendered < 0) return GS_ERR_INVALID_ARGUMENT;
   if (num_rendered > 0x7fffffffLL) return GS_ERR_OVERFLOW;
-  if (!ranges || !point_list || !records || !background || !out_alpha || !n_contrib || !grad_color ||
-      !grad_alpha || !grad_gauss || (compute_depth && !grad_depth))
+  if (!ranges || !point_list || !records || !background || !out_alpha || !n_contrib || !grad_gauss)
     return GS_ERR_INVALID_ARGUMENT;
   if (reinterpret_cast<uintptr_t>(records) & 15) return GS_ERR_MISALIGNED;
   gs::RenderBwdParams p;
@@ -767,8 +772,7 @@ extern "C" int gs_preprocess_bwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
   if (P < 0) return GS_ERR_INVALID_ARGUMENT;
   if (!(filter_variance >= 0.0f) || !__builtin_isfinite(filter_variance)) return GS_ERR_INVALID_ARGUMENT;
   if (P == 0) return GS_OK;
-  if (!means3d || !viewmatrix || !projmatrix || !radii || !grad_gauss || !grad_proj_2d || !grad_conic_2d ||
-      !grad_conic_2d_inv || !grad_means3d || !grad_means2d)
+  if (!means3d || !viewmatrix || !projmatrix || !radii || !grad_gauss || !grad_means3d || !grad_means2d)
     return GS_ERR_INVALID_ARGUMENT;
   if (cov3d_precomp == nullptr && (!scales || !rotations || !grad_scales || !grad_rotations))
     return GS_ERR_INVALID_ARGUMENT;

@@ -522,3 +522,129 @@ extern "C" int gs_tile_ranges_u32(int64_t n, const uint32_t* sorted_tiles, int32
   }
   return gs_status_from_hip(hipGetLastError());
 }
+
+// Packed-key binning after the pair count is known, as one host call so that
+// its launches follow each other without host round trips: emission, the
+// stable sort on the tile field, tile ranges and the per-tile depth sort.
+static inline size_t gs_align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+extern "C" size_t gs_bin_packed_workspace_bytes(int64_t num_rendered) {
+  if (num_rendered <= 0) return 0;
+  return 2 * gs_align256((size_t)num_rendered * sizeof(uint64_t)) + gs_align256(gs_sort_scratch_bytes(num_rendered));
+}
+
+extern "C" int gs_bin_packed(int32_t P, const int32_t* radii, const float* records, const float* conic_2d_inv,
+                             const int32_t* offsets, int32_t image_width, int32_t image_height,
+                             int32_t coverage_mode, int64_t num_rendered, uint32_t depth_min, int32_t depth_bits,
+                             int32_t value_bits, void* workspace, size_t workspace_bytes, int32_t* ranges,
+                             int32_t* point_list, uint64_t* sorted_keys_out, void* const* stage_events,
+                             void* stream) {
+  if (P < 0 || num_rendered < 0 || image_width <= 0 || image_height <= 0 || value_bits < 1 || value_bits > 31 ||
+      depth_bits < 0 || depth_bits > 32)
+    return GS_ERR_INVALID_ARGUMENT;
+  if (num_rendered > 0x7fffffffLL) return GS_ERR_OVERFLOW;
+  const int grid_x = (image_width + gs::kBlockX - 1) / gs::kBlockX;
+  const int grid_y = (image_height + gs::kBlockY - 1) / gs::kBlockY;
+  const int num_tiles = grid_x * grid_y;
+  const int tile_bits = gs_bit_length(num_tiles - 1);
+  const int tile_shift = depth_bits + value_bits;
+  if (tile_shift + tile_bits > 64) return GS_ERR_INVALID_ARGUMENT;
+  if (!ranges) return GS_ERR_INVALID_ARGUMENT;
+  hipStream_t s = (hipStream_t)stream;
+  if (num_rendered == 0) return gs_tile_ranges(0, nullptr, tile_shift, 0, num_tiles, ranges, nullptr, stream);
+  if (!workspace || !point_list) return GS_ERR_INVALID_ARGUMENT;
+  if (workspace_bytes < gs_bin_packed_workspace_bytes(num_rendered)) return GS_ERR_SCRATCH_TOO_SMALL;
+  const size_t key_bytes = gs_align256((size_t)num_rendered * sizeof(uint64_t));
+  uint64_t* keys = reinterpret_cast<uint64_t*>(workspace);
+  uint64_t* keys_alt = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(workspace) + key_bytes);
+  void* scratch = reinterpret_cast<char*>(workspace) + 2 * key_bytes;
+  const size_t scratch_bytes = workspace_bytes - 2 * key_bytes;
+  // Optional profiling: events recorded before emission and after each stage.
+  auto mark = [&](int k) {
+    if (stage_events) (void)hipEventRecord((hipEvent_t)stage_events[k], s);
+  };
+  mark(0);
+  int st = gs_duplicate_keys(P, radii, records, conic_2d_inv, offsets, image_width, image_height, coverage_mode,
+                             num_rendered, depth_min, depth_bits, value_bits, keys, nullptr, stream);
+  if (st != GS_OK) return st;
+  mark(1);
+  st = gs_sort_keys_u64(num_rendered, tile_shift, tile_bits, keys, keys_alt, scratch, scratch_bytes, stream);
+  if (st != GS_OK) return st;
+  mark(2);
+  if (gs_sort_num_passes(tile_bits) % 2) {
+    uint64_t* t = keys;
+    keys = keys_alt;
+    keys_alt = t;
+  }
+  st = gs_tile_ranges(num_rendered, keys, tile_shift, 0, num_tiles, ranges, nullptr, stream);
+  if (st != GS_OK) return st;
+  mark(3);
+  st = gs_sort_tile_segments(num_rendered, keys, keys_alt, num_tiles, ranges, value_bits, depth_bits, value_bits,
+                             point_list, sorted_keys_out != nullptr, stream);
+  if (st != GS_OK) return st;
+  mark(4);
+  if (sorted_keys_out) {
+    const hipError_t e = hipMemcpyAsync(sorted_keys_out, keys, (size_t)num_rendered * sizeof(uint64_t),
+                                        hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) return (int)e;
+  }
+  return GS_OK;
+}
+
+// The forward's read-back of the pair count followed, without returning to the
+// caller, by the packed-key binning into buffers the caller allocated for up to
+// `capacity` pairs before the count was known.  The key layout and the
+// dataflow are the caller's rules (key_layout and the default sort mode):
+//   tile_bits = bit length of T - 1, depth_bits = bit length of the visible
+//   depth-bit range, value_bits = max(1, bit length of P - 1), and the packed
+//   dataflow applies when the three fit in 64 bits and, if max_pairs_per_point
+//   > 0, num_rendered <= max_pairs_per_point * P.
+// result[0] = num_rendered, result[1] = depth_min, result[2] = depth_bits,
+// result[3] = value_bits, result[4] = 1 if the binning was launched, 0 if the
+// caller must bin itself (count outside [0, 2^31 - 1], over capacity, or
+// another dataflow), result[5] = 1 if the standard forward render was
+// launched too (out_color given).
+extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_host_pinned, int32_t P,
+                                      const int32_t* radii, const float* records, const float* conic_2d_inv,
+                                      const int32_t* offsets, int32_t image_width, int32_t image_height,
+                                      int32_t coverage_mode, int32_t max_pairs_per_point, int64_t capacity,
+                                      void* workspace, size_t workspace_bytes, int32_t* ranges, int32_t* point_list,
+                                      const float* background, int32_t compute_depth, float* out_color,
+                                      float* out_depth, float* out_alpha, int32_t* n_contrib,
+                                      void* const* stage_events, int64_t* result, void* stream) {
+  if (!result || P < 0 || capacity < 0 || image_width <= 0 || image_height <= 0) return GS_ERR_INVALID_ARGUMENT;
+  int st = gs_num_rendered_readback(info_dev, info_host_pinned, stream);
+  if (st != GS_OK) return st;
+  const int64_t R = info_host_pinned[0];
+  const uint64_t range = (uint64_t)info_host_pinned[1];
+  const uint32_t depth_min = (uint32_t)(range & 0xFFFFFFFFull);
+  const uint32_t depth_max = (uint32_t)(range >> 32);
+  const int depth_bits = depth_max >= depth_min ? gs_bit_length((long long)(depth_max - depth_min)) : 0;
+  int value_bits = gs_bit_length((long long)P - 1);
+  if (value_bits < 1) value_bits = 1;
+  const int grid_x = (image_width + gs::kBlockX - 1) / gs::kBlockX;
+  const int grid_y = (image_height + gs::kBlockY - 1) / gs::kBlockY;
+  const int tile_bits = gs_bit_length((long long)grid_x * grid_y - 1);
+  result[0] = R;
+  result[1] = depth_min;
+  result[2] = depth_bits;
+  result[3] = value_bits;
+  result[4] = 0;
+  result[5] = 0;
+  if (R <= 0 || R > 0x7fffffffLL || R > capacity) return GS_OK;
+  if (tile_bits + depth_bits + value_bits > 64 || value_bits > 31) return GS_OK;
+  if (max_pairs_per_point > 0 && R > (int64_t)max_pairs_per_point * P) return GS_OK;
+  st = gs_bin_packed(P, radii, records, conic_2d_inv, offsets, image_width, image_height, coverage_mode, R,
+                     depth_min, depth_bits, value_bits, workspace, workspace_bytes, ranges, point_list, nullptr,
+                     stage_events, stream);
+  if (st != GS_OK) return st;
+  result[4] = 1;
+  if (out_color) {
+    st = gs_render_fwd(image_width, image_height, P, R, ranges, point_list, records, background, compute_depth,
+                       out_color, out_depth, out_alpha, n_contrib, stream);
+    if (st != GS_OK) return st;
+    if (stage_events) (void)hipEventRecord((hipEvent_t)stage_events[5], (hipStream_t)stream);
+    result[5] = 1;
+  }
+  return GS_OK;
+}

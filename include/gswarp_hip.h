@@ -211,6 +211,56 @@ int gs_sort_tile_segments(int64_t n, uint64_t* keys, uint64_t* keys_alt, int32_t
                           int32_t write_keys, void* stream);
 
 /*
+ * The packed-key binning after the pair count is known, in one call:
+ * gs_duplicate_keys into workspace, gs_sort_keys_u64 on the tile field,
+ * gs_tile_ranges into ranges ((T, 2) int32, T = tiles of the image) and
+ * gs_sort_tile_segments into point_list (num_rendered int32).  workspace
+ * holds two key buffers and the sort scratch:
+ * gs_bin_packed_workspace_bytes(num_rendered) bytes.  With sorted_keys_out
+ * (num_rendered uint64) the fully sorted keys are copied there too.
+ * value_bits must be >= 1 (the point index is packed in the key).
+ * stage_events, if not NULL, holds five hipEvent_t recorded on the stream
+ * before emission and after emission, the tile sort, the ranges and the
+ * segment sort (for per-stage timing).
+ * Replaces: binning_ops.py:84-431 (_build_binning_state) after the
+ * num_rendered read-back at binning_ops.py:243-252.
+ */
+size_t gs_bin_packed_workspace_bytes(int64_t num_rendered);
+int gs_bin_packed(int32_t P, const int32_t* radii, const float* records, const float* conic_2d_inv,
+                  const int32_t* offsets, int32_t image_width, int32_t image_height, int32_t coverage_mode,
+                  int64_t num_rendered, uint32_t depth_min, int32_t depth_bits, int32_t value_bits, void* workspace,
+                  size_t workspace_bytes, int32_t* ranges, int32_t* point_list, uint64_t* sorted_keys_out,
+                  void* const* stage_events, void* stream);
+
+/*
+ * gs_num_rendered_readback followed, in the same call, by gs_bin_packed into
+ * buffers allocated before the pair count was known (point_list for up to
+ * `capacity` pairs, workspace of gs_bin_packed_workspace_bytes(capacity)
+ * bytes), so the binning launches without a return to the caller.  The key
+ * layout is tile | depth field (bit length of the visible depth-bit range)
+ * | point index (max(1, bit length of P - 1) bits); the packed dataflow is
+ * used when the fields fit in 64 bits and, with max_pairs_per_point > 0,
+ * num_rendered <= max_pairs_per_point * P.  result (5 int64):
+ * num_rendered, depth_min, depth_bits, value_bits, and 1 if the binning was
+ * launched or 0 if the caller must bin itself (count outside
+ * [1, 2^31 - 1], above capacity, or another dataflow).  With out_color
+ * non-NULL the binning is followed by gs_render_fwd into out_color,
+ * out_depth, out_alpha and n_contrib (background, compute_depth as there)
+ * and result (6 int64) ends with 1 if it was launched.  stage_events, if not
+ * NULL, holds the five events of gs_bin_packed and a sixth recorded after
+ * the render.
+ * Replaces: binning_ops.py:243-252 (the .item() read-back) together with
+ * the binning that follows it and render_ops.py:16-93.
+ */
+int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_host_pinned, int32_t P, const int32_t* radii,
+                           const float* records, const float* conic_2d_inv, const int32_t* offsets,
+                           int32_t image_width, int32_t image_height, int32_t coverage_mode,
+                           int32_t max_pairs_per_point, int64_t capacity, void* workspace, size_t workspace_bytes,
+                           int32_t* ranges, int32_t* point_list, const float* background, int32_t compute_depth,
+                           float* out_color, float* out_depth, float* out_alpha, int32_t* n_contrib,
+                           void* const* stage_events, int64_t* result, void* stream);
+
+/*
  * Per-tile front-to-back alpha blending of 16x16 tiles, each covered by
  * independent wave64 workgroups that own a slice of its rows.
  * num_points (N) and num_rendered (R) bound every index read from ranges and
@@ -242,7 +292,9 @@ int gs_render_fwd_flow(int32_t image_width, int32_t image_height, int32_t num_po
 
 /*
  * Reverse blend: accumulates per-Gaussian gradients of the pixel loss into
- * grad_gauss (N,10), which the caller zero-initialises.
+ * grad_gauss (N,10), which the caller zero-initialises.  grad_color,
+ * grad_depth and grad_alpha may each be NULL: an absent upstream gradient
+ * is zero.
  * Replaces: backward_ops.py:183-290 with backward_kernels.py:539-707.
  */
 int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t num_points, int64_t num_rendered,
@@ -264,7 +316,9 @@ int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t num_points,
  * gradient is returned as grad_cov3d (N, 6) instead of being chained into
  * grad_scales / grad_rotations (which may then be NULL).  filter_variance is
  * the forward's Mip-Splatting variance (0 without the filter), added to the
- * recomputed cov2D as in backward_kernels.py:176-178.
+ * recomputed cov2D as in backward_kernels.py:176-178.  The upstream
+ * gradients grad_proj_2d, grad_conic_2d and grad_conic_2d_inv may be NULL
+ * (zero).
  * Replaces: backward_ops.py:376-746 with backward_kernels.py:53-295 (fused),
  * backward_kernels.py:710-870 (precomputed covariances),
  * backward_kernels.py:298-536 and flow_kernels.py:14-28.
