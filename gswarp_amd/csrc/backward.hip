@@ -153,7 +153,6 @@ template <bool kDepth, int kPix>
 __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
   constexpr int kSubs = 4 / kPix;
   __shared__ float4 s_r0[64], s_r1[64], s_r2[64];
-  __shared__ int s_id[64];
   const int lane = threadIdx.x;
   const int2 ts = xcd_tile_sub(blockIdx.x, p.num_tiles, kSubs);
   const int tile = ts.x;
@@ -211,7 +210,7 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
     s_r0[lane] = next.r0;
     s_r1[lane] = next.r1;
     s_r2[lane] = next.r2;
-    s_id[lane] = next.id;
+    const int batch_id = next.id;  // lane j: Gaussian of record j
     uint64_t todo = __ballot(lane < cnt && record_may_touch(next.r0, next.r1, rx0, rx1, ry0, ry1));
     if (bs > 0) {
       const int nbs = imax(0, bs - 64);
@@ -225,38 +224,39 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
       const float4 b = s_r1[jj];
       const float dx = a.x - pfx;
       const float adxx = a.z * dx * dx;
-      const float bdx = a.w * dx;
-      float pw[kPix], dy[kPix];
+      const float b2dx = (a.w * dx) * 2.0f;
+      float q[kPix], dy[kPix];
       bool cand[kPix];
       bool any = false;
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
         dy[k] = a.y - pfy[k];
-        pw[k] = -0.5f * (adxx + b.x * dy[k] * dy[k]) - bdx * dy[k];
-        cand[k] = pos < last[k] && pw[k] <= 0.0f && pw[k] >= b.w;
+        q[k] = conic_q_px(adxx, b2dx, b.x, dy[k]);  // exponent = -0.5 q
+        cand[k] = pos < last[k] && q[k] >= 0.0f && q[k] <= b.w;
         any |= cand[k];
       }
       if (__ballot(any) == 0) continue;
-      // Blend decisions, identical to the forward's: above cutoff + 2e-3 the
-      // forward's alpha is provably >= 1/255 (the cutoff sits 1e-3 below
-      // -ln(255 o) and exp_sw / log_sw err by < 1e-6 relative), below the
-      // cutoff provably < 1/255; only the thin band between needs exp_sw.
-      // e = log2 of the Gaussian value G for pixels that blend, -inf (G = 0)
-      // for the others.
-      const float sure = b.w + kSureMargin;
+      // Blend decisions, identical to the forward's: with the exponent above
+      // power_cutoff + 2e-3 (q <= qcut - 4e-3) the forward's alpha is provably
+      // >= 1/255 (the cutoff sits 1e-3 below -ln(255 o) and exp_sw / log_sw
+      // err by < 1e-6 relative), above qcut provably < 1/255; only the thin
+      // band between needs exp_sw.  e = log2 of the Gaussian value G for
+      // pixels that blend, -inf (G = 0) for the others.
+      const float qsure = b.w - 2.0f * kSureMargin;
       float e[kPix];
       bool band_any = false;
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
-        e[k] = (cand[k] && pw[k] >= sure) ? pw[k] * kLog2e : -__builtin_inff();
-        band_any |= cand[k] && pw[k] < sure;
+        const bool sure = q[k] <= qsure;
+        e[k] = (cand[k] && sure) ? q[k] * (-0.5f * kLog2e) : -__builtin_inff();
+        band_any |= cand[k] && !sure;
       }
       if (__ballot(band_any) != 0) {
 #pragma unroll
         for (int k = 0; k < kPix; ++k) {
-          const bool band = cand[k] && pw[k] < sure;
-          const float a_sw = fminr(kAlphaMax, b.y * exp_sw_nonpos(band ? pw[k] : 0.0f));
-          e[k] = (band && a_sw >= kAlphaMin) ? pw[k] * kLog2e : e[k];
+          const bool band = cand[k] && !(q[k] <= qsure);
+          const float a_sw = fminr(kAlphaMax, b.y * exp_sw_nonpos(band ? -0.5f * q[k] : 0.0f));
+          e[k] = (band && a_sw >= kAlphaMin) ? q[k] * (-0.5f * kLog2e) : e[k];
         }
       }
       const float4 f = s_r2[jj];
@@ -314,7 +314,7 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
       if ((lane & 15) == 0) {
         // Lane 16 r adds row r's three components (zeros are skipped; the
         // depth component is zero when depth is off).
-        float* dst = p.grad_gauss + (size_t)s_id[jj] * kGradFloats;
+        float* dst = p.grad_gauss + (size_t)__builtin_amdgcn_readlane(batch_id, jj) * kGradFloats;
         const int r = lane >> 4;
         const int c0 = (r & 1) + 5 * (r >> 1);
         if (m[0] != 0.0f) unsafeAtomicAdd(dst + c0, m[0]);

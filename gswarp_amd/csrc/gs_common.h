@@ -63,11 +63,14 @@ constexpr int kConicMaskMaxTiles = 64;
 
 // Per-Gaussian render record, 48 bytes = three float4:
 //   r0 = (x, y, conic_a, conic_b)
-//   r1 = (conic_c, opacity, depth, power_cutoff)
+//   r1 = (conic_c, opacity, depth, qcut)
 //   r2 = (r, g, b, 0)
-// power_cutoff is the largest Gaussian exponent for which alpha is provably
-// below 1/255 (see power_cutoff()); the render loops skip the exponential
-// for smaller exponents without changing any decision.
+// The blend loops evaluate the Gaussian exponent of a pixel at offset
+// (dx, dy) = (x - px, y - py) as power = -0.5 q with the quadratic form
+//   q = fma(fma(c, dy, 2 b dx), dy, a dx dx)        (conic_q_px below)
+// and qcut = -2 power_cutoff (quad_cutoff()): a pixel with q > qcut has an
+// alpha provably below 1/255, so the loops skip its exponential without
+// changing any decision; 0 <= q <= qcut is the candidate test.
 constexpr int kRecordFloats = 12;
 
 __host__ __device__ __forceinline__ float fminr(float a, float b) { return a < b ? a : b; }
@@ -167,30 +170,42 @@ __device__ __forceinline__ float power_cutoff(float opacity) {
 }
 
 // Whether a render record can pass the blend loops' candidate test
-// power_cutoff <= power <= 0 at any pixel centre of the rectangle
-// [x0, x1] x [y0, y1].  The candidate set is the ellipse
-//   Q(d) = a dx^2 + 2 b dx dy + c dy^2 <= q,  q = -2 * power_cutoff,
-// whose bounding box has half-widths sqrt(q c / det) and sqrt(q a / det),
-// det = a c - b^2.  The loops evaluate the exponent in fp32: each of its
-// three terms carries a few ulp of relative error, and inside the box every
-// term is at most q * (a c / det), so the fp32 exponent can pass the test
-// only where the exact Q <= q (1 + 4 * 2^-24 * 3 * ac/det).  The box below
-// is computed in double (a c and b^2 are exact there) for q inflated ten
-// times that bound, plus 0.02 px; conics that are not positive definite or
-// so elongated (ac/det >= 1e5) that the bound is weak are never culled.
-// Returning true is always safe: it only costs the per-pixel test.
+// 0 <= q <= qcut at any pixel centre of the rectangle [x0, x1] x [y0, y1].
+// The candidate set is the ellipse
+//   Q(d) = a dx^2 + 2 b dx dy + c dy^2 <= qcut,
+// whose bounding box has half-widths sqrt(qcut c / det) and
+// sqrt(qcut a / det), det = a c - b^2.  The loops evaluate q in fp32 with
+// two fused multiply-adds over per-lane products: every rounding is
+// relative to a term of magnitude at most qcut * (a c / det) inside the box,
+// so the fp32 q can pass the test only where the exact Q <= qcut
+// (1 + 4 * 2^-24 * 3 * ac/det).  The box below is computed in double (a c
+// and b^2 are exact there) for qcut inflated ten times that bound, plus
+// 0.02 px; conics that are not positive definite or so elongated
+// (ac/det >= 1e5) that the bound is weak are never culled.  Returning true
+// is always safe: it only costs the per-pixel test.
 __device__ __forceinline__ bool record_may_touch(float4 r0, float4 r1, float x0, float x1, float y0, float y1) {
-  const float cutoff = r1.w;
-  if (cutoff > 0.0f) return false;  // alpha < 1/255 at every exponent <= 0
+  const float qcut = r1.w;
+  if (qcut < 0.0f) return false;  // alpha < 1/255 at every exponent <= 0
   const double a = r0.z, b = r0.w, c = r1.x;
   const double ac = a * c;
   const double det = ac - b * b;
   if (!(a > 0.0 && c > 0.0 && det > 0.0 && ac < 1.0e5 * det)) return true;
-  const double q = -2.0 * (double)cutoff * (1.0 + 8.0e-6 * (ac / det)) + 1.0e-6;
+  const double q = (double)qcut * (1.0 + 8.0e-6 * (ac / det)) + 1.0e-6;
   const double ex = sqrt(q * c / det) + 0.02;
   const double ey = sqrt(q * a / det) + 0.02;
   const double gx = r0.x, gy = r0.y;
   return !(gx + ex < (double)x0 || gx - ex > (double)x1 || gy + ey < (double)y0 || gy - ey > (double)y1);
+}
+
+// Largest quadratic form q at which alpha can still reach 1/255:
+// -2 * power_cutoff (exact scaling); -inf when it never can.
+__device__ __forceinline__ float quad_cutoff(float opacity) { return -2.0f * power_cutoff(opacity); }
+
+// The blend loops' quadratic form of a pixel offset, from the per-lane
+// adxx = (a dx) dx and b2dx = (b dx) 2 shared by a lane's pixels:
+// q = fma(fma(c, dy, b2dx), dy, adxx); the exponent is -0.5 q (exact).
+__device__ __forceinline__ float conic_q_px(float adxx, float b2dx, float c, float dy) {
+  return fmaf(fmaf(c, dy, b2dx), dy, adxx);
 }
 
 // Workgroups are dispatched round-robin over the eight XCDs (each with its

@@ -248,7 +248,7 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p)
         }
         float4* rec = p.records + 3 * (size_t)idx;
         rec[0] = make_float4(ptx, pty, q0, q1);
-        rec[1] = make_float4(q2, op, p_view_z, power_cutoff(op));
+        rec[1] = make_float4(q2, op, p_view_z, quad_cutoff(op));
         rec[2] = make_float4(col.x, col.y, col.z, 0.0f);
         if (p.clamped != nullptr) p.clamped[idx] = clamp_bits;
       }

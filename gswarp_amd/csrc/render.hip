@@ -16,10 +16,11 @@
 // Semantics follow render_kernels.py:16-147 (and flow_kernels.py:31-176 for
 // the flow variant):
 //   power > 0 skipped; alpha = min(0.99, o*exp(power)); alpha < 1/255 skipped;
+//   (power = -0.5 q with the record's quadratic form q, see gs_common.h)
 //   T*(1-alpha) < 1e-4 ends the pixel without blending that Gaussian;
 //   colour += f*alpha*T, alpha_out = sum alpha*T, depth = sum z*alpha*T;
 //   n_contrib = 1-based list index of the last blended Gaussian.
-// Exponents below the record's power_cutoff are skipped without evaluating
+// Quadratic forms above the record's qcut are skipped without evaluating
 // exp: their alpha is provably below 1/255, so no decision changes.
 #include "gs_common.h"
 #include "gs_capi.h"
@@ -133,22 +134,22 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
       const float4 b = s_r1[j];
       const float dx = a.x - pfx;
       const float adxx = a.z * dx * dx;
-      const float bdx = a.w * dx;
-      float pw[kPixPerLane], dy[kPixPerLane];
+      const float b2dx = (a.w * dx) * 2.0f;
+      float q[kPixPerLane], dy[kPixPerLane];
       bool cand[kPixPerLane];
       bool any = false;
 #pragma unroll
       for (int k = 0; k < kPixPerLane; ++k) {
         dy[k] = a.y - pfy[k];
-        pw[k] = -0.5f * (adxx + b.x * dy[k] * dy[k]) - bdx * dy[k];
-        cand[k] = T[k] > 0.0f && pw[k] <= 0.0f && pw[k] >= b.w;
+        q[k] = conic_q_px(adxx, b2dx, b.x, dy[k]);  // exponent = -0.5 q
+        cand[k] = T[k] > 0.0f && q[k] >= 0.0f && q[k] <= b.w;
         any |= cand[k];
       }
       if (__ballot(any) == 0) continue;
       const float4 f = s_r2[j];
 #pragma unroll
       for (int k = 0; k < kPixPerLane; ++k) {
-        const float alpha = fminr(kAlphaMax, b.y * exp_sw_nonpos(cand[k] ? pw[k] : 0.0f));
+        const float alpha = fminr(kAlphaMax, b.y * exp_sw_nonpos(cand[k] ? -0.5f * q[k] : 0.0f));
         const bool ok = cand[k] && alpha >= kAlphaMin;
         const float test_T = T[k] * (1.0f - alpha);
         const bool fin = ok && test_T < kTransmittanceMin;

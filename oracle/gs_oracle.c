@@ -695,6 +695,23 @@ void or_binning(int P, const int* radii, const float* depths, const int* tiles_t
 }
 
 /*
+ * Gaussian exponent of a pixel offset (render_kernels.py:120 and
+ * backward_kernels.py:643 via _compute_power, math_kernels.py:78-80):
+ *   power = -0.5 (a dx^2 + c dy^2) - b dx dy,  conic co = (a, b, c).
+ * Evaluated in this build's fixed fp32 form, the same in the gfx950 kernels:
+ * the quadratic form q = fma(fma(c, dy, (b dx) 2), dy, (a dx) dx) with two
+ * fused multiply-adds, and power = -0.5 q (exact).  The reference leaves the
+ * contraction of this expression to its GPU compiler, so no rounding order
+ * is fixed by it.
+ */
+static inline float blend_power(const float* co, float d_x, float d_y) {
+  const float adxx = co[0] * d_x * d_x;
+  const float b2dx = (co[1] * d_x) * 2.0f;
+  const float q = fmaf(fmaf(co[2], d_y, b2dx), d_y, adxx);
+  return -0.5f * q;
+}
+
+/*
  * _render_tiles_tiled256_warp_kernel (render_kernels.py:16-147), with the
  * flow auxiliaries of flow_kernels.py:159-166 when top_k > 0 (aux arrays
  * pre-filled with -1 / 0 / 0 as flow_ops.py:119-129 does).  The block-wide
@@ -730,7 +747,7 @@ void or_render_fwd(int W, int H, const int* ranges, const int* point_list, const
       const float* co = conic_opacity + 4 * id;
       const float d_x = points_xy[2 * id] - pixf_x;
       const float d_y = points_xy[2 * id + 1] - pixf_y;
-      const float power = -0.5f * (co[0] * d_x * d_x + co[2] * d_y * d_y) - co[1] * d_x * d_y;
+      const float power = blend_power(co, d_x, d_y);
       if (power <= 0.0f) {
         const float alpha = fmin_(0.99f, co[3] * or_exp(power));
         if (alpha >= (1.0f / 255.0f)) {
@@ -811,7 +828,7 @@ void or_render_bwd(int W, int H, int P_gauss, const int* ranges, const int* poin
         const float* co = conic_opacity + 4 * id;
         const float d_x = points_xy[2 * id] - pixf_x;
         const float d_y = points_xy[2 * id + 1] - pixf_y;
-        const float power = -0.5f * (co[0] * d_x * d_x + co[2] * d_y * d_y) - co[1] * d_x * d_y;
+        const float power = blend_power(co, d_x, d_y);
         if (!(power <= 0.0f)) continue;
         const float G = or_exp(power);
         const float alpha = fmin_(0.99f, co[3] * or_exp(power));
