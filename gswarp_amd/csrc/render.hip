@@ -18,7 +18,8 @@
 //   power > 0 skipped; alpha = min(0.99, o*exp(power)); alpha < 1/255 skipped;
 //   (power = -0.5 q with the record's quadratic form q, see gs_common.h)
 //   T*(1-alpha) < 1e-4 ends the pixel without blending that Gaussian;
-//   colour += f*alpha*T, alpha_out = sum alpha*T, depth = sum z*alpha*T;
+//   colour += f*alpha*T, alpha_out = sum alpha*T, depth = sum z*alpha*T
+//   (colour and depth accumulated with one fused multiply-add per Gaussian);
 //   n_contrib = 1-based list index of the last blended Gaussian.
 // Quadratic forms above the record's qcut are skipped without evaluating
 // exp: their alpha is provably below 1/255, so no decision changes.
@@ -72,7 +73,7 @@ __device__ __forceinline__ Batch load_batch(const RenderFwdParams& p, int first,
   return b;
 }
 
-template <bool kFlow, int kPixPerLane>
+template <bool kFlow, bool kDepth, int kPixPerLane>
 __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
   constexpr int kSubs = 4 / kPixPerLane;
   __shared__ float4 s_r0[64], s_r1[64], s_r2[64];
@@ -157,11 +158,11 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
         // A pixel that does not blend adds a contribution of exactly +0 (the
         // sums are unchanged bit for bit), which replaces per-output selects.
         const float contribution = blend ? alpha * T[k] : 0.0f;
-        c0[k] = c0[k] + f.x * contribution;
-        c1[k] = c1[k] + f.y * contribution;
-        c2[k] = c2[k] + f.z * contribution;
+        c0[k] = fmaf(f.x, contribution, c0[k]);
+        c1[k] = fmaf(f.y, contribution, c1[k]);
+        c2[k] = fmaf(f.z, contribution, c2[k]);
         ws[k] = ws[k] + contribution;
-        if (p.compute_depth) da[k] = da[k] + b.z * contribution;
+        if (kDepth) da[k] = fmaf(b.z, contribution, da[k]);
         if (aux && blend && nsucc[k] < p.top_k) {
           const size_t pix = (size_t)(py0 + 4 * k) * p.W + px;
           const size_t ai = (size_t)nsucc[k] * P + pix;
@@ -171,7 +172,8 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
           p.x_mu[(size_t)p.top_k * P + ai] = dy[k];
         }
         if (kFlow) nsucc[k] += blend ? 1 : 0;
-        T[k] = fin ? -T[k] : (blend ? test_T : T[k]);
+        const float Tb = blend ? test_T : T[k];
+        T[k] = fin ? -T[k] : Tb;
         last[k] = blend ? base + j + 1 : last[k];
       }
     }
@@ -204,10 +206,17 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
 
 static int launch_render_fwd(const RenderFwdParams& p, bool flow, hipStream_t s) {
   const dim3 grid(p.num_tiles * (4 / kFwdPix));
-  if (flow)
-    hipLaunchKernelGGL((render_fwd_kernel<true, kFwdPix>), grid, dim3(64), 0, s, p);
-  else
-    hipLaunchKernelGGL((render_fwd_kernel<false, kFwdPix>), grid, dim3(64), 0, s, p);
+  if (flow) {
+    if (p.compute_depth)
+      hipLaunchKernelGGL((render_fwd_kernel<true, true, kFwdPix>), grid, dim3(64), 0, s, p);
+    else
+      hipLaunchKernelGGL((render_fwd_kernel<true, false, kFwdPix>), grid, dim3(64), 0, s, p);
+  } else {
+    if (p.compute_depth)
+      hipLaunchKernelGGL((render_fwd_kernel<false, true, kFwdPix>), grid, dim3(64), 0, s, p);
+    else
+      hipLaunchKernelGGL((render_fwd_kernel<false, false, kFwdPix>), grid, dim3(64), 0, s, p);
+  }
   return gs_status_from_hip(hipGetLastError());
 }
 

@@ -754,11 +754,14 @@ void or_render_fwd(int W, int H, const int* ranges, const int* point_list, const
           const float test_T = T * (1.0f - alpha);
           if (test_T < 0.0001f) break;
           const float contribution = alpha * T;
-          color0 = color0 + features[3 * id] * contribution;
-          color1 = color1 + features[3 * id + 1] * contribution;
-          color2 = color2 + features[3 * id + 2] * contribution;
+          /* colour and depth accumulate with one fused multiply-add each (this
+           * build's fixed form; the reference leaves the contraction of
+           * C += f * (alpha T) to its GPU compiler) */
+          color0 = fmaf(features[3 * id], contribution, color0);
+          color1 = fmaf(features[3 * id + 1], contribution, color1);
+          color2 = fmaf(features[3 * id + 2], contribution, color2);
           weight = weight + contribution;
-          if (compute_depth) depth_acc = depth_acc + depths[id] * contribution;
+          if (compute_depth) depth_acc = fmaf(depths[id], contribution, depth_acc);
           if (top_k > 0 && n_success < top_k) {
             const long long aux = (long long)n_success * total + pixel_id;
             gs_per_pixel[aux] = id;
