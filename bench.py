@@ -165,6 +165,7 @@ STAGE_OF_KERNEL = (
     ("gs::duplicate_keys_kernel", "duplicate"),
     ("gs::duplicate_tiles_kernel", "duplicate"),
     ("gs_sort::", "sort"),
+    ("gs_seg::", "sort"),
     ("gs::zero_ranges_kernel", "ranges"),
     ("gs::tile_ranges_kernel", "ranges"),
     ("gs::tile_ranges_u32_kernel", "ranges"),
