@@ -6,9 +6,11 @@
 // divided by max(1-alpha, 1e-5) per blended Gaussian, reverse recurrences for
 // colour, depth and alpha, the background term, xy gradients scaled by W/2
 // and H/2, conic gradients with the -1/2 factor).  Per Gaussian each lane
-// sums its pixels' terms, the wave sums the ten components with a transposed
-// lane-swap/DPP reduction (skipped when no pixel of the wave blended it), and
-// one lane per row issues the global float atomics of its row's components.
+// sums its pixels' terms, two transposed lane-swap folds reduce the ten
+// components to 16 partial sums each, which are stored in a per-wave LDS
+// ring slot; a slot is reduced and sent to global memory with one float
+// atomic per component when it is reused (skipped when no pixel of the wave
+// blended the Gaussian).
 // The blend decisions are exactly the forward's (exp_sw is evaluated only in
 // a thin band above the record's power cutoff where the decision needs it);
 // gradient values use the hardware exponential and reciprocal.
@@ -37,15 +39,6 @@ __device__ __forceinline__ float dpp_mov(float src) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(src), kCtrl, kRowMask, 0xF, false));
 }
 
-// Sum over the 16 lanes of each row; every lane of the row receives the total.
-__device__ __forceinline__ float row_sum16(float v) {
-  v = v + dpp_mov<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
-  v = v + dpp_mov<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
-  v = v + dpp_mov<0x141, 0xF>(v);  // row_half_mirror
-  v = v + dpp_mov<0x140, 0xF>(v);  // row_mirror
-  return v;
-}
-
 // v_permlane32_swap exchanges lanes 32-63 of a with lanes 0-31 of b, so the
 // sum of the two results holds a[l] + a[l+32] in lanes 0-31 and
 // b[l-32] + b[l] in lanes 32-63: two half-wave partial sums for one add.
@@ -62,20 +55,57 @@ __device__ __forceinline__ float fold16(float a, float b) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Transposed wave reduction of ten per-lane values: two lane-swap folds
-// leave three registers whose four rows each carry one component, then one
-// row reduction per register (28 VALU operations instead of 60 for ten
-// separate wave sums).  Row r of m[0] holds component {0,1,5,6}[r], of m[1]
-// {2,3,7,8}[r], of m[2] {4,4,9,9}[r].
-__device__ __forceinline__ void wave_sum10(const float (&g)[10], float (&m)[3]) {
+// Partial transposed reduction of ten per-lane values: two lane-swap folds
+// leave three registers in which row r (lanes 16 r .. 16 r + 15) of
+// register i holds 16 partial sums (over 4 lanes each) of component
+// kSlotComp[4 i + r]; the duplicated rows of the third register are unused.
+__device__ __forceinline__ void wave_fold10(const float (&g)[10], float (&m)[3]) {
   const float h0 = fold32(g[0], g[5]);
   const float h1 = fold32(g[1], g[6]);
   const float h2 = fold32(g[2], g[7]);
   const float h3 = fold32(g[3], g[8]);
   const float h4 = fold32(g[4], g[9]);
-  m[0] = row_sum16(fold16(h0, h1));
-  m[1] = row_sum16(fold16(h2, h3));
-  m[2] = row_sum16(fold16(h4, h4));
+  m[0] = fold16(h0, h1);
+  m[1] = fold16(h2, h3);
+  m[2] = fold16(h4, h4);
+}
+
+// Per-wave LDS ring of Gaussian gradient slots.  A slot holds, for the 12
+// (register, row) positions p = 4 i + r of wave_fold10's output, the 16
+// partial sums of lanes 16 r .. 16 r + 15: float p * 16 + lane % 16, so the
+// three registers are stored at float offsets 0, 64 and 128 from
+// slot + lane (plain stores: the slot belongs to one Gaussian of one wave).
+// A slot is reduced (one float4 and a quad sum per position) and sent to
+// global memory with one atomic per component when it is about to be
+// reused, kRingSlots Gaussians later, and at the end of the tile, so the
+// wave never waits on its own LDS stores.
+constexpr int kRingSlots = 8;
+constexpr int kSlotFloats = 12 * 16;
+
+// Component at slot position p (-1: a duplicated row): {0, 1, 5, 6, 2, 3, 7,
+// 8, 4, -1, 9, -1}.
+__device__ __forceinline__ int slot_component(int p) {
+  const int i = p >> 2, r = p & 3;
+  if (i < 2) return 2 * i + (r & 1) + 5 * (r >> 1);
+  return (r & 1) ? -1 : 4 + 5 * (r >> 1);
+}
+
+// Reduces ring slot k and adds its components to grad_gauss[gid]: lanes
+// 0..47 read one float4 each (position lane / 4), sum it, and each quad of
+// lanes sums its position's four float4 sums; the quad's first lane issues
+// the atomic of a used, non-zero component.
+__device__ __forceinline__ void flush_slot(const float* ring, int k, int gid, int lane, int comp,
+                                           float* grad_gauss) {
+  const float4* slot = reinterpret_cast<const float4*>(ring + k * kSlotFloats);
+  float t = 0.0f;
+  if (lane < kSlotFloats / 4) {
+    const float4 v = slot[lane];
+    t = (v.x + v.y) + (v.z + v.w);
+  }
+  t = t + dpp_mov<0xB1, 0xF>(t);  // quad_perm [1,0,3,2]
+  t = t + dpp_mov<0x4E, 0xF>(t);  // quad_perm [2,3,0,1]
+  if ((lane & 3) == 0 && comp >= 0 && t != 0.0f)
+    unsafeAtomicAdd(grad_gauss + (size_t)gid * kGradFloats + comp, t);
 }
 
 __device__ __forceinline__ int wave_max_i32(int v) {
@@ -153,6 +183,7 @@ template <bool kDepth, int kPix>
 __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
   constexpr int kSubs = 4 / kPix;
   __shared__ float4 s_r0[64], s_r1[64], s_r2[64];
+  __shared__ float s_ring[kRingSlots * kSlotFloats];
   const int lane = threadIdx.x;
   const int2 ts = xcd_tile_sub(blockIdx.x, p.num_tiles, kSubs);
   const int tile = ts.x;
@@ -198,6 +229,9 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
   if (max_lc == 0) return;
   const float half_w = 0.5f * (float)p.W;
   const float half_h = 0.5f * (float)p.H;
+  const int flush_comp = lane < kSlotFloats / 4 ? slot_component(lane >> 2) : -1;
+  int nrel = 0;      // Gaussians added to the ring so far
+  int slot_gid = 0;  // lane k: Gaussian of ring slot k
   const float rx0 = (float)sx0, rx1 = (float)(sx0 + kBlockX - 1);
   const float ry0 = (float)sy0, ry1 = (float)(sy0 + 4 * kPix - 1);
 
@@ -310,19 +344,21 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
       g[8] = sb;
       g[9] = sd;
       float m[3];
-      wave_sum10(g, m);
-      if ((lane & 15) == 0) {
-        // Lane 16 r adds row r's three components (zeros are skipped; the
-        // depth component is zero when depth is off).
-        float* dst = p.grad_gauss + (size_t)__builtin_amdgcn_readlane(batch_id, jj) * kGradFloats;
-        const int r = lane >> 4;
-        const int c0 = (r & 1) + 5 * (r >> 1);
-        if (m[0] != 0.0f) unsafeAtomicAdd(dst + c0, m[0]);
-        if (m[1] != 0.0f) unsafeAtomicAdd(dst + c0 + 2, m[1]);
-        if ((r & 1) == 0 && m[2] != 0.0f) unsafeAtomicAdd(dst + 4 + 5 * (r >> 1), m[2]);
-      }
+      wave_fold10(g, m);
+      const int k = nrel & (kRingSlots - 1);
+      if (nrel >= kRingSlots)
+        flush_slot(s_ring, k, __builtin_amdgcn_readlane(slot_gid, k), lane, flush_comp, p.grad_gauss);
+      const int gid = __builtin_amdgcn_readlane(batch_id, jj);
+      slot_gid = lane == k ? gid : slot_gid;
+      float* slot = s_ring + k * kSlotFloats + lane;
+      slot[0] = m[0];
+      slot[64] = m[1];
+      slot[128] = m[2];
+      ++nrel;
     }
   }
+  for (int k = 0; k < imin(nrel, kRingSlots); ++k)
+    flush_slot(s_ring, k, __builtin_amdgcn_readlane(slot_gid, k), lane, flush_comp, p.grad_gauss);
 }
 
 struct PreprocessBwdParams {
