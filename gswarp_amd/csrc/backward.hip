@@ -78,8 +78,10 @@ __device__ __forceinline__ void wave_fold10(const float (&g)[10], float (&m)[3])
 // A slot is reduced (one float4 and a quad sum per position) and sent to
 // global memory with one atomic per component when it is about to be
 // reused, kRingSlots Gaussians later, and at the end of the tile, so the
-// wave never waits on its own LDS stores.
-constexpr int kRingSlots = 8;
+// wave never waits on its own LDS stores.  Two slots already put a whole
+// Gaussian's work between a store and its read-back; more slots cost LDS
+// and with it resident waves.
+constexpr int kRingSlots = 2;
 constexpr int kSlotFloats = 12 * 16;
 
 // Component at slot position p (-1: a duplicated row): {0, 1, 5, 6, 2, 3, 7,
