@@ -627,6 +627,12 @@ def backward(inputs: RasterInputs, radii: torch.Tensor, alpha: torch.Tensor, gra
         view_c = _f32c(inputs.viewmatrix)
         proj_c = _f32c(inputs.projmatrix)
         radii_c = radii.contiguous()
+        # The opacity and colour gradients are columns 5 and 6-8 of grad_gauss
+        # (the reference returns views of its render gradients,
+        # backward_ops.py:538-541); they are written out contiguously here so
+        # that autograd does not copy a strided view into each leaf.
+        grad_opacities = torch.empty((P,), **f)
+        grad_colors_out = torch.empty((P, NUM_CHANNELS), **f) if inputs.colors.numel() != 0 else None
         gp2 = _f32c_or_none(grad_proj_2d)
         gcon = _f32c_or_none(grad_conic_2d)
         gcov = _f32c_or_none(grad_conic_2d_inv)
@@ -641,12 +647,11 @@ def backward(inputs: RasterInputs, radii: torch.Tensor, alpha: torch.Tensor, gra
                 _lib.ptr(grad_scales) if cov_c is None else None,
                 _lib.ptr(grad_rotations) if cov_c is None else None,
                 _lib.ptr(grad_cov3d) if cov_c is not None else None,
-                grad_sh.data_ptr() if has_sh else None, None, None, stream)
-    grad_opacities = grad_gauss[:, 5:6]
-    if grad_opacities.shape != inputs.opacities.shape:
-        grad_opacities = grad_opacities.reshape(inputs.opacities.shape)
-    if inputs.colors.numel() != 0:
-        grad_colors = grad_gauss[:, 6:9].reshape(inputs.colors.shape)
+                grad_sh.data_ptr() if has_sh else None, grad_opacities.data_ptr(),
+                _lib.ptr(grad_colors_out), stream)
+    grad_opacities = grad_opacities.reshape(inputs.opacities.shape)
+    if grad_colors_out is not None:
+        grad_colors = grad_colors_out.reshape(inputs.colors.shape)
     if has_sh:
         grad_sh = grad_sh.reshape(inputs.sh.shape)
     if grad_cov3d.numel() != 0:

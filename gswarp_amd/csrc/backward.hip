@@ -391,6 +391,7 @@ struct PreprocessBwdParams {
   float* grad_sh;
   float* grad_opacity;
   float* grad_colors;
+  int sh_vec16;  // K == 16 and shs / grad_sh 16-byte aligned: float4 SH access
 };
 
 struct V3 {
@@ -400,9 +401,29 @@ struct V3 {
 __device__ __forceinline__ float dot3(V3 a, float b0, float b1, float b2) { return a.x * b0 + a.y * b1 + a.z * b2; }
 
 // SH colour backward for one Gaussian: writes its K x 3 block of grad_sh and
-// returns dL/dmean through the direction normalisation.
-__device__ __forceinline__ V3 sh_backward(const float* __restrict__ sh, float* __restrict__ gsh, int K, int degree,
-                                          float dirx, float diry, float dirz, float g0, float g1, float g2) {
+// returns dL/dmean through the direction normalisation.  With kVec16 the
+// block is K = 16 coefficients (48 floats, 16-byte aligned): it is read and
+// written as 12 float4 through registers, 4x fewer memory instructions than
+// per-float accesses, whose lanes would touch one cache line each.
+template <bool kVec16>
+__device__ __forceinline__ V3 sh_backward(const float* __restrict__ sh_mem, float* __restrict__ gsh_mem, int K,
+                                          int degree, float dirx, float diry, float dirz, float g0, float g1,
+                                          float g2) {
+  float sh_reg[kVec16 ? 48 : 1], gsh_reg[kVec16 ? 48 : 1];
+  if (kVec16) {
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+      const float4 v = reinterpret_cast<const float4*>(sh_mem)[i];
+      sh_reg[4 * i + 0] = v.x;
+      sh_reg[4 * i + 1] = v.y;
+      sh_reg[4 * i + 2] = v.z;
+      sh_reg[4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 48; ++i) gsh_reg[i] = 0.0f;
+  }
+  const float* sh = kVec16 ? sh_reg : sh_mem;
+  float* gsh = kVec16 ? gsh_reg : gsh_mem;
   const float len_sq = dirx * dirx + diry * diry + dirz * dirz;
   const float inv_len = 1.0f / sqrtf(fmaxr(len_sq, 1.0e-20f));
   const float x = dirx * inv_len, y = diry * inv_len, z = dirz * inv_len;
@@ -491,10 +512,17 @@ __device__ __forceinline__ V3 sh_backward(const float* __restrict__ sh, float* _
       }
     }
   }
-  for (int k = written; k < K; ++k) {
-    gsh[3 * k + 0] = 0.0f;
-    gsh[3 * k + 1] = 0.0f;
-    gsh[3 * k + 2] = 0.0f;
+  if (kVec16) {
+#pragma unroll
+    for (int i = 0; i < 12; ++i)
+      reinterpret_cast<float4*>(gsh_mem)[i] =
+          make_float4(gsh_reg[4 * i + 0], gsh_reg[4 * i + 1], gsh_reg[4 * i + 2], gsh_reg[4 * i + 3]);
+  } else {
+    for (int k = written; k < K; ++k) {
+      gsh[3 * k + 0] = 0.0f;
+      gsh[3 * k + 1] = 0.0f;
+      gsh[3 * k + 2] = 0.0f;
+    }
   }
   const float ddir0 = dot3(dx, g0, g1, g2);
   const float ddir1 = dot3(dy, g0, g1, g2);
@@ -723,11 +751,15 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(PreprocessBwdParams
       const float g1 = rcol1 * (1.0f - (float)((cl >> 1) & 1));
       const float g2 = rcol2 * (1.0f - (float)((cl >> 2) & 1));
       const float* sh = p.shs + (size_t)tid * (size_t)(3 * p.K);
-      const V3 gm = sh_backward(sh, gsh, p.K, p.degree, mx - p.campos[0], my - p.campos[1], mz - p.campos[2], g0,
-                                g1, g2);
+      const float dirx = mx - p.campos[0], diry = my - p.campos[1], dirz = mz - p.campos[2];
+      const V3 gm = p.sh_vec16 ? sh_backward<true>(sh, gsh, p.K, p.degree, dirx, diry, dirz, g0, g1, g2)
+                               : sh_backward<false>(sh, gsh, p.K, p.degree, dirx, diry, dirz, g0, g1, g2);
       gsh_x = gm.x;
       gsh_y = gm.y;
       gsh_z = gm.z;
+    } else if (p.sh_vec16) {
+#pragma unroll
+      for (int i = 0; i < 12; ++i) reinterpret_cast<float4*>(gsh)[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     } else {
       for (int k = 0; k < 3 * p.K; ++k) gsh[k] = 0.0f;
     }
@@ -852,6 +884,7 @@ extern "C" int gs_preprocess_bwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
   p.grad_sh = grad_sh;
   p.grad_opacity = grad_opacity;
   p.grad_colors = grad_colors;
+  p.sh_vec16 = (shs != nullptr && sh_coeffs == 16 && ((reinterpret_cast<uintptr_t>(shs) | reinterpret_cast<uintptr_t>(grad_sh)) & 15) == 0) ? 1 : 0;
   hipLaunchKernelGGL(gs::preprocess_bwd_kernel, dim3((P + 255) / 256), dim3(256), 0, (hipStream_t)stream, p);
   return gs_status_from_hip(hipGetLastError());
 }
