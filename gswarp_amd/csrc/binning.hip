@@ -237,35 +237,137 @@ __device__ __forceinline__ void for_each_covered_tile(float px, float py, float 
   }
 }
 
-// 64-bit keys: key = tile << tile_shift | depth_field, where depth_field
-// already holds the depth offset (and the packed point index when values is
-// null).  Writes stop at `limit` (the pair count the scan reported).
-__device__ __forceinline__ void emit_tiles(float px, float py, float ca, float cb, float cc, float opacity,
-                                           float cov_aa, float cov_cc, int radius, int grid_x, int grid_y,
-                                           int mode, unsigned long long depth_field, int tile_shift,
-                                           int point_id, long long off, long long limit,
-                                           unsigned long long* __restrict__ keys, int* __restrict__ values) {
-  for_each_covered_tile(px, py, ca, cb, cc, opacity, cov_aa, cov_cc, radius, grid_x, grid_y, mode, [&](int tile) {
-    if (off < limit) {
-      keys[off] = ((unsigned long long)tile << tile_shift) | depth_field;
-      if (values) values[off] = point_id;
-    }
-    ++off;
-  });
+// Emission is balanced per wave: a lane emits its own Gaussian's pairs when
+// it covers at most kLaneEmitMax tiles; the wave then takes its larger
+// Gaussians one at a time and emits each with its lanes in parallel, one
+// lane per band of the coverage walk (one tile row or column, whose interval
+// is computed exactly as the serial walk computes it) with a wave prefix sum
+// of the band lengths as output offsets, or one lane per tile of the
+// conic-rect masked case (at most 64 tiles).  The pairs land where the
+// serial walk of for_each_covered_tile puts them.  With the heavy tail of
+// large splats (a few hundred tiles each) a serial walk holds a whole wave
+// for the longest of its Gaussians.
+constexpr int kLaneEmitMax = 32;
+
+__device__ __forceinline__ float bcast_f(float v, int src) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
 }
 
-// (tile id, point index) pairs for the stable tile sort.
-__device__ __forceinline__ void emit_tile_ids(float px, float py, float ca, float cb, float cc, float opacity,
-                                              float cov_aa, float cov_cc, int radius, int grid_x, int grid_y,
-                                              int mode, int point_id, long long off, long long limit,
-                                              unsigned* __restrict__ tiles, int* __restrict__ values) {
-  for_each_covered_tile(px, py, ca, cb, cc, opacity, cov_aa, cov_cc, radius, grid_x, grid_y, mode, [&](int tile) {
-    if (off < limit) {
-      tiles[off] = (unsigned)tile;
-      values[off] = point_id;
+__device__ __forceinline__ int wave_inclusive_scan_i32(int x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  return x;
+}
+
+// One Gaussian's pairs written by the whole wave (all lanes hold the same
+// arguments).  write(position, tile id) stores one pair; positions start at
+// off and stop at limit.  Band tiles are first placed in the wave's LDS
+// window (stage, kEmitWindow entries) at their output positions, then
+// written out with consecutive lanes on consecutive positions, so each store
+// instruction covers a contiguous run instead of one cache line per lane.
+constexpr int kEmitWindow = 1024;
+
+template <typename W>
+__device__ __forceinline__ void wave_emit_gaussian(float px, float py, float ca, float cb, float cc, float opacity,
+                                                   float cov_aa, float cov_cc, int radius, int grid_x, int grid_y,
+                                                   int mode, long long off, long long limit, int* stage,
+                                                   W&& write) {
+  const int lane = threadIdx.x & 63;
+  const int4 rect = snugbox_rect(px, py, cov_aa, cov_cc, opacity, radius, grid_x, grid_y);
+  const int span_x = rect.z - rect.x;
+  const int span_y = rect.w - rect.y;
+  const int area = span_x * span_y;
+  const float threshold = coverage_threshold(opacity);
+  if (area > 1 && mode == kCoverageConicRect && area <= kConicMaskMaxTiles) {
+    // rect tiles in row-major order, one per lane; hits are compacted in lane order
+    const int tx = rect.x + (span_x > 0 ? lane % span_x : 0);
+    const int ty = rect.y + (span_x > 0 ? lane / span_x : 0);
+    const bool hit = lane < area && conic_rect_intersects_tile(px, py, ca, cb, cc, threshold, tx, ty);
+    const uint64_t m = __ballot(hit);
+    const long long pos = off + __popcll(m & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
+    if (hit && pos < limit) write(pos, ty * grid_x + tx);
+    return;
+  }
+  // bands: rows of the rect (full rect or AccuTile rows) or AccuTile columns
+  const bool full = area <= 1 || mode == kCoverageSnugbox;
+  const bool columns = !full && span_y > span_x;
+  const int nb = columns ? span_x : span_y;
+  long long base = off;
+  for (int b0 = 0; b0 < nb; b0 += 64) {
+    const int b = b0 + lane;
+    int lo = 0, hi = 0;
+    if (b < nb) {
+      if (full) {
+        lo = rect.x;
+        hi = rect.z;
+      } else if (!columns) {
+        const int2 iv = accutile_band(px, py, ca, cb, cc, threshold, rect.y + b, kBlockX, kBlockY, rect.x, rect.z);
+        lo = iv.x;
+        hi = iv.y;
+      } else {
+        const int2 iv = accutile_band(py, px, cc, cb, ca, threshold, rect.x + b, kBlockY, kBlockX, rect.y, rect.w);
+        lo = iv.x;
+        hi = iv.y;
+      }
     }
-    ++off;
-  });
+    const int len = imax(0, hi - lo);
+    const int incl = wave_inclusive_scan_i32(len);
+    const int excl = incl - len;
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+    // windows [w0, w0 + kEmitWindow) of this band chunk's total positions
+    for (int w0 = 0; w0 < total; w0 += kEmitWindow) {
+      const int k_begin = imax(0, w0 - excl);
+      const int k_end = imin(len, w0 + kEmitWindow - excl);
+      for (int k = k_begin; k < k_end; ++k) {
+        const int t = lo + k;
+        stage[excl + k - w0] = columns ? t * grid_x + (rect.x + b) : (rect.y + b) * grid_x + t;
+      }
+      __builtin_amdgcn_wave_barrier();
+      const int n = imin(kEmitWindow, total - w0);
+      for (int i = lane; i < n; i += 64) {
+        const long long pos = base + w0 + i;
+        if (pos < limit) write(pos, stage[i]);
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    base += total;
+  }
+}
+
+// Per wave: small Gaussians by their own lanes, then large ones by the wave.
+// `count` is the Gaussian's pair count (0 for lanes without one).
+// write_own(pos, tile) stores a pair of the calling lane's Gaussian;
+// write_from(src, pos, tile) one of lane src's Gaussian (src wave-uniform).
+template <typename WO, typename WF>
+__device__ __forceinline__ void emit_balanced(bool active, int count, float px, float py, float ca, float cb,
+                                              float cc, float opacity, float cov_aa, float cov_cc, int radius,
+                                              int grid_x, int grid_y, int mode, long long off, long long limit,
+                                              WO&& write_own, WF&& write_from) {
+  __shared__ int s_stage[256 / 64][kEmitWindow];  // one window per wave of the 256-thread workgroup
+  int* stage = s_stage[threadIdx.x >> 6];
+  const bool large = active && count > kLaneEmitMax;
+  if (active && !large) {
+    long long pos = off;
+    for_each_covered_tile(px, py, ca, cb, cc, opacity, cov_aa, cov_cc, radius, grid_x, grid_y, mode, [&](int tile) {
+      if (pos < limit) write_own(pos, tile);
+      ++pos;
+    });
+  }
+  uint64_t todo = __ballot(large);
+  while (todo != 0) {
+    const int src = __builtin_ctzll(todo);
+    todo &= todo - 1;
+    const long long soff = ((long long)__builtin_amdgcn_readlane((int)(off >> 32), src) << 32) |
+                           (unsigned)__builtin_amdgcn_readlane((int)off, src);
+    wave_emit_gaussian(bcast_f(px, src), bcast_f(py, src), bcast_f(ca, src), bcast_f(cb, src), bcast_f(cc, src),
+                       bcast_f(opacity, src), bcast_f(cov_aa, src), bcast_f(cov_cc, src),
+                       __builtin_amdgcn_readlane(radius, src), grid_x, grid_y, mode, soff, limit, stage,
+                       [&](long long pos, int tile) { write_from(src, pos, tile); });
+  }
 }
 
 __global__ __launch_bounds__(256) void duplicate_keys_kernel(int P, const int* __restrict__ radii,
@@ -277,18 +379,38 @@ __global__ __launch_bounds__(256) void duplicate_keys_kernel(int P, const int* _
                                                             unsigned long long* __restrict__ keys,
                                                             int* __restrict__ values) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= P) return;
-  const int radius = radii[idx];
-  if (radius <= 0) return;
-  const long long off = idx > 0 ? (long long)offsets[idx - 1] : 0;
-  const float4 r0 = records[3 * (size_t)idx + 0];
-  const float4 r1 = records[3 * (size_t)idx + 1];
-  const float cov_aa = cov2d[3 * idx + 0];
-  const float cov_cc = cov2d[3 * idx + 2];
-  const unsigned long long doff = (unsigned long long)(__float_as_uint(r1.z) - depth_min);
-  const unsigned long long field = (doff << value_bits) | (value_bits > 0 ? (unsigned long long)idx : 0ull);
-  emit_tiles(r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, cov_aa, cov_cc, radius, grid_x, grid_y, mode, field,
-             depth_bits + value_bits, idx, off, limit, keys, value_bits > 0 ? nullptr : values);
+  const int radius = idx < P ? radii[idx] : 0;
+  const bool active = radius > 0;
+  long long off = 0;
+  int count = 0;
+  float4 r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1 = r0;
+  float cov_aa = 0.0f, cov_cc = 0.0f;
+  unsigned long long field = 0;
+  if (active) {
+    off = idx > 0 ? (long long)offsets[idx - 1] : 0;
+    count = (int)((long long)offsets[idx] - off);
+    r0 = records[3 * (size_t)idx + 0];
+    r1 = records[3 * (size_t)idx + 1];
+    cov_aa = cov2d[3 * idx + 0];
+    cov_cc = cov2d[3 * idx + 2];
+    const unsigned long long doff = (unsigned long long)(__float_as_uint(r1.z) - depth_min);
+    field = (doff << value_bits) | (value_bits > 0 ? (unsigned long long)idx : 0ull);
+  }
+  const int tile_shift = depth_bits + value_bits;
+  const bool with_values = value_bits == 0;
+  emit_balanced(
+      active, count, r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, cov_aa, cov_cc, radius, grid_x, grid_y, mode, off, limit,
+      [&](long long pos, int tile) {
+        keys[pos] = ((unsigned long long)tile << tile_shift) | field;
+        if (with_values) values[pos] = idx;
+      },
+      [&](int src, long long pos, int tile) {
+        const unsigned long long f = ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)(field >> 32), src)
+                                      << 32) |
+                                     (unsigned)__builtin_amdgcn_readlane((int)field, src);
+        keys[pos] = ((unsigned long long)tile << tile_shift) | f;
+        if (with_values) values[pos] = __builtin_amdgcn_readlane(idx, src);
+      });
 }
 
 // Depth-sort input (binning_kernels.py:27-40 semantics): key = float bits of
@@ -314,18 +436,32 @@ __global__ __launch_bounds__(256) void duplicate_tiles_kernel(int P, const int* 
                                                              unsigned* __restrict__ tiles,
                                                              int* __restrict__ values) {
   const int j = blockIdx.x * blockDim.x + threadIdx.x;
-  if (j >= P) return;
-  const int idx = order[j];
-  if ((unsigned)idx >= (unsigned)P) return;  // never taken for a permutation
-  const int radius = radii[idx];
-  if (radius <= 0) return;
-  const long long off = j > 0 ? (long long)offsets[j - 1] : 0;
-  const float4 r0 = records[3 * (size_t)idx + 0];
-  const float4 r1 = records[3 * (size_t)idx + 1];
-  const float cov_aa = cov2d[3 * idx + 0];
-  const float cov_cc = cov2d[3 * idx + 2];
-  emit_tile_ids(r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, cov_aa, cov_cc, radius, grid_x, grid_y, mode, idx, off, limit,
-                tiles, values);
+  int idx = j < P ? order[j] : -1;
+  if ((unsigned)idx >= (unsigned)P) idx = -1;  // never taken for a permutation
+  const int radius = idx >= 0 ? radii[idx] : 0;
+  const bool active = radius > 0;
+  long long off = 0;
+  int count = 0;
+  float4 r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1 = r0;
+  float cov_aa = 0.0f, cov_cc = 0.0f;
+  if (active) {
+    off = j > 0 ? (long long)offsets[j - 1] : 0;
+    count = (int)((long long)offsets[j] - off);
+    r0 = records[3 * (size_t)idx + 0];
+    r1 = records[3 * (size_t)idx + 1];
+    cov_aa = cov2d[3 * idx + 0];
+    cov_cc = cov2d[3 * idx + 2];
+  }
+  emit_balanced(
+      active, count, r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, cov_aa, cov_cc, radius, grid_x, grid_y, mode, off, limit,
+      [&](long long pos, int tile) {
+        tiles[pos] = (unsigned)tile;
+        values[pos] = idx;
+      },
+      [&](int src, long long pos, int tile) {
+        tiles[pos] = (unsigned)tile;
+        values[pos] = __builtin_amdgcn_readlane(idx, src);
+      });
 }
 
 __global__ __launch_bounds__(256) void tile_ranges_u32_kernel(long long n, const unsigned* __restrict__ tiles,
