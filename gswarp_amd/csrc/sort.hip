@@ -1,9 +1,10 @@
 // Stable LSD radix sort of uint32 or uint64 keys (optionally with int32
 // values) for gfx950, on a bit field [lo_bit, lo_bit + key_bits) of the key.
 //
-// Per 8-bit digit pass (reduce-then-scan):
+// Per digit pass (reduce-then-scan; digits of at most 8 bits, the field split
+// evenly over ceil(bits / 8) passes):
 //   1. upsweep:   each 4096-element block counts its digits -> hist[digit][block].
-//   2. rowscan:   one wave per digit scans hist[digit][*] across blocks
+//   2. rowscan:   one workgroup per digit scans hist[digit][*] across blocks
 //                 (exclusive) and records the digit total.
 //   3. downsweep: each block ranks its elements stably, stages them in LDS in
 //                 digit order, and writes them out so that consecutive lanes
@@ -51,16 +52,19 @@ __device__ __forceinline__ unsigned block_exclusive_scan_u32(unsigned v, unsigne
   return wave_off + inc - v;
 }
 
-// Digit of a pass: bits [shift, shift + 8) of the key, restricted by dmask to
-// the sorted field in the last pass (bits above the field take no part).
+// Digit of a pass: bits [shift, shift + width) of the key, dmask = 2^width - 1
+// (bits above the pass's digit take no part).
 template <typename K>
 __device__ __forceinline__ unsigned digit_of(K key, int shift, unsigned dmask) {
   return (unsigned)(key >> shift) & dmask;
 }
 
-static inline unsigned pass_digit_mask(int key_bits, int pass) {
-  const int bits = key_bits - 8 * pass;
-  return bits >= 8 ? 0xFFu : ((1u << bits) - 1u);
+// Digit width of pass `pass` of `passes`: the key_bits are split as evenly as
+// possible (13 bits: 7 + 6, 26: 7 + 7 + 6 + 6), never above 8.  Narrow
+// digits mean fewer destination runs per block in the scatter, and the
+// passes with wide digits are the ones whose writes scatter the most.
+static inline int pass_digit_bits(int key_bits, int passes, int pass) {
+  return key_bits / passes + (pass < key_bits % passes ? 1 : 0);
 }
 
 // Lanes of the wave holding the same digit d as this lane (among valid lanes).
@@ -113,44 +117,33 @@ __global__ __launch_bounds__(kThreads) void upsweep_kernel(const K* __restrict__
   unsigned c = 0;
 #pragma unroll
   for (int k = 0; k < kCopies; ++k) c += h[k * kCopyStride + d];
-  hist[(size_t)d * nb + blockIdx.x] = c;
+  if ((unsigned)d <= dmask) hist[(size_t)d * nb + blockIdx.x] = c;
 }
 
-// One wave per digit row: hist[d][*] becomes its exclusive prefix over blocks
-// and digit_totals[d] the row total.  Lanes take 16 consecutive entries each,
-// so a row of up to 1024 blocks is one round of loads.
+// One workgroup per digit row: hist[d][*] becomes its exclusive prefix over
+// blocks and digit_totals[d] the row total.  Thread t owns a contiguous
+// segment of the row: it sums the segment, the workgroup scans the 256
+// segment sums, and a second pass over the segment writes the prefixes, so
+// a row of tens of thousands of blocks is two parallel sweeps rather than a
+// chain of dependent chunks.
 __global__ __launch_bounds__(kThreads) void rowscan_kernel(int nb, unsigned* __restrict__ hist,
                                                           unsigned* __restrict__ digit_totals) {
-  constexpr int kPer = 16;
-  const int lane = threadIdx.x & 63;
-  const int d = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  __shared__ unsigned s_lds_w[kWaves];
+  const int d = blockIdx.x;
   unsigned* row = hist + (size_t)d * nb;
-  unsigned carry = 0;
-  for (int base = 0; base < nb; base += 64 * kPer) {
-    unsigned v[kPer];
-    unsigned sum = 0;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int idx = base + lane * kPer + i;
-      v[i] = idx < nb ? row[idx] : 0u;
-      sum += v[i];
-    }
-    unsigned inc = sum;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const unsigned t = __shfl_up(inc, off, 64);
-      if (lane >= off) inc += t;
-    }
-    unsigned run = carry + inc - sum;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int idx = base + lane * kPer + i;
-      if (idx < nb) row[idx] = run;
-      run += v[i];
-    }
-    carry += __shfl(inc, 63, 64);
+  const int seg = (nb + kThreads - 1) / kThreads;
+  const int begin = threadIdx.x * seg;
+  const int end = begin + seg < nb ? begin + seg : nb;
+  unsigned sum = 0;
+  for (int i = begin; i < end; ++i) sum += row[i];
+  unsigned total;
+  unsigned run = block_exclusive_scan_u32(sum, s_lds_w, &total);
+  for (int i = begin; i < end; ++i) {
+    const unsigned v = row[i];
+    row[i] = run;
+    run += v;
   }
-  if (lane == 0) digit_totals[d] = carry;
+  if (threadIdx.x == 0) digit_totals[d] = total;
 }
 
 template <typename K, bool kValues>
@@ -217,10 +210,12 @@ __global__ __launch_bounds__(kThreads) void downsweep_kernel(const K* __restrict
     }
     unsigned tot;
     const unsigned dstart = block_exclusive_scan_u32(run, s_lds_w, &tot);
+    // digits above dmask do not occur in this pass (no table rows exist)
+    const bool used = (unsigned)d <= dmask;
     unsigned gtot;
-    const unsigned gstart = block_exclusive_scan_u32(digit_totals[d], s_lds_w, &gtot);
+    const unsigned gstart = block_exclusive_scan_u32(used ? digit_totals[d] : 0u, s_lds_w, &gtot);
     s_dstart[d] = dstart;
-    s_gbase[d] = (long long)gstart + (long long)hist[(size_t)d * nb + blockIdx.x] - (long long)dstart;
+    s_gbase[d] = (long long)gstart + (long long)(used ? hist[(size_t)d * nb + blockIdx.x] : 0u) - (long long)dstart;
   }
   __syncthreads();
 
@@ -280,14 +275,16 @@ static int gs_sort::sort_impl(int64_t n, int32_t lo_bit, int32_t key_bits, K* ki
   unsigned* hist = reinterpret_cast<unsigned*>(scratch);
   unsigned* digit_totals = hist + (size_t)nb * kRadix;
   const int passes = gs_passes_for_bits(key_bits);
+  int shift = lo_bit;
   for (int pass = 0; pass < passes; ++pass) {
-    const int shift = lo_bit + pass * 8;
-    const unsigned dmask = pass_digit_mask(key_bits, pass);
+    const int bits = pass_digit_bits(key_bits, passes, pass);
+    const unsigned dmask = (1u << bits) - 1u;
     hipLaunchKernelGGL((upsweep_kernel<K>), dim3(nb), dim3(kThreads), 0, s, kin, (long long)n, shift, dmask, nb,
                        hist);
-    hipLaunchKernelGGL(rowscan_kernel, dim3(kRadix / kWaves), dim3(kThreads), 0, s, nb, hist, digit_totals);
+    hipLaunchKernelGGL(rowscan_kernel, dim3(dmask + 1), dim3(kThreads), 0, s, nb, hist, digit_totals);
     hipLaunchKernelGGL((downsweep_kernel<K, kValues>), dim3(nb), dim3(kThreads), 0, s, kin, vin, kout, vout,
                        (long long)n, shift, dmask, nb, hist, digit_totals);
+    shift += bits;
     K* tk = kin;
     kin = kout;
     kout = tk;

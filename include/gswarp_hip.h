@@ -160,7 +160,8 @@ int gs_duplicate_tiles(int32_t P, const int32_t* order, const int32_t* radii, co
                        int32_t* values_out, void* stream);
 
 /*
- * Stable LSD radix sorts, 8 bits per pass, ping-ponging between the primary
+ * Stable LSD radix sorts in gs_sort_num_passes(key_bits) = ceil(key_bits / 8)
+ * passes of at most 8 bits (the field split evenly), ping-ponging between the primary
  * and the _alt buffers: the result ends in the primary buffers when
  * gs_sort_num_passes(key_bits) is even, else in the _alt ones.
  * gs_sort_pairs_u64 sorts (uint64 key, int32 value) pairs on the low
