@@ -464,22 +464,51 @@ __global__ __launch_bounds__(256) void duplicate_tiles_kernel(int P, const int* 
       });
 }
 
-__global__ __launch_bounds__(256) void tile_ranges_u32_kernel(long long n, const unsigned* __restrict__ tiles,
-                                                             int num_tiles, int2* __restrict__ ranges) {
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const unsigned tile = tiles[i];
-  if (tile >= (unsigned)num_tiles) return;  // never taken for ids from duplicate_tiles_kernel
-  if (i == 0) {
-    ranges[tile].x = 0;
-  } else {
-    const unsigned prev = tiles[i - 1];
-    if (tile != prev) {
-      if (prev < (unsigned)num_tiles) ranges[prev].y = (int)i;
-      ranges[tile].x = (int)i;
+// Tile boundaries of sorted tile ids, kRangeItems consecutive pairs per
+// thread (vector loads; the pair before the thread's run is one extra load):
+// at a change from tile a to tile b at position i, ranges[a].y = i and
+// ranges[b].x = i; the first pair starts its tile at 0 and the last ends its
+// tile at n.
+constexpr int kRangeItems = 8;
+
+__device__ __forceinline__ void mark_ranges(long long i0, int cnt, const unsigned (&t)[kRangeItems], unsigned prev,
+                                            long long n, int num_tiles, int2* __restrict__ ranges) {
+#pragma unroll
+  for (int k = 0; k < kRangeItems; ++k) {
+    if (k < cnt) {
+      const long long i = i0 + k;
+      const unsigned tile = t[k];
+      if (tile < (unsigned)num_tiles) {  // always true for ids from the emission kernels
+        if (i == 0) {
+          ranges[tile].x = 0;
+        } else if (tile != prev) {
+          if (prev < (unsigned)num_tiles) ranges[prev].y = (int)i;
+          ranges[tile].x = (int)i;
+        }
+        if (i == n - 1) ranges[tile].y = (int)n;
+      }
+      prev = tile;
     }
   }
-  if (i == n - 1) ranges[tile].y = (int)n;
+}
+
+__global__ __launch_bounds__(256) void tile_ranges_u32_kernel(long long n, const unsigned* __restrict__ tiles,
+                                                             int num_tiles, int2* __restrict__ ranges) {
+  const long long i0 = ((long long)blockIdx.x * blockDim.x + threadIdx.x) * kRangeItems;
+  if (i0 >= n) return;
+  const int cnt = (int)(n - i0 < kRangeItems ? n - i0 : kRangeItems);
+  unsigned t[kRangeItems];
+  if (cnt == kRangeItems) {
+    const uint4 a = reinterpret_cast<const uint4*>(tiles + i0)[0];
+    const uint4 b = reinterpret_cast<const uint4*>(tiles + i0)[1];
+    t[0] = a.x; t[1] = a.y; t[2] = a.z; t[3] = a.w;
+    t[4] = b.x; t[5] = b.y; t[6] = b.z; t[7] = b.w;
+  } else {
+#pragma unroll
+    for (int k = 0; k < kRangeItems; ++k) t[k] = k < cnt ? tiles[i0 + k] : 0u;
+  }
+  const unsigned prev = i0 > 0 ? tiles[i0 - 1] : 0xFFFFFFFFu;
+  mark_ranges(i0, cnt, t, prev, n, num_tiles, ranges);
 }
 
 __global__ void zero_info_kernel(long long* p) {
@@ -492,26 +521,45 @@ __global__ __launch_bounds__(256) void zero_ranges_kernel(int n2, int* __restric
 }
 
 // ranges[t] = [start, end) of tile t in the sorted keys (tile = key >> tile_shift);
-// with value_bits > 0 also unpacks point_list[i] = low value_bits of key i.
+// with value_bits > 0 and point_list given also unpacks point_list[i] = low
+// value_bits of key i.  kRangeItems keys per thread, as above.
 __global__ __launch_bounds__(256) void tile_ranges_kernel(long long n, const unsigned long long* __restrict__ keys,
                                                          int tile_shift, int value_bits, int num_tiles,
                                                          int2* __restrict__ ranges, int* __restrict__ point_list) {
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const unsigned long long k = keys[i];
-  if (value_bits > 0) point_list[i] = (int)(k & ((1ull << value_bits) - 1ull));
-  const unsigned long long tile = k >> tile_shift;
-  if (tile >= (unsigned long long)num_tiles) return;  // never taken for keys from gs_duplicate_keys
-  if (i == 0) {
-    ranges[tile].x = 0;
-  } else {
-    const unsigned long long prev = keys[i - 1] >> tile_shift;
-    if (tile != prev) {
-      if (prev < (unsigned long long)num_tiles) ranges[prev].y = (int)i;
-      ranges[tile].x = (int)i;
+  const long long i0 = ((long long)blockIdx.x * blockDim.x + threadIdx.x) * kRangeItems;
+  if (i0 >= n) return;
+  const int cnt = (int)(n - i0 < kRangeItems ? n - i0 : kRangeItems);
+  unsigned long long k64[kRangeItems];
+  if (cnt == kRangeItems) {
+#pragma unroll
+    for (int q = 0; q < kRangeItems / 2; ++q) {
+      const ulonglong2 v = reinterpret_cast<const ulonglong2*>(keys + i0)[q];
+      k64[2 * q] = v.x;
+      k64[2 * q + 1] = v.y;
     }
+  } else {
+#pragma unroll
+    for (int k = 0; k < kRangeItems; ++k) k64[k] = k < cnt ? keys[i0 + k] : 0ull;
   }
-  if (i == n - 1) ranges[tile].y = (int)n;
+  // tile ids as 32-bit values; ids too large for the grid map above num_tiles
+  unsigned t[kRangeItems];
+#pragma unroll
+  for (int k = 0; k < kRangeItems; ++k) {
+    const unsigned long long tile = k64[k] >> tile_shift;
+    t[k] = tile < (unsigned long long)num_tiles ? (unsigned)tile : 0xFFFFFFFFu;
+  }
+  if (value_bits > 0 && point_list != nullptr) {
+    const unsigned long long vmask = (1ull << value_bits) - 1ull;
+#pragma unroll
+    for (int k = 0; k < kRangeItems; ++k)
+      if (k < cnt) point_list[i0 + k] = (int)(k64[k] & vmask);
+  }
+  unsigned prev = 0xFFFFFFFFu;
+  if (i0 > 0) {
+    const unsigned long long ptile = keys[i0 - 1] >> tile_shift;
+    prev = ptile < (unsigned long long)num_tiles ? (unsigned)ptile : 0xFFFFFFFFu;
+  }
+  mark_ranges(i0, cnt, t, prev, n, num_tiles, ranges);
 }
 
 }  // namespace gs
@@ -609,7 +657,8 @@ extern "C" int gs_tile_ranges(int64_t n, const uint64_t* sorted_keys, int32_t ti
   hipLaunchKernelGGL(gs::zero_ranges_kernel, dim3((n2 + 255) / 256), dim3(256), 0, s, n2, ranges);
   if (n > 0) {
     if (!sorted_keys || (value_bits > 0 && !point_list)) return GS_ERR_INVALID_ARGUMENT;
-    hipLaunchKernelGGL(gs::tile_ranges_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (long long)n,
+    const long long threads = (n + gs::kRangeItems - 1) / gs::kRangeItems;
+    hipLaunchKernelGGL(gs::tile_ranges_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, (long long)n,
                        reinterpret_cast<const unsigned long long*>(sorted_keys), tile_shift, value_bits, num_tiles,
                        reinterpret_cast<int2*>(ranges), point_list);
   }
@@ -653,7 +702,8 @@ extern "C" int gs_tile_ranges_u32(int64_t n, const uint32_t* sorted_tiles, int32
   hipLaunchKernelGGL(gs::zero_ranges_kernel, dim3((n2 + 255) / 256), dim3(256), 0, s, n2, ranges);
   if (n > 0) {
     if (!sorted_tiles) return GS_ERR_INVALID_ARGUMENT;
-    hipLaunchKernelGGL(gs::tile_ranges_u32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+    const long long threads = (n + gs::kRangeItems - 1) / gs::kRangeItems;
+    hipLaunchKernelGGL(gs::tile_ranges_u32_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
                        (long long)n, sorted_tiles, num_tiles, reinterpret_cast<int2*>(ranges));
   }
   return gs_status_from_hip(hipGetLastError());
