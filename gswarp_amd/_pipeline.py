@@ -641,7 +641,8 @@ def backward(inputs: RasterInputs, radii: torch.Tensor, alpha: torch.Tensor, gra
                 "gs_preprocess_bwd", P, K, int(inputs.degree), means_c.data_ptr(), _lib.ptr(scales_c),
                 _lib.ptr(rot_c), _lib.ptr(cov_c), float(inputs.scale_modifier), _lib.ptr(shs), campos_c.data_ptr(),
                 view_c.data_ptr(), proj_c.data_ptr(), tanfovx, tanfovy, _focal(W, tanfovx), _focal(H, tanfovy),
-                radii_c.data_ptr(), pre.clamped.data_ptr(), grad_gauss.data_ptr(), _lib.ptr(gp2), _lib.ptr(gcon),
+                radii_c.data_ptr(), pre.clamped.data_ptr(), grad_gauss.data_ptr(), pre.records.data_ptr(), W, H,
+                _lib.ptr(gp2), _lib.ptr(gcon),
                 _lib.ptr(gcov), int(bool(flow_double)), float(inputs.filter_variance), grad_means3d.data_ptr(),
                 grad_means2d.data_ptr(),
                 _lib.ptr(grad_scales) if cov_c is None else None,

@@ -4,9 +4,9 @@
 // tile's list back to front from the largest n_contrib of their pixels
 // (backward_kernels.py:539-707 semantics: T starts at 1 - alpha_out and is
 // divided by max(1-alpha, 1e-5) per blended Gaussian, reverse recurrences for
-// colour, depth and alpha, the background term, xy gradients scaled by W/2
-// and H/2, conic gradients with the -1/2 factor).  Per Gaussian each lane
-// sums its pixels' terms, two transposed lane-swap folds reduce the ten
+// colour, depth and alpha, the background term).  Per Gaussian each lane
+// sums its pixels' pixel moments and colour / depth terms, two transposed
+// lane-swap folds reduce the ten
 // components to 16 partial sums each, which are stored in a per-wave LDS
 // ring slot; a slot is reduced and sent to global memory with one float
 // atomic per component when it is reused (skipped when no pixel of the wave
@@ -15,7 +15,10 @@
 // a thin band above the record's power cutoff where the decision needs it);
 // gradient values use the hardware exponential and reciprocal.
 //
-// preprocess_bwd: one thread per Gaussian fusing the SH colour backward
+// preprocess_bwd: one thread per Gaussian forming the xy and conic render
+// gradients from the moments (the W/2, H/2 and -1/2 factors of
+// backward_kernels.py:678-685 with the record's conic and opacity), fusing
+// the SH colour backward
 // (backward_kernels.py:298-536), the projected-mean / depth backward
 // (backward_kernels.py:89-112), the cov2D -> cov3D -> scale/rotation backward
 // (backward_kernels.py:114-287) and the accumulation (backward_kernels.py:289-295).
@@ -29,6 +32,8 @@ namespace gs {
 constexpr int kGradFloats = 10;  // dx, dy, conic a, b, c, opacity, r, g, b, depth
 constexpr float kSureMargin = 2.0e-3f;  // exponents this far above the cutoff always blend
 constexpr float kLog2e = 1.44269504088896341f;
+// Comparison predicates of the lane-mask compare builtins (LLVM's codes).
+constexpr int kCmpOGE = 3, kCmpOLE = 5, kCmpSLT = 40;
 #ifndef GS_BWD_PIX
 #define GS_BWD_PIX 2
 #endif
@@ -82,7 +87,9 @@ __device__ __forceinline__ void wave_fold10(const float (&g)[10], float (&m)[3])
 // Gaussian's work between a store and its read-back; more slots cost LDS
 // and with it resident waves.
 constexpr int kRingSlots = 2;
+static_assert(kRingSlots == 2, "the ring's Gaussian ids are kept in two scalar registers");
 constexpr int kSlotFloats = 12 * 16;
+constexpr int kRingPad = 64 * 4 - kSlotFloats;  // a whole wave's float4 read of the last slot
 
 // Component at slot position p (-1: a duplicated row): {0, 1, 5, 6, 2, 3, 7,
 // 8, 4, -1, 9, -1}.
@@ -92,18 +99,16 @@ __device__ __forceinline__ int slot_component(int p) {
   return (r & 1) ? -1 : 4 + 5 * (r >> 1);
 }
 
-// Reduces ring slot k and adds its components to grad_gauss[gid]: lanes
-// 0..47 read one float4 each (position lane / 4), sum it, and each quad of
-// lanes sums its position's four float4 sums; the quad's first lane issues
-// the atomic of a used, non-zero component.
+// Reduces ring slot k and adds its components to grad_gauss[gid]: lane l
+// reads float4 l of the slot (position l / 4 for l < 48), sums it, and each
+// quad of lanes sums its position's four float4 sums; the quad's first lane
+// issues the atomic of a used, non-zero component.
 __device__ __forceinline__ void flush_slot(const float* ring, int k, int gid, int lane, int comp,
                                            float* grad_gauss) {
-  const float4* slot = reinterpret_cast<const float4*>(ring + k * kSlotFloats);
-  float t = 0.0f;
-  if (lane < kSlotFloats / 4) {
-    const float4 v = slot[lane];
-    t = (v.x + v.y) + (v.z + v.w);
-  }
+  // Every lane reads a float4 (the ring is padded so that lanes 48-63 of
+  // the last slot stay inside it); those lanes hold no component.
+  const float4 v = reinterpret_cast<const float4*>(ring + k * kSlotFloats)[lane];
+  float t = (v.x + v.y) + (v.z + v.w);
   t = t + dpp_mov<0xB1, 0xF>(t);  // quad_perm [1,0,3,2]
   t = t + dpp_mov<0x4E, 0xF>(t);  // quad_perm [2,3,0,1]
   if ((lane & 3) == 0 && comp >= 0 && t != 0.0f)
@@ -172,20 +177,22 @@ __device__ __forceinline__ BwdBatch load_bwd_batch(const RenderBwdParams& p, int
 // same recurrence started from S = bg . dL/dcolour instead of 0 (the
 // background is an opaque layer behind the last Gaussian; 1 - alpha >= 0.01
 // since alpha <= 0.99, so the 1e-5 floor never applies to it).  Per
-// Gaussian each lane then sums its pixels' contributions, using
-//   v = G * dL/dalpha_hat per pixel,
-//   dL/dxy    = -(W/2, H/2) * o * (a dx sum(v) + b sum(v dy), c sum(v dy) + b dx sum(v)),
-//   dL/dconic = -1/2 * o * (dx^2 sum(v), dx sum(v dy), sum(v dy^2)),
-//   dL/dopacity = sum(v),
-// the reference's per-pixel expressions summed over pixels sharing dx; then
-// the ten per-lane components are summed over the wave.  Each batch of 64
+// Gaussian each lane then sums, with v = G * dL/dalpha_hat per pixel, the
+// moments (v dx, v dy, v dx^2, v dx dy, v dy^2, v) over its pixels (they
+// share dx) and the colour and depth terms alpha T dL/dpixel; the ten
+// per-lane components are summed over the wave and added to grad_gauss.
+// The per-Gaussian backward forms the reference's per-pixel expressions
+// summed over pixels from the moments:
+//   dL/dxy    = -(W/2, H/2) * o * (a sum(v dx) + b sum(v dy), c sum(v dy) + b sum(v dx)),
+//   dL/dconic = -1/2 * o * (sum(v dx^2), sum(v dx dy), sum(v dy^2)),
+//   dL/dopacity = sum(v).  Each batch of 64
 // records is first tested lane-parallel against the slice rectangle
 // (record_may_touch) and only records that may touch it are visited.
 template <bool kDepth, int kPix>
 __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
   constexpr int kSubs = 4 / kPix;
   __shared__ float4 s_r0[64], s_r1[64], s_r2[64];
-  __shared__ float s_ring[kRingSlots * kSlotFloats];
+  __shared__ __align__(16) float s_ring[kRingSlots * kSlotFloats + kRingPad];
   const int lane = threadIdx.x;
   const int2 ts = xcd_tile_sub(blockIdx.x, p.num_tiles, kSubs);
   const int tile = ts.x;
@@ -229,11 +236,9 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
   }
   const int max_lc = __builtin_amdgcn_readfirstlane(wave_max_i32(lmax));
   if (max_lc == 0) return;
-  const float half_w = 0.5f * (float)p.W;
-  const float half_h = 0.5f * (float)p.H;
   const int flush_comp = lane < kSlotFloats / 4 ? slot_component(lane >> 2) : -1;
-  int nrel = 0;      // Gaussians added to the ring so far
-  int slot_gid = 0;  // lane k: Gaussian of ring slot k
+  int nrel = 0;  // Gaussians added to the ring so far
+  int slot_gid0 = 0, slot_gid1 = 0;  // Gaussians of ring slots 0 and 1 (wave-uniform)
   const float rx0 = (float)sx0, rx1 = (float)(sx0 + kBlockX - 1);
   const float ry0 = (float)sy0, ry1 = (float)(sy0 + 4 * kPix - 1);
 
@@ -277,22 +282,26 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
       // >= 1/255 (the cutoff sits 1e-3 below -ln(255 o) and exp_sw / log_sw
       // err by < 1e-6 relative), above qcut provably < 1/255; only the thin
       // band between needs exp_sw.  e = log2 of the Gaussian value G for
-      // pixels that blend, -inf (G = 0) for the others.
+      // pixels that blend, -inf (G = 0) for the others.  The band test is a
+      // lane-mask operation on the two comparisons.
       const float qsure = b.w - 2.0f * kSureMargin;
       float e[kPix];
-      bool band_any = false;
+      uint64_t band = 0;  // lanes with a pixel in the band
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
         const bool sure = q[k] <= qsure;
         e[k] = (cand[k] && sure) ? q[k] * (-0.5f * kLog2e) : -__builtin_inff();
-        band_any |= cand[k] && !sure;
+        // cand && !sure from the comparisons' lane masks (scalar ANDs; the
+        // compiler reuses the comparisons made above)
+        band |= __builtin_amdgcn_sicmp(pos, last[k], kCmpSLT) & __builtin_amdgcn_fcmpf(q[k], 0.0f, kCmpOGE) &
+                __builtin_amdgcn_fcmpf(q[k], b.w, kCmpOLE) & ~__builtin_amdgcn_fcmpf(q[k], qsure, kCmpOLE);
       }
-      if (__ballot(band_any) != 0) {
+      if (band != 0) {
 #pragma unroll
         for (int k = 0; k < kPix; ++k) {
-          const bool band = cand[k] && !(q[k] <= qsure);
-          const float a_sw = fminr(kAlphaMax, b.y * exp_sw_nonpos(band ? -0.5f * q[k] : 0.0f));
-          e[k] = (band && a_sw >= kAlphaMin) ? q[k] * (-0.5f * kLog2e) : e[k];
+          const bool in_band = cand[k] && !(q[k] <= qsure);
+          const float a_sw = fminr(kAlphaMax, b.y * exp_sw_nonpos(in_band ? -0.5f * q[k] : 0.0f));
+          e[k] = (in_band && a_sw >= kAlphaMin) ? q[k] * (-0.5f * kLog2e) : e[k];
         }
       }
       const float4 f = s_r2[jj];
@@ -305,11 +314,13 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
         // alpha = 0, T * rcp(1) = T, S is unchanged and it adds exact zeros.
         const float G = __builtin_amdgcn_exp2f(e[k]);
         const float alpha = fminf(kAlphaMax, b.y * G);
+        // 1 - alpha >= 1 - kAlphaMax: the reference's 1e-5 floor never applies
         const float oma = 1.0f - alpha;
-        const float Tn = T[k] * __builtin_amdgcn_rcpf(fmaxr(oma, kOneMinusAlphaMin));
+        const float Tn = T[k] * __builtin_amdgcn_rcpf(oma);
         float fu = fmaf(f.z, gp2[k], fmaf(f.y, gp1[k], fmaf(f.x, gp0[k], gpa[k])));
         if (kDepth) fu = fmaf(b.z, gpd[k], fu);
-        const float v = G * (Tn * (fu - S[k]));
+        const float d = fu - S[k];
+        const float v = G * (Tn * d);
         const float dch = alpha * Tn;
         const float vdy = v * dy[k];
         if (k == 0) {
@@ -329,18 +340,22 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
           sb = fmaf(dch, gp2[k], sb);
           if (kDepth) sd = fmaf(dch, gpd[k], sd);
         }
-        // this Gaussian joins what lies behind the next (nearer) one
-        S[k] = fmaf(alpha, fu, oma * S[k]);
+        // this Gaussian joins what lies behind the next (nearer) one:
+        // alpha fu + (1 - alpha) S = S + alpha (fu - S)
+        S[k] = fmaf(alpha, d, S[k]);
         T[k] = Tn;
       }
-      const float s = b.y * sv, sy = b.y * svy, syy = b.y * svyy;
+      // Pixel moments of v about the Gaussian's mean; the conic, opacity
+      // and W/2, H/2 factors are per Gaussian and applied once, when the
+      // per-Gaussian backward turns the sums into 2D gradients.
       float g[kGradFloats];
-      g[0] = -half_w * fmaf(a.z * dx, s, a.w * sy);
-      g[1] = -half_h * fmaf(b.x, sy, a.w * dx * s);
-      g[2] = -0.5f * dx * dx * s;
-      g[3] = -0.5f * dx * sy;
-      g[4] = -0.5f * syy;
-      g[5] = sv;
+      const float vdx = sv * dx;
+      g[0] = vdx;        // sum v dx
+      g[1] = svy;        // sum v dy
+      g[2] = vdx * dx;   // sum v dx^2
+      g[3] = svy * dx;   // sum v dx dy
+      g[4] = svyy;       // sum v dy^2
+      g[5] = sv;         // dL/dopacity
       g[6] = sr;
       g[7] = sg;
       g[8] = sb;
@@ -348,10 +363,12 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
       float m[3];
       wave_fold10(g, m);
       const int k = nrel & (kRingSlots - 1);
-      if (nrel >= kRingSlots)
-        flush_slot(s_ring, k, __builtin_amdgcn_readlane(slot_gid, k), lane, flush_comp, p.grad_gauss);
+      if (nrel >= kRingSlots) flush_slot(s_ring, k, k ? slot_gid1 : slot_gid0, lane, flush_comp, p.grad_gauss);
       const int gid = __builtin_amdgcn_readlane(batch_id, jj);
-      slot_gid = lane == k ? gid : slot_gid;
+      if (k)
+        slot_gid1 = gid;
+      else
+        slot_gid0 = gid;
       float* slot = s_ring + k * kSlotFloats + lane;
       slot[0] = m[0];
       slot[64] = m[1];
@@ -359,8 +376,8 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
       ++nrel;
     }
   }
-  for (int k = 0; k < imin(nrel, kRingSlots); ++k)
-    flush_slot(s_ring, k, __builtin_amdgcn_readlane(slot_gid, k), lane, flush_comp, p.grad_gauss);
+  if (nrel > 0) flush_slot(s_ring, 0, slot_gid0, lane, flush_comp, p.grad_gauss);
+  if (nrel > 1) flush_slot(s_ring, 1, slot_gid1, lane, flush_comp, p.grad_gauss);
 }
 
 struct PreprocessBwdParams {
@@ -377,7 +394,9 @@ struct PreprocessBwdParams {
   float tanfovx, tanfovy, focal_x, focal_y;
   const int* radii;
   const uint8_t* clamped;
-  const float* grad_gauss;
+  const float* grad_gauss;    // render_bwd's pixel moments (N,10)
+  const float4* records;     // the forward's render records: conic and opacity
+  float half_w, half_h;      // W/2, H/2: NDC scaling of the xy gradients
   const float* grad_proj_2d;
   const float* grad_conic_2d;
   const float* grad_conic_2d_inv;
@@ -547,8 +566,26 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(PreprocessBwdParams
   const float mz = p.means3d[3 * tid + 2];
   const int rad = p.radii[tid];
   const float* gg = p.grad_gauss + (size_t)tid * kGradFloats;
-  const float rpx = gg[0], rpy = gg[1];
-  const float rc0 = gg[2], rc1 = gg[3], rc2 = gg[4];
+  // The render gradients from the pixel moments (m0 .. m4 = sums of v dx,
+  // v dy, v dx^2, v dx dy, v dy^2 over the Gaussian's blended pixels) and
+  // the record's conic (a, b, c) and opacity o:
+  //   dL/dxy    = -(W/2, H/2) o (a m0 + b m1, c m1 + b m0),
+  //   dL/dconic = -o/2 (m2, m3, m4),
+  // the reference's per-pixel terms (backward_kernels.py:678-685) summed.
+  // A Gaussian that was never rendered has zero moments (its record is not
+  // read).
+  float rpx = 0.0f, rpy = 0.0f, rc0 = 0.0f, rc1 = 0.0f, rc2 = 0.0f;
+  if (rad > 0) {
+    const float4 r0 = p.records[3 * (size_t)tid];
+    const float4 r1 = p.records[3 * (size_t)tid + 1];
+    const float o = r1.y;
+    rpx = -p.half_w * (o * (r0.z * gg[0] + r0.w * gg[1]));
+    rpy = -p.half_h * (o * (r1.x * gg[1] + r0.w * gg[0]));
+    const float ho = -0.5f * o;
+    rc0 = ho * gg[2];
+    rc1 = ho * gg[3];
+    rc2 = ho * gg[4];
+  }
   const float ropa = gg[5];
   const float rcol0 = gg[6], rcol1 = gg[7], rcol2 = gg[8];
   const float rdepth = gg[9];
@@ -833,7 +870,8 @@ extern "C" int gs_preprocess_bwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
                                  const float* shs, const float* campos, const float* viewmatrix,
                                  const float* projmatrix, float tanfovx, float tanfovy, float focal_x,
                                  float focal_y, const int32_t* radii, const uint8_t* clamped,
-                                 const float* grad_gauss, const float* grad_proj_2d, const float* grad_conic_2d,
+                                 const float* grad_gauss, const float* records, int32_t image_width,
+                                 int32_t image_height, const float* grad_proj_2d, const float* grad_conic_2d,
                                  const float* grad_conic_2d_inv, int32_t flow_double, float filter_variance,
                                  float* grad_means3d, float* grad_means2d, float* grad_scales,
                                  float* grad_rotations,
@@ -842,8 +880,11 @@ extern "C" int gs_preprocess_bwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
   if (P < 0) return GS_ERR_INVALID_ARGUMENT;
   if (!(filter_variance >= 0.0f) || !__builtin_isfinite(filter_variance)) return GS_ERR_INVALID_ARGUMENT;
   if (P == 0) return GS_OK;
-  if (!means3d || !viewmatrix || !projmatrix || !radii || !grad_gauss || !grad_means3d || !grad_means2d)
+  if (!means3d || !viewmatrix || !projmatrix || !radii || !grad_gauss || !records || !grad_means3d ||
+      !grad_means2d)
     return GS_ERR_INVALID_ARGUMENT;
+  if (image_width <= 0 || image_height <= 0) return GS_ERR_INVALID_ARGUMENT;
+  if (reinterpret_cast<uintptr_t>(records) & 15) return GS_ERR_MISALIGNED;
   if (cov3d_precomp == nullptr && (!scales || !rotations || !grad_scales || !grad_rotations))
     return GS_ERR_INVALID_ARGUMENT;
   if (cov3d_precomp != nullptr && !grad_cov3d) return GS_ERR_INVALID_ARGUMENT;
@@ -871,6 +912,9 @@ extern "C" int gs_preprocess_bwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
   p.radii = radii;
   p.clamped = clamped;
   p.grad_gauss = grad_gauss;
+  p.records = reinterpret_cast<const float4*>(records);
+  p.half_w = 0.5f * (float)image_width;
+  p.half_h = 0.5f * (float)image_height;
   p.grad_proj_2d = grad_proj_2d;
   p.grad_conic_2d = grad_conic_2d;
   p.grad_conic_2d_inv = grad_conic_2d_inv;

@@ -25,7 +25,11 @@
  *   images: color (3,H,W), depth (1,H,W), alpha (1,H,W), n_contrib (H,W) int32.
  *   ranges (T,2) int32 [start, end) into the sorted pair list.
  *   grad_gauss (N,10) fp32, zero-initialised by the caller, accumulated by
- *     gs_render_bwd: (dx, dy, conic_a, conic_b, conic_c, opacity, r, g, b, depth).
+ *     gs_render_bwd: per Gaussian, sums over the pixels that blend it of
+ *     v = G * dL/dalpha_hat times (dx, dy, dx^2, dx dy, dy^2, 1), with
+ *     (dx, dy) = mean - pixel, then the colour (r, g, b) and depth gradients.
+ *     Column 5 (sum v) is dL/dopacity; gs_preprocess_bwd turns columns 0-4
+ *     into the xy and conic gradients with the record's conic and opacity.
  */
 #ifndef GSWARP_HIP_H
 #define GSWARP_HIP_H
@@ -292,10 +296,10 @@ int gs_render_fwd_flow(int32_t image_width, int32_t image_height, int32_t num_po
                        float* weight_per_gs_pixel, float* x_mu, void* stream);
 
 /*
- * Reverse blend: accumulates per-Gaussian gradients of the pixel loss into
- * grad_gauss (N,10), which the caller zero-initialises.  grad_color,
- * grad_depth and grad_alpha may each be NULL: an absent upstream gradient
- * is zero.
+ * Reverse blend: accumulates per-Gaussian pixel moments of the loss
+ * gradient (the grad_gauss layout above) into grad_gauss (N,10), which the
+ * caller zero-initialises.  grad_color, grad_depth and grad_alpha may each
+ * be NULL: an absent upstream gradient is zero.
  * Replaces: backward_ops.py:183-290 with backward_kernels.py:539-707.
  */
 int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t num_points, int64_t num_rendered,
@@ -313,7 +317,9 @@ int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t num_points,
  * projected-mean and conic chains, as the reference flow backward does with
  * enable_flow_grad.  grad_sh (N,K,3) is fully written (zeros beyond the
  * evaluated bands); grad_opacity (N) and grad_colors (N,3, when non-NULL)
- * are copied out of grad_gauss.  With cov3d_precomp non-NULL the cov2D
+ * are copied out of grad_gauss.  The xy and conic render gradients are
+ * formed from grad_gauss's moments with the conic and opacity of records
+ * (the forward's, 16-byte aligned) and image_width / 2, image_height / 2.  With cov3d_precomp non-NULL the cov2D
  * gradient is returned as grad_cov3d (N, 6) instead of being chained into
  * grad_scales / grad_rotations (which may then be NULL).  filter_variance is
  * the forward's Mip-Splatting variance (0 without the filter), added to the
@@ -329,7 +335,8 @@ int gs_preprocess_bwd(int32_t P, int32_t sh_coeffs, int32_t degree, const float*
                       const float* shs, const float* campos, const float* viewmatrix,
                       const float* projmatrix, float tanfovx, float tanfovy, float focal_x, float focal_y,
                       const int32_t* radii, const uint8_t* clamped, const float* grad_gauss,
-                      const float* grad_proj_2d, const float* grad_conic_2d, const float* grad_conic_2d_inv,
+                      const float* records, int32_t image_width, int32_t image_height, const float* grad_proj_2d,
+                      const float* grad_conic_2d, const float* grad_conic_2d_inv,
                       int32_t flow_double, float filter_variance, float* grad_means3d, float* grad_means2d,
                       float* grad_scales, float* grad_rotations, float* grad_cov3d, float* grad_sh,
                       float* grad_opacity, float* grad_colors, void* stream);
