@@ -183,6 +183,38 @@ def _stage_of(kernel_name: str):
     return None
 
 
+# The profiling commands behind the committed summaries (from the repository
+# root R on the GPU box, each pass a run of its own); the summaries repeat
+# them so that each file says how it was made.
+_PROFILE_PREAMBLE = "#   cd /tmp && export TMPDIR=/tmp"
+PROFILE_COMMANDS = {
+    "stats": [
+        _PROFILE_PREAMBLE,
+        "#   rocprofv3 --kernel-trace --stats --output-format csv -d $R/gpurun_out/prof_c2 -o c2 -- \\",
+        "#       python3 $R/bench.py --steps 10 --warmup 3 --no-cpu-baseline > $R/gpurun_out/prof_c2/bench.json \\",
+        "#       2> $R/gpurun_out/prof_c2/bench.err",
+        "#   python3 bench.py --stats-summary gpurun_out/prof_c2/c2_kernel_stats.csv profiles/kernel_stats_config2.txt \\",
+        "#       gpurun_out/prof_c2/bench.err",
+    ],
+    "pmc": [
+        _PROFILE_PREAMBLE,
+        "#   rocprofv3 --pmc FETCH_SIZE --output-format csv -d $R/gpurun_out/pmc_c2 -o fetch -- \\",
+        "#       python3 $R/bench.py --steps 3 --warmup 1 --no-cpu-baseline --no-stage-timing",
+        "#   rocprofv3 --pmc WRITE_SIZE --output-format csv -d $R/gpurun_out/pmc_c2 -o write -- \\",
+        "#       python3 $R/bench.py --steps 3 --warmup 1 --no-cpu-baseline --no-stage-timing",
+        "#   python3 bench.py --pmc-summary gpurun_out/pmc_c2/fetch_counter_collection.csv \\",
+        "#       gpurun_out/pmc_c2/write_counter_collection.csv profiles/traffic_config2.txt",
+    ],
+    "sq": [
+        _PROFILE_PREAMBLE,
+        "#   rocprofv3 --pmc SQ_WAVES SQ_INSTS_VALU SQ_ACTIVE_INST_VALU SQ_INSTS_LDS SQ_ACTIVE_INST_LDS \\",
+        "#       SQ_LDS_BANK_CONFLICT SQ_WAVE_CYCLES SQ_BUSY_CYCLES --output-format csv -d $R/gpurun_out/sq_c2 -o sq -- \\",
+        "#       python3 $R/bench.py --steps 3 --warmup 1 --no-cpu-baseline --no-stage-timing",
+        "#   python3 bench.py --sq-summary gpurun_out/sq_c2/sq_counter_collection.csv profiles/sq_counters_config2.txt",
+    ],
+}
+
+
 def summarize_pmc(fetch_csv: str, write_csv: str, out_path: str, copy_bytes: int = 1 << 30) -> None:
     """Turn two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE, then WRITE_SIZE,
     both in KiB per dispatch) into per-stage HBM bytes per launch.  Each counter is
@@ -216,6 +248,9 @@ def summarize_pmc(fetch_csv: str, write_csv: str, out_path: str, copy_bytes: int
         f"(calibration copy of {copy_bytes} B read + {copy_bytes} B written read "
         f"{fetch_copy:.0f} / {write_copy:.0f} units)",
         f"# iterations averaged: {iters} (fetch run), {iters_w} (write run)",
+        "# commands:",
+        *PROFILE_COMMANDS["pmc"],
+        "# format: '<stage>: <bytes per launch> fetch <bytes> write <bytes>' (bench.py reads the first number)",
     ]
     for stage in sorted(set(fetch) | set(write)):
         fb = fetch.get(stage, 0.0) * f_scale / max(iters, 1)
@@ -242,7 +277,10 @@ def summarize_sq(counter_csv: str, out_path: str) -> None:
         per[short][r["Counter_Name"]] += float(r["Counter_Value"])
         dispatches[short].add(r["Dispatch_Id"])
     counters = sorted({c for d in per.values() for c in d})
-    lines = ["# SQ counters per dispatch (mean), one MI355X; columns: kernel, dispatches, "
+    lines = ["# SQ counters per kernel, config 2 (1M Gaussians, 1920x1080, SH3, fwd+bwd), one MI355X",
+             "# commands:", *PROFILE_COMMANDS["sq"],
+             "# lds_conflict_rate = SQ_LDS_BANK_CONFLICT / SQ_ACTIVE_INST_LDS (cycles per LDS-active cycle)",
+             "# SQ counters per dispatch (mean); columns: kernel, dispatches, "
              + ", ".join(counters) + ", lds_conflict_rate, valu_insts_per_wave"]
     for k in sorted(per):
         n = len(dispatches[k])
@@ -256,14 +294,22 @@ def summarize_sq(counter_csv: str, out_path: str) -> None:
     print("\n".join(lines))
 
 
-def summarize_stats(stats_csv: str, out_path: str, header: str = "") -> None:
+def summarize_stats(stats_csv: str, out_path: str, bench_err: str | None = None) -> None:
     """rocprofv3 --kernel-trace --stats kernel_stats.csv -> calls, average / min /
-    max duration (us), share of GPU time and name of each kernel, longest first."""
+    max duration (us), share of GPU time and name of each kernel, longest first;
+    with the profiled bench run's stderr, its own HIP-event stage times too."""
     import csv
 
     rows = list(csv.DictReader(open(stats_csv)))
     rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
-    lines = [line for line in header.split("\n") if line] if header else []
+    lines = ["# Kernel time, config 2 (1M Gaussians, 1920x1080, SH3, fwd+bwd with depth and alpha), one MI355X",
+             "# 23 iterations (3 warm-up, 10 timed, 10 with per-stage events) plus bench.py's 1 GiB copy calibration",
+             "# commands:", *PROFILE_COMMANDS["stats"]]
+    if bench_err:
+        stage_lines = [line.strip() for line in open(bench_err) if line.startswith("[bench]")]
+        if stage_lines:
+            lines.append("# bench.py's own report in the same run (HIP events under the tracer, same cameras):")
+            lines += [f"#   {line}" for line in stage_lines]
     lines.append("# columns: calls, average us, min us, max us, share of GPU time, kernel")
     for r in rows:
         lines.append(f"{int(r['Calls']):5d} {float(r['AverageNs']) / 1e3:10.1f} {float(r['MinNs']) / 1e3:10.1f} "
@@ -313,8 +359,9 @@ def main() -> int:
                         help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) into OUT and exit")
     parser.add_argument("--sq-summary", nargs=2, metavar=("COUNTER_CSV", "OUT"),
                         help="summarise one rocprofv3 --pmc run of SQ counters into OUT and exit")
-    parser.add_argument("--stats-summary", nargs=2, metavar=("KERNEL_STATS_CSV", "OUT"),
-                        help="summarise one rocprofv3 --kernel-trace --stats run into OUT and exit")
+    parser.add_argument("--stats-summary", nargs="+", metavar="PATH",
+                        help="KERNEL_STATS_CSV OUT [BENCH_ERR]: summarise one rocprofv3 --kernel-trace --stats "
+                             "run into OUT and exit")
     args = parser.parse_args()
     if args.stats_summary:
         summarize_stats(*args.stats_summary)
