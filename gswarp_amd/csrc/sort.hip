@@ -23,8 +23,14 @@ namespace gs_sort {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
+// Keys per thread of the radix passes: 16 (4096 per workgroup), or 32 for
+// sorts of at least kLargeSortKeys keys whose workgroup tile fits in 64 KB of
+// LDS, where the longer per-digit runs of each workgroup's scatter outweigh
+// the lower occupancy (and the halved number of histogram columns shortens
+// the digit-row scans).
 constexpr int kItems = 16;
-constexpr int kTile = kThreads * kItems;  // 4096
+constexpr int kItemsLarge = 32;
+constexpr long long kLargeSortKeys = 1ll << 24;
 constexpr int kRadix = 256;
 
 typedef unsigned long long u64;
@@ -93,24 +99,25 @@ __device__ __forceinline__ u64 match_digit(unsigned d, bool valid) {
 constexpr int kCopies = 8;
 constexpr int kCopyStride = kRadix + 1;
 
-template <typename K>
+template <typename K, int kIt>
 __global__ __launch_bounds__(kThreads) void upsweep_kernel(const K* __restrict__ keys, long long n, int shift,
                                                           unsigned dmask, int nb, unsigned* __restrict__ hist) {
+  constexpr int kTile = kThreads * kIt;
   __shared__ unsigned h[kCopies * kCopyStride];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   for (int i = threadIdx.x; i < kCopies * kCopyStride; i += kThreads) h[i] = 0;
-  const long long base = (long long)blockIdx.x * kTile + wave * (64 * kItems) + lane;
-  K key[kItems];
+  const long long base = (long long)blockIdx.x * kTile + wave * (64 * kIt) + lane;
+  K key[kIt];
 #pragma unroll
-  for (int i = 0; i < kItems; ++i) {
+  for (int i = 0; i < kIt; ++i) {
     const long long idx = base + i * 64;
     key[i] = idx < n ? keys[idx] : K(0);
   }
   __syncthreads();
   unsigned* mine = h + (lane & (kCopies - 1)) * kCopyStride;
 #pragma unroll
-  for (int i = 0; i < kItems; ++i)
+  for (int i = 0; i < kIt; ++i)
     if (base + i * 64 < n) atomicAdd(mine + digit_of(key[i], shift, dmask), 1u);
   __syncthreads();
   const int d = threadIdx.x;
@@ -121,38 +128,54 @@ __global__ __launch_bounds__(kThreads) void upsweep_kernel(const K* __restrict__
 }
 
 // One workgroup per digit row: hist[d][*] becomes its exclusive prefix over
-// blocks and digit_totals[d] the row total.  Thread t owns a contiguous
-// segment of the row: it sums the segment, the workgroup scans the 256
-// segment sums, and a second pass over the segment writes the prefixes, so
-// a row of tens of thousands of blocks is two parallel sweeps rather than a
-// chain of dependent chunks.
+// blocks and digit_totals[d] the row total.  The row is scanned in chunks of
+// kRowChunk entries, thread t owning kRowItems consecutive entries of a
+// chunk, so the workgroup reads and writes each chunk as one contiguous
+// span: per-thread sums, one block scan, the prefixes written back, the
+// chunk total carried.  The next chunk is loaded before the current one is
+// scanned, so its loads overlap the scan.
+constexpr int kRowItems = 8;
+constexpr int kRowChunk = kThreads * kRowItems;
 __global__ __launch_bounds__(kThreads) void rowscan_kernel(int nb, unsigned* __restrict__ hist,
                                                           unsigned* __restrict__ digit_totals) {
   __shared__ unsigned s_lds_w[kWaves];
-  const int d = blockIdx.x;
-  unsigned* row = hist + (size_t)d * nb;
-  const int seg = (nb + kThreads - 1) / kThreads;
-  const int begin = threadIdx.x * seg;
-  const int end = begin + seg < nb ? begin + seg : nb;
-  unsigned sum = 0;
-  for (int i = begin; i < end; ++i) sum += row[i];
-  unsigned total;
-  unsigned run = block_exclusive_scan_u32(sum, s_lds_w, &total);
-  for (int i = begin; i < end; ++i) {
-    const unsigned v = row[i];
-    row[i] = run;
-    run += v;
+  unsigned* row = hist + (size_t)blockIdx.x * nb;
+  const int t0 = threadIdx.x * kRowItems;
+  unsigned cur[kRowItems], nxt[kRowItems];
+#pragma unroll
+  for (int k = 0; k < kRowItems; ++k) cur[k] = t0 + k < nb ? row[t0 + k] : 0u;
+  unsigned carry = 0;
+  for (int base = 0; base < nb; base += kRowChunk) {
+#pragma unroll
+    for (int k = 0; k < kRowItems; ++k) {
+      const int i = base + kRowChunk + t0 + k;
+      nxt[k] = i < nb ? row[i] : 0u;
+    }
+    unsigned sum = 0;
+#pragma unroll
+    for (int k = 0; k < kRowItems; ++k) sum += cur[k];
+    unsigned total;
+    unsigned run = carry + block_exclusive_scan_u32(sum, s_lds_w, &total);
+#pragma unroll
+    for (int k = 0; k < kRowItems; ++k) {
+      const int i = base + t0 + k;
+      if (i < nb) row[i] = run;
+      run += cur[k];
+      cur[k] = nxt[k];
+    }
+    carry += total;
   }
-  if (threadIdx.x == 0) digit_totals[d] = total;
+  if (threadIdx.x == 0) digit_totals[blockIdx.x] = carry;
 }
 
-template <typename K, bool kValues>
+template <typename K, bool kValues, int kIt>
 __global__ __launch_bounds__(kThreads) void downsweep_kernel(const K* __restrict__ keys_in,
                                                             const int* __restrict__ vals_in,
                                                             K* __restrict__ keys_out, int* __restrict__ vals_out,
                                                             long long n, int shift, unsigned dmask, int nb,
                                                             const unsigned* __restrict__ hist,
                                                             const unsigned* __restrict__ digit_totals) {
+  constexpr int kTile = kThreads * kIt;
   __shared__ K s_keys[kTile];
   __shared__ int s_vals[kValues ? kTile : 1];
   __shared__ unsigned s_wcount[kWaves][kRadix];
@@ -163,16 +186,16 @@ __global__ __launch_bounds__(kThreads) void downsweep_kernel(const K* __restrict
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const long long block_base = (long long)blockIdx.x * kTile;
-  const long long wave_base = block_base + wave * (64 * kItems) + lane;
+  const long long wave_base = block_base + wave * (64 * kIt) + lane;
   const int block_count = (int)((n - block_base) < kTile ? (n - block_base) : kTile);
 
 #pragma unroll
   for (int i = threadIdx.x; i < kWaves * kRadix; i += kThreads) (&s_wcount[0][0])[i] = 0;
 
-  K key[kItems];
-  int val[kItems];
+  K key[kIt];
+  int val[kIt];
 #pragma unroll
-  for (int i = 0; i < kItems; ++i) {
+  for (int i = 0; i < kIt; ++i) {
     const long long idx = wave_base + i * 64;
     const bool in = idx < n;
     key[i] = in ? keys_in[idx] : K(0);
@@ -181,9 +204,9 @@ __global__ __launch_bounds__(kThreads) void downsweep_kernel(const K* __restrict
   __syncthreads();
 
   const u64 lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  unsigned rank[kItems];
+  unsigned rank[kIt];
 #pragma unroll
-  for (int i = 0; i < kItems; ++i) {
+  for (int i = 0; i < kIt; ++i) {
     const bool valid = (wave_base + i * 64) < n;
     const unsigned d = digit_of(key[i], shift, dmask);
     const u64 peers = match_digit(d, valid);
@@ -220,7 +243,7 @@ __global__ __launch_bounds__(kThreads) void downsweep_kernel(const K* __restrict
   __syncthreads();
 
 #pragma unroll
-  for (int i = 0; i < kItems; ++i) {
+  for (int i = 0; i < kIt; ++i) {
     const bool valid = (wave_base + i * 64) < n;
     if (valid) {
       const unsigned d = digit_of(key[i], shift, dmask);
@@ -232,7 +255,7 @@ __global__ __launch_bounds__(kThreads) void downsweep_kernel(const K* __restrict
   __syncthreads();
 
 #pragma unroll
-  for (int j = 0; j < kItems; ++j) {
+  for (int j = 0; j < kIt; ++j) {
     const int p = j * kThreads + threadIdx.x;
     if (p < block_count) {
       const K k = s_keys[p];
@@ -245,7 +268,14 @@ __global__ __launch_bounds__(kThreads) void downsweep_kernel(const K* __restrict
   }
 }
 
-static inline int num_blocks(long long n) { return (int)((n + kTile - 1) / kTile); }
+static inline int items_for(long long n, size_t key_bytes, bool values) {
+  const size_t tile_bytes = (size_t)kThreads * kItemsLarge * (key_bytes + (values ? sizeof(int) : 0));
+  return (n >= kLargeSortKeys && tile_bytes <= 65536) ? kItemsLarge : kItems;
+}
+static inline int num_blocks(long long n, int items = kItems) {
+  const long long tile = (long long)kThreads * items;
+  return (int)((n + tile - 1) / tile);
+}
 
 template <typename K, bool kValues>
 static int sort_impl(int64_t n, int32_t lo_bit, int32_t key_bits, K* kin, K* kout, int* vin, int* vout,
@@ -271,7 +301,9 @@ static int gs_sort::sort_impl(int64_t n, int32_t lo_bit, int32_t key_bits, K* ki
   if (n == 0 || key_bits == 0) return GS_OK;
   if (!kin || !kout || !scratch || (kValues && (!vin || !vout))) return GS_ERR_INVALID_ARGUMENT;
   if (scratch_bytes < gs_sort_scratch_bytes(n)) return GS_ERR_SCRATCH_TOO_SMALL;
-  const int nb = num_blocks(n);
+  // the scratch query counts 16-key tiles, the most histogram columns
+  const int items = items_for(n, sizeof(K), kValues);
+  const int nb = num_blocks(n, items);
   unsigned* hist = reinterpret_cast<unsigned*>(scratch);
   unsigned* digit_totals = hist + (size_t)nb * kRadix;
   const int passes = gs_passes_for_bits(key_bits);
@@ -279,11 +311,21 @@ static int gs_sort::sort_impl(int64_t n, int32_t lo_bit, int32_t key_bits, K* ki
   for (int pass = 0; pass < passes; ++pass) {
     const int bits = pass_digit_bits(key_bits, passes, pass);
     const unsigned dmask = (1u << bits) - 1u;
-    hipLaunchKernelGGL((upsweep_kernel<K>), dim3(nb), dim3(kThreads), 0, s, kin, (long long)n, shift, dmask, nb,
-                       hist);
+    if (items == kItemsLarge) {
+      hipLaunchKernelGGL((upsweep_kernel<K, kItemsLarge>), dim3(nb), dim3(kThreads), 0, s, kin, (long long)n, shift,
+                         dmask, nb, hist);
+    } else {
+      hipLaunchKernelGGL((upsweep_kernel<K, kItems>), dim3(nb), dim3(kThreads), 0, s, kin, (long long)n, shift,
+                         dmask, nb, hist);
+    }
     hipLaunchKernelGGL(rowscan_kernel, dim3(dmask + 1), dim3(kThreads), 0, s, nb, hist, digit_totals);
-    hipLaunchKernelGGL((downsweep_kernel<K, kValues>), dim3(nb), dim3(kThreads), 0, s, kin, vin, kout, vout,
-                       (long long)n, shift, dmask, nb, hist, digit_totals);
+    if (items == kItemsLarge) {
+      hipLaunchKernelGGL((downsweep_kernel<K, kValues, kItemsLarge>), dim3(nb), dim3(kThreads), 0, s, kin, vin,
+                         kout, vout, (long long)n, shift, dmask, nb, hist, digit_totals);
+    } else {
+      hipLaunchKernelGGL((downsweep_kernel<K, kValues, kItems>), dim3(nb), dim3(kThreads), 0, s, kin, vin, kout,
+                         vout, (long long)n, shift, dmask, nb, hist, digit_totals);
+    }
     shift += bits;
     K* tk = kin;
     kin = kout;

@@ -87,6 +87,11 @@ CASES = [
     ("gs_sort_pairs_u64", 1_500_000, 0, 64, "few"),
     ("gs_sort_pairs_u32", 1_000_000, 0, 32, "uniform"),
     ("gs_sort_pairs_u32", 777_777, 0, 13, "tile_depth"),
+    # more than 2048 blocks of 4096 keys: the digit-row scan runs in several chunks
+    ("gs_sort_pairs_u32", 9_000_001, 0, 13, "tile_depth"),
+    # at least 2^24 keys: 8192-key workgroup tiles
+    ("gs_sort_pairs_u32", 17_000_003, 0, 13, "tile_depth"),
+    ("gs_sort_keys_u64", 16_777_217, 20, 39, "tile_depth"),
     ("gs_sort_pairs_u32", 65_536, 4, 9, "few"),
     ("gs_sort_pairs_u32", 8191, 0, 32, "equal"),
 ]
