@@ -191,7 +191,7 @@ __device__ __forceinline__ BwdBatch load_bwd_batch(const RenderBwdParams& p, int
 template <bool kDepth, int kPix>
 __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
   constexpr int kSubs = 4 / kPix;
-  __shared__ float4 s_r0[64], s_r1[64], s_r2[64];
+  __shared__ float4 s_rec[3 * 64];  // record j at s_rec[3 j .. 3 j + 2]
   __shared__ __align__(16) float s_ring[kRingSlots * kSlotFloats + kRingPad];
   const int lane = threadIdx.x;
   const int2 ts = xcd_tile_sub(blockIdx.x, p.num_tiles, kSubs);
@@ -248,9 +248,9 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
     const int cnt = batch_end - bs;
     // One wave per workgroup: its LDS queue orders these writes before the
     // broadcast reads below.
-    s_r0[lane] = next.r0;
-    s_r1[lane] = next.r1;
-    s_r2[lane] = next.r2;
+    s_rec[3 * lane] = next.r0;
+    s_rec[3 * lane + 1] = next.r1;
+    s_rec[3 * lane + 2] = next.r2;
     const int batch_id = next.id;  // lane j: Gaussian of record j
     uint64_t todo = __ballot(lane < cnt && record_may_touch(next.r0, next.r1, rx0, rx1, ry0, ry1));
     if (bs > 0) {
@@ -261,8 +261,8 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
       const int jj = 63 - __builtin_clzll(todo);
       todo ^= 1ull << jj;
       const int pos = bs + jj;
-      const float4 a = s_r0[jj];
-      const float4 b = s_r1[jj];
+      const float4 a = s_rec[3 * jj];
+      const float4 b = s_rec[3 * jj + 1];
       const float dx = a.x - pfx;
       const float adxx = a.z * dx * dx;
       const float b2dx = (a.w * dx) * 2.0f;
@@ -304,7 +304,7 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
           e[k] = (in_band && a_sw >= kAlphaMin) ? q[k] * (-0.5f * kLog2e) : e[k];
         }
       }
-      const float4 f = s_r2[jj];
+      const float4 f = s_rec[3 * jj + 2];
       float sv, svy, svyy, sr, sg, sb, sd;
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {

@@ -5,8 +5,9 @@
 // lane, exactly as the per-pixel expression would round them.  The tile's
 // sorted Gaussians are fetched 64 at a time, one packed 48-byte record per
 // lane, with the next batch prefetched into registers while the current one
-// is blended from a per-wave LDS slot (one broadcast ds_read_b128 per record
-// quarter; no barriers since each workgroup is one wave).  Each batch is
+// is blended from a per-wave LDS slot (the record's three float4 adjacent,
+// so one address register serves its broadcast reads; no barriers since
+// each workgroup is one wave).  Each batch is
 // first tested lane-parallel against the slice rectangle (record_may_touch)
 // and only records that may touch the slice are visited.  Per Gaussian the
 // per-pixel work is branch-free (select-based updates inside one wave-uniform
@@ -76,7 +77,7 @@ __device__ __forceinline__ Batch load_batch(const RenderFwdParams& p, int first,
 template <bool kFlow, bool kDepth, int kPixPerLane>
 __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
   constexpr int kSubs = 4 / kPixPerLane;
-  __shared__ float4 s_r0[64], s_r1[64], s_r2[64];
+  __shared__ float4 s_rec[3 * 64];  // record j at s_rec[3 j .. 3 j + 2]
   __shared__ int s_id[kFlow ? 64 : 1];
   const int lane = threadIdx.x;
   const int2 ts = xcd_tile_sub(blockIdx.x, p.num_tiles, kSubs);
@@ -122,17 +123,17 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
     const int cnt = imin(64, n - base);
     // One wave per workgroup: LDS writes and the broadcast reads below are
     // ordered by the wave's own in-order LDS queue, no barrier needed.
-    s_r0[lane] = next.r0;
-    s_r1[lane] = next.r1;
-    s_r2[lane] = next.r2;
+    s_rec[3 * lane] = next.r0;
+    s_rec[3 * lane + 1] = next.r1;
+    s_rec[3 * lane + 2] = next.r2;
     if (kFlow) s_id[lane] = next.id;
     uint64_t todo = __ballot(lane < cnt && record_may_touch(next.r0, next.r1, rx0, rx1, ry0, ry1));
     if (base + 64 < n) next = load_batch(p, rg.x + base + 64, imin(64, n - base - 64), lane);
     while (todo != 0) {
       const int j = __builtin_ctzll(todo);
       todo &= todo - 1;
-      const float4 a = s_r0[j];
-      const float4 b = s_r1[j];
+      const float4 a = s_rec[3 * j];
+      const float4 b = s_rec[3 * j + 1];
       const float dx = a.x - pfx;
       const float adxx = a.z * dx * dx;
       const float b2dx = (a.w * dx) * 2.0f;
@@ -147,7 +148,7 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
         any |= cand[k];
       }
       if (__ballot(any) == 0) continue;
-      const float4 f = s_r2[j];
+      const float4 f = s_rec[3 * j + 2];
 #pragma unroll
       for (int k = 0; k < kPixPerLane; ++k) {
         const float alpha = fminr(kAlphaMax, b.y * exp_sw_nonpos(cand[k] ? -0.5f * q[k] : 0.0f));
