@@ -32,7 +32,7 @@ SIGNATURES = {
     "gs_preprocess_fwd": (
         ctypes.c_int,
         [_i32, _i32, _i32, _vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _f32, _f32, _f32, _i32,
-         _i32, _i32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+         _i32, _i32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     ),
     "gs_mark_visible": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp]),
     "gs_scan_scratch_bytes": (_sz, [_i32]),
@@ -40,10 +40,11 @@ SIGNATURES = {
     "gs_scan_tiles": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "gs_num_rendered_readback": (ctypes.c_int, [_vp, _vp, _vp]),
     "gs_duplicate_keys": (
-        ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, ctypes.c_uint32, _i32, _i32, _vp, _vp, _vp],
+        ctypes.c_int,
+        [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, ctypes.c_uint32, _i32, _i32, _vp, _vp, _vp],
     ),
     "gs_duplicate_tiles": (
-        ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp],
+        ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp],
     ),
     "gs_sort_num_passes": (ctypes.c_int, [_i32]),
     "gs_sort_scratch_bytes": (_sz, [_i64]),
@@ -54,10 +55,10 @@ SIGNATURES = {
     "gs_tile_ranges_u32": (ctypes.c_int, [_i64, _vp, _i32, _vp, _vp]),
     "gs_sort_tile_segments": (ctypes.c_int, [_i64, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _i32, _vp]),
     "gs_bin_packed_workspace_bytes": (ctypes.c_size_t, [_i64]),
-    "gs_readback_bin_packed": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64, _vp,
-                                              _sz, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
-    "gs_bin_packed": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, ctypes.c_uint32, _i32, _i32, _vp,
-                                     _sz, _vp, _vp, _vp, _vp, _vp]),
+    "gs_readback_bin_packed": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64,
+                                              _vp, _sz, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "gs_bin_packed": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, ctypes.c_uint32, _i32,
+                                     _i32, _vp, _sz, _vp, _vp, _vp, _vp, _vp]),
     "gs_render_fwd": (ctypes.c_int, [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
     "gs_render_fwd_flow": (
         ctypes.c_int,

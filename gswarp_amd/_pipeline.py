@@ -192,6 +192,7 @@ def preprocess(inputs: RasterInputs, options: ExecutionOptions, *, pack: bool = 
         clamped=clamped,
         coverage_mode=tile_coverage_mode_id(options.tile_coverage_mode),
         geom=geom,
+        coverage=torch.empty((P, 4), dtype=torch.int32, device=device),
     )
     colors = _f32c(inputs.colors) if inputs.colors.numel() != 0 else None
     shs = None
@@ -218,7 +219,8 @@ def preprocess(inputs: RasterInputs, options: ExecutionOptions, *, pack: bool = 
             _focal(H, tanfovy), W, H, out.coverage_mode, float(inputs.filter_variance), out.radii.data_ptr(),
             out.depths.data_ptr(),
             out.proj_2d.data_ptr(), out.conic_2d.data_ptr(), out.conic_2d_inv.data_ptr(),
-            out.tiles_touched.data_ptr(), out.records.data_ptr(), out.clamped.data_ptr(), _stream(device))
+            out.tiles_touched.data_ptr(), out.coverage.data_ptr(), out.records.data_ptr(), out.clamped.data_ptr(),
+            _stream(device))
     return out
 
 
@@ -292,8 +294,8 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
         events = _stage_chain(("duplicate", "sort", "ranges", "sort") + (("render",) if images is not None else ()))
         img = images
         lib.call("gs_readback_bin_packed", info.data_ptr(), pinned.data_ptr(), P, pre.radii.data_ptr(),
-                 pre.records.data_ptr(), pre.conic_2d_inv.data_ptr(), offsets.data_ptr(), image_width, image_height,
-                 pre.coverage_mode, DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN if mode == "warp_depth_stable_tile" else 0,
+                 pre.records.data_ptr(), pre.conic_2d_inv.data_ptr(), _lib.ptr(pre.coverage), offsets.data_ptr(),
+                 image_width, image_height, pre.coverage_mode, DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN if mode == "warp_depth_stable_tile" else 0,
                  capacity, ws.data_ptr(), ws.numel(), ranges.data_ptr(), point_list.data_ptr(),
                  None if img is None else img.background.data_ptr(), int(img is not None and img.compute_depth),
                  None if img is None else img.color.data_ptr(), None if img is None else img.depth.data_ptr(),
@@ -383,7 +385,8 @@ def _binning_depth_tile(pre: PreprocessOutputs, image_width: int, image_height: 
     vals = torch.empty((R,), dtype=torch.int32, device=device)
     with _stage("duplicate"):
         lib.call("gs_duplicate_tiles", P, order.data_ptr(), pre.radii.data_ptr(), pre.records.data_ptr(),
-                 pre.conic_2d_inv.data_ptr(), offsets.data_ptr(), image_width, image_height, pre.coverage_mode, R,
+                 pre.conic_2d_inv.data_ptr(), _lib.ptr(pre.coverage), offsets.data_ptr(), image_width, image_height,
+                 pre.coverage_mode, R,
                  tiles.data_ptr(), vals.data_ptr(), stream)
     tile_bits = (T - 1).bit_length()
     _note("sort_passes", int(lib.gs_sort_num_passes(tile_bits)))
@@ -434,7 +437,7 @@ def _binning_packed(pre: PreprocessOutputs, image_width: int, image_height: int,
         keys_out = torch.empty((R,), dtype=torch.int64, device=device) if keep_keys else None
         events = _stage_chain(("duplicate", "sort", "ranges", "sort"))
         lib.call("gs_bin_packed", P, pre.radii.data_ptr(), pre.records.data_ptr(), pre.conic_2d_inv.data_ptr(),
-                 offsets.data_ptr(), image_width, image_height, pre.coverage_mode, R, layout.depth_min,
+                 _lib.ptr(pre.coverage), offsets.data_ptr(), image_width, image_height, pre.coverage_mode, R, layout.depth_min,
                  layout.depth_bits, layout.value_bits, ws.data_ptr(), ws.numel(), ranges.data_ptr(),
                  point_list.data_ptr(), _lib.ptr(keys_out), events, stream)
         return BinningState(grid_x, grid_y, point_list, ranges, R, keys_out, layout)
@@ -446,7 +449,7 @@ def _binning_packed(pre: PreprocessOutputs, image_width: int, image_height: int,
         vals_alt = torch.empty((R,), dtype=torch.int32, device=device)
     with _stage("duplicate"):
         lib.call("gs_duplicate_keys", P, pre.radii.data_ptr(), pre.records.data_ptr(),
-                 pre.conic_2d_inv.data_ptr(), offsets.data_ptr(), image_width, image_height, pre.coverage_mode, R,
+                 pre.conic_2d_inv.data_ptr(), _lib.ptr(pre.coverage), offsets.data_ptr(), image_width, image_height, pre.coverage_mode, R,
                  layout.depth_min, layout.depth_bits, layout.value_bits, keys.data_ptr(), _lib.ptr(vals), stream)
     sort_bits = tile_bits + layout.depth_bits
     sort_scratch = torch.empty((max(int(lib.gs_sort_scratch_bytes(R)), 1),), dtype=torch.uint8, device=device)

@@ -24,6 +24,7 @@ class PreprocessOutputs:
     clamped: torch.Tensor  # (N,) uint8 SH clamp bits
     coverage_mode: int = 1
     geom: torch.Tensor | None = None  # raw-ABI byte buffer that records and clamped are views of
+    coverage: torch.Tensor | None = None  # (N, 4) int32 cover words for the emission, or None (re-derived)
 
 
 @dataclass(slots=True)

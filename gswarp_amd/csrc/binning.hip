@@ -75,13 +75,16 @@ __device__ __forceinline__ unsigned wave_max_u32(unsigned v) {
 
 // Per block of kScanTile Gaussians: the tile-count sum, and the smallest and
 // largest depth bits of the Gaussians with radius > 0 (min ~0u / max 0 when
-// there are none), packed as max << 32 | min.
+// there are none), packed as max << 32 | min.  With an order, the counts
+// are gathered through it and also stored contiguously in `gathered`, so
+// that the apply pass reads them without a second gather.
 __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(int n, const int* __restrict__ in,
                                                                   const int* __restrict__ order,
                                                                   const int* __restrict__ radii,
                                                                   const float* __restrict__ depths,
                                                                   long long* __restrict__ block_sums,
-                                                                  unsigned long long* __restrict__ block_range) {
+                                                                  unsigned long long* __restrict__ block_range,
+                                                                  int* __restrict__ gathered) {
   __shared__ long long lds4[kScanThreads / 64];
   __shared__ unsigned s_min[kScanThreads / 64], s_max[kScanThreads / 64];
   const long long base = (long long)blockIdx.x * kScanTile;
@@ -97,6 +100,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(int n, const 
     if (idx < n) {
       const int src = order ? order[idx] : (int)idx;
       cnt[i] = in[src];
+      if (gathered) gathered[idx] = cnt[i];
       if (radii) {
         rad[i] = radii[src];
         bits[i] = __float_as_uint(depths[src]);
@@ -177,7 +181,6 @@ __global__ __launch_bounds__(kScanThreads) void scan_blocks_kernel(int nb, long 
 }
 
 __global__ __launch_bounds__(kScanThreads) void scan_apply_kernel(int n, const int* __restrict__ in,
-                                                                 const int* __restrict__ order,
                                                                  const long long* __restrict__ block_offsets,
                                                                  int* __restrict__ out) {
   __shared__ long long lds4[kScanThreads / 64];
@@ -187,7 +190,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_apply_kernel(int n, const i
 #pragma unroll
   for (int i = 0; i < kScanItems; ++i) {
     const long long idx = base + i;
-    v[i] = idx < n ? in[order ? order[idx] : (int)idx] : 0;
+    v[i] = idx < n ? in[idx] : 0;
   }
 #pragma unroll
   for (int i = 0; i < kScanItems; ++i) s += v[i];
@@ -338,24 +341,60 @@ __device__ __forceinline__ void wave_emit_gaussian(float px, float py, float ca,
   }
 }
 
+// Emission from a cover mask recorded by the preprocess: a lane walks the
+// set bits of its Gaussian's mask (the order of the coverage walk), or the
+// wave writes a larger Gaussian's cells one per lane, each hit at the
+// position given by the hits below it.
+template <typename W>
+__device__ __forceinline__ void emit_mask_lane(const CoverWord& c, int grid_x, long long off, long long limit,
+                                               W&& write) {
+  const float rcp_span_u = __builtin_amdgcn_rcpf((float)(c.columns ? c.span_y : c.span_x));
+  uint64_t m = c.mask;
+  long long pos = off;
+  while (m != 0) {
+    const int k = __builtin_ctzll(m);
+    m &= m - 1;
+    if (pos < limit) write(pos, cover_cell_tile(c, rcp_span_u, k, grid_x));
+    ++pos;
+  }
+}
+
+template <typename W>
+__device__ __forceinline__ void wave_emit_mask(const CoverWord& c, int grid_x, long long off, long long limit,
+                                               W&& write) {
+  const int lane = threadIdx.x & 63;
+  const float rcp_span_u = __builtin_amdgcn_rcpf((float)(c.columns ? c.span_y : c.span_x));
+  const bool hit = ((c.mask >> lane) & 1ull) != 0;
+  const long long pos = off + __popcll(c.mask & low_bits64(lane));
+  if (hit && pos < limit) write(pos, cover_cell_tile(c, rcp_span_u, lane, grid_x));
+}
+
 // Per wave: small Gaussians by their own lanes, then large ones by the wave.
 // `count` is the Gaussian's pair count (0 for lanes without one).
 // write_own(pos, tile) stores a pair of the calling lane's Gaussian;
 // write_from(src, pos, tile) one of lane src's Gaussian (src wave-uniform).
+// `cover_w` is the Gaussian's packed cover word (zero: none recorded), and a
+// recorded mask replaces the coverage walk.
 template <typename WO, typename WF>
 __device__ __forceinline__ void emit_balanced(bool active, int count, float px, float py, float ca, float cb,
                                               float cc, float opacity, float cov_aa, float cov_cc, int radius,
-                                              int grid_x, int grid_y, int mode, long long off, long long limit,
-                                              WO&& write_own, WF&& write_from) {
+                                              int grid_x, int grid_y, int mode, int4 cover_w, long long off,
+                                              long long limit, WO&& write_own, WF&& write_from) {
   __shared__ int s_stage[256 / 64][kEmitWindow];  // one window per wave of the 256-thread workgroup
   int* stage = s_stage[threadIdx.x >> 6];
   const bool large = active && count > kLaneEmitMax;
   if (active && !large) {
-    long long pos = off;
-    for_each_covered_tile(px, py, ca, cb, cc, opacity, cov_aa, cov_cc, radius, grid_x, grid_y, mode, [&](int tile) {
-      if (pos < limit) write_own(pos, tile);
-      ++pos;
-    });
+    const CoverWord cw = unpack_cover(cover_w);
+    if (cw.has_mask) {
+      emit_mask_lane(cw, grid_x, off, limit, write_own);
+    } else {
+      long long pos = off;
+      for_each_covered_tile(px, py, ca, cb, cc, opacity, cov_aa, cov_cc, radius, grid_x, grid_y, mode,
+                            [&](int tile) {
+                              if (pos < limit) write_own(pos, tile);
+                              ++pos;
+                            });
+    }
   }
   uint64_t todo = __ballot(large);
   while (todo != 0) {
@@ -363,16 +402,24 @@ __device__ __forceinline__ void emit_balanced(bool active, int count, float px, 
     todo &= todo - 1;
     const long long soff = ((long long)__builtin_amdgcn_readlane((int)(off >> 32), src) << 32) |
                            (unsigned)__builtin_amdgcn_readlane((int)off, src);
-    wave_emit_gaussian(bcast_f(px, src), bcast_f(py, src), bcast_f(ca, src), bcast_f(cb, src), bcast_f(cc, src),
-                       bcast_f(opacity, src), bcast_f(cov_aa, src), bcast_f(cov_cc, src),
-                       __builtin_amdgcn_readlane(radius, src), grid_x, grid_y, mode, soff, limit, stage,
-                       [&](long long pos, int tile) { write_from(src, pos, tile); });
+    const CoverWord sc = unpack_cover(make_int4(
+        __builtin_amdgcn_readlane(cover_w.x, src), __builtin_amdgcn_readlane(cover_w.y, src),
+        __builtin_amdgcn_readlane(cover_w.z, src), __builtin_amdgcn_readlane(cover_w.w, src)));
+    auto write = [&](long long pos, int tile) { write_from(src, pos, tile); };
+    if (sc.has_mask) {
+      wave_emit_mask(sc, grid_x, soff, limit, write);
+    } else {
+      wave_emit_gaussian(bcast_f(px, src), bcast_f(py, src), bcast_f(ca, src), bcast_f(cb, src),
+                         bcast_f(cc, src), bcast_f(opacity, src), bcast_f(cov_aa, src), bcast_f(cov_cc, src),
+                         __builtin_amdgcn_readlane(radius, src), grid_x, grid_y, mode, soff, limit, stage, write);
+    }
   }
 }
 
 __global__ __launch_bounds__(256) void duplicate_keys_kernel(int P, const int* __restrict__ radii,
                                                             const float4* __restrict__ records,
                                                             const float* __restrict__ cov2d,
+                                                            const int4* __restrict__ coverage,
                                                             const int* __restrict__ offsets, int grid_x,
                                                             int grid_y, int mode, long long limit,
                                                             unsigned depth_min, int depth_bits, int value_bits,
@@ -385,21 +432,26 @@ __global__ __launch_bounds__(256) void duplicate_keys_kernel(int P, const int* _
   int count = 0;
   float4 r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1 = r0;
   float cov_aa = 0.0f, cov_cc = 0.0f;
+  int4 cover_w = make_int4(0, 0, 0, 0);
   unsigned long long field = 0;
   if (active) {
     off = idx > 0 ? (long long)offsets[idx - 1] : 0;
     count = (int)((long long)offsets[idx] - off);
     r0 = records[3 * (size_t)idx + 0];
     r1 = records[3 * (size_t)idx + 1];
-    cov_aa = cov2d[3 * idx + 0];
-    cov_cc = cov2d[3 * idx + 2];
+    if (coverage) cover_w = coverage[idx];
+    if (!unpack_cover(cover_w).has_mask) {
+      cov_aa = cov2d[3 * idx + 0];
+      cov_cc = cov2d[3 * idx + 2];
+    }
     const unsigned long long doff = (unsigned long long)(__float_as_uint(r1.z) - depth_min);
     field = (doff << value_bits) | (value_bits > 0 ? (unsigned long long)idx : 0ull);
   }
   const int tile_shift = depth_bits + value_bits;
   const bool with_values = value_bits == 0;
   emit_balanced(
-      active, count, r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, cov_aa, cov_cc, radius, grid_x, grid_y, mode, off, limit,
+      active, count, r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, cov_aa, cov_cc, radius, grid_x, grid_y, mode, cover_w, off,
+      limit,
       [&](long long pos, int tile) {
         keys[pos] = ((unsigned long long)tile << tile_shift) | field;
         if (with_values) values[pos] = idx;
@@ -431,6 +483,7 @@ __global__ __launch_bounds__(256) void duplicate_tiles_kernel(int P, const int* 
                                                              const int* __restrict__ radii,
                                                              const float4* __restrict__ records,
                                                              const float* __restrict__ cov2d,
+                                                             const int4* __restrict__ coverage,
                                                              const int* __restrict__ offsets, int grid_x,
                                                              int grid_y, int mode, long long limit,
                                                              unsigned* __restrict__ tiles,
@@ -444,16 +497,21 @@ __global__ __launch_bounds__(256) void duplicate_tiles_kernel(int P, const int* 
   int count = 0;
   float4 r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1 = r0;
   float cov_aa = 0.0f, cov_cc = 0.0f;
+  int4 cover_w = make_int4(0, 0, 0, 0);
   if (active) {
     off = j > 0 ? (long long)offsets[j - 1] : 0;
     count = (int)((long long)offsets[j] - off);
-    r0 = records[3 * (size_t)idx + 0];
-    r1 = records[3 * (size_t)idx + 1];
-    cov_aa = cov2d[3 * idx + 0];
-    cov_cc = cov2d[3 * idx + 2];
+    if (coverage) cover_w = coverage[idx];
+    if (!unpack_cover(cover_w).has_mask) {
+      r0 = records[3 * (size_t)idx + 0];
+      r1 = records[3 * (size_t)idx + 1];
+      cov_aa = cov2d[3 * idx + 0];
+      cov_cc = cov2d[3 * idx + 2];
+    }
   }
   emit_balanced(
-      active, count, r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, cov_aa, cov_cc, radius, grid_x, grid_y, mode, off, limit,
+      active, count, r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, cov_aa, cov_cc, radius, grid_x, grid_y, mode, cover_w, off,
+      limit,
       [&](long long pos, int tile) {
         tiles[pos] = (unsigned)tile;
         values[pos] = idx;
@@ -585,9 +643,14 @@ extern "C" const char* gs_status_string(int status) {
 
 static inline int gs_scan_blocks(int32_t P) { return (P + gs::kScanTile - 1) / gs::kScanTile; }
 
+// Scratch: the block sums and depth ranges, then room for the counts
+// gathered in the given order.
+static inline size_t gs_scan_block_bytes(int32_t P) {
+  return ((size_t)gs_scan_blocks(P) * 2 * sizeof(long long) + 255) & ~(size_t)255;
+}
 extern "C" size_t gs_scan_scratch_bytes(int32_t P) {
   if (P <= 0) return 0;
-  return ((size_t)gs_scan_blocks(P) * 2 * sizeof(long long) + 255) & ~(size_t)255;
+  return gs_scan_block_bytes(P) + (((size_t)P * sizeof(int) + 255) & ~(size_t)255);
 }
 
 extern "C" int gs_scan_tiles(int32_t P, const int32_t* tiles_touched, const int32_t* order, const int32_t* radii,
@@ -605,12 +668,13 @@ extern "C" int gs_scan_tiles(int32_t P, const int32_t* tiles_touched, const int3
   const int nb = gs_scan_blocks(P);
   long long* block_sums = reinterpret_cast<long long*>(scratch);
   unsigned long long* block_range = reinterpret_cast<unsigned long long*>(block_sums + nb);
+  int* gathered = order ? reinterpret_cast<int*>(static_cast<char*>(scratch) + gs_scan_block_bytes(P)) : nullptr;
   hipLaunchKernelGGL(gs::scan_reduce_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, tiles_touched, order,
-                     radii, depths, block_sums, block_range);
+                     radii, depths, block_sums, block_range, gathered);
   hipLaunchKernelGGL(gs::scan_blocks_kernel, dim3(1), dim3(gs::kScanThreads), 0, s, nb, block_sums, block_range,
                      reinterpret_cast<long long*>(info_dev));
-  hipLaunchKernelGGL(gs::scan_apply_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, tiles_touched, order,
-                     block_sums, offsets);
+  hipLaunchKernelGGL(gs::scan_apply_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P,
+                     gathered ? gathered : tiles_touched, block_sums, offsets);
   return gs_status_from_hip(hipGetLastError());
 }
 
@@ -623,7 +687,8 @@ extern "C" int gs_num_rendered_readback(const int64_t* info_dev, int64_t* info_h
 }
 
 extern "C" int gs_duplicate_keys(int32_t P, const int32_t* radii, const float* records,
-                                 const float* conic_2d_inv, const int32_t* offsets, int32_t image_width,
+                                 const float* conic_2d_inv, const int32_t* coverage, const int32_t* offsets,
+                                 int32_t image_width,
                                  int32_t image_height, int32_t coverage_mode, int64_t num_rendered,
                                  uint32_t depth_min, int32_t depth_bits, int32_t value_bits, uint64_t* keys_out,
                                  int32_t* values_out, void* stream) {
@@ -638,9 +703,10 @@ extern "C" int gs_duplicate_keys(int32_t P, const int32_t* radii, const float* r
   if (P == 0 || num_rendered <= 0) return GS_OK;
   if (!radii || !records || !conic_2d_inv || !offsets || !keys_out || (value_bits == 0 && !values_out))
     return GS_ERR_INVALID_ARGUMENT;
-  if (reinterpret_cast<uintptr_t>(records) & 15) return GS_ERR_MISALIGNED;
+  if ((reinterpret_cast<uintptr_t>(records) | reinterpret_cast<uintptr_t>(coverage)) & 15) return GS_ERR_MISALIGNED;
   hipLaunchKernelGGL(gs::duplicate_keys_kernel, dim3((P + 255) / 256), dim3(256), 0, (hipStream_t)stream, P,
-                     radii, reinterpret_cast<const float4*>(records), conic_2d_inv, offsets, grid_x, grid_y,
+                     radii, reinterpret_cast<const float4*>(records), conic_2d_inv,
+                     reinterpret_cast<const int4*>(coverage), offsets, grid_x, grid_y,
                      coverage_mode, (long long)num_rendered, depth_min, depth_bits, value_bits,
                      reinterpret_cast<unsigned long long*>(keys_out), values_out);
   return gs_status_from_hip(hipGetLastError());
@@ -676,7 +742,8 @@ extern "C" int gs_depth_keys(int32_t P, const int32_t* radii, const float* depth
 }
 
 extern "C" int gs_duplicate_tiles(int32_t P, const int32_t* order, const int32_t* radii, const float* records,
-                                  const float* conic_2d_inv, const int32_t* offsets, int32_t image_width,
+                                  const float* conic_2d_inv, const int32_t* coverage, const int32_t* offsets,
+                                  int32_t image_width,
                                   int32_t image_height, int32_t coverage_mode, int64_t num_rendered,
                                   uint32_t* tiles_out, int32_t* values_out, void* stream) {
   if (P < 0 || image_width <= 0 || image_height <= 0 || coverage_mode < 0 || coverage_mode > 2)
@@ -684,11 +751,12 @@ extern "C" int gs_duplicate_tiles(int32_t P, const int32_t* order, const int32_t
   if (P == 0 || num_rendered <= 0) return GS_OK;
   if (!order || !radii || !records || !conic_2d_inv || !offsets || !tiles_out || !values_out)
     return GS_ERR_INVALID_ARGUMENT;
-  if (reinterpret_cast<uintptr_t>(records) & 15) return GS_ERR_MISALIGNED;
+  if ((reinterpret_cast<uintptr_t>(records) | reinterpret_cast<uintptr_t>(coverage)) & 15) return GS_ERR_MISALIGNED;
   const int grid_x = (image_width + gs::kBlockX - 1) / gs::kBlockX;
   const int grid_y = (image_height + gs::kBlockY - 1) / gs::kBlockY;
   hipLaunchKernelGGL(gs::duplicate_tiles_kernel, dim3((P + 255) / 256), dim3(256), 0, (hipStream_t)stream, P, order,
-                     radii, reinterpret_cast<const float4*>(records), conic_2d_inv, offsets, grid_x, grid_y,
+                     radii, reinterpret_cast<const float4*>(records), conic_2d_inv,
+                     reinterpret_cast<const int4*>(coverage), offsets, grid_x, grid_y,
                      coverage_mode, (long long)num_rendered, tiles_out, values_out);
   return gs_status_from_hip(hipGetLastError());
 }
@@ -720,7 +788,8 @@ extern "C" size_t gs_bin_packed_workspace_bytes(int64_t num_rendered) {
 }
 
 extern "C" int gs_bin_packed(int32_t P, const int32_t* radii, const float* records, const float* conic_2d_inv,
-                             const int32_t* offsets, int32_t image_width, int32_t image_height,
+                             const int32_t* coverage, const int32_t* offsets, int32_t image_width,
+                             int32_t image_height,
                              int32_t coverage_mode, int64_t num_rendered, uint32_t depth_min, int32_t depth_bits,
                              int32_t value_bits, void* workspace, size_t workspace_bytes, int32_t* ranges,
                              int32_t* point_list, uint64_t* sorted_keys_out, void* const* stage_events,
@@ -750,8 +819,8 @@ extern "C" int gs_bin_packed(int32_t P, const int32_t* radii, const float* recor
     if (stage_events) (void)hipEventRecord((hipEvent_t)stage_events[k], s);
   };
   mark(0);
-  int st = gs_duplicate_keys(P, radii, records, conic_2d_inv, offsets, image_width, image_height, coverage_mode,
-                             num_rendered, depth_min, depth_bits, value_bits, keys, nullptr, stream);
+  int st = gs_duplicate_keys(P, radii, records, conic_2d_inv, coverage, offsets, image_width, image_height,
+                             coverage_mode, num_rendered, depth_min, depth_bits, value_bits, keys, nullptr, stream);
   if (st != GS_OK) return st;
   mark(1);
   st = gs_sort_keys_u64(num_rendered, tile_shift, tile_bits, keys, keys_alt, scratch, scratch_bytes, stream);
@@ -792,7 +861,8 @@ extern "C" int gs_bin_packed(int32_t P, const int32_t* radii, const float* recor
 // launched too (out_color given).
 extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_host_pinned, int32_t P,
                                       const int32_t* radii, const float* records, const float* conic_2d_inv,
-                                      const int32_t* offsets, int32_t image_width, int32_t image_height,
+                                      const int32_t* coverage, const int32_t* offsets, int32_t image_width,
+                                      int32_t image_height,
                                       int32_t coverage_mode, int32_t max_pairs_per_point, int64_t capacity,
                                       void* workspace, size_t workspace_bytes, int32_t* ranges, int32_t* point_list,
                                       const float* background, int32_t compute_depth, float* out_color,
@@ -820,7 +890,7 @@ extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_hos
   if (R <= 0 || R > 0x7fffffffLL || R > capacity) return GS_OK;
   if (tile_bits + depth_bits + value_bits > 64 || value_bits > 31) return GS_OK;
   if (max_pairs_per_point > 0 && R > (int64_t)max_pairs_per_point * P) return GS_OK;
-  st = gs_bin_packed(P, radii, records, conic_2d_inv, offsets, image_width, image_height, coverage_mode, R,
+  st = gs_bin_packed(P, radii, records, conic_2d_inv, coverage, offsets, image_width, image_height, coverage_mode, R,
                      depth_min, depth_bits, value_bits, workspace, workspace_bytes, ranges, point_list, nullptr,
                      stage_events, stream);
   if (st != GS_OK) return st;

@@ -336,36 +336,105 @@ __device__ __forceinline__ int2 accutile_band(float pu, float pv, float cuu, flo
   return make_int2(imax(rect_u_min, imin(rect_u_max, tmin)), imax(rect_u_min, imin(rect_u_max, tmax)));
 }
 
-// Number of tiles a Gaussian is binned to under the given coverage mode.
+// Covered tiles of a Gaussian whose tile rectangle has at most
+// kCoverMaskCells cells, as a mask in the order of the coverage walk: bit k
+// is the k-th cell of the rectangle in band order (row-major for row bands
+// and the full or conic-rect walks, column-major for column bands), set when
+// the walk emits that tile.  The preprocess records it beside the count, so
+// that the emission reads the tiles instead of re-deriving the bands.
+constexpr int kCoverMaskCells = 64;
+
+struct TileCover {
+  int4 rect;       // tile rectangle [x, z) x [y, w)
+  int columns;     // 1: bands are tile columns (column-major mask)
+  int has_mask;    // the rectangle has at most kCoverMaskCells cells
+  uint64_t mask;
+};
+
+__device__ __forceinline__ uint64_t low_bits64(int n) { return n >= 64 ? ~0ull : ((1ull << n) - 1ull); }
+
+// Packed per-Gaussian coverage word: x = rect.x | rect.y << 16, y = span_x |
+// span_y << 8 | columns << 16 | has_mask << 17, z / w = mask low / high.
+// Only rectangles with tile coordinates below 2^16 get a mask.
+__device__ __forceinline__ int4 pack_cover(const TileCover& c) {
+  const int span_x = c.rect.z - c.rect.x, span_y = c.rect.w - c.rect.y;
+  if (!c.has_mask) return make_int4(0, 0, 0, 0);
+  return make_int4(c.rect.x | (c.rect.y << 16), span_x | (span_y << 8) | (c.columns << 16) | (1 << 17),
+                   (int)(unsigned)c.mask, (int)(unsigned)(c.mask >> 32));
+}
+
+struct CoverWord {
+  int rx, ry, span_x, span_y, columns, has_mask;
+  uint64_t mask;
+};
+
+__device__ __forceinline__ CoverWord unpack_cover(int4 w) {
+  CoverWord c;
+  c.rx = w.x & 0xffff;
+  c.ry = (unsigned)w.x >> 16;
+  c.span_x = w.y & 0xff;
+  c.span_y = (w.y >> 8) & 0xff;
+  c.columns = (w.y >> 16) & 1;
+  c.has_mask = (w.y >> 17) & 1;
+  c.mask = ((uint64_t)(unsigned)w.w << 32) | (unsigned)w.z;
+  return c;
+}
+
+// Tile id of cell k of a packed rectangle in band order.  k / span is
+// floor((k + 0.5) * rcp(span)): for k < 64 and span <= 64 the quotient is at
+// least 0.5 / span away from an integer, far beyond the float error.
+__device__ __forceinline__ int cover_cell_tile(const CoverWord& c, float rcp_span_u, int k, int grid_x) {
+  const int span_u = c.columns ? c.span_y : c.span_x;
+  const int band = (int)(((float)k + 0.5f) * rcp_span_u);
+  const int u = k - band * span_u;
+  return c.columns ? (c.ry + u) * grid_x + (c.rx + band) : (c.ry + band) * grid_x + (c.rx + u);
+}
+
+// Number of tiles a Gaussian is binned to under the given coverage mode, and
+// its cover mask when the rectangle is small enough.
 // Mode kCoverageConicRect counts tiles exactly only up to kConicMaskMaxTiles
 // candidate tiles and falls back to AccuTile beyond that, which is the
 // effective behaviour of the reference binning stage for that mode.
 __device__ __forceinline__ int count_covered_tiles(float px, float py, float cov_aa, float cov_cc, float ca,
                                                    float cb, float cc, float opacity, int cuda_radius,
-                                                   int grid_x, int grid_y, int mode) {
+                                                   int grid_x, int grid_y, int mode, TileCover& cover) {
   const int4 rect = snugbox_rect(px, py, cov_aa, cov_cc, opacity, cuda_radius, grid_x, grid_y);
   const int span_x = rect.z - rect.x;
   const int span_y = rect.w - rect.y;
   const int area = span_x * span_y;
-  if (area <= 1) return area;
-  if (mode == kCoverageSnugbox) return area;
+  cover.rect = rect;
+  cover.columns = 0;
+  cover.has_mask = span_x >= 0 && span_y >= 0 && area <= kCoverMaskCells && rect.x <= 0xffff && rect.y <= 0xffff;
+  cover.mask = 0;
+  if (area <= 1 || mode == kCoverageSnugbox) {
+    if (cover.has_mask) cover.mask = low_bits64(area);
+    return area;
+  }
   const float threshold = coverage_threshold(opacity);
   int count = 0;
   if (mode == kCoverageConicRect && area <= kConicMaskMaxTiles) {
     for (int ty = rect.y; ty < rect.w; ++ty)
       for (int tx = rect.x; tx < rect.z; ++tx)
-        if (conic_rect_intersects_tile(px, py, ca, cb, cc, threshold, tx, ty)) ++count;
+        if (conic_rect_intersects_tile(px, py, ca, cb, cc, threshold, tx, ty)) {
+          ++count;
+          if (cover.has_mask) cover.mask |= 1ull << ((ty - rect.y) * span_x + (tx - rect.x));
+        }
     return count;
   }
   if (span_y <= span_x) {
     for (int ty = rect.y; ty < rect.w; ++ty) {
       const int2 iv = accutile_band(px, py, ca, cb, cc, threshold, ty, kBlockX, kBlockY, rect.x, rect.z);
-      count += imax(0, iv.y - iv.x);
+      const int len = imax(0, iv.y - iv.x);
+      count += len;
+      if (cover.has_mask && len > 0) cover.mask |= low_bits64(len) << ((ty - rect.y) * span_x + (iv.x - rect.x));
     }
   } else {
+    cover.columns = 1;
     for (int tx = rect.x; tx < rect.z; ++tx) {
       const int2 iv = accutile_band(py, px, cc, cb, ca, threshold, tx, kBlockY, kBlockX, rect.y, rect.w);
-      count += imax(0, iv.y - iv.x);
+      const int len = imax(0, iv.y - iv.x);
+      count += len;
+      if (cover.has_mask && len > 0) cover.mask |= low_bits64(len) << ((tx - rect.x) * span_y + (iv.x - rect.y));
     }
   }
   return count;

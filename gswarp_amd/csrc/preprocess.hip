@@ -44,6 +44,7 @@ struct PreprocessParams {
   float* conic_2d;
   float* conic_2d_inv;
   int* tiles_touched;
+  int4* coverage;  // per-Gaussian packed cover masks (pack_cover), or null
   float4* records;
   uint8_t* clamped;
 };
@@ -124,6 +125,7 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p)
   float con0 = 0.0f, con1 = 0.0f, con2 = 0.0f;
   float cov_a = 0.0f, cov_b = 0.0f, cov_c = 0.0f;
   int touched = 0;
+  int4 cover_word = make_int4(0, 0, 0, 0);
 
   const float p_view_z = V[2] * mx + V[6] * my + V[10] * mz + V[14];
   bool visible = p_view_z > kNearPlane;
@@ -240,8 +242,10 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p)
         pyo = pty;
         con0 = q0; con1 = q1; con2 = q2;
         cov_a = fa; cov_b = cb; cov_c = fc;
+        TileCover cover;
         touched = count_covered_tiles(ptx, pty, fa, fc, q0, q1, q2, op, frad, p.grid_x, p.grid_y,
-                                      p.coverage_mode);
+                                      p.coverage_mode, cover);
+        cover_word = pack_cover(cover);
 
         float3 col;
         uint8_t clamp_bits = 0;
@@ -285,6 +289,7 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p)
   p.conic_2d_inv[3 * idx + 1] = cov_b;
   p.conic_2d_inv[3 * idx + 2] = cov_c;
   p.tiles_touched[idx] = touched;
+  if (p.coverage != nullptr) p.coverage[idx] = cover_word;
 }
 
 // markVisible: view-space z beyond the near plane (preprocess_kernels.py:604-617).
@@ -310,8 +315,8 @@ extern "C" int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
                                  int32_t image_width, int32_t image_height, int32_t coverage_mode,
                                  float filter_variance, int32_t* radii, float* depths, float* proj_2d,
                                  float* conic_2d,
-                                 float* conic_2d_inv, int32_t* tiles_touched, float* records,
-                                 uint8_t* clamped, void* stream) {
+                                 float* conic_2d_inv, int32_t* tiles_touched, int32_t* coverage,
+                                 float* records, uint8_t* clamped, void* stream) {
   if (P < 0 || image_width <= 0 || image_height <= 0) return GS_ERR_INVALID_ARGUMENT;
   if (coverage_mode < 0 || coverage_mode > 2) return GS_ERR_INVALID_ARGUMENT;
   if (!(filter_variance >= 0.0f) || !__builtin_isfinite(filter_variance)) return GS_ERR_INVALID_ARGUMENT;
@@ -323,7 +328,7 @@ extern "C" int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
   if (colors_precomp == nullptr && (shs == nullptr || campos == nullptr || sh_coeffs <= 0))
     return GS_ERR_INVALID_ARGUMENT;
   if ((cov3d_precomp == nullptr && (reinterpret_cast<uintptr_t>(rotations) & 15)) ||
-      (reinterpret_cast<uintptr_t>(records) & 15))
+      (reinterpret_cast<uintptr_t>(records) & 15) || (reinterpret_cast<uintptr_t>(coverage) & 15))
     return GS_ERR_MISALIGNED;
   gs::PreprocessParams p;
   p.P = P;
@@ -357,6 +362,7 @@ extern "C" int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
   p.conic_2d = conic_2d;
   p.conic_2d_inv = conic_2d_inv;
   p.tiles_touched = tiles_touched;
+  p.coverage = reinterpret_cast<int4*>(coverage);
   p.records = reinterpret_cast<float4*>(records);
   p.clamped = clamped;
   const int blocks = (P + 255) / 256;

@@ -73,7 +73,11 @@ const char* gs_status_string(int status);
  * (finite, >= 0) applies the Mip-Splatting screen-space filter to the kept
  * Gaussians: cov2D + f I, its conic, the radius ceil(3 sqrt(max(lambda_max,
  * 0.1))) and the tile count are recomputed; a filtered determinant <= 1e-12
- * culls (depth and position are kept).
+ * culls (depth and position are kept).  coverage ((N,4) int32, 16-byte
+ * aligned, optional) receives each Gaussian's cover word: when its tile
+ * rectangle has at most 64 cells, the rectangle and a 64-bit mask of the
+ * covered cells in the order of the coverage walk (zero otherwise), which
+ * the emission entry points read instead of re-deriving the tiles.
  * Replaces: preprocess_ops.py:289-581 (preprocess_gaussians) with
  * preprocess_kernels.py:83-269 (scales/rotations), preprocess_kernels.py:345-477
  * and 604-624 (precomputed covariances), the SH kernel
@@ -87,7 +91,7 @@ int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, const float*
                       float tanfovx, float tanfovy, float focal_x, float focal_y,
                       int32_t image_width, int32_t image_height, int32_t coverage_mode,
                       float filter_variance, int32_t* radii, float* depths, float* proj_2d, float* conic_2d,
-                      float* conic_2d_inv, int32_t* tiles_touched, float* records,
+                      float* conic_2d_inv, int32_t* tiles_touched, int32_t* coverage, float* records,
                       uint8_t* clamped, void* stream);
 
 /*
@@ -142,11 +146,13 @@ int gs_num_rendered_readback(const int64_t* info_dev, int64_t* info_host_pinned,
  * tile, depth and value fields must fit in 64 bits and i in value_bits.
  * Pairs are produced in point-index order; a stable sort on the tile and
  * depth fields then yields the reference's (tile, depth, index) order.
+ * coverage (optional) is gs_preprocess_fwd's cover words for the same
+ * inputs; Gaussians with a mask are emitted from it.
  * Replaces: binning_kernels.py:411-451 with binning_kernels.py:127-216 and
  * the depth sort that precedes it (binning_ops.py:152-222).
  */
 int gs_duplicate_keys(int32_t P, const int32_t* radii, const float* records, const float* conic_2d_inv,
-                      const int32_t* offsets, int32_t image_width, int32_t image_height,
+                      const int32_t* coverage, const int32_t* offsets, int32_t image_width, int32_t image_height,
                       int32_t coverage_mode, int64_t num_rendered, uint32_t depth_min, int32_t depth_bits,
                       int32_t value_bits, uint64_t* keys_out, int32_t* values_out, void* stream);
 
@@ -155,11 +161,13 @@ int gs_duplicate_keys(int32_t P, const int32_t* radii, const float* records, con
  * Gaussian order[j] (radius > 0) at offsets[j-1] (0 for j == 0) as
  * (tile id, point index) pairs.  With order the depth-sorted point list, a
  * stable sort of the tile ids then yields the reference's per-tile lists.
+ * coverage (optional) as for gs_duplicate_keys.
  * Replaces: binning_kernels.py:411-451 (_duplicate_with_keys_from_order)
  * with binning_kernels.py:127-216.
  */
 int gs_duplicate_tiles(int32_t P, const int32_t* order, const int32_t* radii, const float* records,
-                       const float* conic_2d_inv, const int32_t* offsets, int32_t image_width,
+                       const float* conic_2d_inv, const int32_t* coverage, const int32_t* offsets,
+                       int32_t image_width,
                        int32_t image_height, int32_t coverage_mode, int64_t num_rendered, uint32_t* tiles_out,
                        int32_t* values_out, void* stream);
 
@@ -232,7 +240,8 @@ int gs_sort_tile_segments(int64_t n, uint64_t* keys, uint64_t* keys_alt, int32_t
  */
 size_t gs_bin_packed_workspace_bytes(int64_t num_rendered);
 int gs_bin_packed(int32_t P, const int32_t* radii, const float* records, const float* conic_2d_inv,
-                  const int32_t* offsets, int32_t image_width, int32_t image_height, int32_t coverage_mode,
+                  const int32_t* coverage, const int32_t* offsets, int32_t image_width, int32_t image_height,
+                  int32_t coverage_mode,
                   int64_t num_rendered, uint32_t depth_min, int32_t depth_bits, int32_t value_bits, void* workspace,
                   size_t workspace_bytes, int32_t* ranges, int32_t* point_list, uint64_t* sorted_keys_out,
                   void* const* stage_events, void* stream);
@@ -258,8 +267,8 @@ int gs_bin_packed(int32_t P, const int32_t* radii, const float* records, const f
  * the binning that follows it and render_ops.py:16-93.
  */
 int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_host_pinned, int32_t P, const int32_t* radii,
-                           const float* records, const float* conic_2d_inv, const int32_t* offsets,
-                           int32_t image_width, int32_t image_height, int32_t coverage_mode,
+                           const float* records, const float* conic_2d_inv, const int32_t* coverage,
+                           const int32_t* offsets, int32_t image_width, int32_t image_height, int32_t coverage_mode,
                            int32_t max_pairs_per_point, int64_t capacity, void* workspace, size_t workspace_bytes,
                            int32_t* ranges, int32_t* point_list, const float* background, int32_t compute_depth,
                            float* out_color, float* out_depth, float* out_alpha, int32_t* n_contrib,
