@@ -41,7 +41,7 @@ SIGNATURES = {
     "gs_num_rendered_readback": (ctypes.c_int, [_vp, _vp, _vp]),
     "gs_duplicate_keys": (
         ctypes.c_int,
-        [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, ctypes.c_uint32, _i32, _i32, _vp, _vp, _vp],
+        [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, ctypes.c_uint32, _i32, _i32, _vp, _vp, _vp],
     ),
     "gs_duplicate_tiles": (
         ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp],
@@ -55,10 +55,11 @@ SIGNATURES = {
     "gs_tile_ranges_u32": (ctypes.c_int, [_i64, _vp, _i32, _vp, _vp]),
     "gs_sort_tile_segments": (ctypes.c_int, [_i64, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _i32, _vp]),
     "gs_bin_packed_workspace_bytes": (ctypes.c_size_t, [_i64]),
-    "gs_readback_bin_packed": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i64,
-                                              _vp, _sz, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
-    "gs_bin_packed": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, ctypes.c_uint32, _i32,
-                                     _i32, _vp, _sz, _vp, _vp, _vp, _vp, _vp]),
+    "gs_readback_bin_packed": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
+                                              _i64, _vp, _sz, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
+                                              _vp]),
+    "gs_bin_packed": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, ctypes.c_uint32,
+                                     _i32, _i32, _vp, _sz, _vp, _vp, _vp, _vp, _vp]),
     "gs_render_fwd": (ctypes.c_int, [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
     "gs_render_fwd_flow": (
         ctypes.c_int,

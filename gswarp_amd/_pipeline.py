@@ -294,8 +294,8 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
         events = _stage_chain(("duplicate", "sort", "ranges", "sort") + (("render",) if images is not None else ()))
         img = images
         lib.call("gs_readback_bin_packed", info.data_ptr(), pinned.data_ptr(), P, pre.radii.data_ptr(),
-                 pre.records.data_ptr(), pre.conic_2d_inv.data_ptr(), _lib.ptr(pre.coverage), offsets.data_ptr(),
-                 image_width, image_height, pre.coverage_mode, DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN if mode == "warp_depth_stable_tile" else 0,
+                 pre.records.data_ptr(), pre.conic_2d_inv.data_ptr(), _lib.ptr(pre.coverage), _depths_or_none(pre),
+                 offsets.data_ptr(), image_width, image_height, pre.coverage_mode, DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN if mode == "warp_depth_stable_tile" else 0,
                  capacity, ws.data_ptr(), ws.numel(), ranges.data_ptr(), point_list.data_ptr(),
                  None if img is None else img.background.data_ptr(), int(img is not None and img.compute_depth),
                  None if img is None else img.color.data_ptr(), None if img is None else img.depth.data_ptr(),
@@ -437,7 +437,7 @@ def _binning_packed(pre: PreprocessOutputs, image_width: int, image_height: int,
         keys_out = torch.empty((R,), dtype=torch.int64, device=device) if keep_keys else None
         events = _stage_chain(("duplicate", "sort", "ranges", "sort"))
         lib.call("gs_bin_packed", P, pre.radii.data_ptr(), pre.records.data_ptr(), pre.conic_2d_inv.data_ptr(),
-                 _lib.ptr(pre.coverage), offsets.data_ptr(), image_width, image_height, pre.coverage_mode, R, layout.depth_min,
+                 _lib.ptr(pre.coverage), _depths_or_none(pre), offsets.data_ptr(), image_width, image_height, pre.coverage_mode, R, layout.depth_min,
                  layout.depth_bits, layout.value_bits, ws.data_ptr(), ws.numel(), ranges.data_ptr(),
                  point_list.data_ptr(), _lib.ptr(keys_out), events, stream)
         return BinningState(grid_x, grid_y, point_list, ranges, R, keys_out, layout)
@@ -449,7 +449,8 @@ def _binning_packed(pre: PreprocessOutputs, image_width: int, image_height: int,
         vals_alt = torch.empty((R,), dtype=torch.int32, device=device)
     with _stage("duplicate"):
         lib.call("gs_duplicate_keys", P, pre.radii.data_ptr(), pre.records.data_ptr(),
-                 pre.conic_2d_inv.data_ptr(), _lib.ptr(pre.coverage), offsets.data_ptr(), image_width, image_height, pre.coverage_mode, R,
+                 pre.conic_2d_inv.data_ptr(), _lib.ptr(pre.coverage), _depths_or_none(pre), offsets.data_ptr(),
+                 image_width, image_height, pre.coverage_mode, R,
                  layout.depth_min, layout.depth_bits, layout.value_bits, keys.data_ptr(), _lib.ptr(vals), stream)
     sort_bits = tile_bits + layout.depth_bits
     sort_scratch = torch.empty((max(int(lib.gs_sort_scratch_bytes(R)), 1),), dtype=torch.uint8, device=device)
@@ -562,6 +563,12 @@ def forward(inputs: RasterInputs, options: ExecutionOptions, *, flow: bool = Fal
         state=ForwardState(pre, bins, res.n_contrib),
         aux=res.aux,
     )
+
+
+def _depths_or_none(pre: PreprocessOutputs) -> int | None:
+    """Address of the preprocess depths for the emission's key field, or None
+    (a state restored from raw buffers has none; the records hold a copy)."""
+    return pre.depths.data_ptr() if pre.depths.numel() == pre.radii.numel() and pre.radii.numel() > 0 else None
 
 
 def _f32c_or_none(t: torch.Tensor | None) -> torch.Tensor | None:

@@ -251,6 +251,7 @@ __device__ __forceinline__ void for_each_covered_tile(float px, float py, float 
 // large splats (a few hundred tiles each) a serial walk holds a whole wave
 // for the longest of its Gaussians.
 constexpr int kLaneEmitMax = 32;
+constexpr int kMaskLaneEmitMax = 8;  // the same threshold for Gaussians emitted from a cover mask
 
 __device__ __forceinline__ float bcast_f(float v, int src) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
@@ -382,9 +383,9 @@ __device__ __forceinline__ void emit_balanced(bool active, int count, float px, 
                                               long long limit, WO&& write_own, WF&& write_from) {
   __shared__ int s_stage[256 / 64][kEmitWindow];  // one window per wave of the 256-thread workgroup
   int* stage = s_stage[threadIdx.x >> 6];
-  const bool large = active && count > kLaneEmitMax;
+  const CoverWord cw = unpack_cover(cover_w);
+  const bool large = active && count > (cw.has_mask ? kMaskLaneEmitMax : kLaneEmitMax);
   if (active && !large) {
-    const CoverWord cw = unpack_cover(cover_w);
     if (cw.has_mask) {
       emit_mask_lane(cw, grid_x, off, limit, write_own);
     } else {
@@ -420,6 +421,7 @@ __global__ __launch_bounds__(256) void duplicate_keys_kernel(int P, const int* _
                                                             const float4* __restrict__ records,
                                                             const float* __restrict__ cov2d,
                                                             const int4* __restrict__ coverage,
+                                                            const float* __restrict__ depths,
                                                             const int* __restrict__ offsets, int grid_x,
                                                             int grid_y, int mode, long long limit,
                                                             unsigned depth_min, int depth_bits, int value_bits,
@@ -437,14 +439,19 @@ __global__ __launch_bounds__(256) void duplicate_keys_kernel(int P, const int* _
   if (active) {
     off = idx > 0 ? (long long)offsets[idx - 1] : 0;
     count = (int)((long long)offsets[idx] - off);
-    r0 = records[3 * (size_t)idx + 0];
-    r1 = records[3 * (size_t)idx + 1];
     if (coverage) cover_w = coverage[idx];
+    float depth;
     if (!unpack_cover(cover_w).has_mask) {
+      r0 = records[3 * (size_t)idx + 0];
+      r1 = records[3 * (size_t)idx + 1];
       cov_aa = cov2d[3 * idx + 0];
       cov_cc = cov2d[3 * idx + 2];
+      depth = r1.z;
+    } else {
+      // the record's depth, from the contiguous copy when there is one
+      depth = depths ? depths[idx] : records[3 * (size_t)idx + 1].z;
     }
-    const unsigned long long doff = (unsigned long long)(__float_as_uint(r1.z) - depth_min);
+    const unsigned long long doff = (unsigned long long)(__float_as_uint(depth) - depth_min);
     field = (doff << value_bits) | (value_bits > 0 ? (unsigned long long)idx : 0ull);
   }
   const int tile_shift = depth_bits + value_bits;
@@ -687,8 +694,8 @@ extern "C" int gs_num_rendered_readback(const int64_t* info_dev, int64_t* info_h
 }
 
 extern "C" int gs_duplicate_keys(int32_t P, const int32_t* radii, const float* records,
-                                 const float* conic_2d_inv, const int32_t* coverage, const int32_t* offsets,
-                                 int32_t image_width,
+                                 const float* conic_2d_inv, const int32_t* coverage, const float* depths,
+                                 const int32_t* offsets, int32_t image_width,
                                  int32_t image_height, int32_t coverage_mode, int64_t num_rendered,
                                  uint32_t depth_min, int32_t depth_bits, int32_t value_bits, uint64_t* keys_out,
                                  int32_t* values_out, void* stream) {
@@ -706,7 +713,7 @@ extern "C" int gs_duplicate_keys(int32_t P, const int32_t* radii, const float* r
   if ((reinterpret_cast<uintptr_t>(records) | reinterpret_cast<uintptr_t>(coverage)) & 15) return GS_ERR_MISALIGNED;
   hipLaunchKernelGGL(gs::duplicate_keys_kernel, dim3((P + 255) / 256), dim3(256), 0, (hipStream_t)stream, P,
                      radii, reinterpret_cast<const float4*>(records), conic_2d_inv,
-                     reinterpret_cast<const int4*>(coverage), offsets, grid_x, grid_y,
+                     reinterpret_cast<const int4*>(coverage), depths, offsets, grid_x, grid_y,
                      coverage_mode, (long long)num_rendered, depth_min, depth_bits, value_bits,
                      reinterpret_cast<unsigned long long*>(keys_out), values_out);
   return gs_status_from_hip(hipGetLastError());
@@ -788,7 +795,8 @@ extern "C" size_t gs_bin_packed_workspace_bytes(int64_t num_rendered) {
 }
 
 extern "C" int gs_bin_packed(int32_t P, const int32_t* radii, const float* records, const float* conic_2d_inv,
-                             const int32_t* coverage, const int32_t* offsets, int32_t image_width,
+                             const int32_t* coverage, const float* depths, const int32_t* offsets,
+                             int32_t image_width,
                              int32_t image_height,
                              int32_t coverage_mode, int64_t num_rendered, uint32_t depth_min, int32_t depth_bits,
                              int32_t value_bits, void* workspace, size_t workspace_bytes, int32_t* ranges,
@@ -819,7 +827,7 @@ extern "C" int gs_bin_packed(int32_t P, const int32_t* radii, const float* recor
     if (stage_events) (void)hipEventRecord((hipEvent_t)stage_events[k], s);
   };
   mark(0);
-  int st = gs_duplicate_keys(P, radii, records, conic_2d_inv, coverage, offsets, image_width, image_height,
+  int st = gs_duplicate_keys(P, radii, records, conic_2d_inv, coverage, depths, offsets, image_width, image_height,
                              coverage_mode, num_rendered, depth_min, depth_bits, value_bits, keys, nullptr, stream);
   if (st != GS_OK) return st;
   mark(1);
@@ -861,8 +869,8 @@ extern "C" int gs_bin_packed(int32_t P, const int32_t* radii, const float* recor
 // launched too (out_color given).
 extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_host_pinned, int32_t P,
                                       const int32_t* radii, const float* records, const float* conic_2d_inv,
-                                      const int32_t* coverage, const int32_t* offsets, int32_t image_width,
-                                      int32_t image_height,
+                                      const int32_t* coverage, const float* depths, const int32_t* offsets,
+                                      int32_t image_width, int32_t image_height,
                                       int32_t coverage_mode, int32_t max_pairs_per_point, int64_t capacity,
                                       void* workspace, size_t workspace_bytes, int32_t* ranges, int32_t* point_list,
                                       const float* background, int32_t compute_depth, float* out_color,
@@ -890,7 +898,8 @@ extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_hos
   if (R <= 0 || R > 0x7fffffffLL || R > capacity) return GS_OK;
   if (tile_bits + depth_bits + value_bits > 64 || value_bits > 31) return GS_OK;
   if (max_pairs_per_point > 0 && R > (int64_t)max_pairs_per_point * P) return GS_OK;
-  st = gs_bin_packed(P, radii, records, conic_2d_inv, coverage, offsets, image_width, image_height, coverage_mode, R,
+  st = gs_bin_packed(P, radii, records, conic_2d_inv, coverage, depths, offsets, image_width, image_height,
+                     coverage_mode, R,
                      depth_min, depth_bits, value_bits, workspace, workspace_bytes, ranges, point_list, nullptr,
                      stage_events, stream);
   if (st != GS_OK) return st;

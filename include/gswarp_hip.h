@@ -147,12 +147,14 @@ int gs_num_rendered_readback(const int64_t* info_dev, int64_t* info_host_pinned,
  * Pairs are produced in point-index order; a stable sort on the tile and
  * depth fields then yields the reference's (tile, depth, index) order.
  * coverage (optional) is gs_preprocess_fwd's cover words for the same
- * inputs; Gaussians with a mask are emitted from it.
+ * inputs; Gaussians with a mask are emitted from it.  depths (optional) is
+ * gs_preprocess_fwd's depths, read instead of the records' copy.
  * Replaces: binning_kernels.py:411-451 with binning_kernels.py:127-216 and
  * the depth sort that precedes it (binning_ops.py:152-222).
  */
 int gs_duplicate_keys(int32_t P, const int32_t* radii, const float* records, const float* conic_2d_inv,
-                      const int32_t* coverage, const int32_t* offsets, int32_t image_width, int32_t image_height,
+                      const int32_t* coverage, const float* depths, const int32_t* offsets, int32_t image_width,
+                      int32_t image_height,
                       int32_t coverage_mode, int64_t num_rendered, uint32_t depth_min, int32_t depth_bits,
                       int32_t value_bits, uint64_t* keys_out, int32_t* values_out, void* stream);
 
@@ -240,7 +242,8 @@ int gs_sort_tile_segments(int64_t n, uint64_t* keys, uint64_t* keys_alt, int32_t
  */
 size_t gs_bin_packed_workspace_bytes(int64_t num_rendered);
 int gs_bin_packed(int32_t P, const int32_t* radii, const float* records, const float* conic_2d_inv,
-                  const int32_t* coverage, const int32_t* offsets, int32_t image_width, int32_t image_height,
+                  const int32_t* coverage, const float* depths, const int32_t* offsets, int32_t image_width,
+                  int32_t image_height,
                   int32_t coverage_mode,
                   int64_t num_rendered, uint32_t depth_min, int32_t depth_bits, int32_t value_bits, void* workspace,
                   size_t workspace_bytes, int32_t* ranges, int32_t* point_list, uint64_t* sorted_keys_out,
@@ -268,7 +271,8 @@ int gs_bin_packed(int32_t P, const int32_t* radii, const float* records, const f
  */
 int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_host_pinned, int32_t P, const int32_t* radii,
                            const float* records, const float* conic_2d_inv, const int32_t* coverage,
-                           const int32_t* offsets, int32_t image_width, int32_t image_height, int32_t coverage_mode,
+                           const float* depths, const int32_t* offsets, int32_t image_width, int32_t image_height,
+                           int32_t coverage_mode,
                            int32_t max_pairs_per_point, int64_t capacity, void* workspace, size_t workspace_bytes,
                            int32_t* ranges, int32_t* point_list, const float* background, int32_t compute_depth,
                            float* out_color, float* out_depth, float* out_alpha, int32_t* n_contrib,
