@@ -205,7 +205,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_apply_kernel(int n, const i
 }
 
 // Visits one Gaussian's covered tiles in the enumeration order of
-// count_covered_tiles (binning_kernels.py:127-216 semantics), calling
+// the coverage count (binning_kernels.py:127-216 semantics), calling
 // f(tile_id) for each.
 template <typename F>
 __device__ __forceinline__ void for_each_covered_tile(float px, float py, float ca, float cb, float cc,
@@ -257,15 +257,6 @@ __device__ __forceinline__ float bcast_f(float v, int src) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
 }
 
-__device__ __forceinline__ int wave_inclusive_scan_i32(int x) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
-  }
-  return x;
-}
 
 // One Gaussian's pairs written by the whole wave (all lanes hold the same
 // arguments).  write(position, tile id) stores one pair; positions start at

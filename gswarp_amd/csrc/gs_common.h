@@ -390,52 +390,129 @@ __device__ __forceinline__ int cover_cell_tile(const CoverWord& c, float rcp_spa
   return c.columns ? (c.ry + u) * grid_x + (c.rx + band) : (c.ry + band) * grid_x + (c.rx + u);
 }
 
-// Number of tiles a Gaussian is binned to under the given coverage mode, and
-// its cover mask when the rectangle is small enough.
+// Inclusive sum and maximum over the lanes of a wave (every lane active).
+__device__ __forceinline__ int wave_inclusive_scan_i32(int x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  return x;
+}
+
+__device__ __forceinline__ int wave_inclusive_max_i32(int x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x = y > x ? y : x;
+  }
+  return x;
+}
+
+// Per-wave LDS for wave_count_covered_tiles.
+struct CoverCountLds {
+  int mark[64];
+  unsigned count[64];
+  unsigned long long mask[64];
+};
+
+// Number of tiles each lane's Gaussian is binned to under the given coverage
+// mode (active lanes; inactive ones get 0), and its cover mask when the
+// rectangle is small enough; every lane of the wave must call it.
 // Mode kCoverageConicRect counts tiles exactly only up to kConicMaskMaxTiles
 // candidate tiles and falls back to AccuTile beyond that, which is the
 // effective behaviour of the reference binning stage for that mode.
-__device__ __forceinline__ int count_covered_tiles(float px, float py, float cov_aa, float cov_cc, float ca,
-                                                   float cb, float cc, float opacity, int cuda_radius,
-                                                   int grid_x, int grid_y, int mode, TileCover& cover) {
-  const int4 rect = snugbox_rect(px, py, cov_aa, cov_cc, opacity, cuda_radius, grid_x, grid_y);
-  const int span_x = rect.z - rect.x;
-  const int span_y = rect.w - rect.y;
-  const int area = span_x * span_y;
-  cover.rect = rect;
-  cover.columns = 0;
-  cover.has_mask = span_x >= 0 && span_y >= 0 && area <= kCoverMaskCells && rect.x <= 0xffff && rect.y <= 0xffff;
-  cover.mask = 0;
-  if (area <= 1 || mode == kCoverageSnugbox) {
-    if (cover.has_mask) cover.mask = low_bits64(area);
-    return area;
-  }
-  const float threshold = coverage_threshold(opacity);
+// The AccuTile bands of the wave's Gaussians (one tile row or column each,
+// rows when span_y <= span_x) are walked flattened over the lanes, 64 bands
+// per step, so a step costs one band interval whatever the mix of small and
+// large Gaussians: a band's owner is the last lane whose first band is at
+// or before it (marks in LDS and a prefix maximum), the owner's parameters
+// come by lane shuffle, and each band adds its length and mask bits to its
+// owner's LDS accumulators.  The counts and masks are those of the serial
+// walk band by band (count_covered_tiles semantics of binning_kernels.py).
+__device__ __forceinline__ int wave_count_covered_tiles(bool active, float px, float py, float cov_aa, float cov_cc,
+                                                        float ca, float cb, float cc, float opacity, int cuda_radius,
+                                                        int grid_x, int grid_y, int mode, TileCover& cover,
+                                                        CoverCountLds& lds) {
+  static_assert(kBlockX == kBlockY, "row and column bands share one band routine");
+  const int lane = threadIdx.x & 63;
   int count = 0;
-  if (mode == kCoverageConicRect && area <= kConicMaskMaxTiles) {
-    for (int ty = rect.y; ty < rect.w; ++ty)
-      for (int tx = rect.x; tx < rect.z; ++tx)
-        if (conic_rect_intersects_tile(px, py, ca, cb, cc, threshold, tx, ty)) {
-          ++count;
-          if (cover.has_mask) cover.mask |= 1ull << ((ty - rect.y) * span_x + (tx - rect.x));
-        }
-    return count;
+  int nbands = 0;
+  float threshold = 0.0f;
+  cover.rect = make_int4(0, 0, 0, 0);
+  cover.columns = 0;
+  cover.has_mask = 0;
+  cover.mask = 0;
+  if (active) {
+    const int4 rect = snugbox_rect(px, py, cov_aa, cov_cc, opacity, cuda_radius, grid_x, grid_y);
+    const int span_x = rect.z - rect.x;
+    const int span_y = rect.w - rect.y;
+    const int area = span_x * span_y;
+    cover.rect = rect;
+    cover.has_mask = span_x >= 0 && span_y >= 0 && area <= kCoverMaskCells && rect.x <= 0xffff && rect.y <= 0xffff;
+    if (area <= 1 || mode == kCoverageSnugbox) {
+      count = area;
+      if (cover.has_mask) cover.mask = low_bits64(area);
+    } else {
+      threshold = coverage_threshold(opacity);
+      if (mode == kCoverageConicRect && area <= kConicMaskMaxTiles) {
+        for (int ty = rect.y; ty < rect.w; ++ty)
+          for (int tx = rect.x; tx < rect.z; ++tx)
+            if (conic_rect_intersects_tile(px, py, ca, cb, cc, threshold, tx, ty)) {
+              ++count;
+              if (cover.has_mask) cover.mask |= 1ull << ((ty - rect.y) * span_x + (tx - rect.x));
+            }
+      } else {
+        cover.columns = span_y > span_x;
+        nbands = imax(0, cover.columns ? span_x : span_y);
+      }
+    }
   }
-  if (span_y <= span_x) {
-    for (int ty = rect.y; ty < rect.w; ++ty) {
-      const int2 iv = accutile_band(px, py, ca, cb, cc, threshold, ty, kBlockX, kBlockY, rect.x, rect.z);
+  const int incl = wave_inclusive_scan_i32(nbands);
+  const int excl = incl - nbands;
+  const int total = __builtin_amdgcn_readlane(incl, 63);
+  lds.count[lane] = 0u;
+  lds.mask[lane] = 0ull;
+  // the owner's view, gathered once per step by lane shuffle
+  const float pu = cover.columns ? py : px, pv = cover.columns ? px : py;
+  const float cuu = cover.columns ? cc : ca, cvv = cover.columns ? ca : cc;
+  const int v0 = cover.columns ? cover.rect.x : cover.rect.y;
+  const int u_min = cover.columns ? cover.rect.y : cover.rect.x;
+  const int u_max = cover.columns ? cover.rect.w : cover.rect.z;
+  const int mask_span = cover.has_mask ? u_max - u_min : -1;  // -1: no mask
+  for (int t0 = 0; t0 < total; t0 += 64) {
+    lds.mark[lane] = -1;
+    __builtin_amdgcn_wave_barrier();
+    if (nbands > 0 && excl < t0 && incl > t0) lds.mark[0] = lane;  // bands carried in from the last step
+    __builtin_amdgcn_wave_barrier();
+    if (nbands > 0 && excl >= t0 && excl < t0 + 64) lds.mark[excl - t0] = lane;
+    __builtin_amdgcn_wave_barrier();
+    const int f = t0 + lane;
+    const bool valid = f < total;
+    const int owner = wave_inclusive_max_i32(lds.mark[lane]);  // every lane takes part
+    const int o = (valid && owner >= 0) ? owner : lane;  // every valid position has an owner
+    const int b = f - __shfl(excl, o, 64);
+    const float o_pu = __shfl(pu, o, 64), o_pv = __shfl(pv, o, 64);
+    const float o_cuu = __shfl(cuu, o, 64), o_cuv = __shfl(cb, o, 64), o_cvv = __shfl(cvv, o, 64);
+    const float o_thr = __shfl(threshold, o, 64);
+    const int o_v0 = __shfl(v0, o, 64), o_umin = __shfl(u_min, o, 64), o_umax = __shfl(u_max, o, 64);
+    const int o_mspan = __shfl(mask_span, o, 64);
+    if (valid) {
+      const int2 iv = accutile_band(o_pu, o_pv, o_cuu, o_cuv, o_cvv, o_thr, o_v0 + b, kBlockX, kBlockY, o_umin,
+                                    o_umax);
       const int len = imax(0, iv.y - iv.x);
-      count += len;
-      if (cover.has_mask && len > 0) cover.mask |= low_bits64(len) << ((ty - rect.y) * span_x + (iv.x - rect.x));
+      if (len > 0) {
+        atomicAdd(&lds.count[o], (unsigned)len);
+        if (o_mspan >= 0) atomicOr(&lds.mask[o], low_bits64(len) << (b * o_mspan + (iv.x - o_umin)));
+      }
     }
-  } else {
-    cover.columns = 1;
-    for (int tx = rect.x; tx < rect.z; ++tx) {
-      const int2 iv = accutile_band(py, px, cc, cb, ca, threshold, tx, kBlockY, kBlockX, rect.y, rect.w);
-      const int len = imax(0, iv.y - iv.x);
-      count += len;
-      if (cover.has_mask && len > 0) cover.mask |= low_bits64(len) << ((tx - rect.x) * span_y + (iv.x - rect.y));
-    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  if (nbands > 0) {
+    count += (int)lds.count[lane];
+    cover.mask |= lds.mask[lane];
   }
   return count;
 }

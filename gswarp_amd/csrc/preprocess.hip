@@ -111,9 +111,13 @@ __device__ __forceinline__ float3 sh_color(const float* __restrict__ sh_mem, int
   return c;
 }
 
+// Every lane of the grid stays to the end (lanes past P as culled
+// Gaussians): the tile count is a wave-wide walk.
 __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p) {
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= p.P) return;
+  __shared__ CoverCountLds s_cover[256 / 64];
+  const int idx0 = blockIdx.x * blockDim.x + threadIdx.x;
+  const bool in_range = idx0 < p.P;
+  const int idx = in_range ? idx0 : p.P - 1;  // loads stay in bounds; nothing is stored for it
   const float* __restrict__ V = p.view;
   const float* __restrict__ Pm = p.proj;
   const float mx = p.means3d[3 * idx + 0];
@@ -125,10 +129,13 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p)
   float con0 = 0.0f, con1 = 0.0f, con2 = 0.0f;
   float cov_a = 0.0f, cov_b = 0.0f, cov_c = 0.0f;
   int touched = 0;
-  int4 cover_word = make_int4(0, 0, 0, 0);
+  // inputs of the tile count, set for visible Gaussians
+  bool count_it = false;
+  float c_px = 0.0f, c_py = 0.0f, c_aa = 0.0f, c_cc = 0.0f, c_q0 = 0.0f, c_q1 = 0.0f, c_q2 = 0.0f, c_op = 0.0f;
+  int c_rad = 0;
 
   const float p_view_z = V[2] * mx + V[6] * my + V[10] * mz + V[14];
-  bool visible = p_view_z > kNearPlane;
+  bool visible = in_range && p_view_z > kNearPlane;
   if (visible) {
     const float hom_x = Pm[0] * mx + Pm[4] * my + Pm[8] * mz + Pm[12];
     const float hom_y = Pm[1] * mx + Pm[5] * my + Pm[9] * mz + Pm[13];
@@ -242,10 +249,8 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p)
         pyo = pty;
         con0 = q0; con1 = q1; con2 = q2;
         cov_a = fa; cov_b = cb; cov_c = fc;
-        TileCover cover;
-        touched = count_covered_tiles(ptx, pty, fa, fc, q0, q1, q2, op, frad, p.grid_x, p.grid_y,
-                                      p.coverage_mode, cover);
-        cover_word = pack_cover(cover);
+        count_it = true;
+        c_px = ptx; c_py = pty; c_aa = fa; c_cc = fc; c_q0 = q0; c_q1 = q1; c_q2 = q2; c_op = op; c_rad = frad;
 
         float3 col;
         uint8_t clamp_bits = 0;
@@ -277,6 +282,10 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p)
       }
     }
   }
+  TileCover cover;
+  touched = wave_count_covered_tiles(count_it, c_px, c_py, c_aa, c_cc, c_q0, c_q1, c_q2, c_op, c_rad, p.grid_x,
+                                     p.grid_y, p.coverage_mode, cover, s_cover[threadIdx.x >> 6]);
+  if (!in_range) return;
   if (!visible && p.clamped != nullptr) p.clamped[idx] = 0;
   p.radii[idx] = radius;
   p.depths[idx] = depth;
@@ -289,7 +298,7 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p)
   p.conic_2d_inv[3 * idx + 1] = cov_b;
   p.conic_2d_inv[3 * idx + 2] = cov_c;
   p.tiles_touched[idx] = touched;
-  if (p.coverage != nullptr) p.coverage[idx] = cover_word;
+  if (p.coverage != nullptr) p.coverage[idx] = pack_cover(cover);
 }
 
 // markVisible: view-space z beyond the near plane (preprocess_kernels.py:604-617).

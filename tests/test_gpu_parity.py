@@ -95,9 +95,18 @@ def test_other_sort_modes_match_oracle(case, sort_mode, device, monkeypatch):
     _check_forward(scene, options(sort_mode=sort_mode))
 
 
-@pytest.mark.parametrize("coverage_mode", [0, 2])
-def test_alternative_coverage_modes_match_oracle(coverage_mode, device):
-    scene = configs.make_scene(1, count=20_000, width=320, height=256, device=device)
+COVERAGE_SCENES = {
+    "c1": dict(config=1, count=20_000, width=320, height=256),
+    # large splats: tile rectangles beyond 64 cells take the band walk, the rest the cover masks
+    "c3": dict(config=3, count=20_000, width=480, height=270),
+}
+
+
+@pytest.mark.parametrize("coverage_mode", [0, 1, 2])
+@pytest.mark.parametrize("scene_name", list(COVERAGE_SCENES))
+def test_alternative_coverage_modes_match_oracle(scene_name, coverage_mode, device):
+    kw = dict(COVERAGE_SCENES[scene_name])
+    scene = configs.make_scene(kw.pop("config"), device=device, **kw)
     _check_forward(scene, options(coverage_mode=coverage_mode), coverage_mode=coverage_mode)
 
 
