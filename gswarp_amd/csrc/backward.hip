@@ -268,15 +268,20 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
       const float b2dx = (a.w * dx) * 2.0f;
       float q[kPix], dy[kPix];
       bool cand[kPix];
-      bool any = false;
+      uint64_t cand_lanes[kPix];  // the wave's lanes with cand[k]
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
         dy[k] = a.y - pfy[k];
         q[k] = conic_q_px(adxx, b2dx, b.x, dy[k]);  // exponent = -0.5 q
         cand[k] = pos < last[k] && q[k] >= 0.0f && q[k] <= b.w;
-        any |= cand[k];
+        // the same comparisons as lane masks, ANDed in scalar registers
+        cand_lanes[k] = __builtin_amdgcn_sicmp(pos, last[k], kCmpSLT) & __builtin_amdgcn_fcmpf(q[k], 0.0f, kCmpOGE) &
+                        __builtin_amdgcn_fcmpf(q[k], b.w, kCmpOLE);
       }
-      if (__ballot(any) == 0) continue;
+      uint64_t any_lanes = 0;
+#pragma unroll
+      for (int k = 0; k < kPix; ++k) any_lanes |= cand_lanes[k];
+      if (any_lanes == 0) continue;
       // Blend decisions, identical to the forward's: with the exponent above
       // power_cutoff + 2e-3 (q <= qcut - 4e-3) the forward's alpha is provably
       // >= 1/255 (the cutoff sits 1e-3 below -ln(255 o) and exp_sw / log_sw
@@ -293,8 +298,7 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
         e[k] = (cand[k] && sure) ? q[k] * (-0.5f * kLog2e) : -__builtin_inff();
         // cand && !sure from the comparisons' lane masks (scalar ANDs; the
         // compiler reuses the comparisons made above)
-        band |= __builtin_amdgcn_sicmp(pos, last[k], kCmpSLT) & __builtin_amdgcn_fcmpf(q[k], 0.0f, kCmpOGE) &
-                __builtin_amdgcn_fcmpf(q[k], b.w, kCmpOLE) & ~__builtin_amdgcn_fcmpf(q[k], qsure, kCmpOLE);
+        band |= cand_lanes[k] & ~__builtin_amdgcn_fcmpf(q[k], qsure, kCmpOLE);
       }
       if (band != 0) {
 #pragma unroll
@@ -305,9 +309,14 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
         }
       }
       const float4 f = s_rec[3 * jj + 2];
-      float sv, svy, svyy, sr, sg, sb, sd;
+      // -0 is the additive identity of every float, so the first terms
+      // enter the sums exactly (and the compiler drops the additions).
+      float sv = -0.0f, svy = -0.0f, svyy = -0.0f, sr = -0.0f, sg = -0.0f, sb = -0.0f, sd = -0.0f;
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
+        // A pixel row set with no candidate in the whole wave is skipped:
+        // there G = 0 for every lane, which leaves T, S and the sums unchanged.
+        if (cand_lanes[k] == 0) continue;
         // Gradient values use the hardware exponential (v_exp_f32): they only
         // need the 1e-3 gradient tolerance, the decisions above are exact.
         // A pixel that does not blend this Gaussian gets G = 2^-inf = 0, so
@@ -323,23 +332,13 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
         const float v = G * (Tn * d);
         const float dch = alpha * Tn;
         const float vdy = v * dy[k];
-        if (k == 0) {
-          sv = v;
-          svy = vdy;
-          svyy = vdy * dy[k];
-          sr = dch * gp0[k];
-          sg = dch * gp1[k];
-          sb = dch * gp2[k];
-          sd = kDepth ? dch * gpd[k] : 0.0f;
-        } else {
-          sv += v;
-          svy += vdy;
-          svyy = fmaf(vdy, dy[k], svyy);
-          sr = fmaf(dch, gp0[k], sr);
-          sg = fmaf(dch, gp1[k], sg);
-          sb = fmaf(dch, gp2[k], sb);
-          if (kDepth) sd = fmaf(dch, gpd[k], sd);
-        }
+        sv += v;
+        svy += vdy;
+        svyy = fmaf(vdy, dy[k], svyy);
+        sr = fmaf(dch, gp0[k], sr);
+        sg = fmaf(dch, gp1[k], sg);
+        sb = fmaf(dch, gp2[k], sb);
+        if (kDepth) sd = fmaf(dch, gpd[k], sd);
         // this Gaussian joins what lies behind the next (nearer) one:
         // alpha fu + (1 - alpha) S = S + alpha (fu - S)
         S[k] = fmaf(alpha, d, S[k]);
