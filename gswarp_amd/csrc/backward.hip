@@ -1,7 +1,9 @@
 // Manual backward for gfx950.
 //
-// render_bwd: wave64 workgroups each own a slice of a tile and walk the
-// tile's list back to front from the largest n_contrib of their pixels
+// render_bwd: wave64 workgroups each own a slice of a tile (16x8 with two
+// pixels per lane, or 16x4 with one for tiles whose list is more than four
+// times the mean) and walk the tile's list back to front from the largest
+// n_contrib of their pixels
 // (backward_kernels.py:539-707 semantics: T starts at 1 - alpha_out and is
 // divided by max(1-alpha, 1e-5) per blended Gaussian, reverse recurrences for
 // colour, depth and alpha, the background term).  Per Gaussian each lane
@@ -34,10 +36,10 @@ constexpr float kSureMargin = 2.0e-3f;  // exponents this far above the cutoff a
 constexpr float kLog2e = 1.44269504088896341f;
 // Comparison predicates of the lane-mask compare builtins (LLVM's codes).
 constexpr int kCmpOGE = 3, kCmpOLE = 5, kCmpSLT = 40;
-#ifndef GS_BWD_PIX
-#define GS_BWD_PIX 2
+#ifndef GS_LONG_TILE_FACTOR
+#define GS_LONG_TILE_FACTOR 4
 #endif
-constexpr int kBwdPix = GS_BWD_PIX;  // pixels per lane: 1, 2 or 4
+constexpr int64_t kLongTileFactor = GS_LONG_TILE_FACTOR;  // long tile: list longer than this many times the mean
 
 template <int kCtrl, int kRowMask>
 __device__ __forceinline__ float dpp_mov(float src) {
@@ -138,6 +140,7 @@ struct RenderBwdParams {
   const float* grad_depth;
   const float* grad_alpha;
   int compute_depth;
+  int long_tile;  // list length above which a tile is walked by four one-pixel-per-lane slices
   float* grad_gauss;
 };
 
@@ -188,18 +191,17 @@ __device__ __forceinline__ BwdBatch load_bwd_batch(const RenderBwdParams& p, int
 //   dL/dopacity = sum(v).  Each batch of 64
 // records is first tested lane-parallel against the slice rectangle
 // (record_may_touch) and only records that may touch it are visited.
+// One wave's slice `sub` (rows 4 kPix sub .. 4 kPix sub + 4 kPix - 1) of
+// `tile`; s_rec (3 x 64 float4) and s_ring (kRingSlots x kSlotFloats +
+// kRingPad floats, 16-byte aligned) are the wave's LDS.
 template <bool kDepth, int kPix>
-__global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
-  constexpr int kSubs = 4 / kPix;
-  __shared__ float4 s_rec[3 * 64];  // record j at s_rec[3 j .. 3 j + 2]
-  __shared__ __align__(16) float s_ring[kRingSlots * kSlotFloats + kRingPad];
+__device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int tile, int sub, float4* s_rec,
+                                                 float* s_ring) {
   const int lane = threadIdx.x;
-  const int2 ts = xcd_tile_sub(blockIdx.x, p.num_tiles, kSubs);
-  const int tile = ts.x;
   const int tx = tile % p.grid_x;
   const int ty = tile / p.grid_x;
   const int sx0 = tx * kBlockX;
-  const int sy0 = ty * kBlockY + ts.y * 4 * kPix;
+  const int sy0 = ty * kBlockY + sub * 4 * kPix;
   const int px = sx0 + (lane & 15);
   const int py0 = sy0 + (lane >> 4);
   const int P = p.W * p.H;
@@ -377,6 +379,37 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
   }
   if (nrel > 0) flush_slot(s_ring, 0, slot_gid0, lane, flush_comp, p.grad_gauss);
   if (nrel > 1) flush_slot(s_ring, 1, slot_gid1, lane, flush_comp, p.grad_gauss);
+}
+
+// A tile whose list is longer than p.long_tile is walked by four one-wave
+// workgroups, each a 16x4 slice with one pixel per lane: its serial walk,
+// which bounds the kernel when a few tiles hold most of the pairs, costs
+// less per Gaussian.  Any other tile is walked by two, each a 16x8 slice
+// with two pixels per lane (fewer instructions per pixel).  The grid is a
+// segment of the first and second slices of every tile followed by one of
+// the third and fourth slices, which exit at once for ordinary tiles (each
+// segment padded to a multiple of 8 blocks): workgroups go round-robin to
+// the XCDs' CUs, and exiting workgroups interleaved with working ones at a
+// fixed period would leave some CUs with none of the work, while at the end
+// of the grid they only fill slots that the draining work leaves free.
+template <bool kDepth>
+__global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
+  __shared__ float4 s_rec[3 * 64];  // record j at s_rec[3 j .. 3 j + 2]
+  __shared__ __align__(16) float s_ring[kRingSlots * kSlotFloats + kRingPad];
+  const int two_t = 2 * p.num_tiles;
+  const int seg = (two_t + 7) & ~7;
+  const bool extra = (int)blockIdx.x >= seg;
+  const int unit = xcd_tile(extra ? blockIdx.x - seg : blockIdx.x, seg);
+  if (unit >= two_t) return;  // segment padding
+  const int tile = unit >> 1;
+  const int sub = (unit & 1) + (extra ? 2 : 0);
+  int2 rg = p.ranges[tile];
+  rg.x = imax(0, imin(rg.x, p.num_rendered));
+  rg.y = imax(rg.x, imin(rg.y, p.num_rendered));
+  if (rg.y - rg.x > p.long_tile)
+    render_bwd_slice<kDepth, 1>(p, tile, sub, s_rec, s_ring);
+  else if (!extra)
+    render_bwd_slice<kDepth, 2>(p, tile, sub, s_rec, s_ring);
 }
 
 struct PreprocessBwdParams {
@@ -855,11 +888,14 @@ extern "C" int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t 
   p.grad_alpha = grad_alpha;
   p.compute_depth = compute_depth;
   p.grad_gauss = grad_gauss;
-  const dim3 grid(p.num_tiles * (4 / gs::kBwdPix));
+  // four times the mean list length: only tiles that dominate the walk
+  const int64_t long_tile = gs::kLongTileFactor * num_rendered / p.num_tiles;
+  p.long_tile = long_tile > 0x7fffffffLL ? 0x7fffffff : (int)long_tile;
+  const dim3 grid(2 * ((2 * p.num_tiles + 7) & ~7));
   if (compute_depth)
-    hipLaunchKernelGGL((gs::render_bwd_kernel<true, gs::kBwdPix>), grid, dim3(64), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL((gs::render_bwd_kernel<true>), grid, dim3(64), 0, (hipStream_t)stream, p);
   else
-    hipLaunchKernelGGL((gs::render_bwd_kernel<false, gs::kBwdPix>), grid, dim3(64), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL((gs::render_bwd_kernel<false>), grid, dim3(64), 0, (hipStream_t)stream, p);
   return gs_status_from_hip(hipGetLastError());
 }
 
