@@ -36,10 +36,7 @@ constexpr float kSureMargin = 2.0e-3f;  // exponents this far above the cutoff a
 constexpr float kLog2e = 1.44269504088896341f;
 // Comparison predicates of the lane-mask compare builtins (LLVM's codes).
 constexpr int kCmpOGE = 3, kCmpOLE = 5, kCmpSLT = 40;
-#ifndef GS_LONG_TILE_FACTOR
-#define GS_LONG_TILE_FACTOR 4
-#endif
-constexpr int64_t kLongTileFactor = GS_LONG_TILE_FACTOR;  // long tile: list longer than this many times the mean
+constexpr int64_t kLongTileFactor = 4;  // long tile: list longer than this many times the mean
 
 template <int kCtrl, int kRowMask>
 __device__ __forceinline__ float dpp_mov(float src) {
