@@ -183,8 +183,9 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
 #pragma unroll
   for (int k = 0; k < kPixPerLane; ++k) {
     const int py = py0 + 4 * k;
-    if (px < p.W && py < p.H) {
-      const int pix = py * p.W + px;
+    const bool in_image = px < p.W && py < p.H;
+    const int pix = py * p.W + px;
+    if (in_image) {
       const float Tk = fabsf(T[k]);
       p.n_contrib[pix] = last[k];
       p.out_color[pix] = c0[k] + Tk * p.bg[0];
@@ -192,8 +193,16 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
       p.out_color[2 * P + pix] = c2[k] + Tk * p.bg[2];
       p.out_alpha[pix] = ws[k];
       p.out_depth[pix] = da[k];
-      if (aux) {
-        for (int s = nsucc[k]; s < p.top_k; ++s) {
+    }
+    if (aux) {
+      // Unused slots, plane by plane for the whole wave, so that each store
+      // covers the wave's pixels of one plane (rows of 16 consecutive
+      // pixels) rather than one plane per lane.
+      int s_from = in_image ? nsucc[k] : p.top_k;
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) s_from = imin(s_from, __shfl_xor(s_from, off, 64));
+      for (int s = s_from; s < p.top_k; ++s) {
+        if (in_image && s >= nsucc[k]) {
           const size_t ai = (size_t)s * P + pix;
           p.gs_per_pixel[ai] = -1;
           p.weight[ai] = 0.0f;
