@@ -710,15 +710,16 @@ extern "C" int gs_duplicate_keys(int32_t P, const int32_t* radii, const float* r
   return gs_status_from_hip(hipGetLastError());
 }
 
-extern "C" int gs_tile_ranges(int64_t n, const uint64_t* sorted_keys, int32_t tile_shift, int32_t value_bits,
-                              int32_t num_tiles, int32_t* ranges, int32_t* point_list, void* stream) {
+// Tile ranges, with the clearing of ranges left out when the caller has
+// already cleared them on the stream.
+static int tile_ranges_impl(int64_t n, const uint64_t* sorted_keys, int32_t tile_shift, int32_t value_bits,
+                            int32_t num_tiles, int32_t* ranges, int32_t* point_list, bool cleared, hipStream_t s) {
   if (n < 0 || num_tiles <= 0 || !ranges) return GS_ERR_INVALID_ARGUMENT;
   if (tile_shift < 0 || tile_shift > 63 || value_bits < 0 || value_bits > 31 || value_bits > tile_shift)
     return GS_ERR_INVALID_ARGUMENT;
   if (n > 0x7fffffffLL) return GS_ERR_OVERFLOW;
-  hipStream_t s = (hipStream_t)stream;
   const int n2 = 2 * num_tiles;
-  hipLaunchKernelGGL(gs::zero_ranges_kernel, dim3((n2 + 255) / 256), dim3(256), 0, s, n2, ranges);
+  if (!cleared) hipLaunchKernelGGL(gs::zero_ranges_kernel, dim3((n2 + 255) / 256), dim3(256), 0, s, n2, ranges);
   if (n > 0) {
     if (!sorted_keys || (value_bits > 0 && !point_list)) return GS_ERR_INVALID_ARGUMENT;
     const long long threads = (n + gs::kRangeItems - 1) / gs::kRangeItems;
@@ -727,6 +728,12 @@ extern "C" int gs_tile_ranges(int64_t n, const uint64_t* sorted_keys, int32_t ti
                        reinterpret_cast<int2*>(ranges), point_list);
   }
   return gs_status_from_hip(hipGetLastError());
+}
+
+extern "C" int gs_tile_ranges(int64_t n, const uint64_t* sorted_keys, int32_t tile_shift, int32_t value_bits,
+                              int32_t num_tiles, int32_t* ranges, int32_t* point_list, void* stream) {
+  return tile_ranges_impl(n, sorted_keys, tile_shift, value_bits, num_tiles, ranges, point_list, false,
+                          (hipStream_t)stream);
 }
 
 extern "C" int gs_depth_keys(int32_t P, const int32_t* radii, const float* depths, uint32_t* keys_out,
@@ -785,14 +792,12 @@ extern "C" size_t gs_bin_packed_workspace_bytes(int64_t num_rendered) {
   return 2 * gs_align256((size_t)num_rendered * sizeof(uint64_t)) + gs_align256(gs_sort_scratch_bytes(num_rendered));
 }
 
-extern "C" int gs_bin_packed(int32_t P, const int32_t* radii, const float* records, const float* conic_2d_inv,
-                             const int32_t* coverage, const float* depths, const int32_t* offsets,
-                             int32_t image_width,
-                             int32_t image_height,
-                             int32_t coverage_mode, int64_t num_rendered, uint32_t depth_min, int32_t depth_bits,
-                             int32_t value_bits, void* workspace, size_t workspace_bytes, int32_t* ranges,
-                             int32_t* point_list, uint64_t* sorted_keys_out, void* const* stage_events,
-                             void* stream) {
+static int bin_packed_impl(int32_t P, const int32_t* radii, const float* records, const float* conic_2d_inv,
+                           const int32_t* coverage, const float* depths, const int32_t* offsets, int32_t image_width,
+                           int32_t image_height, int32_t coverage_mode, int64_t num_rendered, uint32_t depth_min,
+                           int32_t depth_bits, int32_t value_bits, void* workspace, size_t workspace_bytes,
+                           int32_t* ranges, int32_t* point_list, uint64_t* sorted_keys_out,
+                           void* const* stage_events, void* stream, bool ranges_cleared) {
   if (P < 0 || num_rendered < 0 || image_width <= 0 || image_height <= 0 || value_bits < 1 || value_bits > 31 ||
       depth_bits < 0 || depth_bits > 32)
     return GS_ERR_INVALID_ARGUMENT;
@@ -805,7 +810,8 @@ extern "C" int gs_bin_packed(int32_t P, const int32_t* radii, const float* recor
   if (tile_shift + tile_bits > 64) return GS_ERR_INVALID_ARGUMENT;
   if (!ranges) return GS_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
-  if (num_rendered == 0) return gs_tile_ranges(0, nullptr, tile_shift, 0, num_tiles, ranges, nullptr, stream);
+  if (num_rendered == 0)
+    return tile_ranges_impl(0, nullptr, tile_shift, 0, num_tiles, ranges, nullptr, ranges_cleared, s);
   if (!workspace || !point_list) return GS_ERR_INVALID_ARGUMENT;
   if (workspace_bytes < gs_bin_packed_workspace_bytes(num_rendered)) return GS_ERR_SCRATCH_TOO_SMALL;
   const size_t key_bytes = gs_align256((size_t)num_rendered * sizeof(uint64_t));
@@ -830,7 +836,7 @@ extern "C" int gs_bin_packed(int32_t P, const int32_t* radii, const float* recor
     keys = keys_alt;
     keys_alt = t;
   }
-  st = gs_tile_ranges(num_rendered, keys, tile_shift, 0, num_tiles, ranges, nullptr, stream);
+  st = tile_ranges_impl(num_rendered, keys, tile_shift, 0, num_tiles, ranges, nullptr, ranges_cleared, s);
   if (st != GS_OK) return st;
   mark(3);
   st = gs_sort_tile_segments(num_rendered, keys, keys_alt, num_tiles, ranges, value_bits, depth_bits, value_bits,
@@ -843,6 +849,19 @@ extern "C" int gs_bin_packed(int32_t P, const int32_t* radii, const float* recor
     if (e != hipSuccess) return (int)e;
   }
   return GS_OK;
+}
+
+extern "C" int gs_bin_packed(int32_t P, const int32_t* radii, const float* records, const float* conic_2d_inv,
+                             const int32_t* coverage, const float* depths, const int32_t* offsets,
+                             int32_t image_width,
+                             int32_t image_height,
+                             int32_t coverage_mode, int64_t num_rendered, uint32_t depth_min, int32_t depth_bits,
+                             int32_t value_bits, void* workspace, size_t workspace_bytes, int32_t* ranges,
+                             int32_t* point_list, uint64_t* sorted_keys_out, void* const* stage_events,
+                             void* stream) {
+  return bin_packed_impl(P, radii, records, conic_2d_inv, coverage, depths, offsets, image_width, image_height,
+                         coverage_mode, num_rendered, depth_min, depth_bits, value_bits, workspace, workspace_bytes,
+                         ranges, point_list, sorted_keys_out, stage_events, stream, false);
 }
 
 // The forward's read-back of the pair count followed, without returning to the
@@ -868,6 +887,14 @@ extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_hos
                                       float* out_depth, float* out_alpha, int32_t* n_contrib,
                                       void* const* stage_events, int64_t* result, void* stream) {
   if (!result || P < 0 || capacity < 0 || image_width <= 0 || image_height <= 0) return GS_ERR_INVALID_ARGUMENT;
+  // The ranges are cleared before the read-back, while the stream would
+  // otherwise wait for the host.
+  const bool clear_first = ranges != nullptr && capacity > 0;
+  if (clear_first) {
+    const int n2 =
+        2 * ((image_width + gs::kBlockX - 1) / gs::kBlockX) * ((image_height + gs::kBlockY - 1) / gs::kBlockY);
+    hipLaunchKernelGGL(gs::zero_ranges_kernel, dim3((n2 + 255) / 256), dim3(256), 0, (hipStream_t)stream, n2, ranges);
+  }
   int st = gs_num_rendered_readback(info_dev, info_host_pinned, stream);
   if (st != GS_OK) return st;
   const int64_t R = info_host_pinned[0];
@@ -889,10 +916,9 @@ extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_hos
   if (R <= 0 || R > 0x7fffffffLL || R > capacity) return GS_OK;
   if (tile_bits + depth_bits + value_bits > 64 || value_bits > 31) return GS_OK;
   if (max_pairs_per_point > 0 && R > (int64_t)max_pairs_per_point * P) return GS_OK;
-  st = gs_bin_packed(P, radii, records, conic_2d_inv, coverage, depths, offsets, image_width, image_height,
-                     coverage_mode, R,
-                     depth_min, depth_bits, value_bits, workspace, workspace_bytes, ranges, point_list, nullptr,
-                     stage_events, stream);
+  st = bin_packed_impl(P, radii, records, conic_2d_inv, coverage, depths, offsets, image_width, image_height,
+                       coverage_mode, R, depth_min, depth_bits, value_bits, workspace, workspace_bytes, ranges,
+                       point_list, nullptr, stage_events, stream, clear_first);
   if (st != GS_OK) return st;
   result[4] = 1;
   if (out_color) {
