@@ -960,7 +960,8 @@ extern "C" int gs_preprocess_bwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
   p.grad_sh = grad_sh;
   p.grad_opacity = grad_opacity;
   p.grad_colors = grad_colors;
-  p.sh_vec16 = (shs != nullptr && sh_coeffs == 16 && ((reinterpret_cast<uintptr_t>(shs) | reinterpret_cast<uintptr_t>(grad_sh)) & 15) == 0) ? 1 : 0;
+  const uintptr_t sh_addr_bits = reinterpret_cast<uintptr_t>(shs) | reinterpret_cast<uintptr_t>(grad_sh);
+  p.sh_vec16 = (shs != nullptr && sh_coeffs == 16 && (sh_addr_bits & 15) == 0) ? 1 : 0;
   hipLaunchKernelGGL(gs::preprocess_bwd_kernel, dim3((P + 255) / 256), dim3(256), 0, (hipStream_t)stream, p);
   return gs_status_from_hip(hipGetLastError());
 }
