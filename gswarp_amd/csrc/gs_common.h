@@ -355,7 +355,8 @@ __device__ __forceinline__ uint64_t low_bits64(int n) { return n >= 64 ? ~0ull :
 
 // Packed per-Gaussian coverage word: x = rect.x | rect.y << 16, y = span_x |
 // span_y << 8 | columns << 16 | has_mask << 17, z / w = mask low / high.
-// Only rectangles with tile coordinates below 2^16 get a mask.
+// Only rectangles with tile coordinates below 2^16 and spans below 2^8 get a
+// mask.
 __device__ __forceinline__ int4 pack_cover(const TileCover& c) {
   const int span_x = c.rect.z - c.rect.x, span_y = c.rect.w - c.rect.y;
   if (!c.has_mask) return make_int4(0, 0, 0, 0);
@@ -451,7 +452,8 @@ __device__ __forceinline__ int wave_count_covered_tiles(bool active, float px, f
     const int span_y = rect.w - rect.y;
     const int area = span_x * span_y;
     cover.rect = rect;
-    cover.has_mask = span_x >= 0 && span_y >= 0 && area <= kCoverMaskCells && rect.x <= 0xffff && rect.y <= 0xffff;
+    cover.has_mask = span_x >= 0 && span_y >= 0 && span_x <= 0xff && span_y <= 0xff &&
+                     area <= kCoverMaskCells && rect.x <= 0xffff && rect.y <= 0xffff;
     if (area <= 1 || mode == kCoverageSnugbox) {
       count = area;
       if (cover.has_mask) cover.mask = low_bits64(area);
