@@ -187,15 +187,22 @@ def _stage_of(kernel_name: str):
 # root R on the GPU box, each pass a run of its own); the summaries repeat
 # them so that each file says how it was made.
 _PROFILE_PREAMBLE = "#   cd /tmp && export TMPDIR=/tmp"
-PROFILE_COMMANDS = {
-    "stats": [
+def _stats_commands(config: int) -> list[str]:
+    c = f"c{config}"
+    cfg = "" if config == 2 else f"--config {config} "
+    return [
         _PROFILE_PREAMBLE,
-        "#   rocprofv3 --kernel-trace --stats --output-format csv -d $R/gpurun_out/prof_c2 -o c2 -- \\",
-        "#       python3 $R/bench.py --steps 10 --warmup 3 --no-cpu-baseline > $R/gpurun_out/prof_c2/bench.json \\",
-        "#       2> $R/gpurun_out/prof_c2/bench.err",
-        "#   python3 bench.py --stats-summary gpurun_out/prof_c2/c2_kernel_stats.csv profiles/kernel_stats_config2.txt \\",
-        "#       gpurun_out/prof_c2/bench.err",
-    ],
+        f"#   rocprofv3 --kernel-trace --stats --output-format csv -d $R/gpurun_out/prof_{c} -o {c} -- \\",
+        f"#       python3 $R/bench.py {cfg}--steps 10 --warmup 3 --no-cpu-baseline > $R/gpurun_out/prof_{c}/bench.json \\",
+        f"#       2> $R/gpurun_out/prof_{c}/bench.err",
+        f"#   python3 bench.py --stats-summary gpurun_out/prof_{c}/{c}_kernel_stats.csv "
+        f"profiles/kernel_stats_config{config}.txt \\",
+        f"#       gpurun_out/prof_{c}/bench.err" + ("" if config == 2 else f" --profile-config {config}"),
+    ]
+
+
+PROFILE_COMMANDS = {
+    "stats": _stats_commands(2),
     "pmc": [
         _PROFILE_PREAMBLE,
         "#   rocprofv3 --pmc FETCH_SIZE --output-format csv -d $R/gpurun_out/pmc_c2 -o fetch -- \\",
@@ -294,7 +301,15 @@ def summarize_sq(counter_csv: str, out_path: str) -> None:
     print("\n".join(lines))
 
 
-def summarize_stats(stats_csv: str, out_path: str, bench_err: str | None = None) -> None:
+CONFIG_TITLES = {
+    1: "config 1 (100k Gaussians, 800x800, SH3, fwd+bwd)",
+    2: "config 2 (1M Gaussians, 1920x1080, SH3, fwd+bwd with depth and alpha)",
+    3: "config 3 (5M Gaussians, 1920x1080, SH3, heavy tail of large splats, fwd+bwd)",
+    4: "config 4 (flow API, 1M Gaussians, 1280x720, SH3, top-K 20, fwd+bwd)",
+}
+
+
+def summarize_stats(stats_csv: str, out_path: str, bench_err: str | None = None, config: int = 2) -> None:
     """rocprofv3 --kernel-trace --stats kernel_stats.csv -> calls, average / min /
     max duration (us), share of GPU time and name of each kernel, longest first;
     with the profiled bench run's stderr, its own HIP-event stage times too."""
@@ -302,9 +317,9 @@ def summarize_stats(stats_csv: str, out_path: str, bench_err: str | None = None)
 
     rows = list(csv.DictReader(open(stats_csv)))
     rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
-    lines = ["# Kernel time, config 2 (1M Gaussians, 1920x1080, SH3, fwd+bwd with depth and alpha), one MI355X",
+    lines = [f"# Kernel time, {CONFIG_TITLES[config]}, one MI355X",
              "# 23 iterations (3 warm-up, 10 timed, 10 with per-stage events) plus bench.py's 1 GiB copy calibration",
-             "# commands:", *PROFILE_COMMANDS["stats"]]
+             "# commands:", *_stats_commands(config)]
     if bench_err:
         stage_lines = [line.strip() for line in open(bench_err) if line.startswith("[bench]")]
         if stage_lines:
@@ -359,12 +374,14 @@ def main() -> int:
                         help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) into OUT and exit")
     parser.add_argument("--sq-summary", nargs=2, metavar=("COUNTER_CSV", "OUT"),
                         help="summarise one rocprofv3 --pmc run of SQ counters into OUT and exit")
+    parser.add_argument("--profile-config", type=int, default=2, choices=(1, 2, 3, 4),
+                        help="configuration a --stats-summary run profiled (for its header)")
     parser.add_argument("--stats-summary", nargs="+", metavar="PATH",
                         help="KERNEL_STATS_CSV OUT [BENCH_ERR]: summarise one rocprofv3 --kernel-trace --stats "
                              "run into OUT and exit")
     args = parser.parse_args()
     if args.stats_summary:
-        summarize_stats(*args.stats_summary)
+        summarize_stats(*args.stats_summary, config=args.profile_config)
         return 0
     if args.sq_summary:
         summarize_sq(*args.sq_summary)
