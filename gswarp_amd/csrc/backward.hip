@@ -34,8 +34,6 @@ namespace gs {
 constexpr int kGradFloats = 10;  // dx, dy, conic a, b, c, opacity, r, g, b, depth
 constexpr float kSureMargin = 2.0e-3f;  // exponents this far above the cutoff always blend
 constexpr float kLog2e = 1.44269504088896341f;
-// Comparison predicates of the lane-mask compare builtins (LLVM's codes).
-constexpr int kCmpOGE = 3, kCmpOLE = 5, kCmpSLT = 40;
 constexpr int64_t kLongTileFactor = 4;  // long tile: list longer than this many times the mean
 
 template <int kCtrl, int kRowMask>

@@ -56,6 +56,10 @@ constexpr float kAlphaMin = 1.0f / 255.0f;
 constexpr float kTransmittanceMin = 0.0001f;
 constexpr float kAlphaMax = 0.99f;
 
+// Comparison predicates of the lane-mask compare builtins
+// (__builtin_amdgcn_fcmpf / sicmp; LLVM's predicate codes).
+constexpr int kCmpOGE = 3, kCmpOLT = 4, kCmpOLE = 5, kCmpSLT = 40;
+
 constexpr int kCoverageSnugbox = 0;
 constexpr int kCoverageAccutile = 1;
 constexpr int kCoverageConicRect = 2;

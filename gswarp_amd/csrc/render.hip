@@ -98,17 +98,19 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
   const int n = rg.y - rg.x;
   const bool aux = kFlow && p.write_aux != 0;
 
-  // T > 0: transmittance of a live pixel; T < 0: -T of a finished pixel
-  // (transmittance never drops below 1e-4 while live); pixels outside the
-  // image start finished.
+  // live_lanes[k]: the wave's lanes whose pixel k is still blending, kept as
+  // a lane mask in scalar registers (pixels outside the image start
+  // finished); T is the pixel's transmittance, finished or not.
   float T[kPixPerLane], c0[kPixPerLane], c1[kPixPerLane], c2[kPixPerLane], ws[kPixPerLane], da[kPixPerLane];
   float pfy[kPixPerLane];
   int last[kPixPerLane], nsucc[kPixPerLane];
+  uint64_t live_lanes[kPixPerLane];
 #pragma unroll
   for (int k = 0; k < kPixPerLane; ++k) {
     const int py = py0 + 4 * k;
     pfy[k] = (float)py;
-    T[k] = (px < p.W && py < p.H) ? 1.0f : -1.0f;
+    T[k] = 1.0f;
+    live_lanes[k] = __ballot(px < p.W && py < p.H);
     c0[k] = c1[k] = c2[k] = ws[k] = da[k] = 0.0f;
     last[k] = 0;
     nsucc[k] = 0;
@@ -116,10 +118,10 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
 
   Batch next = load_batch(p, rg.x, imin(64, n), lane);
   for (int base = 0; base < n; base += 64) {
-    bool live = false;
+    uint64_t live = 0;
 #pragma unroll
-    for (int k = 0; k < kPixPerLane; ++k) live = live || T[k] > 0.0f;
-    if (__ballot(live) == 0) break;
+    for (int k = 0; k < kPixPerLane; ++k) live |= live_lanes[k];
+    if (live == 0) break;
     const int cnt = imin(64, n - base);
     // One wave per workgroup: LDS writes and the broadcast reads below are
     // ordered by the wave's own in-order LDS queue, no barrier needed.
@@ -138,24 +140,32 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
       const float adxx = a.z * dx * dx;
       const float b2dx = (a.w * dx) * 2.0f;
       float q[kPixPerLane], dy[kPixPerLane];
-      bool cand[kPixPerLane];
-      bool any = false;
+      uint64_t cand_lanes[kPixPerLane];  // live && 0 <= q <= qcut, as lane masks
+      uint64_t any = 0;
 #pragma unroll
       for (int k = 0; k < kPixPerLane; ++k) {
         dy[k] = a.y - pfy[k];
         q[k] = conic_q_px(adxx, b2dx, b.x, dy[k]);  // exponent = -0.5 q
-        cand[k] = T[k] > 0.0f && q[k] >= 0.0f && q[k] <= b.w;
-        any |= cand[k];
+        cand_lanes[k] = live_lanes[k] & __builtin_amdgcn_fcmpf(q[k], 0.0f, kCmpOGE) &
+                        __builtin_amdgcn_fcmpf(q[k], b.w, kCmpOLE);
+        any |= cand_lanes[k];
       }
-      if (__ballot(any) == 0) continue;
+      if (any == 0) continue;
       const float4 f = s_rec[3 * j + 2];
 #pragma unroll
       for (int k = 0; k < kPixPerLane; ++k) {
-        const float alpha = fminr(kAlphaMax, b.y * exp_sw_nonpos(cand[k] ? -0.5f * q[k] : 0.0f));
-        const bool ok = cand[k] && alpha >= kAlphaMin;
+        // Every lane evaluates the exponential; the result only counts for
+        // candidate lanes (0 <= q), where the argument is non-positive.  For
+        // the others it may be anything, including inf or NaN, and every
+        // decision below masks it out.  o * exp <= o <= 1, so the minimum
+        // needs no NaN rule of its own.
+        const float alpha = fminf(kAlphaMax, b.y * exp_sw_nonpos(-0.5f * q[k]));
+        // The blend decisions as lane masks: scalar ANDs of the comparisons.
+        const uint64_t ok_lanes = cand_lanes[k] & __builtin_amdgcn_fcmpf(alpha, kAlphaMin, kCmpOGE);
         const float test_T = T[k] * (1.0f - alpha);
-        const bool fin = ok && test_T < kTransmittanceMin;
-        const bool blend = ok && !fin;
+        const uint64_t fin_lanes = ok_lanes & __builtin_amdgcn_fcmpf(test_T, kTransmittanceMin, kCmpOLT);
+        live_lanes[k] &= ~fin_lanes;
+        const bool blend = __builtin_amdgcn_inverse_ballot_w64(ok_lanes & ~fin_lanes);
         // A pixel that does not blend adds a contribution of exactly +0 (the
         // sums are unchanged bit for bit), which replaces per-output selects.
         const float contribution = blend ? alpha * T[k] : 0.0f;
@@ -173,8 +183,7 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
           p.x_mu[(size_t)p.top_k * P + ai] = dy[k];
         }
         if (kFlow) nsucc[k] += blend ? 1 : 0;
-        const float Tb = blend ? test_T : T[k];
-        T[k] = fin ? -T[k] : Tb;
+        T[k] = blend ? test_T : T[k];
         last[k] = blend ? base + j + 1 : last[k];
       }
     }
@@ -186,7 +195,7 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
     const bool in_image = px < p.W && py < p.H;
     const int pix = py * p.W + px;
     if (in_image) {
-      const float Tk = fabsf(T[k]);
+      const float Tk = T[k];
       p.n_contrib[pix] = last[k];
       p.out_color[pix] = c0[k] + Tk * p.bg[0];
       p.out_color[P + pix] = c1[k] + Tk * p.bg[1];
