@@ -300,9 +300,13 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
       if (band != 0) {
 #pragma unroll
         for (int k = 0; k < kPix; ++k) {
-          const bool in_band = cand[k] && !(q[k] <= qsure);
-          const float a_sw = fminr(kAlphaMax, b.y * exp_sw_nonpos(in_band ? -0.5f * q[k] : 0.0f));
-          e[k] = (in_band && a_sw >= kAlphaMin) ? q[k] * (-0.5f * kLog2e) : e[k];
+          // in the band 0 <= q, so the exponential's argument is non-positive;
+          // on other lanes its value (inf or NaN included) is masked out
+          const uint64_t band_lanes = cand_lanes[k] & ~__builtin_amdgcn_fcmpf(q[k], qsure, kCmpOLE);
+          const float a_sw = fminf(kAlphaMax, b.y * exp_sw_nonpos(-0.5f * q[k]));
+          const bool blends = __builtin_amdgcn_inverse_ballot_w64(
+              band_lanes & __builtin_amdgcn_fcmpf(a_sw, kAlphaMin, kCmpOGE));
+          e[k] = blends ? q[k] * (-0.5f * kLog2e) : e[k];
         }
       }
       const float4 f = s_rec[3 * jj + 2];
