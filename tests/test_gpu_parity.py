@@ -224,3 +224,22 @@ def test_mip_filter_with_precomputed_covariance_matches_oracle(device):
 @pytest.mark.parametrize("case", ["c1_full", "c2_small"])
 def test_mip_filter_backward_matches_oracle(case, device):
     _check_backward(dict(_scene(case, device), filter_variance=0.3))
+
+
+def test_stacked_opaque_gaussians_terminate_like_oracle(device):
+    """Eight wide, opaque Gaussians stacked on the view axis: alpha is capped
+    at 0.99, so a pixel where two or more reach the cap has T <= 1e-4 and
+    stops at the next one it would blend (the oracle stops about 300 of the
+    7680 pixels before the eighth).  The stop decisions, n_contrib and the
+    colours match the oracle bit for bit."""
+    k = 8
+    scene = configs.make_scene(1, count=k, width=96, height=80, device=device)
+    z = torch.arange(k, dtype=torch.float32, device=device) * 0.05
+    scene["means3D"] = torch.stack([torch.zeros_like(z), torch.zeros_like(z), z], dim=1).contiguous()
+    scene["scales"] = torch.full((k, 3), 0.8, device=device)
+    scene["opacities"] = torch.full((k, 1), 0.999, device=device)
+    out, _host, ref = _check_forward(scene, options())
+    n_contrib = ref["fwd"]["n_contrib"].reshape(-1)
+    alpha = ref["fwd"]["alpha"].reshape(-1)
+    stopped = (n_contrib > 0) & (n_contrib < k) & (alpha > 0.9998)
+    assert stopped.sum() > 100, int(stopped.sum())
