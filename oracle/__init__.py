@@ -51,6 +51,7 @@ def build(verbose: bool = False) -> Path:
 
 
 _F = ctypes.POINTER(ctypes.c_float)
+_D = ctypes.POINTER(ctypes.c_double)
 _I = ctypes.POINTER(ctypes.c_int)
 _c_int = ctypes.c_int
 _c_float = ctypes.c_float
@@ -75,7 +76,7 @@ _SIGNATURES = {
     ),
     "or_render_bwd": (
         None,
-        [_c_int, _c_int, _c_int, _I, _I, _F, _F, _F, _F, _F, _F, _I, _F, _F, _F, _c_int, _F],
+        [_c_int, _c_int, _c_int, _I, _I, _F, _F, _F, _F, _F, _F, _I, _F, _F, _F, _c_int, _c_int, _F, _D, _D, _D],
     ),
     "or_preprocess_bwd": (
         None,
@@ -116,6 +117,10 @@ def _fp(a: np.ndarray | None):
 
 def _ip(a: np.ndarray | None):
     return None if a is None else a.ctypes.data_as(_I)
+
+
+def _dp(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data_as(_D)
 
 
 def exp(x: float) -> float:
@@ -259,18 +264,33 @@ def render_fwd(pre: dict, bins: dict, features, background, width, height, *, co
 
 
 def render_bwd(pre: dict, bins: dict, features, background, width, height, fwd: dict, grad_color, grad_depth,
-               grad_alpha, *, compute_depth=True) -> np.ndarray:
-    """Per-Gaussian (N, 10) render gradients: dx, dy, conic a, b, c, opacity, rgb, depth."""
+               grad_alpha, *, compute_depth=True, bound=False, value_mode=0):
+    """Per-Gaussian (N, 10) render gradients: dx, dy, conic a, b, c, opacity, rgb, depth.
+
+    With bound=True also returns (err, mag), two (N, 10) float64 arrays: the
+    summed first-order bound on the fp32 rounding of each column's per-pixel
+    terms under any evaluation order, and the summed term magnitudes (every
+    sum in absolute values), which scale the rounding of summing the terms.
+    value_mode 1 (double values from the fp32 inputs) and 2 (a second fp32
+    evaluation order) return the float64 sums instead of float32; they exist
+    to check that bound.
+    """
     features = _f32(features).reshape(-1, 3)
     N = features.shape[0]
     out = np.zeros((N, 10), np.float32)
+    out64 = np.zeros((N, 10), np.float64) if value_mode else None
+    err = np.zeros((N, 10), np.float64) if bound else None
+    mag = np.zeros((N, 10), np.float64) if bound else None
     point_list = _i32(bins["point_list"]) if bins["num_rendered"] > 0 else np.zeros(1, np.int32)
     lib().or_render_bwd(width, height, N, _ip(_i32(bins["ranges"])), _ip(point_list), _fp(_f32(pre["proj_2d"])),
                         _fp(features), _fp(_f32(pre["depths"])), _fp(_f32(pre["conic_opacity"])),
                         _fp(_f32(background).reshape(3)), _fp(_f32(fwd["alpha"])), _ip(_i32(fwd["n_contrib"])),
                         _fp(_f32(grad_color)), _fp(_f32(grad_depth)), _fp(_f32(grad_alpha)),
-                        int(bool(compute_depth)), _fp(out))
-    return out
+                        int(bool(compute_depth)), int(value_mode), _fp(out), _dp(out64), _dp(err), _dp(mag))
+    res = out64 if value_mode else out
+    if bound:
+        return res, err, mag
+    return res
 
 
 def preprocess_bwd(pre: dict, grad_gauss, means3d, scales, rotations, view, proj, campos, *, tanfovx, tanfovy,
@@ -330,20 +350,110 @@ def rasterize(scene: dict, *, coverage_mode=1, compute_depth=True, top_k=0) -> d
     return {"pre": pre, "bins": bins, "fwd": fwd}
 
 
+# Unit roundoff of binary32.
+U32 = 2.0 ** -24
+# Partial sums per (tile, Gaussian) and gradient component that an fp32
+# implementation may add up in an arbitrary order (one per pixel slice of a
+# tile that visits the Gaussian; four 16x4 slices at most).
+PARTIALS_PER_TILE = 4
+# Depth of the summation tree inside one partial sum (pixels of a lane, lane
+# folds, a quad of slots and its shuffles).
+TREE_DEPTH = 8
+# Rounding of the per-Gaussian chain itself (SH, projection, cov2D -> cov3D ->
+# scale / rotation), in units of u times the magnitude of its linear output.
+CHAIN_DEPTH = 64
+
+_OUTPUT_KEYS = ("means3D", "means2D", "scales", "rotations", "cov3D", "sh")
+
+
+def _backward_chain(scene, pre, gg, grad_proj_2d=None, grad_conic_2d=None, grad_conic_2d_inv=None,
+                    flow_double=False) -> dict:
+    s = scene
+    return preprocess_bwd(pre, gg, s["means3D"], s.get("scales"), s.get("rotations"), s["viewmatrix"],
+                          s["projmatrix"], s["campos"], tanfovx=s["tanfovx"], tanfovy=s["tanfovy"],
+                          width=s["width"], height=s["height"], scale_modifier=s.get("scale_modifier", 1.0),
+                          shs=s.get("shs"), degree=s.get("sh_degree", 0), grad_proj_2d=grad_proj_2d,
+                          grad_conic_2d=grad_conic_2d, grad_conic_2d_inv=grad_conic_2d_inv,
+                          flow_double=flow_double, cov3d_precomp=s.get("cov3D_precomp"),
+                          filter_variance=s.get("filter_variance", 0.0))
+
+
+def gradient_bound(scene: dict, result: dict, gg, err, mag, *, grad_proj_2d=None, grad_conic_2d=None,
+                   grad_conic_2d_inv=None, flow_double=False) -> dict:
+    """Per-element bound on |fp32 implementation - oracle| for every output gradient.
+
+    The render stage's bound per Gaussian and column is
+        B = 2 err + (TREE_DEPTH + PARTIALS_PER_TILE tiles_touched) u mag
+    (each side errs by at most err in its terms; the summation of the terms,
+    in any order over that many partial sums, by the second part).  The
+    per-Gaussian backward is linear in the render gradients, so B reaches
+    each output through the absolute value of its Jacobian: column k's
+    Jacobian is the backward of a unit render gradient in column k alone
+    (Gaussians are independent, so one run gives it for all of them), and
+    the bound is  sum_k |J_k| B_k + CHAIN_DEPTH u (M + max M over the Gaussian's
+    components of the same output), M = sum_k |J_k g_k| + |J_meta g_meta|: the
+    rounding of the chain itself, whose intermediate values are on the scale
+    of the Gaussian's largest output component.  Returns a dict of
+    float64 arrays keyed like the gradients (plus "grad_gauss").
+    """
+    pre = result["pre"]
+    tt = np.asarray(pre["tiles_touched"], np.float64)[:, None]
+    B = 2.0 * err + (TREE_DEPTH + PARTIALS_PER_TILE * tt) * U32 * mag
+    N = gg.shape[0]
+    out = {"grad_gauss": B, "opacities": B[:, 5:6].copy(), "colors": B[:, 6:9].copy()}
+    acc_b = {}
+    acc_m = {}
+    zeros_meta = dict(grad_proj_2d=np.zeros((N, 2), np.float32), grad_conic_2d=np.zeros((N, 3), np.float32),
+                      grad_conic_2d_inv=np.zeros((N, 3), np.float32))
+    for k in range(10):
+        if not np.any(B[:, k]) and not np.any(gg[:, k]):
+            continue
+        for src, acc in ((B[:, k], acc_b), (gg[:, k], acc_m)):
+            unit = np.zeros((N, 10), np.float32)
+            unit[:, k] = src
+            part = _backward_chain(scene, pre, unit, flow_double=flow_double, **zeros_meta)
+            for key in _OUTPUT_KEYS:
+                acc[key] = acc.get(key, 0.0) + np.abs(part[key].astype(np.float64))
+    meta = {"grad_proj_2d": grad_proj_2d, "grad_conic_2d": grad_conic_2d, "grad_conic_2d_inv": grad_conic_2d_inv}
+    for name, value in meta.items():
+        if value is None or not np.any(value):
+            continue
+        args = dict(zeros_meta)
+        args[name] = np.ascontiguousarray(value, np.float32)
+        part = _backward_chain(scene, pre, np.zeros((N, 10), np.float32), flow_double=flow_double, **args)
+        for key in _OUTPUT_KEYS:
+            acc_m[key] = acc_m.get(key, 0.0) + np.abs(part[key].astype(np.float64))
+    for key in _OUTPUT_KEYS:
+        m = acc_m.get(key, 0.0)
+        if np.ndim(m):
+            # intermediate values of one Gaussian's chain (dL/dcov3D, dL/dM, ...) are on the scale of its
+            # largest output component, so a component that cancels to near zero still errs by that much
+            m = m + m.reshape(m.shape[0], -1).max(axis=1, initial=0.0).reshape((-1,) + (1,) * (m.ndim - 1))
+        b = acc_b.get(key, 0.0) + CHAIN_DEPTH * U32 * m
+        out[key] = np.asarray(b, np.float64)  # a scalar 0 where no column reaches this output
+    return out
+
+
 def rasterize_backward(scene: dict, result: dict, grad_color, grad_depth, grad_alpha, *, compute_depth=True,
-                       grad_proj_2d=None, grad_conic_2d=None, grad_conic_2d_inv=None, flow_double=False) -> dict:
-    """Full backward matching the reference's gradient tuple (as a dict)."""
+                       grad_proj_2d=None, grad_conic_2d=None, grad_conic_2d_inv=None, flow_double=False,
+                       with_bound=False) -> dict:
+    """Full backward matching the reference's gradient tuple (as a dict).
+
+    with_bound=True adds grads["bound"]: gradient_bound() of every output.
+    """
     s = scene
     pre, bins, fwd = result["pre"], result["bins"], result["fwd"]
-    gg = render_bwd(pre, bins, pre["rgb"], s["bg"], s["width"], s["height"], fwd, grad_color,
+    rb = render_bwd(pre, bins, pre["rgb"], s["bg"], s["width"], s["height"], fwd, grad_color,
                     grad_depth if grad_depth is not None else np.zeros_like(fwd["depth"]), grad_alpha,
-                    compute_depth=compute_depth)
-    grads = preprocess_bwd(pre, gg, s["means3D"], s.get("scales"), s.get("rotations"), s["viewmatrix"],
-                           s["projmatrix"],
-                           s["campos"], tanfovx=s["tanfovx"], tanfovy=s["tanfovy"], width=s["width"],
-                           height=s["height"], scale_modifier=s.get("scale_modifier", 1.0), shs=s.get("shs"),
-                           degree=s.get("sh_degree", 0), grad_proj_2d=grad_proj_2d, grad_conic_2d=grad_conic_2d,
-                           grad_conic_2d_inv=grad_conic_2d_inv, flow_double=flow_double,
-                           cov3d_precomp=s.get("cov3D_precomp"), filter_variance=s.get("filter_variance", 0.0))
+                    compute_depth=compute_depth, bound=with_bound)
+    gg = rb[0] if with_bound else rb
+    grads = _backward_chain(s, pre, gg, grad_proj_2d=grad_proj_2d, grad_conic_2d=grad_conic_2d,
+                            grad_conic_2d_inv=grad_conic_2d_inv, flow_double=flow_double)
     grads["grad_gauss"] = gg
+    if with_bound:
+        bound = gradient_bound(s, result, gg, rb[1], rb[2], grad_proj_2d=grad_proj_2d,
+                               grad_conic_2d=grad_conic_2d, grad_conic_2d_inv=grad_conic_2d_inv,
+                               flow_double=flow_double)
+        grads["bound"] = {k: np.broadcast_to(v, grads[k].shape).copy() if k in grads else v
+                          for k, v in bound.items()}
     return grads

@@ -789,27 +789,70 @@ void or_render_fwd(int W, int H, const int* ranges, const int* point_list, const
  * accumulating in double.  grad_out (P_gauss, 10): dx, dy, conic a, b, c,
  * opacity, r, g, b, depth (the reference's grad_points_xy, grad_conic_opacity,
  * grad_feature and grad_depths, backward_ops.py:200-208).
+ *
+ * Error bound (err_out, mag_out; both (P_gauss, 10) doubles, or NULL).  The
+ * per-pixel terms above are fp32 expressions, and an fp32 implementation may
+ * evaluate them in another algebraically equal order (a running dot product
+ * S = U . acc in place of the per-channel recurrences; pixel moments summed
+ * first and multiplied by the conic, opacity and W/2, H/2 once), with exp and
+ * 1/x a few ulp off.  Alongside each term this routine carries a first-order
+ * running bound (Wilkinson's running error analysis) on |computed - exact|
+ * valid for any such evaluation, where "exact" is real arithmetic on the same
+ * fp32 inputs (q, the conic, opacity, colours, depths, T_final = 1 - alpha and
+ * the upstream gradients).  With u = 2^-24, per blended (pixel, Gaussian):
+ *   G:      rel_G  = (0.75 q + 3) u   (exp(-q/2) by exp2 of a rounded product,
+ *                                      <= 2 ulp of the exponential itself);
+ *   alpha:  rel_a  = rel_G + u, 0 where both sides hit the 0.99 cap;
+ *   1-alpha:rel_om = alpha rel_a / (1 - alpha) + u;
+ *   T:      rel_T += rel_om + 2u per step back (a reciprocal and a product);
+ *   S:      e_S  <- (1-alpha) e_S + alpha e_fu + alpha rel_a (M_fu + m_S) + 4u (M_fu + m_S),
+ *           with M_fu = sum |F_ch U_ch| (colour, depth, alpha), e_fu = 5u M_fu,
+ *           m_S <- (1-alpha) m_S + alpha M_fu its magnitude (m_S >= |S|),
+ *           started at e_S = 3u m_S, m_S = sum |bg_ch U_ch|;
+ *   v = G T (F.U - S):  e_v = G T (e_fu + e_S + u (M_fu + m_S)) + |v| (rel_G + rel_T + 2u).
+ * Each column's term is a product of v (or alpha T) with exact per-Gaussian
+ * and per-pixel factors; err_out sums  |factor| e_v + 4u |factor v|  (colour
+ * and depth: |alpha T U| (rel_a + rel_T + 2u)), and mag_out sums the
+ * term magnitudes with every sum written out in absolute values (column 0:
+ * W/2 o |v| (|a dx| + |b dy|)), which bounds the rounding of any summation
+ * order: a sum of m partial sums of these terms errs by at most
+ * (depth of the summation tree) u mag_out.
+ *
+ * value_mode selects how the term values are computed (the blend decisions
+ * are always the fp32 ones above): 0 the reference's fp32 expressions; 1 the
+ * same expressions in double from the fp32 inputs ("exact" for the bound);
+ * 2 a second fp32 order, the one a wave-parallel kernel uses (exp2 of a
+ * rounded product, 1 - alpha inverted by a reciprocal, S = U . acc with fused
+ * multiply-adds, pixel moments times per-Gaussian factors).  grad_out64, if
+ * not NULL, receives the double sums.
  */
 void or_render_bwd(int W, int H, int P_gauss, const int* ranges, const int* point_list, const float* points_xy,
                    const float* features, const float* depths, const float* conic_opacity, const float* bg,
                    const float* out_alpha, const int* n_contrib, const float* grad_color, const float* grad_depth,
-                   const float* grad_alpha, int compute_depth, float* grad_out) {
+                   const float* grad_alpha, int compute_depth, int value_mode, float* grad_out, double* grad_out64,
+                   double* err_out, double* mag_out) {
   const int grid_x = (W + BLOCK_X - 1) / BLOCK_X;
   const long long total = (long long)W * H;
   const float ddelx_dx = 0.5f * (float)W;
   const float ddely_dy = 0.5f * (float)H;
+  const int bound = err_out != NULL && mag_out != NULL;
+  const double u = ldexp(1.0, -24);
   int nthreads = 1;
 #ifdef _OPENMP
   nthreads = omp_get_max_threads();
 #endif
-  double* acc = (double*)calloc((size_t)nthreads * (size_t)P_gauss * 10, sizeof(double));
+  const size_t per_thread = (size_t)P_gauss * 10;
+  const int nbuf = bound ? 3 : 1;
+  double* acc = (double*)calloc((size_t)nthreads * per_thread * (size_t)nbuf, sizeof(double));
 #pragma omp parallel
   {
     int tid = 0;
 #ifdef _OPENMP
     tid = omp_get_thread_num();
 #endif
-    double* my = acc + (size_t)tid * (size_t)P_gauss * 10;
+    double* my = acc + (size_t)tid * per_thread * (size_t)nbuf;
+    double* my_err = bound ? my + per_thread : NULL;
+    double* my_mag = bound ? my + 2 * per_thread : NULL;
 #pragma omp for schedule(dynamic, 64)
     for (long long pixel_id = 0; pixel_id < total; ++pixel_id) {
       const int pix_x = (int)(pixel_id % W), pix_y = (int)(pixel_id / W);
@@ -826,6 +869,13 @@ void or_render_bwd(int W, int H, int P_gauss, const int* ranges, const int* poin
       const float bg_dot = bg[0] * g0 + bg[1] * g1 + bg[2] * g2;
       float ar0 = 0.0f, ar1 = 0.0f, ar2 = 0.0f, adr = 0.0f, aar = 0.0f;
       float last_alpha = 0.0f, lc0 = 0.0f, lc1 = 0.0f, lc2 = 0.0f, last_depth = 0.0f;
+      /* running bound state: relative error of T, error and magnitude of S */
+      double rel_T = 0.0;
+      double m_S = fabs((double)bg[0] * g0) + fabs((double)bg[1] * g1) + fabs((double)bg[2] * g2);
+      double e_S = 3.0 * u * m_S;
+      /* value_mode 1 / 2 state: T and S = U . acc (background included) */
+      double xT = T_final, xS = (double)bg[0] * g0 + (double)bg[1] * g1 + (double)bg[2] * g2;
+      float yT = T_final, yS = fmaf(bg[2], g2, fmaf(bg[1], g1, bg[0] * g0));
       for (int pos = last_contributor - 1; pos >= 0; --pos) {
         const int id = point_list[start + pos];
         const float* co = conic_opacity + 4 * id;
@@ -848,38 +898,140 @@ void or_render_bwd(int W, int H, int P_gauss, const int* ranges, const int* poin
         lc2 = f[2];
         float dL_dopa = (f[0] - ar0) * g0 + (f[1] - ar1) * g1 + (f[2] - ar2) * g2;
         double* gg = my + (size_t)id * 10;
-        gg[6] += (double)(dchannel_dcolor * g0);
-        gg[7] += (double)(dchannel_dcolor * g1);
-        gg[8] += (double)(dchannel_dcolor * g2);
         if (compute_depth) {
           const float dv = depths[id];
           adr = last_alpha * last_depth + (1.0f - last_alpha) * adr;
           last_depth = dv;
           dL_dopa = dL_dopa + (dv - adr) * gd;
-          gg[9] += (double)(dchannel_dcolor * gd);
         }
         aar = last_alpha + (1.0f - last_alpha) * aar;
         dL_dopa = dL_dopa + (1.0f - aar) * ga;
         dL_dopa = dL_dopa * T;
         last_alpha = alpha;
         dL_dopa = dL_dopa + (-T_final / one_minus_alpha) * bg_dot;
-        const float dL_dG = co[3] * dL_dopa;
-        const float gdx = G * d_x, gdy = G * d_y;
-        const float dG_ddelx = -gdx * co[0] - gdy * co[1];
-        const float dG_ddely = -gdy * co[2] - gdx * co[1];
-        gg[0] += (double)(dL_dG * dG_ddelx * ddelx_dx);
-        gg[1] += (double)(dL_dG * dG_ddely * ddely_dy);
-        gg[2] += (double)(-0.5f * gdx * d_x * dL_dG);
-        gg[3] += (double)(-0.5f * gdx * d_y * dL_dG);
-        gg[4] += (double)(-0.5f * gdy * d_y * dL_dG);
-        gg[5] += (double)(G * dL_dopa);
+        if (value_mode == 0) {
+          gg[6] += (double)(dchannel_dcolor * g0);
+          gg[7] += (double)(dchannel_dcolor * g1);
+          gg[8] += (double)(dchannel_dcolor * g2);
+          if (compute_depth) gg[9] += (double)(dchannel_dcolor * gd);
+          const float dL_dG = co[3] * dL_dopa;
+          const float gdx = G * d_x, gdy = G * d_y;
+          const float dG_ddelx = -gdx * co[0] - gdy * co[1];
+          const float dG_ddely = -gdy * co[2] - gdx * co[1];
+          gg[0] += (double)(dL_dG * dG_ddelx * ddelx_dx);
+          gg[1] += (double)(dL_dG * dG_ddely * ddely_dy);
+          gg[2] += (double)(-0.5f * gdx * d_x * dL_dG);
+          gg[3] += (double)(-0.5f * gdx * d_y * dL_dG);
+          gg[4] += (double)(-0.5f * gdy * d_y * dL_dG);
+          gg[5] += (double)(G * dL_dopa);
+        } else if (value_mode == 1) {
+          /* the same quantities in double: G, alpha, T and the reverse
+           * recurrences from the fp32 inputs */
+          const double Gd = exp((double)power);
+          const double ad = fmin(0.99, (double)co[3] * Gd);
+          const double omd = fmax(1.0 - ad, (double)ONE_MINUS_ALPHA_MIN);
+          xT = xT / omd;
+          const double U[5] = {g0, g1, g2, gd, ga};
+          const double F[5] = {f[0], f[1], f[2], compute_depth ? depths[id] : 0.0, 1.0};
+          double fu = 0.0;
+          for (int c = 0; c < 5; ++c) fu += F[c] * U[c];
+          const double dopa = xT * (fu - xS);
+          const double v = Gd * dopa;
+          const double dxd = d_x, dyd = d_y;
+          gg[0] += -(double)ddelx_dx * co[3] * v * (co[0] * dxd + co[1] * dyd);
+          gg[1] += -(double)ddely_dy * co[3] * v * (co[2] * dyd + co[1] * dxd);
+          gg[2] += -0.5 * co[3] * v * dxd * dxd;
+          gg[3] += -0.5 * co[3] * v * dxd * dyd;
+          gg[4] += -0.5 * co[3] * v * dyd * dyd;
+          gg[5] += v;
+          for (int c = 0; c < (compute_depth ? 4 : 3); ++c) gg[6 + c] += ad * xT * U[c];
+          xS = xS + ad * (fu - xS);
+        } else {
+          /* a second fp32 order */
+          const float Gf = exp2f(-2.0f * power * (-0.5f * 1.44269504088896341f));
+          const float af = fmin_(0.99f, co[3] * Gf);
+          const float omf = 1.0f - af;
+          yT = yT * (1.0f / omf);
+          float fu = fmaf(f[2], g2, fmaf(f[1], g1, fmaf(f[0], g0, ga)));
+          if (compute_depth) fu = fmaf(depths[id], gd, fu);
+          const float dd = fu - yS;
+          const float v = Gf * (yT * dd);
+          const float vdx = v * d_x, vdy = v * d_y;
+          const float o = co[3];
+          gg[0] += (double)(-ddelx_dx * o * (co[0] * vdx + co[1] * vdy));
+          gg[1] += (double)(-ddely_dy * o * (co[2] * vdy + co[1] * vdx));
+          gg[2] += (double)(-0.5f * o * (vdx * d_x));
+          gg[3] += (double)(-0.5f * o * (vdx * d_y));
+          gg[4] += (double)(-0.5f * o * fmaf(vdy, d_y, 0.0f));
+          gg[5] += (double)v;
+          const float dch = af * yT;
+          gg[6] += (double)(dch * g0);
+          gg[7] += (double)(dch * g1);
+          gg[8] += (double)(dch * g2);
+          if (compute_depth) gg[9] += (double)(dch * gd);
+          yS = fmaf(af, dd, yS);
+        }
+        if (bound) {
+          const double q = -2.0 * (double)power;
+          const double a = alpha, o = co[3];
+          const double rel_G = (0.75 * q + 3.0) * u;
+          /* both evaluations are capped when o G clears 0.99 by more than their error */
+          const int capped = (double)co[3] * (double)G > 0.99 * (1.0 + 2.0 * rel_G + 2.0 * u);
+          const double rel_a = capped ? 0.0 : rel_G + u;
+          const double rel_om = a * rel_a / (1.0 - a) + u;
+          rel_T += rel_om + 2.0 * u;
+          const double Tn = T;
+          double M_fu = fabs((double)f[0] * g0) + fabs((double)f[1] * g1) + fabs((double)f[2] * g2) + fabs((double)ga);
+          if (compute_depth) M_fu += fabs((double)depths[id] * gd);
+          const double e_fu = 5.0 * u * M_fu;
+          const double v = (double)G * (double)dL_dopa;
+          const double e_v = (double)G * Tn * (e_fu + e_S + u * (M_fu + m_S)) + fabs(v) * (rel_G + rel_T + 2.0 * u);
+          const double av = fabs(v);
+          const double adx = fabs((double)d_x), ady = fabs((double)d_y);
+          const double fac[6] = {
+              (double)ddelx_dx * o * (fabs((double)co[0]) * adx + fabs((double)co[1]) * ady),
+              (double)ddely_dy * o * (fabs((double)co[2]) * ady + fabs((double)co[1]) * adx),
+              0.5 * o * adx * adx,
+              0.5 * o * adx * ady,
+              0.5 * o * ady * ady,
+              1.0,
+          };
+          double* ge = my_err + (size_t)id * 10;
+          double* gm = my_mag + (size_t)id * 10;
+          for (int k = 0; k < 6; ++k) {
+            ge[k] += fac[k] * e_v + 4.0 * u * fac[k] * av;
+            gm[k] += fac[k] * av;
+          }
+          const double rel_c = rel_a + rel_T + 2.0 * u;
+          const double up[4] = {g0, g1, g2, gd};
+          for (int k = 0; k < (compute_depth ? 4 : 3); ++k) {
+            const double t = fabs(a * Tn * up[k]);
+            ge[6 + k] += t * rel_c;
+            gm[6 + k] += t;
+          }
+          /* this Gaussian joins what lies behind the next one */
+          e_S = (1.0 - a) * e_S + a * e_fu + a * rel_a * (M_fu + m_S) + 4.0 * u * (M_fu + m_S);
+          m_S = (1.0 - a) * m_S + a * M_fu;
+        }
       }
     }
   }
-  for (long long i = 0; i < (long long)P_gauss * 10; ++i) {
-    double s = 0.0;
-    for (int t = 0; t < nthreads; ++t) s += acc[(size_t)t * (size_t)P_gauss * 10 + (size_t)i];
+  for (long long i = 0; i < (long long)per_thread; ++i) {
+    double s = 0.0, se = 0.0, sm = 0.0;
+    for (int t = 0; t < nthreads; ++t) {
+      const double* base = acc + (size_t)t * per_thread * (size_t)nbuf;
+      s += base[i];
+      if (bound) {
+        se += base[per_thread + (size_t)i];
+        sm += base[2 * per_thread + (size_t)i];
+      }
+    }
     grad_out[i] = (float)s;
+    if (grad_out64) grad_out64[i] = s;
+    if (bound) {
+      err_out[i] = se;
+      mag_out[i] = sm;
+    }
   }
   free(acc);
 }

@@ -85,20 +85,45 @@ def oracle_forward(scene: dict, *, coverage_mode: int = 1, compute_depth: bool =
     return host, oracle.rasterize(host, coverage_mode=coverage_mode, compute_depth=compute_depth, top_k=top_k)
 
 
-def grad_mismatch(actual: np.ndarray, expected: np.ndarray, rtol: float = 1e-3, atol: float = 1e-5,
-                  scale_atol: float = 1e-4) -> tuple[int, float]:
-    """Count of elements outside |a-e| <= rtol*|e| + max(atol, scale_atol*max|e|), and the worst ratio.
+# Safety factor on the oracle's per-element rounding bound (oracle.gradient_bound):
+# it covers the second-order terms the first-order analysis drops.  On the
+# CPU the oracle and a second fp32 evaluation order stay within 0.4 of the
+# one-sided bound (tests/test_oracle_bound.py).
+BOUND_FACTOR = 2.0
 
-    Gradients are sums of per-pixel terms accumulated with float atomics in
-    unspecified order on the GPU and in double on the CPU; where terms cancel
-    the absolute error scales with the tensor's magnitude, hence the
-    scale-relative floor.
+
+def grad_mismatch(actual: np.ndarray, expected: np.ndarray, bound=0.0, rtol: float = 1e-3, atol: float = 1e-5,
+                  factor: float = BOUND_FACTOR) -> tuple[int, float, int, float]:
+    """Per-element gradient check.
+
+    An element passes when |a - e| <= rtol |e| + atol + factor * bound, where
+    bound (broadcast to e's shape) is the oracle's bound on the fp32 rounding
+    of that element's sum of per-pixel terms, carried through the
+    per-Gaussian backward (oracle.gradient_bound): where those terms cancel,
+    the rounding of any fp32 evaluation exceeds the 1e-3 / 1e-5 bar, and the
+    bound says by how much for this element alone.
+
+    Returns (failures, worst ratio |a-e| / tolerance, elements outside the
+    plain rtol/atol bar, worst ratio against that bar).
     """
     actual = np.asarray(actual, dtype=np.float64)
     expected = np.asarray(expected, dtype=np.float64)
-    floor = max(atol, scale_atol * float(np.abs(expected).max(initial=0.0)))
-    tol = rtol * np.abs(expected) + floor
+    bound = np.broadcast_to(np.asarray(bound, dtype=np.float64), expected.shape)
     diff = np.abs(actual - expected)
-    bad = diff > tol
-    worst = float((diff / tol).max(initial=0.0))
-    return int(bad.sum()), worst
+    strict = rtol * np.abs(expected) + atol
+    tol = strict + factor * bound
+    bad = int((diff > tol).sum())
+    n_strict = int((diff > strict).sum())
+    with np.errstate(divide="ignore", invalid="ignore"):  # 0/0 where both are exactly zero
+        worst = float(np.nan_to_num(diff / tol, posinf=np.inf).max(initial=0.0))
+        worst_strict = float(np.nan_to_num(diff / strict, posinf=np.inf).max(initial=0.0))
+    return bad, worst, n_strict, worst_strict
+
+
+def report_grad(name: str, actual, expected, bound) -> tuple[int, float]:
+    """grad_mismatch with one printed line per tensor; returns (failures, worst ratio)."""
+    bad, worst, n_strict, worst_strict = grad_mismatch(actual, expected, bound)
+    print(f"[grad] {name}: failures={bad} worst={worst:.3f} | outside 1e-3/1e-5 bar: {n_strict} "
+          f"(worst {worst_strict:.2f}) of {np.size(expected)}; max|e|={np.abs(expected).max(initial=0):.3e}",
+          flush=True)
+    return bad, worst

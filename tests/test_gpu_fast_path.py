@@ -19,7 +19,7 @@ import torch
 
 import oracle
 from gswarp_amd import _pipeline, _workspace, configs
-from helpers import grad_mismatch, options, oracle_forward, raster_inputs, to_np
+from helpers import options, oracle_forward, raster_inputs, report_grad, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -137,14 +137,14 @@ def test_fast_path_backward_matches_oracle(case, device):
     zeros2 = np.zeros((scene["means3D"].shape[0], 2), np.float32)
     zeros3 = np.zeros((scene["means3D"].shape[0], 3), np.float32)
     ref_g = oracle.rasterize_backward(host, ref, to_np(up["color"]), to_np(up["depth"]), to_np(up["alpha"]),
-                                      grad_proj_2d=zeros2, grad_conic_2d=zeros3, grad_conic_2d_inv=zeros3)
+                                      grad_proj_2d=zeros2, grad_conic_2d=zeros3, grad_conic_2d_inv=zeros3,
+                                      with_bound=True)
     failures = []
     for name, actual, key in (("means2D", g_means2d, "means2D"), ("opacities", g_opac, "opacities"),
                               ("means3D", g_means3d, "means3D"), ("scales", g_scales, "scales"),
                               ("rotations", g_rot, "rotations"), ("sh", g_sh, "sh")):
         expected = ref_g[key]
-        bad, worst = grad_mismatch(to_np(actual).reshape(expected.shape), expected)
-        print(f"[fast grad] {name}: mismatches={bad} worst_ratio={worst:.3f}", flush=True)
+        bad, worst = report_grad(name, to_np(actual).reshape(expected.shape), expected, ref_g["bound"][key])
         if bad:
             failures.append((name, bad, worst))
     assert not failures, failures

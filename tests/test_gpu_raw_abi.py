@@ -18,7 +18,7 @@ import torch
 
 import oracle
 from gswarp_amd import _pipeline, _rasterizer, _rasterizer_flow, configs
-from helpers import grad_mismatch, oracle_forward, raster_inputs, to_np, with_precomputed_covariance
+from helpers import oracle_forward, raster_inputs, report_grad, to_np, with_precomputed_covariance
 
 pytestmark = pytest.mark.gpu
 
@@ -53,7 +53,8 @@ def _oracle_grads(scene, up, *, colors=False, flow_double=False):
     host, ref = oracle_forward(scene, colors=colors)
     return oracle.rasterize_backward(
         host, ref, to_np(up["color"]), to_np(up["depth"]), to_np(up["alpha"]), grad_proj_2d=to_np(up["proj_2d"]),
-        grad_conic_2d=to_np(up["conic_2d"]), grad_conic_2d_inv=to_np(up["conic_2d_inv"]), flow_double=flow_double)
+        grad_conic_2d=to_np(up["conic_2d"]), grad_conic_2d_inv=to_np(up["conic_2d_inv"]), flow_double=flow_double,
+        with_bound=True)
 
 
 def _check_grads(scene, grads, ref_g, *, colors=False):
@@ -64,8 +65,7 @@ def _check_grads(scene, grads, ref_g, *, colors=False):
     failures = []
     for name in names:
         expected = ref_g[name]
-        bad, worst = grad_mismatch(to_np(grads[name]).reshape(expected.shape), expected)
-        print(f"[raw grad] {name}: mismatches={bad} worst_ratio={worst:.3f}", flush=True)
+        bad, worst = report_grad(name, to_np(grads[name]).reshape(expected.shape), expected, ref_g["bound"][name])
         if bad:
             failures.append((name, bad, worst))
     assert not failures, failures

@@ -366,7 +366,7 @@ def test_backward_matches_float64_autograd(seed, compute_depth):
                                                                                                   dtype=torch.float64)
     ga = torch.randn(1, H, W, generator=g, dtype=torch.float64)
     grads = oracle.rasterize_backward(s, res, gc.numpy().astype(np.float32), gd.numpy().astype(np.float32),
-                                      ga.numpy().astype(np.float32), compute_depth=compute_depth)
+                                      ga.numpy().astype(np.float32), compute_depth=compute_depth, with_bound=True)
 
     pre, leaves = dense_pre(s, grad=True)
     pre["ndc"].retain_grad()
@@ -387,11 +387,12 @@ def test_backward_matches_float64_autograd(seed, compute_depth):
         "sh": leaves["shs"].grad,
     }
     for name, expected in checks.items():
-        bad, worst = grad_mismatch(grads[name], expected.numpy())
+        bad, worst, _, _ = grad_mismatch(grads[name], expected.numpy(), grads["bound"][name])
         assert bad == 0, (name, worst)
         assert np.abs(expected.numpy()).max() > 0
     # means2D carries dL/d(ndc) with z = 0
-    bad, worst = grad_mismatch(grads["means2D"][:, :2], pre["ndc"].grad.numpy())
+    bad, worst, _, _ = grad_mismatch(grads["means2D"][:, :2], pre["ndc"].grad.numpy(),
+                                     grads["bound"]["means2D"][:, :2])
     assert bad == 0, ("means2D", worst)
     assert not grads["means2D"][:, 2].any()
 
@@ -481,7 +482,7 @@ def test_precomputed_covariance_backward_matches_float64_autograd(seed):
     gd = torch.randn(1, H, W, generator=g, dtype=torch.float64)
     ga = torch.randn(1, H, W, generator=g, dtype=torch.float64)
     grads = oracle.rasterize_backward(s, res, gc.numpy().astype(np.float32), gd.numpy().astype(np.float32),
-                                      ga.numpy().astype(np.float32))
+                                      ga.numpy().astype(np.float32), with_bound=True)
     leaves = {k: t64(s[k]).requires_grad_(True) for k in ("means3D", "opacities", "shs", "cov3D_precomp")}
     pre = dense_ref.preprocess(leaves["means3D"], None, None, t64(s["viewmatrix"]), t64(s["projmatrix"]),
                                t64(s["campos"]), s["tanfovx"], s["tanfovy"], W, H, shs=leaves["shs"],
@@ -493,7 +494,7 @@ def test_precomputed_covariance_backward_matches_float64_autograd(seed):
     for name, key in (("means3D", "means3D"), ("cov3D", "cov3D_precomp"), ("opacities", "opacities"),
                       ("sh", "shs")):
         expected = leaves[key].grad.numpy()
-        bad, worst = grad_mismatch(grads[name], expected)
+        bad, worst, _, _ = grad_mismatch(grads[name], expected, grads["bound"][name])
         assert bad == 0, (name, worst)
         assert np.abs(expected).max() > 0
 
@@ -589,7 +590,7 @@ def test_mip_filter_backward_matches_float64_autograd(seed, precomp):
     gd = torch.randn(1, H, W, generator=g, dtype=torch.float64)
     ga = torch.randn(1, H, W, generator=g, dtype=torch.float64)
     grads = oracle.rasterize_backward(s, res, gc.numpy().astype(np.float32), gd.numpy().astype(np.float32),
-                                      ga.numpy().astype(np.float32))
+                                      ga.numpy().astype(np.float32), with_bound=True)
     names = ("means3D", "opacities", "shs") + (("cov3D_precomp",) if precomp else ("scales", "rotations"))
     leaves = {k: t64(s[k]).requires_grad_(True) for k in names}
     pre = dense_ref.preprocess(leaves["means3D"], leaves.get("scales"), leaves.get("rotations"),
@@ -604,6 +605,7 @@ def test_mip_filter_backward_matches_float64_autograd(seed, precomp):
     key_of = {"cov3D_precomp": "cov3D", "shs": "sh"}
     for name in names:
         expected = leaves[name].grad.numpy()
-        bad, worst = grad_mismatch(grads[key_of.get(name, name)], expected)
+        key = key_of.get(name, name)
+        bad, worst, _, _ = grad_mismatch(grads[key], expected, grads["bound"][key])
         assert bad == 0, (name, worst)
         assert np.abs(expected).max() > 0
