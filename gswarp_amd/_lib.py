@@ -35,6 +35,7 @@ SIGNATURES = {
          _i32, _i32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     ),
     "gs_mark_visible": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp]),
+    "gs_count_tiles": (ctypes.c_int, [_i32, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp]),
     "gs_scan_scratch_bytes": (_sz, [_i32]),
     "gs_depth_keys": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp]),
     "gs_scan_tiles": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),

@@ -301,6 +301,36 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p)
   if (p.coverage != nullptr) p.coverage[idx] = pack_cover(cover);
 }
 
+// Tile count and cover word of already projected Gaussians (the preprocess's
+// count on given 2D inputs, as binning_kernels.py:56-123 recounts them):
+// record (x, y, conic a, b | conic c, opacity), cov2D (a, b, c) and radius.
+// Every lane of the grid stays to the end, as in the preprocess.
+__global__ __launch_bounds__(256) void count_tiles_kernel(int P, const int* __restrict__ radii,
+                                                          const float4* __restrict__ records,
+                                                          const float* __restrict__ cov2d, int grid_x, int grid_y,
+                                                          int coverage_mode, int* tiles_touched, int4* coverage) {
+  __shared__ CoverCountLds s_cover[256 / 64];
+  const int idx0 = blockIdx.x * blockDim.x + threadIdx.x;
+  const bool in_range = idx0 < P;
+  const int idx = in_range ? idx0 : P - 1;
+  const int rad = radii[idx];
+  const bool active = in_range && rad > 0;
+  float4 r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1 = r0;
+  float aa = 0.0f, cc = 0.0f;
+  if (active) {
+    r0 = records[3 * (size_t)idx];
+    r1 = records[3 * (size_t)idx + 1];
+    aa = cov2d[3 * (size_t)idx];
+    cc = cov2d[3 * (size_t)idx + 2];
+  }
+  TileCover cover;
+  const int touched = wave_count_covered_tiles(active, r0.x, r0.y, aa, cc, r0.z, r0.w, r1.x, r1.y, rad, grid_x,
+                                               grid_y, coverage_mode, cover, s_cover[threadIdx.x >> 6]);
+  if (!in_range) return;
+  tiles_touched[idx] = touched;
+  if (coverage != nullptr) coverage[idx] = pack_cover(cover);
+}
+
 // markVisible: view-space z beyond the near plane (preprocess_kernels.py:604-617).
 __global__ __launch_bounds__(256) void mark_visible_kernel(int P, const float* __restrict__ means3d,
                                                            const float* __restrict__ V, uint8_t* visible) {
@@ -386,5 +416,22 @@ extern "C" int gs_mark_visible(int32_t P, const float* means3d, const float* vie
   if (!means3d || !viewmatrix || !visible) return GS_ERR_INVALID_ARGUMENT;
   hipLaunchKernelGGL(gs::mark_visible_kernel, dim3((P + 255) / 256), dim3(256), 0, (hipStream_t)stream, P,
                      means3d, viewmatrix, visible);
+  return gs_status_from_hip(hipGetLastError());
+}
+
+extern "C" int gs_count_tiles(int32_t P, const int32_t* radii, const float* records, const float* conic_2d_inv,
+                              int32_t image_width, int32_t image_height, int32_t coverage_mode,
+                              int32_t* tiles_touched, int32_t* coverage, void* stream) {
+  if (P < 0 || image_width <= 0 || image_height <= 0) return GS_ERR_INVALID_ARGUMENT;
+  if (coverage_mode < 0 || coverage_mode > 2) return GS_ERR_INVALID_ARGUMENT;
+  if (P == 0) return GS_OK;
+  if (!radii || !records || !conic_2d_inv || !tiles_touched) return GS_ERR_INVALID_ARGUMENT;
+  if ((reinterpret_cast<uintptr_t>(records) & 15) || (reinterpret_cast<uintptr_t>(coverage) & 15))
+    return GS_ERR_MISALIGNED;
+  const int grid_x = (image_width + gs::kBlockX - 1) / gs::kBlockX;
+  const int grid_y = (image_height + gs::kBlockY - 1) / gs::kBlockY;
+  hipLaunchKernelGGL(gs::count_tiles_kernel, dim3((P + 255) / 256), dim3(256), 0, (hipStream_t)stream, P, radii,
+                     reinterpret_cast<const float4*>(records), conic_2d_inv, grid_x, grid_y, coverage_mode,
+                     tiles_touched, reinterpret_cast<int4*>(coverage));
   return gs_status_from_hip(hipGetLastError());
 }

@@ -95,6 +95,20 @@ int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, const float*
                       uint8_t* clamped, void* stream);
 
 /*
+ * Tile coverage of already projected Gaussians: for each i with radii[i] > 0,
+ * tiles_touched[i] = the number of tiles it is binned to under coverage_mode
+ * and, when coverage (optional, (N,4) int32, 16-byte aligned) is given, its
+ * cover word, both exactly as gs_preprocess_fwd computes them; radius 0
+ * gives 0.  records (N,12) supplies the screen position, conic and opacity
+ * (floats 0-5 of the record), conic_2d_inv (N,3) the 2D covariance.
+ * Replaces: binning_kernels.py:56-123 (_recount_covered_tiles_warp_kernel)
+ * with math_kernels.py:306-390 (_count_covered_tiles_wp).
+ */
+int gs_count_tiles(int32_t P, const int32_t* radii, const float* records, const float* conic_2d_inv,
+                   int32_t image_width, int32_t image_height, int32_t coverage_mode, int32_t* tiles_touched,
+                   int32_t* coverage, void* stream);
+
+/*
  * visible[i] = view-space z of means3d[i] > 0.2.
  * Replaces: preprocess_ops.py:584-595 (mark_visible) with
  * preprocess_kernels.py:604-624.

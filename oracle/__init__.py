@@ -388,13 +388,13 @@ def gradient_bound(scene: dict, result: dict, gg, err, mag, *, grad_proj_2d=None
     in any order over that many partial sums, by the second part).  The
     per-Gaussian backward is linear in the render gradients, so B reaches
     each output through the absolute value of its Jacobian: column k's
-    Jacobian is the backward of a unit render gradient in column k alone
+    Jacobian J_k is the backward of a unit render gradient in column k alone
     (Gaussians are independent, so one run gives it for all of them), and
     the bound is  sum_k |J_k| B_k + CHAIN_DEPTH u (M + max M over the Gaussian's
-    components of the same output), M = sum_k |J_k g_k| + |J_meta g_meta|: the
+    components of the same output), M = sum_k |J_k| |g_k| + |J_meta g_meta|: the
     rounding of the chain itself, whose intermediate values are on the scale
-    of the Gaussian's largest output component.  Returns a dict of
-    float64 arrays keyed like the gradients (plus "grad_gauss").
+    of the Gaussian's largest output component.  Returns a dict of float64
+    arrays keyed like the gradients (plus "grad_gauss").
     """
     pre = result["pre"]
     tt = np.asarray(pre["tiles_touched"], np.float64)[:, None]
@@ -405,15 +405,42 @@ def gradient_bound(scene: dict, result: dict, gg, err, mag, *, grad_proj_2d=None
     acc_m = {}
     zeros_meta = dict(grad_proj_2d=np.zeros((N, 2), np.float32), grad_conic_2d=np.zeros((N, 3), np.float32),
                       grad_conic_2d_inv=np.zeros((N, 3), np.float32))
+    absg = np.abs(gg)
+    B32 = B.astype(np.float32)  # bound arithmetic needs a few significant digits, not 16
+
+    def add(acc, key, value, index=None):
+        if key not in acc:
+            acc[key] = np.zeros(value.shape if index is None else jac_shapes[key], np.float32)
+        if index is None:
+            acc[key] += value
+        else:
+            acc[key][index] += value
+
+    jac_shapes = {}
     for k in range(10):
-        if not np.any(B[:, k]) and not np.any(gg[:, k]):
+        # column 5 (opacity) leaves the chain untouched; only the colour columns reach the SH gradients
+        if k == 5 or (not np.any(B[:, k]) and not np.any(gg[:, k])):
             continue
-        for src, acc in ((B[:, k], acc_b), (gg[:, k], acc_m)):
-            unit = np.zeros((N, 10), np.float32)
-            unit[:, k] = src
-            part = _backward_chain(scene, pre, unit, flow_double=flow_double, **zeros_meta)
-            for key in _OUTPUT_KEYS:
-                acc[key] = acc.get(key, 0.0) + np.abs(part[key].astype(np.float64))
+        unit = np.zeros((N, 10), np.float32)
+        unit[:, k] = 1.0
+        jac = _backward_chain(scene, pre, unit, flow_double=flow_double, **zeros_meta)
+        for key in _OUTPUT_KEYS:
+            if key == "sh":
+                if k not in (6, 7, 8) or not jac[key].size:
+                    continue
+                # colour channel c reaches only the channel-c SH coefficients
+                jac_shapes[key] = jac[key].shape
+                index = (slice(None), slice(None), k - 6)
+                a = np.abs(jac[key][index])
+                add(acc_b, key, a * B32[:, k:k + 1], index)
+                add(acc_m, key, a * absg[:, k:k + 1], index)
+                continue
+            a = np.abs(jac[key])
+            if not a.size or not a.any():
+                continue
+            shape = (-1,) + (1,) * (a.ndim - 1)
+            add(acc_b, key, a * B32[:, k].reshape(shape))
+            add(acc_m, key, a * absg[:, k].reshape(shape))
     meta = {"grad_proj_2d": grad_proj_2d, "grad_conic_2d": grad_conic_2d, "grad_conic_2d_inv": grad_conic_2d_inv}
     for name, value in meta.items():
         if value is None or not np.any(value):
@@ -422,7 +449,8 @@ def gradient_bound(scene: dict, result: dict, gg, err, mag, *, grad_proj_2d=None
         args[name] = np.ascontiguousarray(value, np.float32)
         part = _backward_chain(scene, pre, np.zeros((N, 10), np.float32), flow_double=flow_double, **args)
         for key in _OUTPUT_KEYS:
-            acc_m[key] = acc_m.get(key, 0.0) + np.abs(part[key].astype(np.float64))
+            if part[key].size:
+                add(acc_m, key, np.abs(part[key]))
     for key in _OUTPUT_KEYS:
         m = acc_m.get(key, 0.0)
         if np.ndim(m):

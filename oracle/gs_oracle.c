@@ -1016,6 +1016,7 @@ void or_render_bwd(int W, int H, int P_gauss, const int* ranges, const int* poin
       }
     }
   }
+#pragma omp parallel for schedule(static)
   for (long long i = 0; i < (long long)per_thread; ++i) {
     double s = 0.0, se = 0.0, sm = 0.0;
     for (int t = 0; t < nthreads; ++t) {
