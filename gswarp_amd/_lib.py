@@ -39,6 +39,8 @@ SIGNATURES = {
     "gs_scan_scratch_bytes": (_sz, [_i32]),
     "gs_depth_keys": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp]),
     "gs_scan_tiles": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "gs_scan_tiles_static_max_points": (_i32, []),
+    "gs_scan_tiles_static": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "gs_num_rendered_readback": (ctypes.c_int, [_vp, _vp, _vp]),
     "gs_duplicate_keys": (
         ctypes.c_int,

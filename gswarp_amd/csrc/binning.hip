@@ -15,6 +15,8 @@
 //   64 bits, so the sort moves 8 bytes per pair.
 // Depths of binned Gaussians are positive, so their float bits order like the
 // depths; both stable sorts therefore give (tile, depth, point index) order.
+#include <mutex>
+
 #include "gs_common.h"
 #include "gs_capi.h"
 
@@ -181,6 +183,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_blocks_kernel(int nb, long 
 }
 
 __global__ __launch_bounds__(kScanThreads) void scan_apply_kernel(int n, const int* __restrict__ in,
+                                                                 const int* __restrict__ order,
                                                                  const long long* __restrict__ block_offsets,
                                                                  int* __restrict__ out) {
   __shared__ long long lds4[kScanThreads / 64];
@@ -190,7 +193,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_apply_kernel(int n, const i
 #pragma unroll
   for (int i = 0; i < kScanItems; ++i) {
     const long long idx = base + i;
-    v[i] = idx < n ? in[idx] : 0;
+    v[i] = idx < n ? in[order ? order[idx] : (int)idx] : 0;
   }
 #pragma unroll
   for (int i = 0; i < kScanItems; ++i) s += v[i];
@@ -634,6 +637,8 @@ extern "C" const char* gs_status_string(int status) {
       return "scratch buffer too small";
     case GS_ERR_OVERFLOW:
       return "size exceeds the int32 index range";
+    case GS_ERR_TOO_LARGE:
+      return "size exceeds the fixed scratch of an allocation-free entry point";
     default:
       return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown error";
   }
@@ -672,7 +677,78 @@ extern "C" int gs_scan_tiles(int32_t P, const int32_t* tiles_touched, const int3
   hipLaunchKernelGGL(gs::scan_blocks_kernel, dim3(1), dim3(gs::kScanThreads), 0, s, nb, block_sums, block_range,
                      reinterpret_cast<long long*>(info_dev));
   hipLaunchKernelGGL(gs::scan_apply_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P,
-                     gathered ? gathered : tiles_touched, block_sums, offsets);
+                     gathered ? gathered : tiles_touched, nullptr, block_sums, offsets);
+  return gs_status_from_hip(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------
+// gs_scan_tiles_static: the same scan with its scratch in a file-scope
+// device array instead of a caller buffer, for callers that cannot allocate.
+// The scratch holds the per-block sums and depth ranges (16 bytes per block
+// of kScanTile Gaussians); the reduce pass writes every entry the later
+// passes read, so nothing has to start at zero.  With an order the counts are
+// gathered through it in both passes (the caller-scratch variant stages the
+// gathered counts in its scratch instead).
+
+constexpr int32_t kStaticScanMaxPoints = 1 << 26;  // 64 Mi Gaussians
+constexpr size_t kStaticScanScratchBytes =
+    (((size_t)kStaticScanMaxPoints / gs::kScanTile) * 2 * sizeof(long long) + 255) & ~(size_t)255;  // 256 KiB
+
+static __device__ __align__(256) unsigned char scratch[kStaticScanScratchBytes];
+
+// Device address of `scratch` on each device, looked up once per device with
+// that device current (the host-side symbol is not a device address).
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mutex;
+static void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+static int static_scan_scratch(hipStream_t s, void** out) {
+  int dev = 0;
+  hipError_t e = s ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return GS_ERR_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int current = 0;
+    e = hipGetDevice(&current);
+    if (e != hipSuccess) return (int)e;
+    if (current != dev && (e = hipSetDevice(dev)) != hipSuccess) return (int)e;
+    void* p = nullptr;
+    const hipError_t lookup = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (current != dev && (e = hipSetDevice(current)) != hipSuccess) return (int)e;
+    if (lookup != hipSuccess) return (int)lookup;
+    if (p == nullptr) return GS_ERR_INVALID_ARGUMENT;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return GS_OK;
+}
+
+extern "C" int32_t gs_scan_tiles_static_max_points(void) { return kStaticScanMaxPoints; }
+
+extern "C" int gs_scan_tiles_static(int32_t P, const int32_t* tiles_touched, const int32_t* order,
+                                    const int32_t* radii, const float* depths, int32_t* offsets, int64_t* info_dev,
+                                    void* stream) {
+  if (P < 0 || !info_dev) return GS_ERR_INVALID_ARGUMENT;
+  if (P > kStaticScanMaxPoints) return GS_ERR_TOO_LARGE;
+  hipStream_t s = (hipStream_t)stream;
+  if (P == 0) {
+    hipLaunchKernelGGL(gs::zero_info_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<long long*>(info_dev));
+    return gs_status_from_hip(hipGetLastError());
+  }
+  if (!tiles_touched || !offsets || (radii == nullptr) != (depths == nullptr)) return GS_ERR_INVALID_ARGUMENT;
+  void* base = nullptr;
+  const int st = static_scan_scratch(s, &base);
+  if (st != GS_OK) return st;
+  const int nb = gs_scan_blocks(P);
+  long long* block_sums = static_cast<long long*>(base);
+  unsigned long long* block_range = reinterpret_cast<unsigned long long*>(block_sums + nb);
+  hipLaunchKernelGGL(gs::scan_reduce_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, tiles_touched, order,
+                     radii, depths, block_sums, block_range, nullptr);
+  hipLaunchKernelGGL(gs::scan_blocks_kernel, dim3(1), dim3(gs::kScanThreads), 0, s, nb, block_sums, block_range,
+                     reinterpret_cast<long long*>(info_dev));
+  hipLaunchKernelGGL(gs::scan_apply_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, tiles_touched, order,
+                     block_sums, offsets);
   return gs_status_from_hip(hipGetLastError());
 }
 

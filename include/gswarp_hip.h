@@ -46,6 +46,7 @@ extern "C" {
 #define GS_ERR_MISALIGNED (-2)
 #define GS_ERR_SCRATCH_TOO_SMALL (-3)
 #define GS_ERR_OVERFLOW (-4)
+#define GS_ERR_TOO_LARGE (-5)
 
 #define GS_COVERAGE_SNUGBOX 0
 #define GS_COVERAGE_ACCUTILE_SWEEP 1
@@ -141,6 +142,22 @@ size_t gs_scan_scratch_bytes(int32_t P);
 int gs_scan_tiles(int32_t P, const int32_t* tiles_touched, const int32_t* order, const int32_t* radii,
                   const float* depths, int32_t* offsets, int64_t* info_dev, void* scratch, size_t scratch_bytes,
                   void* stream);
+
+/*
+ * gs_scan_tiles without a scratch argument: the scratch is a fixed device
+ * array inside the library (256 KiB per GPU, held until the process ends),
+ * so the call allocates nothing.  P may not exceed
+ * gs_scan_tiles_static_max_points() (2^26); larger P returns
+ * GS_ERR_TOO_LARGE.  Outputs and arguments are those of gs_scan_tiles.  All
+ * calls on one GPU share the array: calls that overlap in time on one GPU
+ * (two streams, two threads) race and give wrong results; serialise them.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses
+ * that forbid hipMalloc).
+ */
+int32_t gs_scan_tiles_static_max_points(void);
+int gs_scan_tiles_static(int32_t P, const int32_t* tiles_touched, const int32_t* order, const int32_t* radii,
+                         const float* depths, int32_t* offsets, int64_t* info_dev, void* stream);
 
 /*
  * Copies the two int64 at info_dev into caller-provided pinned host memory
