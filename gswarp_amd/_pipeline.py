@@ -19,7 +19,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib, _packing, _workspace
-from ._coverage import tile_coverage_mode_id
+from ._coverage import kernel_mode
 from ._runtime import BINNING_SORT_MODES, ExecutionOptions
 from ._state import (BinningState, ForwardResult, ForwardState, KeyLayout, PreprocessOutputs, RenderImages,
                      RenderStageResult)
@@ -190,7 +190,7 @@ def preprocess(inputs: RasterInputs, options: ExecutionOptions, *, pack: bool = 
         tiles_touched=torch.empty((P,), dtype=torch.int32, device=device),
         records=records,
         clamped=clamped,
-        coverage_mode=tile_coverage_mode_id(options.tile_coverage_mode),
+        coverage_mode=int(kernel_mode(options.tile_coverage_mode)),
         geom=geom,
         coverage=torch.empty((P, 4), dtype=torch.int32, device=device),
     )

@@ -8,9 +8,9 @@ frozen ``ExecutionOptions`` is bound to a forward and reused by its backward.
 The flow variant adds compute_flow_aux (GSWARP_COMPUTE_FLOW_AUX) and the
 top-K count (GSWARP_FLOW_TOPK, default 20) of flow_ops.py:42-59.
 
-All three sort-mode names select the same stable 64-bit radix sort here;
-they differ in the reference only in how the identical (tile, depth, index)
-order is produced.
+The three sort-mode names select how the (tile, depth, index) order of the
+pairs is produced (gswarp_amd/_pipeline.py:binning); every one gives the
+reference's lists bit for bit.
 """
 
 from __future__ import annotations
@@ -20,8 +20,7 @@ from contextlib import contextmanager
 from contextvars import ContextVar
 from dataclasses import dataclass
 
-from ._coverage import BASELINE_3DGS_COVERAGE, CoverageContract, normalize_tile_coverage_mode, \
-    resolve_tile_coverage_mode
+from ._coverage import check_mode_name, kernel_mode
 
 BINNING_SORT_MODES = ("warp_radix", "torch", "warp_depth_stable_tile")
 DEFAULT_BACKWARD_MODE = "manual"
@@ -94,7 +93,7 @@ def get_tile_coverage_mode() -> str:
 
 def set_tile_coverage_mode(mode: str) -> None:
     global _TILE_COVERAGE_MODE
-    _TILE_COVERAGE_MODE = normalize_tile_coverage_mode(mode)
+    _TILE_COVERAGE_MODE = check_mode_name(mode)
 
 
 def get_compute_depth() -> bool:
@@ -126,16 +125,18 @@ def set_flow_topk(k: int) -> None:
     _FLOW_TOPK = int(k)
 
 
-def resolve_execution_options(raster_settings, *, flow: bool = False,
-                              coverage_contract: CoverageContract = BASELINE_3DGS_COVERAGE) -> ExecutionOptions:
-    """Merge module defaults and per-call settings into an immutable snapshot."""
+def resolve_execution_options(raster_settings, *, flow: bool = False, exact_conic: bool = True) -> ExecutionOptions:
+    """Merge module defaults and per-call settings into an immutable snapshot.
+
+    exact_conic: the method's footprint is the screen-space conic (true for
+    every method of this package), so "auto" coverage means accutile_sweep."""
     backward_mode = getattr(raster_settings, "backward_mode", None)
     binning_sort_mode = getattr(raster_settings, "binning_sort_mode", None)
     compute_flow_aux = getattr(raster_settings, "compute_flow_aux", None) if flow else None
     return ExecutionOptions(
         backward_mode=_BACKWARD_MODE if backward_mode is None else backward_mode,
         binning_sort_mode=_BINNING_SORT_MODE if binning_sort_mode is None else binning_sort_mode,
-        tile_coverage_mode=resolve_tile_coverage_mode(_TILE_COVERAGE_MODE, coverage_contract),
+        tile_coverage_mode=kernel_mode(_TILE_COVERAGE_MODE, exact_conic=exact_conic).public_name,
         compute_depth=_COMPUTE_DEPTH,
         auto_tune=bool(getattr(raster_settings, "auto_tune", True)),
         auto_tune_verbose=bool(getattr(raster_settings, "auto_tune_verbose", True)),
@@ -154,7 +155,7 @@ def get_default_parameter_info() -> dict:
         "DEFAULT_BACKWARD_MODE": {"value": DEFAULT_BACKWARD_MODE, "category": "mode", "auto_tunable": False,
                                   "description": "Only the manual backward is implemented."},
         "DEFAULT_BINNING_SORT_MODE": {"value": DEFAULT_BINNING_SORT_MODE, "category": "mode", "auto_tunable": False,
-                                      "description": "Accepted for compatibility; one 64-bit radix sort runs."},
+                                      "description": "Packed 64-bit keys below 4 pairs per Gaussian, depth then tile above."},
         "DEFAULT_TILE_COVERAGE_MODE": {"value": DEFAULT_TILE_COVERAGE_MODE, "category": "mode",
                                        "auto_tunable": False, "description": "auto resolves to accutile_sweep."},
         "WORKGROUP_SIZE": {"value": 256, "category": "launch", "auto_tunable": False,

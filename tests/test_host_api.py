@@ -100,31 +100,26 @@ def test_pair_count_rejects_negative_and_int32_wrap():
 # ---------------------------------------------------------------- coverage policy
 
 def test_coverage_policy_rejects_exact_culling_for_non_exact_footprints():
-    axis_aligned = _coverage.CoverageContract(footprint=_coverage.FOOTPRINT_AXIS_ALIGNED,
-                                              support=_coverage.SUPPORT_ALPHA_CUTOFF,
-                                              sample_domain=_coverage.SAMPLE_PIXEL_CENTERS)
-    assert _coverage.resolve_tile_coverage_mode("auto", _coverage.CONSERVATIVE_COVERAGE) == "snugbox"
-    assert _coverage.resolve_tile_coverage_mode("auto", axis_aligned) == "snugbox"
-    assert _coverage.resolve_tile_coverage_mode("snugbox", axis_aligned) == "snugbox"
-    with pytest.raises(ValueError, match="cuda_compat_screen_conic"):
-        _coverage.resolve_tile_coverage_mode("conic_rect", _coverage.CONSERVATIVE_COVERAGE)
-    assert _coverage.resolve_tile_coverage_mode("auto", _coverage.BASELINE_3DGS_COVERAGE) == "accutile_sweep"
-    assert _coverage.tile_coverage_mode_id("accutile_sweep") == 1
-    assert _coverage.tile_coverage_mode_id("snugbox") == 0
-    assert _coverage.tile_coverage_mode_id("conic_rect") == 2
-    assert _coverage.resolve_tile_coverage_mode_id("auto", _coverage.BASELINE_3DGS_COVERAGE) == 1
-    with pytest.raises(ValueError, match="resolved"):
-        _coverage.tile_coverage_mode_id("auto")
+    """test_tile_coverage.py:167-230: auto is AccuTile for the exact screen conic
+    and the conservative box otherwise; the culling modes need the exact conic."""
+    CM = _coverage.CoverageMode
+    assert _coverage.kernel_mode("auto") is CM.ACCUTILE_SWEEP
+    assert _coverage.kernel_mode("auto", exact_conic=False) is CM.SNUGBOX
+    assert _coverage.kernel_mode("snugbox", exact_conic=False) is CM.SNUGBOX
+    for name in ("accutile_sweep", "conic_rect"):
+        with pytest.raises(ValueError, match="allows only 'snugbox'"):
+            _coverage.kernel_mode(name, exact_conic=False)
+    # kernel ids are the library's GS_COVERAGE_* values
+    header = HEADER.read_text()
+    for mode in CM:
+        assert f"#define GS_COVERAGE_{mode.name} {int(mode)}" in header
+    assert [_coverage.kernel_mode(n) for n in ("snugbox", "accutile_sweep", "conic_rect")] == [0, 1, 2]
 
 
-def test_coverage_contract_rejects_unknown_semantics():
-    with pytest.raises(ValueError, match="footprint"):
-        _coverage.CoverageContract(footprint="typo", support=_coverage.SUPPORT_ALPHA_CUTOFF,
-                                   sample_domain=_coverage.SAMPLE_PIXEL_CENTERS)
-    with pytest.raises(ValueError, match="CUDA 3-sigma"):
-        _coverage.CoverageContract(footprint=_coverage.FOOTPRINT_AXIS_ALIGNED, support=_coverage.SUPPORT_ALPHA_CUTOFF,
-                                   sample_domain=_coverage.SAMPLE_PIXEL_CENTERS,
-                                   exact_policy=_coverage.BASELINE_3DGS_COVERAGE.exact_policy)
+def test_coverage_mode_names_are_checked():
+    with pytest.raises(ValueError, match="mode must be one of 'auto', 'snugbox', 'accutile_sweep', 'conic_rect'"):
+        _coverage.check_mode_name("typo")
+    assert _coverage.PUBLIC_NAMES == ("auto", "snugbox", "accutile_sweep", "conic_rect")
 
 
 # ---------------------------------------------------------------- runtime options
