@@ -95,7 +95,7 @@ def sort_passes(tiles: int) -> int:
     return math.ceil((32 + math.ceil(math.log2(tiles))) / 8)
 
 
-def algorithmic_bytes(N: int, R: float, P: int, T: int, dataflow: str) -> dict:
+def algorithmic_bytes(N: int, R: float, P: int, T: int, dataflow: str, flow_k: int = 0) -> dict:
     """Bytes crossing each stage boundary once (the SH3, depth-on accounting of the
     reference dataflow): preprocess 112N + SH 228N, scan 8N, duplicate 44N + 12R
     (64-bit key + value) or 44N + 8R (tile id + value), ranges 8R + 8T, render
@@ -103,12 +103,13 @@ def algorithmic_bytes(N: int, R: float, P: int, T: int, dataflow: str) -> dict:
     backward 624N.  Sorts: the one 64-bit key sort moves 24R per pass over
     ceil((32 + ceil(log2 T)) / 8) passes; the depth-then-tile dataflow moves 16N
     per pass over 4 passes for the depth sort and 16R per pass over
-    ceil(log2 T / 8) passes for the tile sort."""
+    ceil(log2 T / 8) passes for the tile sort.  The flow render also writes
+    its top-K auxiliaries, 16 K P (id, weight and the two x_mu components)."""
     out = {
         "preprocess": 340.0 * N,
         "scan": 8.0 * N,
         "ranges": 8.0 * R + 8.0 * T,
-        "render": 44.0 * R + 24.0 * P + 8.0 * T,
+        "render": 44.0 * R + 24.0 * P + 8.0 * T + 16.0 * flow_k * P,
         "render_bwd": 44.0 * R + 28.0 * P + 40.0 * N + 8.0 * T,
         "preprocess_bwd": 624.0 * N,
     }
@@ -122,9 +123,31 @@ def algorithmic_bytes(N: int, R: float, P: int, T: int, dataflow: str) -> dict:
     return out
 
 
-def read_traffic(stage: str):
+def visited_pairs(n_contrib, width: int, height: int) -> int:
+    """Pairs the backward blend reads: each 16x16 tile's list back to front from
+    the largest n_contrib of its pixels, summed over the tiles (at most R;
+    less where a tile's last entries blend into none of its pixels)."""
+    import torch.nn.functional as F
+
+    t = n_contrib.reshape(1, 1, height, width).float()
+    return int(F.max_pool2d(t, 16, stride=16, ceil_mode=True).double().sum().item())
+
+
+def early_stop_share(alpha, width: int, height: int) -> float:
+    """Share of the forward's 16x4 pixel slices that may have stopped before the
+    end of their tile's list: every pixel has alpha > 0.99 (a pixel stops when
+    T would fall below 1e-4, and alpha is at most 0.99 per Gaussian, so it
+    stops only with T < 1e-2).  Where this is 0 the forward reads all R pairs."""
+    import torch.nn.functional as F
+
+    a = alpha.reshape(1, 1, height, width)
+    lowest = -F.max_pool2d(-a, (4, 16), stride=(4, 16), ceil_mode=True)
+    return float((lowest > 0.99).double().mean().item())
+
+
+def read_traffic(stage: str, config: int = 2):
     """HBM bytes per launch of a stage from the committed rocprofv3 PMC summary, if present."""
-    path = ROOT / "profiles" / "traffic_config2.txt"
+    path = ROOT / "profiles" / f"traffic_config{config}.txt"
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
@@ -333,29 +356,118 @@ def summarize_stats(stats_csv: str, out_path: str, bench_err: str | None = None,
     print("\n".join(lines))
 
 
-def cpu_baseline(scene, grads) -> dict:
-    """One fwd+bwd of the same scene with the C oracle on this host's cores."""
+def host_cpu_info() -> dict:
+    """The host's CPUs as this process sees them: os.cpu_count(), the CPUs it may
+    run on, the cgroup quota, the usable count (the smaller of those two) and
+    the model name."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    affinity = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        text = Path("/sys/fs/cgroup/cpu.max").read_text().split()
+        if text and text[0] != "max":
+            quota = float(text[0]) / float(text[1])
+    except (OSError, ValueError, IndexError):
+        pass
+    usable = affinity if quota is None else max(1, min(affinity, math.floor(quota)))
+    return {"os_cpu_count": os.cpu_count(), "affinity_cpus": affinity, "cgroup_cpu_quota": quota,
+            "usable_cpus": usable, "cpu_model": model}
+
+
+def cpu_baseline_and_parity(scene, grads, gpu: dict, flow: bool, top_k: int, reps: int = 3) -> tuple[dict, dict]:
+    """The CPU baseline and the parity check of the iteration-0 view, both from the C oracle.
+
+    Baseline: one untimed warm-up fwd+bwd of the same scene, then `reps` timed
+    ones on all usable host CPUs and one on a single thread.  Parity: the
+    warm-up's forward is the checker for the GPU's outputs of the same view
+    (gpu: images, radii, flow ids and leaf gradients captured after the timed
+    region), the gradients to the per-element bound of the oracle (its
+    rounding bound B, computed outside the timed runs)."""
+    import numpy as np
+
     import oracle
     from gswarp_amd import configs
 
-    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16")), 16)
+    info = host_cpu_info()
+    threads = info["usable_cpus"]
     oracle.set_num_threads(threads)
     host = configs.scene_to_numpy(scene)
-    g = {k: v.detach().cpu().numpy() for k, v in grads.items()}
+    gc = grads["color"].detach().cpu().numpy()
+    zero = np.zeros((1, *gc.shape[1:]), np.float32)
+    gd = zero if flow else grads["depth"].detach().cpu().numpy()
+    ga = zero if flow else grads["alpha"].detach().cpu().numpy()
+
+    def run():
+        res = oracle.rasterize(host, top_k=top_k)
+        oracle.rasterize_backward(host, res, gc, gd, ga, flow_double=flow)
+        return res
+
+    ref = run()
+    seconds = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        seconds.append(time.perf_counter() - t0)
+    oracle.set_num_threads(1)
     t0 = time.perf_counter()
-    res = oracle.rasterize(host)
-    oracle.rasterize_backward(host, res, g["color"], g["depth"], g["alpha"])
-    dt = time.perf_counter() - t0
+    run()
+    one_thread = time.perf_counter() - t0
+    oracle.set_num_threads(threads)
     n = host["means3D"].shape[0]
-    return {
-        "value": n / dt,
+    mean = sum(seconds) / len(seconds)
+    baseline = {
+        "value": n / mean,
         "unit": "Gaussians/s",
-        "cores": oracle.num_threads(),
+        "cores": threads,
         "kind": "port",
-        "sample": f"one fwd+bwd of the iteration-0 view of this workload ({n} Gaussians) by the C oracle "
-                  f"(oracle/gs_oracle.c, OpenMP), {dt:.2f} s",
-        "seconds": dt,
+        "sample": f"fwd+bwd of the iteration-0 view of this workload ({n} Gaussians) by the C oracle "
+                  f"(oracle/gs_oracle.c, OpenMP): 1 warm-up, mean of {reps} timed runs on {threads} threads "
+                  f"({mean:.2f} s), 1 run on 1 thread ({one_thread:.2f} s)",
+        "seconds": mean,
+        "seconds_per_rep": [round(t, 3) for t in seconds],
+        "value_1thread": n / one_thread,
+        "seconds_1thread": one_thread,
+        **info,
     }
+
+    t0 = time.perf_counter()
+    ref_g = oracle.rasterize_backward(host, ref, gc, gd, ga, flow_double=flow, with_bound=True)
+    rf = ref["fwd"]
+    parity = {"view": "iteration 0 (the scene's camera)",
+              "bar": "radii (and flow top-K ids) equal; colour, depth, alpha within 1e-4; each gradient "
+                     "element within 1e-3 |e| + 1e-5 + 2 B (B: the oracle's bound on its fp32 rounding)",
+              "radii_equal": bool(np.array_equal(gpu["radii"], ref["pre"]["radii"]))}
+    ok = parity["radii_equal"]
+    for key in ("color", "depth", "alpha"):
+        err = float(np.abs(gpu[key] - rf[key]).max())
+        parity[f"{key}_max_abs_err"] = err
+        ok = ok and err <= 1e-4
+    if flow:
+        parity["topk_ids_equal"] = bool(np.array_equal(gpu["ids"], rf["gs_per_pixel"]))
+        ok = ok and parity["topk_ids_equal"]
+    grad_report = {}
+    for name in ("means3D", "means2D", "opacities", "scales", "rotations", "sh"):
+        e = ref_g[name].astype(np.float64)
+        a = gpu["grads"][name].reshape(e.shape).astype(np.float64)
+        diff = np.abs(a - e)
+        plain = 1e-3 * np.abs(e) + 1e-5
+        tol = plain + 2.0 * ref_g["bound"][name]
+        failures = int((diff > tol).sum())
+        grad_report[name] = {"failures": failures, "worst_ratio": round(float((diff / tol).max()), 4),
+                             "outside_plain_bar": int((diff > plain).sum()), "elements": int(e.size)}
+        ok = ok and failures == 0
+    parity["gradients"] = grad_report
+    parity["ok"] = bool(ok)
+    parity["check_seconds"] = round(time.perf_counter() - t0, 2)
+    return baseline, parity
 
 
 def main() -> int:
@@ -452,17 +564,32 @@ def main() -> int:
             e1.record()
         if flow:
             outputs, upstream = [out[0], out[9]], [grads["color"], grads["x_mu"]]
+            images = {"color": out[0], "radii": out[1], "depth": out[2], "alpha": out[3], "ids": out[7]}
         else:
-            color, _radii, meta = out
+            color, radii, meta = out
             outputs, upstream = [color, meta.depth, meta.alpha], [grads["color"], grads["depth"], grads["alpha"]]
+            images = {"color": color, "radii": radii, "depth": meta.depth, "alpha": meta.alpha}
         torch.autograd.backward(outputs, upstream)
         if timed:
             e2.record()
             step_events.append((e0, e1, e2))
+        return images
+
+    def capture(i: int) -> dict:
+        """Outputs and leaf gradients of one untimed step, on the host."""
+        images = step(i, False)
+        torch.cuda.synchronize()
+        out = {k: v.detach().cpu().numpy() for k, v in images.items()}
+        out["grads"] = {k: leaves[k].grad.detach().cpu().numpy() for k in ("means3D", "scales", "rotations",
+                                                                         "opacities")}
+        out["grads"]["sh"] = leaves["shs"].grad.detach().cpu().numpy()
+        out["grads"]["means2D"] = means2D.grad.detach().cpu().numpy()
+        return out
 
     for i in range(args.warmup):
         step(i, False)
     torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(device)
     # Headline: the K timed steps run uninstrumented (only the two per-step
     # events around forward and backward).
     t_start = time.perf_counter()
@@ -470,6 +597,7 @@ def main() -> int:
         step(i, True)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t_start
+    peak_bytes = torch.cuda.max_memory_allocated(device)
     fwd_bwd_events = list(step_events)
     # Per-stage breakdown: the same K cameras again with HIP events around
     # every stage (their recording adds host and GPU time, so these steps are
@@ -482,6 +610,21 @@ def main() -> int:
         timer.enabled = False
     _pipeline.STAGE_TIMER = None
     step_events[:] = fwd_bwd_events
+    visited = [visited_pairs(nc, W, H) for nc in timer.notes.pop("n_contrib", [])]
+    R_visited = sum(visited) / len(visited) if visited else None
+    stopped = [early_stop_share(a, W, H) for a in timer.notes.pop("alpha", [])]
+    early_share = sum(stopped) / len(stopped) if stopped else 0.0
+    # Run-to-run repeatability of the iteration-0 view (the float atomics of the
+    # backward add in an unspecified order), and its outputs for the parity check.
+    first = capture(0)
+    second = capture(0)
+    repeat = {"images_max_abs_diff": max(float(abs(first[k] - second[k]).max()) for k in ("color", "depth", "alpha")),
+              "grads_max_abs_diff": max(float(abs(first["grads"][k] - second["grads"][k]).max())
+                                        for k in first["grads"]),
+              "grads_max_rel_diff": max(float((abs(first["grads"][k] - second["grads"][k])
+                                               / (abs(first["grads"][k]) + 1e-30)).max()) for k in first["grads"])}
+    log(f"[bench] run-to-run: images {repeat['images_max_abs_diff']:.3g}, gradients "
+        f"{repeat['grads_max_abs_diff']:.3g} max abs; peak allocated {peak_bytes / 2**30:.2f} GiB")
 
     ms_per_step = 1000.0 * elapsed / args.steps
     fwd_ms = sum(a.elapsed_time(b) for a, b, _ in step_events) / len(step_events)
@@ -497,28 +640,59 @@ def main() -> int:
     stages = {}
     if stage_ms and Rs:
         dataflows = set(timer.notes.get("binning_dataflow", []))
-        algo = algorithmic_bytes(N, R, P, T, "warp_radix" if dataflows == {"packed_key"} else sort_mode)
+        flow_k = _runtime.get_flow_topk() if flow else 0
+        algo = algorithmic_bytes(N, R, P, T, "warp_radix" if dataflows == {"packed_key"} else sort_mode, flow_k)
+        # The formula counts every pair once per stage.  The backward reads each tile's
+        # list only from its largest n_contrib (visited pairs), and the forward stops a
+        # slice once all its pixels have stopped: where that happens the formula does not
+        # describe the work, and its fraction is not given (the visited figures are).
+        visited_algo = algorithmic_bytes(N, R_visited, P, T, "warp_radix", flow_k) if R_visited else {}
+        formula_applies = {"render": early_share <= 0.01,
+                           "render_bwd": R_visited is None or R_visited >= 0.5 * R}
         for name, ms in sorted(stage_ms.items(), key=lambda kv: -kv[1]):
             gbps = algo[name] / (ms * 1e-3) / 1e9 if name in algo else None
-            stages[name] = {"ms": round(ms, 4), "algorithmic_bytes": algo.get(name),
-                            "achieved_GBps": None if gbps is None else round(gbps, 1),
-                            "hbm_frac": None if gbps is None else round(gbps / HBM_PEAK_GBPS, 4)}
-            log(f"[bench]   {name:15s} {ms:8.4f} ms" + ("" if gbps is None else f"  {gbps:8.1f} GB/s"))
+            entry = {"ms": round(ms, 4), "algorithmic_bytes": algo.get(name),
+                     "achieved_GBps": None if gbps is None else round(gbps, 1),
+                     "hbm_frac": None if gbps is None else round(gbps / HBM_PEAK_GBPS, 4)}
+            if name == "render_bwd" and R_visited:
+                vg = visited_algo[name] / (ms * 1e-3) / 1e9
+                entry.update(visited_pairs=round(R_visited), visited_bytes=visited_algo[name],
+                             visited_GBps=round(vg, 1), visited_hbm_frac=round(vg / HBM_PEAK_GBPS, 4))
+            if name == "render":
+                entry["early_stopped_slice_share"] = round(early_share, 4)
+            if not formula_applies.get(name, True):
+                entry["hbm_frac"] = entry["achieved_GBps"] = None
+            traffic = read_traffic(name, args.config)
+            if traffic is not None:
+                entry["counter_bytes"] = traffic
+                entry["counter_hbm_frac"] = round(traffic / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)
+            stages[name] = entry
+            shown = entry.get("visited_GBps") if entry["hbm_frac"] is None else gbps
+            note = "" if entry["hbm_frac"] is not None else (" (visited pairs)" if shown else " (formula n/a)")
+            log(f"[bench]   {name:15s} {ms:8.4f} ms" + ("" if shown is None else f"  {shown:8.1f} GB/s") + note)
         sort_names = [n for n in ("depth_sort", "sort") if n in stage_ms]
         sort_ms = sum(stage_ms[n] for n in sort_names)
         sort_bytes = sum(algo[n] for n in sort_names)
         binning_sort = {"mode": sort_mode, "stages": sort_names, "ms": round(sort_ms, 4),
                         "algorithmic_bytes": sort_bytes,
                         "hbm_frac": round(sort_bytes / (sort_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+        counter = [stages[n].get("counter_bytes") for n in sort_names]
+        if all(c is not None for c in counter):
+            # the bytes the sort kernels actually move (PMC), next to the formula's
+            binning_sort["counter_bytes"] = sum(counter)
+            binning_sort["counter_hbm_frac"] = round(sum(counter) / (sort_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)
         binning_sort["dataflow"] = sorted(dataflows)
         log(f"[bench]   binning sort ({sort_mode}, {'/'.join(sorted(dataflows))}) {sort_ms:.4f} ms  "
-            f"{binning_sort['hbm_frac'] * 100:.1f}% of HBM peak")
+            f"{binning_sort['hbm_frac'] * 100:.1f}% of HBM peak (formula bytes)")
         dominant = max((n for n in stage_ms if n in algo), key=lambda n: stage_ms[n])
         achieved = algo[dominant] / (stage_ms[dominant] * 1e-3) / 1e9
         roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 5),
-                    "traffic": read_traffic(dominant),
+                    "traffic": read_traffic(dominant, args.config),
                     "algorithmic_bytes_per_launch": algo[dominant]}
+        if "visited_GBps" in stages[dominant]:
+            roofline["visited_achieved"] = stages[dominant]["visited_GBps"]
+            roofline["visited_frac"] = stages[dominant]["visited_hbm_frac"]
     copy_gbps = measure_copy_bandwidth(device)
     log(f"[bench] device copy bandwidth {copy_gbps:.0f} GB/s")
     if roofline is not None:
@@ -552,13 +726,19 @@ def main() -> int:
         "stages": stages,
         "binning_sort": binning_sort,
         "roofline": roofline,
+        "peak_allocated_bytes": peak_bytes,
+        "run_to_run": repeat,
         "cpu_baseline": None,
+        "parity": None,
     }
     if not args.no_cpu_baseline:
-        log("[bench] CPU baseline (oracle) ...")
-        result["cpu_baseline"] = cpu_baseline(scene, grads)  # the scene carries the iteration-0 camera
-        log(f"[bench] CPU baseline {result['cpu_baseline']['seconds']:.2f} s on "
-            f"{result['cpu_baseline']['cores']} threads")
+        log("[bench] CPU baseline and parity check (oracle) ...")
+        # the scene carries the iteration-0 camera
+        top_k = _runtime.get_flow_topk() if flow else 0
+        baseline, parity = cpu_baseline_and_parity(scene, grads, first, flow, top_k)
+        result["cpu_baseline"], result["parity"] = baseline, parity
+        log(f"[bench] CPU baseline {baseline['seconds']:.2f} s on {baseline['cores']} threads, "
+            f"{baseline['seconds_1thread']:.2f} s on 1; parity {'ok' if parity['ok'] else 'FAILED'}")
     print(json.dumps(result), flush=True)
     return 0
 

@@ -282,6 +282,10 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
     pinned = _workspace.readback_buffer(device, torch.cuda.current_stream(device))
     capacity = _workspace.pair_capacity(device) if (not pack and not keep_keys and mode != "torch"
                                                     and PACKED_SORT == "segmented" and P > 0) else 0
+    if mode == "warp_depth_stable_tile" and _workspace.last_pairs(device) > DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN * P:
+        # the last forward on this device took the depth-then-tile dataflow, which this one will most
+        # likely take too: provisioning the packed path's buffers would only raise the peak memory
+        capacity = 0
     if capacity > 0:
         # Buffers for the expected pair count are allocated before the count
         # is read back, so that one C call reads it and launches the whole
@@ -310,6 +314,8 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
             layout = KeyLayout(depth_min=int(result[1]), depth_bits=int(result[2]), value_bits=int(result[3]))
             return BinningState(grid_x, grid_y, point_list[:R], ranges, R, None, layout, rendered=bool(result[5]))
         depth_range = int(pinned[1]) & 0xFFFFFFFFFFFFFFFF
+        # declined: release the provisioned buffers before the exact-size binning allocates its own
+        del ws, result, events
         point_list = ranges = None
     else:
         point_list = ranges = None
@@ -551,6 +557,8 @@ def forward(inputs: RasterInputs, options: ExecutionOptions, *, flow: bool = Fal
                        images=None if flow else images)
         res = render(pre, bins, inputs.background, inputs.image_height, inputs.image_width, options, flow=flow,
                      images=images)
+        _note("n_contrib", res.n_contrib)
+        _note("alpha", res.alpha)
     return ForwardResult(
         num_rendered=bins.num_rendered,
         color=res.color,

@@ -73,6 +73,12 @@ def pair_capacity(device: torch.device) -> int:
     return int(last * PAIR_HEADROOM) + 1024 if last > 0 else 0
 
 
+def last_pairs(device: torch.device) -> int:
+    """Pair count of the last forward on the device (0 before the first)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return _pair_hint.get(index, 0)
+
+
 def note_pairs(device: torch.device, count: int) -> None:
     index = device.index if device.index is not None else torch.cuda.current_device()
     _pair_hint[index] = int(count)

@@ -90,16 +90,49 @@ def test_fast_path_declines_over_capacity(device):
     _check_against_oracle(scene, again, ref)
 
 
-def test_fast_path_declines_for_depth_then_tile(device):
+def _spy_calls(monkeypatch):
+    """Names of the C entry points the pipeline calls."""
+    from gswarp_amd import _lib
+
+    lib = _lib.load()
+    names = []
+    real = lib.call
+
+    def call(name, *args):
+        names.append(name)
+        return real(name, *args)
+
+    monkeypatch.setattr(lib, "call", call)
+    return names
+
+
+def test_fast_path_declines_for_depth_then_tile(device, monkeypatch):
     """The heavy-tailed config-3 scene at half resolution has more than four
-    pairs per Gaussian: the default mode's depth-then-tile dataflow runs
-    instead, with the oracle's outputs."""
+    pairs per Gaussian.  Provisioned for its count regardless of the last
+    forward, the one-call path declines (the default mode's depth-then-tile
+    dataflow applies) and the outputs still equal the oracle's."""
     scene = _scene("c3_half", device)
     host, ref = oracle_forward(scene)
     R = ref["bins"]["num_rendered"]
     assert R > 4 * scene["means3D"].shape[0]
-    _workspace.note_pairs(device, R)
+    monkeypatch.setattr(_workspace, "pair_capacity", lambda dev: 2 * R)
+    monkeypatch.setattr(_workspace, "last_pairs", lambda dev: 1)
+    names = _spy_calls(monkeypatch)
     _, result = _forward(scene, options())
+    assert "gs_readback_bin_packed" in names
+    assert not result.state.binning.rendered
+    _check_against_oracle(scene, result, ref)
+
+
+def test_no_provision_after_a_depth_then_tile_forward(device, monkeypatch):
+    """After a forward that took the depth-then-tile dataflow the next one does
+    not provision the packed path's buffers: it reads the count back alone."""
+    scene = _scene("c3_half", device)
+    host, ref = oracle_forward(scene)
+    _workspace.note_pairs(device, ref["bins"]["num_rendered"])
+    names = _spy_calls(monkeypatch)
+    _, result = _forward(scene, options())
+    assert "gs_readback_bin_packed" not in names and "gs_num_rendered_readback" in names
     assert not result.state.binning.rendered
     _check_against_oracle(scene, result, ref)
 
