@@ -396,9 +396,9 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
   __shared__ float4 s_rec[3 * 64];  // record j at s_rec[3 j .. 3 j + 2]
   __shared__ __align__(16) float s_ring[kRingSlots * kSlotFloats + kRingPad];
   const int two_t = 2 * p.num_tiles;
-  const int seg = (two_t + 7) & ~7;
+  const int seg = xcd_grid(two_t);
   const bool extra = (int)blockIdx.x >= seg;
-  const int unit = xcd_tile(extra ? blockIdx.x - seg : blockIdx.x, seg);
+  const int unit = xcd_unit(extra ? blockIdx.x - seg : blockIdx.x, two_t);
   if (unit >= two_t) return;  // segment padding
   const int tile = unit >> 1;
   const int sub = (unit & 1) + (extra ? 2 : 0);
@@ -890,7 +890,7 @@ extern "C" int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t 
   // four times the mean list length: only tiles that dominate the walk
   const int64_t long_tile = gs::kLongTileFactor * num_rendered / p.num_tiles;
   p.long_tile = long_tile > 0x7fffffffLL ? 0x7fffffff : (int)long_tile;
-  const dim3 grid(2 * ((2 * p.num_tiles + 7) & ~7));
+  const dim3 grid(2 * gs::xcd_grid(2 * p.num_tiles));
   if (compute_depth)
     hipLaunchKernelGGL((gs::render_bwd_kernel<true>), grid, dim3(64), 0, (hipStream_t)stream, p);
   else

@@ -223,11 +223,33 @@ __device__ __forceinline__ int xcd_tile(int b, int num_tiles) {
   return xcd * q + (xcd < r ? xcd : r) + (b >> 3);
 }
 
-// Same XCD banding for `subs` independent waves per tile: consecutive
-// workgroups on one XCD are the sub-waves of one tile, then the next tile.
-__device__ __forceinline__ int2 xcd_tile_sub(int b, int num_tiles, int subs) {
-  const int unit = xcd_tile(b, num_tiles * subs);
-  return make_int2(unit / subs, unit % subs);
+// The tile kernels deal their work units (a tile, or one slice of a tile;
+// the units of a tile are consecutive) to the XCDs in chunks of kXcdChunk
+// consecutive units: chunk j runs on XCD j % 8.  Each XCD then gets runs of
+// horizontally neighbouring tiles, which share most of their Gaussians in its
+// L2, from every part of the image, so the eight XCDs carry nearly equal
+// work.  (With one contiguous band of the image per XCD, xcd_tile, the bands
+// through the image centre, where the Gaussians concentrate, carried up to
+// 1.4 times the mean work of a band.)  kXcdChunk 0 selects the banding.
+#ifndef GS_XCD_CHUNK
+#define GS_XCD_CHUNK 32
+#endif
+constexpr int kXcdChunk = GS_XCD_CHUNK;
+
+// Workgroups to launch for num_units units (whole chunks for every XCD);
+// xcd_unit returns >= num_units for the padding workgroups.
+__host__ __device__ __forceinline__ int xcd_grid(int num_units) {
+  if (kXcdChunk <= 0) return (num_units + 7) & ~7;
+  const int span = 8 * kXcdChunk;
+  return (num_units + span - 1) / span * span;
+}
+
+// Unit of workgroup b (dispatched to XCD b % 8), a bijection of
+// [0, xcd_grid(num_units)).
+__device__ __forceinline__ int xcd_unit(int b, int num_units) {
+  if (kXcdChunk <= 0) return xcd_tile(b, xcd_grid(num_units));
+  const int u = b >> 3;  // this workgroup's position among its XCD's workgroups
+  return ((u / kXcdChunk) * 8 + (b & 7)) * kXcdChunk + u % kXcdChunk;
 }
 
 __device__ __forceinline__ float lane_f(float v, int lane) {

@@ -80,7 +80,9 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
   __shared__ float4 s_rec[3 * 64];  // record j at s_rec[3 j .. 3 j + 2]
   __shared__ int s_id[kFlow ? 64 : 1];
   const int lane = threadIdx.x;
-  const int2 ts = xcd_tile_sub(blockIdx.x, p.num_tiles, kSubs);
+  const int unit = xcd_unit(blockIdx.x, p.num_tiles * kSubs);
+  if (unit >= p.num_tiles * kSubs) return;  // grid padding
+  const int2 ts = make_int2(unit / kSubs, unit % kSubs);
   const int tile = ts.x;
   const int tx = tile % p.grid_x;
   const int ty = tile / p.grid_x;
@@ -224,7 +226,7 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
 }
 
 static int launch_render_fwd(const RenderFwdParams& p, bool flow, hipStream_t s) {
-  const dim3 grid(p.num_tiles * (4 / kFwdPix));
+  const dim3 grid(gs::xcd_grid(p.num_tiles * (4 / kFwdPix)));
   if (flow) {
     if (p.compute_depth)
       hipLaunchKernelGGL((render_fwd_kernel<true, true, kFwdPix>), grid, dim3(64), 0, s, p);
