@@ -1,7 +1,7 @@
 // Manual backward for gfx950.
 //
-// render_bwd: wave64 workgroups each own a slice of a tile (16x8 with two
-// pixels per lane, or 16x4 with one for tiles whose list is more than four
+// render_bwd: wave64 workgroups each own a slice of a tile (8x16 with two
+// pixels per lane, or 8x8 with one for tiles whose list is more than four
 // times the mean) and walk the tile's list back to front from the largest
 // n_contrib of their pixels
 // (backward_kernels.py:539-707 semantics: T starts at 1 - alpha_out and is
@@ -160,9 +160,10 @@ __device__ __forceinline__ BwdBatch load_bwd_batch(const RenderBwdParams& p, int
   return b;
 }
 
-// 4/kPix independent wave64 workgroups per tile, lane l owning the kPix
-// pixels of column l % 16 in rows l / 16 + 4k (k < kPix) of its slice (the
-// forward's layout).
+// 4/kPix independent wave64 workgroups per tile, each an 8 x 8 kPix slice,
+// lane l owning the kPix pixels of column l % 8 in rows l / 8 + 8k (k < kPix)
+// of its slice: the two pixels of a lane (kPix 2) lie in the slice's upper
+// and lower 8x8 blocks and share dx.
 //
 // Per pixel the reverse blend keeps two running values: T, the transmittance
 // in front of the current Gaussian, and S = U . acc, the upstream gradient
@@ -186,8 +187,7 @@ __device__ __forceinline__ BwdBatch load_bwd_batch(const RenderBwdParams& p, int
 //   dL/dopacity = sum(v).  Each batch of 64
 // records is first tested lane-parallel against the slice rectangle
 // (record_may_touch) and only records that may touch it are visited.
-// One wave's slice `sub` (rows 4 kPix sub .. 4 kPix sub + 4 kPix - 1) of
-// `tile`; s_rec (3 x 64 float4) and s_ring (kRingSlots x kSlotFloats +
+// One wave's slice `sub` of `tile`; s_rec (3 x 64 float4) and s_ring (kRingSlots x kSlotFloats +
 // kRingPad floats, 16-byte aligned) are the wave's LDS.
 template <bool kDepth, int kPix>
 __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int tile, int sub, float4* s_rec,
@@ -195,10 +195,15 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
   const int lane = threadIdx.x;
   const int tx = tile % p.grid_x;
   const int ty = tile / p.grid_x;
-  const int sx0 = tx * kBlockX;
-  const int sy0 = ty * kBlockY + sub * 4 * kPix;
-  const int px = sx0 + (lane & 15);
-  const int py0 = sy0 + (lane >> 4);
+  // 8 x 8 kPix slices: lane l at column l % 8, rows l / 8 + 8 k; sub 0 / 1
+  // are the left / right halves of the tile's first 8 kPix rows, 2 / 3 of the
+  // next ones
+  constexpr int kSliceW = 8;
+  constexpr int kSliceH = 8 * kPix;
+  const int sx0 = tx * kBlockX + (sub & 1) * kSliceW;
+  const int sy0 = ty * kBlockY + (sub >> 1) * kSliceH;
+  const int px = sx0 + (lane & 7);
+  const int py0 = sy0 + (lane >> 3);
   const int P = p.W * p.H;
   const float pfx = (float)px;
   int2 rg = p.ranges[tile];
@@ -211,7 +216,7 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
   int lmax = 0;
 #pragma unroll
   for (int k = 0; k < kPix; ++k) {
-    const int py = py0 + 4 * k;
+    const int py = py0 + 8 * k;
     pfy[k] = (float)py;
     last[k] = 0;
     T[k] = S[k] = gp0[k] = gp1[k] = gp2[k] = gpd[k] = gpa[k] = 0.0f;
@@ -236,8 +241,8 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
   const int flush_comp = lane < kSlotFloats / 4 ? slot_component(lane >> 2) : -1;
   int nrel = 0;  // Gaussians added to the ring so far
   int slot_gid0 = 0, slot_gid1 = 0;  // Gaussians of ring slots 0 and 1 (wave-uniform)
-  const float rx0 = (float)sx0, rx1 = (float)(sx0 + kBlockX - 1);
-  const float ry0 = (float)sy0, ry1 = (float)(sy0 + 4 * kPix - 1);
+  const float rx0 = (float)sx0, rx1 = (float)(sx0 + kSliceW - 1);
+  const float ry0 = (float)sy0, ry1 = (float)(sy0 + kSliceH - 1);
 
   int bs = imax(0, max_lc - 64);
   BwdBatch next = load_bwd_batch(p, rg.x + bs, max_lc - bs, lane);
@@ -315,7 +320,7 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
       float sv = -0.0f, svy = -0.0f, svyy = -0.0f, sr = -0.0f, sg = -0.0f, sb = -0.0f, sd = -0.0f;
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
-        // A pixel row set with no candidate in the whole wave is skipped:
+        // A block of pixels k with no candidate in the whole wave is skipped:
         // there G = 0 for every lane, which leaves T, S and the sums unchanged.
         if (cand_lanes[k] == 0) continue;
         // Gradient values use the hardware exponential (v_exp_f32): they only
@@ -381,9 +386,9 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
 }
 
 // A tile whose list is longer than p.long_tile is walked by four one-wave
-// workgroups, each a 16x4 slice with one pixel per lane: its serial walk,
+// workgroups, each an 8x8 quadrant with one pixel per lane: its serial walk,
 // which bounds the kernel when a few tiles hold most of the pairs, costs
-// less per Gaussian.  Any other tile is walked by two, each a 16x8 slice
+// less per Gaussian.  Any other tile is walked by two, each an 8x16 half
 // with two pixels per lane (fewer instructions per pixel).  The grid is a
 // segment of the first and second slices of every tile followed by one of
 // the third and fourth slices, which exit at once for ordinary tiles (each

@@ -1,6 +1,12 @@
 // Forward render: each 16x16 tile is covered by 4/kPix independent wave64
-// workgroups, each owning a 16 x 4*kPix slice; lane l owns the kPix pixels
-// of column l % 16 in rows l / 16 + 4k (k < kPix) of its slice.  Pixels of a
+// workgroups, each owning a slice of 64 kPix pixels: an 8x8 quadrant for
+// one pixel per lane (8x16 halves for two, the whole tile for four); lane l
+// owns the pixels of column l % w in rows l / w + (64 / w) k of its slice,
+// w its width.  Square slices are visited by fewer Gaussians than 16-wide
+// rows of the same size (the footprints are small and round).  The flow
+// variant keeps 16-wide rows (16 x 4 kPix slices): its per-pixel top-K
+// planes are written in rows of w consecutive floats, and 8-float rows
+// leave half of each cache line to another wave.  Pixels of a
 // lane share dx to a Gaussian, so a*dx*dx and b*dx are evaluated once per
 // lane, exactly as the per-pixel expression would round them.  The tile's
 // sorted Gaussians are fetched 64 at a time, one packed 48-byte record per
@@ -86,14 +92,20 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
   const int tile = ts.x;
   const int tx = tile % p.grid_x;
   const int ty = tile / p.grid_x;
-  const int sx0 = tx * kBlockX;
-  const int sy0 = ty * kBlockY + ts.y * 4 * kPixPerLane;
-  const int px = sx0 + (lane & 15);
-  const int py0 = sy0 + (lane >> 4);
+  // The wave's slice: kSliceW x kSliceH pixels, lane l at column l % kSliceW
+  // and rows l / kSliceW + kRowStep k of it.
+  constexpr int kSliceW = (kFlow || kPixPerLane == 4) ? 16 : 8;
+  constexpr int kSliceH = 64 * kPixPerLane / kSliceW;
+  constexpr int kRowStep = 64 / kSliceW;
+  constexpr int kAcross = kBlockX / kSliceW;  // slices side by side in a tile
+  const int sx0 = tx * kBlockX + (ts.y % kAcross) * kSliceW;
+  const int sy0 = ty * kBlockY + (ts.y / kAcross) * kSliceH;
+  const int px = sx0 + (lane % kSliceW);
+  const int py0 = sy0 + lane / kSliceW;
   const int P = p.W * p.H;
   const float pfx = (float)px;
-  const float rx0 = (float)sx0, rx1 = (float)(sx0 + kBlockX - 1);
-  const float ry0 = (float)sy0, ry1 = (float)(sy0 + 4 * kPixPerLane - 1);
+  const float rx0 = (float)sx0, rx1 = (float)(sx0 + kSliceW - 1);
+  const float ry0 = (float)sy0, ry1 = (float)(sy0 + kSliceH - 1);
   int2 rg = p.ranges[tile];
   rg.x = imax(0, imin(rg.x, p.num_rendered));
   rg.y = imax(rg.x, imin(rg.y, p.num_rendered));
@@ -109,7 +121,7 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
   uint64_t live_lanes[kPixPerLane];
 #pragma unroll
   for (int k = 0; k < kPixPerLane; ++k) {
-    const int py = py0 + 4 * k;
+    const int py = py0 + kRowStep * k;
     pfy[k] = (float)py;
     T[k] = 1.0f;
     live_lanes[k] = __ballot(px < p.W && py < p.H);
@@ -177,7 +189,7 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
         ws[k] = ws[k] + contribution;
         if (kDepth) da[k] = fmaf(b.z, contribution, da[k]);
         if (aux && blend && nsucc[k] < p.top_k) {
-          const size_t pix = (size_t)(py0 + 4 * k) * p.W + px;
+          const size_t pix = (size_t)(py0 + kRowStep * k) * p.W + px;
           const size_t ai = (size_t)nsucc[k] * P + pix;
           p.gs_per_pixel[ai] = s_id[j];
           p.weight[ai] = contribution;
@@ -193,7 +205,7 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
 
 #pragma unroll
   for (int k = 0; k < kPixPerLane; ++k) {
-    const int py = py0 + 4 * k;
+    const int py = py0 + kRowStep * k;
     const bool in_image = px < p.W && py < p.H;
     const int pix = py * p.W + px;
     if (in_image) {
@@ -207,7 +219,7 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
     }
     if (aux) {
       // Unused slots, plane by plane for the whole wave, so that each store
-      // covers the wave's pixels of one plane (rows of 16 consecutive
+      // covers the wave's pixels of one plane (rows of kSliceW consecutive
       // pixels) rather than one plane per lane.
       int s_from = in_image ? nsucc[k] : p.top_k;
 #pragma unroll
