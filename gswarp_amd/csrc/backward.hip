@@ -1,9 +1,9 @@
 // Manual backward for gfx950.
 //
-// render_bwd: wave64 workgroups each own a slice of a tile (8x16 with two
-// pixels per lane, or 8x8 with one for tiles whose list is more than four
-// times the mean) and walk the tile's list back to front from the largest
-// n_contrib of their pixels
+// render_bwd: wave64 workgroups each own a tile (its four 8x8 blocks, four
+// pixels per lane, or one 8x8 quadrant of it for tiles whose list is more
+// than four times the mean) and walk the tile's list back to front from the
+// largest n_contrib of their pixels
 // (backward_kernels.py:539-707 semantics: T starts at 1 - alpha_out and is
 // divided by max(1-alpha, 1e-5) per blended Gaussian, reverse recurrences for
 // colour, depth and alpha, the background term).  Per Gaussian each lane
@@ -160,10 +160,13 @@ __device__ __forceinline__ BwdBatch load_bwd_batch(const RenderBwdParams& p, int
   return b;
 }
 
-// 4/kPix independent wave64 workgroups per tile, each an 8 x 8 kPix slice,
-// lane l owning the kPix pixels of column l % 8 in rows l / 8 + 8k (k < kPix)
-// of its slice: the two pixels of a lane (kPix 2) lie in the slice's upper
-// and lower 8x8 blocks and share dx.
+// One wave walks a slice of kPix blocks of 8x8 pixels, kCols blocks wide:
+// lane l owns pixel (l % 8, l / 8) of every block, block k lying at
+// ((k % kCols) 8, (k / kCols) 8) from the slice's origin.  Slice `sub` of a
+// tile: with four blocks (kCols 2) the whole tile; with two stacked blocks
+// the left (0) or right (1) half; with one block the quadrant sub (0 / 1
+// the upper left / right, 2 / 3 the lower ones).  Pixels of a lane in one
+// column of blocks share dx to a Gaussian.
 //
 // Per pixel the reverse blend keeps two running values: T, the transmittance
 // in front of the current Gaussian, and S = U . acc, the upstream gradient
@@ -177,35 +180,37 @@ __device__ __forceinline__ BwdBatch load_bwd_batch(const RenderBwdParams& p, int
 // background is an opaque layer behind the last Gaussian; 1 - alpha >= 0.01
 // since alpha <= 0.99, so the 1e-5 floor never applies to it).  Per
 // Gaussian each lane then sums, with v = G * dL/dalpha_hat per pixel, the
-// moments (v dx, v dy, v dx^2, v dx dy, v dy^2, v) over its pixels (they
-// share dx) and the colour and depth terms alpha T dL/dpixel; the ten
-// per-lane components are summed over the wave and added to grad_gauss.
+// moments (v dx, v dy, v dx^2, v dx dy, v dy^2, v) over its pixels (per
+// column of blocks, whose pixels share dx) and the colour and depth terms
+// alpha T dL/dpixel; the ten per-lane components are summed over the wave
+// and added to grad_gauss.
 // The per-Gaussian backward forms the reference's per-pixel expressions
 // summed over pixels from the moments:
 //   dL/dxy    = -(W/2, H/2) * o * (a sum(v dx) + b sum(v dy), c sum(v dy) + b sum(v dx)),
 //   dL/dconic = -1/2 * o * (sum(v dx^2), sum(v dx dy), sum(v dy^2)),
 //   dL/dopacity = sum(v).  Each batch of 64
-// records is first tested lane-parallel against the slice rectangle
-// (record_may_touch) and only records that may touch it are visited.
-// One wave's slice `sub` of `tile`; s_rec (3 x 64 float4) and s_ring (kRingSlots x kSlotFloats +
-// kRingPad floats, 16-byte aligned) are the wave's LDS.
-template <bool kDepth, int kPix>
+// records is first tested lane-parallel against the slice (one bounding box
+// per record, record_box), and only records that may touch it are visited;
+// with kBlockCull each block is tested, and a record's visit skips the
+// blocks its box misses (worth its branches when a slice has four blocks).
+// s_rec (3 x 64 float4) and s_ring (kRingSlots x kSlotFloats + kRingPad
+// floats, 16-byte aligned) are the wave's LDS.
+template <bool kDepth, int kPix, int kCols, bool kBlockCull>
 __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int tile, int sub, float4* s_rec,
                                                  float* s_ring) {
+  static_assert(kPix % kCols == 0 && 8 * kCols <= kBlockX && 8 * (kPix / kCols) <= kBlockY, "slice in a tile");
+  constexpr int kSliceW = 8 * kCols;
+  constexpr int kSliceH = 8 * (kPix / kCols);
+  constexpr int kAcross = kBlockX / kSliceW;
   const int lane = threadIdx.x;
   const int tx = tile % p.grid_x;
   const int ty = tile / p.grid_x;
-  // 8 x 8 kPix slices: lane l at column l % 8, rows l / 8 + 8 k; sub 0 / 1
-  // are the left / right halves of the tile's first 8 kPix rows, 2 / 3 of the
-  // next ones
-  constexpr int kSliceW = 8;
-  constexpr int kSliceH = 8 * kPix;
-  const int sx0 = tx * kBlockX + (sub & 1) * kSliceW;
-  const int sy0 = ty * kBlockY + (sub >> 1) * kSliceH;
-  const int px = sx0 + (lane & 7);
-  const int py0 = sy0 + (lane >> 3);
+  const int sx0 = tx * kBlockX + (sub % kAcross) * kSliceW;
+  const int sy0 = ty * kBlockY + (sub / kAcross) * kSliceH;
   const int P = p.W * p.H;
-  const float pfx = (float)px;
+  float pfx[kCols];
+#pragma unroll
+  for (int c = 0; c < kCols; ++c) pfx[c] = (float)(sx0 + 8 * c + (lane & 7));
   int2 rg = p.ranges[tile];
   rg.x = imax(0, imin(rg.x, p.num_rendered));
   rg.y = imax(rg.x, imin(rg.y, p.num_rendered));
@@ -216,7 +221,8 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
   int lmax = 0;
 #pragma unroll
   for (int k = 0; k < kPix; ++k) {
-    const int py = py0 + 8 * k;
+    const int px = sx0 + 8 * (k % kCols) + (lane & 7);
+    const int py = sy0 + 8 * (k / kCols) + (lane >> 3);
     pfy[k] = (float)py;
     last[k] = 0;
     T[k] = S[k] = gp0[k] = gp1[k] = gp2[k] = gpd[k] = gpa[k] = 0.0f;
@@ -241,8 +247,6 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
   const int flush_comp = lane < kSlotFloats / 4 ? slot_component(lane >> 2) : -1;
   int nrel = 0;  // Gaussians added to the ring so far
   int slot_gid0 = 0, slot_gid1 = 0;  // Gaussians of ring slots 0 and 1 (wave-uniform)
-  const float rx0 = (float)sx0, rx1 = (float)(sx0 + kSliceW - 1);
-  const float ry0 = (float)sy0, ry1 = (float)(sy0 + kSliceH - 1);
 
   int bs = imax(0, max_lc - 64);
   BwdBatch next = load_bwd_batch(p, rg.x + bs, max_lc - bs, lane);
@@ -254,7 +258,26 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
     s_rec[3 * lane + 1] = next.r1;
     s_rec[3 * lane + 2] = next.r2;
     const int batch_id = next.id;  // lane j: Gaussian of record j
-    uint64_t todo = __ballot(lane < cnt && record_may_touch(next.r0, next.r1, rx0, rx1, ry0, ry1));
+    // blk[k]: the batch's records that may touch block k (with kBlockCull;
+    // otherwise those that may touch the slice, for every block)
+    uint64_t blk[kPix], todo = 0;
+    {
+      double bx0 = 0.0, bx1 = 0.0, by0 = 0.0, by1 = 0.0;
+      const bool live = lane < cnt && record_box(next.r0, next.r1, bx0, bx1, by0, by1);
+      if constexpr (kBlockCull) {
+#pragma unroll
+        for (int k = 0; k < kPix; ++k) {
+          const float x0 = (float)(sx0 + 8 * (k % kCols)), y0 = (float)(sy0 + 8 * (k / kCols));
+          blk[k] = __ballot(live && box_meets(bx0, bx1, by0, by1, x0, x0 + 7.0f, y0, y0 + 7.0f));
+          todo |= blk[k];
+        }
+      } else {
+        todo = __ballot(live && box_meets(bx0, bx1, by0, by1, (float)sx0, (float)(sx0 + kSliceW - 1), (float)sy0,
+                                          (float)(sy0 + kSliceH - 1)));
+#pragma unroll
+        for (int k = 0; k < kPix; ++k) blk[k] = todo;
+      }
+    }
     if (bs > 0) {
       const int nbs = imax(0, bs - 64);
       next = load_bwd_batch(p, rg.x + nbs, bs - nbs, lane);
@@ -265,24 +288,32 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
       const int pos = bs + jj;
       const float4 a = s_rec[3 * jj];
       const float4 b = s_rec[3 * jj + 1];
-      const float dx = a.x - pfx;
-      const float adxx = a.z * dx * dx;
-      const float b2dx = (a.w * dx) * 2.0f;
+      float dx[kCols], adxx[kCols], b2dx[kCols];
+#pragma unroll
+      for (int c = 0; c < kCols; ++c) {
+        dx[c] = a.x - pfx[c];
+        adxx[c] = a.z * dx[c] * dx[c];
+        b2dx[c] = (a.w * dx[c]) * 2.0f;
+      }
       float q[kPix], dy[kPix];
       bool cand[kPix];
       uint64_t cand_lanes[kPix];  // the wave's lanes with cand[k]
+      uint64_t any_lanes = 0;
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
+        q[k] = dy[k] = 0.0f;
+        cand[k] = false;
+        cand_lanes[k] = 0;
+        if (kBlockCull && !((blk[k] >> jj) & 1)) continue;  // the record's box misses block k
+        const int c = k % kCols;
         dy[k] = a.y - pfy[k];
-        q[k] = conic_q_px(adxx, b2dx, b.x, dy[k]);  // exponent = -0.5 q
+        q[k] = conic_q_px(adxx[c], b2dx[c], b.x, dy[k]);  // exponent = -0.5 q
         cand[k] = pos < last[k] && q[k] >= 0.0f && q[k] <= b.w;
         // the same comparisons as lane masks, ANDed in scalar registers
         cand_lanes[k] = __builtin_amdgcn_sicmp(pos, last[k], kCmpSLT) & __builtin_amdgcn_fcmpf(q[k], 0.0f, kCmpOGE) &
                         __builtin_amdgcn_fcmpf(q[k], b.w, kCmpOLE);
+        any_lanes |= cand_lanes[k];
       }
-      uint64_t any_lanes = 0;
-#pragma unroll
-      for (int k = 0; k < kPix; ++k) any_lanes |= cand_lanes[k];
       if (any_lanes == 0) continue;
       // Blend decisions, identical to the forward's: with the exponent above
       // power_cutoff + 2e-3 (q <= qcut - 4e-3) the forward's alpha is provably
@@ -296,6 +327,8 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
       uint64_t band = 0;  // lanes with a pixel in the band
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
+        // branch-free, so that the blocks' instruction chains interleave (a
+        // block the record's box misses has cand false and gets -inf)
         const bool sure = q[k] <= qsure;
         e[k] = (cand[k] && sure) ? q[k] * (-0.5f * kLog2e) : -__builtin_inff();
         // cand && !sure from the comparisons' lane masks (scalar ANDs; the
@@ -317,12 +350,16 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
       const float4 f = s_rec[3 * jj + 2];
       // -0 is the additive identity of every float, so the first terms
       // enter the sums exactly (and the compiler drops the additions).
-      float sv = -0.0f, svy = -0.0f, svyy = -0.0f, sr = -0.0f, sg = -0.0f, sb = -0.0f, sd = -0.0f;
+      float sv[kCols], svy[kCols];
+#pragma unroll
+      for (int c = 0; c < kCols; ++c) sv[c] = svy[c] = -0.0f;
+      float svyy = -0.0f, sr = -0.0f, sg = -0.0f, sb = -0.0f, sd = -0.0f;
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
-        // A block of pixels k with no candidate in the whole wave is skipped:
-        // there G = 0 for every lane, which leaves T, S and the sums unchanged.
+        // A block with no candidate in the whole wave is skipped: there G = 0
+        // for every lane, which leaves T, S and the sums unchanged.
         if (cand_lanes[k] == 0) continue;
+        const int c = k % kCols;
         // Gradient values use the hardware exponential (v_exp_f32): they only
         // need the 1e-3 gradient tolerance, the decisions above are exact.
         // A pixel that does not blend this Gaussian gets G = 2^-inf = 0, so
@@ -338,8 +375,8 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
         const float v = G * (Tn * d);
         const float dch = alpha * Tn;
         const float vdy = v * dy[k];
-        sv += v;
-        svy += vdy;
+        sv[c] += v;
+        svy[c] += vdy;
         svyy = fmaf(vdy, dy[k], svyy);
         sr = fmaf(dch, gp0[k], sr);
         sg = fmaf(dch, gp1[k], sg);
@@ -354,13 +391,22 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
       // and W/2, H/2 factors are per Gaussian and applied once, when the
       // per-Gaussian backward turns the sums into 2D gradients.
       float g[kGradFloats];
-      const float vdx = sv * dx;
-      g[0] = vdx;        // sum v dx
-      g[1] = svy;        // sum v dy
-      g[2] = vdx * dx;   // sum v dx^2
-      g[3] = svy * dx;   // sum v dx dy
-      g[4] = svyy;       // sum v dy^2
-      g[5] = sv;         // dL/dopacity
+      float vdx = sv[0] * dx[0];
+      g[0] = vdx;               // sum v dx
+      g[1] = svy[0];            // sum v dy
+      g[2] = vdx * dx[0];       // sum v dx^2
+      g[3] = svy[0] * dx[0];    // sum v dx dy
+      g[5] = sv[0];             // dL/dopacity
+#pragma unroll
+      for (int c = 1; c < kCols; ++c) {
+        vdx = sv[c] * dx[c];
+        g[0] += vdx;
+        g[1] += svy[c];
+        g[2] = fmaf(vdx, dx[c], g[2]);
+        g[3] = fmaf(svy[c], dx[c], g[3]);
+        g[5] += sv[c];
+      }
+      g[4] = svyy;              // sum v dy^2
       g[6] = sr;
       g[7] = sg;
       g[8] = sb;
@@ -385,35 +431,49 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
   if (nrel > 1) flush_slot(s_ring, 1, slot_gid1, lane, flush_comp, p.grad_gauss);
 }
 
-// A tile whose list is longer than p.long_tile is walked by four one-wave
-// workgroups, each an 8x8 quadrant with one pixel per lane: its serial walk,
-// which bounds the kernel when a few tiles hold most of the pairs, costs
-// less per Gaussian.  Any other tile is walked by two, each an 8x16 half
-// with two pixels per lane (fewer instructions per pixel).  The grid is a
-// segment of the first and second slices of every tile followed by one of
-// the third and fourth slices, which exit at once for ordinary tiles (each
-// segment padded to a multiple of 8 blocks): workgroups go round-robin to
-// the XCDs' CUs, and exiting workgroups interleaved with working ones at a
-// fixed period would leave some CUs with none of the work, while at the end
-// of the grid they only fill slots that the draining work leaves free.
-template <bool kDepth>
+// How a tile is split over waves.  With small Gaussians (a few tiles each)
+// two waves walk an ordinary tile, one 8x16 half each (two blocks, two
+// pixels per lane): many waves per SIMD (few registers) hide the latency of
+// the walk.  When the Gaussians are large (kWholeTiles: more than
+// kWholeTilePairsPerPoint tiles each on average) one wave walks the whole
+// tile (four blocks, four pixels per lane), so the moments of a Gaussian that
+// covers most of the tile are folded and sent once per tile instead of
+// twice.  Measured on one MI355X: halves 20% faster at 1M Gaussians, 1080p
+// (about 3 pairs per Gaussian), whole tiles 36% faster at 5M with the large
+// splats (about 30).  A tile whose list is longer than p.long_tile is walked
+// by four one-wave workgroups, one 8x8 quadrant each: its serial walk, which
+// bounds the kernel when a few tiles hold most of the pairs, is then
+// shorter.  The grid is a segment of kFirst workgroups per tile (the halves
+// or the whole tile of an ordinary tile, the first quadrants of a long one)
+// followed by one of 4 - kFirst per tile for the other quadrants, which exit
+// at once for ordinary tiles: workgroups go round-robin to the XCDs' CUs,
+// and exiting workgroups interleaved with working ones at a fixed period
+// would leave some CUs with none of the work, while at the end of the grid
+// they only fill slots that the draining work leaves free.
+constexpr int64_t kWholeTilePairsPerPoint = 4;
+
+template <bool kDepth, bool kWholeTiles>
 __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
+  constexpr int kFirst = kWholeTiles ? 1 : 2;
   __shared__ float4 s_rec[3 * 64];  // record j at s_rec[3 j .. 3 j + 2]
   __shared__ __align__(16) float s_ring[kRingSlots * kSlotFloats + kRingPad];
-  const int two_t = 2 * p.num_tiles;
-  const int seg = xcd_grid(two_t);
+  const int first_units = kFirst * p.num_tiles;
+  const int extra_units = (4 - kFirst) * p.num_tiles;
+  const int seg = xcd_grid(first_units);
   const bool extra = (int)blockIdx.x >= seg;
-  const int unit = xcd_unit(extra ? blockIdx.x - seg : blockIdx.x, two_t);
-  if (unit >= two_t) return;  // segment padding
-  const int tile = unit >> 1;
-  const int sub = (unit & 1) + (extra ? 2 : 0);
+  const int unit = extra ? xcd_unit(blockIdx.x - seg, extra_units) : xcd_unit(blockIdx.x, first_units);
+  if (unit >= (extra ? extra_units : first_units)) return;  // segment padding
+  const int tile = extra ? unit / (4 - kFirst) : unit / kFirst;
+  const int quadrant = extra ? kFirst + unit % (4 - kFirst) : unit % kFirst;
   int2 rg = p.ranges[tile];
   rg.x = imax(0, imin(rg.x, p.num_rendered));
   rg.y = imax(rg.x, imin(rg.y, p.num_rendered));
   if (rg.y - rg.x > p.long_tile)
-    render_bwd_slice<kDepth, 1>(p, tile, sub, s_rec, s_ring);
+    render_bwd_slice<kDepth, 1, 1, false>(p, tile, quadrant, s_rec, s_ring);
+  else if (!extra && kWholeTiles)
+    render_bwd_slice<kDepth, 4, 2, true>(p, tile, 0, s_rec, s_ring);
   else if (!extra)
-    render_bwd_slice<kDepth, 2>(p, tile, sub, s_rec, s_ring);
+    render_bwd_slice<kDepth, 2, 1, false>(p, tile, quadrant, s_rec, s_ring);
 }
 
 struct PreprocessBwdParams {
@@ -895,11 +955,21 @@ extern "C" int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t 
   // four times the mean list length: only tiles that dominate the walk
   const int64_t long_tile = gs::kLongTileFactor * num_rendered / p.num_tiles;
   p.long_tile = long_tile > 0x7fffffffLL ? 0x7fffffff : (int)long_tile;
-  const dim3 grid(2 * gs::xcd_grid(2 * p.num_tiles));
-  if (compute_depth)
-    hipLaunchKernelGGL((gs::render_bwd_kernel<true>), grid, dim3(64), 0, (hipStream_t)stream, p);
-  else
-    hipLaunchKernelGGL((gs::render_bwd_kernel<false>), grid, dim3(64), 0, (hipStream_t)stream, p);
+  const bool whole = num_rendered > gs::kWholeTilePairsPerPoint * (int64_t)num_points;
+  const int first = whole ? 1 : 2;
+  const dim3 grid(gs::xcd_grid(first * p.num_tiles) + gs::xcd_grid((4 - first) * p.num_tiles));
+  const hipStream_t s = (hipStream_t)stream;
+  if (compute_depth) {
+    if (whole)
+      hipLaunchKernelGGL((gs::render_bwd_kernel<true, true>), grid, dim3(64), 0, s, p);
+    else
+      hipLaunchKernelGGL((gs::render_bwd_kernel<true, false>), grid, dim3(64), 0, s, p);
+  } else {
+    if (whole)
+      hipLaunchKernelGGL((gs::render_bwd_kernel<false, true>), grid, dim3(64), 0, s, p);
+    else
+      hipLaunchKernelGGL((gs::render_bwd_kernel<false, false>), grid, dim3(64), 0, s, p);
+  }
   return gs_status_from_hip(hipGetLastError());
 }
 

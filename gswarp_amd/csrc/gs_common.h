@@ -186,19 +186,41 @@ __device__ __forceinline__ float power_cutoff(float opacity) {
 // and b^2 are exact there) for qcut inflated ten times that bound, plus
 // 0.02 px; conics that are not positive definite or so elongated
 // (ac/det >= 1e5) that the bound is weak are never culled.  Returning true
-// is always safe: it only costs the per-pixel test.
-__device__ __forceinline__ bool record_may_touch(float4 r0, float4 r1, float x0, float x1, float y0, float y1) {
+// is always safe: it only costs the per-pixel test.  record_box gives the box
+// (the whole plane for a conic it never culls) and returns false when no
+// pixel can blend the record; record_may_touch tests it against one
+// rectangle.
+__device__ __forceinline__ bool record_box(float4 r0, float4 r1, double& bx0, double& bx1, double& by0,
+                                           double& by1) {
   const float qcut = r1.w;
   if (qcut < 0.0f) return false;  // alpha < 1/255 at every exponent <= 0
   const double a = r0.z, b = r0.w, c = r1.x;
   const double ac = a * c;
   const double det = ac - b * b;
-  if (!(a > 0.0 && c > 0.0 && det > 0.0 && ac < 1.0e5 * det)) return true;
+  if (!(a > 0.0 && c > 0.0 && det > 0.0 && ac < 1.0e5 * det)) {
+    bx0 = by0 = -__builtin_inf();
+    bx1 = by1 = __builtin_inf();
+    return true;
+  }
   const double q = (double)qcut * (1.0 + 8.0e-6 * (ac / det)) + 1.0e-6;
   const double ex = sqrt(q * c / det) + 0.02;
   const double ey = sqrt(q * a / det) + 0.02;
-  const double gx = r0.x, gy = r0.y;
-  return !(gx + ex < (double)x0 || gx - ex > (double)x1 || gy + ey < (double)y0 || gy - ey > (double)y1);
+  bx0 = (double)r0.x - ex;
+  bx1 = (double)r0.x + ex;
+  by0 = (double)r0.y - ey;
+  by1 = (double)r0.y + ey;
+  return true;
+}
+
+// Whether a record_box meets the pixel rectangle [x0, x1] x [y0, y1].
+__device__ __forceinline__ bool box_meets(double bx0, double bx1, double by0, double by1, float x0, float x1,
+                                          float y0, float y1) {
+  return !(bx1 < (double)x0 || bx0 > (double)x1 || by1 < (double)y0 || by0 > (double)y1);
+}
+
+__device__ __forceinline__ bool record_may_touch(float4 r0, float4 r1, float x0, float x1, float y0, float y1) {
+  double bx0, bx1, by0, by1;
+  return record_box(r0, r1, bx0, bx1, by0, by1) && box_meets(bx0, bx1, by0, by1, x0, x1, y0, y1);
 }
 
 // Largest quadratic form q at which alpha can still reach 1/255:
