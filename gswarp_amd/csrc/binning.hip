@@ -75,46 +75,75 @@ __device__ __forceinline__ unsigned wave_max_u32(unsigned v) {
   return v;
 }
 
-// Per block of kScanTile Gaussians: the tile-count sum, and the smallest and
-// largest depth bits of the Gaussians with radius > 0 (min ~0u / max 0 when
-// there are none), packed as max << 32 | min.  With an order, the counts
-// are gathered through it and also stored contiguously in `gathered`, so
-// that the apply pass reads them without a second gather.
+// The scan runs in two passes over blocks of kScanTile = 4096 Gaussians.
+// Thread t of a block owns elements 4t .. 4t + 3 of each of its four
+// 1024-element chunks, so every load and store of a wave covers 1 KB of
+// consecutive elements (16-byte vector accesses when nothing is gathered).
+constexpr int kScanChunk = kScanThreads * 4;
+static_assert(kScanTile == 4 * kScanChunk, "four chunks of four elements per thread");
+
+// The four elements of thread t in chunk k of block `base`, gathered through
+// order when there is one; elements past n are 0.
+__device__ __forceinline__ void scan_load4(const int* __restrict__ in, const int* __restrict__ order, long long i0,
+                                           long long n, bool vec, int (&v)[4], int (&src)[4]) {
+  if (vec && i0 + 3 < n) {
+    const int4 o = order ? *reinterpret_cast<const int4*>(order + i0) : make_int4(0, 0, 0, 0);
+    src[0] = order ? o.x : (int)i0;
+    src[1] = order ? o.y : (int)i0 + 1;
+    src[2] = order ? o.z : (int)i0 + 2;
+    src[3] = order ? o.w : (int)i0 + 3;
+    if (!order) {
+      const int4 x = *reinterpret_cast<const int4*>(in + i0);
+      v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+      return;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) src[j] = i0 + j < n ? (order ? order[i0 + j] : (int)(i0 + j)) : -1;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = src[j] >= 0 ? in[src[j]] : 0;
+}
+
+// Per block: the tile-count sum, and the smallest and largest depth bits of
+// the Gaussians with radius > 0 (min ~0u / max 0 when there are none), packed
+// as max << 32 | min.  With an order, the counts are gathered through it and
+// also stored contiguously in `gathered` (when given), so that the apply pass
+// reads them without a second gather.
 __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(int n, const int* __restrict__ in,
                                                                   const int* __restrict__ order,
                                                                   const int* __restrict__ radii,
                                                                   const float* __restrict__ depths,
                                                                   long long* __restrict__ block_sums,
                                                                   unsigned long long* __restrict__ block_range,
-                                                                  int* __restrict__ gathered) {
+                                                                  int* __restrict__ gathered, int vec) {
   __shared__ long long lds4[kScanThreads / 64];
   __shared__ unsigned s_min[kScanThreads / 64], s_max[kScanThreads / 64];
   const long long base = (long long)blockIdx.x * kScanTile;
   long long s = 0;
   unsigned dmin = ~0u, dmax = 0u;
-  int cnt[kScanItems], rad[kScanItems];
-  unsigned bits[kScanItems];
 #pragma unroll
-  for (int i = 0; i < kScanItems; ++i) {
-    const long long idx = base + (long long)i * kScanThreads + threadIdx.x;
-    cnt[i] = rad[i] = 0;
-    bits[i] = 0u;
-    if (idx < n) {
-      const int src = order ? order[idx] : (int)idx;
-      cnt[i] = in[src];
-      if (gathered) gathered[idx] = cnt[i];
-      if (radii) {
-        rad[i] = radii[src];
-        bits[i] = __float_as_uint(depths[src]);
+  for (int k = 0; k < 4; ++k) {
+    const long long i0 = base + k * kScanChunk + 4 * threadIdx.x;
+    int v[4], src[4];
+    scan_load4(in, order, i0, n, vec != 0, v, src);
+    if (gathered) {
+      if (vec && i0 + 3 < n) {
+        *reinterpret_cast<int4*>(gathered + i0) = make_int4(v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (i0 + j < n) gathered[i0 + j] = v[j];
       }
     }
-  }
 #pragma unroll
-  for (int i = 0; i < kScanItems; ++i) {
-    s += cnt[i];
-    if (rad[i] > 0) {
-      dmin = bits[i] < dmin ? bits[i] : dmin;
-      dmax = bits[i] > dmax ? bits[i] : dmax;
+    for (int j = 0; j < 4; ++j) {
+      s += v[j];
+      if (radii && src[j] >= 0 && radii[src[j]] > 0) {
+        const unsigned bits = __float_as_uint(depths[src[j]]);
+        dmin = bits < dmin ? bits : dmin;
+        dmax = bits > dmax ? bits : dmax;
+      }
     }
   }
   dmin = wave_min_u32(dmin);
@@ -138,72 +167,76 @@ __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(int n, const 
   }
 }
 
-// Single-workgroup exclusive scan of the block sums; stores the total pair
-// count in info[0] and the visible depth-bit range (max << 32 | min, or 0
-// when nothing is visible) in info[1].
-__global__ __launch_bounds__(kScanThreads) void scan_blocks_kernel(int nb, long long* __restrict__ block_sums,
-                                                                  const unsigned long long* __restrict__ block_range,
-                                                                  long long* __restrict__ info) {
+// Inclusive prefix sums of the block's elements: its offset is the sum of the
+// preceding blocks' sums (each block adds them up itself, so no pass runs
+// between the two), then each chunk is scanned and carried into the next.
+// The last block also stores the total pair count in info[0] and the visible
+// depth-bit range (max << 32 | min, or 0 when nothing is visible) in
+// info[1].  Offsets are int32 (meaningful when the total fits).
+__global__ __launch_bounds__(kScanThreads) void scan_apply_kernel(int n, int nb, const int* __restrict__ in,
+                                                                 const int* __restrict__ order,
+                                                                 const long long* __restrict__ block_sums,
+                                                                 const unsigned long long* __restrict__ block_range,
+                                                                 int* __restrict__ out, long long* __restrict__ info,
+                                                                 int vec) {
   __shared__ long long lds4[kScanThreads / 64];
   __shared__ unsigned s_min[kScanThreads / 64], s_max[kScanThreads / 64];
-  long long carry = 0;
+  const int b = blockIdx.x;
+  const bool last = b == nb - 1;
+  long long pre = 0;
   unsigned dmin = ~0u, dmax = 0u;
-  for (int base = 0; base < nb; base += kScanThreads) {
-    const int i = base + threadIdx.x;
-    const long long v = i < nb ? block_sums[i] : 0;
-    if (i < nb) {
-      const unsigned long long r = block_range[i];
+  for (int j = threadIdx.x; j < (last ? nb : b); j += kScanThreads) {
+    if (j < b) pre += block_sums[j];
+    if (last) {
+      const unsigned long long r = block_range[j];
       const unsigned mn = (unsigned)r, mx = (unsigned)(r >> 32);
       dmin = mn < dmin ? mn : dmin;
       dmax = mx > dmax ? mx : dmax;
     }
-    long long tot;
-    const long long ex = block_exclusive_scan_i64(v, lds4, &tot);
-    if (i < nb) block_sums[i] = carry + ex;
-    carry += tot;
   }
-  dmin = wave_min_u32(dmin);
-  dmax = wave_max_u32(dmax);
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
-    s_min[wave] = dmin;
-    s_max[wave] = dmax;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned mn = ~0u, mx = 0u;
-#pragma unroll
-    for (int w = 0; w < kScanThreads / 64; ++w) {
-      mn = s_min[w] < mn ? s_min[w] : mn;
-      mx = s_max[w] > mx ? s_max[w] : mx;
+  long long pre_total;
+  block_exclusive_scan_i64(pre, lds4, &pre_total);
+  if (last) {
+    dmin = wave_min_u32(dmin);
+    dmax = wave_max_u32(dmax);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+      s_min[wave] = dmin;
+      s_max[wave] = dmax;
     }
-    info[0] = carry;
-    info[1] = mx >= mn ? (long long)(((unsigned long long)mx << 32) | mn) : 0;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      unsigned mn = ~0u, mx = 0u;
+#pragma unroll
+      for (int w = 0; w < kScanThreads / 64; ++w) {
+        mn = s_min[w] < mn ? s_min[w] : mn;
+        mx = s_max[w] > mx ? s_max[w] : mx;
+      }
+      info[0] = pre_total + block_sums[b];
+      info[1] = mx >= mn ? (long long)(((unsigned long long)mx << 32) | mn) : 0;
+    }
   }
-}
-
-__global__ __launch_bounds__(kScanThreads) void scan_apply_kernel(int n, const int* __restrict__ in,
-                                                                 const int* __restrict__ order,
-                                                                 const long long* __restrict__ block_offsets,
-                                                                 int* __restrict__ out) {
-  __shared__ long long lds4[kScanThreads / 64];
-  const long long base = (long long)blockIdx.x * kScanTile + (long long)threadIdx.x * kScanItems;
-  int v[kScanItems];
-  long long s = 0;
+  long long carry = pre_total;
+  const long long base = (long long)b * kScanTile;
 #pragma unroll
-  for (int i = 0; i < kScanItems; ++i) {
-    const long long idx = base + i;
-    v[i] = idx < n ? in[order ? order[idx] : (int)idx] : 0;
-  }
+  for (int k = 0; k < 4; ++k) {
+    const long long i0 = base + k * kScanChunk + 4 * threadIdx.x;
+    int v[4], src[4];
+    scan_load4(in, order, i0, n, vec != 0, v, src);
+    v[1] += v[0];
+    v[2] += v[1];
+    v[3] += v[2];
+    long long chunk_total;
+    const long long run = carry + block_exclusive_scan_i64(v[3], lds4, &chunk_total);
+    if (vec && i0 + 3 < n) {
+      *reinterpret_cast<int4*>(out + i0) =
+          make_int4((int)(run + v[0]), (int)(run + v[1]), (int)(run + v[2]), (int)(run + v[3]));
+    } else {
 #pragma unroll
-  for (int i = 0; i < kScanItems; ++i) s += v[i];
-  long long total;
-  long long run = block_offsets[blockIdx.x] + block_exclusive_scan_i64(s, lds4, &total);
-#pragma unroll
-  for (int i = 0; i < kScanItems; ++i) {
-    const long long idx = base + i;
-    run += v[i];
-    if (idx < n) out[idx] = (int)run;
+      for (int j = 0; j < 4; ++j)
+        if (i0 + j < n) out[i0 + j] = (int)(run + v[j]);
+    }
+    carry += chunk_total;
   }
 }
 
@@ -646,6 +679,13 @@ extern "C" const char* gs_status_string(int status) {
 
 static inline int gs_scan_blocks(int32_t P) { return (P + gs::kScanTile - 1) / gs::kScanTile; }
 
+// 16-byte vector accesses need every contiguous array 16-byte aligned.
+static inline int gs_scan_vec(const void* in, const void* order, const void* out, const void* gathered) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(order) |
+                      reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(gathered);
+  return (a & 15) == 0 ? 1 : 0;
+}
+
 // Scratch: the block sums and depth ranges, then room for the counts
 // gathered in the given order.
 static inline size_t gs_scan_block_bytes(int32_t P) {
@@ -672,12 +712,12 @@ extern "C" int gs_scan_tiles(int32_t P, const int32_t* tiles_touched, const int3
   long long* block_sums = reinterpret_cast<long long*>(scratch);
   unsigned long long* block_range = reinterpret_cast<unsigned long long*>(block_sums + nb);
   int* gathered = order ? reinterpret_cast<int*>(static_cast<char*>(scratch) + gs_scan_block_bytes(P)) : nullptr;
+  const int vec = gs_scan_vec(tiles_touched, order, offsets, gathered);
   hipLaunchKernelGGL(gs::scan_reduce_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, tiles_touched, order,
-                     radii, depths, block_sums, block_range, gathered);
-  hipLaunchKernelGGL(gs::scan_blocks_kernel, dim3(1), dim3(gs::kScanThreads), 0, s, nb, block_sums, block_range,
-                     reinterpret_cast<long long*>(info_dev));
-  hipLaunchKernelGGL(gs::scan_apply_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P,
-                     gathered ? gathered : tiles_touched, nullptr, block_sums, offsets);
+                     radii, depths, block_sums, block_range, gathered, vec);
+  hipLaunchKernelGGL(gs::scan_apply_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, nb,
+                     gathered ? gathered : tiles_touched, nullptr, block_sums, block_range, offsets,
+                     reinterpret_cast<long long*>(info_dev), vec);
   return gs_status_from_hip(hipGetLastError());
 }
 
@@ -743,12 +783,11 @@ extern "C" int gs_scan_tiles_static(int32_t P, const int32_t* tiles_touched, con
   const int nb = gs_scan_blocks(P);
   long long* block_sums = static_cast<long long*>(base);
   unsigned long long* block_range = reinterpret_cast<unsigned long long*>(block_sums + nb);
+  const int vec = gs_scan_vec(tiles_touched, order, offsets, nullptr);
   hipLaunchKernelGGL(gs::scan_reduce_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, tiles_touched, order,
-                     radii, depths, block_sums, block_range, nullptr);
-  hipLaunchKernelGGL(gs::scan_blocks_kernel, dim3(1), dim3(gs::kScanThreads), 0, s, nb, block_sums, block_range,
-                     reinterpret_cast<long long*>(info_dev));
-  hipLaunchKernelGGL(gs::scan_apply_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, tiles_touched, order,
-                     block_sums, offsets);
+                     radii, depths, block_sums, block_range, nullptr, vec);
+  hipLaunchKernelGGL(gs::scan_apply_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, nb, tiles_touched, order,
+                     block_sums, block_range, offsets, reinterpret_cast<long long*>(info_dev), vec);
   return gs_status_from_hip(hipGetLastError());
 }
 
