@@ -98,7 +98,8 @@ def sort_passes(tiles: int) -> int:
 def algorithmic_bytes(N: int, R: float, P: int, T: int, dataflow: str, flow_k: int = 0) -> dict:
     """Bytes crossing each stage boundary once (the SH3, depth-on accounting of the
     reference dataflow): preprocess 112N + SH 228N, scan 8N, duplicate 44N + 12R
-    (64-bit key + value) or 44N + 8R (tile id + value), ranges 8R + 8T, render
+    (64-bit key + value) or 44N + 8R (tile id + value), ranges 8R + 8T (4R + 8T
+    over the depth-then-tile dataflow's 32-bit tile ids), render
     44R + 24P + 8T, render backward 44R + 28P + 40N + 8T, SH + preprocess
     backward 624N.  Sorts: the one 64-bit key sort moves 24R per pass over
     ceil((32 + ceil(log2 T)) / 8) passes; the depth-then-tile dataflow moves 16N
@@ -120,6 +121,7 @@ def algorithmic_bytes(N: int, R: float, P: int, T: int, dataflow: str, flow_k: i
         out["duplicate"] = 44.0 * N + 8.0 * R
         out["depth_sort"] = 4 * 16.0 * N
         out["sort"] = math.ceil((T - 1).bit_length() / 8) * 16.0 * R
+        out["ranges"] = 4.0 * R + 8.0 * T  # the sorted 32-bit tile ids, not 64-bit keys
     return out
 
 
