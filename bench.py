@@ -226,28 +226,36 @@ def _stats_commands(config: int) -> list[str]:
     ]
 
 
-PROFILE_COMMANDS = {
-    "stats": _stats_commands(2),
-    "pmc": [
+def _pmc_commands(config: int) -> list[str]:
+    c = f"c{config}"
+    cfg = "" if config == 2 else f"--config {config} "
+    run = f"python3 $R/bench.py {cfg}--steps 3 --warmup 1 --no-cpu-baseline --no-stage-timing"
+    return [
         _PROFILE_PREAMBLE,
-        "#   rocprofv3 --pmc FETCH_SIZE --output-format csv -d $R/gpurun_out/pmc_c2 -o fetch -- \\",
-        "#       python3 $R/bench.py --steps 3 --warmup 1 --no-cpu-baseline --no-stage-timing",
-        "#   rocprofv3 --pmc WRITE_SIZE --output-format csv -d $R/gpurun_out/pmc_c2 -o write -- \\",
-        "#       python3 $R/bench.py --steps 3 --warmup 1 --no-cpu-baseline --no-stage-timing",
-        "#   python3 bench.py --pmc-summary gpurun_out/pmc_c2/fetch_counter_collection.csv \\",
-        "#       gpurun_out/pmc_c2/write_counter_collection.csv profiles/traffic_config2.txt",
-    ],
-    "sq": [
+        f"#   rocprofv3 --pmc FETCH_SIZE --output-format csv -d $R/gpurun_out/pmc_{c} -o fetch -- \\",
+        f"#       {run}",
+        f"#   rocprofv3 --pmc WRITE_SIZE --output-format csv -d $R/gpurun_out/pmc_{c} -o write -- \\",
+        f"#       {run}",
+        f"#   python3 bench.py --pmc-summary gpurun_out/pmc_{c}/fetch_counter_collection.csv \\",
+        f"#       gpurun_out/pmc_{c}/write_counter_collection.csv profiles/traffic_config{config}.txt"
+        + ("" if config == 2 else f" --profile-config {config}"),
+    ]
+
+
+def _sq_commands(config: int) -> list[str]:
+    c = f"c{config}"
+    cfg = "" if config == 2 else f"--config {config} "
+    return [
         _PROFILE_PREAMBLE,
         "#   rocprofv3 --pmc SQ_WAVES SQ_INSTS_VALU SQ_ACTIVE_INST_VALU SQ_INSTS_LDS SQ_ACTIVE_INST_LDS \\",
-        "#       SQ_LDS_BANK_CONFLICT SQ_WAVE_CYCLES SQ_BUSY_CYCLES --output-format csv -d $R/gpurun_out/sq_c2 -o sq -- \\",
-        "#       python3 $R/bench.py --steps 3 --warmup 1 --no-cpu-baseline --no-stage-timing",
-        "#   python3 bench.py --sq-summary gpurun_out/sq_c2/sq_counter_collection.csv profiles/sq_counters_config2.txt",
-    ],
-}
+        f"#       SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_BUSY_CYCLES --output-format csv -d $R/gpurun_out/sq_{c} -o sq -- \\",
+        f"#       python3 $R/bench.py {cfg}--steps 3 --warmup 1 --no-cpu-baseline --no-stage-timing",
+        f"#   python3 bench.py --sq-summary gpurun_out/sq_{c}/sq_counter_collection.csv "
+        f"profiles/sq_counters_config{config}.txt" + ("" if config == 2 else f" --profile-config {config}"),
+    ]
 
 
-def summarize_pmc(fetch_csv: str, write_csv: str, out_path: str, copy_bytes: int = 1 << 30) -> None:
+def summarize_pmc(fetch_csv: str, write_csv: str, out_path: str, copy_bytes: int = 1 << 30, config: int = 2) -> None:
     """Turn two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE, then WRITE_SIZE,
     both in KiB per dispatch) into per-stage HBM bytes per launch.  Each counter is
     scaled by what it reads for the calibration copy (the largest device copy, of
@@ -275,13 +283,13 @@ def summarize_pmc(fetch_csv: str, write_csv: str, out_path: str, copy_bytes: int
     f_scale = copy_bytes / fetch_copy
     w_scale = copy_bytes / write_copy
     lines = [
-        "# HBM traffic per launch of each stage (bytes), config 2, from rocprofv3 --pmc",
+        f"# HBM traffic per launch of each stage (bytes), {CONFIG_TITLES[config]}, from rocprofv3 --pmc",
         f"# FETCH_SIZE scale {f_scale:.2f} B/unit, WRITE_SIZE scale {w_scale:.2f} B/unit "
         f"(calibration copy of {copy_bytes} B read + {copy_bytes} B written read "
         f"{fetch_copy:.0f} / {write_copy:.0f} units)",
         f"# iterations averaged: {iters} (fetch run), {iters_w} (write run)",
         "# commands:",
-        *PROFILE_COMMANDS["pmc"],
+        *_pmc_commands(config),
         "# format: '<stage>: <bytes per launch> fetch <bytes> write <bytes>' (bench.py reads the first number)",
     ]
     for stage in sorted(set(fetch) | set(write)):
@@ -292,10 +300,11 @@ def summarize_pmc(fetch_csv: str, write_csv: str, out_path: str, copy_bytes: int
     print("\n".join(lines))
 
 
-def summarize_sq(counter_csv: str, out_path: str) -> None:
+def summarize_sq(counter_csv: str, out_path: str, config: int = 2) -> None:
     """Per-kernel means per dispatch of the SQ counters in one rocprofv3 --pmc
-    counter_collection.csv, with the LDS bank-conflict rate
-    (SQ_LDS_BANK_CONFLICT / SQ_ACTIVE_INST_LDS, both in cycles) and VALU
+    counter_collection.csv, with the LDS bank-conflict rate in conflict cycles
+    per LDS access cycle, SQ_LDS_BANK_CONFLICT / (SQ_LDS_IDX_ACTIVE -
+    SQ_LDS_BANK_CONFLICT) (rocprofv3's LdsBankConflict), and VALU
     instructions per wave."""
     import csv
 
@@ -309,16 +318,18 @@ def summarize_sq(counter_csv: str, out_path: str) -> None:
         per[short][r["Counter_Name"]] += float(r["Counter_Value"])
         dispatches[short].add(r["Dispatch_Id"])
     counters = sorted({c for d in per.values() for c in d})
-    lines = ["# SQ counters per kernel, config 2 (1M Gaussians, 1920x1080, SH3, fwd+bwd), one MI355X",
-             "# commands:", *PROFILE_COMMANDS["sq"],
-             "# lds_conflict_rate = SQ_LDS_BANK_CONFLICT / SQ_ACTIVE_INST_LDS (cycles per LDS-active cycle)",
+    lines = [f"# SQ counters per kernel, {CONFIG_TITLES[config]}, one MI355X",
+             "# commands:", *_sq_commands(config),
+             "# lds_conflict_rate = SQ_LDS_BANK_CONFLICT / (SQ_LDS_IDX_ACTIVE - SQ_LDS_BANK_CONFLICT) "
+             "(conflict cycles per LDS access cycle)",
              "# SQ counters per dispatch (mean); columns: kernel, dispatches, "
              + ", ".join(counters) + ", lds_conflict_rate, valu_insts_per_wave"]
     for k in sorted(per):
         n = len(dispatches[k])
         d = {c: per[k][c] / n for c in counters}
-        lds = d.get("SQ_ACTIVE_INST_LDS", 0.0)
-        rate = d.get("SQ_LDS_BANK_CONFLICT", 0.0) / lds if lds else 0.0
+        conflict = d.get("SQ_LDS_BANK_CONFLICT", 0.0)
+        access = d.get("SQ_LDS_IDX_ACTIVE", 0.0) - conflict
+        rate = conflict / access if access > 0 else 0.0
         waves = d.get("SQ_WAVES", 0.0)
         vpw = d.get("SQ_INSTS_VALU", 0.0) / waves if waves else 0.0
         lines.append(f"{k} {n} " + " ".join(f"{d[c]:.4g}" for c in counters) + f" {rate:.4f} {vpw:.1f}")
@@ -489,7 +500,7 @@ def main() -> int:
     parser.add_argument("--sq-summary", nargs=2, metavar=("COUNTER_CSV", "OUT"),
                         help="summarise one rocprofv3 --pmc run of SQ counters into OUT and exit")
     parser.add_argument("--profile-config", type=int, default=2, choices=(1, 2, 3, 4),
-                        help="configuration a --stats-summary run profiled (for its header)")
+                        help="configuration a --stats-summary, --pmc-summary or --sq-summary run profiled")
     parser.add_argument("--stats-summary", nargs="+", metavar="PATH",
                         help="KERNEL_STATS_CSV OUT [BENCH_ERR]: summarise one rocprofv3 --kernel-trace --stats "
                              "run into OUT and exit")
@@ -498,10 +509,10 @@ def main() -> int:
         summarize_stats(*args.stats_summary, config=args.profile_config)
         return 0
     if args.sq_summary:
-        summarize_sq(*args.sq_summary)
+        summarize_sq(*args.sq_summary, config=args.profile_config)
         return 0
     if args.pmc_summary:
-        summarize_pmc(*args.pmc_summary)
+        summarize_pmc(*args.pmc_summary, config=args.profile_config)
         return 0
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
