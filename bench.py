@@ -135,15 +135,17 @@ def visited_pairs(n_contrib, width: int, height: int) -> int:
     return int(F.max_pool2d(t, 16, stride=16, ceil_mode=True).double().sum().item())
 
 
-def early_stop_share(alpha, width: int, height: int) -> float:
-    """Share of the forward's 16x4 pixel slices that may have stopped before the
-    end of their tile's list: every pixel has alpha > 0.99 (a pixel stops when
-    T would fall below 1e-4, and alpha is at most 0.99 per Gaussian, so it
-    stops only with T < 1e-2).  Where this is 0 the forward reads all R pairs."""
+def early_stop_share(alpha, width: int, height: int, flow: bool = False) -> float:
+    """Share of the forward's pixel slices (8x8 quadrants; 16x4 rows for the
+    flow variant) that may have stopped before the end of their tile's list:
+    every pixel has alpha > 0.99 (a pixel stops when T would fall below 1e-4,
+    and alpha is at most 0.99 per Gaussian, so it stops only with T < 1e-2).
+    Where this is 0 the forward reads all R pairs."""
     import torch.nn.functional as F
 
     a = alpha.reshape(1, 1, height, width)
-    lowest = -F.max_pool2d(-a, (4, 16), stride=(4, 16), ceil_mode=True)
+    window = (4, 16) if flow else (8, 8)
+    lowest = -F.max_pool2d(-a, window, stride=window, ceil_mode=True)
     return float((lowest > 0.99).double().mean().item())
 
 
@@ -625,7 +627,7 @@ def main() -> int:
     step_events[:] = fwd_bwd_events
     visited = [visited_pairs(nc, W, H) for nc in timer.notes.pop("n_contrib", [])]
     R_visited = sum(visited) / len(visited) if visited else None
-    stopped = [early_stop_share(a, W, H) for a in timer.notes.pop("alpha", [])]
+    stopped = [early_stop_share(a, W, H, flow) for a in timer.notes.pop("alpha", [])]
     early_share = sum(stopped) / len(stopped) if stopped else 0.0
     # Run-to-run repeatability of the iteration-0 view (the float atomics of the
     # backward add in an unspecified order), and its outputs for the parity check.

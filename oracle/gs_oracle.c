@@ -15,14 +15,20 @@
  * (warp-lang is absent).  This oracle evaluates them with its own
  * published-method routines: exp by Cody–Waite reduction and the degree-7
  * Taylor polynomial, ln by the atanh series in s = (m-1)/(m+1); both are
- * checked against libm in double precision by tests/test_oracle_pins.py.
+ * checked against libm in double precision by tests/test_oracle_pipeline.py
+ * (test_exp_matches_libm, test_log_matches_libm).
  *
  * Differences from the reference that do not change results:
  *  - binning follows the reference's own dataflow: stable depth sort of all
  *    points, inclusive scan of tiles_touched in depth order, duplicate in
  *    depth order, stable tile sort (binning_ops.py:152-343);
  *  - render backward gradients are accumulated in double precision (the
- *    reference accumulates fp32 atomics in unspecified order).
+ *    reference accumulates fp32 atomics in unspecified order); alongside
+ *    them or_render_bwd can carry a first-order running error bound per
+ *    gradient element (Wilkinson-style: each rounding contributes at most
+ *    u = 2^-24 of its result's magnitude), which the tests use as the
+ *    per-element tolerance for the GPU's different but equally valid fp32
+ *    evaluation order.
  */
 #include <math.h>
 #include <stdint.h>

@@ -5,6 +5,11 @@ lists and tile ranges bit-exact; colour / depth / alpha within 1e-4
 absolute; flow top-K ids exact; gradients within 1e-3 relative + 1e-5
 absolute plus, per element, twice the oracle's bound on the fp32 rounding of
 that element's sum of per-pixel terms (helpers.grad_mismatch).
+
+The forward kernels evaluate every fp32 expression in the oracle's order
+with the same exp/log, so the forward is asserted stricter than the bar:
+colour, depth, alpha and the flow weights / x_mu equal the oracle's bit for
+bit (EXACT_FORWARD).
 """
 
 from __future__ import annotations
@@ -28,6 +33,7 @@ CASES = {
 }
 
 COLOR_ATOL = 1e-4
+EXACT_FORWARD = True
 
 
 def _scene(name, device, seed=0):
@@ -66,13 +72,16 @@ def _check_forward(scene, opts, *, coverage_mode=1, flow=False, top_k=0, colors=
     assert np.array_equal(to_np(bins.ranges), rb["ranges"])
     # render
     assert np.array_equal(to_np(res.n_contrib).reshape(rf["n_contrib"].shape), rf["n_contrib"])
-    for key, t in (("color", res.color), ("depth", res.depth), ("alpha", res.alpha)):
-        err = float(np.abs(to_np(t) - rf[key]).max())
-        assert err <= COLOR_ATOL, (key, err)
+    floats = [("color", res.color, rf["color"]), ("depth", res.depth, rf["depth"]), ("alpha", res.alpha, rf["alpha"])]
     if flow and top_k:
         assert np.array_equal(to_np(res.aux[0]), rf["gs_per_pixel"])
-        assert float(np.abs(to_np(res.aux[1]) - rf["weight_per_gs_pixel"]).max()) <= COLOR_ATOL
-        assert float(np.abs(to_np(res.aux[2]) - rf["x_mu"]).max()) <= COLOR_ATOL
+        floats += [("weights", res.aux[1], rf["weight_per_gs_pixel"]), ("x_mu", res.aux[2], rf["x_mu"])]
+    for key, t, expected in floats:
+        got = to_np(t)
+        err = float(np.abs(got - expected).max()) if got.size else 0.0
+        assert err <= COLOR_ATOL, (key, err)
+        if EXACT_FORWARD:
+            assert np.array_equal(got, expected), (key, err)
     return out, host, ref
 
 
