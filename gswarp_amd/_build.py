@@ -19,7 +19,7 @@ PACKAGE_DIR = Path(__file__).resolve().parent
 CSRC_DIR = PACKAGE_DIR / "csrc"
 LIB_NAME = "libgswarp_hip.so"
 LIB_PATH = PACKAGE_DIR / LIB_NAME
-SOURCES = ("preprocess.hip", "binning.hip", "sort.hip", "render.hip", "backward.hip")
+SOURCES = ("preprocess.hip", "binning.hip", "buckets.hip", "sort.hip", "render.hip", "backward.hip")
 OFFLOAD_ARCH = "gfx950"
 
 HIPCC_FLAGS = (

@@ -194,6 +194,9 @@ def preprocess(inputs: RasterInputs, options: ExecutionOptions, *, pack: bool = 
         geom=geom,
         coverage=torch.empty((P, 4), dtype=torch.int32, device=device),
     )
+    if buckets_possible(options, W, H):
+        # the bucketed binning reads the banded Gaussians' coverage bands instead of recomputing them
+        out.band_store = torch.empty((max(int(lib.gs_band_store_words(P)), 1),), dtype=torch.int32, device=device)
     colors = _f32c(inputs.colors) if inputs.colors.numel() != 0 else None
     shs = None
     K = 0
@@ -220,8 +223,16 @@ def preprocess(inputs: RasterInputs, options: ExecutionOptions, *, pack: bool = 
             out.depths.data_ptr(),
             out.proj_2d.data_ptr(), out.conic_2d.data_ptr(), out.conic_2d_inv.data_ptr(),
             out.tiles_touched.data_ptr(), out.coverage.data_ptr(), out.records.data_ptr(), out.clamped.data_ptr(),
-            _stream(device))
+            _lib.ptr(out.band_store), _stream(device))
     return out
+
+
+def buckets_possible(options: ExecutionOptions, image_width: int, image_height: int) -> bool:
+    """Whether the binning may take the bucketed dataflow: the default sort mode
+    with it selected, on images of at most BUCKET_MAX_GRID tiles per side."""
+    grid_x, grid_y = grid_dims(image_width, image_height)
+    return (options.binning_sort_mode == "warp_depth_stable_tile" and HEAVY_DATAFLOW == "buckets"
+            and grid_x <= BUCKET_MAX_GRID and grid_y <= BUCKET_MAX_GRID)
 
 
 def key_layout(P: int, T: int, depth_min: int, depth_max: int) -> KeyLayout:
@@ -240,9 +251,18 @@ def key_layout(P: int, T: int, depth_min: int, depth_max: int) -> KeyLayout:
 # (gs_sort_tile_segments); "full" runs the radix sort over tile and depth bits.
 PACKED_SORT = "segmented"
 
-# Above this many pairs per Gaussian the default mode sorts Gaussians by depth
-# and then pairs by tile (two short sorts) instead of one 64-bit key per pair.
+# Above this many pairs per Gaussian the default mode sorts the Gaussians by
+# depth and builds the tile lists from that order instead of sorting one
+# 64-bit key per pair.
 DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN = 4
+
+# How the default mode builds the lists above that ratio: "buckets" writes
+# each pair once through 8 x 8-tile squares (gs_bin_buckets); "depth_tile"
+# emits (tile, point) pairs in depth order and sorts them by tile, the
+# reference's dataflow (also the fallback when the image or a Gaussian's
+# tile rectangle is too large for the bucketed binning's cover words).
+HEAVY_DATAFLOW = "buckets"
+BUCKET_MAX_GRID = 255  # tiles per image side the bucketed binning takes
 
 
 def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options: ExecutionOptions,
@@ -274,11 +294,20 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
     T = grid_x * grid_y
     stream = _stream(device)
     offsets = torch.empty((P,), dtype=torch.int32, device=device)
-    info = torch.empty((2,), dtype=torch.int64, device=device)
+    info = torch.empty((4,), dtype=torch.int64, device=device)
     scan_scratch = torch.empty((max(int(lib.gs_scan_scratch_bytes(P)), 1),), dtype=torch.uint8, device=device)
+    # the default mode's scan also sizes the bucketed binning (entries and
+    # valid Gaussians in info[2] and info[3]) for the case of many pairs per Gaussian
+    sized = buckets_possible(options, image_width, image_height) and pre.coverage is not None
     with _stage("scan"):
-        lib.call("gs_scan_tiles", P, pre.tiles_touched.data_ptr(), None, pre.radii.data_ptr(), pre.depths.data_ptr(),
-                 offsets.data_ptr(), info.data_ptr(), scan_scratch.data_ptr(), scan_scratch.numel(), stream)
+        if sized:
+            lib.call("gs_scan_tiles_entries", P, pre.tiles_touched.data_ptr(), pre.radii.data_ptr(),
+                     pre.depths.data_ptr(), pre.coverage.data_ptr(), offsets.data_ptr(), info.data_ptr(),
+                     scan_scratch.data_ptr(), scan_scratch.numel(), stream)
+        else:
+            lib.call("gs_scan_tiles", P, pre.tiles_touched.data_ptr(), None, pre.radii.data_ptr(),
+                     pre.depths.data_ptr(), offsets.data_ptr(), info.data_ptr(), scan_scratch.data_ptr(),
+                     scan_scratch.numel(), stream)
     pinned = _workspace.readback_buffer(device, torch.cuda.current_stream(device))
     capacity = _workspace.pair_capacity(device) if (not pack and not keep_keys and mode != "torch"
                                                     and PACKED_SORT == "segmented" and P > 0) else 0
@@ -317,13 +346,16 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
         # declined: release the provisioned buffers before the exact-size binning allocates its own
         del ws, result, events
         point_list = ranges = None
+        if sized:  # the fast path read back two values only
+            lib.call("gs_info_readback", info.data_ptr(), pinned.data_ptr(), 4, stream)
     else:
         point_list = ranges = None
-        lib.call("gs_num_rendered_readback", info.data_ptr(), pinned.data_ptr(), stream)
+        lib.call("gs_info_readback", info.data_ptr(), pinned.data_ptr(), 4 if sized else 2, stream)
         R = validate_pair_count(int(pinned[0]))
         depth_range = int(pinned[1]) & 0xFFFFFFFFFFFFFFFF
         _workspace.note_pairs(device, R)
         _note("num_rendered", R)
+    entries, valid_points = (int(pinned[2]), int(pinned[3])) if sized else (-1, 0)
     buffer = None
     if pack:
         buffer, point_list, ranges = _packing.allocate_binning(R, T, device)
@@ -338,6 +370,10 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
                                 and R <= DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN * P):
         _note("binning_dataflow", "packed_key")
         bins = _binning_packed(pre, image_width, image_height, offsets, R, layout, keep_keys, point_list, ranges)
+    elif sized and 0 <= entries <= MAX_BINNING_PAIRS:
+        _note("binning_dataflow", "buckets")
+        bins = _binning_buckets(pre, image_width, image_height, R, entries, valid_points,
+                                depth_range & 0xFFFFFFFF, depth_range >> 32, keep_keys, ranges)
     else:
         _note("binning_dataflow", "depth_then_tile")
         bins = _binning_depth_tile(pre, image_width, image_height, R, keep_keys, mode == "torch", ranges)
@@ -417,6 +453,35 @@ def _binning_depth_tile(pre: PreprocessOutputs, image_width: int, image_height: 
         keys = (tiles.to(torch.int64) << 32) | (pre.depths.view(torch.int32)[vals.long()].to(torch.int64)
                                                 & 0xFFFFFFFF)
     return BinningState(grid_x, grid_y, vals, ranges, R, keys, KeyLayout(depth_min=0, depth_bits=32, value_bits=0))
+
+
+def _binning_buckets(pre: PreprocessOutputs, image_width: int, image_height: int, R: int, entries: int,
+                     valid_points: int, depth_min: int, depth_max: int, keep_keys: bool,
+                     ranges: torch.Tensor | None = None) -> BinningState:
+    """Depth order of the Gaussians, then per 8 x 8-tile square entries with
+    tile masks, then the tile lists, each pair written once (gs_bin_buckets):
+    the lists and ranges of binning_ops.py:152-431."""
+    lib = _lib.load()
+    device = pre.radii.device
+    P = pre.radii.shape[0]
+    grid_x, grid_y = grid_dims(image_width, image_height)
+    T = grid_x * grid_y
+    stream = _stream(device)
+    point_list = torch.empty((R,), dtype=torch.int32, device=device)
+    if ranges is None:
+        ranges = torch.empty((T, 2), dtype=torch.int32, device=device)
+    nbytes = int(lib.gs_bin_buckets_workspace_bytes(P, valid_points, entries, image_width, image_height))
+    ws = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=device)
+    events = _stage_chain(("depth_sort", "bucket", "bucket_tiles"))
+    lib.call("gs_bin_buckets", P, valid_points, entries, R, pre.depths.data_ptr(), depth_min, depth_max,
+             pre.coverage.data_ptr(), _lib.ptr(pre.band_store), pre.records.data_ptr(), image_width, image_height,
+             ws.data_ptr(), ws.numel(), ranges.data_ptr(), point_list.data_ptr(), events, stream)
+    keys = None
+    if keep_keys:  # tile << 32 | depth bits, for tests
+        lengths = (ranges[:, 1] - ranges[:, 0]).long()
+        tiles = torch.repeat_interleave(torch.arange(T, device=device, dtype=torch.int64), lengths)
+        keys = (tiles << 32) | (pre.depths.view(torch.int32)[point_list.long()].to(torch.int64) & 0xFFFFFFFF)
+    return BinningState(grid_x, grid_y, point_list, ranges, R, keys, KeyLayout(depth_min=0, depth_bits=32, value_bits=0))
 
 
 def _binning_packed(pre: PreprocessOutputs, image_width: int, image_height: int, offsets: torch.Tensor, R: int,

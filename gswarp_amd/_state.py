@@ -25,6 +25,7 @@ class PreprocessOutputs:
     coverage_mode: int = 1
     geom: torch.Tensor | None = None  # raw-ABI byte buffer that records and clamped are views of
     coverage: torch.Tensor | None = None  # (N, 4) int32 cover words for the emission, or None (re-derived)
+    band_store: torch.Tensor | None = None  # int32 coverage bands of the banded Gaussians, or None
 
 
 @dataclass(slots=True)

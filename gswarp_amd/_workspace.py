@@ -40,7 +40,9 @@ def device_lock(device: torch.device) -> threading.RLock:
 
 
 def readback_buffer(device: torch.device, stream: torch.cuda.Stream) -> torch.Tensor:
-    """Pinned int64[2] host buffer owned by (device, stream)."""
+    """Pinned int64[4] host buffer owned by (device, stream): the pair count,
+    the visible depth-bit range and the bucketed binning's entry and valid
+    Gaussian counts."""
     global _evictions
     index = device.index if device.index is not None else torch.cuda.current_device()
     key = (index, stream.cuda_stream)
@@ -55,7 +57,7 @@ def readback_buffer(device: torch.device, stream: torch.cuda.Stream) -> torch.Te
             old = _entries.pop(victim)
             old["stream"].synchronize()
             _evictions += 1
-        entry = {"pinned": torch.zeros(2, dtype=torch.int64, pin_memory=True), "stream": stream}
+        entry = {"pinned": torch.zeros(4, dtype=torch.int64, pin_memory=True), "stream": stream}
         _entries[key] = entry
         return entry["pinned"]
 

@@ -116,17 +116,33 @@ __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(int n, const 
                                                                   const float* __restrict__ depths,
                                                                   long long* __restrict__ block_sums,
                                                                   unsigned long long* __restrict__ block_range,
-                                                                  int* __restrict__ gathered, int vec) {
+                                                                  int* __restrict__ gathered, int vec,
+                                                                  const int4* __restrict__ coverage,
+                                                                  long long* __restrict__ block_ev) {
   __shared__ long long lds4[kScanThreads / 64];
   __shared__ unsigned s_min[kScanThreads / 64], s_max[kScanThreads / 64];
   const long long base = (long long)blockIdx.x * kScanTile;
   long long s = 0;
   unsigned dmin = ~0u, dmax = 0u;
+  long long units = 0;  // with coverage: super-tile units of the block's valid words
+  int valid = 0, bad = 0;  // valid words; Gaussians with tiles but no valid word
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const long long i0 = base + k * kScanChunk + 4 * threadIdx.x;
     int v[4], src[4];
     scan_load4(in, order, i0, n, vec != 0, v, src);
+    if (coverage) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (i0 + j < n) {
+          const CoverWord w = unpack_cover(coverage[i0 + j]);
+          const int u = super_units(w);
+          units += u;
+          valid += w.valid;
+          bad |= (v[j] > 0 && !w.valid) ? 1 : 0;
+        }
+      }
+    }
     if (gathered) {
       if (vec && i0 + 3 < n) {
         *reinterpret_cast<int4*>(gathered + i0) = make_int4(v[0], v[1], v[2], v[3]);
@@ -155,6 +171,16 @@ __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(int n, const 
   }
   long long total;
   block_exclusive_scan_i64(s, lds4, &total);  // its barriers also order s_min / s_max
+  if (coverage) {
+    long long units_total, valid_total, bad_total;
+    block_exclusive_scan_i64(units, lds4, &units_total);
+    block_exclusive_scan_i64(valid, lds4, &valid_total);
+    block_exclusive_scan_i64(bad, lds4, &bad_total);
+    if (threadIdx.x == 0) {
+      block_ev[2 * blockIdx.x] = bad_total > 0 ? -1 : units_total;
+      block_ev[2 * blockIdx.x + 1] = valid_total;
+    }
+  }
   if (threadIdx.x == 0) {
     block_sums[blockIdx.x] = total;
     unsigned mn = ~0u, mx = 0u;
@@ -172,13 +198,16 @@ __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(int n, const 
 // between the two), then each chunk is scanned and carried into the next.
 // The last block also stores the total pair count in info[0] and the visible
 // depth-bit range (max << 32 | min, or 0 when nothing is visible) in
-// info[1].  Offsets are int32 (meaningful when the total fits).
+// info[1].  Offsets are int32 (meaningful when the total fits).  With
+// block_ev (the reduce pass's per-block super-tile units and valid words) it
+// also stores info[2] = the total units (-1 when a Gaussian with tiles has no
+// valid cover word) and info[3] = the number of valid words.
 __global__ __launch_bounds__(kScanThreads) void scan_apply_kernel(int n, int nb, const int* __restrict__ in,
                                                                  const int* __restrict__ order,
                                                                  const long long* __restrict__ block_sums,
                                                                  const unsigned long long* __restrict__ block_range,
                                                                  int* __restrict__ out, long long* __restrict__ info,
-                                                                 int vec) {
+                                                                 int vec, const long long* __restrict__ block_ev) {
   __shared__ long long lds4[kScanThreads / 64];
   __shared__ unsigned s_min[kScanThreads / 64], s_max[kScanThreads / 64];
   const int b = blockIdx.x;
@@ -214,6 +243,23 @@ __global__ __launch_bounds__(kScanThreads) void scan_apply_kernel(int n, int nb,
       }
       info[0] = pre_total + block_sums[b];
       info[1] = mx >= mn ? (long long)(((unsigned long long)mx << 32) | mn) : 0;
+    }
+    if (block_ev) {
+      long long units = 0, valid = 0, bad = 0;
+      for (int j = threadIdx.x; j < nb; j += kScanThreads) {
+        const long long u = block_ev[2 * j];
+        bad += u < 0 ? 1 : 0;
+        units += u < 0 ? 0 : u;
+        valid += block_ev[2 * j + 1];
+      }
+      long long units_total, valid_total, bad_total;
+      block_exclusive_scan_i64(units, lds4, &units_total);
+      block_exclusive_scan_i64(valid, lds4, &valid_total);
+      block_exclusive_scan_i64(bad, lds4, &bad_total);
+      if (threadIdx.x == 0) {
+        info[2] = bad_total > 0 ? -1 : units_total;
+        info[3] = valid_total;
+      }
     }
   }
   long long carry = pre_total;
@@ -714,11 +760,54 @@ extern "C" int gs_scan_tiles(int32_t P, const int32_t* tiles_touched, const int3
   int* gathered = order ? reinterpret_cast<int*>(static_cast<char*>(scratch) + gs_scan_block_bytes(P)) : nullptr;
   const int vec = gs_scan_vec(tiles_touched, order, offsets, gathered);
   hipLaunchKernelGGL(gs::scan_reduce_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, tiles_touched, order,
-                     radii, depths, block_sums, block_range, gathered, vec);
+                     radii, depths, block_sums, block_range, gathered, vec, nullptr, nullptr);
   hipLaunchKernelGGL(gs::scan_apply_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, nb,
                      gathered ? gathered : tiles_touched, nullptr, block_sums, block_range, offsets,
-                     reinterpret_cast<long long*>(info_dev), vec);
+                     reinterpret_cast<long long*>(info_dev), vec, nullptr);
   return gs_status_from_hip(hipGetLastError());
+}
+
+// The point-order scan with the bucketed binning's sizes: the reduce pass
+// also sums each valid cover word's super-tile count and counts the valid
+// words (block_ev, 16 bytes per block, in the scratch region that the
+// point-order scan leaves unused), and the apply pass's last block totals
+// them into info[2] and info[3].
+extern "C" int gs_scan_tiles_entries(int32_t P, const int32_t* tiles_touched, const int32_t* radii,
+                                     const float* depths, const int32_t* coverage, int32_t* offsets,
+                                     int64_t* info_dev, void* scratch, size_t scratch_bytes, void* stream) {
+  if (P < 0 || !info_dev) return GS_ERR_INVALID_ARGUMENT;
+  hipStream_t s = (hipStream_t)stream;
+  if (P == 0) {
+    hipLaunchKernelGGL(gs::zero_info_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<long long*>(info_dev));
+    hipLaunchKernelGGL(gs::zero_info_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<long long*>(info_dev) + 2);
+    return gs_status_from_hip(hipGetLastError());
+  }
+  if (!tiles_touched || !offsets || !scratch || !coverage || (radii == nullptr) != (depths == nullptr))
+    return GS_ERR_INVALID_ARGUMENT;
+  if (reinterpret_cast<uintptr_t>(coverage) & 15) return GS_ERR_MISALIGNED;
+  if (scratch_bytes < gs_scan_scratch_bytes(P)) return GS_ERR_SCRATCH_TOO_SMALL;
+  const int nb = gs_scan_blocks(P);
+  // block sums and ranges, then the per-block units and valid counts; the
+  // scratch has room for them: gs_scan_scratch_bytes(P) >= 32 bytes per block
+  long long* block_sums = reinterpret_cast<long long*>(scratch);
+  unsigned long long* block_range = reinterpret_cast<unsigned long long*>(block_sums + nb);
+  long long* block_ev = reinterpret_cast<long long*>(static_cast<char*>(scratch) + gs_scan_block_bytes(P));
+  const int vec = gs_scan_vec(tiles_touched, nullptr, offsets, nullptr);
+  hipLaunchKernelGGL(gs::scan_reduce_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, tiles_touched, nullptr,
+                     radii, depths, block_sums, block_range, nullptr, vec,
+                     reinterpret_cast<const int4*>(coverage), block_ev);
+  hipLaunchKernelGGL(gs::scan_apply_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, nb, tiles_touched, nullptr,
+                     block_sums, block_range, offsets, reinterpret_cast<long long*>(info_dev), vec, block_ev);
+  return gs_status_from_hip(hipGetLastError());
+}
+
+extern "C" int gs_info_readback(const int64_t* info_dev, int64_t* info_host_pinned, int32_t count, void* stream) {
+  if (!info_dev || !info_host_pinned || count < 1 || count > 16) return GS_ERR_INVALID_ARGUMENT;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e =
+      hipMemcpyAsync(info_host_pinned, info_dev, (size_t)count * sizeof(int64_t), hipMemcpyDeviceToHost, s);
+  if (e != hipSuccess) return (int)e;
+  return gs_status_from_hip(hipStreamSynchronize(s));
 }
 
 // ---------------------------------------------------------------------------
@@ -785,9 +874,9 @@ extern "C" int gs_scan_tiles_static(int32_t P, const int32_t* tiles_touched, con
   unsigned long long* block_range = reinterpret_cast<unsigned long long*>(block_sums + nb);
   const int vec = gs_scan_vec(tiles_touched, order, offsets, nullptr);
   hipLaunchKernelGGL(gs::scan_reduce_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, tiles_touched, order,
-                     radii, depths, block_sums, block_range, nullptr, vec);
+                     radii, depths, block_sums, block_range, nullptr, vec, nullptr, nullptr);
   hipLaunchKernelGGL(gs::scan_apply_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, nb, tiles_touched, order,
-                     block_sums, block_range, offsets, reinterpret_cast<long long*>(info_dev), vec);
+                     block_sums, block_range, offsets, reinterpret_cast<long long*>(info_dev), vec, nullptr);
   return gs_status_from_hip(hipGetLastError());
 }
 

@@ -395,26 +395,45 @@ constexpr int kCoverMaskCells = 64;
 struct TileCover {
   int4 rect;       // tile rectangle [x, z) x [y, w)
   int columns;     // 1: bands are tile columns (column-major mask)
-  int has_mask;    // the rectangle has at most kCoverMaskCells cells
+  int valid;       // non-empty rectangle that fits the packed word (origin < 2^16, spans < 2^8)
+  int has_mask;    // valid, with at most kCoverMaskCells cells
+  int full;        // every tile of the rectangle is covered (area <= 1 or the SnugBox mode)
+  int band_off;    // banded (valid, neither mask nor full): index of its stored bands, or -1
   uint64_t mask;
 };
 
+// Band store: the coverage bands of a valid Gaussian with neither a mask nor
+// a full rectangle, one word per band (interval [lo, hi) of tile columns for
+// a row band, of tile rows for a column band: lo | hi << 16), in band order.
+// Wave w of a preprocess launch owns words [w kBandSlots, (w + 1) kBandSlots)
+// and fills them in lane order; a Gaussian whose bands do not fit its wave's
+// region is not stored (band_off -1) and its consumers recompute its bands.
+constexpr int kBandSlots = 256;
+
 __device__ __forceinline__ uint64_t low_bits64(int n) { return n >= 64 ? ~0ull : ((1ull << n) - 1ull); }
 
-// Packed per-Gaussian coverage word: x = rect.x | rect.y << 16, y = span_x |
-// span_y << 8 | columns << 16 | has_mask << 17, z / w = mask low / high.
-// Only rectangles with tile coordinates below 2^16 and spans below 2^8 get a
-// mask.
+// Packed per-Gaussian coverage word:
+//   x = rect.x | rect.y << 16,
+//   y = span_x | span_y << 8 | columns << 16 | has_mask << 17 | valid << 18 | full << 19,
+//   z / w = mask low / high with has_mask; else z = the band store index
+//   (band_off, -1 when not stored) for a banded Gaussian, and w = 0.
+// The word is all zero unless the Gaussian covers a valid rectangle.  Which
+// tiles of a valid rectangle are covered follows from the word: all of them
+// (full), the mask's cells (has_mask), or else the coverage bands (tile rows,
+// or tile columns with `columns`) of the Gaussian's conic.
 __device__ __forceinline__ int4 pack_cover(const TileCover& c) {
   const int span_x = c.rect.z - c.rect.x, span_y = c.rect.w - c.rect.y;
-  if (!c.has_mask) return make_int4(0, 0, 0, 0);
-  return make_int4(c.rect.x | (c.rect.y << 16), span_x | (span_y << 8) | (c.columns << 16) | (1 << 17),
-                   (int)(unsigned)c.mask, (int)(unsigned)(c.mask >> 32));
+  if (!c.valid) return make_int4(0, 0, 0, 0);
+  return make_int4(c.rect.x | (c.rect.y << 16),
+                   span_x | (span_y << 8) | (c.columns << 16) | (c.has_mask << 17) | (1 << 18) | (c.full << 19),
+                   c.has_mask ? (int)(unsigned)c.mask : (c.full ? 0 : c.band_off),
+                   c.has_mask ? (int)(unsigned)(c.mask >> 32) : 0);
 }
 
 struct CoverWord {
-  int rx, ry, span_x, span_y, columns, has_mask;
-  uint64_t mask;
+  int rx, ry, span_x, span_y, columns, has_mask, valid, full;
+  uint64_t mask;  // with has_mask
+  int band_off;   // banded: index into the band store, or -1
 };
 
 __device__ __forceinline__ CoverWord unpack_cover(int4 w) {
@@ -425,8 +444,36 @@ __device__ __forceinline__ CoverWord unpack_cover(int4 w) {
   c.span_y = (w.y >> 8) & 0xff;
   c.columns = (w.y >> 16) & 1;
   c.has_mask = (w.y >> 17) & 1;
+  c.valid = (w.y >> 18) & 1;
+  c.full = (w.y >> 19) & 1;
   c.mask = ((uint64_t)(unsigned)w.w << 32) | (unsigned)w.z;
+  c.band_off = w.z;
   return c;
+}
+
+// Super-tiles: squares of kSuperTile x kSuperTile tiles, numbered row-major
+// over the grid (ceil(grid_x / 8) per row).  A tile's cells within its
+// super-tile are bit (ty % 8) * 8 + (tx % 8) of a 64-bit mask.  super_rect
+// gives the super-tiles met by a valid cover word's rectangle: nx x ny of
+// them from (sx0, sy0); none for an invalid word.
+constexpr int kSuperTile = 8;
+
+struct SuperRect {
+  int sx0, sy0, nx, ny;
+};
+
+__device__ __forceinline__ SuperRect super_rect(const CoverWord& w) {
+  SuperRect r;
+  r.sx0 = w.rx / kSuperTile;
+  r.sy0 = w.ry / kSuperTile;
+  r.nx = w.valid ? (w.rx + w.span_x - 1) / kSuperTile - r.sx0 + 1 : 0;
+  r.ny = w.valid ? (w.ry + w.span_y - 1) / kSuperTile - r.sy0 + 1 : 0;
+  return r;
+}
+
+__device__ __forceinline__ int super_units(const CoverWord& w) {
+  const SuperRect r = super_rect(w);
+  return r.nx * r.ny;
 }
 
 // Tile id of cell k of a packed rectangle in band order.  k / span is
@@ -481,10 +528,13 @@ struct CoverCountLds {
 // come by lane shuffle, and each band adds its length and mask bits to its
 // owner's LDS accumulators.  The counts and masks are those of the serial
 // walk band by band (count_covered_tiles semantics of binning_kernels.py).
+// With band_store, the bands of the wave's banded Gaussians are also stored
+// in the wave's region starting at band_base (see kBandSlots).
 __device__ __forceinline__ int wave_count_covered_tiles(bool active, float px, float py, float cov_aa, float cov_cc,
                                                         float ca, float cb, float cc, float opacity, int cuda_radius,
                                                         int grid_x, int grid_y, int mode, TileCover& cover,
-                                                        CoverCountLds& lds) {
+                                                        CoverCountLds& lds, unsigned* band_store = nullptr,
+                                                        int band_base = 0) {
   static_assert(kBlockX == kBlockY, "row and column bands share one band routine");
   const int lane = threadIdx.x & 63;
   int count = 0;
@@ -492,7 +542,10 @@ __device__ __forceinline__ int wave_count_covered_tiles(bool active, float px, f
   float threshold = 0.0f;
   cover.rect = make_int4(0, 0, 0, 0);
   cover.columns = 0;
+  cover.valid = 0;
   cover.has_mask = 0;
+  cover.full = 0;
+  cover.band_off = -1;
   cover.mask = 0;
   if (active) {
     const int4 rect = snugbox_rect(px, py, cov_aa, cov_cc, opacity, cuda_radius, grid_x, grid_y);
@@ -500,9 +553,11 @@ __device__ __forceinline__ int wave_count_covered_tiles(bool active, float px, f
     const int span_y = rect.w - rect.y;
     const int area = span_x * span_y;
     cover.rect = rect;
-    cover.has_mask = span_x >= 0 && span_y >= 0 && span_x <= 0xff && span_y <= 0xff &&
-                     area <= kCoverMaskCells && rect.x <= 0xffff && rect.y <= 0xffff;
+    cover.valid = span_x > 0 && span_y > 0 && span_x <= 0xff && span_y <= 0xff && rect.x <= 0xffff &&
+                  rect.y <= 0xffff;
+    cover.has_mask = cover.valid && area <= kCoverMaskCells;
     if (area <= 1 || mode == kCoverageSnugbox) {
+      cover.full = 1;
       count = area;
       if (cover.has_mask) cover.mask = low_bits64(area);
     } else {
@@ -523,6 +578,11 @@ __device__ __forceinline__ int wave_count_covered_tiles(bool active, float px, f
   const int incl = wave_inclusive_scan_i32(nbands);
   const int excl = incl - nbands;
   const int total = __builtin_amdgcn_readlane(incl, 63);
+  if (band_store != nullptr) {  // uniform
+    const int stored = cover.valid && !cover.has_mask ? nbands : 0;
+    const int sincl = wave_inclusive_scan_i32(stored);
+    if (stored > 0 && sincl <= kBandSlots) cover.band_off = band_base + sincl - stored;
+  }
   lds.count[lane] = 0u;
   lds.mask[lane] = 0ull;
   // the owner's view, gathered once per step by lane shuffle
@@ -549,9 +609,11 @@ __device__ __forceinline__ int wave_count_covered_tiles(bool active, float px, f
     const float o_thr = __shfl(threshold, o, 64);
     const int o_v0 = __shfl(v0, o, 64), o_umin = __shfl(u_min, o, 64), o_umax = __shfl(u_max, o, 64);
     const int o_mspan = __shfl(mask_span, o, 64);
+    const int o_boff = __shfl(cover.band_off, o, 64);
     if (valid) {
       const int2 iv = accutile_band(o_pu, o_pv, o_cuu, o_cuv, o_cvv, o_thr, o_v0 + b, kBlockX, kBlockY, o_umin,
                                     o_umax);
+      if (o_boff >= 0) band_store[o_boff + b] = (unsigned)iv.x | ((unsigned)iv.y << 16);
       const int len = imax(0, iv.y - iv.x);
       if (len > 0) {
         atomicAdd(&lds.count[o], (unsigned)len);

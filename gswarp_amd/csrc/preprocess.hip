@@ -47,6 +47,7 @@ struct PreprocessParams {
   int4* coverage;  // per-Gaussian packed cover masks (pack_cover), or null
   float4* records;
   uint8_t* clamped;
+  unsigned* band_store;  // kBandSlots words per wave for the banded Gaussians' bands, or null
 };
 
 // SH colour of one Gaussian; sh_mem points at its coefficient block (K x 3).
@@ -284,7 +285,8 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p)
   }
   TileCover cover;
   touched = wave_count_covered_tiles(count_it, c_px, c_py, c_aa, c_cc, c_q0, c_q1, c_q2, c_op, c_rad, p.grid_x,
-                                     p.grid_y, p.coverage_mode, cover, s_cover[threadIdx.x >> 6]);
+                                     p.grid_y, p.coverage_mode, cover, s_cover[threadIdx.x >> 6], p.band_store,
+                                     (idx0 >> 6) * kBandSlots);
   if (!in_range) return;
   if (!visible && p.clamped != nullptr) p.clamped[idx] = 0;
   p.radii[idx] = radius;
@@ -355,8 +357,11 @@ extern "C" int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
                                  float filter_variance, int32_t* radii, float* depths, float* proj_2d,
                                  float* conic_2d,
                                  float* conic_2d_inv, int32_t* tiles_touched, int32_t* coverage,
-                                 float* records, uint8_t* clamped, void* stream) {
+                                 float* records, uint8_t* clamped, int32_t* band_store, void* stream) {
   if (P < 0 || image_width <= 0 || image_height <= 0) return GS_ERR_INVALID_ARGUMENT;
+  if (band_store != nullptr && (coverage == nullptr || gs_band_store_words(P) > 0x7fffffffLL)) {
+    return coverage == nullptr ? GS_ERR_INVALID_ARGUMENT : GS_ERR_OVERFLOW;
+  }
   if (coverage_mode < 0 || coverage_mode > 2) return GS_ERR_INVALID_ARGUMENT;
   if (!(filter_variance >= 0.0f) || !__builtin_isfinite(filter_variance)) return GS_ERR_INVALID_ARGUMENT;
   if (P == 0) return GS_OK;
@@ -404,9 +409,14 @@ extern "C" int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
   p.coverage = reinterpret_cast<int4*>(coverage);
   p.records = reinterpret_cast<float4*>(records);
   p.clamped = clamped;
+  p.band_store = reinterpret_cast<unsigned*>(band_store);
   const int blocks = (P + 255) / 256;
   hipLaunchKernelGGL(gs::preprocess_fwd_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, p);
   return gs_status_from_hip(hipGetLastError());
+}
+
+extern "C" int64_t gs_band_store_words(int32_t P) {
+  return P <= 0 ? 0 : (int64_t)((P + 63) / 64) * gs::kBandSlots;
 }
 
 extern "C" int gs_mark_visible(int32_t P, const float* means3d, const float* viewmatrix, uint8_t* visible,

@@ -75,10 +75,17 @@ const char* gs_status_string(int status);
  * Gaussians: cov2D + f I, its conic, the radius ceil(3 sqrt(max(lambda_max,
  * 0.1))) and the tile count are recomputed; a filtered determinant <= 1e-12
  * culls (depth and position are kept).  coverage ((N,4) int32, 16-byte
- * aligned, optional) receives each Gaussian's cover word: when its tile
- * rectangle has at most 64 cells, the rectangle and a 64-bit mask of the
- * covered cells in the order of the coverage walk (zero otherwise), which
- * the emission entry points read instead of re-deriving the tiles.
+ * aligned, optional) receives each Gaussian's cover word: for a non-empty
+ * tile rectangle with origin below 2^16 and spans below 2^8 (zero word
+ * otherwise) the rectangle, whether every tile of it is covered, and, when
+ * it has at most 64 cells, a 64-bit mask of the covered cells in the order of
+ * the coverage walk, which the emission entry points read instead of
+ * re-deriving the tiles.  band_store (optional, with coverage;
+ * gs_band_store_words(P) int32) receives the coverage bands (one word per
+ * tile row or column: lo | hi << 16) of the Gaussians whose word has neither
+ * a mask nor a full rectangle, 256 words per wave of 64 Gaussians; such a
+ * word then holds the index of its bands (or -1 when they did not fit), and
+ * gs_bin_buckets reads them instead of recomputing them.
  * Replaces: preprocess_ops.py:289-581 (preprocess_gaussians) with
  * preprocess_kernels.py:83-269 (scales/rotations), preprocess_kernels.py:345-477
  * and 604-624 (precomputed covariances), the SH kernel
@@ -93,7 +100,8 @@ int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, const float*
                       int32_t image_width, int32_t image_height, int32_t coverage_mode,
                       float filter_variance, int32_t* radii, float* depths, float* proj_2d, float* conic_2d,
                       float* conic_2d_inv, int32_t* tiles_touched, int32_t* coverage, float* records,
-                      uint8_t* clamped, void* stream);
+                      uint8_t* clamped, int32_t* band_store, void* stream);
+int64_t gs_band_store_words(int32_t P);
 
 /*
  * Tile coverage of already projected Gaussians: for each i with radii[i] > 0,
@@ -158,6 +166,28 @@ int gs_scan_tiles(int32_t P, const int32_t* tiles_touched, const int32_t* order,
 int32_t gs_scan_tiles_static_max_points(void);
 int gs_scan_tiles_static(int32_t P, const int32_t* tiles_touched, const int32_t* order, const int32_t* radii,
                          const float* depths, int32_t* offsets, int64_t* info_dev, void* stream);
+
+/*
+ * gs_scan_tiles in point order (order == NULL) that also sizes the bucketed
+ * binning: with coverage = gs_preprocess_fwd's cover words it stores, after
+ * info[0] and info[1] as gs_scan_tiles does, info[2] = the number of
+ * (Gaussian, super-tile) entries, i.e. the sum over the valid cover words of
+ * the 8 x 8-tile squares their tile rectangle meets (-1 when a Gaussian with
+ * tiles has no valid word: its rectangle does not fit the word), and
+ * info[3] = the number of valid words.  info_dev holds four int64; the
+ * scratch is gs_scan_scratch_bytes(P) bytes.
+ * Replaces: memory.py:539-551 and binning_ops.py:62-81, as gs_scan_tiles.
+ */
+int gs_scan_tiles_entries(int32_t P, const int32_t* tiles_touched, const int32_t* radii, const float* depths,
+                          const int32_t* coverage, int32_t* offsets, int64_t* info_dev, void* scratch,
+                          size_t scratch_bytes, void* stream);
+
+/*
+ * Copies count (1 to 16) int64 at info_dev into pinned host memory and waits
+ * for the stream.
+ * Replaces: binning_ops.py:243-252 (the num_rendered .item()).
+ */
+int gs_info_readback(const int64_t* info_dev, int64_t* info_host_pinned, int32_t count, void* stream);
 
 /*
  * Copies the two int64 at info_dev into caller-provided pinned host memory
@@ -308,6 +338,38 @@ int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_host_pinned, i
                            int32_t* ranges, int32_t* point_list, const float* background, int32_t compute_depth,
                            float* out_color, float* out_depth, float* out_alpha, int32_t* n_contrib,
                            void* const* stage_events, int64_t* result, void* stream);
+
+/*
+ * Bucketed binning, for many tiles per Gaussian: the per-tile lists in
+ * (depth, point index) order, written straight into point_list
+ * (num_rendered int32) with their ranges ((T, 2) int32; [0, 0] for empty
+ * tiles), without a key per pair.  The Gaussians with a valid cover word
+ * (coverage from gs_preprocess_fwd; num_valid of them) are sorted stably by
+ * the bits of depths[i] above depth_min; each yields, per 8 x 8-tile square
+ * its tile rectangle meets, an entry (point index, mask of the covered tiles
+ * there; num_entries of them in all), which a stable partition lists per
+ * square in depth order; each square's entries are then written into the
+ * lists of the tiles they cover.  num_entries and num_valid are
+ * gs_scan_tiles_entries's info[2] and info[3], depth_min / depth_max its
+ * visible depth-bit range (info[1]); band_store (optional) and records are
+ * gs_preprocess_fwd's: the stored coverage bands, and the conic of Gaussians
+ * whose bands were not stored, which are recomputed.  The image may
+ * be at most 255 x 255 tiles (GS_ERR_TOO_LARGE otherwise).  workspace is
+ * gs_bin_buckets_workspace_bytes(P, num_valid, num_entries, W, H) bytes,
+ * 16-byte aligned.  stage_events, if not NULL, holds four hipEvent_t
+ * recorded before the depth sort and after it, after the super-square
+ * entries and after the tile lists.
+ * Replaces: binning_ops.py:152-222 (depth sort) and binning_ops.py:297-431
+ * (duplicate-with-keys from the depth order, tile sort and tile ranges):
+ * the same lists and ranges.
+ */
+size_t gs_bin_buckets_workspace_bytes(int32_t P, int32_t num_valid, int64_t num_entries, int32_t image_width,
+                                      int32_t image_height);
+int gs_bin_buckets(int32_t P, int32_t num_valid, int64_t num_entries, int64_t num_rendered, const float* depths,
+                   uint32_t depth_min, uint32_t depth_max, const int32_t* coverage, const int32_t* band_store,
+                   const float* records, int32_t image_width, int32_t image_height, void* workspace,
+                   size_t workspace_bytes, int32_t* ranges, int32_t* point_list, void* const* stage_events,
+                   void* stream);
 
 /*
  * Per-tile front-to-back alpha blending of 16x16 tiles, each covered by

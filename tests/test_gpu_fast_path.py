@@ -109,8 +109,8 @@ def _spy_calls(monkeypatch):
 def test_fast_path_declines_for_depth_then_tile(device, monkeypatch):
     """The heavy-tailed config-3 scene at half resolution has more than four
     pairs per Gaussian.  Provisioned for its count regardless of the last
-    forward, the one-call path declines (the default mode's depth-then-tile
-    dataflow applies) and the outputs still equal the oracle's."""
+    forward, the one-call path declines (the default mode's bucketed binning
+    applies) and the outputs still equal the oracle's."""
     scene = _scene("c3_half", device)
     host, ref = oracle_forward(scene)
     R = ref["bins"]["num_rendered"]
@@ -119,20 +119,22 @@ def test_fast_path_declines_for_depth_then_tile(device, monkeypatch):
     monkeypatch.setattr(_workspace, "last_pairs", lambda dev: 1)
     names = _spy_calls(monkeypatch)
     _, result = _forward(scene, options())
-    assert "gs_readback_bin_packed" in names
+    assert "gs_readback_bin_packed" in names and "gs_bin_buckets" in names
     assert not result.state.binning.rendered
     _check_against_oracle(scene, result, ref)
 
 
 def test_no_provision_after_a_depth_then_tile_forward(device, monkeypatch):
-    """After a forward that took the depth-then-tile dataflow the next one does
-    not provision the packed path's buffers: it reads the count back alone."""
+    """After a forward with many pairs per Gaussian the next one does not
+    provision the packed path's buffers: it reads the counts back alone (the
+    pair count and the bucketed binning's sizes) and bins by buckets."""
     scene = _scene("c3_half", device)
     host, ref = oracle_forward(scene)
     _workspace.note_pairs(device, ref["bins"]["num_rendered"])
     names = _spy_calls(monkeypatch)
     _, result = _forward(scene, options())
-    assert "gs_readback_bin_packed" not in names and "gs_num_rendered_readback" in names
+    assert "gs_readback_bin_packed" not in names and "gs_info_readback" in names
+    assert "gs_scan_tiles_entries" in names and "gs_bin_buckets" in names
     assert not result.state.binning.rendered
     _check_against_oracle(scene, result, ref)
 

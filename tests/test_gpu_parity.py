@@ -92,15 +92,17 @@ def test_forward_stages_match_oracle(case, device):
     _check_forward(scene, options(flow=flow), flow=flow, top_k=20 if flow else 0)
 
 
-@pytest.mark.parametrize("sort_mode", ["warp_radix", "torch", "depth_then_tile"])
+@pytest.mark.parametrize("sort_mode", ["warp_radix", "torch", "depth_then_tile", "buckets"])
 @pytest.mark.parametrize("case", ["c0_full", "c2_small", "c3_small", "c1_ragged"])
 def test_other_sort_modes_match_oracle(case, sort_mode, device, monkeypatch):
     """Every binning dataflow gives the oracle's bit-exact lists: the packed
-    64-bit key sort, the torch.sort dataflow, and the HIP depth-then-tile
-    dataflow (forced here; the default mode uses it above a pair-count ratio)."""
+    64-bit key sort, the torch.sort dataflow, and the default mode's two
+    dataflows for many pairs per Gaussian, the HIP depth-then-tile sort and the
+    bucketed binning (both forced here at any pair-count ratio)."""
     scene = _scene(case, device)
-    if sort_mode == "depth_then_tile":
+    if sort_mode in ("depth_then_tile", "buckets"):
         monkeypatch.setattr(_pipeline, "DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN", 0)
+        monkeypatch.setattr(_pipeline, "HEAVY_DATAFLOW", "depth_tile" if sort_mode == "depth_then_tile" else "buckets")
         sort_mode = "warp_depth_stable_tile"
     _check_forward(scene, options(sort_mode=sort_mode))
 
