@@ -35,7 +35,7 @@
 
 namespace gs {
 
-constexpr int kL1Chunk = 256;            // depth positions per level-1 workgroup (one wave, 4 groups of 64)
+constexpr int kL1Chunk = 128;            // depth positions per level-1 workgroup (one wave, 2 groups of 64)
 constexpr int kL1Groups = kL1Chunk / 64;
 constexpr int kL2Chunk = 1024;           // entries per level-2 workgroup (one wave)
 constexpr int kStageRing = 32;           // level-2 staged pairs per tile (two flush blocks of 16)
@@ -156,93 +156,6 @@ __device__ __forceinline__ Clip clip_to_super(const CoverWord& w, int sx, int sy
   return k;
 }
 
-// Tiles of the super-tile covered by every tile of the rectangle.
-__device__ __forceinline__ uint64_t mask_full(const Clip& k) {
-  if (k.x1 <= k.x0 || k.y1 <= k.y0) return 0ull;
-  const uint64_t row = low_bits64(k.x1 - k.x0) << (k.x0 - k.bx);
-  const uint64_t rows = low_bits64(8 * (k.y1 - k.y0)) << (8 * (k.y0 - k.by));
-  return (row * 0x0101010101010101ull) & rows;
-}
-
-// Tiles of the super-tile among a recorded mask's cells (band order:
-// row-major over the rectangle, or column-major with `columns`).
-__device__ __forceinline__ uint64_t mask_cells(const CoverWord& w, const Clip& k) {
-  uint64_t m = 0ull;
-  if (k.x1 <= k.x0 || k.y1 <= k.y0) return m;
-  if (!w.columns) {
-    for (int ty = k.y0; ty < k.y1; ++ty) {
-      const uint64_t bits = (w.mask >> ((ty - w.ry) * w.span_x + (k.x0 - w.rx))) & low_bits64(k.x1 - k.x0);
-      m |= bits << ((ty - k.by) * 8 + (k.x0 - k.bx));
-    }
-  } else {
-    for (int tx = k.x0; tx < k.x1; ++tx) {
-      uint64_t bits = (w.mask >> ((tx - w.rx) * w.span_y + (k.y0 - w.ry))) & low_bits64(k.y1 - k.y0);
-      while (bits != 0ull) {
-        const int r = __builtin_ctzll(bits);
-        bits &= bits - 1ull;
-        m |= 1ull << ((k.y0 - k.by + r) * 8 + (tx - k.bx));
-      }
-    }
-  }
-  return m;
-}
-
-// Tiles of the super-tile covered by the Gaussian's coverage bands: the
-// stored bands when there are any, else each band recomputed from the conic
-// (accutile_band with the arguments of the preprocess's count).  Band b of a
-// row-band Gaussian is tile row ry + b ([lo, hi) in tile columns); of a
-// column-band Gaussian, tile column rx + b ([lo, hi) in tile rows).
-__device__ __forceinline__ uint64_t mask_bands(const CoverWord& w, const Clip& k,
-                                               const unsigned* __restrict__ band_store, float px, float py,
-                                               float ca, float cb, float cc, float thr) {
-  uint64_t m = 0ull;
-  if (k.x1 <= k.x0 || k.y1 <= k.y0) return m;
-  const bool stored = w.band_off >= 0 && band_store != nullptr;
-  if (!w.columns) {
-#pragma unroll
-    for (int i = 0; i < kSuperTile; ++i) {
-      const int ty = k.y0 + i;
-      if (ty < k.y1) {
-        int lo, hi;
-        if (stored) {
-          const unsigned word = band_store[w.band_off + (ty - w.ry)];
-          lo = (int)(word & 0xFFFFu);
-          hi = (int)(word >> 16);
-        } else {
-          const int2 iv = accutile_band(px, py, ca, cb, cc, thr, ty, kBlockX, kBlockY, w.rx, w.rx + w.span_x);
-          lo = iv.x;
-          hi = iv.y;
-        }
-        lo = imax(lo, k.bx);
-        hi = imin(hi, k.bx + kSuperTile);
-        if (hi > lo) m |= low_bits64(hi - lo) << ((ty - k.by) * 8 + (lo - k.bx));
-      }
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < kSuperTile; ++i) {
-      const int tx = k.x0 + i;
-      if (tx < k.x1) {
-        int lo, hi;
-        if (stored) {
-          const unsigned word = band_store[w.band_off + (tx - w.rx)];
-          lo = (int)(word & 0xFFFFu);
-          hi = (int)(word >> 16);
-        } else {
-          const int2 iv = accutile_band(py, px, cc, cb, ca, thr, tx, kBlockY, kBlockX, w.ry, w.ry + w.span_y);
-          lo = iv.x;
-          hi = iv.y;
-        }
-        lo = imax(lo, k.by);
-        hi = imin(hi, k.by + kSuperTile);
-        if (hi > lo)
-          m |= (0x0101010101010101ull << (tx - k.bx)) & (low_bits64(8 * (hi - lo)) << (8 * (lo - k.by)));
-      }
-    }
-  }
-  return m;
-}
-
 // Lanes (among `valid` ones) whose value of the low `bits` bits of d equals this lane's.
 __device__ __forceinline__ uint64_t match_bits(unsigned d, bool valid, int bits) {
   uint64_t peers = __ballot(valid);
@@ -256,16 +169,79 @@ __device__ __forceinline__ uint64_t match_bits(unsigned d, bool valid, int bits)
   return peers;
 }
 
-// Level-1 ranking: chunk c walks its Gaussians in depth order, 64 at a time.
-// Their entries (flat positions: Gaussian-major, super-tiles row-major within
-// a Gaussian's super-rectangle) are taken 64 per round, one per lane: the
-// lane finds its entry's Gaussian (the last lane whose first entry is at or
-// before it: marks and a prefix maximum), reads that Gaussian's cover word and
-// parameters from a per-group LDS table, computes the entry's tile mask
-// (from the recorded mask, the full rectangle, or the coverage bands), and
-// ranks the entry among the round's entries of the same super-tile (ballot
-// matching, lane order) on top of the running per-super-tile positions, which
-// start at the chunk's offsets from the scanned counts.
+// Transpose of an 8 x 8 bit matrix held as 8 bytes (bit 8 r + c is entry
+// (r, c)): three rounds of delta swaps.
+__device__ __forceinline__ uint64_t transpose8x8(uint64_t x) {
+  uint64_t t = (x ^ (x >> 7)) & 0x00AA00AA00AA00AAull;
+  x = x ^ t ^ (t << 7);
+  t = (x ^ (x >> 14)) & 0x0000CCCC0000CCCCull;
+  x = x ^ t ^ (t << 14);
+  t = (x ^ (x >> 28)) & 0x00000000F0F0F0F0ull;
+  return x ^ t ^ (t << 28);
+}
+
+// The tile mask of an entry in one code path for every kind of coverage, so
+// that a round's lanes do not diverge on it.  The super-tile's 8 lines are
+// its tile rows, or its tile columns for column-oriented coverage (a
+// column-major cell mask or column bands); line i's byte holds the covered
+// tiles along it, taken (by selects) from the recorded cells of band
+// (line - rect origin), from that band's interval in `bands` (LDS), or from
+// the whole clipped rectangle; the bytes of a column-oriented entry are then
+// transposed.  `bands` must be readable at [0, lines of the rectangle) for
+// every kind (its words only count for banded coverage).
+__device__ __forceinline__ uint64_t entry_mask(const CoverWord& w, const Clip& k, const unsigned* bands) {
+  if (k.x1 <= k.x0 || k.y1 <= k.y0) return 0ull;
+  const bool cols = w.columns;
+  const int l0 = cols ? k.x0 : k.y0, l1 = cols ? k.x1 : k.y1;      // lines present, in tile coordinates
+  const int lb = cols ? k.bx : k.by;                               // first line of the super-tile
+  const int u0 = cols ? k.y0 : k.x0, u1 = cols ? k.y1 : k.x1;      // clipped extent along a line
+  const int ub = cols ? k.by : k.bx;
+  const int rl = cols ? w.rx : w.ry, ru = cols ? w.ry : w.rx;      // rectangle origin: band index, along a line
+  const int span_u = cols ? w.span_y : w.span_x, span_l = cols ? w.span_x : w.span_y;
+  const unsigned width = (1u << (u1 - u0)) - 1u;
+  const unsigned full = width << (u0 - ub);
+  uint64_t m = 0ull;
+#pragma unroll
+  for (int i = 0; i < kSuperTile; ++i) {
+    const int line = l0 + i;
+    const int b = line - rl;
+    const unsigned from_cells = ((unsigned)(w.mask >> ((b * span_u + (u0 - ru)) & 63)) & width) << (u0 - ub);
+    const unsigned word = bands[imin(b, span_l - 1)];
+    const int lo = imax((int)(word & 0xFFFFu), ub), hi = imin((int)(word >> 16), ub + kSuperTile);
+    const unsigned from_band = hi > lo ? ((1u << (hi - lo)) - 1u) << (lo - ub) : 0u;
+    const unsigned byte = w.has_mask ? from_cells : (w.full ? full : from_band);
+    m |= line < l1 ? (uint64_t)(byte & 0xFFu) << (8 * (line - lb)) : 0ull;
+  }
+  return cols ? transpose8x8(m) : m;
+}
+
+// Largest index g of a nondecreasing table of kL1Chunk values with t[g] <= v
+// (0 when none), by binary search in LDS.
+__device__ __forceinline__ int table_floor(const int* t, int v) {
+  int lo = 0;
+#pragma unroll
+  for (int step = kL1Chunk / 2; step > 0; step >>= 1)
+    if (t[lo + step] <= v) lo += step;
+  return lo;
+}
+
+constexpr int kL1BandCap = 2048;   // band words of a level-1 chunk held in LDS
+constexpr int kL1OwnerCap = 2048;  // entries of a level-1 chunk whose Gaussian is looked up in a table
+
+// Level-1 ranking.  Chunk c (kL1Chunk Gaussians in depth order) first loads
+// the Gaussians' cover words and indices and the chunk's running
+// per-super-tile positions (from the scanned counts) into LDS.  Its entries
+// (flat positions: Gaussian-major, super-tiles row-major within a Gaussian's
+// super-rectangle) are then handled in segments of whole Gaussians whose
+// coverage bands fit an LDS buffer of kL1BandCap words: the segment's bands
+// are staged (stored ones loaded, the others recomputed from the conic), and
+// its entries are taken 64 per round, one per lane: the lane finds its
+// entry's Gaussian (a per-entry table, or binary search over the Gaussians'
+// first entries), computes the entry's tile mask and ranks the entry among
+// the round's entries of the same super-tile (ballot matching, lane order) on
+// top of the running position.  The rounds make no global loads, so no load
+// waits behind their stores (one counter covers loads and stores); only a
+// segment's staging does, once.
 __global__ __launch_bounds__(64) void bucket_scatter_kernel(int V, const int4* __restrict__ cw_sorted,
                                                            const int* __restrict__ idx_sorted,
                                                            const unsigned* __restrict__ band_store,
@@ -275,85 +251,112 @@ __global__ __launch_bounds__(64) void bucket_scatter_kernel(int V, const int4* _
                                                            int* __restrict__ e_idx,
                                                            unsigned long long* __restrict__ e_mask) {
   extern __shared__ int cnt[];  // B running positions
-  __shared__ int4 s_own[64];    // per lane: first entry, super-rectangle width, sx0 | sy0 << 8 | height << 16, index
-  __shared__ int4 s_cw[64];     // per lane: cover word
-  __shared__ int s_mark[64];
+  __shared__ int4 s_cw[kL1Chunk];
+  __shared__ int s_idx[kL1Chunk];
+  __shared__ int s_excl[kL1Chunk];   // first entry of each Gaussian
+  __shared__ int s_bexcl[kL1Chunk];  // first LDS band word of each Gaussian
+  __shared__ unsigned s_band[kL1BandCap];
+  __shared__ unsigned char s_owner[kL1OwnerCap];  // Gaussian of each entry, for chunks of few entries
   const int lane = threadIdx.x;
   const int c = blockIdx.x;
+  const int j0 = c * kL1Chunk;
+  // loads: words, indices, positions
+#pragma unroll
+  for (int q = 0; q < kL1Groups; ++q) {
+    const int j = j0 + q * 64 + lane;
+    s_cw[q * 64 + lane] = j < V ? cw_sorted[j] : make_int4(0, 0, 0, 0);
+    s_idx[q * 64 + lane] = j < V ? idx_sorted[j] : 0;
+  }
   for (int b = lane; b < B; b += 64) {
     const long long f = (long long)b * nchunks + c;
     cnt[b] = f > 0 ? hist_incl[f - 1] : 0;
   }
   __syncthreads();
-  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-  int j = c * kL1Chunk + lane;
-  int4 cwv = j < V ? cw_sorted[j] : make_int4(0, 0, 0, 0);
-  int idx = j < V ? idx_sorted[j] : 0;
-  for (int g = 0; g < kL1Groups; ++g, j += 64) {
-    // the next group's loads go out first
-    int4 next_cw = make_int4(0, 0, 0, 0);
-    int next_idx = 0;
-    if (g + 1 < kL1Groups && j + 64 < V) {
-      next_cw = cw_sorted[j + 64];
-      next_idx = idx_sorted[j + 64];
-    }
-    const SuperRect r = super_rect(unpack_cover(cwv));
+  // entries and coverage bands per Gaussian, scanned over the chunk
+  int carry = 0, bcarry = 0;
+#pragma unroll
+  for (int q = 0; q < kL1Groups; ++q) {
+    const CoverWord w = unpack_cover(s_cw[q * 64 + lane]);
+    const SuperRect r = super_rect(w);
     const int n = r.nx * r.ny;
-    const int incl = wave_scan_add_dpp(n);
-    const int total = __builtin_amdgcn_readlane(incl, 63);
-    const int excl = incl - n;
-    s_own[lane] = make_int4(excl, r.nx, r.sx0 | (r.sy0 << 8) | (r.ny << 16), idx);
-    s_cw[lane] = cwv;
-    __builtin_amdgcn_wave_barrier();
-    for (int r0 = 0; r0 < total; r0 += 64) {
-      s_mark[lane] = -1;
-      __builtin_amdgcn_wave_barrier();
-      if (n > 0 && excl < r0 && excl + n > r0) s_mark[0] = lane;  // a Gaussian carried in from before r0
-      __builtin_amdgcn_wave_barrier();
-      if (n > 0 && excl >= r0 && excl < r0 + 64) s_mark[excl - r0] = lane;
-      __builtin_amdgcn_wave_barrier();
-      const int owner = wave_scan_max_dpp(s_mark[lane]);
-      const int slot = r0 + lane;
-      const bool ok = slot < total && owner >= 0;
-      const int4 own = s_own[ok ? owner : 0];
-      const int u = slot - own.x;
-      const int o_ny = own.z >> 16;
-      const bool in_owner = ok && u >= 0 && u < own.y * o_ny;
-      // u / width by a float reciprocal: exact for u < 2^16 and widths up to 32
-      const int uy = in_owner ? (int)(((float)u + 0.5f) * __builtin_amdgcn_rcpf((float)own.y)) : 0;
-      const int ux = u - uy * own.y;
-      const int sx = (own.z & 0xFF) + ux, sy = ((own.z >> 8) & 0xFF) + uy;
-      const int bucket = in_owner ? sy * nsx + sx : 0;
-      const bool live = in_owner && ux >= 0 && ux < own.y && bucket >= 0 && bucket < B;
-      uint64_t m = 0ull;
-      if (live) {
-        const CoverWord w = unpack_cover(s_cw[owner]);
-        const Clip k = clip_to_super(w, sx, sy);
-        if (w.has_mask) {
-          m = mask_cells(w, k);
-        } else if (w.full) {
-          m = mask_full(k);
-        } else {
-          // the conic, for a banded Gaussian whose bands were not stored
-          float px = 0.0f, py = 0.0f, ca = 0.0f, cb = 0.0f, cc = 0.0f, thr = 0.0f;
-          if (w.band_off < 0 || band_store == nullptr) {
-            const float4 r0v = records[3 * (size_t)own.w];
-            const float4 r1v = records[3 * (size_t)own.w + 1];
-            px = r0v.x;
-            py = r0v.y;
-            ca = r0v.z;
-            cb = r0v.w;
-            cc = r1v.x;
-            thr = coverage_threshold(r1v.y);
-          }
-          m = mask_bands(w, k, band_store, px, py, ca, cb, cc, thr);
-        }
+    const bool banded = w.valid && !w.has_mask && !w.full;
+    const int nb = banded ? (w.columns ? w.span_x : w.span_y) : 0;
+    const int incl = wave_scan_add_dpp(n), bincl = wave_scan_add_dpp(nb);
+    s_excl[q * 64 + lane] = carry + incl - n;
+    s_bexcl[q * 64 + lane] = bcarry + bincl - nb;
+    carry += __builtin_amdgcn_readlane(incl, 63);
+    bcarry += __builtin_amdgcn_readlane(bincl, 63);
+  }
+  const int total = carry;
+  const int band_all = bcarry;
+  __syncthreads();
+  const bool owner_table = total <= kL1OwnerCap;
+  if (owner_table) {
+#pragma unroll
+    for (int q = 0; q < kL1Groups; ++q) {
+      const int g = q * 64 + lane;
+      const int e0 = s_excl[g], e1 = g + 1 < kL1Chunk ? s_excl[g + 1] : total;
+      for (int e = e0; e < e1; ++e) s_owner[e] = (unsigned char)g;
+    }
+  }
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  // Segments of whole Gaussians whose bands fit the LDS band buffer: each
+  // segment's bands are staged (stored ones loaded, the others recomputed
+  // from the conic), then its entries are ranked and written.
+  for (int g0 = 0; g0 < kL1Chunk;) {
+    const int b0 = s_bexcl[g0];
+    // the segment [g0, g1) ends where its bands would pass the buffer: g1 is the
+    // last Gaussian whose first band word still fits (every band span is < 256)
+    int g1 = table_floor(s_bexcl, b0 + kL1BandCap);
+    if (g1 == kL1Chunk - 1 && band_all <= b0 + kL1BandCap) g1 = kL1Chunk;
+    if (g1 <= g0) g1 = g0 + 1;
+    const int b1 = g1 < kL1Chunk ? s_bexcl[g1] : band_all;
+    const int e_begin = s_excl[g0], e_end = g1 < kL1Chunk ? s_excl[g1] : total;
+    __syncthreads();  // the previous segment's rounds are done with s_band
+    for (int t = b0 + lane; t < b1; t += 64) {
+      const int g = table_floor(s_bexcl, t);
+      const CoverWord w = unpack_cover(s_cw[g]);
+      const int b = t - s_bexcl[g];
+      if (w.band_off >= 0 && band_store != nullptr) {
+        s_band[t - b0] = band_store[w.band_off + b];
+      } else {
+        const int idx = s_idx[g];
+        const float4 r0v = records[3 * (size_t)idx];
+        const float4 r1v = records[3 * (size_t)idx + 1];
+        const float thr = coverage_threshold(r1v.y);
+        const int2 iv = w.columns ? accutile_band(r0v.y, r0v.x, r1v.x, r0v.w, r0v.z, thr, w.rx + b, kBlockY,
+                                                  kBlockX, w.ry, w.ry + w.span_y)
+                                  : accutile_band(r0v.x, r0v.y, r0v.z, r0v.w, r1v.x, thr, w.ry + b, kBlockX,
+                                                  kBlockY, w.rx, w.rx + w.span_x);
+        s_band[t - b0] = (unsigned)iv.x | ((unsigned)iv.y << 16);
       }
+    }
+    __syncthreads();
+    for (int r0 = e_begin; r0 < e_end; r0 += 64) {
+      const int slot = r0 + lane;
+      const bool ok = slot < e_end;
+      const int g = owner_table ? (ok ? (int)s_owner[slot] : g0) : table_floor(s_excl, slot);
+      const CoverWord w = unpack_cover(s_cw[g]);
+      const SuperRect r = super_rect(w);
+      const int u = slot - s_excl[g];
+      const bool in_owner = ok && u >= 0 && u < r.nx * r.ny;
+      // u / width by a float reciprocal: exact for u < 2^16 and widths up to 32
+      const int uy = in_owner ? (int)(((float)u + 0.5f) * __builtin_amdgcn_rcpf((float)r.nx)) : 0;
+      const int ux = u - uy * r.nx;
+      const int sx = r.sx0 + ux, sy = r.sy0 + uy;
+      const int bucket = in_owner ? sy * nsx + sx : 0;
+      const bool live = in_owner && ux >= 0 && ux < r.nx && bucket >= 0 && bucket < B;
+      const bool banded = w.valid && !w.has_mask && !w.full;
+      // a banded Gaussian's words in this segment's buffer (kept in bounds
+      // whatever the word says); other kinds read any words and ignore them
+      const int nb = w.columns ? w.span_x : w.span_y;
+      const int boff = banded ? imax(0, imin(s_bexcl[g] - b0, kL1BandCap - nb)) : 0;
+      const uint64_t m = live ? entry_mask(w, clip_to_super(w, sx, sy), s_band + boff) : 0ull;
       const uint64_t peers = match_bits((unsigned)bucket, live, bucket_bits);
       const int base = live ? cnt[bucket] : 0;
       const long long pos = (long long)base + __popcll(peers & below);
       if (live && pos < E) {
-        e_idx[pos] = own.w;
+        e_idx[pos] = s_idx[g];
         e_mask[pos] = m;
       }
       __builtin_amdgcn_wave_barrier();
@@ -361,8 +364,7 @@ __global__ __launch_bounds__(64) void bucket_scatter_kernel(int V, const int4* _
       if (live && (peers >> lane) == 1ull) cnt[bucket] = base + __popcll(peers);
       __builtin_amdgcn_wave_barrier();
     }
-    cwv = next_cw;
-    idx = next_idx;
+    g0 = g1;
   }
 }
 
@@ -419,31 +421,34 @@ __device__ __forceinline__ unsigned mask_bit(unsigned long long m, int lane) {
 }
 
 // Level-2 counts: lane k of chunk g counts the chunk's entries covering tile k
-// of its super-tile into cnt2[g * 64 + k].  The chunk's masks pass through
-// LDS 64 at a time (one coalesced load each, the next one in flight) and
-// every lane reads them all.
+// of its super-tile into cnt2[g * 64 + k].  The chunk's masks are copied into
+// LDS (coalesced) and every lane reads them all, 16 per batch of reads.
 __global__ __launch_bounds__(64) void bucket_tile_count_kernel(const int* __restrict__ list_start,
                                                               const int* __restrict__ chunk_start, int B, int E,
                                                               const unsigned long long* __restrict__ e_mask,
                                                               int* __restrict__ cnt2) {
-  __shared__ unsigned long long s_m[64];
+  __shared__ __align__(16) unsigned long long s_m[kL2Chunk];
   const int g = blockIdx.x;
   if (g >= chunk_start[B]) return;
   const int s = chunk_super(chunk_start, B, g);
   const int e0 = list_start[s] + (g - chunk_start[s]) * kL2Chunk;
   const int e1 = imin(imin(e0 + kL2Chunk, list_start[s + 1]), E);
+  const int n16 = (e1 - e0 + 15) & ~15;  // entries past the chunk count nothing: zero masks
   const int lane = threadIdx.x;
+#pragma unroll 4
+  for (int i = lane; i < n16; i += 64) s_m[i] = e0 + i < e1 ? e_mask[e0 + i] : 0ull;
+  __syncthreads();
   int count = 0;
-  unsigned long long cur = e0 + lane < e1 ? e_mask[e0 + lane] : 0ull;
-  for (int eb = e0; eb < e1; eb += 64) {
-    const unsigned long long next = eb + 64 + lane < e1 ? e_mask[eb + 64 + lane] : 0ull;
-    s_m[lane] = cur;
-    __builtin_amdgcn_wave_barrier();
-    const int n = imin(64, e1 - eb);
-#pragma unroll 8
-    for (int i = 0; i < n; ++i) count += mask_bit(s_m[i], lane);
-    __builtin_amdgcn_wave_barrier();
-    cur = next;
+  for (int i0 = 0; i0 < n16; i0 += 16) {
+    unsigned long long mm[16];
+#pragma unroll
+    for (int q = 0; q < 16; q += 2) {
+      const ulonglong2 v = *reinterpret_cast<const ulonglong2*>(s_m + i0 + q);
+      mm[q] = v.x;
+      mm[q + 1] = v.y;
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) count += mask_bit(mm[q], lane);
   }
   cnt2[(size_t)g * 64 + lane] = count;
 }
@@ -496,11 +501,14 @@ __global__ __launch_bounds__(1024) void bucket_ranges_kernel(int T, const int* _
 // Four consecutive ints at a dword-aligned address (one vector store).
 typedef int int4_dw __attribute__((ext_vector_type(4), aligned(4)));
 
-// Level-2 scatter: chunk g walks its entries in order, 64 at a time through
-// LDS; lane k appends the point index of every entry covering tile k to its
-// LDS ring (the store goes out for every entry, the ring position only moves
-// on a hit), and every 16 entries the lanes with 16 staged pairs write them to
-// their tile's list as four 16-byte stores; the rest follows at the end.
+// Level-2 scatter: chunk g first copies its entries (masks and point indices)
+// into LDS, so that no load waits behind the stores that follow, then walks
+// them in order; lane k appends the point index of every entry covering tile
+// k to its LDS ring (the store goes out for every entry, the ring position
+// only moves on a hit).  Every 16 entries a lane writes out the staged pairs
+// up to the next 64-byte boundary of its tile's list once (the head), and
+// after that whole 64-byte blocks of 16 as four 16-byte stores, so the list
+// is written in full HBM sectors; the rest follows at the end.
 __global__ __launch_bounds__(64) void bucket_tile_scatter_kernel(const int* __restrict__ list_start,
                                                                 const int* __restrict__ chunk_start, int B, int E,
                                                                 int nsx, int grid_x, int grid_y,
@@ -509,60 +517,76 @@ __global__ __launch_bounds__(64) void bucket_tile_scatter_kernel(const int* __re
                                                                 const int* __restrict__ cnt2,
                                                                 const int2* __restrict__ ranges, long long R,
                                                                 int* __restrict__ point_list) {
-  __shared__ unsigned long long s_m[64];
-  __shared__ int s_id[64];
+  __shared__ __align__(16) unsigned long long s_m[kL2Chunk];
+  __shared__ __align__(16) int s_id[kL2Chunk];
   __shared__ int s_ring[kStageRing * 64];  // slot-major: slot q of tile k at q * 64 + k (conflict-free)
   const int g = blockIdx.x;
   if (g >= chunk_start[B]) return;
   const int s = chunk_super(chunk_start, B, g);
   const int e0 = list_start[s] + (g - chunk_start[s]) * kL2Chunk;
   const int e1 = imin(imin(e0 + kL2Chunk, list_start[s + 1]), E);
+  const int n = e1 - e0;
+  const int n16 = (n + 15) & ~15;  // entries past n have no tile: zero masks
   const int lane = threadIdx.x;
+#pragma unroll 4
+  for (int i = lane; i < n16; i += 64) {
+    s_m[i] = i < n ? e_mask[e0 + i] : 0ull;
+    s_id[i] = i < n ? e_idx[e0 + i] : 0;
+  }
   const int tx = (s % nsx) * kSuperTile + (lane & 7);
   const int ty = (s / nsx) * kSuperTile + (lane >> 3);
   const bool tile_ok = tx < grid_x && ty < grid_y;
-  long long out = tile_ok ? (long long)ranges[ty * grid_x + tx].x + cnt2[(size_t)g * 64 + lane] : 0;
+  const long long out = tile_ok ? (long long)ranges[ty * grid_x + tx].x + cnt2[(size_t)g * 64 + lane] : 0;
+  int head = (int)((16 - (out & 15)) & 15);  // pairs before the list's next 64-byte boundary
   // staged pairs [flushed, staged) in ring slots modulo kStageRing
   int staged = 0, flushed = 0;
   int* ring = s_ring + lane;
-  unsigned long long cur_m = e0 + lane < e1 ? e_mask[e0 + lane] : 0ull;
-  int cur_id = e0 + lane < e1 ? e_idx[e0 + lane] : 0;
-  for (int eb = e0; eb < e1; eb += 64) {
-    const bool more = eb + 64 + lane < e1;
-    const unsigned long long next_m = more ? e_mask[eb + 64 + lane] : 0ull;
-    const int next_id = more ? e_idx[eb + 64 + lane] : 0;
-    s_m[lane] = cur_m;
-    s_id[lane] = cur_id;
-    __builtin_amdgcn_wave_barrier();
-    const int n = imin(64, e1 - eb);
-    for (int i0 = 0; i0 < n; i0 += 16) {
-      const int i1 = imin(n, i0 + 16);
-#pragma unroll 4
-      for (int i = i0; i < i1; ++i) {
-        ring[(staged & (kStageRing - 1)) * 64] = s_id[i];
-        staged += (int)mask_bit(s_m[i], lane);
-      }
-      // 16 staged pairs (ring slots 0-15 or 16-31): one flush of four 16-byte stores
-      if (staged - flushed >= 16) {
-        const int* src = ring + (flushed & (kStageRing - 1)) * 64;
-        if (out + flushed + 16 <= R) {
-          int4_dw* dst = reinterpret_cast<int4_dw*>(point_list + out + flushed);
+  __syncthreads();
+  for (int i0 = 0; i0 < n16; i0 += 16) {
+    // 16 entries: all their LDS reads first, then the ring positions in
+    // registers, then the ring writes, so no write waits on a read
+    unsigned long long mm[16];
+    int id[16];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            int4_dw v;
-            v.x = src[(4 * q) * 64];
-            v.y = src[(4 * q + 1) * 64];
-            v.z = src[(4 * q + 2) * 64];
-            v.w = src[(4 * q + 3) * 64];
-            dst[q] = v;
-          }
-        }
-        flushed += 16;
-      }
+    for (int q = 0; q < 16; q += 2) {
+      const ulonglong2 v = *reinterpret_cast<const ulonglong2*>(s_m + i0 + q);
+      mm[q] = v.x;
+      mm[q + 1] = v.y;
     }
-    __builtin_amdgcn_wave_barrier();
-    cur_m = next_m;
-    cur_id = next_id;
+#pragma unroll
+    for (int q = 0; q < 16; q += 4) {
+      const int4 v = *reinterpret_cast<const int4*>(s_id + i0 + q);
+      id[q] = v.x;
+      id[q + 1] = v.y;
+      id[q + 2] = v.z;
+      id[q + 3] = v.w;
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      ring[(staged & (kStageRing - 1)) * 64] = id[q];
+      staged += (int)mask_bit(mm[q], lane);
+    }
+    if (head > 0 && staged - flushed >= head) {
+      for (int q = 0; q < head; ++q)
+        if (out + flushed + q < R) point_list[out + flushed + q] = ring[((flushed + q) & (kStageRing - 1)) * 64];
+      flushed += head;
+      head = 0;
+    }
+    if (head == 0 && staged - flushed >= 16) {
+      if (out + flushed + 16 <= R) {
+        int4_dw* dst = reinterpret_cast<int4_dw*>(point_list + out + flushed);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          int4_dw v;
+          v.x = ring[((flushed + 4 * q) & (kStageRing - 1)) * 64];
+          v.y = ring[((flushed + 4 * q + 1) & (kStageRing - 1)) * 64];
+          v.z = ring[((flushed + 4 * q + 2) & (kStageRing - 1)) * 64];
+          v.w = ring[((flushed + 4 * q + 3) & (kStageRing - 1)) * 64];
+          dst[q] = v;
+        }
+      }
+      flushed += 16;
+    }
   }
   for (int q = flushed; q < staged; ++q)
     if (out + q < R) point_list[out + q] = ring[(q & (kStageRing - 1)) * 64];

@@ -408,7 +408,7 @@ struct TileCover {
 // Wave w of a preprocess launch owns words [w kBandSlots, (w + 1) kBandSlots)
 // and fills them in lane order; a Gaussian whose bands do not fit its wave's
 // region is not stored (band_off -1) and its consumers recompute its bands.
-constexpr int kBandSlots = 256;
+constexpr int kBandSlots = 512;
 
 __device__ __forceinline__ uint64_t low_bits64(int n) { return n >= 64 ? ~0ull : ((1ull << n) - 1ull); }
 
