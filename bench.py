@@ -95,20 +95,27 @@ def sort_passes(tiles: int) -> int:
     return math.ceil((32 + math.ceil(math.log2(tiles))) / 8)
 
 
-def algorithmic_bytes(N: int, R: float, P: int, T: int, dataflow: str, flow_k: int = 0) -> dict:
+def algorithmic_bytes(N: int, R: float, P: int, T: int, dataflow: str, flow_k: int = 0, entries: float = 0.0,
+                      valid: float = 0.0, sized_scan: bool = False) -> dict:
     """Bytes crossing each stage boundary once (the SH3, depth-on accounting of the
-    reference dataflow): preprocess 112N + SH 228N, scan 8N, duplicate 44N + 12R
-    (64-bit key + value) or 44N + 8R (tile id + value), ranges 8R + 8T (4R + 8T
-    over the depth-then-tile dataflow's 32-bit tile ids), render
-    44R + 24P + 8T, render backward 44R + 28P + 40N + 8T, SH + preprocess
-    backward 624N.  Sorts: the one 64-bit key sort moves 24R per pass over
-    ceil((32 + ceil(log2 T)) / 8) passes; the depth-then-tile dataflow moves 16N
-    per pass over 4 passes for the depth sort and 16R per pass over
-    ceil(log2 T / 8) passes for the tile sort.  The flow render also writes
-    its top-K auxiliaries, 16 K P (id, weight and the two x_mu components)."""
+    reference dataflow): preprocess 112N + SH 228N, scan 8N (24N when it also
+    reads the 16-byte cover words to size the bucketed binning), duplicate
+    44N + 12R (64-bit key + value) or 44N + 8R (tile id + value), ranges
+    8R + 8T (4R + 8T over the depth-then-tile dataflow's 32-bit tile ids),
+    render 44R + 24P + 8T, render backward 44R + 28P + 40N + 8T, SH +
+    preprocess backward 624N.  Sorts: the one 64-bit key sort moves 24R per
+    pass over ceil((32 + ceil(log2 T)) / 8) passes; the depth-then-tile
+    dataflow moves 16N per pass over 4 passes for the depth sort and 16R per
+    pass over ceil(log2 T / 8) passes for the tile sort.  The bucketed binning
+    (E entries of V Gaussians with a valid cover word) sorts depth as above,
+    reads the depth order and the cover words and writes its entries (index +
+    64-bit mask) in `bucket`, 20V + 12E, and reads the entries and writes the
+    point list and ranges in `bucket_tiles`, 12E + 4R + 8T.  The flow render
+    also writes its top-K auxiliaries, 16 K P (id, weight and the two x_mu
+    components)."""
     out = {
         "preprocess": 340.0 * N,
-        "scan": 8.0 * N,
+        "scan": (24.0 if sized_scan else 8.0) * N,
         "ranges": 8.0 * R + 8.0 * T,
         "render": 44.0 * R + 24.0 * P + 8.0 * T + 16.0 * flow_k * P,
         "render_bwd": 44.0 * R + 28.0 * P + 40.0 * N + 8.0 * T,
@@ -117,6 +124,10 @@ def algorithmic_bytes(N: int, R: float, P: int, T: int, dataflow: str, flow_k: i
     if dataflow == "warp_radix":
         out["duplicate"] = 44.0 * N + 12.0 * R
         out["sort"] = sort_passes(T) * 24.0 * R
+    elif dataflow == "buckets":
+        out["depth_sort"] = 4 * 16.0 * N
+        out["bucket"] = 20.0 * valid + 12.0 * entries
+        out["bucket_tiles"] = 12.0 * entries + 4.0 * R + 8.0 * T
     else:
         out["duplicate"] = 44.0 * N + 8.0 * R
         out["depth_sort"] = 4 * 16.0 * N
@@ -656,7 +667,14 @@ def main() -> int:
     if stage_ms and Rs:
         dataflows = set(timer.notes.get("binning_dataflow", []))
         flow_k = _runtime.get_flow_topk() if flow else 0
-        algo = algorithmic_bytes(N, R, P, T, "warp_radix" if dataflows == {"packed_key"} else sort_mode, flow_k)
+        Es, Vs = timer.notes.get("bucket_entries", []), timer.notes.get("bucket_valid", [])
+        E_mean = sum(Es) / len(Es) if Es else 0.0
+        V_mean = sum(Vs) / len(Vs) if Vs else 0.0
+        flow_of = ("warp_radix" if dataflows == {"packed_key"} else "buckets" if dataflows == {"buckets"}
+                   else sort_mode)
+        # a scan that sizes the bucketed binning also reads the cover words
+        sized_scan = "buckets" in dataflows
+        algo = algorithmic_bytes(N, R, P, T, flow_of, flow_k, E_mean, V_mean, sized_scan)
         # The formula counts every pair once per stage.  The backward reads each tile's
         # list only from its largest n_contrib (visited pairs), and the forward stops a
         # slice once all its pixels have stopped: where that happens the formula does not
@@ -685,7 +703,7 @@ def main() -> int:
             shown = entry.get("visited_GBps") if entry["hbm_frac"] is None else gbps
             note = "" if entry["hbm_frac"] is not None else (" (visited pairs)" if shown else " (formula n/a)")
             log(f"[bench]   {name:15s} {ms:8.4f} ms" + ("" if shown is None else f"  {shown:8.1f} GB/s") + note)
-        sort_names = [n for n in ("depth_sort", "sort") if n in stage_ms]
+        sort_names = [n for n in ("depth_sort", "sort", "bucket", "bucket_tiles") if n in stage_ms]
         sort_ms = sum(stage_ms[n] for n in sort_names)
         sort_bytes = sum(algo[n] for n in sort_names)
         binning_sort = {"mode": sort_mode, "stages": sort_names, "ms": round(sort_ms, 4),

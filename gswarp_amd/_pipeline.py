@@ -194,7 +194,7 @@ def preprocess(inputs: RasterInputs, options: ExecutionOptions, *, pack: bool = 
         geom=geom,
         coverage=torch.empty((P, 4), dtype=torch.int32, device=device),
     )
-    if buckets_possible(options, W, H):
+    if buckets_expected(options, W, H, P, device):
         # the bucketed binning reads the banded Gaussians' coverage bands instead of recomputing them
         out.band_store = torch.empty((max(int(lib.gs_band_store_words(P)), 1),), dtype=torch.int32, device=device)
     colors = _f32c(inputs.colors) if inputs.colors.numel() != 0 else None
@@ -235,6 +235,17 @@ def buckets_possible(options: ExecutionOptions, image_width: int, image_height: 
             and grid_x <= BUCKET_MAX_GRID and grid_y <= BUCKET_MAX_GRID)
 
 
+def buckets_expected(options: ExecutionOptions, image_width: int, image_height: int, num_points: int,
+                     device: torch.device) -> bool:
+    """Whether this forward prepares the bucketed binning (BUCKET_SIZING): the
+    preprocess and the binning of one forward agree, since the device's pair
+    count history only changes at the binning's read-back."""
+    if not buckets_possible(options, image_width, image_height):
+        return False
+    return (BUCKET_SIZING == "always"
+            or _workspace.last_pairs(device) > DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN * num_points)
+
+
 def key_layout(P: int, T: int, depth_min: int, depth_max: int) -> KeyLayout:
     """Binning key fields: tile id above the visible depth range's bits above the
     packed point index; the index is carried separately when the three do not fit."""
@@ -263,6 +274,12 @@ DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN = 4
 # tile rectangle is too large for the bucketed binning's cover words).
 HEAVY_DATAFLOW = "buckets"
 BUCKET_MAX_GRID = 255  # tiles per image side the bucketed binning takes
+# When the forward prepares the bucketed binning (the preprocess stores the
+# coverage bands, the scan sizes the entries): "auto" when the last forward on
+# the device had more than DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN pairs per
+# Gaussian (a forward without that history bins by the depth-then-tile sort),
+# "always" on every forward that may take it.
+BUCKET_SIZING = "auto"
 
 
 def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options: ExecutionOptions,
@@ -298,7 +315,7 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
     scan_scratch = torch.empty((max(int(lib.gs_scan_scratch_bytes(P)), 1),), dtype=torch.uint8, device=device)
     # the default mode's scan also sizes the bucketed binning (entries and
     # valid Gaussians in info[2] and info[3]) for the case of many pairs per Gaussian
-    sized = buckets_possible(options, image_width, image_height) and pre.coverage is not None
+    sized = buckets_expected(options, image_width, image_height, P, device) and pre.coverage is not None
     with _stage("scan"):
         if sized:
             lib.call("gs_scan_tiles_entries", P, pre.tiles_touched.data_ptr(), pre.radii.data_ptr(),
@@ -372,6 +389,8 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
         bins = _binning_packed(pre, image_width, image_height, offsets, R, layout, keep_keys, point_list, ranges)
     elif sized and 0 <= entries <= MAX_BINNING_PAIRS:
         _note("binning_dataflow", "buckets")
+        _note("bucket_entries", entries)
+        _note("bucket_valid", valid_points)
         bins = _binning_buckets(pre, image_width, image_height, R, entries, valid_points,
                                 depth_range & 0xFFFFFFFF, depth_range >> 32, keep_keys, ranges)
     else:

@@ -39,6 +39,7 @@ def _spy_calls(monkeypatch):
 def _force_buckets(monkeypatch):
     monkeypatch.setattr(_pipeline, "DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN", 0)
     monkeypatch.setattr(_pipeline, "HEAVY_DATAFLOW", "buckets")
+    monkeypatch.setattr(_pipeline, "BUCKET_SIZING", "always")
 
 
 def _large_splats(device, count=3000, width=960, height=540, seed=3):
@@ -134,11 +135,23 @@ def test_scan_sizes_the_buckets(name, device):
 
 
 def test_default_mode_takes_buckets_for_many_pairs(device, monkeypatch):
-    """Unforced: the heavy-tailed scene (more than four pairs per Gaussian) takes
-    the bucketed binning in the default sort mode and matches the oracle."""
+    """Unforced: a forward of the heavy-tailed scene (more than four pairs per
+    Gaussian) after one with that ratio on the device takes the bucketed
+    binning in the default sort mode and matches the oracle; without the
+    history the forward bins by the depth-then-tile sort, with the same lists."""
+    from gswarp_amd import _workspace
+
     scene = configs.make_scene(3, count=20_000, width=960, height=540, device=device)
-    out, ref = _check_lists(scene, 1, monkeypatch)
-    assert ref["bins"]["num_rendered"] > 4 * scene["means3D"].shape[0]
+    host, ref = oracle_forward(scene)
+    R = ref["bins"]["num_rendered"]
+    assert R > 4 * scene["means3D"].shape[0]
+    monkeypatch.setattr(_workspace, "last_pairs", lambda dev: 0)
+    names = _spy_calls(monkeypatch)
+    out = gpu_forward(scene, options())
+    assert "gs_bin_buckets" not in names and "gs_duplicate_tiles" in names
+    assert np.array_equal(to_np(out["bins"].point_list), ref["bins"]["point_list"])
+    monkeypatch.setattr(_workspace, "last_pairs", lambda dev: R)
+    _check_lists(scene, 1, monkeypatch)
 
 
 def test_oversized_image_falls_back_to_depth_tile(device, monkeypatch):

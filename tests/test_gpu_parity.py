@@ -103,6 +103,7 @@ def test_other_sort_modes_match_oracle(case, sort_mode, device, monkeypatch):
     if sort_mode in ("depth_then_tile", "buckets"):
         monkeypatch.setattr(_pipeline, "DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN", 0)
         monkeypatch.setattr(_pipeline, "HEAVY_DATAFLOW", "depth_tile" if sort_mode == "depth_then_tile" else "buckets")
+        monkeypatch.setattr(_pipeline, "BUCKET_SIZING", "always")
         sort_mode = "warp_depth_stable_tile"
     _check_forward(scene, options(sort_mode=sort_mode))
 
