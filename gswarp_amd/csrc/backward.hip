@@ -72,21 +72,18 @@ __device__ __forceinline__ void wave_fold10(const float (&g)[10], float (&m)[3])
   m[2] = fold16(h4, h4);
 }
 
-// Per-wave LDS ring of Gaussian gradient slots.  A slot holds, for the 12
-// (register, row) positions p = 4 i + r of wave_fold10's output, the 16
-// partial sums of lanes 16 r .. 16 r + 15: float p * 16 + lane % 16, so the
-// three registers are stored at float offsets 0, 64 and 128 from
-// slot + lane (plain stores: the slot belongs to one Gaussian of one wave).
-// A slot is reduced (one float4 and a quad sum per position) and sent to
-// global memory with one atomic per component when it is about to be
-// reused, kRingSlots Gaussians later, and at the end of the tile, so the
-// wave never waits on its own LDS stores.  Two slots already put a whole
-// Gaussian's work between a store and its read-back; more slots cost LDS
-// and with it resident waves.
-constexpr int kRingSlots = 2;
-static_assert(kRingSlots == 2, "the ring's Gaussian ids are kept in two scalar registers");
+// Per-wave LDS slot of a Gaussian's gradient partial sums.  It holds, for
+// the 12 (register, row) positions p = 4 i + r of wave_fold10's output, the
+// 16 partial sums of lanes 16 r .. 16 r + 15: float p * 16 + lane % 16, so
+// the three registers are stored at float offsets 0, 64 and 128 from
+// slot + lane (plain stores: the slot belongs to one wave).  The slot of the
+// previous Gaussian is reduced (one float4 and a quad sum per position) and
+// sent to global memory with one atomic per component just before the next
+// Gaussian's sums are stored, and at the end of the slice: a whole
+// Gaussian's work lies between a store and its read-back, and the slot's
+// address is the same for every Gaussian.
 constexpr int kSlotFloats = 12 * 16;
-constexpr int kRingPad = 64 * 4 - kSlotFloats;  // a whole wave's float4 read of the last slot
+constexpr int kSlotPad = 64 * 4 - kSlotFloats;  // a whole wave's float4 read of the slot
 
 // Component at slot position p (-1: a duplicated row): {0, 1, 5, 6, 2, 3, 7,
 // 8, 4, -1, 9, -1}.
@@ -96,20 +93,37 @@ __device__ __forceinline__ int slot_component(int p) {
   return (r & 1) ? -1 : 4 + 5 * (r >> 1);
 }
 
-// Reduces ring slot k and adds its components to grad_gauss[gid]: lane l
-// reads float4 l of the slot (position l / 4 for l < 48), sums it, and each
-// quad of lanes sums its position's four float4 sums; the quad's first lane
+// Reduces the slot and adds its components to grad_gauss[gid]: lane l reads
+// float4 l of the slot (position l / 4 for l < 48), sums it, and each quad
+// of lanes sums its position's four float4 sums; the quad's first lane
 // issues the atomic of a used, non-zero component.
-__device__ __forceinline__ void flush_slot(const float* ring, int k, int gid, int lane, int comp,
-                                           float* grad_gauss) {
-  // Every lane reads a float4 (the ring is padded so that lanes 48-63 of
-  // the last slot stay inside it); those lanes hold no component.
-  const float4 v = reinterpret_cast<const float4*>(ring + k * kSlotFloats)[lane];
+__device__ __forceinline__ void flush_slot(const float* slot, int gid, int lane, int comp, float* grad_gauss) {
+  // Every lane reads a float4 (the slot is padded so that lanes 48-63 stay
+  // inside it); those lanes hold no component.
+  const float4 v = reinterpret_cast<const float4*>(slot)[lane];
   float t = (v.x + v.y) + (v.z + v.w);
   t = t + dpp_mov<0xB1, 0xF>(t);  // quad_perm [1,0,3,2]
   t = t + dpp_mov<0x4E, 0xF>(t);  // quad_perm [2,3,0,1]
   if ((lane & 3) == 0 && comp >= 0 && t != 0.0f)
     unsafeAtomicAdd(grad_gauss + (size_t)gid * kGradFloats + comp, t);
+}
+
+// A record's pixel classes as thresholds on the bits of q: for q >= +0 (sign
+// bit clear) bits(q) < cand exactly when q <= qcut (a candidate) and
+// bits(q) < sure exactly when q <= qcut - 2 kSureMargin (surely blends);
+// negative q, -0 and NaN have larger bits, and a negative threshold allows
+// nothing (0).  Both are computed from the record's qcut as the visits'
+// float compares would.
+struct BlendThresholds {
+  unsigned cand, sure;
+};
+
+__device__ __forceinline__ BlendThresholds blend_thresholds(float qcut) {
+  const float qsure = qcut - 2.0f * kSureMargin;
+  BlendThresholds t;
+  t.cand = qcut >= 0.0f ? __float_as_uint(qcut) + 1u : 0u;
+  t.sure = qsure >= 0.0f ? __float_as_uint(qsure) + 1u : 0u;
+  return t;
 }
 
 __device__ __forceinline__ int wave_max_i32(int v) {
@@ -168,8 +182,10 @@ __device__ __forceinline__ BwdBatch load_bwd_batch(const RenderBwdParams& p, int
 // the upper left / right, 2 / 3 the lower ones).  Pixels of a lane in one
 // column of blocks share dx to a Gaussian.
 //
-// Per pixel the reverse blend keeps two running values: T, the transmittance
-// in front of the current Gaussian, and S = U . acc, the upstream gradient
+// Per pixel the reverse blend keeps two running values: 1 / T, T the
+// transmittance in front of the current Gaussian (the reference's division
+// T <- T / (1 - alpha) becomes the product 1/T <- (1/T) (1 - alpha), one
+// fused multiply-add, and T = rcp(1/T)), and S = U . acc, the upstream gradient
 // U = (dL/dr, dL/dg, dL/db, dL/ddepth, dL/dalpha) dotted with the
 // accumulated features behind it, acc = (colour, depth, alpha) of everything
 // behind, each Gaussian adding F = (r, g, b, depth, 1) as
@@ -193,11 +209,14 @@ __device__ __forceinline__ BwdBatch load_bwd_batch(const RenderBwdParams& p, int
 // per record, record_box), and only records that may touch it are visited;
 // with kBlockCull each block is tested, and a record's visit skips the
 // blocks its box misses (worth its branches when a slice has four blocks).
-// s_rec (3 x 64 float4) and s_ring (kRingSlots x kSlotFloats + kRingPad
-// floats, 16-byte aligned) are the wave's LDS.
+// The batch's LDS copy of a record carries the candidate and sure-blend
+// thresholds of blend_thresholds in the words the records leave unused, so
+// a visit classifies a pixel with two unsigned compares of q's bits.
+// s_rec (3 x 64 float4) and s_slot (kSlotFloats + kSlotPad floats, 16-byte
+// aligned) are the wave's LDS.
 template <bool kDepth, int kPix, int kCols, bool kBlockCull>
 __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int tile, int sub, float4* s_rec,
-                                                 float* s_ring) {
+                                                 float* s_slot) {
   static_assert(kPix % kCols == 0 && 8 * kCols <= kBlockX && 8 * (kPix / kCols) <= kBlockY, "slice in a tile");
   constexpr int kSliceW = 8 * kCols;
   constexpr int kSliceH = 8 * (kPix / kCols);
@@ -216,7 +235,7 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
   rg.y = imax(rg.x, imin(rg.y, p.num_rendered));
   const int n = rg.y - rg.x;
 
-  float pfy[kPix], T[kPix], S[kPix], gp0[kPix], gp1[kPix], gp2[kPix], gpd[kPix], gpa[kPix];
+  float pfy[kPix], Ti[kPix], S[kPix], gp0[kPix], gp1[kPix], gp2[kPix], gpd[kPix], gpa[kPix];
   int last[kPix];
   int lmax = 0;
 #pragma unroll
@@ -225,11 +244,15 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
     const int py = sy0 + 8 * (k / kCols) + (lane >> 3);
     pfy[k] = (float)py;
     last[k] = 0;
-    T[k] = S[k] = gp0[k] = gp1[k] = gp2[k] = gpd[k] = gpa[k] = 0.0f;
+    Ti[k] = 1.0f;
+    S[k] = gp0[k] = gp1[k] = gp2[k] = gpd[k] = gpa[k] = 0.0f;
     if (px < p.W && py < p.H && n > 0) {
       const int pix = py * p.W + px;
-      last[k] = imax(0, imin(p.n_contrib[pix], n));
-      T[k] = 1.0f - p.out_alpha[pix];
+      const float T0 = 1.0f - p.out_alpha[pix];
+      // With T = 0 every term of the pixel is an exact zero, as for a pixel
+      // that blends nothing (and 1/T would be infinite).
+      last[k] = T0 == 0.0f ? 0 : imax(0, imin(p.n_contrib[pix], n));
+      if (T0 != 0.0f) Ti[k] = 1.0f / T0;
       // absent upstream gradients (null) are zero
       if (p.grad_color) {
         gp0[k] = p.grad_color[pix];
@@ -245,19 +268,27 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
   const int max_lc = __builtin_amdgcn_readfirstlane(wave_max_i32(lmax));
   if (max_lc == 0) return;
   const int flush_comp = lane < kSlotFloats / 4 ? slot_component(lane >> 2) : -1;
-  int nrel = 0;  // Gaussians added to the ring so far
-  int slot_gid0 = 0, slot_gid1 = 0;  // Gaussians of ring slots 0 and 1 (wave-uniform)
+  int slot_gid = -1;  // Gaussian whose sums the slot holds (wave-uniform), -1: none
 
   int bs = imax(0, max_lc - 64);
   BwdBatch next = load_bwd_batch(p, rg.x + bs, max_lc - bs, lane);
   for (int batch_end = max_lc; batch_end > 0; batch_end = bs, bs = imax(0, bs - 64)) {
     const int cnt = batch_end - bs;
     // One wave per workgroup: its LDS queue orders these writes before the
-    // broadcast reads below.
-    s_rec[3 * lane] = next.r0;
-    s_rec[3 * lane + 1] = next.r1;
-    s_rec[3 * lane + 2] = next.r2;
+    // broadcast reads below.  The records' unused words (r1.w holds qcut,
+    // which the visits only need as a threshold, and r2.w) carry the
+    // thresholds.
+    {
+      const BlendThresholds th = blend_thresholds(next.r1.w);
+      s_rec[3 * lane] = next.r0;
+      s_rec[3 * lane + 1] = make_float4(next.r1.x, next.r1.y, next.r1.z, __uint_as_float(th.cand));
+      s_rec[3 * lane + 2] = make_float4(next.r2.x, next.r2.y, next.r2.z, __uint_as_float(th.sure));
+    }
     const int batch_id = next.id;  // lane j: Gaussian of record j
+    // A conic with a <= 0 can give q = -0 (adxx = (a dx) dx = -0), which
+    // the forward's 0 <= q test takes and the bit compares do not; batches
+    // with such a record add the q == 0 lanes to the candidates.
+    const bool signed_zero = __ballot(lane < cnt && !(next.r0.z > 0.0f)) != 0;
     // blk[k]: the batch's records that may touch block k (with kBlockCull;
     // otherwise those that may touch the slice, for every block)
     uint64_t blk[kPix], todo = 0;
@@ -288,6 +319,8 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
       const int pos = bs + jj;
       const float4 a = s_rec[3 * jj];
       const float4 b = s_rec[3 * jj + 1];
+      const float4 f = s_rec[3 * jj + 2];
+      const unsigned thr_cand = __float_as_uint(b.w), thr_sure = __float_as_uint(f.w);
       float dx[kCols], adxx[kCols], b2dx[kCols];
 #pragma unroll
       for (int c = 0; c < kCols; ++c) {
@@ -296,58 +329,49 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
         b2dx[c] = (a.w * dx[c]) * 2.0f;
       }
       float q[kPix], dy[kPix];
-      bool cand[kPix];
-      uint64_t cand_lanes[kPix];  // the wave's lanes with cand[k]
-      uint64_t any_lanes = 0;
+      uint64_t cand_lanes[kPix];  // the wave's lanes whose pixel k is a candidate
+      uint64_t sure_lanes[kPix];  // ... and surely blends
+      uint64_t any_lanes = 0, band = 0;  // band: lanes with a candidate that is not sure
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
         q[k] = dy[k] = 0.0f;
-        cand[k] = false;
-        cand_lanes[k] = 0;
+        cand_lanes[k] = sure_lanes[k] = 0;
         if (kBlockCull && !((blk[k] >> jj) & 1)) continue;  // the record's box misses block k
         const int c = k % kCols;
         dy[k] = a.y - pfy[k];
         q[k] = conic_q_px(adxx[c], b2dx[c], b.x, dy[k]);  // exponent = -0.5 q
-        cand[k] = pos < last[k] && q[k] >= 0.0f && q[k] <= b.w;
-        // the same comparisons as lane masks, ANDed in scalar registers
-        cand_lanes[k] = __builtin_amdgcn_sicmp(pos, last[k], kCmpSLT) & __builtin_amdgcn_fcmpf(q[k], 0.0f, kCmpOGE) &
-                        __builtin_amdgcn_fcmpf(q[k], b.w, kCmpOLE);
+        // Lane masks of pos < last, 0 <= q <= qcut and 0 <= q <= qsure (the
+        // bit compares of blend_thresholds), ANDed in scalar registers.
+        const uint64_t act = __builtin_amdgcn_sicmp(pos, last[k], kCmpSLT);
+        cand_lanes[k] = act & __builtin_amdgcn_uicmp(__float_as_uint(q[k]), thr_cand, kCmpULT);
+        if (signed_zero) cand_lanes[k] |= act & __builtin_amdgcn_fcmpf(q[k], 0.0f, kCmpOEQ);
+        sure_lanes[k] = cand_lanes[k] & __builtin_amdgcn_uicmp(__float_as_uint(q[k]), thr_sure, kCmpULT);
         any_lanes |= cand_lanes[k];
+        band |= cand_lanes[k] & ~sure_lanes[k];
       }
       if (any_lanes == 0) continue;
       // Blend decisions, identical to the forward's: with the exponent above
       // power_cutoff + 2e-3 (q <= qcut - 4e-3) the forward's alpha is provably
       // >= 1/255 (the cutoff sits 1e-3 below -ln(255 o) and exp_sw / log_sw
       // err by < 1e-6 relative), above qcut provably < 1/255; only the thin
-      // band between needs exp_sw.  e = log2 of the Gaussian value G for
-      // pixels that blend, -inf (G = 0) for the others.  The band test is a
-      // lane-mask operation on the two comparisons.
-      const float qsure = b.w - 2.0f * kSureMargin;
+      // band between (and q = -0) needs exp_sw.  e = log2 of the Gaussian
+      // value G for pixels that blend, -inf (G = 0) for the others.
       float e[kPix];
-      uint64_t band = 0;  // lanes with a pixel in the band
 #pragma unroll
-      for (int k = 0; k < kPix; ++k) {
-        // branch-free, so that the blocks' instruction chains interleave (a
-        // block the record's box misses has cand false and gets -inf)
-        const bool sure = q[k] <= qsure;
-        e[k] = (cand[k] && sure) ? q[k] * (-0.5f * kLog2e) : -__builtin_inff();
-        // cand && !sure from the comparisons' lane masks (scalar ANDs; the
-        // compiler reuses the comparisons made above)
-        band |= cand_lanes[k] & ~__builtin_amdgcn_fcmpf(q[k], qsure, kCmpOLE);
-      }
+      for (int k = 0; k < kPix; ++k)
+        e[k] = __builtin_amdgcn_inverse_ballot_w64(sure_lanes[k]) ? q[k] * (-0.5f * kLog2e) : -__builtin_inff();
       if (band != 0) {
 #pragma unroll
         for (int k = 0; k < kPix; ++k) {
           // in the band 0 <= q, so the exponential's argument is non-positive;
           // on other lanes its value (inf or NaN included) is masked out
-          const uint64_t band_lanes = cand_lanes[k] & ~__builtin_amdgcn_fcmpf(q[k], qsure, kCmpOLE);
+          const uint64_t band_lanes = cand_lanes[k] & ~sure_lanes[k];
           const float a_sw = fminf(kAlphaMax, b.y * exp_sw_nonpos(-0.5f * q[k]));
           const bool blends = __builtin_amdgcn_inverse_ballot_w64(
               band_lanes & __builtin_amdgcn_fcmpf(a_sw, kAlphaMin, kCmpOGE));
           e[k] = blends ? q[k] * (-0.5f * kLog2e) : e[k];
         }
       }
-      const float4 f = s_rec[3 * jj + 2];
       // -0 is the additive identity of every float, so the first terms
       // enter the sums exactly (and the compiler drops the additions).
       float sv[kCols], svy[kCols];
@@ -357,18 +381,20 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
         // A block with no candidate in the whole wave is skipped: there G = 0
-        // for every lane, which leaves T, S and the sums unchanged.
+        // for every lane, which leaves 1/T, S and the sums unchanged.
         if (cand_lanes[k] == 0) continue;
         const int c = k % kCols;
         // Gradient values use the hardware exponential (v_exp_f32): they only
         // need the 1e-3 gradient tolerance, the decisions above are exact.
         // A pixel that does not blend this Gaussian gets G = 2^-inf = 0, so
-        // alpha = 0, T * rcp(1) = T, S is unchanged and it adds exact zeros.
+        // alpha = 0, 1/T is unchanged (an exact fma), S is unchanged and it
+        // adds exact zeros.
         const float G = __builtin_amdgcn_exp2f(e[k]);
         const float alpha = fminf(kAlphaMax, b.y * G);
-        // 1 - alpha >= 1 - kAlphaMax: the reference's 1e-5 floor never applies
-        const float oma = 1.0f - alpha;
-        const float Tn = T[k] * __builtin_amdgcn_rcpf(oma);
+        // 1/T in front of this Gaussian: (1/T behind it) (1 - alpha), with
+        // 1 - alpha >= 1 - kAlphaMax (the reference's 1e-5 floor never applies)
+        const float tin = fmaf(-alpha, Ti[k], Ti[k]);
+        const float Tn = __builtin_amdgcn_rcpf(tin);
         float fu = fmaf(f.z, gp2[k], fmaf(f.y, gp1[k], fmaf(f.x, gp0[k], gpa[k])));
         if (kDepth) fu = fmaf(b.z, gpd[k], fu);
         const float d = fu - S[k];
@@ -385,7 +411,7 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
         // this Gaussian joins what lies behind the next (nearer) one:
         // alpha fu + (1 - alpha) S = S + alpha (fu - S)
         S[k] = fmaf(alpha, d, S[k]);
-        T[k] = Tn;
+        Ti[k] = tin;
       }
       // Pixel moments of v about the Gaussian's mean; the conic, opacity
       // and W/2, H/2 factors are per Gaussian and applied once, when the
@@ -413,22 +439,16 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
       g[9] = sd;
       float m[3];
       wave_fold10(g, m);
-      const int k = nrel & (kRingSlots - 1);
-      if (nrel >= kRingSlots) flush_slot(s_ring, k, k ? slot_gid1 : slot_gid0, lane, flush_comp, p.grad_gauss);
-      const int gid = __builtin_amdgcn_readlane(batch_id, jj);
-      if (k)
-        slot_gid1 = gid;
-      else
-        slot_gid0 = gid;
-      float* slot = s_ring + k * kSlotFloats + lane;
-      slot[0] = m[0];
-      slot[64] = m[1];
-      slot[128] = m[2];
-      ++nrel;
+      if (slot_gid >= 0) flush_slot(s_slot, slot_gid, lane, flush_comp, p.grad_gauss);
+      slot_gid = __builtin_amdgcn_readlane(batch_id, jj);
+      // The wave's LDS operations complete in order: these stores follow
+      // the flush's read of the previous Gaussian's sums.
+      s_slot[lane] = m[0];
+      s_slot[64 + lane] = m[1];
+      s_slot[128 + lane] = m[2];
     }
   }
-  if (nrel > 0) flush_slot(s_ring, 0, slot_gid0, lane, flush_comp, p.grad_gauss);
-  if (nrel > 1) flush_slot(s_ring, 1, slot_gid1, lane, flush_comp, p.grad_gauss);
+  if (slot_gid >= 0) flush_slot(s_slot, slot_gid, lane, flush_comp, p.grad_gauss);
 }
 
 // How a tile is split over waves.  With small Gaussians (a few tiles each)
@@ -456,7 +476,7 @@ template <bool kDepth, bool kWholeTiles>
 __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
   constexpr int kFirst = kWholeTiles ? 1 : 2;
   __shared__ float4 s_rec[3 * 64];  // record j at s_rec[3 j .. 3 j + 2]
-  __shared__ __align__(16) float s_ring[kRingSlots * kSlotFloats + kRingPad];
+  __shared__ __align__(16) float s_slot[kSlotFloats + kSlotPad];
   const int first_units = kFirst * p.num_tiles;
   const int extra_units = (4 - kFirst) * p.num_tiles;
   const int seg = xcd_grid(first_units);
@@ -469,11 +489,11 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
   rg.x = imax(0, imin(rg.x, p.num_rendered));
   rg.y = imax(rg.x, imin(rg.y, p.num_rendered));
   if (rg.y - rg.x > p.long_tile)
-    render_bwd_slice<kDepth, 1, 1, false>(p, tile, quadrant, s_rec, s_ring);
+    render_bwd_slice<kDepth, 1, 1, false>(p, tile, quadrant, s_rec, s_slot);
   else if (!extra && kWholeTiles)
-    render_bwd_slice<kDepth, 4, 2, true>(p, tile, 0, s_rec, s_ring);
+    render_bwd_slice<kDepth, 4, 2, true>(p, tile, 0, s_rec, s_slot);
   else if (!extra)
-    render_bwd_slice<kDepth, 2, 1, false>(p, tile, quadrant, s_rec, s_ring);
+    render_bwd_slice<kDepth, 2, 1, false>(p, tile, quadrant, s_rec, s_slot);
 }
 
 struct PreprocessBwdParams {

@@ -58,7 +58,7 @@ constexpr float kAlphaMax = 0.99f;
 
 // Comparison predicates of the lane-mask compare builtins
 // (__builtin_amdgcn_fcmpf / sicmp; LLVM's predicate codes).
-constexpr int kCmpOGE = 3, kCmpOLT = 4, kCmpOLE = 5, kCmpSLT = 40;
+constexpr int kCmpOEQ = 1, kCmpOGE = 3, kCmpOLT = 4, kCmpOLE = 5, kCmpULT = 36, kCmpSLT = 40;
 
 constexpr int kCoverageSnugbox = 0;
 constexpr int kCoverageAccutile = 1;
