@@ -60,7 +60,8 @@ __device__ __forceinline__ float fold16(float a, float b) {
 // Partial transposed reduction of ten per-lane values: two lane-swap folds
 // leave three registers in which row r (lanes 16 r .. 16 r + 15) of
 // register i holds 16 partial sums (over 4 lanes each) of component
-// kSlotComp[4 i + r]; the duplicated rows of the third register are unused.
+// slot_component(4 i + r); the duplicated rows of the third register are
+// unused.
 __device__ __forceinline__ void wave_fold10(const float (&g)[10], float (&m)[3]) {
   const float h0 = fold32(g[0], g[5]);
   const float h1 = fold32(g[1], g[6]);
@@ -70,6 +71,28 @@ __device__ __forceinline__ void wave_fold10(const float (&g)[10], float (&m)[3])
   m[0] = fold16(h0, h1);
   m[1] = fold16(h2, h3);
   m[2] = fold16(h4, h4);
+}
+
+// The same reduction when every lane's pixels lie in one pixel column (a
+// slice one block wide), from the seven per-lane sums of v, v dy, v dy^2
+// and the colour and depth terms.  The first fold adds lanes l and l + 32,
+// which share the column l % 8 and with it dx, so one product by the lane's
+// dx turns the folded (sum v | sum v dy) register into (sum v dx |
+// sum v dx dy) and a second gives sum v dx^2 (its upper half is unused):
+// the three dx moments cost two products instead of three products and
+// two more components to fold.  The depth term enters only the second
+// fold, so its 64 lanes arrive as two positions of 16 partial sums.  Row r
+// of register i holds component slot_component_column(4 i + r).
+__device__ __forceinline__ void wave_fold_column(float sv, float svy, float svyy, float sr, float sg, float sb,
+                                                 float sd, float dx, float (&m)[3]) {
+  const float h0 = fold32(sv, svy);
+  const float h1 = fold32(svyy, sr);
+  const float h2 = fold32(sg, sb);
+  const float hd = h0 * dx;
+  const float hd2 = hd * dx;
+  m[0] = fold16(h0, h1);
+  m[1] = fold16(h2, sd);
+  m[2] = fold16(hd, hd2);
 }
 
 // Per-wave LDS slot of a Gaussian's gradient partial sums.  It holds, for
@@ -91,6 +114,12 @@ __device__ __forceinline__ int slot_component(int p) {
   const int i = p >> 2, r = p & 3;
   if (i < 2) return 2 * i + (r & 1) + 5 * (r >> 1);
   return (r & 1) ? -1 : 4 + 5 * (r >> 1);
+}
+
+// Component at slot position p of wave_fold_column's registers: {5, 4, 1, 6,
+// 7, 9, 8, 9, 0, 2, 3, -1}, stored plus one in the nibbles of a constant.
+__device__ __forceinline__ int slot_component_column(int p) {
+  return (int)((0x431a9a87256ull >> (4 * p)) & 15) - 1;
 }
 
 // Reduces the slot and adds its components to grad_gauss[gid]: lane l reads
@@ -267,7 +296,8 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
   }
   const int max_lc = __builtin_amdgcn_readfirstlane(wave_max_i32(lmax));
   if (max_lc == 0) return;
-  const int flush_comp = lane < kSlotFloats / 4 ? slot_component(lane >> 2) : -1;
+  const int flush_comp =
+      lane < kSlotFloats / 4 ? (kCols == 1 ? slot_component_column(lane >> 2) : slot_component(lane >> 2)) : -1;
   int slot_gid = -1;  // Gaussian whose sums the slot holds (wave-uniform), -1: none
 
   int bs = imax(0, max_lc - 64);
@@ -378,11 +408,9 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
 #pragma unroll
       for (int c = 0; c < kCols; ++c) sv[c] = svy[c] = -0.0f;
       float svyy = -0.0f, sr = -0.0f, sg = -0.0f, sb = -0.0f, sd = -0.0f;
-#pragma unroll
-      for (int k = 0; k < kPix; ++k) {
-        // A block with no candidate in the whole wave is skipped: there G = 0
-        // for every lane, which leaves 1/T, S and the sums unchanged.
-        if (cand_lanes[k] == 0) continue;
+      // One pixel's terms; the sums start at -0, the additive identity of
+      // every float, so the first pixel's terms enter them exactly.
+      auto blend = [&](int k) {
         const int c = k % kCols;
         // Gradient values use the hardware exponential (v_exp_f32): they only
         // need the 1e-3 gradient tolerance, the decisions above are exact.
@@ -412,33 +440,53 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
         // alpha fu + (1 - alpha) S = S + alpha (fu - S)
         S[k] = fmaf(alpha, d, S[k]);
         Ti[k] = tin;
+      };
+      // A block with no candidate in the whole wave is skipped: there G = 0
+      // for every lane, which leaves 1/T, S and the sums unchanged.  With two
+      // blocks, whichever is visited first starts the sums on each path, so
+      // a visit that skips the first block computes no -0 starting values.
+      if constexpr (kPix == 2) {
+        if (cand_lanes[0] != 0) {
+          blend(0);
+          if (cand_lanes[1] != 0) blend(1);
+        } else {
+          blend(1);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < kPix; ++k)
+          if (cand_lanes[k] != 0) blend(k);
       }
       // Pixel moments of v about the Gaussian's mean; the conic, opacity
       // and W/2, H/2 factors are per Gaussian and applied once, when the
       // per-Gaussian backward turns the sums into 2D gradients.
-      float g[kGradFloats];
-      float vdx = sv[0] * dx[0];
-      g[0] = vdx;               // sum v dx
-      g[1] = svy[0];            // sum v dy
-      g[2] = vdx * dx[0];       // sum v dx^2
-      g[3] = svy[0] * dx[0];    // sum v dx dy
-      g[5] = sv[0];             // dL/dopacity
-#pragma unroll
-      for (int c = 1; c < kCols; ++c) {
-        vdx = sv[c] * dx[c];
-        g[0] += vdx;
-        g[1] += svy[c];
-        g[2] = fmaf(vdx, dx[c], g[2]);
-        g[3] = fmaf(svy[c], dx[c], g[3]);
-        g[5] += sv[c];
-      }
-      g[4] = svyy;              // sum v dy^2
-      g[6] = sr;
-      g[7] = sg;
-      g[8] = sb;
-      g[9] = sd;
       float m[3];
-      wave_fold10(g, m);
+      if constexpr (kCols == 1) {
+        wave_fold_column(sv[0], svy[0], svyy, sr, sg, sb, sd, dx[0], m);
+      } else {
+        float g[kGradFloats];
+        float vdx = sv[0] * dx[0];
+        g[0] = vdx;               // sum v dx
+        g[1] = svy[0];            // sum v dy
+        g[2] = vdx * dx[0];       // sum v dx^2
+        g[3] = svy[0] * dx[0];    // sum v dx dy
+        g[5] = sv[0];             // dL/dopacity
+#pragma unroll
+        for (int c = 1; c < kCols; ++c) {
+          vdx = sv[c] * dx[c];
+          g[0] += vdx;
+          g[1] += svy[c];
+          g[2] = fmaf(vdx, dx[c], g[2]);
+          g[3] = fmaf(svy[c], dx[c], g[3]);
+          g[5] += sv[c];
+        }
+        g[4] = svyy;              // sum v dy^2
+        g[6] = sr;
+        g[7] = sg;
+        g[8] = sb;
+        g[9] = sd;
+        wave_fold10(g, m);
+      }
       if (slot_gid >= 0) flush_slot(s_slot, slot_gid, lane, flush_comp, p.grad_gauss);
       slot_gid = __builtin_amdgcn_readlane(batch_id, jj);
       // The wave's LDS operations complete in order: these stores follow
