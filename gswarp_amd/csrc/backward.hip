@@ -117,15 +117,21 @@ __device__ __forceinline__ int slot_component(int p) {
 }
 
 // Component at slot position p of wave_fold_column's registers: {5, 4, 1, 6,
-// 7, 9, 8, 9, 0, 2, 3, -1}, stored plus one in the nibbles of a constant.
+// 7, -1, 8, 9, 0, 2, 3, -1} (position 5, the other half of the depth term,
+// is added to position 7 by flush_slot<true>), stored plus one in the
+// nibbles of a constant.
 __device__ __forceinline__ int slot_component_column(int p) {
-  return (int)((0x431a9a87256ull >> (4 * p)) & 15) - 1;
+  return (int)((0x431a9087256ull >> (4 * p)) & 15) - 1;
 }
 
 // Reduces the slot and adds its components to grad_gauss[gid]: lane l reads
 // float4 l of the slot (position l / 4 for l < 48), sums it, and each quad
 // of lanes sums its position's four float4 sums; the quad's first lane
-// issues the atomic of a used, non-zero component.
+// issues the atomic of a used, non-zero component.  kMergeDepth (the layout
+// of wave_fold_column) first adds position 5's sum to position 7's, the two
+// halves of the depth term: one atomic per address, so the instruction's
+// atomics need a single pass.
+template <bool kMergeDepth>
 __device__ __forceinline__ void flush_slot(const float* slot, int gid, int lane, int comp, float* grad_gauss) {
   // Every lane reads a float4 (the slot is padded so that lanes 48-63 stay
   // inside it); those lanes hold no component.
@@ -133,6 +139,11 @@ __device__ __forceinline__ void flush_slot(const float* slot, int gid, int lane,
   float t = (v.x + v.y) + (v.z + v.w);
   t = t + dpp_mov<0xB1, 0xF>(t);  // quad_perm [1,0,3,2]
   t = t + dpp_mov<0x4E, 0xF>(t);  // quad_perm [2,3,0,1]
+  // t[28] += t[20]: row_shr:8 written to lanes 28-31 only (row 1, bank 3),
+  // the other lanes keep t (one instruction; s_nop 1 covers the DPP read of
+  // the VALU result above)
+  if (kMergeDepth)
+    asm volatile("s_nop 1\n\tv_add_f32_dpp %0, %0, %0 row_shr:8 row_mask:0x2 bank_mask:0x8" : "+v"(t));
   if ((lane & 3) == 0 && comp >= 0 && t != 0.0f)
     unsafeAtomicAdd(grad_gauss + (size_t)gid * kGradFloats + comp, t);
 }
@@ -365,21 +376,25 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
         q[k] = dy[k] = 0.0f;
-        cand_lanes[k] = sure_lanes[k] = 0;
+        cand_lanes[k] = 0;
         if (kBlockCull && !((blk[k] >> jj) & 1)) continue;  // the record's box misses block k
         const int c = k % kCols;
         dy[k] = a.y - pfy[k];
         q[k] = conic_q_px(adxx[c], b2dx[c], b.x, dy[k]);  // exponent = -0.5 q
-        // Lane masks of pos < last, 0 <= q <= qcut and 0 <= q <= qsure (the
-        // bit compares of blend_thresholds), ANDed in scalar registers.
+        // Lane masks of pos < last and 0 <= q <= qcut (the bit compare of
+        // blend_thresholds), ANDed in scalar registers.
         const uint64_t act = __builtin_amdgcn_sicmp(pos, last[k], kCmpSLT);
         cand_lanes[k] = act & __builtin_amdgcn_uicmp(__float_as_uint(q[k]), thr_cand, kCmpULT);
         if (signed_zero) cand_lanes[k] |= act & __builtin_amdgcn_fcmpf(q[k], 0.0f, kCmpOEQ);
-        sure_lanes[k] = cand_lanes[k] & __builtin_amdgcn_uicmp(__float_as_uint(q[k]), thr_sure, kCmpULT);
         any_lanes |= cand_lanes[k];
-        band |= cand_lanes[k] & ~sure_lanes[k];
       }
       if (any_lanes == 0) continue;
+      // ... and 0 <= q <= qsure, only for visits with a candidate
+#pragma unroll
+      for (int k = 0; k < kPix; ++k) {
+        sure_lanes[k] = cand_lanes[k] & __builtin_amdgcn_uicmp(__float_as_uint(q[k]), thr_sure, kCmpULT);
+        band |= cand_lanes[k] & ~sure_lanes[k];
+      }
       // Blend decisions, identical to the forward's: with the exponent above
       // power_cutoff + 2e-3 (q <= qcut - 4e-3) the forward's alpha is provably
       // >= 1/255 (the cutoff sits 1e-3 below -ln(255 o) and exp_sw / log_sw
@@ -487,7 +502,7 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
         g[9] = sd;
         wave_fold10(g, m);
       }
-      if (slot_gid >= 0) flush_slot(s_slot, slot_gid, lane, flush_comp, p.grad_gauss);
+      if (slot_gid >= 0) flush_slot<kCols == 1>(s_slot, slot_gid, lane, flush_comp, p.grad_gauss);
       slot_gid = __builtin_amdgcn_readlane(batch_id, jj);
       // The wave's LDS operations complete in order: these stores follow
       // the flush's read of the previous Gaussian's sums.
@@ -496,7 +511,7 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
       s_slot[128 + lane] = m[2];
     }
   }
-  if (slot_gid >= 0) flush_slot(s_slot, slot_gid, lane, flush_comp, p.grad_gauss);
+  if (slot_gid >= 0) flush_slot<kCols == 1>(s_slot, slot_gid, lane, flush_comp, p.grad_gauss);
 }
 
 // How a tile is split over waves.  With small Gaussians (a few tiles each)
