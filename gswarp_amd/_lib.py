@@ -32,7 +32,7 @@ SIGNATURES = {
     "gs_preprocess_fwd": (
         ctypes.c_int,
         [_i32, _i32, _i32, _vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _f32, _f32, _f32, _i32,
-         _i32, _i32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+         _i32, _i32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     ),
     "gs_band_store_words": (_i64, [_i32]),
     "gs_mark_visible": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp]),
@@ -45,6 +45,11 @@ SIGNATURES = {
     "gs_num_rendered_readback": (ctypes.c_int, [_vp, _vp, _vp]),
     "gs_scan_tiles_entries": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "gs_info_readback": (ctypes.c_int, [_vp, _vp, _i32, _vp]),
+    "gs_scan_state_bytes": (_sz, [_i32]),
+    "gs_scan_state_status_offset": (_i64, [_i32]),
+    "gs_scan_state_status_words": (_i64, [_i32]),
+    "gs_scan_state_prepare": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "gs_scan_tiles_onepass": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _sz, _i32, _i32, _vp]),
     "gs_bin_buckets_workspace_bytes": (_sz, [_i32, _i32, _i64, _i32, _i32]),
     "gs_bin_buckets": (ctypes.c_int, [_i32, _i32, _i64, _i64, _vp, ctypes.c_uint32, ctypes.c_uint32, _vp, _vp, _vp,
                                       _i32, _i32, _vp, _sz, _vp, _vp, _vp, _vp]),

@@ -197,6 +197,9 @@ def preprocess(inputs: RasterInputs, options: ExecutionOptions, *, pack: bool = 
     if buckets_expected(options, W, H, P, device):
         # the bucketed binning reads the banded Gaussians' coverage bands instead of recomputing them
         out.band_store = torch.empty((max(int(lib.gs_band_store_words(P)), 1),), dtype=torch.int32, device=device)
+    if SCAN_ONEPASS and P > 0:
+        # the binning's one-pass scan state, which the preprocess prepares
+        out.scan_state = torch.empty((int(lib.gs_scan_state_bytes(P)) // 8,), dtype=torch.int64, device=device)
     colors = _f32c(inputs.colors) if inputs.colors.numel() != 0 else None
     shs = None
     K = 0
@@ -223,7 +226,7 @@ def preprocess(inputs: RasterInputs, options: ExecutionOptions, *, pack: bool = 
             out.depths.data_ptr(),
             out.proj_2d.data_ptr(), out.conic_2d.data_ptr(), out.conic_2d_inv.data_ptr(),
             out.tiles_touched.data_ptr(), out.coverage.data_ptr(), out.records.data_ptr(), out.clamped.data_ptr(),
-            _lib.ptr(out.band_store), _stream(device))
+            _lib.ptr(out.band_store), _lib.ptr(out.scan_state), _stream(device))
     return out
 
 
@@ -281,6 +284,13 @@ BUCKET_MAX_GRID = 255  # tiles per image side the bucketed binning takes
 # "always" on every forward that may take it.
 BUCKET_SIZING = "auto"
 
+# The binning's point-order scan: one kernel (gs_scan_tiles_onepass, a
+# decoupled look-back over a state that the preprocess prepares) when True,
+# else the two-pass gs_scan_tiles.  SCAN_SPIN_LIMIT bounds each of its waits
+# (sleeps of about 64 cycles); a wait never comes near it in practice.
+SCAN_ONEPASS = True
+SCAN_SPIN_LIMIT = 1 << 20
+
 
 def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options: ExecutionOptions,
             keep_keys: bool = False, pack: bool = False, images: RenderImages | None = None) -> BinningState:
@@ -312,16 +322,23 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
     stream = _stream(device)
     offsets = torch.empty((P,), dtype=torch.int32, device=device)
     info = torch.empty((4,), dtype=torch.int64, device=device)
-    scan_scratch = torch.empty((max(int(lib.gs_scan_scratch_bytes(P)), 1),), dtype=torch.uint8, device=device)
     # the default mode's scan also sizes the bucketed binning (entries and
     # valid Gaussians in info[2] and info[3]) for the case of many pairs per Gaussian
     sized = buckets_expected(options, image_width, image_height, P, device) and pre.coverage is not None
+    scan_state, pre.scan_state = pre.scan_state, None  # a prepared state serves one scan
     with _stage("scan"):
-        if sized:
+        if scan_state is not None:
+            lib.call("gs_scan_tiles_onepass", P, pre.tiles_touched.data_ptr(), offsets.data_ptr(), info.data_ptr(),
+                     scan_state.data_ptr(), scan_state.numel() * 8, int(sized), SCAN_SPIN_LIMIT, stream)
+        elif sized:
+            scan_scratch = torch.empty((max(int(lib.gs_scan_scratch_bytes(P)), 1),), dtype=torch.uint8,
+                                       device=device)
             lib.call("gs_scan_tiles_entries", P, pre.tiles_touched.data_ptr(), pre.radii.data_ptr(),
                      pre.depths.data_ptr(), pre.coverage.data_ptr(), offsets.data_ptr(), info.data_ptr(),
                      scan_scratch.data_ptr(), scan_scratch.numel(), stream)
         else:
+            scan_scratch = torch.empty((max(int(lib.gs_scan_scratch_bytes(P)), 1),), dtype=torch.uint8,
+                                       device=device)
             lib.call("gs_scan_tiles", P, pre.tiles_touched.data_ptr(), None, pre.radii.data_ptr(),
                      pre.depths.data_ptr(), offsets.data_ptr(), info.data_ptr(), scan_scratch.data_ptr(),
                      scan_scratch.numel(), stream)

@@ -26,6 +26,8 @@ class PreprocessOutputs:
     geom: torch.Tensor | None = None  # raw-ABI byte buffer that records and clamped are views of
     coverage: torch.Tensor | None = None  # (N, 4) int32 cover words for the emission, or None (re-derived)
     band_store: torch.Tensor | None = None  # int32 coverage bands of the banded Gaussians, or None
+    # gs_scan_tiles_onepass state that the preprocess prepared (serves one scan), or None
+    scan_state: torch.Tensor | None = None
 
 
 @dataclass(slots=True)

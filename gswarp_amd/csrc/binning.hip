@@ -57,24 +57,6 @@ __device__ __forceinline__ long long block_exclusive_scan_i64(long long v, long 
   return wave_off + inc - v;
 }
 
-__device__ __forceinline__ unsigned wave_min_u32(unsigned v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const unsigned o = __shfl_xor(v, off, 64);
-    v = o < v ? o : v;
-  }
-  return v;
-}
-
-__device__ __forceinline__ unsigned wave_max_u32(unsigned v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const unsigned o = __shfl_xor(v, off, 64);
-    v = o > v ? o : v;
-  }
-  return v;
-}
-
 // The scan runs in two passes over blocks of kScanTile = 4096 Gaussians.
 // Thread t of a block owns elements 4t .. 4t + 3 of each of its four
 // 1024-element chunks, so every load and store of a wave covers 1 KB of
@@ -105,97 +87,171 @@ __device__ __forceinline__ void scan_load4(const int* __restrict__ in, const int
   for (int j = 0; j < 4; ++j) v[j] = src[j] >= 0 ? in[src[j]] : 0;
 }
 
+// All kScanTile elements of the block at `base` (thread t: elements 4t ..
+// 4t + 3 of each chunk), gathered through order when there is one.  A full
+// block with 16-byte aligned arrays (the block-uniform common case) issues
+// its vector loads (and then its gathers) without a branch between them, so
+// they are all in flight together; the last, partial block takes
+// scan_load4 per chunk.
+__device__ __forceinline__ void scan_load_block(const int* __restrict__ in, const int* __restrict__ order,
+                                                long long base, long long n, bool vec, int (&v)[4][4],
+                                                int (&src)[4][4]) {
+  if (vec && base + kScanTile <= n) {
+    int4 x[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      x[k] = *reinterpret_cast<const int4*>((order ? order : in) + base + k * kScanChunk + 4 * threadIdx.x);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i0 = (int)(base + k * kScanChunk + 4 * threadIdx.x);
+      if (order) {
+        src[k][0] = x[k].x; src[k][1] = x[k].y; src[k][2] = x[k].z; src[k][3] = x[k].w;
+      } else {
+        src[k][0] = i0; src[k][1] = i0 + 1; src[k][2] = i0 + 2; src[k][3] = i0 + 3;
+        v[k][0] = x[k].x; v[k][1] = x[k].y; v[k][2] = x[k].z; v[k][3] = x[k].w;
+      }
+    }
+    if (order) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[k][j] = in[src[k][j]];
+    }
+    return;
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) scan_load4(in, order, base + k * kScanChunk + 4 * threadIdx.x, n, vec, v[k], src[k]);
+}
+
 // Per block: the tile-count sum, and the smallest and largest depth bits of
 // the Gaussians with radius > 0 (min ~0u / max 0 when there are none), packed
 // as max << 32 | min.  With an order, the counts are gathered through it and
 // also stored contiguously in `gathered` (when given), so that the apply pass
-// reads them without a second gather.
+// reads them without a second gather.  With coverage it also stores the
+// block's super-tile units of valid cover words (-1 when a Gaussian with
+// tiles has no valid word) and its valid words in block_ev.  Every load of
+// the block is issued before any is used (the radii and depths as 16-byte
+// vectors on the identity order, vec_rd), and the block's totals take one
+// barrier.
 __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(int n, const int* __restrict__ in,
                                                                   const int* __restrict__ order,
                                                                   const int* __restrict__ radii,
                                                                   const float* __restrict__ depths,
                                                                   long long* __restrict__ block_sums,
                                                                   unsigned long long* __restrict__ block_range,
-                                                                  int* __restrict__ gathered, int vec,
+                                                                  int* __restrict__ gathered, int vec, int vec_rd,
                                                                   const int4* __restrict__ coverage,
                                                                   long long* __restrict__ block_ev) {
-  __shared__ long long lds4[kScanThreads / 64];
-  __shared__ unsigned s_min[kScanThreads / 64], s_max[kScanThreads / 64];
+  constexpr int kWaves = kScanThreads / 64;
+  __shared__ long long s_sum[kWaves], s_units[kWaves];
+  __shared__ int s_valid[kWaves], s_bad[kWaves];
+  __shared__ unsigned s_min[kWaves], s_max[kWaves];
   const long long base = (long long)blockIdx.x * kScanTile;
+  int v[4][4], src[4][4];
+  scan_load_block(in, order, base, n, vec != 0, v, src);
+  int r[4][4];
+  float d[4][4];
+  if (radii) {
+    if (vec_rd && base + kScanTile <= n) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const long long i0 = base + k * kScanChunk + 4 * threadIdx.x;
+        const int4 r4 = *reinterpret_cast<const int4*>(radii + i0);
+        const float4 d4 = *reinterpret_cast<const float4*>(depths + i0);
+        r[k][0] = r4.x; r[k][1] = r4.y; r[k][2] = r4.z; r[k][3] = r4.w;
+        d[k][0] = d4.x; d[k][1] = d4.y; d[k][2] = d4.z; d[k][3] = d4.w;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          r[k][j] = src[k][j] >= 0 ? radii[src[k][j]] : 0;
+          d[k][j] = src[k][j] >= 0 ? depths[src[k][j]] : 0.0f;
+        }
+    }
+  }
   long long s = 0;
   unsigned dmin = ~0u, dmax = 0u;
-  long long units = 0;  // with coverage: super-tile units of the block's valid words
-  int valid = 0, bad = 0;  // valid words; Gaussians with tiles but no valid word
+  long long units = 0;
+  int valid = 0, bad = 0;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const long long i0 = base + k * kScanChunk + 4 * threadIdx.x;
-    int v[4], src[4];
-    scan_load4(in, order, i0, n, vec != 0, v, src);
     if (coverage) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         if (i0 + j < n) {
           const CoverWord w = unpack_cover(coverage[i0 + j]);
-          const int u = super_units(w);
-          units += u;
+          units += super_units(w);
           valid += w.valid;
-          bad |= (v[j] > 0 && !w.valid) ? 1 : 0;
+          bad |= (v[k][j] > 0 && !w.valid) ? 1 : 0;
         }
       }
     }
     if (gathered) {
       if (vec && i0 + 3 < n) {
-        *reinterpret_cast<int4*>(gathered + i0) = make_int4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<int4*>(gathered + i0) = make_int4(v[k][0], v[k][1], v[k][2], v[k][3]);
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          if (i0 + j < n) gathered[i0 + j] = v[j];
+          if (i0 + j < n) gathered[i0 + j] = v[k][j];
       }
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      s += v[j];
-      if (radii && src[j] >= 0 && radii[src[j]] > 0) {
-        const unsigned bits = __float_as_uint(depths[src[j]]);
+      s += v[k][j];
+      if (radii && r[k][j] > 0) {
+        const unsigned bits = __float_as_uint(d[k][j]);
         dmin = bits < dmin ? bits : dmin;
         dmax = bits > dmax ? bits : dmax;
       }
     }
   }
+  s = wave_sum_i64(s);
   dmin = wave_min_u32(dmin);
   dmax = wave_max_u32(dmax);
+  if (coverage) {
+    units = wave_sum_i64(units);
+    valid = (int)wave_sum_i64(valid);
+    bad = (int)wave_sum_i64(bad);
+  }
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
+    s_sum[wave] = s;
     s_min[wave] = dmin;
     s_max[wave] = dmax;
+    s_units[wave] = units;
+    s_valid[wave] = valid;
+    s_bad[wave] = bad;
   }
-  long long total;
-  block_exclusive_scan_i64(s, lds4, &total);  // its barriers also order s_min / s_max
-  if (coverage) {
-    long long units_total, valid_total, bad_total;
-    block_exclusive_scan_i64(units, lds4, &units_total);
-    block_exclusive_scan_i64(valid, lds4, &valid_total);
-    block_exclusive_scan_i64(bad, lds4, &bad_total);
-    if (threadIdx.x == 0) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    long long total = 0, units_total = 0, valid_total = 0, bad_total = 0;
+    unsigned mn = ~0u, mx = 0u;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      total += s_sum[w];
+      mn = s_min[w] < mn ? s_min[w] : mn;
+      mx = s_max[w] > mx ? s_max[w] : mx;
+      units_total += s_units[w];
+      valid_total += s_valid[w];
+      bad_total += s_bad[w];
+    }
+    block_sums[blockIdx.x] = total;
+    block_range[blockIdx.x] = ((unsigned long long)mx << 32) | mn;
+    if (coverage) {
       block_ev[2 * blockIdx.x] = bad_total > 0 ? -1 : units_total;
       block_ev[2 * blockIdx.x + 1] = valid_total;
     }
-  }
-  if (threadIdx.x == 0) {
-    block_sums[blockIdx.x] = total;
-    unsigned mn = ~0u, mx = 0u;
-#pragma unroll
-    for (int w = 0; w < kScanThreads / 64; ++w) {
-      mn = s_min[w] < mn ? s_min[w] : mn;
-      mx = s_max[w] > mx ? s_max[w] : mx;
-    }
-    block_range[blockIdx.x] = ((unsigned long long)mx << 32) | mn;
   }
 }
 
 // Inclusive prefix sums of the block's elements: its offset is the sum of the
 // preceding blocks' sums (each block adds them up itself, so no pass runs
-// between the two), then each chunk is scanned and carried into the next.
+// between the two).  The block's elements are loaded first; each thread's
+// four chunks are scanned by one wave scan each and one exchange of the
+// waves' chunk totals (the chunk sums fit int32 whenever the offsets do).
 // The last block also stores the total pair count in info[0] and the visible
 // depth-bit range (max << 32 | min, or 0 when nothing is visible) in
 // info[1].  Offsets are int32 (meaningful when the total fits).  With
@@ -208,81 +264,444 @@ __global__ __launch_bounds__(kScanThreads) void scan_apply_kernel(int n, int nb,
                                                                  const unsigned long long* __restrict__ block_range,
                                                                  int* __restrict__ out, long long* __restrict__ info,
                                                                  int vec, const long long* __restrict__ block_ev) {
-  __shared__ long long lds4[kScanThreads / 64];
-  __shared__ unsigned s_min[kScanThreads / 64], s_max[kScanThreads / 64];
+  constexpr int kWaves = kScanThreads / 64;
+  __shared__ long long s_pre[kWaves];
+  __shared__ int s_tot[kWaves][4];
+  __shared__ long long s_units[kWaves], s_valid[kWaves];
+  __shared__ int s_bad[kWaves];
+  __shared__ unsigned s_min[kWaves], s_max[kWaves];
   const int b = blockIdx.x;
-  const bool last = b == nb - 1;
-  long long pre = 0;
-  unsigned dmin = ~0u, dmax = 0u;
-  for (int j = threadIdx.x; j < (last ? nb : b); j += kScanThreads) {
-    if (j < b) pre += block_sums[j];
-    if (last) {
-      const unsigned long long r = block_range[j];
-      const unsigned mn = (unsigned)r, mx = (unsigned)(r >> 32);
-      dmin = mn < dmin ? mn : dmin;
-      dmax = mx > dmax ? mx : dmax;
-    }
-  }
-  long long pre_total;
-  block_exclusive_scan_i64(pre, lds4, &pre_total);
-  if (last) {
-    dmin = wave_min_u32(dmin);
-    dmax = wave_max_u32(dmax);
-    const int wave = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) {
-      s_min[wave] = dmin;
-      s_max[wave] = dmax;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      unsigned mn = ~0u, mx = 0u;
-#pragma unroll
-      for (int w = 0; w < kScanThreads / 64; ++w) {
-        mn = s_min[w] < mn ? s_min[w] : mn;
-        mx = s_max[w] > mx ? s_max[w] : mx;
-      }
-      info[0] = pre_total + block_sums[b];
-      info[1] = mx >= mn ? (long long)(((unsigned long long)mx << 32) | mn) : 0;
-    }
-    if (block_ev) {
-      long long units = 0, valid = 0, bad = 0;
-      for (int j = threadIdx.x; j < nb; j += kScanThreads) {
-        const long long u = block_ev[2 * j];
-        bad += u < 0 ? 1 : 0;
-        units += u < 0 ? 0 : u;
-        valid += block_ev[2 * j + 1];
-      }
-      long long units_total, valid_total, bad_total;
-      block_exclusive_scan_i64(units, lds4, &units_total);
-      block_exclusive_scan_i64(valid, lds4, &valid_total);
-      block_exclusive_scan_i64(bad, lds4, &bad_total);
-      if (threadIdx.x == 0) {
-        info[2] = bad_total > 0 ? -1 : units_total;
-        info[3] = valid_total;
-      }
-    }
-  }
-  long long carry = pre_total;
   const long long base = (long long)b * kScanTile;
+  int v[4][4], src[4][4];
+  scan_load_block(in, order, base, n, vec != 0, v, src);
+  long long pre = 0;
+  for (int j = threadIdx.x; j < b; j += kScanThreads) pre += block_sums[j];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int t[4], inc[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    v[k][1] += v[k][0];
+    v[k][2] += v[k][1];
+    v[k][3] += v[k][2];
+    t[k] = v[k][3];
+    inc[k] = wave_scan_add_dpp(t[k]);
+  }
+  pre = wave_sum_i64(pre);
+  if (lane == 63) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s_tot[wave][k] = inc[k];
+  }
+  if (lane == 0) s_pre[wave] = pre;
+  __syncthreads();
+  long long pre_total = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) pre_total += s_pre[w];
+  long long run = pre_total;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const long long i0 = base + k * kScanChunk + 4 * threadIdx.x;
-    int v[4], src[4];
-    scan_load4(in, order, i0, n, vec != 0, v, src);
-    v[1] += v[0];
-    v[2] += v[1];
-    v[3] += v[2];
-    long long chunk_total;
-    const long long run = carry + block_exclusive_scan_i64(v[3], lds4, &chunk_total);
+    int before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const int x = s_tot[w][k];
+      all += x;
+      before += w < wave ? x : 0;
+    }
+    const long long off = run + before + (inc[k] - t[k]);
     if (vec && i0 + 3 < n) {
       *reinterpret_cast<int4*>(out + i0) =
-          make_int4((int)(run + v[0]), (int)(run + v[1]), (int)(run + v[2]), (int)(run + v[3]));
+          make_int4((int)(off + v[k][0]), (int)(off + v[k][1]), (int)(off + v[k][2]), (int)(off + v[k][3]));
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        if (i0 + j < n) out[i0 + j] = (int)(run + v[j]);
+        if (i0 + j < n) out[i0 + j] = (int)(off + v[k][j]);
     }
-    carry += chunk_total;
+    run += all;
+  }
+  if (b != nb - 1) return;
+  // The last block: the pair total, the visible depth range and the sizes of
+  // the bucketed binning.
+  unsigned dmin = ~0u, dmax = 0u;
+  long long units = 0, valid = 0;
+  int bad = 0;
+  for (int j = threadIdx.x; j < nb; j += kScanThreads) {
+    const unsigned long long r = block_range[j];
+    const unsigned mn = (unsigned)r, mx = (unsigned)(r >> 32);
+    dmin = mn < dmin ? mn : dmin;
+    dmax = mx > dmax ? mx : dmax;
+    if (block_ev) {
+      const long long u = block_ev[2 * j];
+      bad |= u < 0 ? 1 : 0;
+      units += u < 0 ? 0 : u;
+      valid += block_ev[2 * j + 1];
+    }
+  }
+  dmin = wave_min_u32(dmin);
+  dmax = wave_max_u32(dmax);
+  units = wave_sum_i64(units);
+  valid = wave_sum_i64(valid);
+  bad = (int)wave_sum_i64(bad);
+  if (lane == 0) {
+    s_min[wave] = dmin;
+    s_max[wave] = dmax;
+    s_units[wave] = units;
+    s_valid[wave] = valid;
+    s_bad[wave] = bad;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned mn = ~0u, mx = 0u;
+    long long units_total = 0, valid_total = 0;
+    int bad_total = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      mn = s_min[w] < mn ? s_min[w] : mn;
+      mx = s_max[w] > mx ? s_max[w] : mx;
+      units_total += s_units[w];
+      valid_total += s_valid[w];
+      bad_total += s_bad[w];
+    }
+    info[0] = pre_total + block_sums[b];
+    info[1] = mx >= mn ? (long long)(((unsigned long long)mx << 32) | mn) : 0;
+    if (block_ev) {
+      info[2] = bad_total > 0 ? -1 : units_total;
+      info[3] = valid_total;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// One-pass scan (decoupled look-back) in point order.  Its state holds the
+// per-256-Gaussian aggregates of store_scan_aggregates (kScanAggWords words
+// each; depth range, super-tile units, valid cover words), which the
+// preprocess (or gs_scan_state_prepare) writes, then per block of kScanTile
+// counts a status word (flag in the top two bits: 0 unpublished, kStatusAgg
+// the block's own sum, kStatusIncl the sum of all counts up to its end; value
+// in the low 62 bits) and kPublishedWords published words (kPublished |
+// value: the block's depth range as two words, its units (-1 when a Gaussian
+// with tiles has no valid cover word), its valid words), which must hold
+// zeros when the kernel starts (the same writer clears them).  Each block
+// loads its counts and its 16 aggregates once, publishes its sum and its
+// aggregates, walks back over the preceding status words 256 at a time,
+// adding sums up to the nearest inclusive word, and stores its inclusive
+// word before writing its offsets.  Every word is published on its own (no
+// store waits for another) and crosses blocks through coherent (agent-scope
+// atomic) accesses (a release store would write back the whole L2 of the
+// XCD).  Block nb - 1 stores the pair total in info[0] and, once every
+// block's words are published, totals info[1..3].  Blocks start in index
+// order, so every word a block waits for belongs to a block that is running
+// or done; each wait is nevertheless bounded by spin_limit sleeps: a block
+// whose look-back times out adds up the counts before it directly (slow,
+// same offsets), and a final wait that times out stores the widest depth
+// range (every positive float) and no sizes (info[2] = -1, info[3] = 0),
+// which the callers treat as a Gaussian without a valid cover word.
+constexpr unsigned long long kStatusAgg = 1ull << 62;
+constexpr unsigned long long kStatusIncl = 2ull << 62;
+constexpr unsigned long long kStatusValue = (1ull << 62) - 1;
+constexpr unsigned long long kPublished = 1ull << 63;
+constexpr int kPublishedWords = 4;
+constexpr int kAggPerBlock = kScanTile / kScanAggGaussians;  // 16
+static_assert(kAggPerBlock <= 64, "one lane per aggregate");
+
+// A published word holds a value in [-2^62, 2^62) below its flag bit.
+__device__ __forceinline__ unsigned long long publish(long long v) {
+  return kPublished | ((unsigned long long)v & ~kPublished);
+}
+
+__device__ __forceinline__ long long published_value(unsigned long long w) {
+  return (long long)(w << 1) >> 1;  // sign-extends bit 62
+}
+
+// Agent-scope relaxed atomic accesses: coherent across the XCDs' L2s.
+__device__ __forceinline__ unsigned long long status_load(const unsigned long long* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void status_store(unsigned long long* p, unsigned long long v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Aggregates of 256 consecutive Gaussians for the one-pass scan (the
+// preprocess writes the same from its registers), and the cleared status and
+// published words (fewer than this grid's threads).
+__global__ __launch_bounds__(kScanAggGaussians) void scan_prepare_kernel(int n, const int* __restrict__ tiles,
+                                                                        const int* __restrict__ radii,
+                                                                        const float* __restrict__ depths,
+                                                                        const int4* __restrict__ coverage,
+                                                                        unsigned long long* agg,
+                                                                        unsigned long long* status,
+                                                                        int clear_words) {
+  __shared__ ScanAggLds s_agg;
+  const int i = blockIdx.x * kScanAggGaussians + threadIdx.x;
+  if (i < clear_words) status[i] = 0ull;
+  const bool in_range = i < n;
+  bool visible = false;
+  float depth = 0.0f;
+  int units = 0, valid = 0, bad = 0;
+  if (in_range) {
+    visible = radii != nullptr && radii[i] > 0;
+    depth = visible ? depths[i] : 0.0f;
+    if (coverage) {
+      const CoverWord w = unpack_cover(coverage[i]);
+      units = super_units(w);
+      valid = w.valid;
+      bad = (tiles[i] > 0 && !w.valid) ? 1 : 0;
+    }
+  }
+  store_scan_aggregates(visible, depth, units, valid, bad, s_agg, agg);
+}
+
+__global__ __launch_bounds__(kScanThreads) void scan_onepass_kernel(int n, int nb, const int* __restrict__ in,
+                                                                   const unsigned long long* __restrict__ agg,
+                                                                   int n_agg, int sized,
+                                                                   unsigned long long* status,
+                                                                   unsigned long long* pub, int* __restrict__ out,
+                                                                   long long* __restrict__ info, int vec,
+                                                                   int spin_limit) {
+  constexpr int kWaves = kScanThreads / 64;
+  __shared__ int s_tot[kWaves][4];
+  __shared__ long long s_sum[kWaves], s_units[kWaves], s_valid[kWaves];
+  __shared__ int s_bad[kWaves];
+  __shared__ unsigned s_min[kWaves], s_max[kWaves];
+  __shared__ unsigned long long s_incl[kWaves], s_ready[kWaves], s_part[kWaves];
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const long long base = (long long)b * kScanTile;
+  int v[4][4], src[4][4];
+  scan_load_block(in, nullptr, base, n, vec != 0, v, src);
+  // lane l < kAggPerBlock of the first wave: the block's aggregate l
+  const int ai = b * kAggPerBlock + lane;
+  const bool has_agg = wave == 0 && lane < kAggPerBlock && ai < n_agg;
+  unsigned long long g0 = 0, g1 = 0, g2 = 0;
+  if (has_agg) {
+    g0 = agg[kScanAggWords * ai];
+    g1 = agg[kScanAggWords * ai + 1];
+    g2 = agg[kScanAggWords * ai + 2];
+  }
+  long long s = 0;
+  int t[4], inc[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s += v[k][j];
+    v[k][1] += v[k][0];
+    v[k][2] += v[k][1];
+    v[k][3] += v[k][2];
+    t[k] = v[k][3];
+    inc[k] = wave_scan_add_dpp(t[k]);
+  }
+  s = wave_sum_i64(s);
+  if (lane == 63) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s_tot[wave][k] = inc[k];
+  }
+  if (lane == 0) s_sum[wave] = s;
+  __syncthreads();
+  long long total = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) total += s_sum[w];
+  if (wave == 0) {
+    const unsigned lo = wave_min_u32(has_agg ? (unsigned)g0 : ~0u);
+    const unsigned hi = wave_max_u32(has_agg ? (unsigned)(g0 >> 32) : 0u);
+    const long long units = wave_sum_i64(has_agg && (long long)g1 >= 0 ? (long long)g1 : 0);
+    const long long bad = wave_sum_i64(has_agg && (long long)g1 < 0 ? 1 : 0);
+    const long long valid = wave_sum_i64(has_agg ? (long long)g2 : 0);
+    if (lane == 0) {
+      status_store(status + b, (b == 0 ? kStatusIncl : kStatusAgg) | ((unsigned long long)total & kStatusValue));
+      unsigned long long* q = pub + kPublishedWords * b;
+      status_store(q, publish(lo));
+      status_store(q + 1, publish(hi));
+      status_store(q + 2, publish(bad ? -1 : units));
+      status_store(q + 3, publish(valid));
+    }
+  }
+  // Look-back by the whole block, 256 preceding words per round (thread t:
+  // block j - t), adding sums up to the nearest inclusive word.  Every
+  // decision is block-uniform (taken from the waves' ballots in LDS).
+  unsigned long long prefix = 0;
+  if (b > 0) {
+    int j = b - 1, spins = 0;
+    bool timed_out = false;
+    while (true) {
+      const int idx = j - (int)threadIdx.x;
+      const unsigned long long w = idx >= 0 ? status_load(status + idx) : kStatusIncl;
+      const unsigned long long flag = w & ~kStatusValue;
+      const uint64_t incl = __ballot(flag == kStatusIncl);
+      const uint64_t ready = __ballot(flag != 0);
+      if (lane == 0) {
+        s_incl[wave] = incl;
+        s_ready[wave] = ready;
+      }
+      __syncthreads();
+      // first: the thread of the nearest inclusive word (kScanThreads: none
+      // in this window); every word up to it must be published
+      int first = kScanThreads;
+      bool all_ready = true;
+#pragma unroll
+      for (int q = 0; q < kWaves; ++q) {
+        const uint64_t iq = s_incl[q], rq = s_ready[q];
+        if (first < kScanThreads) continue;
+        if (iq != 0) {
+          const int f = __builtin_ctzll(iq);
+          const uint64_t need = f == 63 ? ~0ull : ((2ull << f) - 1);
+          all_ready = all_ready && (rq & need) == need;
+          first = q * 64 + f;
+        } else {
+          all_ready = all_ready && rq == ~0ull;
+        }
+      }
+      if (!all_ready) {
+        __syncthreads();  // every thread has read the ballots before they are rewritten
+        if (++spins > spin_limit) {
+          timed_out = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        continue;
+      }
+      const unsigned long long part = wave_sum_u64((int)threadIdx.x <= first ? (w & kStatusValue) : 0ull);
+      if (lane == 0) s_part[wave] = part;
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < kWaves; ++q) prefix += s_part[q];
+      const bool found = first < kScanThreads;
+      __syncthreads();  // s_part and the ballots are read before the next round rewrites them
+      if (found) break;
+      j -= kScanThreads;
+    }
+    if (timed_out) {
+      // the counts before the block, added up by the block (four loads in
+      // flight per thread)
+      long long a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+      long long i = threadIdx.x;
+      for (; i + 3 * kScanThreads < base; i += 4 * kScanThreads) {
+        a0 += in[i];
+        a1 += in[i + kScanThreads];
+        a2 += in[i + 2 * kScanThreads];
+        a3 += in[i + 3 * kScanThreads];
+      }
+      for (; i < base; i += kScanThreads) a0 += in[i];
+      const long long direct = wave_sum_i64((a0 + a1) + (a2 + a3));
+      if (lane == 0) s_part[wave] = (unsigned long long)direct;
+      __syncthreads();
+      prefix = 0;
+#pragma unroll
+      for (int q = 0; q < kWaves; ++q) prefix += s_part[q];
+    }
+    if (threadIdx.x == 0) status_store(status + b, kStatusIncl | ((prefix + (unsigned long long)total) & kStatusValue));
+  }
+  long long run = (long long)prefix;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const long long i0 = base + k * kScanChunk + 4 * threadIdx.x;
+    int before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const int x = s_tot[w][k];
+      all += x;
+      before += w < wave ? x : 0;
+    }
+    const long long off = run + before + (inc[k] - t[k]);
+    if (vec && i0 + 3 < n) {
+      *reinterpret_cast<int4*>(out + i0) =
+          make_int4((int)(off + v[k][0]), (int)(off + v[k][1]), (int)(off + v[k][2]), (int)(off + v[k][3]));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (i0 + j < n) out[i0 + j] = (int)(off + v[k][j]);
+    }
+    run += all;
+  }
+  if (b != nb - 1) return;
+  // Block nb - 1: the pair total, and every block's published words.
+  int spins = 0;
+  bool timed_out = false;
+  unsigned mn = ~0u, mx = 0u;
+  long long units = 0, valid = 0;
+  int bad = 0;
+  while (true) {
+    int ready = 1;
+    mn = ~0u;
+    mx = 0u;
+    units = valid = 0;
+    bad = 0;
+    // four blocks' words per thread in flight at once
+    for (int i0 = threadIdx.x; i0 < nb; i0 += 4 * kScanThreads) {
+      unsigned long long w[4][kPublishedWords];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int idx = i0 + r * kScanThreads;
+#pragma unroll
+        for (int c = 0; c < kPublishedWords; ++c)
+          w[r][c] = idx < nb ? status_load(pub + kPublishedWords * idx + c) : kPublished | 0xffffffffull;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (i0 + r * kScanThreads >= nb) continue;
+        ready &= ((w[r][0] & w[r][1] & w[r][2] & w[r][3]) & kPublished) != 0 ? 1 : 0;
+        const unsigned lo = (unsigned)published_value(w[r][0]), hi = (unsigned)published_value(w[r][1]);
+        mn = lo < mn ? lo : mn;
+        mx = hi > mx ? hi : mx;
+        const long long u = published_value(w[r][2]);
+        bad |= u < 0 ? 1 : 0;
+        units += u < 0 ? 0 : u;
+        valid += published_value(w[r][3]);
+      }
+    }
+    if (__syncthreads_and(ready)) break;
+    if (++spins > spin_limit) {
+      timed_out = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  mn = wave_min_u32(mn);
+  mx = wave_max_u32(mx);
+  units = wave_sum_i64(units);
+  valid = wave_sum_i64(valid);
+  bad = (int)wave_sum_i64(bad);
+  if (lane == 0) {
+    s_min[wave] = mn;
+    s_max[wave] = mx;
+    s_units[wave] = units;
+    s_valid[wave] = valid;
+    s_bad[wave] = bad;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned lo = ~0u, hi = 0u;
+    long long units_all = 0, valid_all = 0;
+    int bad_all = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      lo = s_min[w] < lo ? s_min[w] : lo;
+      hi = s_max[w] > hi ? s_max[w] : hi;
+      units_all += s_units[w];
+      valid_all += s_valid[w];
+      bad_all |= s_bad[w];
+    }
+    info[0] = (long long)(prefix + (unsigned long long)total);
+    if (timed_out) {
+      info[1] = (long long)(((unsigned long long)0x7f7fffffu << 32) | 0u);
+      if (sized) {
+        info[2] = -1;
+        info[3] = 0;
+      }
+    } else {
+      info[1] = hi >= lo ? (long long)(((unsigned long long)hi << 32) | lo) : 0;
+      if (sized) {
+        info[2] = bad_all ? -1 : units_all;
+        info[3] = valid_all;
+      }
+    }
   }
 }
 
@@ -732,6 +1151,13 @@ static inline int gs_scan_vec(const void* in, const void* order, const void* out
   return (a & 15) == 0 ? 1 : 0;
 }
 
+// Radii and depths as 16-byte vectors: the identity order and both arrays
+// 16-byte aligned.
+static inline int gs_scan_vec_rd(const void* order, const void* radii, const void* depths) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(radii) | reinterpret_cast<uintptr_t>(depths);
+  return order == nullptr && radii != nullptr && (a & 15) == 0 ? 1 : 0;
+}
+
 // Scratch: the block sums and depth ranges, then room for the counts
 // gathered in the given order.
 static inline size_t gs_scan_block_bytes(int32_t P) {
@@ -760,10 +1186,71 @@ extern "C" int gs_scan_tiles(int32_t P, const int32_t* tiles_touched, const int3
   int* gathered = order ? reinterpret_cast<int*>(static_cast<char*>(scratch) + gs_scan_block_bytes(P)) : nullptr;
   const int vec = gs_scan_vec(tiles_touched, order, offsets, gathered);
   hipLaunchKernelGGL(gs::scan_reduce_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, tiles_touched, order,
-                     radii, depths, block_sums, block_range, gathered, vec, nullptr, nullptr);
+                     radii, depths, block_sums, block_range, gathered, vec, gs_scan_vec_rd(order, radii, depths),
+                     nullptr, nullptr);
   hipLaunchKernelGGL(gs::scan_apply_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, nb,
                      gathered ? gathered : tiles_touched, nullptr, block_sums, block_range, offsets,
                      reinterpret_cast<long long*>(info_dev), vec, nullptr);
+  return gs_status_from_hip(hipGetLastError());
+}
+
+// One-pass scan state: the aggregates of every 256 Gaussians, then per block
+// of kScanTile counts a status word and the published words (zero when the
+// scan starts).
+static inline int64_t gs_scan_agg_words(int32_t P) {
+  return (int64_t)((P + gs::kScanAggGaussians - 1) / gs::kScanAggGaussians) * gs::kScanAggWords;
+}
+extern "C" int64_t gs_scan_state_status_offset(int32_t P) { return P <= 0 ? 0 : gs_scan_agg_words(P); }
+extern "C" int64_t gs_scan_state_status_words(int32_t P) {
+  return P <= 0 ? 0 : (int64_t)gs_scan_blocks(P) * (1 + gs::kPublishedWords);
+}
+extern "C" size_t gs_scan_state_bytes(int32_t P) {
+  return P <= 0 ? 0
+                : ((((size_t)gs_scan_agg_words(P) + (size_t)gs_scan_state_status_words(P)) * sizeof(long long) +
+                    255) &
+                   ~(size_t)255);
+}
+
+extern "C" int gs_scan_state_prepare(int32_t P, const int32_t* tiles_touched, const int32_t* radii,
+                                     const float* depths, const int32_t* coverage, void* state, size_t state_bytes,
+                                     void* stream) {
+  if (P < 0) return GS_ERR_INVALID_ARGUMENT;
+  if (P == 0) return GS_OK;
+  if (!state || (radii == nullptr) != (depths == nullptr) || (coverage != nullptr && tiles_touched == nullptr))
+    return GS_ERR_INVALID_ARGUMENT;
+  if ((reinterpret_cast<uintptr_t>(coverage) & 15) || (reinterpret_cast<uintptr_t>(state) & 7))
+    return GS_ERR_MISALIGNED;
+  if (state_bytes < gs_scan_state_bytes(P)) return GS_ERR_SCRATCH_TOO_SMALL;
+  unsigned long long* agg = static_cast<unsigned long long*>(state);
+  hipLaunchKernelGGL(gs::scan_prepare_kernel, dim3((P + gs::kScanAggGaussians - 1) / gs::kScanAggGaussians),
+                     dim3(gs::kScanAggGaussians), 0, (hipStream_t)stream, P, tiles_touched, radii, depths,
+                     reinterpret_cast<const int4*>(coverage), agg, agg + gs_scan_agg_words(P),
+                     (int)gs_scan_state_status_words(P));
+  return gs_status_from_hip(hipGetLastError());
+}
+
+extern "C" int gs_scan_tiles_onepass(int32_t P, const int32_t* tiles_touched, int32_t* offsets, int64_t* info_dev,
+                                     void* state, size_t state_bytes, int32_t sized, int32_t spin_limit,
+                                     void* stream) {
+  if (P < 0 || !info_dev || spin_limit < 0) return GS_ERR_INVALID_ARGUMENT;
+  hipStream_t s = (hipStream_t)stream;
+  if (P == 0) {
+    hipLaunchKernelGGL(gs::zero_info_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<long long*>(info_dev));
+    if (sized)
+      hipLaunchKernelGGL(gs::zero_info_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<long long*>(info_dev) + 2);
+    return gs_status_from_hip(hipGetLastError());
+  }
+  if (!tiles_touched || !offsets || !state) return GS_ERR_INVALID_ARGUMENT;
+  if (reinterpret_cast<uintptr_t>(state) & 7) return GS_ERR_MISALIGNED;
+  if (state_bytes < gs_scan_state_bytes(P)) return GS_ERR_SCRATCH_TOO_SMALL;
+  const int nb = gs_scan_blocks(P);
+  unsigned long long* agg = static_cast<unsigned long long*>(state);
+  unsigned long long* status = agg + gs_scan_agg_words(P);
+  const int vec = gs_scan_vec(tiles_touched, nullptr, offsets, nullptr);
+  hipLaunchKernelGGL(gs::scan_onepass_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, nb, tiles_touched, agg,
+                     (P + gs::kScanAggGaussians - 1) / gs::kScanAggGaussians, sized ? 1 : 0, status, status + nb,
+                     offsets,
+                     reinterpret_cast<long long*>(info_dev), vec, spin_limit);
   return gs_status_from_hip(hipGetLastError());
 }
 
@@ -794,7 +1281,7 @@ extern "C" int gs_scan_tiles_entries(int32_t P, const int32_t* tiles_touched, co
   long long* block_ev = reinterpret_cast<long long*>(static_cast<char*>(scratch) + gs_scan_block_bytes(P));
   const int vec = gs_scan_vec(tiles_touched, nullptr, offsets, nullptr);
   hipLaunchKernelGGL(gs::scan_reduce_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, tiles_touched, nullptr,
-                     radii, depths, block_sums, block_range, nullptr, vec,
+                     radii, depths, block_sums, block_range, nullptr, vec, gs_scan_vec_rd(nullptr, radii, depths),
                      reinterpret_cast<const int4*>(coverage), block_ev);
   hipLaunchKernelGGL(gs::scan_apply_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, nb, tiles_touched, nullptr,
                      block_sums, block_range, offsets, reinterpret_cast<long long*>(info_dev), vec, block_ev);
@@ -874,7 +1361,8 @@ extern "C" int gs_scan_tiles_static(int32_t P, const int32_t* tiles_touched, con
   unsigned long long* block_range = reinterpret_cast<unsigned long long*>(block_sums + nb);
   const int vec = gs_scan_vec(tiles_touched, order, offsets, nullptr);
   hipLaunchKernelGGL(gs::scan_reduce_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, tiles_touched, order,
-                     radii, depths, block_sums, block_range, nullptr, vec, nullptr, nullptr);
+                     radii, depths, block_sums, block_range, nullptr, vec, gs_scan_vec_rd(order, radii, depths),
+                     nullptr, nullptr);
   hipLaunchKernelGGL(gs::scan_apply_kernel, dim3(nb), dim3(gs::kScanThreads), 0, s, P, nb, tiles_touched, order,
                      block_sums, block_range, offsets, reinterpret_cast<long long*>(info_dev), vec, nullptr);
   return gs_status_from_hip(hipGetLastError());

@@ -46,35 +46,6 @@ __global__ __launch_bounds__(256) void bucket_zero_kernel(int n, int* __restrict
   if (i < n) p[i] = 0;
 }
 
-// Inclusive sum and maximum over the wave with DPP row shifts (rows of 16
-// lanes, no LDS round trip) and the three row totals read back: about a
-// dozen instructions and no memory latency.
-__device__ __forceinline__ int wave_scan_add_dpp(int x) {
-  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
-  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
-  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
-  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
-  const int lane = threadIdx.x & 63;
-  const int r0 = __builtin_amdgcn_readlane(x, 15), r1 = __builtin_amdgcn_readlane(x, 31);
-  const int r2 = __builtin_amdgcn_readlane(x, 47);
-  return x + (lane >= 16 ? r0 : 0) + (lane >= 32 ? r1 : 0) + (lane >= 48 ? r2 : 0);
-}
-
-__device__ __forceinline__ int wave_scan_max_dpp(int x) {
-  x = imax(x, __builtin_amdgcn_update_dpp(-1, x, 0x111, 0xF, 0xF, false));
-  x = imax(x, __builtin_amdgcn_update_dpp(-1, x, 0x112, 0xF, 0xF, false));
-  x = imax(x, __builtin_amdgcn_update_dpp(-1, x, 0x114, 0xF, 0xF, false));
-  x = imax(x, __builtin_amdgcn_update_dpp(-1, x, 0x118, 0xF, 0xF, false));
-  const int lane = threadIdx.x & 63;
-  const int r0 = __builtin_amdgcn_readlane(x, 15), r1 = __builtin_amdgcn_readlane(x, 31);
-  const int r2 = __builtin_amdgcn_readlane(x, 47);
-  int before = -1;
-  if (lane >= 16) before = r0;
-  if (lane >= 32) before = imax(before, r1);
-  if (lane >= 48) before = imax(before, r2);
-  return imax(x, before);
-}
-
 // Sort key of the depth order: the float bits of the depth above the
 // smallest visible depth's bits, plus one, for Gaussians with a valid cover
 // word (positive depths order like their bits); 0 for the others.

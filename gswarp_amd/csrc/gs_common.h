@@ -234,6 +234,97 @@ __device__ __forceinline__ float conic_q_px(float adxx, float b2dx, float c, flo
   return fmaf(fmaf(c, dy, b2dx), dy, adxx);
 }
 
+__device__ __forceinline__ unsigned wave_min_u32(unsigned v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned o = __shfl_xor(v, off, 64);
+    v = o < v ? o : v;
+  }
+  return v;
+}
+
+__device__ __forceinline__ unsigned wave_max_u32(unsigned v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned o = __shfl_xor(v, off, 64);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+__device__ __forceinline__ long long wave_sum_i64(long long v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// The one-pass scan's aggregates of kScanAggGaussians consecutive Gaussians
+// (one 256-thread workgroup, thread t: Gaussian 256 b + t): the smallest
+// and largest float bits of the depths of the visible ones (radius > 0;
+// ~0u / 0 when there are none), the super-tile units of the valid cover
+// words, their number, and whether a Gaussian with tiles has no valid word.
+// Stored as kScanAggWords words at agg + kScanAggWords * b: max << 32 | min,
+// the units (-1 in the last case) and the valid words.  Every thread of the
+// workgroup calls it (it holds a barrier).
+constexpr int kScanAggGaussians = 256;
+constexpr int kScanAggWords = 3;
+
+struct ScanAggLds {
+  unsigned mn[4], mx[4];
+  long long units[4];
+  int valid[4], bad[4];
+};
+
+__device__ __forceinline__ void store_scan_aggregates(bool visible, float depth, int units, int valid, int bad,
+                                                      ScanAggLds& lds, unsigned long long* agg) {
+  const unsigned bits = __float_as_uint(depth);
+  const unsigned mn = wave_min_u32(visible ? bits : ~0u);
+  const unsigned mx = wave_max_u32(visible ? bits : 0u);
+  const long long u = wave_sum_i64(units);
+  const long long v = wave_sum_i64(valid);
+  const long long bd = wave_sum_i64(bad);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    lds.mn[wave] = mn;
+    lds.mx[wave] = mx;
+    lds.units[wave] = u;
+    lds.valid[wave] = (int)v;
+    lds.bad[wave] = (int)bd;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned lo = ~0u, hi = 0u;
+    long long units_all = 0, valid_all = 0;
+    int bad_all = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      lo = lds.mn[w] < lo ? lds.mn[w] : lo;
+      hi = lds.mx[w] > hi ? lds.mx[w] : hi;
+      units_all += lds.units[w];
+      valid_all += lds.valid[w];
+      bad_all |= lds.bad[w];
+    }
+    unsigned long long* q = agg + (size_t)kScanAggWords * blockIdx.x;
+    q[0] = ((unsigned long long)hi << 32) | lo;
+    q[1] = bad_all ? ~0ull : (unsigned long long)units_all;
+    q[2] = (unsigned long long)valid_all;
+  }
+}
+
+// Inclusive sum over the wave with DPP row shifts (rows of 16 lanes, no LDS
+// round trip) and the three row totals read back: about a dozen
+// instructions and no memory latency.
+__device__ __forceinline__ int wave_scan_add_dpp(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  const int lane = threadIdx.x & 63;
+  const int r0 = __builtin_amdgcn_readlane(x, 15), r1 = __builtin_amdgcn_readlane(x, 31);
+  const int r2 = __builtin_amdgcn_readlane(x, 47);
+  return x + (lane >= 16 ? r0 : 0) + (lane >= 32 ? r1 : 0) + (lane >= 48 ? r2 : 0);
+}
+
 // Workgroups are dispatched round-robin over the eight XCDs (each with its
 // own L2).  Mapping workgroup b to tile start(b % 8) + b / 8 gives every XCD
 // one contiguous band of tiles, so neighbouring tiles, which share most of

@@ -48,6 +48,11 @@ struct PreprocessParams {
   float4* records;
   uint8_t* clamped;
   unsigned* band_store;  // kBandSlots words per wave for the banded Gaussians' bands, or null
+  // the binning's one-pass scan state: this kernel writes its per-256-Gaussian
+  // aggregates and clears its status words (or null)
+  unsigned long long* scan_agg;
+  unsigned long long* scan_status;
+  int scan_status_words;
 };
 
 // SH colour of one Gaussian; sh_mem points at its coefficient block (K x 3).
@@ -115,10 +120,15 @@ __device__ __forceinline__ float3 sh_color(const float* __restrict__ sh_mem, int
 // Every lane of the grid stays to the end (lanes past P as culled
 // Gaussians): the tile count is a wave-wide walk.
 __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p) {
+  static_assert(kScanAggGaussians == 256, "one workgroup's Gaussians per scan aggregate");
   __shared__ CoverCountLds s_cover[256 / 64];
+  __shared__ ScanAggLds s_agg;
   const int idx0 = blockIdx.x * blockDim.x + threadIdx.x;
   const bool in_range = idx0 < p.P;
   const int idx = in_range ? idx0 : p.P - 1;  // loads stay in bounds; nothing is stored for it
+  // the next stage's one-pass scan starts from cleared status words (fewer
+  // than this grid's threads)
+  if (p.scan_status != nullptr && idx0 < p.scan_status_words) p.scan_status[idx0] = 0ull;
   const float* __restrict__ V = p.view;
   const float* __restrict__ Pm = p.proj;
   const float mx = p.means3d[3 * idx + 0];
@@ -287,6 +297,18 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p)
   touched = wave_count_covered_tiles(count_it, c_px, c_py, c_aa, c_cc, c_q0, c_q1, c_q2, c_op, c_rad, p.grid_x,
                                      p.grid_y, p.coverage_mode, cover, s_cover[threadIdx.x >> 6], p.band_store,
                                      (idx0 >> 6) * kBandSlots);
+  if (p.scan_agg != nullptr) {
+    // this workgroup's 256 Gaussians for the one-pass scan: depth range,
+    // super-tile units and valid cover words
+    int units = 0, valid = 0, bad = 0;
+    if (p.coverage != nullptr && in_range) {
+      const CoverWord w = unpack_cover(pack_cover(cover));
+      units = super_units(w);
+      valid = w.valid;
+      bad = (touched > 0 && !w.valid) ? 1 : 0;
+    }
+    store_scan_aggregates(in_range && radius > 0, depth, units, valid, bad, s_agg, p.scan_agg);
+  }
   if (!in_range) return;
   if (!visible && p.clamped != nullptr) p.clamped[idx] = 0;
   p.radii[idx] = radius;
@@ -357,8 +379,10 @@ extern "C" int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
                                  float filter_variance, int32_t* radii, float* depths, float* proj_2d,
                                  float* conic_2d,
                                  float* conic_2d_inv, int32_t* tiles_touched, int32_t* coverage,
-                                 float* records, uint8_t* clamped, int32_t* band_store, void* stream) {
+                                 float* records, uint8_t* clamped, int32_t* band_store, int64_t* scan_state,
+                                 void* stream) {
   if (P < 0 || image_width <= 0 || image_height <= 0) return GS_ERR_INVALID_ARGUMENT;
+  if (reinterpret_cast<uintptr_t>(scan_state) & 7) return GS_ERR_MISALIGNED;
   if (band_store != nullptr && (coverage == nullptr || gs_band_store_words(P) > 0x7fffffffLL)) {
     return coverage == nullptr ? GS_ERR_INVALID_ARGUMENT : GS_ERR_OVERFLOW;
   }
@@ -410,6 +434,9 @@ extern "C" int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
   p.records = reinterpret_cast<float4*>(records);
   p.clamped = clamped;
   p.band_store = reinterpret_cast<unsigned*>(band_store);
+  p.scan_agg = reinterpret_cast<unsigned long long*>(scan_state);
+  p.scan_status = p.scan_agg ? p.scan_agg + gs_scan_state_status_offset(P) : nullptr;
+  p.scan_status_words = p.scan_agg ? (int)gs_scan_state_status_words(P) : 0;
   const int blocks = (P + 255) / 256;
   hipLaunchKernelGGL(gs::preprocess_fwd_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, p);
   return gs_status_from_hip(hipGetLastError());

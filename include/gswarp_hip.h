@@ -85,7 +85,10 @@ const char* gs_status_string(int status);
  * tile row or column: lo | hi << 16) of the Gaussians whose word has neither
  * a mask nor a full rectangle, 256 words per wave of 64 Gaussians; such a
  * word then holds the index of its bands (or -1 when they did not fit), and
- * gs_bin_buckets reads them instead of recomputing them.
+ * gs_bin_buckets reads them instead of recomputing them.  scan_state
+ * (optional, gs_scan_state_bytes(P) bytes, 8-byte aligned) is prepared for
+ * gs_scan_tiles_onepass as gs_scan_state_prepare would prepare it from these
+ * outputs, from the values in registers (no launch or read of its own).
  * Replaces: preprocess_ops.py:289-581 (preprocess_gaussians) with
  * preprocess_kernels.py:83-269 (scales/rotations), preprocess_kernels.py:345-477
  * and 604-624 (precomputed covariances), the SH kernel
@@ -100,7 +103,7 @@ int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, const float*
                       int32_t image_width, int32_t image_height, int32_t coverage_mode,
                       float filter_variance, int32_t* radii, float* depths, float* proj_2d, float* conic_2d,
                       float* conic_2d_inv, int32_t* tiles_touched, int32_t* coverage, float* records,
-                      uint8_t* clamped, int32_t* band_store, void* stream);
+                      uint8_t* clamped, int32_t* band_store, int64_t* scan_state, void* stream);
 int64_t gs_band_store_words(int32_t P);
 
 /*
@@ -181,6 +184,34 @@ int gs_scan_tiles_static(int32_t P, const int32_t* tiles_touched, const int32_t*
 int gs_scan_tiles_entries(int32_t P, const int32_t* tiles_touched, const int32_t* radii, const float* depths,
                           const int32_t* coverage, int32_t* offsets, int64_t* info_dev, void* scratch,
                           size_t scratch_bytes, void* stream);
+
+/*
+ * The point-order scan of gs_scan_tiles, and with sized != 0 the bucketed
+ * binning's sizes of gs_scan_tiles_entries (info[0..3]), in one kernel that
+ * reads only tiles_touched: a decoupled look-back over blocks of 4096
+ * Gaussians.  The depth range and the sizes come from the state, which
+ * gs_scan_state_prepare (from radii, depths and, for the sizes, the cover
+ * words) or gs_preprocess_fwd (scan_state) prepares: per 256 Gaussians their
+ * depth range, super-tile units and valid cover words, and five zero words
+ * per 4096 (gs_scan_state_status_words(P) int64 from word
+ * gs_scan_state_status_offset(P)).  A state serves one scan.  Every wait of
+ * a block on its predecessors is bounded by spin_limit sleeps (about 64
+ * cycles each; 2^20 is far beyond any normal wait): a block whose look-back
+ * times out adds up the counts before it itself (slower, same offsets), and
+ * a final wait that times out stores info[1] = the widest depth range (every
+ * positive float) and info[2] = -1, info[3] = 0, as for a Gaussian without a
+ * valid cover word.  Otherwise outputs equal gs_scan_tiles'
+ * (gs_scan_tiles_entries').
+ * Concurrent calls must use distinct states.
+ * Replaces: memory.py:539-551 and binning_ops.py:62-81, as gs_scan_tiles.
+ */
+size_t gs_scan_state_bytes(int32_t P);
+int64_t gs_scan_state_status_offset(int32_t P);
+int64_t gs_scan_state_status_words(int32_t P);
+int gs_scan_state_prepare(int32_t P, const int32_t* tiles_touched, const int32_t* radii, const float* depths,
+                          const int32_t* coverage, void* state, size_t state_bytes, void* stream);
+int gs_scan_tiles_onepass(int32_t P, const int32_t* tiles_touched, int32_t* offsets, int64_t* info_dev,
+                          void* state, size_t state_bytes, int32_t sized, int32_t spin_limit, void* stream);
 
 /*
  * Copies count (1 to 16) int64 at info_dev into pinned host memory and waits

@@ -135,7 +135,9 @@ def test_no_provision_after_a_depth_then_tile_forward(device, monkeypatch):
     names = _spy_calls(monkeypatch)
     _, result = _forward(scene, options())
     assert "gs_readback_bin_packed" not in names and "gs_info_readback" in names
-    assert "gs_scan_tiles_entries" in names and "gs_bin_buckets" in names
+    # the sizing scan: one pass by default (its state cleared by the preprocess), else two
+    scan = "gs_scan_tiles_onepass" if _pipeline.SCAN_ONEPASS else "gs_scan_tiles_entries"
+    assert scan in names and "gs_bin_buckets" in names
     assert not result.state.binning.rendered
     _check_against_oracle(scene, result, ref)
 
