@@ -98,8 +98,9 @@ def sort_passes(tiles: int) -> int:
 def algorithmic_bytes(N: int, R: float, P: int, T: int, dataflow: str, flow_k: int = 0, entries: float = 0.0,
                       valid: float = 0.0, sized_scan: bool = False) -> dict:
     """Bytes crossing each stage boundary once (the SH3, depth-on accounting of the
-    reference dataflow): preprocess 112N + SH 228N, scan 8N (24N when it also
-    reads the 16-byte cover words to size the bucketed binning), duplicate
+    reference dataflow): preprocess 112N + SH 228N, scan 8N (the two-pass
+    scan that sizes the bucketed binning also reads the 16-byte cover words,
+    24N; the one-pass scan takes the sizes from the preprocess), duplicate
     44N + 12R (64-bit key + value) or 44N + 8R (tile id + value), ranges
     8R + 8T (4R + 8T over the depth-then-tile dataflow's 32-bit tile ids),
     render 44R + 24P + 8T, render backward 44R + 28P + 40N + 8T, SH +
@@ -689,8 +690,8 @@ def main() -> int:
         V_mean = sum(Vs) / len(Vs) if Vs else 0.0
         flow_of = ("warp_radix" if dataflows == {"packed_key"} else "buckets" if dataflows == {"buckets"}
                    else sort_mode)
-        # a scan that sizes the bucketed binning also reads the cover words
-        sized_scan = "buckets" in dataflows
+        # the two-pass sizing scan reads the cover words; the one-pass scan does not
+        sized_scan = "buckets" in dataflows and not _pipeline.SCAN_ONEPASS
         algo = algorithmic_bytes(N, R, P, T, flow_of, flow_k, E_mean, V_mean, sized_scan)
         # The formula counts every pair once per stage.  The backward reads each tile's
         # list only from its largest n_contrib (visited pairs), and the forward stops a
