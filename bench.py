@@ -31,6 +31,11 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, GB/s
+# VALU issue peak: 256 CUs x 4 SIMDs, one wave64 instruction per SIMD every 4 cycles (16 lanes)
+# at the 2.4 GHz peak engine clock, in wave instructions per second.  A stream of independent
+# fp32 FMAs reaches 94% of it on one MI355X, v_exp_f32 / v_rcp_f32 half of that.
+VALU_SIMDS = 1024
+VALU_PEAK_INSTS = VALU_SIMDS * 2.4e9 / 4
 METRIC = "fwd+bwd ms/iter & Gaussians/s @1M Gaussians 1080p SH3; % HBM roofline"
 
 
@@ -174,6 +179,46 @@ def read_traffic(stage: str, config: int = 2):
             except ValueError:
                 return None
     return None
+
+
+def read_valu_insts(stage: str, config: int = 2):
+    """VALU wave instructions per launch of a stage's kernel (the variant with the
+    most dispatches) from the committed SQ counter summary, if present."""
+    path = ROOT / "profiles" / f"sq_counters_config{config}.txt"
+    if not path.exists():
+        return None
+    columns, best = None, None
+    for line in path.read_text().splitlines():
+        if line.startswith("# SQ counters per dispatch"):
+            columns = [c.strip() for c in line.split("columns:", 1)[1].split(",")]
+            continue
+        if line.startswith("#") or columns is None:
+            continue
+        tokens = line.split()
+        values = tokens[-(len(columns) - 1):]
+        name = " ".join(tokens[:len(tokens) - len(values)])
+        if _stage_of(name, config) != stage:
+            continue
+        row = dict(zip(columns[1:], values))
+        try:
+            dispatches, insts = float(row["dispatches"]), float(row["SQ_INSTS_VALU"])
+        except (KeyError, ValueError):
+            continue
+        if best is None or dispatches > best[0]:
+            best = (dispatches, insts)
+    return None if best is None else best[1]
+
+
+def valu_issue(stage: str, ms: float, config: int = 2):
+    """The stage's VALU issue rate against VALU_PEAK_INSTS, from the committed
+    instruction count and this run's stage time (transcendentals take four
+    issue slots and are counted once, so the true busy share is higher)."""
+    insts = read_valu_insts(stage, config)
+    if insts is None or ms <= 0:
+        return None
+    rate = insts / (ms * 1e-3)
+    return {"insts_per_launch": insts, "achieved": round(rate / 1e9, 1), "peak": round(VALU_PEAK_INSTS / 1e9, 1),
+            "unit": "G wave-instructions/s", "frac": round(rate / VALU_PEAK_INSTS, 4)}
 
 
 def measure_copy_bandwidth(device, nbytes: int = 1 << 30, reps: int = 5) -> float:
@@ -717,6 +762,10 @@ def main() -> int:
             if traffic is not None:
                 entry["counter_bytes"] = traffic
                 entry["counter_hbm_frac"] = round(traffic / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)
+            if name == "render_bwd":  # VALU-issue-bound (the forward issues instructions cheaper than an FMA)
+                valu = valu_issue(name, ms, args.config)
+                if valu is not None:
+                    entry["valu_issue"] = valu
             stages[name] = entry
             shown = entry.get("visited_GBps") if entry["hbm_frac"] is None else gbps
             note = "" if entry["hbm_frac"] is not None else (" (visited pairs)" if shown else " (formula n/a)")
@@ -744,6 +793,9 @@ def main() -> int:
         if "visited_GBps" in stages[dominant]:
             roofline["visited_achieved"] = stages[dominant]["visited_GBps"]
             roofline["visited_frac"] = stages[dominant]["visited_hbm_frac"]
+        if "valu_issue" in stages[dominant]:
+            # the bound that binds: VALU issue (the bytes' fraction is reported as the contract asks)
+            roofline["valu_issue"] = stages[dominant]["valu_issue"]
     copy_gbps = measure_copy_bandwidth(device)
     log(f"[bench] device copy bandwidth {copy_gbps:.0f} GB/s")
     if roofline is not None:
