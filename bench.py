@@ -31,11 +31,13 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, GB/s
-# VALU issue peak: 256 CUs x 4 SIMDs, one wave64 instruction per SIMD every 4 cycles (16 lanes)
-# at the 2.4 GHz peak engine clock, in wave instructions per second.  A stream of independent
-# fp32 FMAs reaches 94% of it on one MI355X, v_exp_f32 / v_rcp_f32 half of that.
+# VALU issue peak: 256 CUs x 4 SIMDs, one wave64 instruction per SIMD every 2 cycles (the
+# 157.3 TFLOP/s fp32 vector rate) at the 2.4 GHz peak engine clock, in wave instructions per
+# second.  Measured on one MI355X: fp32 add / mul / fma with VGPR or literal operands issue at
+# 2.1-2.8 cycles; with an SGPR operand, and compares, selects, min / max, conversions and DPP, at
+# about 4; v_exp_f32, v_rcp_f32 and the lane-swap permutes at about 8.
 VALU_SIMDS = 1024
-VALU_PEAK_INSTS = VALU_SIMDS * 2.4e9 / 4
+VALU_PEAK_INSTS = VALU_SIMDS * 2.4e9 / 2
 METRIC = "fwd+bwd ms/iter & Gaussians/s @1M Gaussians 1080p SH3; % HBM roofline"
 
 
@@ -211,8 +213,9 @@ def read_valu_insts(stage: str, config: int = 2):
 
 def valu_issue(stage: str, ms: float, config: int = 2):
     """The stage's VALU issue rate against VALU_PEAK_INSTS, from the committed
-    instruction count and this run's stage time (transcendentals take four
-    issue slots and are counted once, so the true busy share is higher)."""
+    instruction count and this run's stage time (slower instruction forms take
+    two to four times the issue time of the fastest and are counted once, so a
+    mix with them cannot reach 1.0)."""
     insts = read_valu_insts(stage, config)
     if insts is None or ms <= 0:
         return None

@@ -161,8 +161,8 @@ struct BlendThresholds {
 __device__ __forceinline__ BlendThresholds blend_thresholds(float qcut) {
   const float qsure = qcut - 2.0f * kSureMargin;
   BlendThresholds t;
-  t.cand = qcut >= 0.0f ? __float_as_uint(qcut) + 1u : 0u;
-  t.sure = qsure >= 0.0f ? __float_as_uint(qsure) + 1u : 0u;
+  t.cand = cand_threshold(qcut);
+  t.sure = cand_threshold(qsure);
   return t;
 }
 
@@ -318,10 +318,11 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
     // One wave per workgroup: its LDS queue orders these writes before the
     // broadcast reads below.  The records' unused words (r1.w holds qcut,
     // which the visits only need as a threshold, and r2.w) carry the
-    // thresholds.
+    // thresholds, and r0.w holds 2b (the visits need b only as 2 b dx, and
+    // (2b) dx rounds exactly as (b dx) 2).
     {
       const BlendThresholds th = blend_thresholds(next.r1.w);
-      s_rec[3 * lane] = next.r0;
+      s_rec[3 * lane] = make_float4(next.r0.x, next.r0.y, next.r0.z, 2.0f * next.r0.w);
       s_rec[3 * lane + 1] = make_float4(next.r1.x, next.r1.y, next.r1.z, __uint_as_float(th.cand));
       s_rec[3 * lane + 2] = make_float4(next.r2.x, next.r2.y, next.r2.z, __uint_as_float(th.sure));
     }
@@ -367,7 +368,7 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
       for (int c = 0; c < kCols; ++c) {
         dx[c] = a.x - pfx[c];
         adxx[c] = a.z * dx[c] * dx[c];
-        b2dx[c] = (a.w * dx[c]) * 2.0f;
+        b2dx[c] = a.w * dx[c];  // a.w = 2b
       }
       float q[kPix], dy[kPix];
       uint64_t cand_lanes[kPix];  // the wave's lanes whose pixel k is a candidate
@@ -411,7 +412,7 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
           // in the band 0 <= q, so the exponential's argument is non-positive;
           // on other lanes its value (inf or NaN included) is masked out
           const uint64_t band_lanes = cand_lanes[k] & ~sure_lanes[k];
-          const float a_sw = fminf(kAlphaMax, b.y * exp_sw_nonpos(-0.5f * q[k]));
+          const float a_sw = fminf(kAlphaMax, b.y * exp_sw_q(q[k]));
           const bool blends = __builtin_amdgcn_inverse_ballot_w64(
               band_lanes & __builtin_amdgcn_fcmpf(a_sw, kAlphaMin, kCmpOGE));
           e[k] = blends ? q[k] * (-0.5f * kLog2e) : e[k];

@@ -95,47 +95,53 @@ __host__ __device__ __forceinline__ int f2i(float f) {
   return (int)f;
 }
 
-// exp(x) by Cody-Waite range reduction x = n*ln2 + r (|r| <= ln2/2, ln2 split
-// into an exact 9-bit head and a tail) followed by the degree-7 Taylor
-// polynomial of e^r in Horner form and an exact scaling by 2^n.  Every step
-// is a single correctly rounded fused multiply-add, so a host evaluating the
-// same fmaf sequence reproduces the result bit for bit.  Results are within
-// 2 ulp of exp(x) for x in [-87, 88]; x < -87 returns 0 (the result would be
-// below 1.7e-38 and only ever feeds an alpha < 1/255 decision).
-__device__ __forceinline__ float exp_sw(float x) {
-  if (x < -87.0f) return 0.0f;
-  if (x > 88.0f) x = 88.0f;
-  const float n = rintf(x * 1.44269504088896341f);
-  float r = fmaf(n, -0.693359375f, x);
-  r = fmaf(n, 2.12194440e-4f, r);
-  float p = 1.98412698e-4f;          // 1/5040
-  p = fmaf(p, r, 1.38888889e-3f);    // 1/720
-  p = fmaf(p, r, 8.33333333e-3f);    // 1/120
-  p = fmaf(p, r, 4.16666667e-2f);    // 1/24
-  p = fmaf(p, r, 1.66666667e-1f);    // 1/6
-  p = fmaf(p, r, 0.5f);
-  p = fmaf(p, r, 1.0f);
-  p = fmaf(p, r, 1.0f);
-  return ldexpf(p, (int)n);
-}
+// Software exponential of the blend loops.  exp(x), x <= 0, is defined as
+// Cody-Waite range reduction x = n ln2 + r, |r| <= ln2/2, with n the integer
+// nearest to x log2(e) (one fused multiply-add onto 1.5 * 2^23, which leaves
+// n in the low mantissa bits, then one exact subtraction) and ln2 split into
+// an exact 9-bit head and a tail; then a degree-6 minimax polynomial of e^r
+// (relative error 3.6e-9 on |r| <= ln2/2; coefficients from Lawson's
+// iteration, rounded to float) in Horner form and an exact scaling by 2^n:
+//   t = fma(x, log2e, 1.5*2^23), n = t - 1.5*2^23,
+//   r = fma(n, -ln2_lo, fma(n, -ln2_hi, x)),
+//   p = fma(...fma(fma(c6, r, c5), r, c4)..., r, 1), exp = p 2^n.
+// Every step is one correctly rounded operation, so a host evaluating the same
+// sequence reproduces the result bit for bit; against a long double exp it is
+// within 0.9 ulp at every float of [-87, 0].  Below -87 it is defined as 0
+// (the result would be below 1.7e-38 and only ever feeds an alpha < 1/255
+// decision), and the loops never evaluate it there.
+//
+// exp_sw_q(q) evaluates exp(-q/2) of the loops' quadratic forms, q in
+// [-0, 174] (they need it only where 0 <= q <= qcut, and qcut = -2
+// power_cutoff <= 174), by the same operations on q = -2x with every
+// intermediate scaled by a power of two, which commutes with each rounding:
+// the product q (-log2(e)/2), the reduced argument carried as rho = -2r and
+// the polynomial in rho with the coefficients c_k (-1/2)^k.  2^n is applied
+// by adding n << 23 to the exponent field (t's bits << 23 equal n << 23
+// modulo 2^32, since 1.5 * 2^23 contributes only bits at or above 2^45); for
+// q <= 174 the result is a normal number, so this is exact.  The result is
+// bit-identical to the x form at x = -q/2 (checked at every float of
+// [-87, 0]) and needs no conversion, rounding or ldexp instruction.  For q
+// outside the range the value is unspecified; the loops mask such lanes out.
+constexpr float kExpMagic = 12582912.0f;  // 1.5 * 2^23
+constexpr float kExpLog2e = 1.44269504088896341f;
+constexpr float kExpLn2Hi = 0.693359375f;
+constexpr float kExpLn2Lo = -2.12194440e-4f;
+constexpr float kExpC2 = 0x1.fffffcp-2f, kExpC3 = 0x1.555492p-3f, kExpC4 = 0x1.5558f2p-5f, kExpC5 = 0x1.123a2p-7f,
+                kExpC6 = 0x1.6a23dp-10f;
 
-// exp_sw restricted to x in [-87, 0], where its two range guards are no-ops:
-// the same fmaf sequence, so the result is bit-identical to exp_sw(x).  The
-// render loops only evaluate exponents in [power_cutoff, 0] and power_cutoff
-// is never below -87.
-__device__ __forceinline__ float exp_sw_nonpos(float x) {
-  const float n = rintf(x * 1.44269504088896341f);
-  float r = fmaf(n, -0.693359375f, x);
-  r = fmaf(n, 2.12194440e-4f, r);
-  float p = 1.98412698e-4f;
-  p = fmaf(p, r, 1.38888889e-3f);
-  p = fmaf(p, r, 8.33333333e-3f);
-  p = fmaf(p, r, 4.16666667e-2f);
-  p = fmaf(p, r, 1.66666667e-1f);
-  p = fmaf(p, r, 0.5f);
-  p = fmaf(p, r, 1.0f);
-  p = fmaf(p, r, 1.0f);
-  return ldexpf(p, (int)n);
+__device__ __forceinline__ float exp_sw_q(float q) {
+  const float t = fmaf(q, -0.5f * kExpLog2e, kExpMagic);
+  const float n = t - kExpMagic;
+  float rho = fmaf(n, 2.0f * kExpLn2Hi, q);
+  rho = fmaf(n, 2.0f * kExpLn2Lo, rho);
+  float p = fmaf(kExpC6 * (1.0f / 64.0f), rho, kExpC5 * (-1.0f / 32.0f));
+  p = fmaf(p, rho, kExpC4 * (1.0f / 16.0f));
+  p = fmaf(p, rho, kExpC3 * (-1.0f / 8.0f));
+  p = fmaf(p, rho, kExpC2 * (1.0f / 4.0f));
+  p = fmaf(p, rho, -0.5f);
+  p = fmaf(p, rho, 1.0f);
+  return __uint_as_float(__float_as_uint(p) + (__float_as_uint(t) << 23));
 }
 
 // ln(y) for finite y > 0: y = m * 2^e with m in [sqrt(1/2), sqrt(2)), then
@@ -162,9 +168,9 @@ __device__ __forceinline__ float log_sw(float y) {
 }
 
 // Largest exponent below which o*exp(power) < 1/255 holds for every power,
-// with a 1e-3 margin that covers exp_sw and product rounding (relative error
+// with a 1e-3 margin that covers exp_sw_q and product rounding (relative error
 // < 1e-6).  Returns FLT_MAX when the Gaussian can never reach the alpha
-// cut-off.  Never below -87: exp_sw is 0 there, so alpha is 0 and skipping
+// cut-off.  Never below -87: the software exponential is 0 there, so alpha is 0 and skipping
 // those exponents changes no decision either.
 __device__ __forceinline__ float power_cutoff(float opacity) {
   const float o255 = 255.0f * opacity;
@@ -232,6 +238,16 @@ __device__ __forceinline__ float quad_cutoff(float opacity) { return -2.0f * pow
 // q = fma(fma(c, dy, b2dx), dy, adxx); the exponent is -0.5 q (exact).
 __device__ __forceinline__ float conic_q_px(float adxx, float b2dx, float c, float dy) {
   return fmaf(fmaf(c, dy, b2dx), dy, adxx);
+}
+
+// The candidate test 0 <= q <= qcut as one unsigned compare of q's bits: for
+// q >= +0 (sign bit clear) bits(q) < cand_threshold(qcut) exactly when
+// q <= qcut; negative q, -0 and NaN have larger bits, and a negative or NaN
+// qcut allows nothing (0).  q = -0 passes the float test but not this one; it
+// needs a <= 0 (adxx = (a dx) dx is then -0 for dx = 0), so the loops add the
+// q == 0 lanes only for batches holding such a conic.
+__device__ __forceinline__ unsigned cand_threshold(float qcut) {
+  return qcut >= 0.0f ? __float_as_uint(qcut) + 1u : 0u;
 }
 
 __device__ __forceinline__ unsigned wave_min_u32(unsigned v) {

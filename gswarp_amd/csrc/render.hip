@@ -138,11 +138,18 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
     if (live == 0) break;
     const int cnt = imin(64, n - base);
     // One wave per workgroup: LDS writes and the broadcast reads below are
-    // ordered by the wave's own in-order LDS queue, no barrier needed.
-    s_rec[3 * lane] = next.r0;
-    s_rec[3 * lane + 1] = next.r1;
+    // ordered by the wave's own in-order LDS queue, no barrier needed.  The
+    // LDS copy holds 2b in r0.w (the visits need b only as 2 b dx, and
+    // (2b) dx rounds exactly as (b dx) 2) and qcut as its bound on q's bits
+    // in r1.w (cand_threshold).
+    s_rec[3 * lane] = make_float4(next.r0.x, next.r0.y, next.r0.z, 2.0f * next.r0.w);
+    s_rec[3 * lane + 1] = make_float4(next.r1.x, next.r1.y, next.r1.z, __uint_as_float(cand_threshold(next.r1.w)));
     s_rec[3 * lane + 2] = next.r2;
     if (kFlow) s_id[lane] = next.id;
+    // A conic with a <= 0 can give q = -0 (adxx = (a dx) dx = -0), which the
+    // 0 <= q test takes and the bit compare does not; batches with such a
+    // record add the q == 0 lanes to the candidates.
+    const bool signed_zero = __ballot(lane < cnt && !(next.r0.z > 0.0f)) != 0;
     uint64_t todo = __ballot(lane < cnt && record_may_touch(next.r0, next.r1, rx0, rx1, ry0, ry1));
     if (base + 64 < n) next = load_batch(p, rg.x + base + 64, imin(64, n - base - 64), lane);
     while (todo != 0) {
@@ -152,7 +159,8 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
       const float4 b = s_rec[3 * j + 1];
       const float dx = a.x - pfx;
       const float adxx = a.z * dx * dx;
-      const float b2dx = (a.w * dx) * 2.0f;
+      const float b2dx = a.w * dx;  // a.w = 2b
+      const unsigned thr = __float_as_uint(b.w);
       float q[kPixPerLane], dy[kPixPerLane];
       uint64_t cand_lanes[kPixPerLane];  // live && 0 <= q <= qcut, as lane masks
       uint64_t any = 0;
@@ -160,8 +168,8 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
       for (int k = 0; k < kPixPerLane; ++k) {
         dy[k] = a.y - pfy[k];
         q[k] = conic_q_px(adxx, b2dx, b.x, dy[k]);  // exponent = -0.5 q
-        cand_lanes[k] = live_lanes[k] & __builtin_amdgcn_fcmpf(q[k], 0.0f, kCmpOGE) &
-                        __builtin_amdgcn_fcmpf(q[k], b.w, kCmpOLE);
+        cand_lanes[k] = live_lanes[k] & __builtin_amdgcn_uicmp(__float_as_uint(q[k]), thr, kCmpULT);
+        if (signed_zero) cand_lanes[k] |= live_lanes[k] & __builtin_amdgcn_fcmpf(q[k], 0.0f, kCmpOEQ);
         any |= cand_lanes[k];
       }
       if (any == 0) continue;
@@ -173,7 +181,7 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
         // the others it may be anything, including inf or NaN, and every
         // decision below masks it out.  o * exp <= o <= 1, so the minimum
         // needs no NaN rule of its own.
-        const float alpha = fminf(kAlphaMax, b.y * exp_sw_nonpos(-0.5f * q[k]));
+        const float alpha = fminf(kAlphaMax, b.y * exp_sw_q(q[k]));
         // The blend decisions as lane masks: scalar ANDs of the comparisons.
         const uint64_t ok_lanes = cand_lanes[k] & __builtin_amdgcn_fcmpf(alpha, kAlphaMin, kCmpOGE);
         const float test_T = T[k] * (1.0f - alpha);

@@ -78,11 +78,13 @@ def tile_sets_of(res: dict, n: int, width: int) -> list:
 # ---------------------------------------------------------------- math
 
 def test_exp_matches_libm():
+    # within 0.9 ulp (every float of [-87, 0] was checked against a long double
+    # exp); 0.9 ulp is at most 1.08e-7 relative
     xs = np.concatenate([np.linspace(-87.0, 88.0, 20001), -np.logspace(-8, 1.9, 2000), [0.0, -1e-30]])
     for x in xs.astype(np.float32):
         got = oracle.exp(float(x))
         want = math.exp(float(x))
-        assert abs(got - want) <= 3e-7 * want, (x, got, want)
+        assert abs(got - want) <= 1.1e-7 * want, (x, got, want)
     assert oracle.exp(-87.5) == 0.0
 
 
