@@ -258,6 +258,7 @@ STAGE_OF_KERNEL = (
     ("gs::tile_ranges_u32_kernel", "ranges"),
     ("gs::render_fwd_kernel", "render"),
     ("gs::render_bwd_kernel", "render_bwd"),
+    ("gs::render_bwd_whole_kernel", "render_bwd"),
     ("gs::preprocess_bwd_kernel", "preprocess_bwd"),
     ("gs::bucket_depth_keys_kernel", "depth_sort"),
     ("gs::bucket_count_kernel", "bucket"),
@@ -765,7 +766,7 @@ def main() -> int:
             if traffic is not None:
                 entry["counter_bytes"] = traffic
                 entry["counter_hbm_frac"] = round(traffic / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)
-            if name == "render_bwd":  # VALU-issue-bound (the forward issues instructions cheaper than an FMA)
+            if name == "render_bwd":  # VALU-issue-bound
                 valu = valu_issue(name, ms, args.config)
                 if valu is not None:
                     entry["valu_issue"] = valu

@@ -1,18 +1,18 @@
 // Manual backward for gfx950.
 //
-// render_bwd: wave64 workgroups each own a tile (its four 8x8 blocks, four
-// pixels per lane, or one 8x8 quadrant of it for tiles whose list is more
-// than four times the mean) and walk the tile's list back to front from the
+// render_bwd: wave64 workgroups each own a slice of a tile (an 8x16 half,
+// two pixels per lane; the whole tile, four pixels per lane, when the
+// Gaussians are large; one 8x8 quadrant for tiles whose list is more than
+// four times the mean) and walk the tile's list back to front from the
 // largest n_contrib of their pixels
 // (backward_kernels.py:539-707 semantics: T starts at 1 - alpha_out and is
 // divided by max(1-alpha, 1e-5) per blended Gaussian, reverse recurrences for
 // colour, depth and alpha, the background term).  Per Gaussian each lane
-// sums its pixels' pixel moments and colour / depth terms, two transposed
-// lane-swap folds reduce the ten
-// components to 16 partial sums each, which are stored in a per-wave LDS
-// ring slot; a slot is reduced and sent to global memory with one float
-// atomic per component when it is reused (skipped when no pixel of the wave
-// blended the Gaussian).
+// sums its pixels' pixel moments and colour / depth terms; the wave reduces
+// them through LDS (a transposed store and per-column sums for one-column
+// slices, two lane-swap folds for the whole tile) into a per-wave slot, which
+// is reduced and sent to global memory with one float atomic per component
+// at the next Gaussian (skipped for a zero sum).
 // The blend decisions are exactly the forward's (exp_sw is evaluated only in
 // a thin band above the record's power cutoff where the decision needs it);
 // gradient values use the hardware exponential and reciprocal.
@@ -73,28 +73,6 @@ __device__ __forceinline__ void wave_fold10(const float (&g)[10], float (&m)[3])
   m[2] = fold16(h4, h4);
 }
 
-// The same reduction when every lane's pixels lie in one pixel column (a
-// slice one block wide), from the seven per-lane sums of v, v dy, v dy^2
-// and the colour and depth terms.  The first fold adds lanes l and l + 32,
-// which share the column l % 8 and with it dx, so one product by the lane's
-// dx turns the folded (sum v | sum v dy) register into (sum v dx |
-// sum v dx dy) and a second gives sum v dx^2 (its upper half is unused):
-// the three dx moments cost two products instead of three products and
-// two more components to fold.  The depth term enters only the second
-// fold, so its 64 lanes arrive as two positions of 16 partial sums.  Row r
-// of register i holds component slot_component_column(4 i + r).
-__device__ __forceinline__ void wave_fold_column(float sv, float svy, float svyy, float sr, float sg, float sb,
-                                                 float sd, float dx, float (&m)[3]) {
-  const float h0 = fold32(sv, svy);
-  const float h1 = fold32(svyy, sr);
-  const float h2 = fold32(sg, sb);
-  const float hd = h0 * dx;
-  const float hd2 = hd * dx;
-  m[0] = fold16(h0, h1);
-  m[1] = fold16(h2, sd);
-  m[2] = fold16(hd, hd2);
-}
-
 // Per-wave LDS slot of a Gaussian's gradient partial sums.  It holds, for
 // the 12 (register, row) positions p = 4 i + r of wave_fold10's output, the
 // 16 partial sums of lanes 16 r .. 16 r + 15: float p * 16 + lane % 16, so
@@ -116,22 +94,10 @@ __device__ __forceinline__ int slot_component(int p) {
   return (r & 1) ? -1 : 4 + 5 * (r >> 1);
 }
 
-// Component at slot position p of wave_fold_column's registers: {5, 4, 1, 6,
-// 7, -1, 8, 9, 0, 2, 3, -1} (position 5, the other half of the depth term,
-// is added to position 7 by flush_slot<true>), stored plus one in the
-// nibbles of a constant.
-__device__ __forceinline__ int slot_component_column(int p) {
-  return (int)((0x431a9087256ull >> (4 * p)) & 15) - 1;
-}
-
 // Reduces the slot and adds its components to grad_gauss[gid]: lane l reads
 // float4 l of the slot (position l / 4 for l < 48), sums it, and each quad
 // of lanes sums its position's four float4 sums; the quad's first lane
-// issues the atomic of a used, non-zero component.  kMergeDepth (the layout
-// of wave_fold_column) first adds position 5's sum to position 7's, the two
-// halves of the depth term: one atomic per address, so the instruction's
-// atomics need a single pass.
-template <bool kMergeDepth>
+// issues the atomic of a used, non-zero component.
 __device__ __forceinline__ void flush_slot(const float* slot, int gid, int lane, int comp, float* grad_gauss) {
   // Every lane reads a float4 (the slot is padded so that lanes 48-63 stay
   // inside it); those lanes hold no component.
@@ -139,14 +105,67 @@ __device__ __forceinline__ void flush_slot(const float* slot, int gid, int lane,
   float t = (v.x + v.y) + (v.z + v.w);
   t = t + dpp_mov<0xB1, 0xF>(t);  // quad_perm [1,0,3,2]
   t = t + dpp_mov<0x4E, 0xF>(t);  // quad_perm [2,3,0,1]
-  // t[28] += t[20]: row_shr:8 written to lanes 28-31 only (row 1, bank 3),
-  // the other lanes keep t (one instruction; s_nop 1 covers the DPP read of
-  // the VALU result above)
-  if (kMergeDepth)
-    asm volatile("s_nop 1\n\tv_add_f32_dpp %0, %0, %0 row_shr:8 row_mask:0x2 bank_mask:0x8" : "+v"(t));
   if ((lane & 3) == 0 && comp >= 0 && t != 0.0f)
     unsafeAtomicAdd(grad_gauss + (size_t)gid * kGradFloats + comp, t);
 }
+
+// Column-slice reduction through LDS (kCols == 1: a lane's pixels lie in the
+// column lane % 8 and share its dx).  Cross-lane VALU moves are the slow
+// part of a wave-wide sum (a v_permlane swap costs four fast adds), so the
+// wave transposes its sums through LDS instead.  The seven per-lane sums
+// (v, v dy, v dy^2 and the three colour and the depth terms) are stored so
+// that the eight lanes of one column hold a contiguous group of 8 floats:
+// component c of lane l at float
+//   c * 64 + col * 8 + ((row + 4 (col / 4)) % 8),   col = l % 8, row = l / 8
+// (the rotation by 4 (col / 4) puts each half-wave's 32 stores on 32 banks).
+// Lane 8 c + col (c < 7; lanes 56-63 repeat c = 6) reads its group as two
+// float4 and adds them: the column sum S of component c; with the column's
+// dx it forms S dx and S dx^2, the dx moments (used for c = 0 and 1).  These
+// go to the slot: S at float lane, S dx at 64 + lane, S dx^2 at 128 + lane.
+// The slot is reduced at the next Gaussian, or at the slice's end: lane
+// 2 k + h (k < 10) reads the float4 of columns 4 h .. 4 h + 3 of output k and
+// adds it, the lane pair adds its two sums (one DPP add) and the even lane
+// sends output k with one atomic.  Outputs 0-6 are the column sums (grad
+// components 5, 1, 4, 6, 7, 8, 9), 7 sum v dx (component 0), 8 sum v dy dx
+// (3) and 9 sum v dx^2 (2).
+constexpr int kColSlotFloats = 3 * 64;
+constexpr int kColRawFloats = 7 * 64;
+
+__device__ __forceinline__ int col_raw_offset(int lane) {
+  const int col = lane & 7, row = lane >> 3;
+  return col * 8 + ((row + 4 * (col >> 2)) & 7);
+}
+
+// float4 index (in the raw area) of the first of a lane's two groups
+__device__ __forceinline__ int col_group_index(int lane) {
+  return imin(lane >> 3, 6) * 16 + (lane & 7) * 2;
+}
+
+// float4 index (in the slot) that lane 2 k + h reads for output k
+__device__ __forceinline__ int col_flush_index(int lane) {
+  const int k = lane >> 1, h = lane & 1;
+  if (k >= 10) return 0;
+  const int f = k < 7 ? 8 * k : (k == 7 ? 64 : (k == 8 ? 72 : 128));
+  return (f >> 2) + h;
+}
+
+// grad component that lane 2 k sends (-1: none), stored in the nibbles of a constant
+__device__ __forceinline__ int col_flush_component(int lane) {
+  if (lane >= 20 || (lane & 1)) return -1;
+  return (int)((0x2309876415ull >> (4 * (lane >> 1))) & 15);
+}
+
+__device__ __forceinline__ void flush_col_slot(float4 v, int gid, int comp, float* grad_gauss) {
+  float t = (v.x + v.y) + (v.z + v.w);
+  t = t + dpp_mov<0xB1, 0xF>(t);  // quad_perm [1,0,3,2]: the pair partner's sum
+  if (comp >= 0 && t != 0.0f) unsafeAtomicAdd(grad_gauss + (size_t)gid * kGradFloats + comp, t);
+}
+
+// The wave's LDS besides the records: the fold slot of wave_fold10, or the
+// column slot and the transposed sums.
+constexpr int kSlotLdsFloats =
+    (kSlotFloats + kSlotPad) > (kColSlotFloats + kColRawFloats) ? (kSlotFloats + kSlotPad)
+                                                                : (kColSlotFloats + kColRawFloats);
 
 // A record's pixel classes as thresholds on the bits of q: for q >= +0 (sign
 // bit clear) bits(q) < cand exactly when q <= qcut (a candidate) and
@@ -252,8 +271,8 @@ __device__ __forceinline__ BwdBatch load_bwd_batch(const RenderBwdParams& p, int
 // The batch's LDS copy of a record carries the candidate and sure-blend
 // thresholds of blend_thresholds in the words the records leave unused, so
 // a visit classifies a pixel with two unsigned compares of q's bits.
-// s_rec (3 x 64 float4) and s_slot (kSlotFloats + kSlotPad floats, 16-byte
-// aligned) are the wave's LDS.
+// s_rec (3 x 64 float4) and s_slot (kSlotLdsFloats floats, 16-byte aligned)
+// are the wave's LDS.
 template <bool kDepth, int kPix, int kCols, bool kBlockCull>
 __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int tile, int sub, float4* s_rec,
                                                  float* s_slot) {
@@ -307,8 +326,12 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
   }
   const int max_lc = __builtin_amdgcn_readfirstlane(wave_max_i32(lmax));
   if (max_lc == 0) return;
-  const int flush_comp =
-      lane < kSlotFloats / 4 ? (kCols == 1 ? slot_component_column(lane >> 2) : slot_component(lane >> 2)) : -1;
+  const int flush_comp = lane < kSlotFloats / 4 ? slot_component(lane >> 2) : -1;  // kCols == 2
+  float* const col_raw = s_slot + kColSlotFloats;  // kCols == 1: the column slot, then the sums
+  const int raw_ofs = col_raw_offset(lane);
+  const int raw_grp = col_group_index(lane);
+  const int col_fidx = col_flush_index(lane);
+  const int col_fcomp = col_flush_component(lane);
   int slot_gid = -1;  // Gaussian whose sums the slot holds (wave-uniform), -1: none
 
   int bs = imax(0, max_lc - 64);
@@ -476,10 +499,30 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
       // Pixel moments of v about the Gaussian's mean; the conic, opacity
       // and W/2, H/2 factors are per Gaussian and applied once, when the
       // per-Gaussian backward turns the sums into 2D gradients.
-      float m[3];
       if constexpr (kCols == 1) {
-        wave_fold_column(sv[0], svy[0], svyy, sr, sg, sb, sd, dx[0], m);
+        // The transposed store of this Gaussian's sums, then (the wave's LDS
+        // operations complete in order) the reads of the previous Gaussian's
+        // slot and of this Gaussian's column groups, and the new slot after
+        // the flush.
+        col_raw[raw_ofs] = sv[0];
+        col_raw[64 + raw_ofs] = svy[0];
+        col_raw[128 + raw_ofs] = svyy;
+        col_raw[192 + raw_ofs] = sr;
+        col_raw[256 + raw_ofs] = sg;
+        col_raw[320 + raw_ofs] = sb;
+        col_raw[384 + raw_ofs] = sd;
+        const float4 prev = reinterpret_cast<const float4*>(s_slot)[col_fidx];
+        const float4 ga = reinterpret_cast<const float4*>(col_raw)[raw_grp];
+        const float4 gb = reinterpret_cast<const float4*>(col_raw)[raw_grp + 1];
+        if (slot_gid >= 0) flush_col_slot(prev, slot_gid, col_fcomp, p.grad_gauss);
+        slot_gid = __builtin_amdgcn_readlane(batch_id, jj);
+        const float col_sum = ((ga.x + ga.y) + (ga.z + ga.w)) + ((gb.x + gb.y) + (gb.z + gb.w));
+        const float col_dx = col_sum * dx[0];
+        s_slot[lane] = col_sum;
+        s_slot[64 + lane] = col_dx;
+        s_slot[128 + lane] = col_dx * dx[0];
       } else {
+        float m[3];
         float g[kGradFloats];
         float vdx = sv[0] * dx[0];
         g[0] = vdx;               // sum v dx
@@ -502,17 +545,22 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
         g[8] = sb;
         g[9] = sd;
         wave_fold10(g, m);
+        if (slot_gid >= 0) flush_slot(s_slot, slot_gid, lane, flush_comp, p.grad_gauss);
+        slot_gid = __builtin_amdgcn_readlane(batch_id, jj);
+        // The wave's LDS operations complete in order: these stores follow
+        // the flush's read of the previous Gaussian's sums.
+        s_slot[lane] = m[0];
+        s_slot[64 + lane] = m[1];
+        s_slot[128 + lane] = m[2];
       }
-      if (slot_gid >= 0) flush_slot<kCols == 1>(s_slot, slot_gid, lane, flush_comp, p.grad_gauss);
-      slot_gid = __builtin_amdgcn_readlane(batch_id, jj);
-      // The wave's LDS operations complete in order: these stores follow
-      // the flush's read of the previous Gaussian's sums.
-      s_slot[lane] = m[0];
-      s_slot[64 + lane] = m[1];
-      s_slot[128 + lane] = m[2];
     }
   }
-  if (slot_gid >= 0) flush_slot<kCols == 1>(s_slot, slot_gid, lane, flush_comp, p.grad_gauss);
+  if (slot_gid >= 0) {
+    if constexpr (kCols == 1)
+      flush_col_slot(reinterpret_cast<const float4*>(s_slot)[col_fidx], slot_gid, col_fcomp, p.grad_gauss);
+    else
+      flush_slot(s_slot, slot_gid, lane, flush_comp, p.grad_gauss);
+  }
 }
 
 // How a tile is split over waves.  With small Gaussians (a few tiles each)
@@ -537,10 +585,10 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
 constexpr int64_t kWholeTilePairsPerPoint = 4;
 
 template <bool kDepth, bool kWholeTiles>
-__global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
+__device__ __forceinline__ void render_bwd_tiles(const RenderBwdParams& p) {
   constexpr int kFirst = kWholeTiles ? 1 : 2;
   __shared__ float4 s_rec[3 * 64];  // record j at s_rec[3 j .. 3 j + 2]
-  __shared__ __align__(16) float s_slot[kSlotFloats + kSlotPad];
+  __shared__ __align__(16) float s_slot[kSlotLdsFloats];
   const int first_units = kFirst * p.num_tiles;
   const int extra_units = (4 - kFirst) * p.num_tiles;
   const int seg = xcd_grid(first_units);
@@ -558,6 +606,18 @@ __global__ __launch_bounds__(64) void render_bwd_kernel(RenderBwdParams p) {
     render_bwd_slice<kDepth, 4, 2, true>(p, tile, 0, s_rec, s_slot);
   else if (!extra)
     render_bwd_slice<kDepth, 2, 1, false>(p, tile, quadrant, s_rec, s_slot);
+}
+
+// The halves and quadrants fit 80 VGPRs, six waves per SIMD, which hide
+// more of a visit's latency than five; the whole-tile walk needs more.
+template <bool kDepth>
+__global__ __launch_bounds__(64, 6) void render_bwd_kernel(RenderBwdParams p) {
+  render_bwd_tiles<kDepth, false>(p);
+}
+
+template <bool kDepth>
+__global__ __launch_bounds__(64) void render_bwd_whole_kernel(RenderBwdParams p) {
+  render_bwd_tiles<kDepth, true>(p);
 }
 
 struct PreprocessBwdParams {
@@ -1045,14 +1105,14 @@ extern "C" int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t 
   const hipStream_t s = (hipStream_t)stream;
   if (compute_depth) {
     if (whole)
-      hipLaunchKernelGGL((gs::render_bwd_kernel<true, true>), grid, dim3(64), 0, s, p);
+      hipLaunchKernelGGL((gs::render_bwd_whole_kernel<true>), grid, dim3(64), 0, s, p);
     else
-      hipLaunchKernelGGL((gs::render_bwd_kernel<true, false>), grid, dim3(64), 0, s, p);
+      hipLaunchKernelGGL((gs::render_bwd_kernel<true>), grid, dim3(64), 0, s, p);
   } else {
     if (whole)
-      hipLaunchKernelGGL((gs::render_bwd_kernel<false, true>), grid, dim3(64), 0, s, p);
+      hipLaunchKernelGGL((gs::render_bwd_whole_kernel<false>), grid, dim3(64), 0, s, p);
     else
-      hipLaunchKernelGGL((gs::render_bwd_kernel<false, false>), grid, dim3(64), 0, s, p);
+      hipLaunchKernelGGL((gs::render_bwd_kernel<false>), grid, dim3(64), 0, s, p);
   }
   return gs_status_from_hip(hipGetLastError());
 }
