@@ -15,6 +15,8 @@
 //   64 bits, so the sort moves 8 bytes per pair.
 // Depths of binned Gaussians are positive, so their float bits order like the
 // depths; both stable sorts therefore give (tile, depth, point index) order.
+#include <atomic>
+#include <cstring>
 #include <mutex>
 
 #include "gs_common.h"
@@ -1119,6 +1121,16 @@ __global__ __launch_bounds__(256) void tile_ranges_kernel(long long n, const uns
   mark_ranges(i0, cnt, t, prev, n, num_tiles, ranges);
 }
 
+// Publishes count info words to a slot of coherent pinned host memory and
+// then raises the slot's flag (its last word) to seq with a system-scope
+// release store, after which the host may read the words.  One wave.
+__global__ __launch_bounds__(64) void publish_info_kernel(const int64_t* info, int count, int64_t* slot,
+                                                         int flag_word, int64_t seq) {
+  const int i = threadIdx.x;
+  if (i < count) slot[i] = info[i];
+  if (i == 0) __hip_atomic_store(slot + flag_word, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 }  // namespace gs
 
 extern "C" int gs_version(void) { return 10000; }
@@ -1288,13 +1300,100 @@ extern "C" int gs_scan_tiles_entries(int32_t P, const int32_t* tiles_touched, co
   return gs_status_from_hip(hipGetLastError());
 }
 
+// Read-back of a few info words without a device-to-host copy and a blocking
+// stream synchronisation: publish_info_kernel writes them into a slot of
+// library-owned coherent pinned host memory and raises the slot's flag, and
+// the host spins on the flag (reading it with acquire order, the words after
+// it).  Slots are taken round-robin by a per-process sequence number, which
+// is also the flag value, so a slot's stale flag never matches; a call blocks
+// until its own flag is up, so concurrent calls never share a slot.  Every
+// 1024 spins the stream is polled: an error ends the wait, and a drained
+// stream whose flag is still down (a launch that did not run) falls back to a
+// copy.  Where the pinned memory cannot be had, the copy and synchronisation
+// are used throughout.
+namespace {
+constexpr int kReadbackSlots = 64;
+constexpr int kReadbackSlotWords = 32;  // up to 16 info words; the flag in the last word
+std::mutex g_readback_mutex;
+int64_t* g_readback_host = nullptr;  // kReadbackSlots x kReadbackSlotWords, never freed
+bool g_readback_failed = false;
+std::atomic<uint64_t> g_readback_seq{0};
+
+int64_t* readback_slots() {
+  std::lock_guard<std::mutex> lock(g_readback_mutex);
+  if (!g_readback_host && !g_readback_failed) {
+    void* p = nullptr;
+    const size_t bytes = (size_t)kReadbackSlots * kReadbackSlotWords * sizeof(int64_t);
+    if (hipHostMalloc(&p, bytes, hipHostMallocPortable | hipHostMallocMapped | hipHostMallocCoherent) ==
+        hipSuccess) {
+      std::memset(p, 0, bytes);
+      g_readback_host = static_cast<int64_t*>(p);
+    } else {
+      (void)hipGetLastError();
+      g_readback_failed = true;
+    }
+  }
+  return g_readback_host;
+}
+
+struct ReadbackTicket {
+  int64_t* slot = nullptr;  // host address, or null: use the copy
+  int64_t seq = 0;
+};
+
+// Enqueues the publication of count words at info_dev on s.
+int readback_begin(const int64_t* info_dev, int count, hipStream_t s, ReadbackTicket* t) {
+  t->slot = nullptr;
+  int64_t* slots = readback_slots();
+  if (!slots) return GS_OK;
+  const uint64_t seq = g_readback_seq.fetch_add(1, std::memory_order_relaxed) + 1;
+  int64_t* slot = slots + (size_t)(seq % kReadbackSlots) * kReadbackSlotWords;
+  void* dslot = nullptr;
+  if (hipHostGetDevicePointer(&dslot, slot, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return GS_OK;
+  }
+  hipLaunchKernelGGL(gs::publish_info_kernel, dim3(1), dim3(64), 0, s, info_dev, count,
+                     static_cast<int64_t*>(dslot), kReadbackSlotWords - 1, (int64_t)seq);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  t->slot = slot;
+  t->seq = (int64_t)seq;
+  return GS_OK;
+}
+
+// Waits for the words of readback_begin and copies them to out.
+int readback_wait(const ReadbackTicket& t, const int64_t* info_dev, int64_t* out, int count, hipStream_t s) {
+  if (t.slot) {
+    const int64_t* flag = t.slot + kReadbackSlotWords - 1;
+    for (uint64_t spin = 1;; ++spin) {
+      if (__atomic_load_n(flag, __ATOMIC_ACQUIRE) == t.seq) {
+        for (int i = 0; i < count; ++i) out[i] = t.slot[i];
+        return GS_OK;
+      }
+      if ((spin & 1023) == 0) {
+        const hipError_t q = hipStreamQuery(s);
+        if (q == hipErrorNotReady) continue;
+        if (q != hipSuccess) return (int)q;
+        if (__atomic_load_n(flag, __ATOMIC_ACQUIRE) == t.seq) continue;  // read at the loop's top
+        break;  // drained without the flag: copy below
+      }
+      __builtin_ia32_pause();
+    }
+  }
+  const hipError_t e = hipMemcpyAsync(out, info_dev, (size_t)count * sizeof(int64_t), hipMemcpyDeviceToHost, s);
+  if (e != hipSuccess) return (int)e;
+  return gs_status_from_hip(hipStreamSynchronize(s));
+}
+}  // namespace
+
 extern "C" int gs_info_readback(const int64_t* info_dev, int64_t* info_host_pinned, int32_t count, void* stream) {
   if (!info_dev || !info_host_pinned || count < 1 || count > 16) return GS_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
-  hipError_t e =
-      hipMemcpyAsync(info_host_pinned, info_dev, (size_t)count * sizeof(int64_t), hipMemcpyDeviceToHost, s);
-  if (e != hipSuccess) return (int)e;
-  return gs_status_from_hip(hipStreamSynchronize(s));
+  ReadbackTicket t;
+  const int st = readback_begin(info_dev, count, s, &t);
+  if (st != GS_OK) return st;
+  return readback_wait(t, info_dev, info_host_pinned, count, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -1370,10 +1469,7 @@ extern "C" int gs_scan_tiles_static(int32_t P, const int32_t* tiles_touched, con
 
 extern "C" int gs_num_rendered_readback(const int64_t* info_dev, int64_t* info_host_pinned, void* stream) {
   if (!info_dev || !info_host_pinned) return GS_ERR_INVALID_ARGUMENT;
-  hipStream_t s = (hipStream_t)stream;
-  hipError_t e = hipMemcpyAsync(info_host_pinned, info_dev, 2 * sizeof(int64_t), hipMemcpyDeviceToHost, s);
-  if (e != hipSuccess) return (int)e;
-  return gs_status_from_hip(hipStreamSynchronize(s));
+  return gs_info_readback(info_dev, info_host_pinned, 2, stream);
 }
 
 extern "C" int gs_duplicate_keys(int32_t P, const int32_t* radii, const float* records,
@@ -1579,15 +1675,20 @@ extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_hos
                                       float* out_depth, float* out_alpha, int32_t* n_contrib,
                                       void* const* stage_events, int64_t* result, void* stream) {
   if (!result || P < 0 || capacity < 0 || image_width <= 0 || image_height <= 0) return GS_ERR_INVALID_ARGUMENT;
-  // The ranges are cleared before the read-back, while the stream would
-  // otherwise wait for the host.
+  // The ranges are cleared while the host waits for the count: the clearing
+  // is enqueued after the count's publication, so it runs during the wait
+  // instead of delaying it.
+  hipStream_t hs = (hipStream_t)stream;
+  ReadbackTicket ticket;
+  int st = readback_begin(info_dev, 2, hs, &ticket);
+  if (st != GS_OK) return st;
   const bool clear_first = ranges != nullptr && capacity > 0;
   if (clear_first) {
     const int n2 =
         2 * ((image_width + gs::kBlockX - 1) / gs::kBlockX) * ((image_height + gs::kBlockY - 1) / gs::kBlockY);
-    hipLaunchKernelGGL(gs::zero_ranges_kernel, dim3((n2 + 255) / 256), dim3(256), 0, (hipStream_t)stream, n2, ranges);
+    hipLaunchKernelGGL(gs::zero_ranges_kernel, dim3((n2 + 255) / 256), dim3(256), 0, hs, n2, ranges);
   }
-  int st = gs_num_rendered_readback(info_dev, info_host_pinned, stream);
+  st = readback_wait(ticket, info_dev, info_host_pinned, 2, hs);
   if (st != GS_OK) return st;
   const int64_t R = info_host_pinned[0];
   const uint64_t range = (uint64_t)info_host_pinned[1];

@@ -214,16 +214,20 @@ int gs_scan_tiles_onepass(int32_t P, const int32_t* tiles_touched, int32_t* offs
                           void* state, size_t state_bytes, int32_t sized, int32_t spin_limit, void* stream);
 
 /*
- * Copies count (1 to 16) int64 at info_dev into pinned host memory and waits
- * for the stream.
+ * Copies count (1 to 16) int64 at info_dev into host memory at
+ * info_host_pinned, returning once the work enqueued on the stream before the
+ * call has completed.  A one-wave kernel publishes the words into a slot of
+ * library-owned coherent pinned host memory (allocated on first use, kept
+ * until the process ends) and raises the slot's flag; the host spins on the
+ * flag, polling the stream, instead of a copy and a blocking
+ * synchronisation (the copy and synchronisation remain the fallback).
  * Replaces: binning_ops.py:243-252 (the num_rendered .item()).
  */
 int gs_info_readback(const int64_t* info_dev, int64_t* info_host_pinned, int32_t count, void* stream);
 
 /*
- * Copies the two int64 at info_dev into caller-provided pinned host memory
- * and waits for the stream: the single device-to-host synchronisation of a
- * forward pass.
+ * gs_info_readback of the two int64 at info_dev (pair count and depth range):
+ * the single device-to-host synchronisation of a forward pass.
  * Replaces: binning_ops.py:243-252 (the num_rendered .item()).
  */
 int gs_num_rendered_readback(const int64_t* info_dev, int64_t* info_host_pinned, void* stream);
