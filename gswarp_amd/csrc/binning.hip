@@ -920,7 +920,22 @@ __global__ __launch_bounds__(256) void duplicate_keys_kernel(int P, const int* _
                                                             int grid_y, int mode, long long limit,
                                                             unsigned depth_min, int depth_bits, int value_bits,
                                                             unsigned long long* __restrict__ keys,
-                                                            int* __restrict__ values) {
+                                                            int* __restrict__ values,
+                                                            const long long* __restrict__ dev_info) {
+  // With dev_info (the scan's pair count and visible depth range) the key
+  // layout is taken from device memory, as the host would compute it after
+  // reading the same words back: depth_min the range's low bits, depth_bits
+  // the bit length of the range's width, at most dev_info[0] keys.  A layout
+  // wider than 64 bits, which the host declines, writes nothing.
+  if (dev_info) {
+    const unsigned long long range = (unsigned long long)dev_info[1];
+    const unsigned dmin = (unsigned)range, dmax = (unsigned)(range >> 32);
+    depth_min = dmin;
+    depth_bits = dmax >= dmin ? 32 - __clz((int)(dmax - dmin)) : 0;
+    limit = dev_info[0] < limit ? dev_info[0] : limit;
+    const int tile_bits = 32 - __clz(grid_x * grid_y - 1);
+    if (depth_bits + value_bits + tile_bits > 64) limit = 0;
+  }
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   const int radius = idx < P ? radii[idx] : 0;
   const bool active = radius > 0;
@@ -1494,7 +1509,7 @@ extern "C" int gs_duplicate_keys(int32_t P, const int32_t* radii, const float* r
                      radii, reinterpret_cast<const float4*>(records), conic_2d_inv,
                      reinterpret_cast<const int4*>(coverage), depths, offsets, grid_x, grid_y,
                      coverage_mode, (long long)num_rendered, depth_min, depth_bits, value_bits,
-                     reinterpret_cast<unsigned long long*>(keys_out), values_out);
+                     reinterpret_cast<unsigned long long*>(keys_out), values_out, nullptr);
   return gs_status_from_hip(hipGetLastError());
 }
 
@@ -1585,7 +1600,8 @@ static int bin_packed_impl(int32_t P, const int32_t* radii, const float* records
                            int32_t image_height, int32_t coverage_mode, int64_t num_rendered, uint32_t depth_min,
                            int32_t depth_bits, int32_t value_bits, void* workspace, size_t workspace_bytes,
                            int32_t* ranges, int32_t* point_list, uint64_t* sorted_keys_out,
-                           void* const* stage_events, void* stream, bool ranges_cleared) {
+                           void* const* stage_events, void* stream, bool ranges_cleared,
+                           bool keys_emitted = false) {
   if (P < 0 || num_rendered < 0 || image_width <= 0 || image_height <= 0 || value_bits < 1 || value_bits > 31 ||
       depth_bits < 0 || depth_bits > 32)
     return GS_ERR_INVALID_ARGUMENT;
@@ -1611,11 +1627,14 @@ static int bin_packed_impl(int32_t P, const int32_t* radii, const float* records
   auto mark = [&](int k) {
     if (stage_events) (void)hipEventRecord((hipEvent_t)stage_events[k], s);
   };
-  mark(0);
-  int st = gs_duplicate_keys(P, radii, records, conic_2d_inv, coverage, depths, offsets, image_width, image_height,
-                             coverage_mode, num_rendered, depth_min, depth_bits, value_bits, keys, nullptr, stream);
-  if (st != GS_OK) return st;
-  mark(1);
+  int st = GS_OK;
+  if (!keys_emitted) {  // (else the caller has emitted them into the workspace and marked the stage)
+    mark(0);
+    st = gs_duplicate_keys(P, radii, records, conic_2d_inv, coverage, depths, offsets, image_width, image_height,
+                           coverage_mode, num_rendered, depth_min, depth_bits, value_bits, keys, nullptr, stream);
+    if (st != GS_OK) return st;
+    mark(1);
+  }
   st = gs_sort_keys_u64(num_rendered, tile_shift, tile_bits, keys, keys_alt, scratch, scratch_bytes, stream);
   if (st != GS_OK) return st;
   mark(2);
@@ -1683,10 +1702,35 @@ extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_hos
   int st = readback_begin(info_dev, 2, hs, &ticket);
   if (st != GS_OK) return st;
   const bool clear_first = ranges != nullptr && capacity > 0;
+  const int grid_x = (image_width + gs::kBlockX - 1) / gs::kBlockX;
+  const int grid_y = (image_height + gs::kBlockY - 1) / gs::kBlockY;
+  const int tile_bits = gs_bit_length((long long)grid_x * grid_y - 1);
+  int value_bits = gs_bit_length((long long)P - 1);
+  if (value_bits < 1) value_bits = 1;
   if (clear_first) {
-    const int n2 =
-        2 * ((image_width + gs::kBlockX - 1) / gs::kBlockX) * ((image_height + gs::kBlockY - 1) / gs::kBlockY);
+    const int n2 = 2 * grid_x * grid_y;
     hipLaunchKernelGGL(gs::zero_ranges_kernel, dim3((n2 + 255) / 256), dim3(256), 0, hs, n2, ranges);
+  }
+  // The keys are emitted before the count is known, into the start of the
+  // workspace (where the binning keeps them), with the key layout and the
+  // count read from info_dev by the kernel and at most capacity keys
+  // written: the emission runs while the host waits for the count and
+  // launches the sort.  When the host then declines the packed binning the
+  // keys are not used.
+  bool emitted = false;
+  if (capacity > 0 && P > 0 && workspace && workspace_bytes >= (size_t)capacity * sizeof(uint64_t) && radii &&
+      records && conic_2d_inv && offsets && point_list && value_bits <= 31 && coverage_mode >= 0 &&
+      coverage_mode <= 2 && ((reinterpret_cast<uintptr_t>(records) | reinterpret_cast<uintptr_t>(coverage)) & 15) == 0) {
+    if (stage_events) (void)hipEventRecord((hipEvent_t)stage_events[0], hs);
+    hipLaunchKernelGGL(gs::duplicate_keys_kernel, dim3((P + 255) / 256), dim3(256), 0, hs, P, radii,
+                       reinterpret_cast<const float4*>(records), conic_2d_inv, reinterpret_cast<const int4*>(coverage),
+                       depths, offsets, grid_x, grid_y, coverage_mode, (long long)capacity, 0u, 0, value_bits,
+                       reinterpret_cast<unsigned long long*>(workspace), nullptr,
+                       reinterpret_cast<const long long*>(info_dev));
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    if (stage_events) (void)hipEventRecord((hipEvent_t)stage_events[1], hs);
+    emitted = true;
   }
   st = readback_wait(ticket, info_dev, info_host_pinned, 2, hs);
   if (st != GS_OK) return st;
@@ -1695,11 +1739,6 @@ extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_hos
   const uint32_t depth_min = (uint32_t)(range & 0xFFFFFFFFull);
   const uint32_t depth_max = (uint32_t)(range >> 32);
   const int depth_bits = depth_max >= depth_min ? gs_bit_length((long long)(depth_max - depth_min)) : 0;
-  int value_bits = gs_bit_length((long long)P - 1);
-  if (value_bits < 1) value_bits = 1;
-  const int grid_x = (image_width + gs::kBlockX - 1) / gs::kBlockX;
-  const int grid_y = (image_height + gs::kBlockY - 1) / gs::kBlockY;
-  const int tile_bits = gs_bit_length((long long)grid_x * grid_y - 1);
   result[0] = R;
   result[1] = depth_min;
   result[2] = depth_bits;
@@ -1711,7 +1750,7 @@ extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_hos
   if (max_pairs_per_point > 0 && R > (int64_t)max_pairs_per_point * P) return GS_OK;
   st = bin_packed_impl(P, radii, records, conic_2d_inv, coverage, depths, offsets, image_width, image_height,
                        coverage_mode, R, depth_min, depth_bits, value_bits, workspace, workspace_bytes, ranges,
-                       point_list, nullptr, stage_events, stream, clear_first);
+                       point_list, nullptr, stage_events, stream, clear_first, emitted);
   if (st != GS_OK) return st;
   result[4] = 1;
   if (out_color) {
