@@ -361,7 +361,11 @@ int gs_bin_packed(int32_t P, const int32_t* radii, const float* records, const f
  * out_depth, out_alpha and n_contrib (background, compute_depth as there)
  * and result (6 int64) ends with 1 if it was launched.  stage_events, if not
  * NULL, holds the five events of gs_bin_packed and a sixth recorded after
- * the render.
+ * the render.  The keys are emitted into the start of workspace before the
+ * count is read back (the kernel reads the layout and the count from
+ * info_dev, at most capacity keys), so workspace is written even when the
+ * call then launches no binning (result[4] == 0); info_dev must hold the
+ * scan's words (and offsets its offsets).
  * Replaces: binning_ops.py:243-252 (the .item() read-back) together with
  * the binning that follows it and render_ops.py:16-93.
  */
