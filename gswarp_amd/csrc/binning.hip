@@ -1393,7 +1393,9 @@ int readback_wait(const ReadbackTicket& t, const int64_t* info_dev, int64_t* out
         if (__atomic_load_n(flag, __ATOMIC_ACQUIRE) == t.seq) continue;  // read at the loop's top
         break;  // drained without the flag: copy below
       }
+#if defined(__x86_64__) || defined(__i386__)
       __builtin_ia32_pause();
+#endif
     }
   }
   const hipError_t e = hipMemcpyAsync(out, info_dev, (size_t)count * sizeof(int64_t), hipMemcpyDeviceToHost, s);
