@@ -921,7 +921,11 @@ __global__ __launch_bounds__(256) void duplicate_keys_kernel(int P, const int* _
                                                             unsigned depth_min, int depth_bits, int value_bits,
                                                             unsigned long long* __restrict__ keys,
                                                             int* __restrict__ values,
-                                                            const long long* __restrict__ dev_info) {
+                                                            const long long* __restrict__ dev_info,
+                                                            int* __restrict__ clear, int clear_count) {
+  // clear: an int array the grid sets to 0 on the way (the tile ranges of the
+  // binning that follows), clear_count ints.
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < clear_count; i += gridDim.x * blockDim.x) clear[i] = 0;
   // With dev_info (the scan's pair count and visible depth range) the key
   // layout is taken from device memory, as the host would compute it after
   // reading the same words back: depth_min the range's low bits, depth_bits
@@ -1325,7 +1329,9 @@ extern "C" int gs_scan_tiles_entries(int32_t P, const int32_t* tiles_touched, co
 // 1024 spins the stream is polled: an error ends the wait, and a drained
 // stream whose flag is still down (a launch that did not run) falls back to a
 // copy.  Where the pinned memory cannot be had, the copy and synchronisation
-// are used throughout.
+// are used throughout.  (Publishing from a side stream made to wait on the
+// caller's stream with an event was tried: the cross-stream wait cost more
+// than the kernel it took off the caller's stream.)
 namespace {
 constexpr int kReadbackSlots = 64;
 constexpr int kReadbackSlotWords = 32;  // up to 16 info words; the flag in the last word
@@ -1511,7 +1517,7 @@ extern "C" int gs_duplicate_keys(int32_t P, const int32_t* radii, const float* r
                      radii, reinterpret_cast<const float4*>(records), conic_2d_inv,
                      reinterpret_cast<const int4*>(coverage), depths, offsets, grid_x, grid_y,
                      coverage_mode, (long long)num_rendered, depth_min, depth_bits, value_bits,
-                     reinterpret_cast<unsigned long long*>(keys_out), values_out, nullptr);
+                     reinterpret_cast<unsigned long long*>(keys_out), values_out, nullptr, nullptr, 0);
   return gs_status_from_hip(hipGetLastError());
 }
 
@@ -1698,7 +1704,7 @@ extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_hos
   if (!result || P < 0 || capacity < 0 || image_width <= 0 || image_height <= 0) return GS_ERR_INVALID_ARGUMENT;
   // The ranges are cleared while the host waits for the count: the clearing
   // is enqueued after the count's publication, so it runs during the wait
-  // instead of delaying it.
+  // instead of delaying it (by the key emission when there is one).
   hipStream_t hs = (hipStream_t)stream;
   ReadbackTicket ticket;
   int st = readback_begin(info_dev, 2, hs, &ticket);
@@ -1709,16 +1715,13 @@ extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_hos
   const int tile_bits = gs_bit_length((long long)grid_x * grid_y - 1);
   int value_bits = gs_bit_length((long long)P - 1);
   if (value_bits < 1) value_bits = 1;
-  if (clear_first) {
-    const int n2 = 2 * grid_x * grid_y;
-    hipLaunchKernelGGL(gs::zero_ranges_kernel, dim3((n2 + 255) / 256), dim3(256), 0, hs, n2, ranges);
-  }
+  const int n2 = 2 * grid_x * grid_y;  // range words
   // The keys are emitted before the count is known, into the start of the
   // workspace (where the binning keeps them), with the key layout and the
   // count read from info_dev by the kernel and at most capacity keys
   // written: the emission runs while the host waits for the count and
   // launches the sort.  When the host then declines the packed binning the
-  // keys are not used.
+  // keys are not used.  The same kernel clears the tile ranges.
   bool emitted = false;
   if (capacity > 0 && P > 0 && workspace && workspace_bytes >= (size_t)capacity * sizeof(uint64_t) && radii &&
       records && conic_2d_inv && offsets && point_list && value_bits <= 31 && coverage_mode >= 0 &&
@@ -1728,11 +1731,14 @@ extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_hos
                        reinterpret_cast<const float4*>(records), conic_2d_inv, reinterpret_cast<const int4*>(coverage),
                        depths, offsets, grid_x, grid_y, coverage_mode, (long long)capacity, 0u, 0, value_bits,
                        reinterpret_cast<unsigned long long*>(workspace), nullptr,
-                       reinterpret_cast<const long long*>(info_dev));
+                       reinterpret_cast<const long long*>(info_dev), clear_first ? ranges : nullptr,
+                       clear_first ? n2 : 0);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
     if (stage_events) (void)hipEventRecord((hipEvent_t)stage_events[1], hs);
     emitted = true;
+  } else if (clear_first) {
+    hipLaunchKernelGGL(gs::zero_ranges_kernel, dim3((n2 + 255) / 256), dim3(256), 0, hs, n2, ranges);
   }
   st = readback_wait(ticket, info_dev, info_host_pinned, 2, hs);
   if (st != GS_OK) return st;
