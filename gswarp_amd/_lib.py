@@ -70,11 +70,13 @@ SIGNATURES = {
     "gs_sort_tile_segments": (ctypes.c_int, [_i64, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _i32, _vp]),
     "gs_bin_packed_workspace_bytes": (ctypes.c_size_t, [_i64]),
     "gs_readback_bin_packed": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
-                                              _i64, _vp, _sz, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
-                                              _vp]),
+                                              _i64, _vp, _sz, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64,
+                                              _vp, _vp, _vp]),
     "gs_bin_packed": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, ctypes.c_uint32,
                                      _i32, _i32, _vp, _sz, _vp, _vp, _vp, _vp, _vp]),
     "gs_render_fwd": (ctypes.c_int, [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "gs_render_fwd_clear": (
+        ctypes.c_int, [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
     "gs_render_fwd_flow": (
         ctypes.c_int,
         [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],

@@ -293,7 +293,8 @@ SCAN_SPIN_LIMIT = 1 << 20
 
 
 def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options: ExecutionOptions,
-            keep_keys: bool = False, pack: bool = False, images: RenderImages | None = None) -> BinningState:
+            keep_keys: bool = False, pack: bool = False, images: RenderImages | None = None,
+            grad_clear: torch.Tensor | None = None) -> BinningState:
     """Per-tile Gaussian lists (binning_ops.py:84-431) in the requested sort mode.
 
     Every mode yields the same lists: per tile, the Gaussians in (depth, index)
@@ -367,7 +368,7 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
                  None if img is None else img.background.data_ptr(), int(img is not None and img.compute_depth),
                  None if img is None else img.color.data_ptr(), None if img is None else img.depth.data_ptr(),
                  None if img is None else img.alpha.data_ptr(), None if img is None else img.n_contrib.data_ptr(),
-                 events, result, stream)
+                 _lib.ptr(grad_clear), 0 if grad_clear is None else grad_clear.numel(), events, result, stream)
         R = validate_pair_count(int(result[0]))
         _workspace.note_pairs(device, R)
         _note("num_rendered", R)
@@ -593,10 +594,12 @@ def render_images(background: torch.Tensor, image_height: int, image_width: int,
 
 def render(pre: PreprocessOutputs, bins: BinningState, background: torch.Tensor, image_height: int,
            image_width: int, options: ExecutionOptions, *, flow: bool = False,
-           images: RenderImages | None = None) -> RenderStageResult:
+           images: RenderImages | None = None, grad_clear: torch.Tensor | None = None) -> RenderStageResult:
     """Tile blend (render_ops.py:16-93; flow: flow_ops.py:109-193).  ``images``
     are preallocated outputs; when the binning already launched the render into
-    them (``bins.rendered``) nothing more is launched."""
+    them (``bins.rendered``) nothing more is launched.  ``grad_clear`` (the
+    backward's gradient accumulator, if any) is zeroed by the render kernel,
+    or by the binning's render when that ran."""
     lib = _lib.load()
     device = pre.radii.device
     P = pre.radii.shape[0]
@@ -610,6 +613,9 @@ def render(pre: PreprocessOutputs, bins: BinningState, background: torch.Tensor,
         return RenderStageResult(color, depth, alpha, n_contrib, aux)
     write_aux = bool(flow and options.compute_flow_aux)
     k = int(options.flow_topk or 0) if write_aux else 0
+    if grad_clear is not None and (flow or bins.num_rendered == 0):
+        grad_clear.zero_()
+        grad_clear = None
     if bins.num_rendered == 0:
         color.copy_(bg.reshape(NUM_CHANNELS, 1, 1).expand_as(color))
         depth.zero_()
@@ -634,16 +640,19 @@ def render(pre: PreprocessOutputs, bins: BinningState, background: torch.Tensor,
                      aux[2].data_ptr() if write_aux else None, stream)
     else:
         with _stage("render"):
-            lib.call("gs_render_fwd", W, H, P, bins.num_rendered, bins.ranges.data_ptr(),
+            lib.call("gs_render_fwd_clear", W, H, P, bins.num_rendered, bins.ranges.data_ptr(),
                      bins.point_list.data_ptr(), pre.records.data_ptr(), bg.data_ptr(), compute_depth,
-                     color.data_ptr(), depth.data_ptr(), alpha.data_ptr(), n_contrib.data_ptr(), stream)
+                     color.data_ptr(), depth.data_ptr(), alpha.data_ptr(), n_contrib.data_ptr(),
+                     _lib.ptr(grad_clear), 0 if grad_clear is None else grad_clear.numel(), stream)
     return RenderStageResult(color, depth, alpha, n_contrib, aux)
 
 
 def forward(inputs: RasterInputs, options: ExecutionOptions, *, flow: bool = False,
-            pack: bool = False) -> ForwardResult:
+            pack: bool = False, grad_buffer: bool = False) -> ForwardResult:
     """One typed forward: the reference's execute_typed_forward (pipeline.py:11-45).
-    ``pack`` lays the state out in the raw ABI's geom / binning buffers."""
+    ``pack`` lays the state out in the raw ABI's geom / binning buffers.
+    ``grad_buffer`` has the render zero the backward's (N, 10) gradient
+    accumulator on its way, kept in the state for one backward."""
     means = inputs.means3d
     if means.ndim != 2 or means.shape[1] != 3:
         raise ValueError("means3D must have dimensions (num_points, 3)")
@@ -654,10 +663,12 @@ def forward(inputs: RasterInputs, options: ExecutionOptions, *, flow: bool = Fal
             return empty_forward(inputs, k)
         pre = preprocess(inputs, options, pack=pack)
         images = render_images(inputs.background, inputs.image_height, inputs.image_width, options, device)
+        grad_gauss = torch.empty((means.shape[0], _lib.GS_GRAD_FLOATS), dtype=torch.float32,
+                                 device=device) if grad_buffer else None
         bins = binning(pre, inputs.image_height, inputs.image_width, options, pack=pack,
-                       images=None if flow else images)
+                       images=None if flow else images, grad_clear=grad_gauss)
         res = render(pre, bins, inputs.background, inputs.image_height, inputs.image_width, options, flow=flow,
-                     images=images)
+                     images=images, grad_clear=grad_gauss)
         _note("n_contrib", res.n_contrib)
         _note("alpha", res.alpha)
     return ForwardResult(
@@ -669,7 +680,7 @@ def forward(inputs: RasterInputs, options: ExecutionOptions, *, flow: bool = Fal
         proj_2d=pre.proj_2d,
         conic_2d=pre.conic_2d,
         conic_2d_inv=pre.conic_2d_inv,
-        state=ForwardState(pre, bins, res.n_contrib),
+        state=ForwardState(pre, bins, res.n_contrib, grad_gauss),
         aux=res.aux,
     )
 
@@ -711,7 +722,12 @@ def backward(inputs: RasterInputs, radii: torch.Tensor, alpha: torch.Tensor, gra
         else:
             pre, bins, n_contrib = forward_state.preprocess, forward_state.binning, forward_state.n_contrib
         stream = _stream(device)
-        grad_gauss = torch.zeros((P, _lib.GS_GRAD_FLOATS), dtype=torch.float32, device=device)
+        # the accumulator the forward render zeroed serves one backward
+        grad_gauss = None if forward_state is None else forward_state.grad_gauss
+        if grad_gauss is not None:
+            forward_state.grad_gauss = None
+        if grad_gauss is None or grad_gauss.shape[0] != P:
+            grad_gauss = torch.zeros((P, _lib.GS_GRAD_FLOATS), dtype=torch.float32, device=device)
         if bins.num_rendered != 0:
             bg = _f32c(inputs.background.to(device))
             gc = _f32c_or_none(grad_color)

@@ -94,6 +94,9 @@ class ForwardState:
     preprocess: PreprocessOutputs
     binning: BinningState
     n_contrib: torch.Tensor
+    # (N, 10) float32 gradient accumulator that the forward render zeroed on
+    # its way (None when the forward made none); one backward takes it
+    grad_gauss: torch.Tensor | None = None
 
 
 @dataclass(slots=True)

@@ -1699,8 +1699,9 @@ extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_hos
                                       int32_t coverage_mode, int32_t max_pairs_per_point, int64_t capacity,
                                       void* workspace, size_t workspace_bytes, int32_t* ranges, int32_t* point_list,
                                       const float* background, int32_t compute_depth, float* out_color,
-                                      float* out_depth, float* out_alpha, int32_t* n_contrib,
-                                      void* const* stage_events, int64_t* result, void* stream) {
+                                      float* out_depth, float* out_alpha, int32_t* n_contrib, float* grad_clear,
+                                      int64_t grad_clear_floats, void* const* stage_events, int64_t* result,
+                                      void* stream) {
   if (!result || P < 0 || capacity < 0 || image_width <= 0 || image_height <= 0) return GS_ERR_INVALID_ARGUMENT;
   // The ranges are cleared while the host waits for the count: the clearing
   // is enqueued after the count's publication, so it runs during the wait
@@ -1762,8 +1763,9 @@ extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_hos
   if (st != GS_OK) return st;
   result[4] = 1;
   if (out_color) {
-    st = gs_render_fwd(image_width, image_height, P, R, ranges, point_list, records, background, compute_depth,
-                       out_color, out_depth, out_alpha, n_contrib, stream);
+    st = gs_render_fwd_clear(image_width, image_height, P, R, ranges, point_list, records, background,
+                             compute_depth, out_color, out_depth, out_alpha, n_contrib, grad_clear,
+                             grad_clear_floats, stream);
     if (st != GS_OK) return st;
     if (stage_events) (void)hipEventRecord((hipEvent_t)stage_events[5], (hipStream_t)stream);
     result[5] = 1;

@@ -57,6 +57,10 @@ struct RenderFwdParams {
   int* gs_per_pixel;
   float* weight;
   float* x_mu;
+  // optional: clear_floats floats at clear (16-byte aligned) set to 0 by the
+  // grid on the way, the backward's gradient accumulator
+  float* clear;
+  long long clear_floats;
 };
 
 struct Batch {
@@ -80,6 +84,21 @@ __device__ __forceinline__ Batch load_batch(const RenderFwdParams& p, int first,
   return b;
 }
 
+// Workgroup blockIdx.x's share of the optional buffer to zero, float4 stores
+// issued after its last image store: no later load of the wave waits for them
+// (the vector memory counter covers stores too), and the stores of a finished
+// workgroup overlap the blending of the others.
+__device__ __forceinline__ void clear_share(const RenderFwdParams& p, int lane) {
+  if (!p.clear) return;
+  const long long n4 = p.clear_floats >> 2;
+  const long long per = (n4 + gridDim.x - 1) / gridDim.x;
+  const long long b0 = (long long)blockIdx.x * per;
+  const long long b1 = b0 + per < n4 ? b0 + per : n4;
+  float4* c4 = reinterpret_cast<float4*>(p.clear);
+  for (long long i = b0 + lane; i < b1; i += 64) c4[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (blockIdx.x == 0 && lane < (int)(p.clear_floats & 3)) p.clear[(n4 << 2) + lane] = 0.0f;
+}
+
 template <bool kFlow, bool kDepth, int kPixPerLane>
 __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
   constexpr int kSubs = 4 / kPixPerLane;
@@ -87,7 +106,10 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
   __shared__ int s_id[kFlow ? 64 : 1];
   const int lane = threadIdx.x;
   const int unit = xcd_unit(blockIdx.x, p.num_tiles * kSubs);
-  if (unit >= p.num_tiles * kSubs) return;  // grid padding
+  if (unit >= p.num_tiles * kSubs) {  // grid padding
+    clear_share(p, lane);
+    return;
+  }
   const int2 ts = make_int2(unit / kSubs, unit % kSubs);
   const int tile = ts.x;
   const int tx = tile % p.grid_x;
@@ -243,6 +265,7 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
       }
     }
   }
+  clear_share(p, lane);
 }
 
 static int launch_render_fwd(const RenderFwdParams& p, bool flow, hipStream_t s) {
@@ -267,8 +290,11 @@ static int gs_render_fwd_common(int32_t W, int32_t H, int32_t num_points, int64_
                                 const int32_t* ranges, const int32_t* point_list, const float* records,
                                 const float* background, int32_t compute_depth, int32_t write_aux, int32_t top_k,
                                 float* out_color, float* out_depth, float* out_alpha, int32_t* n_contrib,
-                                int32_t* gs_per_pixel, float* weight, float* x_mu, bool flow, void* stream) {
+                                int32_t* gs_per_pixel, float* weight, float* x_mu, bool flow, void* stream,
+                                float* clear = nullptr, int64_t clear_floats = 0) {
   if (W <= 0 || H <= 0 || (long long)W * H > 0x7fffffffLL) return GS_ERR_INVALID_ARGUMENT;
+  if (clear_floats < 0 || (clear_floats > 0 && !clear)) return GS_ERR_INVALID_ARGUMENT;
+  if (reinterpret_cast<uintptr_t>(clear) & 15) return GS_ERR_MISALIGNED;
   if (num_points <= 0 || num_rendered < 0) return GS_ERR_INVALID_ARGUMENT;
   if (num_rendered > 0x7fffffffLL) return GS_ERR_OVERFLOW;
   if (!ranges || !point_list || !records || !background || !out_color || !out_depth || !out_alpha || !n_contrib)
@@ -296,6 +322,8 @@ static int gs_render_fwd_common(int32_t W, int32_t H, int32_t num_points, int64_
   p.gs_per_pixel = gs_per_pixel;
   p.weight = weight;
   p.x_mu = x_mu;
+  p.clear = clear_floats > 0 ? clear : nullptr;
+  p.clear_floats = clear_floats;
   return gs::launch_render_fwd(p, flow, (hipStream_t)stream);
 }
 
@@ -306,6 +334,16 @@ extern "C" int gs_render_fwd(int32_t image_width, int32_t image_height, int32_t 
   return gs_render_fwd_common(image_width, image_height, num_points, num_rendered, ranges, point_list, records,
                               background, compute_depth, 0, 0, out_color, out_depth, out_alpha, n_contrib, nullptr,
                               nullptr, nullptr, false, stream);
+}
+
+extern "C" int gs_render_fwd_clear(int32_t image_width, int32_t image_height, int32_t num_points,
+                                   int64_t num_rendered, const int32_t* ranges, const int32_t* point_list,
+                                   const float* records, const float* background, int32_t compute_depth,
+                                   float* out_color, float* out_depth, float* out_alpha, int32_t* n_contrib,
+                                   float* clear, int64_t clear_floats, void* stream) {
+  return gs_render_fwd_common(image_width, image_height, num_points, num_rendered, ranges, point_list, records,
+                              background, compute_depth, 0, 0, out_color, out_depth, out_alpha, n_contrib, nullptr,
+                              nullptr, nullptr, false, stream, clear, clear_floats);
 }
 
 extern "C" int gs_render_fwd_flow(int32_t image_width, int32_t image_height, int32_t num_points,

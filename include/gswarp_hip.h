@@ -359,7 +359,9 @@ int gs_bin_packed(int32_t P, const int32_t* radii, const float* records, const f
  * [1, 2^31 - 1], above capacity, or another dataflow).  With out_color
  * non-NULL the binning is followed by gs_render_fwd into out_color,
  * out_depth, out_alpha and n_contrib (background, compute_depth as there)
- * and result (6 int64) ends with 1 if it was launched.  stage_events, if not
+ * and result (6 int64) ends with 1 if it was launched; that render zeroes
+ * grad_clear as gs_render_fwd_clear does (grad_clear_floats 0: nothing),
+ * and only when it is launched.  stage_events, if not
  * NULL, holds the five events of gs_bin_packed and a sixth recorded after
  * the render.  The keys are emitted into the start of workspace before the
  * count is read back (the kernel reads the layout and the count from
@@ -376,7 +378,8 @@ int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_host_pinned, i
                            int32_t max_pairs_per_point, int64_t capacity, void* workspace, size_t workspace_bytes,
                            int32_t* ranges, int32_t* point_list, const float* background, int32_t compute_depth,
                            float* out_color, float* out_depth, float* out_alpha, int32_t* n_contrib,
-                           void* const* stage_events, int64_t* result, void* stream);
+                           float* grad_clear, int64_t grad_clear_floats, void* const* stage_events,
+                           int64_t* result, void* stream);
 
 /*
  * Bucketed binning, for many tiles per Gaussian: the per-tile lists in
@@ -424,6 +427,21 @@ int gs_render_fwd(int32_t image_width, int32_t image_height, int32_t num_points,
                   const int32_t* point_list, const float* records, const float* background,
                   int32_t compute_depth, float* out_color, float* out_depth, float* out_alpha,
                   int32_t* n_contrib, void* stream);
+
+/*
+ * gs_render_fwd that also sets clear_floats floats at clear (16-byte
+ * aligned; clear_floats 0: nothing) to zero, spread over the blend's
+ * workgroups: the backward's grad_gauss accumulator, zeroed by the forward
+ * without a launch of its own.  The buffer must not overlap any other
+ * argument.
+ * Replaces: render_ops.py:16-93 together with the zero fill of the
+ * backward's render accumulators (backward_ops.py:203, the torch.zeros of
+ * the combined per-Gaussian gradient buffer).
+ */
+int gs_render_fwd_clear(int32_t image_width, int32_t image_height, int32_t num_points, int64_t num_rendered,
+                        const int32_t* ranges, const int32_t* point_list, const float* records,
+                        const float* background, int32_t compute_depth, float* out_color, float* out_depth,
+                        float* out_alpha, int32_t* n_contrib, float* clear, int64_t clear_floats, void* stream);
 
 /*
  * gs_render_fwd plus the flow auxiliaries of the first top_k blended

@@ -60,14 +60,20 @@ def with_precomputed_covariance(scene: dict, seed: int = 5) -> dict:
     return out
 
 
-def gpu_forward(scene: dict, opts: ExecutionOptions, *, flow: bool = False, colors: bool = False) -> dict:
+def gpu_forward(scene: dict, opts: ExecutionOptions, *, flow: bool = False, colors: bool = False,
+                grad_buffer: bool = False) -> dict:
+    """The forward stages; with ``grad_buffer`` the render also zeroes a
+    NaN-filled (N, 10) gradient accumulator, returned as ``grad_gauss``."""
     inputs = raster_inputs(scene, colors=colors)
-    with torch.cuda.device(scene["means3D"].device):
+    dev = scene["means3D"].device
+    grad_gauss = torch.full((scene["means3D"].shape[0], 10), float("nan"), device=dev) if grad_buffer else None
+    with torch.cuda.device(dev):
         pre = _pipeline.preprocess(inputs, opts)
         bins = _pipeline.binning(pre, scene["height"], scene["width"], opts, keep_keys=True)
-        res = _pipeline.render(pre, bins, scene["bg"], scene["height"], scene["width"], opts, flow=flow)
+        res = _pipeline.render(pre, bins, scene["bg"], scene["height"], scene["width"], opts, flow=flow,
+                               grad_clear=grad_gauss)
     torch.cuda.synchronize()
-    out = {"pre": pre, "bins": bins, "res": res, "inputs": inputs}
+    out = {"pre": pre, "bins": bins, "res": res, "inputs": inputs, "grad_gauss": grad_gauss}
     return out
 
 

@@ -150,13 +150,15 @@ def _upstream(scene, seed, with_meta=True):
 
 def _check_backward(scene, *, flow_double=False, compute_depth=True, colors=False, seed=3):
     opts = options(compute_depth=compute_depth)
-    out = gpu_forward(scene, opts, colors=colors)
+    # the forward render zeroes the backward's NaN-filled accumulator
+    out = gpu_forward(scene, opts, colors=colors, grad_buffer=True)
     host, ref = oracle_forward(scene, compute_depth=compute_depth, colors=colors)
     up = _upstream(scene, seed)
     with torch.cuda.device(scene["means3D"].device):
         grads = _pipeline.backward(out["inputs"], out["pre"].radii, out["res"].alpha, up["color"], up["depth"],
                                    up["alpha"], up["proj_2d"], up["conic_2d"], up["conic_2d_inv"], opts,
-                                   _pipeline.ForwardState(out["pre"], out["bins"], out["res"].n_contrib),
+                                   _pipeline.ForwardState(out["pre"], out["bins"], out["res"].n_contrib,
+                                                          out["grad_gauss"]),
                                    flow_double=flow_double)
     torch.cuda.synchronize()
     g_means2d, g_colors, g_opac, g_means3d, g_cov, g_sh, g_scales, g_rot = grads
