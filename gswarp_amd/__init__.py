@@ -27,6 +27,9 @@ from .rasterizer import (  # noqa: F401
     set_compute_depth,
     set_tile_coverage_mode,
 )
+from . import _lib
+
+_lib.preload()
 
 
 def fused_ssim(*args, **kwargs):

@@ -6,6 +6,7 @@ rasterizer call raises ``RuntimeError`` — there is no CPU or eager fallback.
 
 from __future__ import annotations
 
+import atexit
 import ctypes
 import os
 import threading
@@ -32,7 +33,7 @@ SIGNATURES = {
     "gs_preprocess_fwd": (
         ctypes.c_int,
         [_i32, _i32, _i32, _vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _f32, _f32, _f32, _i32,
-         _i32, _i32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+         _i32, _i32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _sz, _vp],
     ),
     "gs_band_store_words": (_i64, [_i32]),
     "gs_mark_visible": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp]),
@@ -42,9 +43,10 @@ SIGNATURES = {
     "gs_scan_tiles": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "gs_scan_tiles_static_max_points": (_i32, []),
     "gs_scan_tiles_static": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
-    "gs_num_rendered_readback": (ctypes.c_int, [_vp, _vp, _vp]),
+    "gs_readback_slot_bytes": (_sz, []),
+    "gs_num_rendered_readback": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
     "gs_scan_tiles_entries": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
-    "gs_info_readback": (ctypes.c_int, [_vp, _vp, _i32, _vp]),
+    "gs_info_readback": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp]),
     "gs_scan_state_bytes": (_sz, [_i32]),
     "gs_scan_state_status_offset": (_i64, [_i32]),
     "gs_scan_state_status_words": (_i64, [_i32]),
@@ -69,7 +71,7 @@ SIGNATURES = {
     "gs_tile_ranges_u32": (ctypes.c_int, [_i64, _vp, _i32, _vp, _vp]),
     "gs_sort_tile_segments": (ctypes.c_int, [_i64, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _i32, _vp]),
     "gs_bin_packed_workspace_bytes": (ctypes.c_size_t, [_i64]),
-    "gs_readback_bin_packed": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
+    "gs_readback_bin_packed": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
                                               _i64, _vp, _sz, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64,
                                               _vp, _vp, _vp]),
     "gs_bin_packed": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, ctypes.c_uint32,
@@ -118,6 +120,24 @@ class _Lib:
         return getattr(self.handle, name)
 
 
+def _synchronize_at_exit() -> None:
+    """Wait for the work of every device the rasterizer ran on before the
+    interpreter exits, so that none of the library's kernels is still running
+    when the process tears down the HIP runtime and unregisters the library's
+    code objects (the reference synchronises before a workspace is evicted or
+    cleared, gswarp/_internal/backends/warp/memory.py:209-230, 381-385)."""
+    from . import _workspace
+
+    try:
+        import torch
+
+        if torch.cuda.is_initialized():
+            for index in sorted(_workspace.used_devices()):
+                torch.cuda.synchronize(index)
+    except Exception:  # a device already in an error state has nothing left to wait for
+        pass
+
+
 def load() -> _Lib:
     """Load the HIP library; raises RuntimeError when it is not built."""
     global _handle
@@ -130,7 +150,21 @@ def load() -> _Lib:
                         "(hipcc, gfx950) before using the rasterizer"
                     )
                 _handle = _Lib(ctypes.CDLL(str(LIB_PATH)))
+                atexit.register(_synchronize_at_exit)
     return _handle
+
+
+def preload() -> None:
+    """Load the library at package import when it is built (a missing library
+    raises at the first call instead).  Loaded then, before any GPU work, its
+    code objects are registered with the HIP runtime in the same order as
+    torch's own kernels, and unregistered after the runtime's exit handlers as
+    theirs are, rather than by a library that a first call loaded after the
+    GPU was initialised."""
+    import torch  # noqa: F401  (its HIP runtime must be the one the library binds to)
+
+    if LIB_PATH.exists():
+        load()
 
 
 def ptr(tensor) -> int | None:

@@ -226,7 +226,8 @@ def preprocess(inputs: RasterInputs, options: ExecutionOptions, *, pack: bool = 
             out.depths.data_ptr(),
             out.proj_2d.data_ptr(), out.conic_2d.data_ptr(), out.conic_2d_inv.data_ptr(),
             out.tiles_touched.data_ptr(), out.coverage.data_ptr(), out.records.data_ptr(), out.clamped.data_ptr(),
-            _lib.ptr(out.band_store), _lib.ptr(out.scan_state), _stream(device))
+            _lib.ptr(out.band_store), 0 if out.band_store is None else out.band_store.numel(),
+            _lib.ptr(out.scan_state), 0 if out.scan_state is None else out.scan_state.numel() * 8, _stream(device))
     return out
 
 
@@ -343,7 +344,7 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
             lib.call("gs_scan_tiles", P, pre.tiles_touched.data_ptr(), None, pre.radii.data_ptr(),
                      pre.depths.data_ptr(), offsets.data_ptr(), info.data_ptr(), scan_scratch.data_ptr(),
                      scan_scratch.numel(), stream)
-    pinned = _workspace.readback_buffer(device, torch.cuda.current_stream(device))
+    slot = _workspace.readback_slot(device, torch.cuda.current_stream(device))
     capacity = _workspace.pair_capacity(device) if (not pack and not keep_keys and mode != "torch"
                                                     and PACKED_SORT == "segmented" and P > 0) else 0
     if mode == "warp_depth_stable_tile" and _workspace.last_pairs(device) > DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN * P:
@@ -361,7 +362,7 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
         result = (ctypes.c_int64 * 6)()
         events = _stage_chain(("duplicate", "sort", "ranges", "sort") + (("render",) if images is not None else ()))
         img = images
-        lib.call("gs_readback_bin_packed", info.data_ptr(), pinned.data_ptr(), P, pre.radii.data_ptr(),
+        lib.call("gs_readback_bin_packed", info.data_ptr(), slot.address, slot.next_seq(), P, pre.radii.data_ptr(),
                  pre.records.data_ptr(), pre.conic_2d_inv.data_ptr(), _lib.ptr(pre.coverage), _depths_or_none(pre),
                  offsets.data_ptr(), image_width, image_height, pre.coverage_mode, DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN if mode == "warp_depth_stable_tile" else 0,
                  capacity, ws.data_ptr(), ws.numel(), ranges.data_ptr(), point_list.data_ptr(),
@@ -377,20 +378,20 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
             _note("sort_passes", int(lib.gs_sort_num_passes((T - 1).bit_length())))
             layout = KeyLayout(depth_min=int(result[1]), depth_bits=int(result[2]), value_bits=int(result[3]))
             return BinningState(grid_x, grid_y, point_list[:R], ranges, R, None, layout, rendered=bool(result[5]))
-        depth_range = int(pinned[1]) & 0xFFFFFFFFFFFFFFFF
+        depth_range = slot[1] & 0xFFFFFFFFFFFFFFFF
         # declined: release the provisioned buffers before the exact-size binning allocates its own
         del ws, result, events
         point_list = ranges = None
         if sized:  # the fast path read back two values only
-            lib.call("gs_info_readback", info.data_ptr(), pinned.data_ptr(), 4, stream)
+            lib.call("gs_info_readback", info.data_ptr(), slot.address, slot.next_seq(), 4, stream)
     else:
         point_list = ranges = None
-        lib.call("gs_info_readback", info.data_ptr(), pinned.data_ptr(), 4 if sized else 2, stream)
-        R = validate_pair_count(int(pinned[0]))
-        depth_range = int(pinned[1]) & 0xFFFFFFFFFFFFFFFF
+        lib.call("gs_info_readback", info.data_ptr(), slot.address, slot.next_seq(), 4 if sized else 2, stream)
+        R = validate_pair_count(slot[0])
+        depth_range = slot[1] & 0xFFFFFFFFFFFFFFFF
         _workspace.note_pairs(device, R)
         _note("num_rendered", R)
-    entries, valid_points = (int(pinned[2]), int(pinned[3])) if sized else (-1, 0)
+    entries, valid_points = (slot[2], slot[3]) if sized else (-1, 0)
     buffer = None
     if pack:
         buffer, point_list, ranges = _packing.allocate_binning(R, T, device)

@@ -18,6 +18,7 @@
 #include <atomic>
 #include <cstring>
 #include <mutex>
+#include <sched.h>
 
 #include "gs_common.h"
 #include "gs_capi.h"
@@ -1152,7 +1153,7 @@ __global__ __launch_bounds__(64) void publish_info_kernel(const int64_t* info, i
 
 }  // namespace gs
 
-extern "C" int gs_version(void) { return 10000; }
+extern "C" int gs_version(void) { return 10100; }
 
 extern "C" const char* gs_status_string(int status) {
   switch (status) {
@@ -1320,81 +1321,66 @@ extern "C" int gs_scan_tiles_entries(int32_t P, const int32_t* tiles_touched, co
 }
 
 // Read-back of a few info words without a device-to-host copy and a blocking
-// stream synchronisation: publish_info_kernel writes them into a slot of
-// library-owned coherent pinned host memory and raises the slot's flag, and
-// the host spins on the flag (reading it with acquire order, the words after
-// it).  Slots are taken round-robin by a per-process sequence number, which
-// is also the flag value, so a slot's stale flag never matches; a call blocks
-// until its own flag is up, so concurrent calls never share a slot.  Every
-// 1024 spins the stream is polled: an error ends the wait, and a drained
-// stream whose flag is still down (a launch that did not run) falls back to a
-// copy.  Where the pinned memory cannot be had, the copy and synchronisation
-// are used throughout.  (Publishing from a side stream made to wait on the
-// caller's stream with an event was tried: the cross-stream wait cost more
-// than the kernel it took off the caller's stream.)
+// stream synchronisation.  The caller owns the slot: kReadbackSlotWords int64
+// of host memory, the info words first and the flag in the last word, which
+// the device can write (coherent pinned memory: hipHostMalloc with
+// hipHostMallocPortable | hipHostMallocMapped | hipHostMallocCoherent), and a
+// sequence number seq > 0 that the slot's flag does not hold yet (the caller
+// counts its uses of the slot).  publish_info_kernel writes the words into
+// the slot and raises its flag to seq; the host spins on the flag (acquire
+// order, so the words are read after it).  A slot serves one call at a time:
+// the words stay in it for the caller to read.  Every 1024 spins the stream
+// is polled: an error ends the wait, and a drained stream whose flag is still
+// down (a launch that did not run) falls back to a copy.  A slot the device
+// cannot address (pageable memory) is filled by a copy and a stream
+// synchronisation.  The library keeps no state between calls.  (Publishing
+// from a side stream made to wait on the caller's stream with an event was
+// tried: the cross-stream wait cost more than the kernel it took off the
+// caller's stream.)
 namespace {
-constexpr int kReadbackSlots = 64;
 constexpr int kReadbackSlotWords = 32;  // up to 16 info words; the flag in the last word
-std::mutex g_readback_mutex;
-int64_t* g_readback_host = nullptr;  // kReadbackSlots x kReadbackSlotWords, never freed
-bool g_readback_failed = false;
-std::atomic<uint64_t> g_readback_seq{0};
-
-int64_t* readback_slots() {
-  std::lock_guard<std::mutex> lock(g_readback_mutex);
-  if (!g_readback_host && !g_readback_failed) {
-    void* p = nullptr;
-    const size_t bytes = (size_t)kReadbackSlots * kReadbackSlotWords * sizeof(int64_t);
-    if (hipHostMalloc(&p, bytes, hipHostMallocPortable | hipHostMallocMapped | hipHostMallocCoherent) ==
-        hipSuccess) {
-      std::memset(p, 0, bytes);
-      g_readback_host = static_cast<int64_t*>(p);
-    } else {
-      (void)hipGetLastError();
-      g_readback_failed = true;
-    }
-  }
-  return g_readback_host;
-}
+constexpr int kReadbackFlagWord = kReadbackSlotWords - 1;
 
 struct ReadbackTicket {
-  int64_t* slot = nullptr;  // host address, or null: use the copy
+  int64_t* slot = nullptr;
   int64_t seq = 0;
+  bool flagged = false;  // publish_info_kernel was launched: wait on the flag
 };
 
-// Enqueues the publication of count words at info_dev on s.
-int readback_begin(const int64_t* info_dev, int count, hipStream_t s, ReadbackTicket* t) {
-  t->slot = nullptr;
-  int64_t* slots = readback_slots();
-  if (!slots) return GS_OK;
-  const uint64_t seq = g_readback_seq.fetch_add(1, std::memory_order_relaxed) + 1;
-  int64_t* slot = slots + (size_t)(seq % kReadbackSlots) * kReadbackSlotWords;
+// Enqueues the publication of count words at info_dev into slot on s.
+int readback_begin(const int64_t* info_dev, int count, int64_t* slot, int64_t seq, hipStream_t s,
+                   ReadbackTicket* t) {
+  t->slot = slot;
+  t->seq = seq;
+  t->flagged = false;
+  if (seq <= 0 || __atomic_load_n(slot + kReadbackFlagWord, __ATOMIC_ACQUIRE) == seq)
+    return GS_ERR_INVALID_ARGUMENT;  // a flag that already holds seq would end the wait at once
   void* dslot = nullptr;
-  if (hipHostGetDevicePointer(&dslot, slot, 0) != hipSuccess) {
-    (void)hipGetLastError();
+  if (hipHostGetDevicePointer(&dslot, slot, 0) != hipSuccess || dslot == nullptr) {
+    (void)hipGetLastError();  // not device-mapped: the wait copies instead
     return GS_OK;
   }
   hipLaunchKernelGGL(gs::publish_info_kernel, dim3(1), dim3(64), 0, s, info_dev, count,
-                     static_cast<int64_t*>(dslot), kReadbackSlotWords - 1, (int64_t)seq);
+                     static_cast<int64_t*>(dslot), kReadbackFlagWord, seq);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  t->slot = slot;
-  t->seq = (int64_t)seq;
+  t->flagged = true;
   return GS_OK;
 }
 
-// Waits for the words of readback_begin and copies them to out.
-int readback_wait(const ReadbackTicket& t, const int64_t* info_dev, int64_t* out, int count, hipStream_t s) {
-  if (t.slot) {
-    const int64_t* flag = t.slot + kReadbackSlotWords - 1;
+// Waits until the words of readback_begin are in slot[0, count).
+int readback_wait(const ReadbackTicket& t, const int64_t* info_dev, int count, hipStream_t s) {
+  if (t.flagged) {
+    const int64_t* flag = t.slot + kReadbackFlagWord;
     for (uint64_t spin = 1;; ++spin) {
-      if (__atomic_load_n(flag, __ATOMIC_ACQUIRE) == t.seq) {
-        for (int i = 0; i < count; ++i) out[i] = t.slot[i];
-        return GS_OK;
-      }
+      if (__atomic_load_n(flag, __ATOMIC_ACQUIRE) == t.seq) return GS_OK;
       if ((spin & 1023) == 0) {
         const hipError_t q = hipStreamQuery(s);
-        if (q == hipErrorNotReady) continue;
+        if (q == hipErrorNotReady) {
+          // past the first ~10^4 spins, give the core to other runnable threads now and then
+          if (spin >= 16384 && (spin & 4095) == 0) sched_yield();
+          continue;
+        }
         if (q != hipSuccess) return (int)q;
         if (__atomic_load_n(flag, __ATOMIC_ACQUIRE) == t.seq) continue;  // read at the loop's top
         break;  // drained without the flag: copy below
@@ -1404,19 +1390,22 @@ int readback_wait(const ReadbackTicket& t, const int64_t* info_dev, int64_t* out
 #endif
     }
   }
-  const hipError_t e = hipMemcpyAsync(out, info_dev, (size_t)count * sizeof(int64_t), hipMemcpyDeviceToHost, s);
+  const hipError_t e =
+      hipMemcpyAsync(t.slot, info_dev, (size_t)count * sizeof(int64_t), hipMemcpyDeviceToHost, s);
   if (e != hipSuccess) return (int)e;
   return gs_status_from_hip(hipStreamSynchronize(s));
 }
 }  // namespace
 
-extern "C" int gs_info_readback(const int64_t* info_dev, int64_t* info_host_pinned, int32_t count, void* stream) {
-  if (!info_dev || !info_host_pinned || count < 1 || count > 16) return GS_ERR_INVALID_ARGUMENT;
+extern "C" size_t gs_readback_slot_bytes(void) { return (size_t)kReadbackSlotWords * sizeof(int64_t); }
+
+extern "C" int gs_info_readback(const int64_t* info_dev, int64_t* slot, int64_t seq, int32_t count, void* stream) {
+  if (!info_dev || !slot || count < 1 || count > 16) return GS_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
   ReadbackTicket t;
-  const int st = readback_begin(info_dev, count, s, &t);
+  const int st = readback_begin(info_dev, count, slot, seq, s, &t);
   if (st != GS_OK) return st;
-  return readback_wait(t, info_dev, info_host_pinned, count, s);
+  return readback_wait(t, info_dev, count, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -1490,9 +1479,8 @@ extern "C" int gs_scan_tiles_static(int32_t P, const int32_t* tiles_touched, con
   return gs_status_from_hip(hipGetLastError());
 }
 
-extern "C" int gs_num_rendered_readback(const int64_t* info_dev, int64_t* info_host_pinned, void* stream) {
-  if (!info_dev || !info_host_pinned) return GS_ERR_INVALID_ARGUMENT;
-  return gs_info_readback(info_dev, info_host_pinned, 2, stream);
+extern "C" int gs_num_rendered_readback(const int64_t* info_dev, int64_t* slot, int64_t seq, void* stream) {
+  return gs_info_readback(info_dev, slot, seq, 2, stream);
 }
 
 extern "C" int gs_duplicate_keys(int32_t P, const int32_t* radii, const float* records,
@@ -1692,7 +1680,7 @@ extern "C" int gs_bin_packed(int32_t P, const int32_t* radii, const float* recor
 // caller must bin itself (count outside [0, 2^31 - 1], over capacity, or
 // another dataflow), result[5] = 1 if the standard forward render was
 // launched too (out_color given).
-extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_host_pinned, int32_t P,
+extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* slot, int64_t seq, int32_t P,
                                       const int32_t* radii, const float* records, const float* conic_2d_inv,
                                       const int32_t* coverage, const float* depths, const int32_t* offsets,
                                       int32_t image_width, int32_t image_height,
@@ -1702,13 +1690,14 @@ extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_hos
                                       float* out_depth, float* out_alpha, int32_t* n_contrib, float* grad_clear,
                                       int64_t grad_clear_floats, void* const* stage_events, int64_t* result,
                                       void* stream) {
-  if (!result || P < 0 || capacity < 0 || image_width <= 0 || image_height <= 0) return GS_ERR_INVALID_ARGUMENT;
+  if (!info_dev || !slot || !result || P < 0 || capacity < 0 || image_width <= 0 || image_height <= 0)
+    return GS_ERR_INVALID_ARGUMENT;
   // The ranges are cleared while the host waits for the count: the clearing
   // is enqueued after the count's publication, so it runs during the wait
   // instead of delaying it (by the key emission when there is one).
   hipStream_t hs = (hipStream_t)stream;
   ReadbackTicket ticket;
-  int st = readback_begin(info_dev, 2, hs, &ticket);
+  int st = readback_begin(info_dev, 2, slot, seq, hs, &ticket);
   if (st != GS_OK) return st;
   const bool clear_first = ranges != nullptr && capacity > 0;
   const int grid_x = (image_width + gs::kBlockX - 1) / gs::kBlockX;
@@ -1741,10 +1730,10 @@ extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_hos
   } else if (clear_first) {
     hipLaunchKernelGGL(gs::zero_ranges_kernel, dim3((n2 + 255) / 256), dim3(256), 0, hs, n2, ranges);
   }
-  st = readback_wait(ticket, info_dev, info_host_pinned, 2, hs);
+  st = readback_wait(ticket, info_dev, 2, hs);
   if (st != GS_OK) return st;
-  const int64_t R = info_host_pinned[0];
-  const uint64_t range = (uint64_t)info_host_pinned[1];
+  const int64_t R = slot[0];
+  const uint64_t range = (uint64_t)slot[1];
   const uint32_t depth_min = (uint32_t)(range & 0xFFFFFFFFull);
   const uint32_t depth_max = (uint32_t)(range >> 32);
   const int depth_bits = depth_max >= depth_min ? gs_bit_length((long long)(depth_max - depth_min)) : 0;

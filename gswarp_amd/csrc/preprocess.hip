@@ -379,13 +379,16 @@ extern "C" int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, c
                                  float filter_variance, int32_t* radii, float* depths, float* proj_2d,
                                  float* conic_2d,
                                  float* conic_2d_inv, int32_t* tiles_touched, int32_t* coverage,
-                                 float* records, uint8_t* clamped, int32_t* band_store, int64_t* scan_state,
+                                 float* records, uint8_t* clamped, int32_t* band_store,
+                                 int64_t band_store_words, int64_t* scan_state, size_t scan_state_bytes,
                                  void* stream) {
   if (P < 0 || image_width <= 0 || image_height <= 0) return GS_ERR_INVALID_ARGUMENT;
   if (reinterpret_cast<uintptr_t>(scan_state) & 7) return GS_ERR_MISALIGNED;
   if (band_store != nullptr && (coverage == nullptr || gs_band_store_words(P) > 0x7fffffffLL)) {
     return coverage == nullptr ? GS_ERR_INVALID_ARGUMENT : GS_ERR_OVERFLOW;
   }
+  if (band_store != nullptr && band_store_words < gs_band_store_words(P)) return GS_ERR_SCRATCH_TOO_SMALL;
+  if (scan_state != nullptr && scan_state_bytes < gs_scan_state_bytes(P)) return GS_ERR_SCRATCH_TOO_SMALL;
   if (coverage_mode < 0 || coverage_mode > 2) return GS_ERR_INVALID_ARGUMENT;
   if (!(filter_variance >= 0.0f) || !__builtin_isfinite(filter_variance)) return GS_ERR_INVALID_ARGUMENT;
   if (P == 0) return GS_OK;

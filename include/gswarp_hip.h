@@ -4,10 +4,14 @@
  * Every entry point is extern "C", takes device pointers, explicit sizes and
  * a HIP stream (passed as void*, i.e. hipStream_t), enqueues its kernels on
  * that stream and returns an int status: GS_OK (0), a GS_ERR_* code, or a
- * positive hipError_t value.  No entry point allocates device memory or keeps
- * mutable global state; scratch is always caller-provided and sized by the
- * matching *_scratch_bytes query.  Calls on different streams with disjoint
- * buffers may run concurrently.
+ * positive hipError_t value.  No entry point allocates memory (device or
+ * host) or keeps mutable state between calls: scratch is caller-provided and
+ * sized by the matching *_scratch_bytes / *_workspace_bytes query, and the
+ * read-back's host slot is the caller's (gs_readback_slot_bytes).  Calls on
+ * different streams with disjoint buffers may run concurrently.  One entry
+ * point is the exception, by design: gs_scan_tiles_static keeps its scratch
+ * in a fixed device array of the library (one per GPU), so calls that
+ * overlap on one GPU race on it.  ABI version (gs_version): 10100.
  *
  * Each function replaces one stage of the reference host pipeline
  * (fancifulland2718/gswarp 1.1.0, Warp backend); the stage it replaces is
@@ -81,12 +85,13 @@ const char* gs_status_string(int status);
  * it has at most 64 cells, a 64-bit mask of the covered cells in the order of
  * the coverage walk, which the emission entry points read instead of
  * re-deriving the tiles.  band_store (optional, with coverage;
- * gs_band_store_words(P) int32) receives the coverage bands (one word per
- * tile row or column: lo | hi << 16) of the Gaussians whose word has neither
- * a mask nor a full rectangle, 256 words per wave of 64 Gaussians; such a
- * word then holds the index of its bands (or -1 when they did not fit), and
- * gs_bin_buckets reads them instead of recomputing them.  scan_state
- * (optional, gs_scan_state_bytes(P) bytes, 8-byte aligned) is prepared for
+ * band_store_words >= gs_band_store_words(P) int32) receives the coverage
+ * bands (one word per tile row or column: lo | hi << 16) of the Gaussians
+ * whose word has neither a mask nor a full rectangle, 512 words per wave of
+ * 64 Gaussians; such a word then holds the index of its bands (or -1 when
+ * they did not fit), and gs_bin_buckets reads them instead of recomputing
+ * them.  scan_state (optional, scan_state_bytes >= gs_scan_state_bytes(P)
+ * bytes, 8-byte aligned) is prepared for
  * gs_scan_tiles_onepass as gs_scan_state_prepare would prepare it from these
  * outputs, from the values in registers (no launch or read of its own).
  * Replaces: preprocess_ops.py:289-581 (preprocess_gaussians) with
@@ -103,7 +108,8 @@ int gs_preprocess_fwd(int32_t P, int32_t sh_coeffs, int32_t degree, const float*
                       int32_t image_width, int32_t image_height, int32_t coverage_mode,
                       float filter_variance, int32_t* radii, float* depths, float* proj_2d, float* conic_2d,
                       float* conic_2d_inv, int32_t* tiles_touched, int32_t* coverage, float* records,
-                      uint8_t* clamped, int32_t* band_store, int64_t* scan_state, void* stream);
+                      uint8_t* clamped, int32_t* band_store, int64_t band_store_words, int64_t* scan_state,
+                      size_t scan_state_bytes, void* stream);
 int64_t gs_band_store_words(int32_t P);
 
 /*
@@ -214,23 +220,32 @@ int gs_scan_tiles_onepass(int32_t P, const int32_t* tiles_touched, int32_t* offs
                           void* state, size_t state_bytes, int32_t sized, int32_t spin_limit, void* stream);
 
 /*
- * Copies count (1 to 16) int64 at info_dev into host memory at
- * info_host_pinned, returning once the work enqueued on the stream before the
- * call has completed.  A one-wave kernel publishes the words into a slot of
- * library-owned coherent pinned host memory (allocated on first use, kept
- * until the process ends) and raises the slot's flag; the host spins on the
- * flag, polling the stream, instead of a copy and a blocking
- * synchronisation (the copy and synchronisation remain the fallback).
+ * Copies count (1 to 16) int64 at info_dev into slot[0, count), returning
+ * once the work enqueued on the stream before the call has completed.  The
+ * slot is the caller's host memory of gs_readback_slot_bytes() bytes (256:
+ * the info words first, a flag word last), 8-byte aligned.  When the device
+ * can address it (hipHostMalloc with hipHostMallocPortable |
+ * hipHostMallocMapped | hipHostMallocCoherent), a one-wave kernel publishes
+ * the words into it and raises its flag to seq, and the host spins on the
+ * flag, polling the stream, instead of a copy and a blocking synchronisation
+ * (the copy and synchronisation remain the fallback, and serve slots in
+ * pageable memory).  seq must be positive and differ from the value the
+ * flag holds (the caller counts its uses of the slot: seq = previous + 1;
+ * GS_ERR_INVALID_ARGUMENT otherwise).  A slot serves one call at a time:
+ * calls that overlap (two threads, two streams) need distinct slots.  The
+ * wait is a spin on the host core that yields it to other runnable threads
+ * after about 10^4 polls.
  * Replaces: binning_ops.py:243-252 (the num_rendered .item()).
  */
-int gs_info_readback(const int64_t* info_dev, int64_t* info_host_pinned, int32_t count, void* stream);
+size_t gs_readback_slot_bytes(void);
+int gs_info_readback(const int64_t* info_dev, int64_t* slot, int64_t seq, int32_t count, void* stream);
 
 /*
  * gs_info_readback of the two int64 at info_dev (pair count and depth range):
  * the single device-to-host synchronisation of a forward pass.
  * Replaces: binning_ops.py:243-252 (the num_rendered .item()).
  */
-int gs_num_rendered_readback(const int64_t* info_dev, int64_t* info_host_pinned, void* stream);
+int gs_num_rendered_readback(const int64_t* info_dev, int64_t* slot, int64_t seq, void* stream);
 
 /*
  * For every Gaussian i with radius > 0, emits one key per covered tile at
@@ -346,7 +361,8 @@ int gs_bin_packed(int32_t P, const int32_t* radii, const float* records, const f
                   void* const* stage_events, void* stream);
 
 /*
- * gs_num_rendered_readback followed, in the same call, by gs_bin_packed into
+ * gs_num_rendered_readback (into slot, with seq, as there) followed, in the
+ * same call, by gs_bin_packed into
  * buffers allocated before the pair count was known (point_list for up to
  * `capacity` pairs, workspace of gs_bin_packed_workspace_bytes(capacity)
  * bytes), so the binning launches without a return to the caller.  The key
@@ -371,7 +387,7 @@ int gs_bin_packed(int32_t P, const int32_t* radii, const float* records, const f
  * Replaces: binning_ops.py:243-252 (the .item() read-back) together with
  * the binning that follows it and render_ops.py:16-93.
  */
-int gs_readback_bin_packed(const int64_t* info_dev, int64_t* info_host_pinned, int32_t P, const int32_t* radii,
+int gs_readback_bin_packed(const int64_t* info_dev, int64_t* slot, int64_t seq, int32_t P, const int32_t* radii,
                            const float* records, const float* conic_2d_inv, const int32_t* coverage,
                            const float* depths, const int32_t* offsets, int32_t image_width, int32_t image_height,
                            int32_t coverage_mode,
