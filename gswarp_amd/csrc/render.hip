@@ -99,11 +99,41 @@ __device__ __forceinline__ void clear_share(const RenderFwdParams& p, int lane) 
   if (blockIdx.x == 0 && lane < (int)(p.clear_floats & 3)) p.clear[(n4 << 2) + lane] = 0.0f;
 }
 
-template <bool kFlow, bool kDepth, int kPixPerLane>
+// Top-K auxiliaries of up to this many slots are staged in LDS (below).
+constexpr int kMaxStagedTopK = 64;
+
+// Slot s of a staged pixel's top-K: the Gaussian id, its weight (alpha T)
+// and its offset (dx, dy) from the pixel, recomputed from the id by the
+// walk's own operations (so bit for bit the walk's values), with Tw the
+// transmittance in front of it, which the call advances; id < 0 gives the
+// unused slot's -1 / 0 / 0 / 0.
+__device__ __forceinline__ void topk_slot(int id, const float4& r0, const float4& r1, float pfx, float pfy,
+                                          float& Tw, float& w, float& dx, float& dy) {
+  w = dx = dy = 0.0f;
+  if (id < 0) return;
+  dx = r0.x - pfx;
+  dy = r0.y - pfy;
+  const float adxx = r0.z * dx * dx;
+  const float b2dx = (2.0f * r0.w) * dx;
+  const float q = conic_q_px(adxx, b2dx, r1.x, dy);
+  const float alpha = fminf(kAlphaMax, r1.y * exp_sw_q(q));
+  w = alpha * Tw;
+  Tw = Tw * (1.0f - alpha);
+}
+
+// kStaged (flow with K <= kMaxStagedTopK): the walk only records the ids of
+// each pixel's first K blended Gaussians in LDS (slot-major, 64 K kPix
+// ints of dynamic LDS); after the walk every lane writes all K slots of its
+// pixel plane by plane, so that each store instruction writes whole rows of
+// 16 consecutive pixels of one plane (64-byte segments) instead of one
+// scattered word per blended Gaussian, and the unused slots in the same
+// stores.  Larger K keep the direct stores during the walk.
+template <bool kFlow, bool kDepth, int kPixPerLane, bool kStaged = false>
 __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
   constexpr int kSubs = 4 / kPixPerLane;
   __shared__ float4 s_rec[3 * 64];  // record j at s_rec[3 j .. 3 j + 2]
   __shared__ int s_id[kFlow ? 64 : 1];
+  extern __shared__ int s_topk[];   // kStaged: id of slot s of pixel k at [(s kPix + k) 64 + lane]
   const int lane = threadIdx.x;
   const int unit = xcd_unit(blockIdx.x, p.num_tiles * kSubs);
   if (unit >= p.num_tiles * kSubs) {  // grid padding
@@ -218,7 +248,9 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
         c2[k] = fmaf(f.z, contribution, c2[k]);
         ws[k] = ws[k] + contribution;
         if (kDepth) da[k] = fmaf(b.z, contribution, da[k]);
-        if (aux && blend && nsucc[k] < p.top_k) {
+        if (kStaged) {
+          if (aux && blend && nsucc[k] < p.top_k) s_topk[(nsucc[k] * kPixPerLane + k) * 64 + lane] = s_id[j];
+        } else if (aux && blend && nsucc[k] < p.top_k) {
           const size_t pix = (size_t)(py0 + kRowStep * k) * p.W + px;
           const size_t ai = (size_t)nsucc[k] * P + pix;
           p.gs_per_pixel[ai] = s_id[j];
@@ -247,7 +279,36 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
       p.out_alpha[pix] = ws[k];
       p.out_depth[pix] = da[k];
     }
-    if (aux) {
+    if (kStaged && aux) {
+      // Slots in plane order, each the next record's loads issued before the
+      // current slot's arithmetic.
+      float Tw = 1.0f;
+      const int* ids = s_topk + k * 64 + lane;
+      int id_n = nsucc[k] > 0 ? ids[0] : -1;
+      float4 r0n = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1n = r0n;
+      if (id_n >= 0) {
+        r0n = p.records[3 * (size_t)id_n];
+        r1n = p.records[3 * (size_t)id_n + 1];
+      }
+      for (int s = 0; s < p.top_k; ++s) {
+        const int id = id_n;
+        const float4 r0 = r0n, r1 = r1n;
+        id_n = (s + 1 < nsucc[k] && s + 1 < p.top_k) ? ids[(s + 1) * kPixPerLane * 64] : -1;
+        if (id_n >= 0) {
+          r0n = p.records[3 * (size_t)id_n];
+          r1n = p.records[3 * (size_t)id_n + 1];
+        }
+        float w, sdx, sdy;
+        topk_slot(id, r0, r1, pfx, pfy[k], Tw, w, sdx, sdy);
+        if (in_image) {
+          const size_t ai = (size_t)s * P + pix;
+          p.gs_per_pixel[ai] = id;
+          p.weight[ai] = w;
+          p.x_mu[ai] = sdx;
+          p.x_mu[(size_t)p.top_k * P + ai] = sdy;
+        }
+      }
+    } else if (aux) {
       // Unused slots, plane by plane for the whole wave, so that each store
       // covers the wave's pixels of one plane (rows of kSliceW consecutive
       // pixels) rather than one plane per lane.
@@ -270,7 +331,13 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
 
 static int launch_render_fwd(const RenderFwdParams& p, bool flow, hipStream_t s) {
   const dim3 grid(gs::xcd_grid(p.num_tiles * (4 / kFwdPix)));
-  if (flow) {
+  if (flow && p.write_aux && p.top_k <= kMaxStagedTopK) {
+    const size_t lds = (size_t)p.top_k * kFwdPix * 64 * sizeof(int);
+    if (p.compute_depth)
+      hipLaunchKernelGGL((render_fwd_kernel<true, true, kFwdPix, true>), grid, dim3(64), lds, s, p);
+    else
+      hipLaunchKernelGGL((render_fwd_kernel<true, false, kFwdPix, true>), grid, dim3(64), lds, s, p);
+  } else if (flow) {
     if (p.compute_depth)
       hipLaunchKernelGGL((render_fwd_kernel<true, true, kFwdPix>), grid, dim3(64), 0, s, p);
     else
