@@ -16,9 +16,9 @@ reference's lists bit for bit.
 from __future__ import annotations
 
 import os
+import threading
 from contextlib import contextmanager
-from contextvars import ContextVar
-from dataclasses import dataclass
+from typing import NamedTuple
 
 from ._coverage import check_mode_name, kernel_mode
 
@@ -27,17 +27,28 @@ DEFAULT_BACKWARD_MODE = "manual"
 DEFAULT_BINNING_SORT_MODE = "warp_depth_stable_tile"
 DEFAULT_TILE_COVERAGE_MODE = "auto"
 
-_BACKWARD_MODE = DEFAULT_BACKWARD_MODE
-_BINNING_SORT_MODE = DEFAULT_BINNING_SORT_MODE
-_TILE_COVERAGE_MODE = DEFAULT_TILE_COVERAGE_MODE
-_COMPUTE_DEPTH = os.environ.get("GSWARP_COMPUTE_DEPTH", "1") != "0"
-_COMPUTE_FLOW_AUX = os.environ.get("GSWARP_COMPUTE_FLOW_AUX", "1") != "0"
-_FLOW_TOPK = int(os.environ.get("GSWARP_FLOW_TOPK", "20"))
+
+class _ModuleDefaults:
+    """The process-wide values the getters read and the setters change;
+    environment variables give the start values of the two flags and K."""
+
+    def __init__(self) -> None:
+        self.backward_mode = DEFAULT_BACKWARD_MODE
+        self.binning_sort_mode = DEFAULT_BINNING_SORT_MODE
+        self.tile_coverage_mode = DEFAULT_TILE_COVERAGE_MODE
+        self.compute_depth = os.environ.get("GSWARP_COMPUTE_DEPTH", "1") != "0"
+        self.compute_flow_aux = os.environ.get("GSWARP_COMPUTE_FLOW_AUX", "1") != "0"
+        self.flow_topk = int(os.environ.get("GSWARP_FLOW_TOPK", "20"))
 
 
-@dataclass(frozen=True, slots=True)
-class ExecutionOptions:
-    """Immutable runtime choices owned by one frontend invocation."""
+_defaults = _ModuleDefaults()
+
+
+class ExecutionOptions(NamedTuple):
+    """The option values a rasterizer call runs with: the module values
+    merged with the call's settings when the forward starts, then handed
+    unchanged to the backward of the same call, so that setters used in
+    between change neither.  Flow fields are None for the standard path."""
 
     backward_mode: str
     binning_sort_mode: str
@@ -49,99 +60,108 @@ class ExecutionOptions:
     flow_topk: int | None = None
 
 
-_ACTIVE: ContextVar[ExecutionOptions | None] = ContextVar("gswarp_amd_active_execution_options", default=None)
+class _ScopeStack(threading.local):
+    """Per thread, the options of the calls in progress, innermost last."""
+
+    def __init__(self) -> None:
+        self.frames: list[ExecutionOptions] = []
+
+
+_scopes = _ScopeStack()
 
 
 @contextmanager
 def execution_options(options: ExecutionOptions):
-    token = _ACTIVE.set(options)
+    """Run the body with ``options`` as this thread's innermost call options
+    (what a raw-ABI call made inside it resolves to)."""
+    _scopes.frames.append(options)
     try:
         yield options
     finally:
-        _ACTIVE.reset(token)
+        _scopes.frames.pop()
 
 
 def active_options() -> ExecutionOptions | None:
-    return _ACTIVE.get()
+    """This thread's innermost call options, or None outside any call."""
+    frames = _scopes.frames
+    return frames[-1] if frames else None
 
 
 def get_backward_mode() -> str:
-    return _BACKWARD_MODE
+    return _defaults.backward_mode
 
 
 def set_backward_mode(mode: str) -> None:
-    global _BACKWARD_MODE
     if mode != "manual":
         raise ValueError("mode must be 'manual'")
-    _BACKWARD_MODE = mode
+    _defaults.backward_mode = mode
 
 
 def get_binning_sort_mode() -> str:
-    return _BINNING_SORT_MODE
+    return _defaults.binning_sort_mode
 
 
 def set_binning_sort_mode(mode: str) -> None:
-    global _BINNING_SORT_MODE
     if mode not in BINNING_SORT_MODES:
         raise ValueError("mode must be one of 'torch', 'warp_radix', or 'warp_depth_stable_tile'")
-    _BINNING_SORT_MODE = mode
+    _defaults.binning_sort_mode = mode
 
 
 def get_tile_coverage_mode() -> str:
-    return _TILE_COVERAGE_MODE
+    return _defaults.tile_coverage_mode
 
 
 def set_tile_coverage_mode(mode: str) -> None:
-    global _TILE_COVERAGE_MODE
-    _TILE_COVERAGE_MODE = check_mode_name(mode)
+    _defaults.tile_coverage_mode = check_mode_name(mode)
 
 
 def get_compute_depth() -> bool:
-    return _COMPUTE_DEPTH
+    return _defaults.compute_depth
 
 
 def set_compute_depth(enabled: bool) -> None:
-    global _COMPUTE_DEPTH
-    _COMPUTE_DEPTH = bool(enabled)
+    _defaults.compute_depth = bool(enabled)
 
 
 def get_compute_flow_aux() -> bool:
-    return _COMPUTE_FLOW_AUX
+    return _defaults.compute_flow_aux
 
 
 def set_compute_flow_aux(enabled: bool) -> None:
-    global _COMPUTE_FLOW_AUX
-    _COMPUTE_FLOW_AUX = bool(enabled)
+    _defaults.compute_flow_aux = bool(enabled)
 
 
 def get_flow_topk() -> int:
-    return _FLOW_TOPK
+    return _defaults.flow_topk
 
 
 def set_flow_topk(k: int) -> None:
-    global _FLOW_TOPK
     if int(k) <= 0:
         raise ValueError("flow_topk must be positive")
-    _FLOW_TOPK = int(k)
+    _defaults.flow_topk = int(k)
 
 
 def resolve_execution_options(raster_settings, *, flow: bool = False, exact_conic: bool = True) -> ExecutionOptions:
-    """Merge module defaults and per-call settings into an immutable snapshot.
+    """The options of one call: a settings field that is present and not
+    None wins over the module value.
 
     exact_conic: the method's footprint is the screen-space conic (true for
     every method of this package), so "auto" coverage means accutile_sweep."""
-    backward_mode = getattr(raster_settings, "backward_mode", None)
-    binning_sort_mode = getattr(raster_settings, "binning_sort_mode", None)
-    compute_flow_aux = getattr(raster_settings, "compute_flow_aux", None) if flow else None
+    d = _defaults
+
+    def setting(name, default):
+        value = getattr(raster_settings, name, None)
+        return default if value is None else value
+
     return ExecutionOptions(
-        backward_mode=_BACKWARD_MODE if backward_mode is None else backward_mode,
-        binning_sort_mode=_BINNING_SORT_MODE if binning_sort_mode is None else binning_sort_mode,
-        tile_coverage_mode=kernel_mode(_TILE_COVERAGE_MODE, exact_conic=exact_conic).public_name,
-        compute_depth=_COMPUTE_DEPTH,
-        auto_tune=bool(getattr(raster_settings, "auto_tune", True)),
-        auto_tune_verbose=bool(getattr(raster_settings, "auto_tune_verbose", True)),
-        compute_flow_aux=(_COMPUTE_FLOW_AUX if compute_flow_aux is None else bool(compute_flow_aux)) if flow else None,
-        flow_topk=_FLOW_TOPK if flow else None,
+        backward_mode=setting("backward_mode", d.backward_mode),
+        binning_sort_mode=setting("binning_sort_mode", d.binning_sort_mode),
+        tile_coverage_mode=kernel_mode(d.tile_coverage_mode, exact_conic=exact_conic).public_name,
+        compute_depth=d.compute_depth,
+        auto_tune=bool(setting("auto_tune", True)),
+        auto_tune_verbose=bool(setting("auto_tune_verbose", True)),
+        compute_flow_aux=bool(setting("compute_flow_aux", d.compute_flow_aux)) if flow else None,
+        flow_topk=d.flow_topk if flow else None,
     )
 
 

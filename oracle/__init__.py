@@ -20,7 +20,9 @@ import numpy as np
 
 ORACLE_DIR = Path(__file__).resolve().parent
 SOURCE = ORACLE_DIR / "gs_oracle.c"
-LIB_PATH = ORACLE_DIR / "libgs_oracle.so"
+# GS_ORACLE_LIB selects another build of the same source (the sanitizer
+# build of oracle/sanitize.sh).
+LIB_PATH = Path(os.environ.get("GS_ORACLE_LIB", ORACLE_DIR / "libgs_oracle.so"))
 
 CFLAGS = (
     "-O2",
