@@ -121,19 +121,24 @@ __device__ __forceinline__ void topk_slot(int id, const float4& r0, const float4
   Tw = Tw * (1.0f - alpha);
 }
 
-// kStaged (flow with K <= kMaxStagedTopK): the walk only records the ids of
-// each pixel's first K blended Gaussians in LDS (slot-major, 64 K kPix
-// ints of dynamic LDS); after the walk every lane writes all K slots of its
-// pixel plane by plane, so that each store instruction writes whole rows of
-// 16 consecutive pixels of one plane (64-byte segments) instead of one
-// scattered word per blended Gaussian, and the unused slots in the same
-// stores.  Larger K keep the direct stores during the walk.
+// Tiles with fewer pairs than this stage their top-K as 16-bit list positions.
+constexpr int kStagedMaxList = 1 << 16;
+
+// kStaged (flow with K <= kMaxStagedTopK): the walk only records where each
+// pixel's first K blended Gaussians are in the tile's list, as 16-bit
+// positions in LDS (slot-major, 64 K kPix of them in dynamic LDS: 2.5 KB at
+// K = 20, so the LDS keeps about seven waves per SIMD resident); after the
+// walk every lane writes all K slots of its pixel plane by plane, so that
+// each store instruction writes whole rows of 16 consecutive pixels of one
+// plane (64-byte segments) instead of one scattered word per blended
+// Gaussian, and the unused slots in the same stores.  Larger K, and tiles
+// of kStagedMaxList pairs or more, keep the direct stores during the walk.
 template <bool kFlow, bool kDepth, int kPixPerLane, bool kStaged = false>
 __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
   constexpr int kSubs = 4 / kPixPerLane;
   __shared__ float4 s_rec[3 * 64];  // record j at s_rec[3 j .. 3 j + 2]
   __shared__ int s_id[kFlow ? 64 : 1];
-  extern __shared__ int s_topk[];   // kStaged: id of slot s of pixel k at [(s kPix + k) 64 + lane]
+  extern __shared__ unsigned short s_pos[];  // kStaged: slot s of pixel k at [(s kPix + k) 64 + lane]
   const int lane = threadIdx.x;
   const int unit = xcd_unit(blockIdx.x, p.num_tiles * kSubs);
   if (unit >= p.num_tiles * kSubs) {  // grid padding
@@ -163,6 +168,7 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
   rg.y = imax(rg.x, imin(rg.y, p.num_rendered));
   const int n = rg.y - rg.x;
   const bool aux = kFlow && p.write_aux != 0;
+  const bool staged = kStaged && n < kStagedMaxList;  // uniform per workgroup
 
   // live_lanes[k]: the wave's lanes whose pixel k is still blending, kept as
   // a lane mask in scalar registers (pixels outside the image start
@@ -248,8 +254,9 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
         c2[k] = fmaf(f.z, contribution, c2[k]);
         ws[k] = ws[k] + contribution;
         if (kDepth) da[k] = fmaf(b.z, contribution, da[k]);
-        if (kStaged) {
-          if (aux && blend && nsucc[k] < p.top_k) s_topk[(nsucc[k] * kPixPerLane + k) * 64 + lane] = s_id[j];
+        if (staged) {
+          if (aux && blend && nsucc[k] < p.top_k)
+            s_pos[(nsucc[k] * kPixPerLane + k) * 64 + lane] = (unsigned short)(base + j);
         } else if (aux && blend && nsucc[k] < p.top_k) {
           const size_t pix = (size_t)(py0 + kRowStep * k) * p.W + px;
           const size_t ai = (size_t)nsucc[k] * P + pix;
@@ -279,25 +286,33 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
       p.out_alpha[pix] = ws[k];
       p.out_depth[pix] = da[k];
     }
-    if (kStaged && aux) {
-      // Slots in plane order, each the next record's loads issued before the
-      // current slot's arithmetic.
+    if (staged && aux) {
+      // Slots in plane order: the list entry of slot s + 2 and the record of
+      // slot s + 1 are loaded before slot s's arithmetic.
       float Tw = 1.0f;
-      const int* ids = s_topk + k * 64 + lane;
-      int id_n = nsucc[k] > 0 ? ids[0] : -1;
-      float4 r0n = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1n = r0n;
-      if (id_n >= 0) {
-        r0n = p.records[3 * (size_t)id_n];
-        r1n = p.records[3 * (size_t)id_n + 1];
+      const unsigned short* pos = s_pos + k * 64 + lane;
+      const int used = imin(nsucc[k], p.top_k);
+      auto list_id = [&](int s) {
+        if (s >= used) return -1;
+        int id = p.point_list[rg.x + pos[s * kPixPerLane * 64]];
+        return (unsigned)id < (unsigned)p.num_points ? id : 0;  // as load_batch
+      };
+      int id_a = list_id(0);
+      int id_b = list_id(1);
+      float4 r0a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1a = r0a;
+      if (id_a >= 0) {
+        r0a = p.records[3 * (size_t)id_a];
+        r1a = p.records[3 * (size_t)id_a + 1];
       }
       for (int s = 0; s < p.top_k; ++s) {
-        const int id = id_n;
-        const float4 r0 = r0n, r1 = r1n;
-        id_n = (s + 1 < nsucc[k] && s + 1 < p.top_k) ? ids[(s + 1) * kPixPerLane * 64] : -1;
-        if (id_n >= 0) {
-          r0n = p.records[3 * (size_t)id_n];
-          r1n = p.records[3 * (size_t)id_n + 1];
+        const int id = id_a;
+        const float4 r0 = r0a, r1 = r1a;
+        id_a = id_b;
+        if (id_a >= 0) {
+          r0a = p.records[3 * (size_t)id_a];
+          r1a = p.records[3 * (size_t)id_a + 1];
         }
+        id_b = list_id(s + 2);
         float w, sdx, sdy;
         topk_slot(id, r0, r1, pfx, pfy[k], Tw, w, sdx, sdy);
         if (in_image) {
@@ -332,7 +347,7 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
 static int launch_render_fwd(const RenderFwdParams& p, bool flow, hipStream_t s) {
   const dim3 grid(gs::xcd_grid(p.num_tiles * (4 / kFwdPix)));
   if (flow && p.write_aux && p.top_k <= kMaxStagedTopK) {
-    const size_t lds = (size_t)p.top_k * kFwdPix * 64 * sizeof(int);
+    const size_t lds = (size_t)p.top_k * kFwdPix * 64 * sizeof(unsigned short);
     if (p.compute_depth)
       hipLaunchKernelGGL((render_fwd_kernel<true, true, kFwdPix, true>), grid, dim3(64), lds, s, p);
     else
