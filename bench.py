@@ -20,6 +20,7 @@ import argparse
 import json
 import math
 import os
+import re
 import sys
 import time
 from collections import defaultdict
@@ -88,8 +89,12 @@ class StageTimer:
             self.events[name].append((a, b))
         return (ctypes.c_void_p * len(events))(*[e.cuda_event for e in events])
 
+    # scalar facts of a step (pair count, dataflow, sizes) are kept on every
+    # step, so that an uninstrumented run (the profiler's) still reports its R
+    ALWAYS = frozenset({"num_rendered", "binning_dataflow", "sort_passes", "bucket_entries", "bucket_valid"})
+
     def note(self, key, value):
-        if self.enabled:
+        if self.enabled or key in self.ALWAYS:
             self.notes[key].append(value)
 
     def mean_ms(self, steps: int) -> dict:
@@ -103,15 +108,16 @@ def sort_passes(tiles: int) -> int:
 
 
 def algorithmic_bytes(N: int, R: float, P: int, T: int, dataflow: str, flow_k: int = 0, entries: float = 0.0,
-                      valid: float = 0.0, sized_scan: bool = False) -> dict:
-    """Bytes crossing each stage boundary once (the SH3, depth-on accounting of the
-    reference dataflow): preprocess 112N + SH 228N, scan 8N (the two-pass
+                      valid: float = 0.0, sized_scan: bool = False, sh_coeffs: int = 16) -> dict:
+    """Bytes crossing each stage boundary once (the depth-on accounting of the
+    reference dataflow): preprocess 112N + SH (36 + 12 K)N with K SH
+    coefficients per Gaussian (228N at SH3, 48N at SH0), scan 8N (the two-pass
     scan that sizes the bucketed binning also reads the 16-byte cover words,
     24N; the one-pass scan takes the sizes from the preprocess), duplicate
     44N + 12R (64-bit key + value) or 44N + 8R (tile id + value), ranges
     8R + 8T (4R + 8T over the depth-then-tile dataflow's 32-bit tile ids),
     render 44R + 24P + 8T, render backward 44R + 28P + 40N + 8T, SH +
-    preprocess backward 624N.  Sorts: the one 64-bit key sort moves 24R per
+    preprocess backward (240 + 24 K)N (624N at SH3).  Sorts: the one 64-bit key sort moves 24R per
     pass over ceil((32 + ceil(log2 T)) / 8) passes; the depth-then-tile
     dataflow moves 16N per pass over 4 passes for the depth sort and 16R per
     pass over ceil(log2 T / 8) passes for the tile sort.  The bucketed binning
@@ -122,12 +128,12 @@ def algorithmic_bytes(N: int, R: float, P: int, T: int, dataflow: str, flow_k: i
     also writes its top-K auxiliaries, 16 K P (id, weight and the two x_mu
     components)."""
     out = {
-        "preprocess": 340.0 * N,
+        "preprocess": (148.0 + 12.0 * sh_coeffs) * N,
         "scan": (24.0 if sized_scan else 8.0) * N,
         "ranges": 8.0 * R + 8.0 * T,
         "render": 44.0 * R + 24.0 * P + 8.0 * T + 16.0 * flow_k * P,
         "render_bwd": 44.0 * R + 28.0 * P + 40.0 * N + 8.0 * T,
-        "preprocess_bwd": 624.0 * N,
+        "preprocess_bwd": (240.0 + 24.0 * sh_coeffs) * N,
     }
     if dataflow == "warp_radix":
         out["duplicate"] = 44.0 * N + 12.0 * R
@@ -168,9 +174,29 @@ def early_stop_share(alpha, width: int, height: int, flow: bool = False) -> floa
     return float((lowest > 0.99).double().mean().item())
 
 
+def profile_path(kind: str, config: int) -> Path:
+    return ROOT / "profiles" / f"{kind}_config{config}.txt"
+
+
+def profile_provenance(kind: str, config: int):
+    """Where a committed profile's figures come from: the file and the mean pair
+    count R of the profiled run (its '# profiled run:' header line), or None."""
+    path = profile_path(kind, config)
+    if not path.exists():
+        return None
+    out = {"file": str(path.relative_to(ROOT)), "R": None}
+    for line in path.read_text().splitlines():
+        if line.startswith("# profiled run:"):
+            m = re.search(r"mean R=([0-9.]+)", line)
+            if m:
+                out["R"] = float(m.group(1))
+            break
+    return out
+
+
 def read_traffic(stage: str, config: int = 2):
     """HBM bytes per launch of a stage from the committed rocprofv3 PMC summary, if present."""
-    path = ROOT / "profiles" / f"traffic_config{config}.txt"
+    path = profile_path("traffic", config)
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
@@ -186,7 +212,7 @@ def read_traffic(stage: str, config: int = 2):
 def read_valu_insts(stage: str, config: int = 2):
     """VALU wave instructions per launch of a stage's kernel (the variant with the
     most dispatches) from the committed SQ counter summary, if present."""
-    path = ROOT / "profiles" / f"sq_counters_config{config}.txt"
+    path = profile_path("sq_counters", config)
     if not path.exists():
         return None
     columns, best = None, None
@@ -209,6 +235,18 @@ def read_valu_insts(stage: str, config: int = 2):
         if best is None or dispatches > best[0]:
             best = (dispatches, insts)
     return None if best is None else best[1]
+
+
+def profiled_run_line(bench_log: str | None) -> list[str]:
+    """The header line naming the profiled bench run's mean pair count, taken
+    from that run's own '[bench] ... mean R=' report (stderr)."""
+    if not bench_log:
+        return []
+    for line in open(bench_log, errors="replace"):
+        m = re.search(r"\[bench\] .*ms/step.*mean R=([0-9]+)", line)
+        if m:
+            return [f"# profiled run: mean R={m.group(1)} (bench.py's report: {line.strip()[8:]})"]
+    return []
 
 
 def valu_issue(stage: str, ms: float, config: int = 2):
@@ -307,12 +345,12 @@ def _pmc_commands(config: int) -> list[str]:
     return [
         _PROFILE_PREAMBLE,
         f"#   rocprofv3 --pmc FETCH_SIZE --output-format csv -d $R/gpurun_out/pmc_{c} -o fetch -- \\",
-        f"#       {run}",
+        f"#       {run} > $R/gpurun_out/pmc_{c}/fetch.json 2> $R/gpurun_out/pmc_{c}/fetch.err",
         f"#   rocprofv3 --pmc WRITE_SIZE --output-format csv -d $R/gpurun_out/pmc_{c} -o write -- \\",
-        f"#       {run}",
+        f"#       {run} > $R/gpurun_out/pmc_{c}/write.json 2> $R/gpurun_out/pmc_{c}/write.err",
         f"#   python3 bench.py --pmc-summary gpurun_out/pmc_{c}/fetch_counter_collection.csv \\",
-        f"#       gpurun_out/pmc_{c}/write_counter_collection.csv profiles/traffic_config{config}.txt"
-        + ("" if config == 2 else f" --profile-config {config}"),
+        f"#       gpurun_out/pmc_{c}/write_counter_collection.csv profiles/traffic_config{config}.txt \\",
+        f"#       gpurun_out/pmc_{c}/fetch.err" + ("" if config == 2 else f" --profile-config {config}"),
     ]
 
 
@@ -323,13 +361,16 @@ def _sq_commands(config: int) -> list[str]:
         _PROFILE_PREAMBLE,
         "#   rocprofv3 --pmc SQ_WAVES SQ_INSTS_VALU SQ_ACTIVE_INST_VALU SQ_INSTS_LDS SQ_ACTIVE_INST_LDS \\",
         f"#       SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_BUSY_CYCLES --output-format csv -d $R/gpurun_out/sq_{c} -o sq -- \\",
-        f"#       python3 $R/bench.py {cfg}--steps 3 --warmup 1 --no-cpu-baseline --no-stage-timing",
+        f"#       python3 $R/bench.py {cfg}--steps 3 --warmup 1 --no-cpu-baseline --no-stage-timing \\",
+        f"#       > $R/gpurun_out/sq_{c}/sq.json 2> $R/gpurun_out/sq_{c}/sq.err",
         f"#   python3 bench.py --sq-summary gpurun_out/sq_{c}/sq_counter_collection.csv "
-        f"profiles/sq_counters_config{config}.txt" + ("" if config == 2 else f" --profile-config {config}"),
+        f"profiles/sq_counters_config{config}.txt gpurun_out/sq_{c}/sq.err"
+        + ("" if config == 2 else f" --profile-config {config}"),
     ]
 
 
-def summarize_pmc(fetch_csv: str, write_csv: str, out_path: str, copy_bytes: int = 1 << 30, config: int = 2) -> None:
+def summarize_pmc(fetch_csv: str, write_csv: str, out_path: str, bench_log: str | None = None,
+                  copy_bytes: int = 1 << 30, config: int = 2) -> None:
     """Turn two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE, then WRITE_SIZE,
     both in KiB per dispatch) into per-stage HBM bytes per launch.  Each counter is
     scaled by what it reads for the calibration copy (the largest device copy, of
@@ -362,6 +403,7 @@ def summarize_pmc(fetch_csv: str, write_csv: str, out_path: str, copy_bytes: int
         f"(calibration copy of {copy_bytes} B read + {copy_bytes} B written read "
         f"{fetch_copy:.0f} / {write_copy:.0f} units)",
         f"# iterations averaged: {iters} (fetch run), {iters_w} (write run)",
+        *profiled_run_line(bench_log),
         "# commands:",
         *_pmc_commands(config),
         "# format: '<stage>: <bytes per launch> fetch <bytes> write <bytes>' (bench.py reads the first number)",
@@ -374,7 +416,7 @@ def summarize_pmc(fetch_csv: str, write_csv: str, out_path: str, copy_bytes: int
     print("\n".join(lines))
 
 
-def summarize_sq(counter_csv: str, out_path: str, config: int = 2) -> None:
+def summarize_sq(counter_csv: str, out_path: str, bench_log: str | None = None, config: int = 2) -> None:
     """Per-kernel means per dispatch of the SQ counters in one rocprofv3 --pmc
     counter_collection.csv, with the LDS bank-conflict rate in conflict cycles
     per LDS access cycle, SQ_LDS_BANK_CONFLICT / (SQ_LDS_IDX_ACTIVE -
@@ -393,6 +435,7 @@ def summarize_sq(counter_csv: str, out_path: str, config: int = 2) -> None:
         dispatches[short].add(r["Dispatch_Id"])
     counters = sorted({c for d in per.values() for c in d})
     lines = [f"# SQ counters per kernel, {CONFIG_TITLES[config]}, one MI355X",
+             *profiled_run_line(bench_log),
              "# commands:", *_sq_commands(config),
              "# lds_conflict_rate = SQ_LDS_BANK_CONFLICT / (SQ_LDS_IDX_ACTIVE - SQ_LDS_BANK_CONFLICT) "
              "(conflict cycles per LDS access cycle)",
@@ -412,6 +455,7 @@ def summarize_sq(counter_csv: str, out_path: str, config: int = 2) -> None:
 
 
 CONFIG_TITLES = {
+    0: "config 0 (10k Gaussians, 256x256, SH0, forward only)",
     1: "config 1 (100k Gaussians, 800x800, SH3, fwd+bwd)",
     2: "config 2 (1M Gaussians, 1920x1080, SH3, fwd+bwd with depth and alpha)",
     3: "config 3 (5M Gaussians, 1920x1080, SH3, heavy tail of large splats, fwd+bwd)",
@@ -429,6 +473,7 @@ def summarize_stats(stats_csv: str, out_path: str, bench_err: str | None = None,
     rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
     lines = [f"# Kernel time, {CONFIG_TITLES[config]}, one MI355X",
              "# 23 iterations (3 warm-up, 10 timed, 10 with per-stage events) plus bench.py's 1 GiB copy calibration",
+             *profiled_run_line(bench_err),
              "# commands:", *_stats_commands(config)]
     if bench_err:
         stage_lines = [line.strip() for line in open(bench_err) if line.startswith("[bench]")]
@@ -441,6 +486,43 @@ def summarize_stats(stats_csv: str, out_path: str, bench_err: str | None = None,
                      f"{float(r['MaxNs']) / 1e3:10.1f} {float(r['Percentage']):6.2f}%  {r['Name'][:110]}")
     Path(out_path).write_text("\n".join(lines) + "\n")
     print("\n".join(lines))
+
+
+def signature(tensor) -> dict:
+    """numel, finite count, sum, sum of |x| and max |x| of a device tensor, in the
+    tensor's own precision (the reference microbenchmark's `_signature`,
+    benchmarks/rasterizer_microbench.py:44-53)."""
+    import torch
+
+    value = tensor.detach()
+    return {"numel": value.numel(), "finite": int(torch.isfinite(value).sum().item()),
+            "sum": float(value.sum().item()), "abs_sum": float(value.abs().sum().item()),
+            "max_abs": float(value.abs().max().item()) if value.numel() else 0.0}
+
+
+def signature_difference(left: dict, right: dict) -> dict:
+    """Largest absolute and relative difference between two runs' signatures
+    over the sum, abs_sum and max_abs fields, relative to max(|right|, 1); inf
+    when a tensor's size or finite count differs (the reference's
+    `_difference`, benchmarks/rasterizer_microbench.py:145-163)."""
+    largest_abs = largest_rel = 0.0
+    for name, a in left.items():
+        b = right[name]
+        if a["numel"] != b["numel"] or a["finite"] != a["numel"] or b["finite"] != b["numel"]:
+            return {"max_abs": math.inf, "max_rel": math.inf}
+        for field in ("sum", "abs_sum", "max_abs"):
+            delta = abs(a[field] - b[field])
+            largest_abs = max(largest_abs, delta)
+            largest_rel = max(largest_rel, delta / max(abs(b[field]), 1.0))
+    return {"max_abs": largest_abs, "max_rel": largest_rel}
+
+
+def median(values):
+    v = sorted(values)
+    n = len(v)
+    if n == 0:
+        return None
+    return v[n // 2] if n % 2 else 0.5 * (v[n // 2 - 1] + v[n // 2])
 
 
 def host_cpu_info() -> dict:
@@ -469,11 +551,13 @@ def host_cpu_info() -> dict:
             "usable_cpus": usable, "cpu_model": model}
 
 
-def cpu_baseline_and_parity(scene, grads, gpu: dict, flow: bool, top_k: int, reps: int = 3) -> tuple[dict, dict]:
+def cpu_baseline_and_parity(scene, grads, gpu: dict, flow: bool, top_k: int, reps: int = 3,
+                            backward: bool = True) -> tuple[dict, dict]:
     """The CPU baseline and the parity check of the iteration-0 view, both from the C oracle.
 
-    Baseline: one untimed warm-up fwd+bwd of the same scene, then `reps` timed
-    ones on all usable host CPUs and one on a single thread.  Parity: the
+    Baseline: one untimed warm-up fwd+bwd (the forward alone for a forward-only
+    workload) of the same scene, then `reps` timed ones on all usable host CPUs
+    and one on a single thread.  Parity: the
     warm-up's forward is the checker for the GPU's outputs of the same view
     (gpu: images, radii, flow ids and leaf gradients captured after the timed
     region), the gradients to the per-element bound of the oracle (its
@@ -494,7 +578,8 @@ def cpu_baseline_and_parity(scene, grads, gpu: dict, flow: bool, top_k: int, rep
 
     def run():
         res = oracle.rasterize(host, top_k=top_k)
-        oracle.rasterize_backward(host, res, gc, gd, ga, flow_double=flow)
+        if backward:
+            oracle.rasterize_backward(host, res, gc, gd, ga, flow_double=flow)
         return res
 
     ref = run()
@@ -515,7 +600,8 @@ def cpu_baseline_and_parity(scene, grads, gpu: dict, flow: bool, top_k: int, rep
         "unit": "Gaussians/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"fwd+bwd of the iteration-0 view of this workload ({n} Gaussians) by the C oracle "
+        "sample": f"{'fwd+bwd' if backward else 'forward'} of the iteration-0 view of this workload "
+                  f"({n} Gaussians) by the C oracle "
                   f"(oracle/gs_oracle.c, OpenMP): 1 warm-up, mean of {reps} timed runs on {threads} threads "
                   f"({mean:.2f} s), 1 run on 1 thread ({one_thread:.2f} s)",
         "seconds": mean,
@@ -526,11 +612,12 @@ def cpu_baseline_and_parity(scene, grads, gpu: dict, flow: bool, top_k: int, rep
     }
 
     t0 = time.perf_counter()
-    ref_g = oracle.rasterize_backward(host, ref, gc, gd, ga, flow_double=flow, with_bound=True)
+    ref_g = oracle.rasterize_backward(host, ref, gc, gd, ga, flow_double=flow, with_bound=True) if backward else None
     rf = ref["fwd"]
     parity = {"view": "iteration 0 (the scene's camera)",
-              "bar": "radii (and flow top-K ids) equal; colour, depth, alpha within 1e-4; each gradient "
-                     "element within 1e-3 |e| + 1e-5 + 2 B (B: the oracle's bound on its fp32 rounding)",
+              "bar": "radii (and flow top-K ids) equal; colour, depth, alpha within 1e-4"
+                     + ("; each gradient element within 1e-3 |e| + 1e-5 + 2 B (B: the oracle's bound on its "
+                        "fp32 rounding)" if backward else ""),
               "radii_equal": bool(np.array_equal(gpu["radii"], ref["pre"]["radii"]))}
     ok = parity["radii_equal"]
     for key in ("color", "depth", "alpha"):
@@ -541,7 +628,7 @@ def cpu_baseline_and_parity(scene, grads, gpu: dict, flow: bool, top_k: int, rep
         parity["topk_ids_equal"] = bool(np.array_equal(gpu["ids"], rf["gs_per_pixel"]))
         ok = ok and parity["topk_ids_equal"]
     grad_report = {}
-    for name in ("means3D", "means2D", "opacities", "scales", "rotations", "sh"):
+    for name in ("means3D", "means2D", "opacities", "scales", "rotations", "sh") if backward else ():
         e = ref_g[name].astype(np.float64)
         a = gpu["grads"][name].reshape(e.shape).astype(np.float64)
         diff = np.abs(a - e)
@@ -551,10 +638,111 @@ def cpu_baseline_and_parity(scene, grads, gpu: dict, flow: bool, top_k: int, rep
         grad_report[name] = {"failures": failures, "worst_ratio": round(float((diff / tol).max()), 4),
                              "outside_plain_bar": int((diff > plain).sum()), "elements": int(e.size)}
         ok = ok and failures == 0
-    parity["gradients"] = grad_report
+    if backward:
+        parity["gradients"] = grad_report
     parity["ok"] = bool(ok)
     parity["check_seconds"] = round(time.perf_counter() - t0, 2)
     return baseline, parity
+
+
+# The reference's published full forward + backward runs with precomputed RGB
+# (docs/rasterizer.md:315, Warp on one RTX 5090): Gaussians, image side, ms,
+# peak MiB, repeated-output max abs difference.
+REFERENCE_MICROBENCH = ((262_144, 384, 2.215, 85.8, 5.59e-9), (1_048_576, 640, 4.733, 345.5, 5.96e-8))
+
+
+def reference_microbench(warmups: int = 20, repeats: int = 100, seed: int = 20260710) -> dict:
+    """Context only (not the headline): the reference microbenchmark's workload
+    (benchmarks/rasterizer_microbench.py:57-128) at the two sizes it publishes
+    figures for: means x, y ~ U[-0.65, 0.65], z ~ U[2, 3], precomputed RGB ~
+    U[0, 1), opacity ~ U[0.1, 0.9], scales ~ U[0.025, 0.06], identity
+    rotations, identity view and projection, tan(fov) = 1, background
+    (0.05, 0.15, 0.25), SH degree 0, warp_depth_stable_tile binning; drawn
+    from a device generator seeded seed + count in that order; the loss
+    color^2 mean + alpha mean + 0.01 depth mean + 1e-4 (proj_2D^2 mean +
+    conic_2D sum + conic_2D_inv sum).  Timing follows the reference: events
+    around `repeats` back-to-back steps after `warmups` (lines 166-186), with
+    the signature repeatability of two collected steps (lines 172-175) and
+    torch's peak allocation over the timed steps."""
+    import torch
+
+    from gswarp_amd.rasterizer import GaussianRasterizationSettings, rasterize_gaussians
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    records = []
+    for count, side, ref_ms, ref_mib, ref_rep in REFERENCE_MICROBENCH:
+        g = torch.Generator(device=device).manual_seed(seed + count)
+        means3D = torch.empty((count, 3), dtype=torch.float32, device=device)
+        means3D[:, :2].uniform_(-0.65, 0.65, generator=g)
+        means3D[:, 2].uniform_(2.0, 3.0, generator=g)
+        colors = torch.rand((count, 3), dtype=torch.float32, device=device, generator=g)
+        opacities = torch.empty((count, 1), dtype=torch.float32, device=device).uniform_(0.1, 0.9, generator=g)
+        scales = torch.empty((count, 3), dtype=torch.float32, device=device).uniform_(0.025, 0.06, generator=g)
+        rotations = torch.zeros((count, 4), dtype=torch.float32, device=device)
+        rotations[:, 0] = 1.0
+        leaves = {"means3D": means3D, "means2D": torch.zeros((count, 3), dtype=torch.float32, device=device),
+                  "colors_precomp": colors, "opacities": opacities, "scales": scales, "rotations": rotations}
+        for t in leaves.values():
+            t.requires_grad_(True)
+        empty = torch.empty((0,), dtype=torch.float32, device=device)
+        settings = GaussianRasterizationSettings(
+            image_height=side, image_width=side, tanfovx=1.0, tanfovy=1.0,
+            bg=torch.tensor((0.05, 0.15, 0.25), dtype=torch.float32, device=device), scale_modifier=1.0,
+            viewmatrix=torch.eye(4, dtype=torch.float32, device=device),
+            projmatrix=torch.eye(4, dtype=torch.float32, device=device), sh_degree=0,
+            campos=torch.zeros(3, dtype=torch.float32, device=device), prefiltered=False, auto_tune=False,
+            auto_tune_verbose=False, binning_sort_mode="warp_depth_stable_tile")
+
+        def run(collect: bool):
+            for t in leaves.values():
+                t.grad = None
+            color, radii, meta = rasterize_gaussians(
+                leaves["means3D"], leaves["means2D"], empty, leaves["colors_precomp"], leaves["opacities"],
+                leaves["scales"], leaves["rotations"], empty, settings)
+            loss = (color.square().mean() + meta.alpha.mean() + 0.01 * meta.depth.mean()
+                    + 1.0e-4 * (meta.proj_2D.square().mean() + meta.conic_2D.sum() + meta.conic_2D_inv.sum()))
+            loss.backward()
+            if not collect:
+                return None
+            tensors = {"loss": loss.reshape(1), "color": color, "depth": meta.depth, "alpha": meta.alpha,
+                       "proj_2D": meta.proj_2D, "conic_2D": meta.conic_2D, "conic_2D_inv": meta.conic_2D_inv}
+            tensors.update({f"grad.{k}": v.grad for k, v in leaves.items()})
+            return int((radii > 0).sum().item()), {k: signature(v) for k, v in tensors.items()}
+
+        for _ in range(warmups):
+            run(False)
+        torch.cuda.synchronize()
+        visible, first = run(True)
+        _, second = run(True)
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats(device)
+        host = []
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(repeats):
+            h0 = time.perf_counter()
+            run(False)
+            host.append(time.perf_counter() - h0)
+        end.record()
+        end.synchronize()
+        ms = start.elapsed_time(end) / repeats
+        peak = torch.cuda.max_memory_allocated(device) / 2.0 ** 20
+        rep = signature_difference(second, first)
+        records.append({"gaussians": count, "image": f"{side}x{side}", "visible_gaussians": visible,
+                        "fwd_bwd_ms": round(ms, 4), "host_step_median_ms": round(1e3 * median(host), 4),
+                        "peak_allocated_mib": round(peak, 1), "repeatability": rep,
+                        "reference_rtx5090_warp": {"fwd_bwd_ms": ref_ms, "peak_allocated_mib": ref_mib,
+                                                   "repeat_max_abs": ref_rep}})
+        log(f"[bench] reference microbench {count} Gaussians {side}x{side}: {ms:.3f} ms fwd+bwd "
+            f"(reference 5090/Warp {ref_ms} ms), {visible} visible, peak {peak:.1f} MiB, "
+            f"repeat max abs {rep['max_abs']:.3g}")
+        del leaves, means3D, colors, opacities, scales, rotations
+        torch.cuda.empty_cache()
+    return {"mode": "reference microbenchmark workloads (context only, not the headline metric)",
+            "warmups": warmups, "repeats": repeats, "seed": seed, "dtype": "f32",
+            "data": "synthetic, the reference microbenchmark's distributions (device generator)",
+            "records": records}
 
 
 def main() -> int:
@@ -562,23 +750,31 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4))
+    parser.add_argument("--config", type=int, default=2, choices=(0, 1, 2, 3, 4))
     parser.add_argument("--count", type=int, default=None, help="override the Gaussian count")
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-stage-timing", action="store_true")
     parser.add_argument("--sort-mode", default=None, choices=("warp_depth_stable_tile", "warp_radix", "torch"),
                         help="binning sort mode (default: the API default, warp_depth_stable_tile)")
-    parser.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OUT"),
-                        help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) into OUT and exit")
-    parser.add_argument("--sq-summary", nargs=2, metavar=("COUNTER_CSV", "OUT"),
-                        help="summarise one rocprofv3 --pmc run of SQ counters into OUT and exit")
-    parser.add_argument("--profile-config", type=int, default=2, choices=(1, 2, 3, 4),
+    parser.add_argument("--pmc-summary", nargs="+", metavar="PATH",
+                        help="FETCH_CSV WRITE_CSV OUT [BENCH_ERR]: summarise two rocprofv3 --pmc runs "
+                             "(FETCH_SIZE, WRITE_SIZE) into OUT and exit")
+    parser.add_argument("--sq-summary", nargs="+", metavar="PATH",
+                        help="COUNTER_CSV OUT [BENCH_ERR]: summarise one rocprofv3 --pmc run of SQ counters "
+                             "into OUT and exit")
+    parser.add_argument("--profile-config", type=int, default=2, choices=(0, 1, 2, 3, 4),
                         help="configuration a --stats-summary, --pmc-summary or --sq-summary run profiled")
+    parser.add_argument("--reference-microbench", action="store_true",
+                        help="context only: time the reference microbenchmark's two published precomputed-RGB "
+                             "workloads (256K at 384x384, 1024K at 640x640) and print their JSON line")
     parser.add_argument("--stats-summary", nargs="+", metavar="PATH",
                         help="KERNEL_STATS_CSV OUT [BENCH_ERR]: summarise one rocprofv3 --kernel-trace --stats "
                              "run into OUT and exit")
     args = parser.parse_args()
+    if args.reference_microbench:
+        print(json.dumps(reference_microbench()), flush=True)
+        return 0
     if args.stats_summary:
         summarize_stats(*args.stats_summary, config=args.profile_config)
         return 0
@@ -627,6 +823,7 @@ def main() -> int:
     else:
         cams = [scene] * total_steps
     flow = spec.flow
+    sh_coeffs = (spec.sh_degree + 1) ** 2
     settings = []
     for cam in cams:
         common = dict(image_height=H, image_width=W, tanfovx=cam["tanfovx"], tanfovy=cam["tanfovy"],
@@ -643,6 +840,9 @@ def main() -> int:
     _pipeline.STAGE_TIMER = timer
     step_events = []
 
+    backward = spec.backward
+    host_times = []  # (forward, backward) host seconds of each timed step
+
     def step(i: int, timed: bool):
         for t in (*leaves.values(), means2D):
             t.grad = None
@@ -651,8 +851,15 @@ def main() -> int:
         if timed:
             e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
             e0.record()
-        out = rast(leaves["means3D"], means2D, leaves["opacities"], shs=leaves["shs"], scales=leaves["scales"],
-                   rotations=leaves["rotations"])
+        h0 = time.perf_counter()
+        if backward:
+            out = rast(leaves["means3D"], means2D, leaves["opacities"], shs=leaves["shs"], scales=leaves["scales"],
+                       rotations=leaves["rotations"])
+        else:
+            with torch.no_grad():
+                out = rast(leaves["means3D"], means2D, leaves["opacities"], shs=leaves["shs"],
+                           scales=leaves["scales"], rotations=leaves["rotations"])
+        h1 = time.perf_counter()
         if timed:
             e1.record()
         if flow:
@@ -662,26 +869,39 @@ def main() -> int:
             color, radii, meta = out
             outputs, upstream = [color, meta.depth, meta.alpha], [grads["color"], grads["depth"], grads["alpha"]]
             images = {"color": color, "radii": radii, "depth": meta.depth, "alpha": meta.alpha}
-        torch.autograd.backward(outputs, upstream)
+        h2 = time.perf_counter()
+        if backward:
+            torch.autograd.backward(outputs, upstream)
+        h3 = time.perf_counter()
         if timed:
             e2.record()
             step_events.append((e0, e1, e2))
+            host_times.append((h1 - h0, h3 - h2))
         return images
 
     def capture(i: int) -> dict:
-        """Outputs and leaf gradients of one untimed step, on the host."""
+        """Outputs and leaf gradients of one untimed step, on the host, with the
+        reference microbenchmark's signatures (numel, finite count, sum, sum of
+        absolute values, largest absolute value) of each, taken on the device
+        in fp32 as it takes them (rasterizer_microbench.py:44-53)."""
         images = step(i, False)
         torch.cuda.synchronize()
         out = {k: v.detach().cpu().numpy() for k, v in images.items()}
-        out["grads"] = {k: leaves[k].grad.detach().cpu().numpy() for k in ("means3D", "scales", "rotations",
-                                                                         "opacities")}
-        out["grads"]["sh"] = leaves["shs"].grad.detach().cpu().numpy()
-        out["grads"]["means2D"] = means2D.grad.detach().cpu().numpy()
+        tensors = {f"output.{k}": images[k] for k in ("color", "depth", "alpha")}
+        if backward:
+            out["grads"] = {k: leaves[k].grad.detach().cpu().numpy() for k in ("means3D", "scales", "rotations",
+                                                                             "opacities")}
+            out["grads"]["sh"] = leaves["shs"].grad.detach().cpu().numpy()
+            out["grads"]["means2D"] = means2D.grad.detach().cpu().numpy()
+            tensors.update({f"grad.{k}": leaves[k].grad for k in leaves})
+            tensors["grad.means2D"] = means2D.grad
+        out["signature"] = {k: signature(v) for k, v in tensors.items()}
         return out
 
     for i in range(args.warmup):
         step(i, False)
     torch.cuda.synchronize()
+    timer.notes.clear()  # the warm-up cameras are not the timed ones
     torch.cuda.reset_peak_memory_stats(device)
     # Headline: the K timed steps run uninstrumented (only the two per-step
     # events around forward and backward).
@@ -711,22 +931,40 @@ def main() -> int:
     # backward add in an unspecified order), and its outputs for the parity check.
     first = capture(0)
     second = capture(0)
-    repeat = {"images_max_abs_diff": max(float(abs(first[k] - second[k]).max()) for k in ("color", "depth", "alpha")),
-              "grads_max_abs_diff": max(float(abs(first["grads"][k] - second["grads"][k]).max())
-                                        for k in first["grads"]),
-              "grads_max_rel_diff": max(float((abs(first["grads"][k] - second["grads"][k])
-                                               / (abs(first["grads"][k]) + 1e-30)).max()) for k in first["grads"])}
-    log(f"[bench] run-to-run: images {repeat['images_max_abs_diff']:.3g}, gradients "
-        f"{repeat['grads_max_abs_diff']:.3g} max abs; peak allocated {peak_bytes / 2**30:.2f} GiB")
+    repeat = {"images_max_abs_diff": max(float(abs(first[k] - second[k]).max()) for k in ("color", "depth", "alpha"))}
+    if backward:
+        repeat["grads_max_abs_diff"] = max(float(abs(first["grads"][k] - second["grads"][k]).max())
+                                           for k in first["grads"])
+        repeat["grads_max_rel_diff"] = max(float((abs(first["grads"][k] - second["grads"][k])
+                                                  / (abs(first["grads"][k]) + 1e-30)).max()) for k in first["grads"])
+    # the reference's repeatability figure: the same view twice, compared through
+    # per-tensor signatures (sum, abs_sum, max_abs) of the images and gradients
+    repeat["signature"] = signature_difference(second["signature"], first["signature"])
+    log(f"[bench] run-to-run: images {repeat['images_max_abs_diff']:.3g}"
+        + (f", gradients {repeat['grads_max_abs_diff']:.3g} max abs" if backward else "")
+        + f"; signatures {repeat['signature']['max_abs']:.3g} max abs, {repeat['signature']['max_rel']:.3g} max rel"
+        + f"; peak allocated {peak_bytes / 2**30:.2f} GiB")
 
     ms_per_step = 1000.0 * elapsed / args.steps
-    fwd_ms = sum(a.elapsed_time(b) for a, b, _ in step_events) / len(step_events)
-    bwd_ms = sum(b.elapsed_time(c) for _, b, c in step_events) / len(step_events)
+    fwd_list = [a.elapsed_time(b) for a, b, _ in step_events]
+    bwd_list = [b.elapsed_time(c) for _, b, c in step_events]
+    fwd_ms = sum(fwd_list) / len(fwd_list)
+    bwd_ms = sum(bwd_list) / len(bwd_list) if backward else None
+    # Host time per call (Python dispatch plus, in the forward, the wait for the
+    # pair count), as the reference reports a host median beside the GPU time
+    # (docs/rasterizer.md:313).  The backward returns once its kernels are queued.
+    host = {"fwd_median_ms": round(1e3 * median([h[0] for h in host_times]), 4),
+            "bwd_median_ms": round(1e3 * median([h[1] for h in host_times]), 4) if backward else None,
+            "gpu_fwd_median_ms": round(median(fwd_list), 4),
+            "gpu_bwd_median_ms": round(median(bwd_list), 4) if backward else None}
     stage_ms = timer.mean_ms(args.steps) if not args.no_stage_timing else {}
     passes = timer.notes.get("sort_passes", [])
     Rs = timer.notes.get("num_rendered", [])
     R = sum(Rs) / len(Rs) if Rs else float("nan")
-    log(f"[bench] {ms_per_step:.3f} ms/step (fwd {fwd_ms:.3f} ms, bwd {bwd_ms:.3f} ms), mean R={R:.0f}")
+    log(f"[bench] {ms_per_step:.3f} ms/step (fwd {fwd_ms:.3f} ms"
+        + (f", bwd {bwd_ms:.3f} ms" if backward else ", forward only") + f"), mean R={R:.0f}")
+    log(f"[bench] host medians: fwd {host['fwd_median_ms']:.3f} ms"
+        + (f", bwd {host['bwd_median_ms']:.3f} ms" if backward else ""))
 
     roofline = None
     binning_sort = None
@@ -741,12 +979,13 @@ def main() -> int:
                    else sort_mode)
         # the two-pass sizing scan reads the cover words; the one-pass scan does not
         sized_scan = "buckets" in dataflows and not _pipeline.SCAN_ONEPASS
-        algo = algorithmic_bytes(N, R, P, T, flow_of, flow_k, E_mean, V_mean, sized_scan)
+        algo = algorithmic_bytes(N, R, P, T, flow_of, flow_k, E_mean, V_mean, sized_scan, sh_coeffs)
         # The formula counts every pair once per stage.  The backward reads each tile's
         # list only from its largest n_contrib (visited pairs), and the forward stops a
         # slice once all its pixels have stopped: where that happens the formula does not
         # describe the work, and its fraction is not given (the visited figures are).
-        visited_algo = algorithmic_bytes(N, R_visited, P, T, "warp_radix", flow_k) if R_visited else {}
+        visited_algo = (algorithmic_bytes(N, R_visited, P, T, "warp_radix", flow_k, sh_coeffs=sh_coeffs)
+                        if R_visited else {})
         formula_applies = {"render": early_share <= 0.01,
                            "render_bwd": R_visited is None or R_visited >= 0.5 * R}
         for name, ms in sorted(stage_ms.items(), key=lambda kv: -kv[1]):
@@ -794,6 +1033,9 @@ def main() -> int:
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 5),
                     "traffic": read_traffic(dominant, args.config),
                     "algorithmic_bytes_per_launch": algo[dominant]}
+        if roofline["traffic"] is not None:
+            # the counters come from a separate profiled run of the same workload: its R
+            roofline["traffic_source"] = profile_provenance("traffic", args.config)
         if "visited_GBps" in stages[dominant]:
             roofline["visited_achieved"] = stages[dominant]["visited_GBps"]
             roofline["visited_frac"] = stages[dominant]["visited_hbm_frac"]
@@ -804,7 +1046,13 @@ def main() -> int:
     log(f"[bench] device copy bandwidth {copy_gbps:.0f} GB/s")
     if roofline is not None:
         roofline["copy_GBps"] = round(copy_gbps, 1)
-    iteration_bytes = 1056.0 * N + 252.0 * R + 52.0 * P + 24.0 * T if Rs else None
+    if not Rs:
+        iteration_bytes = None
+    elif backward:  # the SH3, depth-on fwd+bwd headline formula
+        iteration_bytes = 1056.0 * N + 252.0 * R + 52.0 * P + 24.0 * T
+    else:  # forward only: preprocess + SH + scan + duplicate, keys, sort, ranges, render
+        iteration_bytes = ((112.0 + 36.0 + 12.0 * sh_coeffs + 8.0 + 44.0) * N
+                           + (12.0 + 24.0 * sort_passes(T) + 8.0 + 44.0) * R + 24.0 * P + 16.0 * T)
 
     result = {
         "metric": METRIC,
@@ -826,7 +1074,8 @@ def main() -> int:
                    "parallelism": "single GPU"},
         "fwd_ms": fwd_ms,
         "bwd_ms": bwd_ms,
-        "fwd_bwd_ms": ms_per_step,
+        "fwd_bwd_ms": ms_per_step if backward else None,
+        "host_ms": host,
         "hbm_copy_GBps": round(copy_gbps, 1),
         "iteration_hbm_frac": None if iteration_bytes is None else
         round(iteration_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 5),
@@ -835,6 +1084,10 @@ def main() -> int:
         "roofline": roofline,
         "peak_allocated_bytes": peak_bytes,
         "run_to_run": repeat,
+        # figures read from the committed profiles (counter_bytes, roofline.traffic,
+        # valu_issue) were measured in these profiled runs, whose mean R may differ
+        "profile_sources": {kind: profile_provenance(kind, args.config)
+                            for kind in ("traffic", "sq_counters", "kernel_stats")},
         "cpu_baseline": None,
         "parity": None,
     }
@@ -842,7 +1095,7 @@ def main() -> int:
         log("[bench] CPU baseline and parity check (oracle) ...")
         # the scene carries the iteration-0 camera
         top_k = _runtime.get_flow_topk() if flow else 0
-        baseline, parity = cpu_baseline_and_parity(scene, grads, first, flow, top_k)
+        baseline, parity = cpu_baseline_and_parity(scene, grads, first, flow, top_k, backward=backward)
         result["cpu_baseline"], result["parity"] = baseline, parity
         log(f"[bench] CPU baseline {baseline['seconds']:.2f} s on {baseline['cores']} threads, "
             f"{baseline['seconds_1thread']:.2f} s on 1; parity {'ok' if parity['ok'] else 'FAILED'}")

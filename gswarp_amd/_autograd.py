@@ -30,7 +30,8 @@ def _run_forward(ctx, means3D, sh, colors_precomp, opacities, scales, rotations,
     options = resolve_execution_options(raster_settings, flow=flow)
     inputs = _forward_args(means3D, sh, colors_precomp, opacities, scales, rotations, cov3Ds_precomp, raster_settings)
     with execution_options(options):
-        result = _pipeline.forward(inputs, options, flow=flow, grad_buffer=any(ctx.needs_input_grad))
+        result = _pipeline.forward(inputs, options, flow=flow,
+                                   grad_buffer=_pipeline.ACCUMULATOR_IN_FORWARD and any(ctx.needs_input_grad))
     ctx.raster_settings = raster_settings
     ctx.execution_options = options
     ctx.num_rendered = result.num_rendered

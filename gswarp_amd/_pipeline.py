@@ -34,6 +34,14 @@ MAX_BINNING_PAIRS = (1 << 31) - 1
 # HIP events on the launch stream).  None disables it.
 STAGE_TIMER = None
 
+# The autograd forward allocates the backward's (N, 10) gradient accumulator
+# and has its render zero it (gs_render_fwd_clear), which spares the backward
+# a fill launch; the buffer (40 B per Gaussian) is then held from the forward
+# until its backward.  A loop that runs several forwards before one backward
+# holds one per pending forward: with False the backward allocates and fills
+# its own, one at a time.
+ACCUMULATOR_IN_FORWARD = True
+
 
 def _stage(name: str):
     timer = STAGE_TIMER

@@ -113,3 +113,24 @@ def test_autograd_uses_the_cleared_buffer_once(device):
         for other in (b, c):
             err = float((a - other).abs().max())
             assert err <= 1e-4 * scale, (i, err, scale)
+
+
+def test_accumulator_allocated_in_backward(device):
+    """With ACCUMULATOR_IN_FORWARD off the forward allocates no accumulator
+    and the backward allocates and fills its own: the gradients equal those of
+    the default path (to the rounding of the atomics' order)."""
+    from gswarp_amd import _pipeline
+
+    scene = configs.make_scene(2, count=20_000, width=320, height=200, device=device)
+    default = _autograd_step(scene, device)
+    _pipeline.ACCUMULATOR_IN_FORWARD = False
+    try:
+        own = _autograd_step(scene, device)
+    finally:
+        _pipeline.ACCUMULATOR_IN_FORWARD = True
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(default, own)):
+        assert bool(torch.isfinite(b).all()), i
+        scale = float(a.abs().max()) + 1e-30
+        err = float((a - b).abs().max())
+        assert err <= 1e-4 * scale, (i, err, scale)
