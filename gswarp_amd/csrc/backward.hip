@@ -86,6 +86,29 @@ __device__ __forceinline__ void wave_fold10(const float (&g)[10], float (&m)[3])
 constexpr int kSlotFloats = 12 * 16;
 constexpr int kSlotPad = 64 * 4 - kSlotFloats;  // a whole wave's float4 read of the slot
 
+// The address of Gaussian gid's (wave-uniform) row of grad_gauss, formed on
+// the scalar unit: the empty asm keeps it in scalar registers and opaque, so
+// the compiler adds each lane's component offset to it (the atomics'
+// scalar-base addressing) instead of merging the per-lane pointers with a
+// 64-bit vector multiply-add at every flush.
+typedef __attribute__((address_space(1))) float global_float;
+
+__device__ __forceinline__ global_float* grad_row(float* grad_gauss, int gid) {
+  uint64_t addr = reinterpret_cast<uint64_t>(grad_gauss) +
+                  (uint64_t)(unsigned)__builtin_amdgcn_readfirstlane(gid) * (kGradFloats * sizeof(float));
+  asm volatile("" : "+s"(addr));
+  return reinterpret_cast<global_float*>(addr);
+}
+
+// Adds v to component comp of a grad_gauss row (no value returned); the
+// 32-bit byte offset lets the atomic take the row address from scalar
+// registers.
+__device__ __forceinline__ void global_add(global_float* row, unsigned comp, float v) {
+  typedef __attribute__((address_space(1))) char global_char;
+  global_float* const p = reinterpret_cast<global_float*>(reinterpret_cast<global_char*>(row) + comp * 4u);
+  (void)__builtin_amdgcn_global_atomic_fadd_f32(p, v);
+}
+
 // Component at slot position p (-1: a duplicated row): {0, 1, 5, 6, 2, 3, 7,
 // 8, 4, -1, 9, -1}.
 __device__ __forceinline__ int slot_component(int p) {
@@ -105,8 +128,8 @@ __device__ __forceinline__ void flush_slot(const float* slot, int gid, int lane,
   float t = (v.x + v.y) + (v.z + v.w);
   t = t + dpp_mov<0xB1, 0xF>(t);  // quad_perm [1,0,3,2]
   t = t + dpp_mov<0x4E, 0xF>(t);  // quad_perm [2,3,0,1]
-  if ((lane & 3) == 0 && comp >= 0 && t != 0.0f)
-    unsafeAtomicAdd(grad_gauss + (size_t)gid * kGradFloats + comp, t);
+  global_float* const row = grad_row(grad_gauss, gid);
+  if ((lane & 3) == 0 && comp >= 0 && t != 0.0f) global_add(row, (unsigned)comp, t);
 }
 
 // Column-slice reduction through LDS (kCols == 1: a lane's pixels lie in the
@@ -158,7 +181,10 @@ __device__ __forceinline__ int col_flush_component(int lane) {
 __device__ __forceinline__ void flush_col_slot(float4 v, int gid, int comp, float* grad_gauss) {
   float t = (v.x + v.y) + (v.z + v.w);
   t = t + dpp_mov<0xB1, 0xF>(t);  // quad_perm [1,0,3,2]: the pair partner's sum
-  if (comp >= 0 && t != 0.0f) unsafeAtomicAdd(grad_gauss + (size_t)gid * kGradFloats + comp, t);
+  // The Gaussian's row is wave-uniform: its address is formed on the scalar
+  // unit, and each lane adds only its component's offset.
+  global_float* const row = grad_row(grad_gauss, gid);
+  if (comp >= 0 && t != 0.0f) global_add(row, (unsigned)comp, t);
 }
 
 // The wave's LDS besides the records: the fold slot of wave_fold10, or the
@@ -211,27 +237,6 @@ struct RenderBwdParams {
   int long_tile;  // list length above which a tile is walked by four one-pixel-per-lane slices
   float* grad_gauss;
 };
-
-struct BwdBatch {
-  float4 r0, r1, r2;
-  int id;
-};
-
-__device__ __forceinline__ BwdBatch load_bwd_batch(const RenderBwdParams& p, int first, int cnt, int lane) {
-  BwdBatch b;
-  b.id = 0;
-  b.r0 = b.r1 = b.r2 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  if (lane < cnt) {
-    int id = p.point_list[first + lane];
-    if ((unsigned)id >= (unsigned)p.num_points) id = 0;  // guards inconsistent caller input only
-    const float4* rec = p.records + 3 * (size_t)id;
-    b.r0 = rec[0];
-    b.r1 = rec[1];
-    b.r2 = rec[2];
-    b.id = id;
-  }
-  return b;
-}
 
 // One wave walks a slice of kPix blocks of 8x8 pixels, kCols blocks wide:
 // lane l owns pixel (l % 8, l / 8) of every block, block k lying at
@@ -334,14 +339,25 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
   const int col_fcomp = col_flush_component(lane);
   int slot_gid = -1;  // Gaussian whose sums the slot holds (wave-uniform), -1: none
 
+  // Batches of 64 list entries, back to front: [bs, batch_end).  The loads
+  // run ahead: a batch's records were requested during the batch before it,
+  // from indices requested one batch earlier still, so the only wait for
+  // memory is the one at each batch's start (which also covers the
+  // flushes' atomics: one counter tracks every vector memory operation).
+  // The loads are unconditional (in-bounds entries for lanes past a batch),
+  // which leaves the compiler nothing to merge, and so nothing to wait for,
+  // right after them.
+  const int* const list = p.point_list + rg.x;
   int bs = imax(0, max_lc - 64);
-  BwdBatch next = load_bwd_batch(p, rg.x + bs, max_lc - bs, lane);
+  int id = checked_point(batch_entry(list, bs, max_lc - bs, max_lc, lane), p.num_points);
+  int id_ahead = batch_entry(list, imax(0, bs - 64), bs - imax(0, bs - 64), max_lc, lane);
+  RecordRegs next = load_record(p.records, id);
   for (int batch_end = max_lc; batch_end > 0; batch_end = bs, bs = imax(0, bs - 64)) {
     const int cnt = batch_end - bs;
     // One wave per workgroup: its LDS queue orders these writes before the
-    // broadcast reads below.  The records' unused words (r1.w holds qcut,
-    // which the visits only need as a threshold, and r2.w) carry the
-    // thresholds, and r0.w holds 2b (the visits need b only as 2 b dx, and
+    // broadcast reads below.  In the LDS copy r1.w (qcut, which the visits
+    // only need as a threshold) and r2.w (the culling half-widths, used
+    // above) carry the thresholds, and r0.w holds 2b (the visits need b only as 2 b dx, and
     // (2b) dx rounds exactly as (b dx) 2).
     {
       const BlendThresholds th = blend_thresholds(next.r1.w);
@@ -349,7 +365,7 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
       s_rec[3 * lane + 1] = make_float4(next.r1.x, next.r1.y, next.r1.z, __uint_as_float(th.cand));
       s_rec[3 * lane + 2] = make_float4(next.r2.x, next.r2.y, next.r2.z, __uint_as_float(th.sure));
     }
-    const int batch_id = next.id;  // lane j: Gaussian of record j
+    const int batch_id = id;  // lane j: Gaussian of record j
     // A conic with a <= 0 can give q = -0 (adxx = (a dx) dx = -0), which
     // the forward's 0 <= q test takes and the bit compares do not; batches
     // with such a record add the q == 0 lanes to the candidates.
@@ -358,25 +374,29 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
     // otherwise those that may touch the slice, for every block)
     uint64_t blk[kPix], todo = 0;
     {
-      double bx0 = 0.0, bx1 = 0.0, by0 = 0.0, by1 = 0.0;
-      const bool live = lane < cnt && record_box(next.r0, next.r1, bx0, bx1, by0, by1);
+      const bool live = lane < cnt;
+      const unsigned ext = __float_as_uint(next.r2.w);
       if constexpr (kBlockCull) {
 #pragma unroll
         for (int k = 0; k < kPix; ++k) {
           const float x0 = (float)(sx0 + 8 * (k % kCols)), y0 = (float)(sy0 + 8 * (k / kCols));
-          blk[k] = __ballot(live && box_meets(bx0, bx1, by0, by1, x0, x0 + 7.0f, y0, y0 + 7.0f));
+          blk[k] = __ballot(live && extents_meet(next.r0.x, next.r0.y, ext, x0, x0 + 7.0f, y0, y0 + 7.0f));
           todo |= blk[k];
         }
       } else {
-        todo = __ballot(live && box_meets(bx0, bx1, by0, by1, (float)sx0, (float)(sx0 + kSliceW - 1), (float)sy0,
-                                          (float)(sy0 + kSliceH - 1)));
+        todo = __ballot(live && extents_meet(next.r0.x, next.r0.y, ext, (float)sx0, (float)(sx0 + kSliceW - 1),
+                                             (float)sy0, (float)(sy0 + kSliceH - 1)));
 #pragma unroll
         for (int k = 0; k < kPix; ++k) blk[k] = todo;
       }
     }
-    if (bs > 0) {
-      const int nbs = imax(0, bs - 64);
-      next = load_bwd_batch(p, rg.x + nbs, bs - nbs, lane);
+    // the next batch [bs - 64, bs): its records; and the indices of the one
+    // after it (either may be empty: the loads then read a valid entry)
+    {
+      const int nbs = imax(0, bs - 64), nnbs = imax(0, nbs - 64);
+      id = checked_point(id_ahead, p.num_points);
+      next = load_record(p.records, id);
+      id_ahead = batch_entry(list, nnbs, nbs - nnbs, max_lc, lane);
     }
     while (todo != 0) {
       const int jj = 63 - __builtin_clzll(todo);

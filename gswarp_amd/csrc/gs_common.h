@@ -68,7 +68,7 @@ constexpr int kConicMaskMaxTiles = 64;
 // Per-Gaussian render record, 48 bytes = three float4:
 //   r0 = (x, y, conic_a, conic_b)
 //   r1 = (conic_c, opacity, depth, qcut)
-//   r2 = (r, g, b, 0)
+//   r2 = (r, g, b, extents): extents = record_extents(r0, r1), two binary16
 // The blend loops evaluate the Gaussian exponent of a pixel at offset
 // (dx, dy) = (x - px, y - py) as power = -0.5 q with the quadratic form
 //   q = fma(fma(c, dy, 2 b dx), dy, a dx dx)        (conic_q_px below)
@@ -180,53 +180,65 @@ __device__ __forceinline__ float power_cutoff(float opacity) {
 }
 
 // Whether a render record can pass the blend loops' candidate test
-// 0 <= q <= qcut at any pixel centre of the rectangle [x0, x1] x [y0, y1].
-// The candidate set is the ellipse
+// 0 <= q <= qcut at any pixel centre near its mean.  The candidate set is the
+// ellipse
 //   Q(d) = a dx^2 + 2 b dx dy + c dy^2 <= qcut,
 // whose bounding box has half-widths sqrt(qcut c / det) and
 // sqrt(qcut a / det), det = a c - b^2.  The loops evaluate q in fp32 with
 // two fused multiply-adds over per-lane products: every rounding is
 // relative to a term of magnitude at most qcut * (a c / det) inside the box,
 // so the fp32 q can pass the test only where the exact Q <= qcut
-// (1 + 4 * 2^-24 * 3 * ac/det).  The box below is computed in double (a c
+// (1 + 4 * 2^-24 * 3 * ac/det).  The half-widths are computed in double (a c
 // and b^2 are exact there) for qcut inflated ten times that bound, plus
 // 0.02 px; conics that are not positive definite or so elongated
-// (ac/det >= 1e5) that the bound is weak are never culled.  Returning true
-// is always safe: it only costs the per-pixel test.  record_box gives the box
-// (the whole plane for a conic it never culls) and returns false when no
-// pixel can blend the record; record_may_touch tests it against one
-// rectangle.
-__device__ __forceinline__ bool record_box(float4 r0, float4 r1, double& bx0, double& bx1, double& by0,
-                                           double& by1) {
+// (ac/det >= 1e5) that the bound is weak are never culled (infinite
+// half-widths), and a record that no pixel can blend (qcut < 0) gets
+// negative infinite ones.  The preprocess stores them in the record's last
+// word (record_extents), so the blend kernels test a batch against a pixel
+// rectangle with a few fp32 operations (extents_meet) instead of evaluating
+// the box per batch.  Meeting is always safe to report: it only costs the
+// per-pixel test.
+
+// x >= 0 (or +inf) as binary16, rounded up.
+__device__ __forceinline__ unsigned half_bits_up(float x) {
+  const _Float16 h = (_Float16)x;  // round to nearest (overflow: +inf)
+  unsigned bits = (unsigned)__builtin_bit_cast(unsigned short, h);
+  if ((float)h < x) bits += 1u;  // the next binary16 above (0x7bff + 1 = +inf)
+  return bits;
+}
+
+// The record's candidate half-widths (ex, ey) about its mean (r0.x, r0.y),
+// as two binary16 rounded up, ex in the low half: widened by 1/64 px, which
+// covers the fp32 rounding of extents_meet's sums for coordinates below
+// 2^16 (beyond that the widths are infinite).  Never-culled conics: +inf;
+// records that no pixel blends: -inf.
+__device__ __forceinline__ unsigned record_extents(float4 r0, float4 r1) {
+  const unsigned kInf = 0x7C00u, kNegInf = 0xFC00u;
   const float qcut = r1.w;
-  if (qcut < 0.0f) return false;  // alpha < 1/255 at every exponent <= 0
+  if (qcut < 0.0f) return kNegInf | (kNegInf << 16);  // alpha < 1/255 at every exponent <= 0
   const double a = r0.z, b = r0.w, c = r1.x;
   const double ac = a * c;
   const double det = ac - b * b;
-  if (!(a > 0.0 && c > 0.0 && det > 0.0 && ac < 1.0e5 * det)) {
-    bx0 = by0 = -__builtin_inf();
-    bx1 = by1 = __builtin_inf();
-    return true;
-  }
+  if (!(a > 0.0 && c > 0.0 && det > 0.0 && ac < 1.0e5 * det)) return kInf | (kInf << 16);
   const double q = (double)qcut * (1.0 + 8.0e-6 * (ac / det)) + 1.0e-6;
-  const double ex = sqrt(q * c / det) + 0.02;
-  const double ey = sqrt(q * a / det) + 0.02;
-  bx0 = (double)r0.x - ex;
-  bx1 = (double)r0.x + ex;
-  by0 = (double)r0.y - ey;
-  by1 = (double)r0.y + ey;
-  return true;
+  const double ex = sqrt(q * c / det) + 0.02 + 1.0 / 64.0;
+  const double ey = sqrt(q * a / det) + 0.02 + 1.0 / 64.0;
+  const double far = 65536.0;
+  if (!(fabs((double)r0.x) + ex < far && fabs((double)r0.y) + ey < far)) return kInf | (kInf << 16);
+  // double -> float rounded up, then -> binary16 rounded up
+  float fx = (float)ex, fy = (float)ey;  // positive and finite here
+  if ((double)fx < ex) fx = __uint_as_float(__float_as_uint(fx) + 1u);
+  if ((double)fy < ey) fy = __uint_as_float(__float_as_uint(fy) + 1u);
+  return half_bits_up(fx) | (half_bits_up(fy) << 16);
 }
 
-// Whether a record_box meets the pixel rectangle [x0, x1] x [y0, y1].
-__device__ __forceinline__ bool box_meets(double bx0, double bx1, double by0, double by1, float x0, float x1,
-                                          float y0, float y1) {
-  return !(bx1 < (double)x0 || bx0 > (double)x1 || by1 < (double)y0 || by0 > (double)y1);
-}
-
-__device__ __forceinline__ bool record_may_touch(float4 r0, float4 r1, float x0, float x1, float y0, float y1) {
-  double bx0, bx1, by0, by1;
-  return record_box(r0, r1, bx0, bx1, by0, by1) && box_meets(bx0, bx1, by0, by1, x0, x1, y0, y1);
+// Whether a record with half-widths word w about (cx, cy) may meet the pixel
+// rectangle [x0, x1] x [y0, y1] (pixel centres).
+__device__ __forceinline__ bool extents_meet(float cx, float cy, unsigned w, float x0, float x1, float y0,
+                                             float y1) {
+  const float ex = (float)__builtin_bit_cast(_Float16, (unsigned short)(w & 0xFFFFu));
+  const float ey = (float)__builtin_bit_cast(_Float16, (unsigned short)(w >> 16));
+  return cx + ex >= x0 && cx - ex <= x1 && cy + ey >= y0 && cy - ey <= y1;
 }
 
 // Largest quadratic form q at which alpha can still reach 1/255:
@@ -248,6 +260,35 @@ __device__ __forceinline__ float conic_q_px(float adxx, float b2dx, float c, flo
 // q == 0 lanes only for batches holding such a conic.
 __device__ __forceinline__ unsigned cand_threshold(float qcut) {
   return qcut >= 0.0f ? __float_as_uint(qcut) + 1u : 0u;
+}
+
+// A render record as the blend kernels load it: three float4.
+struct RecordRegs {
+  float4 r0, r1, r2;
+};
+
+__device__ __forceinline__ RecordRegs load_record(const float4* records, int id) {
+  const float4* rec = records + 3 * (size_t)id;
+  RecordRegs r;
+  r.r0 = rec[0];
+  r.r1 = rec[1];
+  r.r2 = rec[2];
+  return r;
+}
+
+// A list entry's Gaussian index, 0 for an index outside [0, num_points)
+// (which only inconsistent caller input can hold).
+__device__ __forceinline__ int checked_point(int id, int num_points) {
+  return (unsigned)id < (unsigned)num_points ? id : 0;
+}
+
+// The entry of lane `lane` in the batch [first, first + cnt) of a list of n
+// >= 1 entries.  Lanes past the batch read its first entry, and an empty
+// batch reads a valid one, so the blend kernels can issue the load
+// unconditionally: nothing merges the loaded value with another, and so no
+// wait for it comes before it is used, a batch later.
+__device__ __forceinline__ int batch_entry(const int* list, int first, int cnt, int n, int lane) {
+  return list[imax(0, imin(first + imin(lane, imax(cnt, 1) - 1), n - 1))];
 }
 
 __device__ __forceinline__ unsigned wave_min_u32(unsigned v) {

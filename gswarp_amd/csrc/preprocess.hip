@@ -286,9 +286,11 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p)
           if (col.z < 0.0f) { col.z = 0.0f; clamp_bits |= 4; }
         }
         float4* rec = p.records + 3 * (size_t)idx;
-        rec[0] = make_float4(ptx, pty, q0, q1);
-        rec[1] = make_float4(q2, op, p_view_z, quad_cutoff(op));
-        rec[2] = make_float4(col.x, col.y, col.z, 0.0f);
+        const float4 w0 = make_float4(ptx, pty, q0, q1);
+        const float4 w1 = make_float4(q2, op, p_view_z, quad_cutoff(op));
+        rec[0] = w0;
+        rec[1] = w1;
+        rec[2] = make_float4(col.x, col.y, col.z, __uint_as_float(record_extents(w0, w1)));
         if (p.clamped != nullptr) p.clamped[idx] = clamp_bits;
       }
     }

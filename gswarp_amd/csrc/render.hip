@@ -63,27 +63,6 @@ struct RenderFwdParams {
   long long clear_floats;
 };
 
-struct Batch {
-  float4 r0, r1, r2;
-  int id;
-};
-
-__device__ __forceinline__ Batch load_batch(const RenderFwdParams& p, int first, int cnt, int lane) {
-  Batch b;
-  b.id = 0;
-  b.r0 = b.r1 = b.r2 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  if (lane < cnt) {
-    int id = p.point_list[first + lane];
-    if ((unsigned)id >= (unsigned)p.num_points) id = 0;  // guards inconsistent caller input only
-    const float4* rec = p.records + 3 * (size_t)id;
-    b.r0 = rec[0];
-    b.r1 = rec[1];
-    b.r2 = rec[2];
-    b.id = id;
-  }
-  return b;
-}
-
 // Workgroup blockIdx.x's share of the optional buffer to zero, float4 stores
 // issued after its last image store: no later load of the wave waits for them
 // (the vector memory counter covers stores too), and the stores of a finished
@@ -188,7 +167,20 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
     nsucc[k] = 0;
   }
 
-  Batch next = load_batch(p, rg.x, imin(64, n), lane);
+  // Batches of 64 list entries, front to back.  The loads run ahead: a
+  // batch's records were requested during the batch before it, from indices
+  // requested one batch earlier still, so no wave waits for memory but at a
+  // batch's start, for loads issued a whole batch before.  The loads are
+  // unconditional (in-bounds entries for lanes past the list).
+  const int* const list = p.point_list + rg.x;
+  int id = 0, id_ahead = 0;
+  RecordRegs next;
+  next.r0 = next.r1 = next.r2 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (n > 0) {
+    id = checked_point(batch_entry(list, 0, imin(64, n), n, lane), p.num_points);
+    id_ahead = batch_entry(list, 64, imin(64, n - 64), n, lane);
+    next = load_record(p.records, id);
+  }
   for (int base = 0; base < n; base += 64) {
     uint64_t live = 0;
 #pragma unroll
@@ -203,13 +195,17 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
     s_rec[3 * lane] = make_float4(next.r0.x, next.r0.y, next.r0.z, 2.0f * next.r0.w);
     s_rec[3 * lane + 1] = make_float4(next.r1.x, next.r1.y, next.r1.z, __uint_as_float(cand_threshold(next.r1.w)));
     s_rec[3 * lane + 2] = next.r2;
-    if (kFlow) s_id[lane] = next.id;
+    if (kFlow) s_id[lane] = id;
     // A conic with a <= 0 can give q = -0 (adxx = (a dx) dx = -0), which the
     // 0 <= q test takes and the bit compare does not; batches with such a
     // record add the q == 0 lanes to the candidates.
     const bool signed_zero = __ballot(lane < cnt && !(next.r0.z > 0.0f)) != 0;
-    uint64_t todo = __ballot(lane < cnt && record_may_touch(next.r0, next.r1, rx0, rx1, ry0, ry1));
-    if (base + 64 < n) next = load_batch(p, rg.x + base + 64, imin(64, n - base - 64), lane);
+    uint64_t todo = __ballot(lane < cnt && extents_meet(next.r0.x, next.r0.y, __float_as_uint(next.r2.w), rx0, rx1,
+                                                        ry0, ry1));
+    // the next batch's records and the indices of the one after it
+    id = checked_point(id_ahead, p.num_points);
+    next = load_record(p.records, id);
+    id_ahead = batch_entry(list, base + 128, imin(64, n - base - 128), n, lane);
     while (todo != 0) {
       const int j = __builtin_ctzll(todo);
       todo &= todo - 1;
@@ -295,7 +291,7 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
       auto list_id = [&](int s) {
         if (s >= used) return -1;
         int id = p.point_list[rg.x + pos[s * kPixPerLane * 64]];
-        return (unsigned)id < (unsigned)p.num_points ? id : 0;  // as load_batch
+        return (unsigned)id < (unsigned)p.num_points ? id : 0;  // as checked_point
       };
       int id_a = list_id(0);
       int id_b = list_id(1);

@@ -25,7 +25,10 @@
  *   campos (3), background (3): all fp32, C-contiguous.
  *   records (N,12) fp32, 16-byte aligned: per-Gaussian render record
  *     (x, y, conic_a, conic_b | conic_c, opacity, depth, power_cutoff |
- *      r, g, b, 0).
+ *      r, g, b, extents): extents packs the half-widths of the pixel
+ *      region the record can blend as two binary16 (rounded up) for the
+ *      blend kernels' culling; gs_render_* expect it as gs_preprocess_fwd
+ *      writes it.
  *   images: color (3,H,W), depth (1,H,W), alpha (1,H,W), n_contrib (H,W) int32.
  *   ranges (T,2) int32 [start, end) into the sorted pair list.
  *   grad_gauss (N,10) fp32, zero-initialised by the caller, accumulated by
