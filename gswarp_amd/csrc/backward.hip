@@ -26,6 +26,8 @@
 // (backward_kernels.py:114-287) and the accumulation (backward_kernels.py:289-295).
 // cov3D is recomputed from scale and rotation with the forward's exact
 // expression instead of being stored by the forward pass.
+#include <type_traits>
+
 #include "gs_common.h"
 #include "gs_capi.h"
 
@@ -87,26 +89,22 @@ constexpr int kSlotFloats = 12 * 16;
 constexpr int kSlotPad = 64 * 4 - kSlotFloats;  // a whole wave's float4 read of the slot
 
 // The address of Gaussian gid's (wave-uniform) row of grad_gauss, formed on
-// the scalar unit: the empty asm keeps it in scalar registers and opaque, so
-// the compiler adds each lane's component offset to it (the atomics'
-// scalar-base addressing) instead of merging the per-lane pointers with a
-// 64-bit vector multiply-add at every flush.
-typedef __attribute__((address_space(1))) float global_float;
-
-__device__ __forceinline__ global_float* grad_row(float* grad_gauss, int gid) {
-  uint64_t addr = reinterpret_cast<uint64_t>(grad_gauss) +
-                  (uint64_t)(unsigned)__builtin_amdgcn_readfirstlane(gid) * (kGradFloats * sizeof(float));
-  asm volatile("" : "+s"(addr));
-  return reinterpret_cast<global_float*>(addr);
+// the scalar unit.
+__device__ __forceinline__ uint64_t grad_row(float* grad_gauss, int gid) {
+  return reinterpret_cast<uint64_t>(grad_gauss) +
+         (uint64_t)(unsigned)__builtin_amdgcn_readfirstlane(gid) * (kGradFloats * sizeof(float));
 }
 
-// Adds v to component comp of a grad_gauss row (no value returned); the
-// 32-bit byte offset lets the atomic take the row address from scalar
-// registers.
-__device__ __forceinline__ void global_add(global_float* row, unsigned comp, float v) {
-  typedef __attribute__((address_space(1))) char global_char;
-  global_float* const p = reinterpret_cast<global_float*>(reinterpret_cast<global_char*>(row) + comp * 4u);
-  (void)__builtin_amdgcn_global_atomic_fadd_f32(p, v);
+// Adds v to component comp of a grad_gauss row, no value returned: a vector
+// memory atomic in its scalar-base form (the row address in scalar
+// registers, each lane's 32-bit byte offset in a vector register).  Written
+// as one instruction because the compiler otherwise forms every lane's
+// 64-bit address with a vector 64-bit add at each flush.  Its completion is
+// counted by the same in-order vector memory counter as the compiler's own
+// loads, so any wait the compiler places for a load issued before it also
+// covers it; nothing in the kernel reads grad_gauss.
+__device__ __forceinline__ void global_add(uint64_t row, unsigned comp, float v) {
+  asm volatile("global_atomic_add_f32 %0, %1, %2" : : "v"(comp * 4u), "v"(v), "s"(row) : "memory");
 }
 
 // Component at slot position p (-1: a duplicated row): {0, 1, 5, 6, 2, 3, 7,
@@ -128,7 +126,7 @@ __device__ __forceinline__ void flush_slot(const float* slot, int gid, int lane,
   float t = (v.x + v.y) + (v.z + v.w);
   t = t + dpp_mov<0xB1, 0xF>(t);  // quad_perm [1,0,3,2]
   t = t + dpp_mov<0x4E, 0xF>(t);  // quad_perm [2,3,0,1]
-  global_float* const row = grad_row(grad_gauss, gid);
+  const uint64_t row = grad_row(grad_gauss, gid);
   if ((lane & 3) == 0 && comp >= 0 && t != 0.0f) global_add(row, (unsigned)comp, t);
 }
 
@@ -183,7 +181,7 @@ __device__ __forceinline__ void flush_col_slot(float4 v, int gid, int comp, floa
   t = t + dpp_mov<0xB1, 0xF>(t);  // quad_perm [1,0,3,2]: the pair partner's sum
   // The Gaussian's row is wave-uniform: its address is formed on the scalar
   // unit, and each lane adds only its component's offset.
-  global_float* const row = grad_row(grad_gauss, gid);
+  const uint64_t row = grad_row(grad_gauss, gid);
   if (comp >= 0 && t != 0.0f) global_add(row, (unsigned)comp, t);
 }
 
@@ -398,182 +396,201 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
       next = load_record(p.records, id);
       id_ahead = batch_entry(list, nnbs, nbs - nnbs, max_lc, lane);
     }
-    while (todo != 0) {
-      const int jj = 63 - __builtin_clzll(todo);
-      todo ^= 1ull << jj;
-      const int pos = bs + jj;
-      const float4 a = s_rec[3 * jj];
-      const float4 b = s_rec[3 * jj + 1];
-      const float4 f = s_rec[3 * jj + 2];
-      const unsigned thr_cand = __float_as_uint(b.w), thr_sure = __float_as_uint(f.w);
-      float dx[kCols], adxx[kCols], b2dx[kCols];
+    // Pixel k is active at list position pos when pos < last[k].  The
+    // lanes whose pixel is active at every position of the batch (last >=
+    // batch_end) form one mask per pixel; only a batch in which some pixel's
+    // last contributor lies (bs < last < batch_end) has its visits compare
+    // positions.  The walk is instantiated for both cases.
+    uint64_t act_all[kPix];
+    bool partial = false;
 #pragma unroll
-      for (int c = 0; c < kCols; ++c) {
-        dx[c] = a.x - pfx[c];
-        adxx[c] = a.z * dx[c] * dx[c];
-        b2dx[c] = a.w * dx[c];  // a.w = 2b
-      }
-      float q[kPix], dy[kPix];
-      uint64_t cand_lanes[kPix];  // the wave's lanes whose pixel k is a candidate
-      uint64_t sure_lanes[kPix];  // ... and surely blends
-      uint64_t any_lanes = 0, band = 0;  // band: lanes with a candidate that is not sure
-#pragma unroll
-      for (int k = 0; k < kPix; ++k) {
-        q[k] = dy[k] = 0.0f;
-        cand_lanes[k] = 0;
-        if (kBlockCull && !((blk[k] >> jj) & 1)) continue;  // the record's box misses block k
-        const int c = k % kCols;
-        dy[k] = a.y - pfy[k];
-        q[k] = conic_q_px(adxx[c], b2dx[c], b.x, dy[k]);  // exponent = -0.5 q
-        // Lane masks of pos < last and 0 <= q <= qcut (the bit compare of
-        // blend_thresholds), ANDed in scalar registers.
-        const uint64_t act = __builtin_amdgcn_sicmp(pos, last[k], kCmpSLT);
-        cand_lanes[k] = act & __builtin_amdgcn_uicmp(__float_as_uint(q[k]), thr_cand, kCmpULT);
-        if (signed_zero) cand_lanes[k] |= act & __builtin_amdgcn_fcmpf(q[k], 0.0f, kCmpOEQ);
-        any_lanes |= cand_lanes[k];
-      }
-      if (any_lanes == 0) continue;
-      // ... and 0 <= q <= qsure, only for visits with a candidate
-#pragma unroll
-      for (int k = 0; k < kPix; ++k) {
-        sure_lanes[k] = cand_lanes[k] & __builtin_amdgcn_uicmp(__float_as_uint(q[k]), thr_sure, kCmpULT);
-        band |= cand_lanes[k] & ~sure_lanes[k];
-      }
-      // Blend decisions, identical to the forward's: with the exponent above
-      // power_cutoff + 2e-3 (q <= qcut - 4e-3) the forward's alpha is provably
-      // >= 1/255 (the cutoff sits 1e-3 below -ln(255 o) and exp_sw / log_sw
-      // err by < 1e-6 relative), above qcut provably < 1/255; only the thin
-      // band between (and q = -0) needs exp_sw.  e = log2 of the Gaussian
-      // value G for pixels that blend, -inf (G = 0) for the others.
-      float e[kPix];
-#pragma unroll
-      for (int k = 0; k < kPix; ++k)
-        e[k] = __builtin_amdgcn_inverse_ballot_w64(sure_lanes[k]) ? q[k] * (-0.5f * kLog2e) : -__builtin_inff();
-      if (band != 0) {
-#pragma unroll
-        for (int k = 0; k < kPix; ++k) {
-          // in the band 0 <= q, so the exponential's argument is non-positive;
-          // on other lanes its value (inf or NaN included) is masked out
-          const uint64_t band_lanes = cand_lanes[k] & ~sure_lanes[k];
-          const float a_sw = fminf(kAlphaMax, b.y * exp_sw_q(q[k]));
-          const bool blends = __builtin_amdgcn_inverse_ballot_w64(
-              band_lanes & __builtin_amdgcn_fcmpf(a_sw, kAlphaMin, kCmpOGE));
-          e[k] = blends ? q[k] * (-0.5f * kLog2e) : e[k];
-        }
-      }
-      // -0 is the additive identity of every float, so the first terms
-      // enter the sums exactly (and the compiler drops the additions).
-      float sv[kCols], svy[kCols];
-#pragma unroll
-      for (int c = 0; c < kCols; ++c) sv[c] = svy[c] = -0.0f;
-      float svyy = -0.0f, sr = -0.0f, sg = -0.0f, sb = -0.0f, sd = -0.0f;
-      // One pixel's terms; the sums start at -0, the additive identity of
-      // every float, so the first pixel's terms enter them exactly.
-      auto blend = [&](int k) {
-        const int c = k % kCols;
-        // Gradient values use the hardware exponential (v_exp_f32): they only
-        // need the 1e-3 gradient tolerance, the decisions above are exact.
-        // A pixel that does not blend this Gaussian gets G = 2^-inf = 0, so
-        // alpha = 0, 1/T is unchanged (an exact fma), S is unchanged and it
-        // adds exact zeros.
-        const float G = __builtin_amdgcn_exp2f(e[k]);
-        const float alpha = fminf(kAlphaMax, b.y * G);
-        // 1/T in front of this Gaussian: (1/T behind it) (1 - alpha), with
-        // 1 - alpha >= 1 - kAlphaMax (the reference's 1e-5 floor never applies)
-        const float tin = fmaf(-alpha, Ti[k], Ti[k]);
-        const float Tn = __builtin_amdgcn_rcpf(tin);
-        float fu = fmaf(f.z, gp2[k], fmaf(f.y, gp1[k], fmaf(f.x, gp0[k], gpa[k])));
-        if (kDepth) fu = fmaf(b.z, gpd[k], fu);
-        const float d = fu - S[k];
-        const float v = G * (Tn * d);
-        const float dch = alpha * Tn;
-        const float vdy = v * dy[k];
-        sv[c] += v;
-        svy[c] += vdy;
-        svyy = fmaf(vdy, dy[k], svyy);
-        sr = fmaf(dch, gp0[k], sr);
-        sg = fmaf(dch, gp1[k], sg);
-        sb = fmaf(dch, gp2[k], sb);
-        if (kDepth) sd = fmaf(dch, gpd[k], sd);
-        // this Gaussian joins what lies behind the next (nearer) one:
-        // alpha fu + (1 - alpha) S = S + alpha (fu - S)
-        S[k] = fmaf(alpha, d, S[k]);
-        Ti[k] = tin;
-      };
-      // A block with no candidate in the whole wave is skipped: there G = 0
-      // for every lane, which leaves 1/T, S and the sums unchanged.  With two
-      // blocks, whichever is visited first starts the sums on each path, so
-      // a visit that skips the first block computes no -0 starting values.
-      if constexpr (kPix == 2) {
-        if (cand_lanes[0] != 0) {
-          blend(0);
-          if (cand_lanes[1] != 0) blend(1);
-        } else {
-          blend(1);
-        }
-      } else {
-#pragma unroll
-        for (int k = 0; k < kPix; ++k)
-          if (cand_lanes[k] != 0) blend(k);
-      }
-      // Pixel moments of v about the Gaussian's mean; the conic, opacity
-      // and W/2, H/2 factors are per Gaussian and applied once, when the
-      // per-Gaussian backward turns the sums into 2D gradients.
-      if constexpr (kCols == 1) {
-        // The transposed store of this Gaussian's sums, then (the wave's LDS
-        // operations complete in order) the reads of the previous Gaussian's
-        // slot and of this Gaussian's column groups, and the new slot after
-        // the flush.
-        col_raw[raw_ofs] = sv[0];
-        col_raw[64 + raw_ofs] = svy[0];
-        col_raw[128 + raw_ofs] = svyy;
-        col_raw[192 + raw_ofs] = sr;
-        col_raw[256 + raw_ofs] = sg;
-        col_raw[320 + raw_ofs] = sb;
-        col_raw[384 + raw_ofs] = sd;
-        const float4 prev = reinterpret_cast<const float4*>(s_slot)[col_fidx];
-        const float4 ga = reinterpret_cast<const float4*>(col_raw)[raw_grp];
-        const float4 gb = reinterpret_cast<const float4*>(col_raw)[raw_grp + 1];
-        if (slot_gid >= 0) flush_col_slot(prev, slot_gid, col_fcomp, p.grad_gauss);
-        slot_gid = __builtin_amdgcn_readlane(batch_id, jj);
-        const float col_sum = ((ga.x + ga.y) + (ga.z + ga.w)) + ((gb.x + gb.y) + (gb.z + gb.w));
-        const float col_dx = col_sum * dx[0];
-        s_slot[lane] = col_sum;
-        s_slot[64 + lane] = col_dx;
-        s_slot[128 + lane] = col_dx * dx[0];
-      } else {
-        float m[3];
-        float g[kGradFloats];
-        float vdx = sv[0] * dx[0];
-        g[0] = vdx;               // sum v dx
-        g[1] = svy[0];            // sum v dy
-        g[2] = vdx * dx[0];       // sum v dx^2
-        g[3] = svy[0] * dx[0];    // sum v dx dy
-        g[5] = sv[0];             // dL/dopacity
-#pragma unroll
-        for (int c = 1; c < kCols; ++c) {
-          vdx = sv[c] * dx[c];
-          g[0] += vdx;
-          g[1] += svy[c];
-          g[2] = fmaf(vdx, dx[c], g[2]);
-          g[3] = fmaf(svy[c], dx[c], g[3]);
-          g[5] += sv[c];
-        }
-        g[4] = svyy;              // sum v dy^2
-        g[6] = sr;
-        g[7] = sg;
-        g[8] = sb;
-        g[9] = sd;
-        wave_fold10(g, m);
-        if (slot_gid >= 0) flush_slot(s_slot, slot_gid, lane, flush_comp, p.grad_gauss);
-        slot_gid = __builtin_amdgcn_readlane(batch_id, jj);
-        // The wave's LDS operations complete in order: these stores follow
-        // the flush's read of the previous Gaussian's sums.
-        s_slot[lane] = m[0];
-        s_slot[64 + lane] = m[1];
-        s_slot[128 + lane] = m[2];
-      }
+    for (int k = 0; k < kPix; ++k) {
+      act_all[k] = __ballot(last[k] >= batch_end);
+      partial |= __ballot(last[k] > bs && last[k] < batch_end) != 0;
     }
+    auto walk = [&](auto partial_tag) {
+      constexpr bool kPartial = decltype(partial_tag)::value;
+      while (todo != 0) {
+        const int jj = 63 - __builtin_clzll(todo);
+        todo ^= 1ull << jj;
+        const int pos = bs + jj;
+        const float4 a = s_rec[3 * jj];
+        const float4 b = s_rec[3 * jj + 1];
+        const float4 f = s_rec[3 * jj + 2];
+        const unsigned thr_cand = __float_as_uint(b.w), thr_sure = __float_as_uint(f.w);
+        float dx[kCols], adxx[kCols], b2dx[kCols];
+  #pragma unroll
+        for (int c = 0; c < kCols; ++c) {
+          dx[c] = a.x - pfx[c];
+          adxx[c] = a.z * dx[c] * dx[c];
+          b2dx[c] = a.w * dx[c];  // a.w = 2b
+        }
+        float q[kPix], dy[kPix];
+        uint64_t cand_lanes[kPix];  // the wave's lanes whose pixel k is a candidate
+        uint64_t sure_lanes[kPix];  // ... and surely blends
+        uint64_t any_lanes = 0, band = 0;  // band: lanes with a candidate that is not sure
+  #pragma unroll
+        for (int k = 0; k < kPix; ++k) {
+          q[k] = dy[k] = 0.0f;
+          cand_lanes[k] = 0;
+          if (kBlockCull && !((blk[k] >> jj) & 1)) continue;  // the record's box misses block k
+          const int c = k % kCols;
+          dy[k] = a.y - pfy[k];
+          q[k] = conic_q_px(adxx[c], b2dx[c], b.x, dy[k]);  // exponent = -0.5 q
+          // Lane masks of pos < last and 0 <= q <= qcut (the bit compare of
+          // blend_thresholds), ANDed in scalar registers.
+          const uint64_t act = kPartial ? __builtin_amdgcn_sicmp(pos, last[k], kCmpSLT) : act_all[k];
+          cand_lanes[k] = act & __builtin_amdgcn_uicmp(__float_as_uint(q[k]), thr_cand, kCmpULT);
+          if (signed_zero) cand_lanes[k] |= act & __builtin_amdgcn_fcmpf(q[k], 0.0f, kCmpOEQ);
+          any_lanes |= cand_lanes[k];
+        }
+        if (any_lanes == 0) continue;
+        // ... and 0 <= q <= qsure, only for visits with a candidate
+  #pragma unroll
+        for (int k = 0; k < kPix; ++k) {
+          sure_lanes[k] = cand_lanes[k] & __builtin_amdgcn_uicmp(__float_as_uint(q[k]), thr_sure, kCmpULT);
+          band |= cand_lanes[k] & ~sure_lanes[k];
+        }
+        // Blend decisions, identical to the forward's: with the exponent above
+        // power_cutoff + 2e-3 (q <= qcut - 4e-3) the forward's alpha is provably
+        // >= 1/255 (the cutoff sits 1e-3 below -ln(255 o) and exp_sw / log_sw
+        // err by < 1e-6 relative), above qcut provably < 1/255; only the thin
+        // band between (and q = -0) needs exp_sw.  e = log2 of the Gaussian
+        // value G for pixels that blend, -inf (G = 0) for the others.
+        float e[kPix];
+  #pragma unroll
+        for (int k = 0; k < kPix; ++k)
+          e[k] = __builtin_amdgcn_inverse_ballot_w64(sure_lanes[k]) ? q[k] * (-0.5f * kLog2e) : -__builtin_inff();
+        if (band != 0) {
+  #pragma unroll
+          for (int k = 0; k < kPix; ++k) {
+            // in the band 0 <= q, so the exponential's argument is non-positive;
+            // on other lanes its value (inf or NaN included) is masked out
+            const uint64_t band_lanes = cand_lanes[k] & ~sure_lanes[k];
+            const float a_sw = fminf(kAlphaMax, b.y * exp_sw_q(q[k]));
+            const bool blends = __builtin_amdgcn_inverse_ballot_w64(
+                band_lanes & __builtin_amdgcn_fcmpf(a_sw, kAlphaMin, kCmpOGE));
+            e[k] = blends ? q[k] * (-0.5f * kLog2e) : e[k];
+          }
+        }
+        // -0 is the additive identity of every float, so the first terms
+        // enter the sums exactly (and the compiler drops the additions).
+        float sv[kCols], svy[kCols];
+  #pragma unroll
+        for (int c = 0; c < kCols; ++c) sv[c] = svy[c] = -0.0f;
+        float svyy = -0.0f, sr = -0.0f, sg = -0.0f, sb = -0.0f, sd = -0.0f;
+        // One pixel's terms; the sums start at -0, the additive identity of
+        // every float, so the first pixel's terms enter them exactly.
+        auto blend = [&](int k) {
+          const int c = k % kCols;
+          // Gradient values use the hardware exponential (v_exp_f32): they only
+          // need the 1e-3 gradient tolerance, the decisions above are exact.
+          // A pixel that does not blend this Gaussian gets G = 2^-inf = 0, so
+          // alpha = 0, 1/T is unchanged (an exact fma), S is unchanged and it
+          // adds exact zeros.
+          const float G = __builtin_amdgcn_exp2f(e[k]);
+          const float alpha = fminf(kAlphaMax, b.y * G);
+          // 1/T in front of this Gaussian: (1/T behind it) (1 - alpha), with
+          // 1 - alpha >= 1 - kAlphaMax (the reference's 1e-5 floor never applies)
+          const float tin = fmaf(-alpha, Ti[k], Ti[k]);
+          const float Tn = __builtin_amdgcn_rcpf(tin);
+          float fu = fmaf(f.z, gp2[k], fmaf(f.y, gp1[k], fmaf(f.x, gp0[k], gpa[k])));
+          if (kDepth) fu = fmaf(b.z, gpd[k], fu);
+          const float d = fu - S[k];
+          const float v = G * (Tn * d);
+          const float dch = alpha * Tn;
+          const float vdy = v * dy[k];
+          sv[c] += v;
+          svy[c] += vdy;
+          svyy = fmaf(vdy, dy[k], svyy);
+          sr = fmaf(dch, gp0[k], sr);
+          sg = fmaf(dch, gp1[k], sg);
+          sb = fmaf(dch, gp2[k], sb);
+          if (kDepth) sd = fmaf(dch, gpd[k], sd);
+          // this Gaussian joins what lies behind the next (nearer) one:
+          // alpha fu + (1 - alpha) S = S + alpha (fu - S)
+          S[k] = fmaf(alpha, d, S[k]);
+          Ti[k] = tin;
+        };
+        // A block with no candidate in the whole wave is skipped: there G = 0
+        // for every lane, which leaves 1/T, S and the sums unchanged.  With two
+        // blocks, whichever is visited first starts the sums on each path, so
+        // a visit that skips the first block computes no -0 starting values.
+        if constexpr (kPix == 2) {
+          if (cand_lanes[0] != 0) {
+            blend(0);
+            if (cand_lanes[1] != 0) blend(1);
+          } else {
+            blend(1);
+          }
+        } else {
+  #pragma unroll
+          for (int k = 0; k < kPix; ++k)
+            if (cand_lanes[k] != 0) blend(k);
+        }
+        // Pixel moments of v about the Gaussian's mean; the conic, opacity
+        // and W/2, H/2 factors are per Gaussian and applied once, when the
+        // per-Gaussian backward turns the sums into 2D gradients.
+        if constexpr (kCols == 1) {
+          // The transposed store of this Gaussian's sums, then (the wave's LDS
+          // operations complete in order) the reads of the previous Gaussian's
+          // slot and of this Gaussian's column groups, and the new slot after
+          // the flush.
+          col_raw[raw_ofs] = sv[0];
+          col_raw[64 + raw_ofs] = svy[0];
+          col_raw[128 + raw_ofs] = svyy;
+          col_raw[192 + raw_ofs] = sr;
+          col_raw[256 + raw_ofs] = sg;
+          col_raw[320 + raw_ofs] = sb;
+          col_raw[384 + raw_ofs] = sd;
+          const float4 prev = reinterpret_cast<const float4*>(s_slot)[col_fidx];
+          const float4 ga = reinterpret_cast<const float4*>(col_raw)[raw_grp];
+          const float4 gb = reinterpret_cast<const float4*>(col_raw)[raw_grp + 1];
+          if (slot_gid >= 0) flush_col_slot(prev, slot_gid, col_fcomp, p.grad_gauss);
+          slot_gid = __builtin_amdgcn_readlane(batch_id, jj);
+          const float col_sum = ((ga.x + ga.y) + (ga.z + ga.w)) + ((gb.x + gb.y) + (gb.z + gb.w));
+          const float col_dx = col_sum * dx[0];
+          s_slot[lane] = col_sum;
+          s_slot[64 + lane] = col_dx;
+          s_slot[128 + lane] = col_dx * dx[0];
+        } else {
+          float m[3];
+          float g[kGradFloats];
+          float vdx = sv[0] * dx[0];
+          g[0] = vdx;               // sum v dx
+          g[1] = svy[0];            // sum v dy
+          g[2] = vdx * dx[0];       // sum v dx^2
+          g[3] = svy[0] * dx[0];    // sum v dx dy
+          g[5] = sv[0];             // dL/dopacity
+  #pragma unroll
+          for (int c = 1; c < kCols; ++c) {
+            vdx = sv[c] * dx[c];
+            g[0] += vdx;
+            g[1] += svy[c];
+            g[2] = fmaf(vdx, dx[c], g[2]);
+            g[3] = fmaf(svy[c], dx[c], g[3]);
+            g[5] += sv[c];
+          }
+          g[4] = svyy;              // sum v dy^2
+          g[6] = sr;
+          g[7] = sg;
+          g[8] = sb;
+          g[9] = sd;
+          wave_fold10(g, m);
+          if (slot_gid >= 0) flush_slot(s_slot, slot_gid, lane, flush_comp, p.grad_gauss);
+          slot_gid = __builtin_amdgcn_readlane(batch_id, jj);
+          // The wave's LDS operations complete in order: these stores follow
+          // the flush's read of the previous Gaussian's sums.
+          s_slot[lane] = m[0];
+          s_slot[64 + lane] = m[1];
+          s_slot[128 + lane] = m[2];
+        }
+      }
+    };
+    if (partial)
+      walk(std::true_type{});
+    else
+      walk(std::false_type{});
   }
   if (slot_gid >= 0) {
     if constexpr (kCols == 1)
