@@ -419,7 +419,7 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
         const float4 f = s_rec[3 * jj + 2];
         const unsigned thr_cand = __float_as_uint(b.w), thr_sure = __float_as_uint(f.w);
         float dx[kCols], adxx[kCols], b2dx[kCols];
-  #pragma unroll
+#pragma unroll
         for (int c = 0; c < kCols; ++c) {
           dx[c] = a.x - pfx[c];
           adxx[c] = a.z * dx[c] * dx[c];
@@ -429,7 +429,7 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
         uint64_t cand_lanes[kPix];  // the wave's lanes whose pixel k is a candidate
         uint64_t sure_lanes[kPix];  // ... and surely blends
         uint64_t any_lanes = 0, band = 0;  // band: lanes with a candidate that is not sure
-  #pragma unroll
+#pragma unroll
         for (int k = 0; k < kPix; ++k) {
           q[k] = dy[k] = 0.0f;
           cand_lanes[k] = 0;
@@ -446,7 +446,7 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
         }
         if (any_lanes == 0) continue;
         // ... and 0 <= q <= qsure, only for visits with a candidate
-  #pragma unroll
+#pragma unroll
         for (int k = 0; k < kPix; ++k) {
           sure_lanes[k] = cand_lanes[k] & __builtin_amdgcn_uicmp(__float_as_uint(q[k]), thr_sure, kCmpULT);
           band |= cand_lanes[k] & ~sure_lanes[k];
@@ -458,11 +458,11 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
         // band between (and q = -0) needs exp_sw.  e = log2 of the Gaussian
         // value G for pixels that blend, -inf (G = 0) for the others.
         float e[kPix];
-  #pragma unroll
+#pragma unroll
         for (int k = 0; k < kPix; ++k)
           e[k] = __builtin_amdgcn_inverse_ballot_w64(sure_lanes[k]) ? q[k] * (-0.5f * kLog2e) : -__builtin_inff();
         if (band != 0) {
-  #pragma unroll
+#pragma unroll
           for (int k = 0; k < kPix; ++k) {
             // in the band 0 <= q, so the exponential's argument is non-positive;
             // on other lanes its value (inf or NaN included) is masked out
@@ -476,7 +476,7 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
         // -0 is the additive identity of every float, so the first terms
         // enter the sums exactly (and the compiler drops the additions).
         float sv[kCols], svy[kCols];
-  #pragma unroll
+#pragma unroll
         for (int c = 0; c < kCols; ++c) sv[c] = svy[c] = -0.0f;
         float svyy = -0.0f, sr = -0.0f, sg = -0.0f, sb = -0.0f, sd = -0.0f;
         // One pixel's terms; the sums start at -0, the additive identity of
@@ -524,7 +524,7 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
             blend(1);
           }
         } else {
-  #pragma unroll
+#pragma unroll
           for (int k = 0; k < kPix; ++k)
             if (cand_lanes[k] != 0) blend(k);
         }
@@ -562,7 +562,7 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
           g[2] = vdx * dx[0];       // sum v dx^2
           g[3] = svy[0] * dx[0];    // sum v dx dy
           g[5] = sv[0];             // dL/dopacity
-  #pragma unroll
+#pragma unroll
           for (int c = 1; c < kCols; ++c) {
             vdx = sv[c] * dx[c];
             g[0] += vdx;
