@@ -73,18 +73,19 @@ SIGNATURES = {
     "gs_bin_packed_workspace_bytes": (ctypes.c_size_t, [_i64]),
     "gs_readback_bin_packed": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
                                               _i64, _vp, _sz, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64,
-                                              _vp, _vp, _vp]),
+                                              _vp, _vp, _vp, _vp]),
     "gs_bin_packed": (ctypes.c_int, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, ctypes.c_uint32,
                                      _i32, _i32, _vp, _sz, _vp, _vp, _vp, _vp, _vp]),
-    "gs_render_fwd": (ctypes.c_int, [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "gs_tile_order": (ctypes.c_int, [_i32, _vp, _vp, _vp]),
+    "gs_render_fwd": (ctypes.c_int, [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "gs_render_fwd_clear": (
-        ctypes.c_int, [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
+        ctypes.c_int, [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp]),
     "gs_render_fwd_flow": (
         ctypes.c_int,
-        [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+        [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     ),
     "gs_render_bwd": (
-        ctypes.c_int, [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp],
+        ctypes.c_int, [_i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp],
     ),
     "gs_preprocess_bwd": (
         ctypes.c_int,
@@ -155,8 +156,8 @@ def load() -> _Lib:
 
 
 def preload() -> None:
-    """Load the library at package import when it is built (a missing library
-    raises at the first call instead).  Loaded then, before any GPU work, its
+    """Load the library at package import when it is built (a missing or
+    stale library raises at the first call instead).  Loaded then, before any GPU work, its
     code objects are registered with the HIP runtime in the same order as
     torch's own kernels, and unregistered after the runtime's exit handlers as
     theirs are, rather than by a library that a first call loaded after the
@@ -164,7 +165,13 @@ def preload() -> None:
     import torch  # noqa: F401  (its HIP runtime must be the one the library binds to)
 
     if LIB_PATH.exists():
-        load()
+        try:
+            load()
+        except (AttributeError, OSError):
+            # A library built from other sources (a symbol missing) or not
+            # loadable: the package still imports, so that it can be rebuilt,
+            # and the first call raises the same error again.
+            pass
 
 
 def ptr(tensor) -> int | None:

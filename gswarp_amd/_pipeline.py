@@ -370,6 +370,7 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
         result = (ctypes.c_int64 * 6)()
         events = _stage_chain(("duplicate", "sort", "ranges", "sort") + (("render",) if images is not None else ()))
         img = images
+        order = None if img is None else tile_order_buffer(image_width, image_height, device)
         lib.call("gs_readback_bin_packed", info.data_ptr(), slot.address, slot.next_seq(), P, pre.radii.data_ptr(),
                  pre.records.data_ptr(), pre.conic_2d_inv.data_ptr(), _lib.ptr(pre.coverage), _depths_or_none(pre),
                  offsets.data_ptr(), image_width, image_height, pre.coverage_mode, DEPTH_TILE_MIN_PAIRS_PER_GAUSSIAN if mode == "warp_depth_stable_tile" else 0,
@@ -377,7 +378,8 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
                  None if img is None else img.background.data_ptr(), int(img is not None and img.compute_depth),
                  None if img is None else img.color.data_ptr(), None if img is None else img.depth.data_ptr(),
                  None if img is None else img.alpha.data_ptr(), None if img is None else img.n_contrib.data_ptr(),
-                 _lib.ptr(grad_clear), 0 if grad_clear is None else grad_clear.numel(), events, result, stream)
+                 _lib.ptr(grad_clear), 0 if grad_clear is None else grad_clear.numel(), events, result,
+                 _lib.ptr(order), stream)
         R = validate_pair_count(int(result[0]))
         _workspace.note_pairs(device, R)
         _note("num_rendered", R)
@@ -385,7 +387,8 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
             _note("binning_dataflow", "packed_key")
             _note("sort_passes", int(lib.gs_sort_num_passes((T - 1).bit_length())))
             layout = KeyLayout(depth_min=int(result[1]), depth_bits=int(result[2]), value_bits=int(result[3]))
-            return BinningState(grid_x, grid_y, point_list[:R], ranges, R, None, layout, rendered=bool(result[5]))
+            return BinningState(grid_x, grid_y, point_list[:R], ranges, R, None, layout, rendered=bool(result[5]),
+                                tile_order=order if result[5] else None)
         depth_range = slot[1] & 0xFFFFFFFFFFFFFFFF
         # declined: release the provisioned buffers before the exact-size binning allocates its own
         del ws, result, events
@@ -429,6 +432,15 @@ def binning(pre: PreprocessOutputs, image_height: int, image_width: int, options
             bins.point_list = point_list
         bins.buffer = buffer
     return bins
+
+
+def tile_order_buffer(image_width: int, image_height: int, device) -> torch.Tensor:
+    """Buffer for the blend kernels' tile order (gs_tile_order, one int32 per
+    16 x 16 tile): the forward render orders the tiles into it, longest list
+    first, when that pays (R <= 4 N, R >= 192 T), and the backward, given the
+    same buffer (BinningState.tile_order), takes the tiles in that order."""
+    num_tiles = ((image_width + 15) // 16) * ((image_height + 15) // 16)
+    return torch.empty((max(num_tiles, 1),), dtype=torch.int32, device=device)
 
 
 def _note(key: str, value) -> None:
@@ -635,6 +647,8 @@ def render(pre: PreprocessOutputs, bins: BinningState, background: torch.Tensor,
         return RenderStageResult(color, depth, alpha, n_contrib, aux)
     compute_depth = int(bool(options.compute_depth))
     stream = _stream(device)
+    if bins.tile_order is None:
+        bins.tile_order = tile_order_buffer(W, H, device)
     if flow:
         if write_aux:
             aux = (torch.empty((k, H, W), dtype=torch.int32, device=device), torch.empty((k, H, W), **f),
@@ -646,13 +660,14 @@ def render(pre: PreprocessOutputs, bins: BinningState, background: torch.Tensor,
                      bins.point_list.data_ptr(), pre.records.data_ptr(), bg.data_ptr(), compute_depth,
                      int(write_aux), k, color.data_ptr(), depth.data_ptr(), alpha.data_ptr(), n_contrib.data_ptr(),
                      aux[0].data_ptr() if write_aux else None, aux[1].data_ptr() if write_aux else None,
-                     aux[2].data_ptr() if write_aux else None, stream)
+                     aux[2].data_ptr() if write_aux else None, bins.tile_order.data_ptr(), stream)
     else:
         with _stage("render"):
             lib.call("gs_render_fwd_clear", W, H, P, bins.num_rendered, bins.ranges.data_ptr(),
                      bins.point_list.data_ptr(), pre.records.data_ptr(), bg.data_ptr(), compute_depth,
                      color.data_ptr(), depth.data_ptr(), alpha.data_ptr(), n_contrib.data_ptr(),
-                     _lib.ptr(grad_clear), 0 if grad_clear is None else grad_clear.numel(), stream)
+                     _lib.ptr(grad_clear), 0 if grad_clear is None else grad_clear.numel(),
+                     bins.tile_order.data_ptr(), stream)
     return RenderStageResult(color, depth, alpha, n_contrib, aux)
 
 
@@ -747,7 +762,8 @@ def backward(inputs: RasterInputs, radii: torch.Tensor, alpha: torch.Tensor, gra
                 lib.call("gs_render_bwd", W, H, P, bins.num_rendered, bins.ranges.data_ptr(),
                          bins.point_list.data_ptr(), pre.records.data_ptr(), bg.data_ptr(), alpha_c.data_ptr(),
                          n_contrib.data_ptr(), _lib.ptr(gc), _lib.ptr(gd), _lib.ptr(ga),
-                         int(bool(options.compute_depth)), grad_gauss.data_ptr(), stream)
+                         int(bool(options.compute_depth)), grad_gauss.data_ptr(), _lib.ptr(bins.tile_order),
+                         stream)
         has_sh = inputs.sh.numel() != 0
         shs = _f32c(inputs.sh).reshape(P, -1, NUM_CHANNELS) if has_sh else None
         K = shs.shape[1] if has_sh else 0

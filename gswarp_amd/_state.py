@@ -68,6 +68,7 @@ class BinningState:
     key_layout: KeyLayout = field(default_factory=KeyLayout)
     buffer: torch.Tensor | None = None  # raw-ABI (R + 2T) int32 buffer that point_list and ranges are views of
     rendered: bool = False  # the standard forward render was launched with the binning (RenderImages)
+    tile_order: torch.Tensor | None = None  # (T,) int32 buffer the forward render was given (gs_tile_order)
 
     def decode_keys(self) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         """(tile id, depth float bits, sort field = tile and depth fields as one

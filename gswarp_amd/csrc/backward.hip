@@ -234,6 +234,7 @@ struct RenderBwdParams {
   int compute_depth;
   int long_tile;  // list length above which a tile is walked by four one-pixel-per-lane slices
   float* grad_gauss;
+  const int* tile_order;  // the tiles in the order the workgroups take them (gs_tile_order), null: tile order
 };
 
 // One wave walks a slice of kPix blocks of 8x8 pixels, kCols blocks wide:
@@ -632,7 +633,10 @@ __device__ __forceinline__ void render_bwd_tiles(const RenderBwdParams& p) {
   const bool extra = (int)blockIdx.x >= seg;
   const int unit = extra ? xcd_unit(blockIdx.x - seg, extra_units) : xcd_unit(blockIdx.x, first_units);
   if (unit >= (extra ? extra_units : first_units)) return;  // segment padding
-  const int tile = extra ? unit / (4 - kFirst) : unit / kFirst;
+  const int slot = extra ? unit / (4 - kFirst) : unit / kFirst;
+  // (clamped: a buffer the forward did not write cannot send a workgroup
+  // outside the ranges)
+  const int tile = p.tile_order ? imax(0, imin(p.tile_order[slot], p.num_tiles - 1)) : slot;
   const int quadrant = extra ? kFirst + unit % (4 - kFirst) : unit % kFirst;
   int2 rg = p.ranges[tile];
   rg.x = imax(0, imin(rg.x, p.num_rendered));
@@ -1107,7 +1111,7 @@ extern "C" int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t 
                              const int32_t* point_list, const float* records, const float* background,
                              const float* out_alpha, const int32_t* n_contrib, const float* grad_color,
                              const float* grad_depth, const float* grad_alpha, int32_t compute_depth,
-                             float* grad_gauss, void* stream) {
+                             float* grad_gauss, const int32_t* tile_order, void* stream) {
   if (image_width <= 0 || image_height <= 0 || (long long)image_width * image_height > 0x7fffffffLL)
     return GS_ERR_INVALID_ARGUMENT;
   if (num_points <= 0 || num_rendered < 0) return GS_ERR_INVALID_ARGUMENT;
@@ -1138,8 +1142,10 @@ extern "C" int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t 
   p.long_tile = long_tile > 0x7fffffffLL ? 0x7fffffff : (int)long_tile;
   const bool whole = num_rendered > gs::kWholeTilePairsPerPoint * (int64_t)num_points;
   const int first = whole ? 1 : 2;
-  const dim3 grid(gs::xcd_grid(first * p.num_tiles) + gs::xcd_grid((4 - first) * p.num_tiles));
   const hipStream_t s = (hipStream_t)stream;
+  // Longest lists first, in the order the forward wrote (tile_order_pays).
+  p.tile_order = tile_order && gs::tile_order_pays(num_rendered, num_points, p.num_tiles) ? tile_order : nullptr;
+  const dim3 grid(gs::xcd_grid(first * p.num_tiles) + gs::xcd_grid((4 - first) * p.num_tiles));
   if (compute_depth) {
     if (whole)
       hipLaunchKernelGGL((gs::render_bwd_whole_kernel<true>), grid, dim3(64), 0, s, p);

@@ -1153,7 +1153,7 @@ __global__ __launch_bounds__(64) void publish_info_kernel(const int64_t* info, i
 
 }  // namespace gs
 
-extern "C" int gs_version(void) { return 10100; }
+extern "C" int gs_version(void) { return 10200; }
 
 extern "C" const char* gs_status_string(int status) {
   switch (status) {
@@ -1689,7 +1689,7 @@ extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* slot, in
                                       const float* background, int32_t compute_depth, float* out_color,
                                       float* out_depth, float* out_alpha, int32_t* n_contrib, float* grad_clear,
                                       int64_t grad_clear_floats, void* const* stage_events, int64_t* result,
-                                      void* stream) {
+                                      int32_t* tile_order, void* stream) {
   if (!info_dev || !slot || !result || P < 0 || capacity < 0 || image_width <= 0 || image_height <= 0)
     return GS_ERR_INVALID_ARGUMENT;
   // The ranges are cleared while the host waits for the count: the clearing
@@ -1754,7 +1754,7 @@ extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* slot, in
   if (out_color) {
     st = gs_render_fwd_clear(image_width, image_height, P, R, ranges, point_list, records, background,
                              compute_depth, out_color, out_depth, out_alpha, n_contrib, grad_clear,
-                             grad_clear_floats, stream);
+                             grad_clear_floats, tile_order, stream);
     if (st != GS_OK) return st;
     if (stage_events) (void)hipEventRecord((hipEvent_t)stage_events[5], (hipStream_t)stream);
     result[5] = 1;

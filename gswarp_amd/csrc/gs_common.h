@@ -422,6 +422,20 @@ __device__ __forceinline__ int xcd_unit(int b, int num_units) {
   return ((u / kXcdChunk) * 8 + (b & 7)) * kXcdChunk + u % kXcdChunk;
 }
 
+// The blend kernels take the tiles longest list first (gs_tile_order) when
+// the lists hold at most 4 pairs per Gaussian (the backward's halves; the
+// heavier lists of its whole-tile walk measured faster in the XCD tile
+// order, whose neighbouring tiles share the large Gaussians' records in L2)
+// and at least 192 pairs per tile on average: below that the walks are
+// short and the order's own launch (about 5 us) costs more than the tail it
+// removes (100k Gaussians at 800x800, 95 pairs a tile: 8 us slower).  A
+// forward given an order buffer writes the order into it under this
+// condition; the backward, given the same buffer, reads it under the same
+// condition of the same arguments.
+inline bool tile_order_pays(int64_t num_rendered, int64_t num_points, int64_t num_tiles) {
+  return num_rendered > 0 && num_rendered <= 4 * num_points && num_rendered >= 192 * num_tiles;
+}
+
 __device__ __forceinline__ float lane_f(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }

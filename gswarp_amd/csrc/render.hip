@@ -57,6 +57,9 @@ struct RenderFwdParams {
   int* gs_per_pixel;
   float* weight;
   float* x_mu;
+  // optional: the tiles in the order the workgroups take them (gs_tile_order),
+  // null: in tile order
+  const int* tile_order;
   // optional: clear_floats floats at clear (16-byte aligned) set to 0 by the
   // grid on the way, the backward's gradient accumulator
   float* clear;
@@ -124,7 +127,7 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
     clear_share(p, lane);
     return;
   }
-  const int2 ts = make_int2(unit / kSubs, unit % kSubs);
+  const int2 ts = make_int2(p.tile_order ? p.tile_order[unit / kSubs] : unit / kSubs, unit % kSubs);
   const int tile = ts.x;
   const int tx = tile % p.grid_x;
   const int ty = tile / p.grid_x;
@@ -340,6 +343,44 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
   clear_share(p, lane);
 }
 
+// The order in which the blend kernels take the tiles: longest list first,
+// by a counting sort over 256 classes of the list length (4 pairs wide
+// below 512, 64 wide above, the last class open; one workgroup).  The
+// longest walks then start first and the end of the grid is made of short
+// ones: in tile order the long lists at the image's centre start half way
+// through the grid and the last of them finish well after the rest.
+// Ordering groups of 4 x 4 tiles instead, to keep neighbours (which share
+// Gaussians) together in one XCD's L2, measured slower at configs 2 and 4.
+__device__ __forceinline__ int tile_length_class(int2 r) {
+  const int len = imax(0, r.y - r.x);
+  const int c = len < 512 ? len >> 2 : 128 + imin(127, (len - 512) >> 6);
+  return 255 - c;  // longest first
+}
+
+__global__ __launch_bounds__(1024) void tile_order_kernel(int T, const int2* __restrict__ ranges,
+                                                         int* __restrict__ order) {
+  __shared__ __align__(16) int s_count[256];
+  const int t0 = threadIdx.x;
+  if (t0 < 256) s_count[t0] = 0;
+  __syncthreads();
+  for (int t = t0; t < T; t += 1024) atomicAdd(&s_count[tile_length_class(ranges[t])], 1);
+  __syncthreads();
+  if (t0 < 64) {  // exclusive prefix over the 256 classes, four per lane
+    const int4 c = reinterpret_cast<const int4*>(s_count)[t0];
+    const int sum = c.x + c.y + c.z + c.w;
+    int incl = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(incl, off, 64);
+      if (t0 >= off) incl += o;
+    }
+    const int e = incl - sum;
+    reinterpret_cast<int4*>(s_count)[t0] = make_int4(e, e + c.x, e + c.x + c.y, e + c.x + c.y + c.z);
+  }
+  __syncthreads();
+  for (int t = t0; t < T; t += 1024) order[atomicAdd(&s_count[tile_length_class(ranges[t])], 1)] = t;
+}
+
 static int launch_render_fwd(const RenderFwdParams& p, bool flow, hipStream_t s) {
   const dim3 grid(gs::xcd_grid(p.num_tiles * (4 / kFwdPix)));
   if (flow && p.write_aux && p.top_k <= kMaxStagedTopK) {
@@ -369,7 +410,7 @@ static int gs_render_fwd_common(int32_t W, int32_t H, int32_t num_points, int64_
                                 const float* background, int32_t compute_depth, int32_t write_aux, int32_t top_k,
                                 float* out_color, float* out_depth, float* out_alpha, int32_t* n_contrib,
                                 int32_t* gs_per_pixel, float* weight, float* x_mu, bool flow, void* stream,
-                                float* clear = nullptr, int64_t clear_floats = 0) {
+                                int32_t* tile_order, float* clear = nullptr, int64_t clear_floats = 0) {
   if (W <= 0 || H <= 0 || (long long)W * H > 0x7fffffffLL) return GS_ERR_INVALID_ARGUMENT;
   if (clear_floats < 0 || (clear_floats > 0 && !clear)) return GS_ERR_INVALID_ARGUMENT;
   if (reinterpret_cast<uintptr_t>(clear) & 15) return GS_ERR_MISALIGNED;
@@ -402,26 +443,40 @@ static int gs_render_fwd_common(int32_t W, int32_t H, int32_t num_points, int64_
   p.x_mu = x_mu;
   p.clear = clear_floats > 0 ? clear : nullptr;
   p.clear_floats = clear_floats;
+  p.tile_order = nullptr;
+  if (tile_order && gs::tile_order_pays(num_rendered, num_points, p.num_tiles)) {
+    const int st = gs_tile_order(p.num_tiles, ranges, tile_order, stream);
+    if (st != GS_OK) return st;
+    p.tile_order = tile_order;
+  }
   return gs::launch_render_fwd(p, flow, (hipStream_t)stream);
+}
+
+extern "C" int gs_tile_order(int32_t num_tiles, const int32_t* ranges, int32_t* order, void* stream) {
+  if (num_tiles < 0 || (num_tiles > 0 && (!ranges || !order))) return GS_ERR_INVALID_ARGUMENT;
+  if (num_tiles == 0) return GS_OK;
+  hipLaunchKernelGGL(gs::tile_order_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, num_tiles,
+                     reinterpret_cast<const int2*>(ranges), order);
+  return gs_status_from_hip(hipGetLastError());
 }
 
 extern "C" int gs_render_fwd(int32_t image_width, int32_t image_height, int32_t num_points, int64_t num_rendered,
                              const int32_t* ranges, const int32_t* point_list, const float* records,
                              const float* background, int32_t compute_depth, float* out_color, float* out_depth,
-                             float* out_alpha, int32_t* n_contrib, void* stream) {
+                             float* out_alpha, int32_t* n_contrib, int32_t* tile_order, void* stream) {
   return gs_render_fwd_common(image_width, image_height, num_points, num_rendered, ranges, point_list, records,
                               background, compute_depth, 0, 0, out_color, out_depth, out_alpha, n_contrib, nullptr,
-                              nullptr, nullptr, false, stream);
+                              nullptr, nullptr, false, stream, tile_order);
 }
 
 extern "C" int gs_render_fwd_clear(int32_t image_width, int32_t image_height, int32_t num_points,
                                    int64_t num_rendered, const int32_t* ranges, const int32_t* point_list,
                                    const float* records, const float* background, int32_t compute_depth,
                                    float* out_color, float* out_depth, float* out_alpha, int32_t* n_contrib,
-                                   float* clear, int64_t clear_floats, void* stream) {
+                                   float* clear, int64_t clear_floats, int32_t* tile_order, void* stream) {
   return gs_render_fwd_common(image_width, image_height, num_points, num_rendered, ranges, point_list, records,
                               background, compute_depth, 0, 0, out_color, out_depth, out_alpha, n_contrib, nullptr,
-                              nullptr, nullptr, false, stream, clear, clear_floats);
+                              nullptr, nullptr, false, stream, tile_order, clear, clear_floats);
 }
 
 extern "C" int gs_render_fwd_flow(int32_t image_width, int32_t image_height, int32_t num_points,
@@ -429,8 +484,8 @@ extern "C" int gs_render_fwd_flow(int32_t image_width, int32_t image_height, int
                                   const float* records, const float* background, int32_t compute_depth,
                                   int32_t write_aux, int32_t top_k, float* out_color, float* out_depth,
                                   float* out_alpha, int32_t* n_contrib, int32_t* gs_per_pixel,
-                                  float* weight_per_gs_pixel, float* x_mu, void* stream) {
+                                  float* weight_per_gs_pixel, float* x_mu, int32_t* tile_order, void* stream) {
   return gs_render_fwd_common(image_width, image_height, num_points, num_rendered, ranges, point_list, records,
                               background, compute_depth, write_aux, top_k, out_color, out_depth, out_alpha,
-                              n_contrib, gs_per_pixel, weight_per_gs_pixel, x_mu, true, stream);
+                              n_contrib, gs_per_pixel, weight_per_gs_pixel, x_mu, true, stream, tile_order);
 }

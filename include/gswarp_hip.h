@@ -11,7 +11,7 @@
  * different streams with disjoint buffers may run concurrently.  One entry
  * point is the exception, by design: gs_scan_tiles_static keeps its scratch
  * in a fixed device array of the library (one per GPU), so calls that
- * overlap on one GPU race on it.  ABI version (gs_version): 10100.
+ * overlap on one GPU race on it.  ABI version (gs_version): 10200.
  *
  * Each function replaces one stage of the reference host pipeline
  * (fancifulland2718/gswarp 1.1.0, Warp backend); the stage it replaces is
@@ -380,7 +380,7 @@ int gs_bin_packed(int32_t P, const int32_t* radii, const float* records, const f
  * out_depth, out_alpha and n_contrib (background, compute_depth as there)
  * and result (6 int64) ends with 1 if it was launched; that render zeroes
  * grad_clear as gs_render_fwd_clear does (grad_clear_floats 0: nothing),
- * and only when it is launched.  stage_events, if not
+ * and only when it is launched; tile_order is gs_render_fwd's.  stage_events, if not
  * NULL, holds the five events of gs_bin_packed and a sixth recorded after
  * the render.  The keys are emitted into the start of workspace before the
  * count is read back (the kernel reads the layout and the count from
@@ -398,7 +398,7 @@ int gs_readback_bin_packed(const int64_t* info_dev, int64_t* slot, int64_t seq, 
                            int32_t* ranges, int32_t* point_list, const float* background, int32_t compute_depth,
                            float* out_color, float* out_depth, float* out_alpha, int32_t* n_contrib,
                            float* grad_clear, int64_t grad_clear_floats, void* const* stage_events,
-                           int64_t* result, void* stream);
+                           int64_t* result, int32_t* tile_order, void* stream);
 
 /*
  * Bucketed binning, for many tiles per Gaussian: the per-tile lists in
@@ -433,19 +433,34 @@ int gs_bin_buckets(int32_t P, int32_t num_valid, int64_t num_entries, int64_t nu
                    void* stream);
 
 /*
+ * The tiles ordered by their list length (ranges (T, 2)), longest first,
+ * into order (num_tiles int32): the order in which the blend kernels take
+ * the tiles when given an order buffer, so that the longest walks start
+ * first and the end of the grid is made of short ones.  One workgroup.
+ * No counterpart in the reference (its kernels take the tiles in tile
+ * order); it changes no result, only the schedule.
+ */
+int gs_tile_order(int32_t num_tiles, const int32_t* ranges, int32_t* order, void* stream);
+
+/*
  * Per-tile front-to-back alpha blending of 16x16 tiles, each covered by
  * independent wave64 workgroups that own a slice of its rows.
  * num_points (N) and num_rendered (R) bound every index read from ranges and
  * point_list.
  * Writes color + T*bg, alpha = sum of weights, depth (zero unless
  * compute_depth) and n_contrib (1-based index of the last blended Gaussian).
+ * tile_order (optional, T int32 of caller memory): when given, R <= 4 N
+ * and R >= 192 T, the call first orders the tiles into it (gs_tile_order)
+ * and its workgroups take them longest list first; otherwise they take them
+ * in tile order and the buffer is not written.  Keep it for gs_render_bwd.
+ * The results do not depend on it.
  * Replaces: render_ops.py:16-93 with render_kernels.py:16-147.
  */
 int gs_render_fwd(int32_t image_width, int32_t image_height, int32_t num_points, int64_t num_rendered,
                   const int32_t* ranges,
                   const int32_t* point_list, const float* records, const float* background,
                   int32_t compute_depth, float* out_color, float* out_depth, float* out_alpha,
-                  int32_t* n_contrib, void* stream);
+                  int32_t* n_contrib, int32_t* tile_order, void* stream);
 
 /*
  * gs_render_fwd that also sets clear_floats floats at clear (16-byte
@@ -460,7 +475,8 @@ int gs_render_fwd(int32_t image_width, int32_t image_height, int32_t num_points,
 int gs_render_fwd_clear(int32_t image_width, int32_t image_height, int32_t num_points, int64_t num_rendered,
                         const int32_t* ranges, const int32_t* point_list, const float* records,
                         const float* background, int32_t compute_depth, float* out_color, float* out_depth,
-                        float* out_alpha, int32_t* n_contrib, float* clear, int64_t clear_floats, void* stream);
+                        float* out_alpha, int32_t* n_contrib, float* clear, int64_t clear_floats,
+                        int32_t* tile_order, void* stream);
 
 /*
  * gs_render_fwd plus the flow auxiliaries of the first top_k blended
@@ -475,13 +491,17 @@ int gs_render_fwd_flow(int32_t image_width, int32_t image_height, int32_t num_po
                        const int32_t* point_list, const float* records, const float* background,
                        int32_t compute_depth, int32_t write_aux, int32_t top_k, float* out_color,
                        float* out_depth, float* out_alpha, int32_t* n_contrib, int32_t* gs_per_pixel,
-                       float* weight_per_gs_pixel, float* x_mu, void* stream);
+                       float* weight_per_gs_pixel, float* x_mu, int32_t* tile_order, void* stream);
 
 /*
  * Reverse blend: accumulates per-Gaussian pixel moments of the loss
  * gradient (the grad_gauss layout above) into grad_gauss (N,10), which the
  * caller zero-initialises.  grad_color, grad_depth and grad_alpha may each
- * be NULL: an absent upstream gradient is zero.
+ * be NULL: an absent upstream gradient is zero.  tile_order: the buffer
+ * that the forward call over the same ranges (gs_render_fwd, _clear, _flow
+ * or gs_readback_bin_packed) was given, or NULL; under the forward's
+ * condition (R <= 4 N, R >= 192 T) the workgroups take the tiles in the
+ * order the forward wrote into it, otherwise in tile order.
  * Replaces: backward_ops.py:183-290 with backward_kernels.py:539-707.
  */
 int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t num_points, int64_t num_rendered,
@@ -489,7 +509,7 @@ int gs_render_bwd(int32_t image_width, int32_t image_height, int32_t num_points,
                   const int32_t* point_list, const float* records, const float* background,
                   const float* out_alpha, const int32_t* n_contrib, const float* grad_color,
                   const float* grad_depth, const float* grad_alpha, int32_t compute_depth,
-                  float* grad_gauss, void* stream);
+                  float* grad_gauss, const int32_t* tile_order, void* stream);
 
 /*
  * Fused per-Gaussian backward: SH colour backward (when shs != NULL), the

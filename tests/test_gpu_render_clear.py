@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import ctypes
 
+import numpy as np
 import pytest
 import torch
 
@@ -38,8 +39,8 @@ def _render(lib, scene, out, images, clear=None, count=0):
     args = (W, H, pre.radii.shape[0], bins.num_rendered, bins.ranges.data_ptr(), bins.point_list.data_ptr(),
             pre.records.data_ptr(), scene["bg"].data_ptr(), 1) + tuple(t.data_ptr() for t in images)
     if clear is None and count == 0:
-        return lib.gs_render_fwd(*args, stream)
-    return lib.gs_render_fwd_clear(*args, clear, count, stream)
+        return lib.gs_render_fwd(*args, None, stream)
+    return lib.gs_render_fwd_clear(*args, clear, count, None, stream)
 
 
 @pytest.mark.parametrize("count_of", ["p10", "p10_minus_1", "three", "large_plus_5"])
@@ -71,7 +72,7 @@ def test_clear_argument_checks(device):
     assert _render(lib, scene, out, images, buf.data_ptr() + 4, 8) != 0  # not 16-byte aligned
     assert _render(lib, scene, out, images, buf.data_ptr(), -1) != 0
     assert lib.gs_render_fwd_clear(64, 64, 1, 1, None, None, None, None, 1, None, None, None, None, None, 8,
-                                   None) != 0
+                                   None, None) != 0
     torch.cuda.synchronize()
 
 
@@ -134,3 +135,77 @@ def test_accumulator_allocated_in_backward(device):
         scale = float(a.abs().max()) + 1e-30
         err = float((a - b).abs().max())
         assert err <= 1e-4 * scale, (i, err, scale)
+
+
+def _check_order(o, ranges):
+    T = ranges.shape[0]
+    assert np.array_equal(np.sort(o), np.arange(T))
+    r = ranges.cpu().numpy()
+    length = np.maximum(r[:, 1] - r[:, 0], 0)[o]
+    cls = np.where(length < 512, length >> 2, 128 + np.minimum(127, (length - 512) >> 6))
+    assert np.all(np.diff(cls) <= 0)
+
+
+def test_tile_order_is_longest_first_permutation(device):
+    """gs_tile_order: a permutation of the tiles whose list lengths never
+    rise by more than the width of its length classes (4 pairs below 512,
+    64 above) along the order; the forward render is bit-identical with and
+    without it (the order changes only the schedule)."""
+    lib = _lib.load()
+    scene = configs.make_scene(2, count=150_000, width=480, height=270, device=device)
+    out = gpu_forward(scene, options())
+    bins = out["bins"]
+    T = bins.ranges.shape[0]
+    order = torch.full((T + GUARD,), -7, dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    assert lib.gs_tile_order(T, bins.ranges.data_ptr(), order.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    o = order.cpu().numpy()
+    assert np.all(o[T:] == -7), "written past num_tiles"
+    _check_order(o[:T], bins.ranges)
+    a, b = _images(scene["height"], scene["width"], device), _images(scene["height"], scene["width"], device)
+    assert _render(lib, scene, out, a) == 0
+    args = (scene["width"], scene["height"], out["pre"].radii.shape[0], bins.num_rendered, bins.ranges.data_ptr(),
+            bins.point_list.data_ptr(), out["pre"].records.data_ptr(), scene["bg"].data_ptr(), 1)
+    P = out["pre"].radii.shape[0]
+    assert 192 * T <= bins.num_rendered <= 4 * P, "the order is used at this R"
+    order.fill_(-7)
+    assert lib.gs_render_fwd(*args, *(t.data_ptr() for t in b), order.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    _check_order(order.cpu().numpy()[:T], bins.ranges)  # the forward wrote an order (ties in any order)
+    for x, y in zip(a, b):
+        assert torch.equal(x.view(torch.int32), y.view(torch.int32))
+    # The backward over the forward's order: the same gradients up to the
+    # rounding of its float atomics, whose order the schedule changes.
+    g = torch.Generator(device="cpu").manual_seed(3)
+    ups = [torch.randn(shape, generator=g).to(device) for shape in ((3,) + a[0].shape[1:], a[1].shape, a[2].shape)]
+    grads = []
+    for buf in (None, order.data_ptr()):
+        gg = torch.zeros((P, _lib.GS_GRAD_FLOATS), dtype=torch.float32, device=device)
+        assert lib.gs_render_bwd(scene["width"], scene["height"], P, bins.num_rendered, bins.ranges.data_ptr(),
+                                 bins.point_list.data_ptr(), out["pre"].records.data_ptr(), scene["bg"].data_ptr(),
+                                 a[2].data_ptr(), a[3].data_ptr(), *(u.data_ptr() for u in ups), 1, gg.data_ptr(),
+                                 buf, stream) == 0
+        grads.append(gg)
+    torch.cuda.synchronize()
+    scale = float(grads[0].abs().max()) + 1e-30
+    assert float((grads[0] - grads[1]).abs().max()) <= 1e-4 * scale
+
+
+def test_forward_writes_no_order_when_it_does_not_pay(device):
+    """Below 192 pairs a tile the forward leaves the buffer untouched and the
+    backward, given it, takes the tiles in tile order (it never reads it)."""
+    lib = _lib.load()
+    scene = configs.make_scene(1, count=2_000, width=256, height=256, device=device)
+    out = gpu_forward(scene, options())
+    bins = out["bins"]
+    T = bins.ranges.shape[0]
+    assert 0 < bins.num_rendered < 192 * T
+    order = torch.full((T,), -7, dtype=torch.int32, device=device)
+    images = _images(scene["height"], scene["width"], device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    args = (scene["width"], scene["height"], out["pre"].radii.shape[0], bins.num_rendered, bins.ranges.data_ptr(),
+            bins.point_list.data_ptr(), out["pre"].records.data_ptr(), scene["bg"].data_ptr(), 1)
+    assert lib.gs_render_fwd(*args, *(t.data_ptr() for t in images), order.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    assert bool((order == -7).all())

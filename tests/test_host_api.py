@@ -238,7 +238,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     for name in _declared_functions():
         assert hasattr(handle, name), name
     lib = _lib.load()
-    assert lib.gs_version() == 10100
+    assert lib.gs_version() == 10200
     assert lib.gs_readback_slot_bytes() == 256
     assert lib.status_string(0) == "ok"
     for code in (-1, -2, -3, -4):
