@@ -702,28 +702,20 @@ __device__ __forceinline__ float dot3(V3 a, float b0, float b1, float b2) { retu
 
 // SH colour backward for one Gaussian: writes its K x 3 block of grad_sh and
 // returns dL/dmean through the direction normalisation.  With kVec16 the
-// block is K = 16 coefficients (48 floats, 16-byte aligned): it is read and
-// written as 12 float4 through registers, 4x fewer memory instructions than
-// per-float accesses, whose lanes would touch one cache line each.
+// block is K = 16 coefficients (48 floats) and sh_mem / gsh_mem are the
+// caller's 48-float register arrays (the kernel moves them between HBM and
+// registers through LDS); otherwise they point at the Gaussian's blocks in
+// global memory.
 template <bool kVec16>
 __device__ __forceinline__ V3 sh_backward(const float* __restrict__ sh_mem, float* __restrict__ gsh_mem, int K,
                                           int degree, float dirx, float diry, float dirz, float g0, float g1,
                                           float g2) {
-  float sh_reg[kVec16 ? 48 : 1], gsh_reg[kVec16 ? 48 : 1];
   if (kVec16) {
 #pragma unroll
-    for (int i = 0; i < 12; ++i) {
-      const float4 v = reinterpret_cast<const float4*>(sh_mem)[i];
-      sh_reg[4 * i + 0] = v.x;
-      sh_reg[4 * i + 1] = v.y;
-      sh_reg[4 * i + 2] = v.z;
-      sh_reg[4 * i + 3] = v.w;
-    }
-#pragma unroll
-    for (int i = 0; i < 48; ++i) gsh_reg[i] = 0.0f;
+    for (int i = 0; i < 48; ++i) gsh_mem[i] = 0.0f;
   }
-  const float* sh = kVec16 ? sh_reg : sh_mem;
-  float* gsh = kVec16 ? gsh_reg : gsh_mem;
+  const float* sh = sh_mem;
+  float* gsh = gsh_mem;
   const float len_sq = dirx * dirx + diry * diry + dirz * dirz;
   const float inv_len = 1.0f / sqrtf(fmaxr(len_sq, 1.0e-20f));
   const float x = dirx * inv_len, y = diry * inv_len, z = dirz * inv_len;
@@ -812,12 +804,7 @@ __device__ __forceinline__ V3 sh_backward(const float* __restrict__ sh_mem, floa
       }
     }
   }
-  if (kVec16) {
-#pragma unroll
-    for (int i = 0; i < 12; ++i)
-      reinterpret_cast<float4*>(gsh_mem)[i] =
-          make_float4(gsh_reg[4 * i + 0], gsh_reg[4 * i + 1], gsh_reg[4 * i + 2], gsh_reg[4 * i + 3]);
-  } else {
+  if (!kVec16) {
     for (int k = written; k < K; ++k) {
       gsh[3 * k + 0] = 0.0f;
       gsh[3 * k + 1] = 0.0f;
@@ -837,9 +824,200 @@ __device__ __forceinline__ V3 sh_backward(const float* __restrict__ sh_mem, floa
   return r;
 }
 
-__global__ __launch_bounds__(256) void preprocess_bwd_kernel(PreprocessBwdParams p) {
-  const int tid = blockIdx.x * blockDim.x + threadIdx.x;
-  if (tid >= p.P) return;
+// The float4 SH path (K = 16) moves each wave's coefficient and gradient
+// blocks (64 Gaussians x 192 bytes, contiguous) between HBM and LDS with
+// whole-wave accesses (64 consecutive float4, 1 KB, per instruction), and each
+// lane works on its Gaussian's row in LDS: a lane's own 12 float4 at a
+// 192-byte stride make every memory instruction touch 64 cache lines (the
+// address unit was then busy for 80% of the kernel).  The coefficients are
+// requested at the kernel's start, so their loads overlap the rest of the
+// Gaussian backward; rows are 13 float4 apart, so that the lanes' row
+// accesses fall in distinct LDS banks.  The staging is wave-wide, so every
+// lane of the grid runs the Gaussian backward (lanes past P on Gaussian
+// P - 1, storing nothing).  The 13 KB per wave hold the kernel to three
+// waves per SIMD; staging 96 bytes per Gaussian at a time (four waves per
+// SIMD) measured slower, its second half's loads waiting on the first's use.
+constexpr int kShRow = 13;
+
+struct ShStage {
+  float4* rows;  // the wave's 64 rows of kShRow float4 in LDS
+  int lane, w0, nvalid;  // w0: the wave's first Gaussian; nvalid: its Gaussians below P
+};
+
+// The wave's coefficient blocks into its LDS rows.
+__device__ __forceinline__ void sh_stage_in(const ShStage& st, const float* shs) {
+  const float4* src = reinterpret_cast<const float4*>(shs) + (size_t)st.w0 * 12;
+#pragma unroll
+  for (int j = 0; j < 12; ++j) {
+    const int f = j * 64 + st.lane, g = f / 12;
+    if (g < st.nvalid) st.rows[g * kShRow + (f - g * 12)] = src[f];
+  }
+  __builtin_amdgcn_wave_barrier();  // the lanes' row reads follow these writes (LDS order)
+}
+
+// The wave's gradient blocks from its LDS rows to grad_sh (after every
+// lane's rows are written: the wave's LDS accesses complete in order).
+__device__ __forceinline__ void sh_stage_out(const ShStage& st, float* grad_sh) {
+  __builtin_amdgcn_wave_barrier();
+  float4* dst = reinterpret_cast<float4*>(grad_sh) + (size_t)st.w0 * 12;
+#pragma unroll
+  for (int j = 0; j < 12; ++j) {
+    const int f = j * 64 + st.lane, g = f / 12;
+    if (g < st.nvalid) dst[f] = st.rows[g * kShRow + (f - g * 12)];
+  }
+}
+
+// Half h of a row (floats 24 h .. 24 h + 23 of the Gaussian's block).
+__device__ __forceinline__ void row_half_in(const float4* row, int h, float (&v)[24]) {
+#pragma unroll
+  for (int k = 0; k < 6; ++k) {
+    const float4 q = row[6 * h + k];
+    v[4 * k + 0] = q.x;
+    v[4 * k + 1] = q.y;
+    v[4 * k + 2] = q.z;
+    v[4 * k + 3] = q.w;
+  }
+}
+
+__device__ __forceinline__ void row_half_out(float4* row, int h, const float (&v)[24]) {
+#pragma unroll
+  for (int k = 0; k < 6; ++k) row[6 * h + k] = make_float4(v[4 * k + 0], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+}
+
+// sh_backward for K = 16 on the Gaussian's LDS row: its coefficients are
+// read and replaced by their gradients half by half (24 live at a time).
+// The direction gradient sums are accumulated coefficient by coefficient in
+// ascending order, which is the association order of sh_backward's
+// expressions, so the results are the same bit for bit.  `active` (a kept
+// Gaussian below P) selects the lanes whose gradients are computed (the
+// others write zeros).
+__device__ __forceinline__ V3 sh_backward_row(float4* row, int degree, bool active, float dirx, float diry,
+                                              float dirz, float g0, float g1, float g2) {
+  const float len_sq = dirx * dirx + diry * diry + dirz * dirz;
+  const float inv_len = 1.0f / sqrtf(fmaxr(len_sq, 1.0e-20f));
+  const float x = dirx * inv_len, y = diry * inv_len, z = dirz * inv_len;
+  const float xx = x * x, yy = y * y, zz = z * z;
+  const float xy = x * y, yz = y * z, xz = x * z;
+  const bool d1 = active && degree > 0, d2 = d1 && degree > 1, d3 = d2 && degree > 2;
+  V3 dx = {0.0f, 0.0f, 0.0f}, dy = {0.0f, 0.0f, 0.0f}, dz = {0.0f, 0.0f, 0.0f};
+  float v[24];
+  // coefficients 0-7
+  row_half_in(row, 0, v);
+#define GS_C(k, c) v[3 * (k) + (c)]
+  if (d1) {
+    dx = {-kShC1 * GS_C(3, 0), -kShC1 * GS_C(3, 1), -kShC1 * GS_C(3, 2)};
+    dy = {-kShC1 * GS_C(1, 0), -kShC1 * GS_C(1, 1), -kShC1 * GS_C(1, 2)};
+    dz = {kShC1 * GS_C(2, 0), kShC1 * GS_C(2, 1), kShC1 * GS_C(2, 2)};
+  }
+  const float ex4 = kShC2_0 * y, ex6 = kShC2_2 * (-2.0f * x), ex7 = kShC2_3 * z, ex8 = kShC2_4 * (2.0f * x);
+  const float ey4 = kShC2_0 * x, ey5 = kShC2_1 * z, ey6 = kShC2_2 * (-2.0f * y), ey8 = kShC2_4 * (-2.0f * y);
+  const float ez5 = kShC2_1 * y, ez6 = kShC2_2 * (4.0f * z), ez7 = kShC2_3 * x;
+  if (d2) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      float ax = dx.x, ay = dy.x, az = dz.x;
+      if (c == 1) { ax = dx.y; ay = dy.y; az = dz.y; }
+      if (c == 2) { ax = dx.z; ay = dy.z; az = dz.z; }
+      ax = ax + ex4 * GS_C(4, c);
+      ax = ax + ex6 * GS_C(6, c);
+      ax = ax + ex7 * GS_C(7, c);
+      ay = ay + ey4 * GS_C(4, c);
+      ay = ay + ey5 * GS_C(5, c);
+      ay = ay + ey6 * GS_C(6, c);
+      az = az + ez5 * GS_C(5, c);
+      az = az + ez6 * GS_C(6, c);
+      az = az + ez7 * GS_C(7, c);
+      if (c == 0) { dx.x = ax; dy.x = ay; dz.x = az; }
+      if (c == 1) { dx.y = ax; dy.y = ay; dz.y = az; }
+      if (c == 2) { dx.z = ax; dy.z = ay; dz.z = az; }
+    }
+  }
+  // coefficients 8-15
+  row_half_in(row, 1, v);
+#undef GS_C
+#define GS_C(k, c) v[3 * ((k) - 8) + (c)]
+  if (d2) {
+    dx.x = dx.x + ex8 * GS_C(8, 0); dx.y = dx.y + ex8 * GS_C(8, 1); dx.z = dx.z + ex8 * GS_C(8, 2);
+    dy.x = dy.x + ey8 * GS_C(8, 0); dy.y = dy.y + ey8 * GS_C(8, 1); dy.z = dy.z + ey8 * GS_C(8, 2);
+  }
+  const float ex9 = kShC3_0 * (6.0f * xy), ex10 = kShC3_1 * yz, ex11 = kShC3_2 * (-2.0f * xy);
+  const float ex12 = kShC3_3 * (-6.0f * xz), ex13 = kShC3_4 * (-3.0f * xx + 4.0f * zz - yy);
+  const float ex14 = kShC3_5 * (2.0f * xz), ex15 = kShC3_6 * (3.0f * (xx - yy));
+  const float ey9 = kShC3_0 * (3.0f * (xx - yy)), ey10 = kShC3_1 * xz;
+  const float ey11 = kShC3_2 * (-3.0f * yy + 4.0f * zz - xx), ey12 = kShC3_3 * (-6.0f * yz);
+  const float ey13 = kShC3_4 * (-2.0f * xy), ey14 = kShC3_5 * (-2.0f * yz), ey15 = kShC3_6 * (-6.0f * xy);
+  const float ez10 = kShC3_1 * xy, ez11 = kShC3_2 * (8.0f * yz);
+  const float ez12 = kShC3_3 * (3.0f * (2.0f * zz - xx - yy)), ez13 = kShC3_4 * (8.0f * xz);
+  const float ez14 = kShC3_5 * (xx - yy);
+  if (d3) {
+#define GS_DX(acc, c)                                                                                      \
+  acc = acc + ex9 * GS_C(9, c) + ex10 * GS_C(10, c) + ex11 * GS_C(11, c) + ex12 * GS_C(12, c) +           \
+        ex13 * GS_C(13, c) + ex14 * GS_C(14, c) + ex15 * GS_C(15, c)
+#define GS_DY(acc, c)                                                                                      \
+  acc = acc + ey9 * GS_C(9, c) + ey10 * GS_C(10, c) + ey11 * GS_C(11, c) + ey12 * GS_C(12, c) +           \
+        ey13 * GS_C(13, c) + ey14 * GS_C(14, c) + ey15 * GS_C(15, c)
+#define GS_DZ(acc, c)                                                                                      \
+  acc = acc + ez10 * GS_C(10, c) + ez11 * GS_C(11, c) + ez12 * GS_C(12, c) + ez13 * GS_C(13, c) +         \
+        ez14 * GS_C(14, c)
+    GS_DX(dx.x, 0); GS_DX(dx.y, 1); GS_DX(dx.z, 2);
+    GS_DY(dy.x, 0); GS_DY(dy.y, 1); GS_DY(dy.z, 2);
+    GS_DZ(dz.x, 0); GS_DZ(dz.y, 1); GS_DZ(dz.z, 2);
+#undef GS_DX
+#undef GS_DY
+#undef GS_DZ
+  }
+#undef GS_C
+  // gradients of coefficients 0-7, then 8-15 (zero beyond the degree)
+  {
+    const float w1 = -kShC1 * y, w2 = kShC1 * z, w3 = -kShC1 * x;
+    const float w4 = kShC2_0 * xy, w5 = kShC2_1 * yz, w6 = kShC2_2 * (2.0f * zz - xx - yy);
+    const float w7 = kShC2_3 * xz;
+    const float wk[8] = {kShC0, w1, w2, w3, w4, w5, w6, w7};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const bool on = k == 0 ? active : (k < 4 ? d1 : d2);
+      v[3 * k + 0] = on ? wk[k] * g0 : 0.0f;
+      v[3 * k + 1] = on ? wk[k] * g1 : 0.0f;
+      v[3 * k + 2] = on ? wk[k] * g2 : 0.0f;
+    }
+    row_half_out(row, 0, v);
+  }
+  {
+    const float w8 = kShC2_4 * (xx - yy);
+    const float w9 = kShC3_0 * y * (3.0f * xx - yy);
+    const float w10 = kShC3_1 * xy * z;
+    const float w11 = kShC3_2 * y * (4.0f * zz - xx - yy);
+    const float w12 = kShC3_3 * z * (2.0f * zz - 3.0f * xx - 3.0f * yy);
+    const float w13 = kShC3_4 * x * (4.0f * zz - xx - yy);
+    const float w14 = kShC3_5 * z * (xx - yy);
+    const float w15 = kShC3_6 * x * (xx - 3.0f * yy);
+    const float wk[8] = {w8, w9, w10, w11, w12, w13, w14, w15};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const bool on = k == 0 ? d2 : d3;
+      v[3 * k + 0] = on ? wk[k] * g0 : 0.0f;
+      v[3 * k + 1] = on ? wk[k] * g1 : 0.0f;
+      v[3 * k + 2] = on ? wk[k] * g2 : 0.0f;
+    }
+    row_half_out(row, 1, v);
+  }
+  const float ddir0 = dot3(dx, g0, g1, g2);
+  const float ddir1 = dot3(dy, g0, g1, g2);
+  const float ddir2 = dot3(dz, g0, g1, g2);
+  // d normalize(v) / dv applied to dL/ddir (math_kernels.py:90-97).
+  const float sum2 = dirx * dirx + diry * diry + dirz * dirz;
+  const float invsum32 = 1.0f / sqrtf(fmaxr(sum2 * sum2 * sum2, 1.0e-20f));
+  V3 r;
+  r.x = ((sum2 - dirx * dirx) * ddir0 - diry * dirx * ddir1 - dirz * dirx * ddir2) * invsum32;
+  r.y = (-dirx * diry * ddir0 + (sum2 - diry * diry) * ddir1 - dirz * diry * ddir2) * invsum32;
+  r.z = (-dirx * dirz * ddir0 - diry * dirz * ddir1 + (sum2 - dirz * dirz) * ddir2) * invsum32;
+  return r;
+}
+
+// One Gaussian's backward; `valid`: tid < P (else tid = P - 1 and nothing
+// is stored).
+__device__ __forceinline__ void preprocess_bwd_one(const PreprocessBwdParams& p, int tid, bool valid,
+                                                   const ShStage& stage) {
   const float* __restrict__ V = p.view;
   const float* __restrict__ Pm = p.proj;
   const float mx = p.means3d[3 * tid + 0];
@@ -1026,7 +1204,9 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(PreprocessBwdParams
     if (precomp) {
       // dL/dcov3D is the output (backward_ops.py:734-737); no scale / rotation chain.
       float* gcv = p.grad_cov3d + 6 * (size_t)tid;
-      gcv[0] = gc0; gcv[1] = gc1; gcv[2] = gc2; gcv[3] = gc3; gcv[4] = gc4; gcv[5] = gc5;
+      if (valid) {
+        gcv[0] = gc0; gcv[1] = gc1; gcv[2] = gc2; gcv[3] = gc3; gcv[4] = gc4; gcv[5] = gc5;
+      }
     } else {
       const float sg00 = gc0, sg01 = 0.5f * gc1, sg02 = 0.5f * gc2;
       const float sg11 = gc3, sg12 = 0.5f * gc4, sg22 = gc5;
@@ -1055,7 +1235,8 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(PreprocessBwdParams
     }
   } else if (p.grad_cov3d != nullptr) {
     float* gcv = p.grad_cov3d + 6 * (size_t)tid;
-    for (int k = 0; k < 6; ++k) gcv[k] = 0.0f;
+    if (valid)
+      for (int k = 0; k < 6; ++k) gcv[k] = 0.0f;
   }
 
   // SH colour backward (its colour gradient is identically zero for culled
@@ -1063,25 +1244,30 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(PreprocessBwdParams
   float gsh_x = 0.0f, gsh_y = 0.0f, gsh_z = 0.0f;
   if (p.shs != nullptr) {
     float* gsh = p.grad_sh + (size_t)tid * (size_t)(3 * p.K);
-    if (rad > 0) {
-      const uint8_t cl = p.clamped != nullptr ? p.clamped[tid] : 0;
-      const float g0 = rcol0 * (1.0f - (float)(cl & 1));
-      const float g1 = rcol1 * (1.0f - (float)((cl >> 1) & 1));
-      const float g2 = rcol2 * (1.0f - (float)((cl >> 2) & 1));
+    const uint8_t cl = rad > 0 && p.clamped != nullptr ? p.clamped[tid] : 0;
+    const float g0 = rcol0 * (1.0f - (float)(cl & 1));
+    const float g1 = rcol1 * (1.0f - (float)((cl >> 1) & 1));
+    const float g2 = rcol2 * (1.0f - (float)((cl >> 2) & 1));
+    const float dirx = mx - p.campos[0], diry = my - p.campos[1], dirz = mz - p.campos[2];
+    if (p.sh_vec16) {  // uniform: the whole wave stages its blocks
+      const V3 gm = sh_backward_row(stage.rows + stage.lane * kShRow, p.degree, valid && rad > 0, dirx, diry,
+                                    dirz, g0, g1, g2);
+      if (rad > 0) {
+        gsh_x = gm.x;
+        gsh_y = gm.y;
+        gsh_z = gm.z;
+      }
+    } else if (valid && rad > 0) {
       const float* sh = p.shs + (size_t)tid * (size_t)(3 * p.K);
-      const float dirx = mx - p.campos[0], diry = my - p.campos[1], dirz = mz - p.campos[2];
-      const V3 gm = p.sh_vec16 ? sh_backward<true>(sh, gsh, p.K, p.degree, dirx, diry, dirz, g0, g1, g2)
-                               : sh_backward<false>(sh, gsh, p.K, p.degree, dirx, diry, dirz, g0, g1, g2);
+      const V3 gm = sh_backward<false>(sh, gsh, p.K, p.degree, dirx, diry, dirz, g0, g1, g2);
       gsh_x = gm.x;
       gsh_y = gm.y;
       gsh_z = gm.z;
-    } else if (p.sh_vec16) {
-#pragma unroll
-      for (int i = 0; i < 12; ++i) reinterpret_cast<float4*>(gsh)[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    } else {
+    } else if (valid) {
       for (int k = 0; k < 3 * p.K; ++k) gsh[k] = 0.0f;
     }
   }
+  if (!valid) return;
 
   // Part C: accumulate.
   p.grad_means3d[3 * tid + 0] = pm_x + gcm_x + gsh_x;
@@ -1102,6 +1288,21 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(PreprocessBwdParams
     p.grad_colors[3 * tid + 1] = rcol1;
     p.grad_colors[3 * tid + 2] = rcol2;
   }
+}
+
+__global__ __launch_bounds__(256) void preprocess_bwd_kernel(PreprocessBwdParams p) {
+  __shared__ float4 s_sh[256 / 64][64 * kShRow];
+  if (p.P <= 0) return;
+  const int tid = blockIdx.x * blockDim.x + threadIdx.x;
+  ShStage stage;
+  stage.lane = threadIdx.x & 63;
+  stage.rows = s_sh[threadIdx.x >> 6];
+  stage.w0 = tid - stage.lane;
+  stage.nvalid = p.P - stage.w0 < 64 ? p.P - stage.w0 : 64;
+  const bool staged = p.shs != nullptr && p.sh_vec16 != 0;  // uniform
+  if (staged) sh_stage_in(stage, p.shs);
+  preprocess_bwd_one(p, tid < p.P ? tid : p.P - 1, tid < p.P, stage);
+  if (staged) sh_stage_out(stage, p.grad_sh);
 }
 
 }  // namespace gs
