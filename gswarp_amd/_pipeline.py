@@ -295,8 +295,12 @@ BUCKET_SIZING = "auto"
 
 # The binning's point-order scan: one kernel (gs_scan_tiles_onepass, a
 # decoupled look-back over a state that the preprocess prepares) when True,
-# else the two-pass gs_scan_tiles.  SCAN_SPIN_LIMIT bounds each of its waits
-# (sleeps of about 64 cycles); a wait never comes near it in practice.
+# else the two-pass gs_scan_tiles.  SCAN_SPIN_LIMIT bounds the rounds of each
+# of its waits; a round is an agent-scope load of 256 status words across the
+# XCDs, two ballots, two workgroup barriers and a short sleep (on the order of
+# a microsecond), so the bound is about a second, where a real wait (blocks
+# start in index order) takes a few microseconds.  A timed-out wait falls back
+# to summing the counts directly (exact, slower).
 SCAN_ONEPASS = True
 SCAN_SPIN_LIMIT = 1 << 20
 
