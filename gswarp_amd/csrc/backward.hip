@@ -514,21 +514,14 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
           Ti[k] = tin;
         };
         // A block with no candidate in the whole wave is skipped: there G = 0
-        // for every lane, which leaves 1/T, S and the sums unchanged.  With two
-        // blocks, whichever is visited first starts the sums on each path, so
-        // a visit that skips the first block computes no -0 starting values.
-        if constexpr (kPix == 2) {
-          if (cand_lanes[0] != 0) {
-            blend(0);
-            if (cand_lanes[1] != 0) blend(1);
-          } else {
-            blend(1);
-          }
-        } else {
+        // for every lane, which leaves 1/T, S and the sums unchanged.  (Giving
+        // the two blocks of a half their own paths, so that a visit skipping
+        // the first one computes no -0 starting values, made the compiler
+        // copy the four carried pixel states between registers on every
+        // visit and took 79 VGPRs instead of 72: 1-2% slower.)
 #pragma unroll
-          for (int k = 0; k < kPix; ++k)
-            if (cand_lanes[k] != 0) blend(k);
-        }
+        for (int k = 0; k < kPix; ++k)
+          if (cand_lanes[k] != 0) blend(k);
         // Pixel moments of v about the Gaussian's mean; the conic, opacity
         // and W/2, H/2 factors are per Gaussian and applied once, when the
         // per-Gaussian backward turns the sums into 2D gradients.
@@ -649,8 +642,8 @@ __device__ __forceinline__ void render_bwd_tiles(const RenderBwdParams& p) {
     render_bwd_slice<kDepth, 2, 1, false>(p, tile, quadrant, s_rec, s_slot);
 }
 
-// The halves and quadrants fit 80 VGPRs, six waves per SIMD, which hide
-// more of a visit's latency than five; the whole-tile walk needs more.
+// The halves and quadrants need 72 VGPRs, seven waves per SIMD (the bound
+// keeps them at six or more); the whole-tile walk needs more.
 template <bool kDepth>
 __global__ __launch_bounds__(64, 6) void render_bwd_kernel(RenderBwdParams p) {
   render_bwd_tiles<kDepth, false>(p);
