@@ -60,6 +60,7 @@ struct RenderFwdParams {
   // optional: the tiles in the order the workgroups take them (gs_tile_order),
   // null: in tile order
   const int* tile_order;
+  int masked;  // blend updates under the exec mask of the blending lanes (render_fwd_tile)
   // optional: clear_floats floats at clear (16-byte aligned) set to 0 by the
   // grid on the way, the backward's gradient accumulator
   float* clear;
@@ -115,19 +116,20 @@ constexpr int kStagedMaxList = 1 << 16;
 // plane (64-byte segments) instead of one scattered word per blended
 // Gaussian, and the unused slots in the same stores.  Larger K, and tiles
 // of kStagedMaxList pairs or more, keep the direct stores during the walk.
-template <bool kFlow, bool kDepth, int kPixPerLane, bool kStaged = false>
-__global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
-  constexpr int kSubs = 4 / kPixPerLane;
-  __shared__ float4 s_rec[3 * 64];  // record j at s_rec[3 j .. 3 j + 2]
-  __shared__ int s_id[kFlow ? 64 : 1];
-  extern __shared__ unsigned short s_pos[];  // kStaged: slot s of pixel k at [(s kPix + k) 64 + lane]
-  const int lane = threadIdx.x;
-  const int unit = xcd_unit(blockIdx.x, p.num_tiles * kSubs);
-  if (unit >= p.num_tiles * kSubs) {  // grid padding
-    clear_share(p, lane);
-    return;
-  }
-  const int2 ts = make_int2(p.tile_order ? p.tile_order[unit / kSubs] : unit / kSubs, unit % kSubs);
+//
+// kMasked: a pixel's blend updates run under the exec mask of the lanes that
+// blend (a visit with none skips them), which replaces three selects (four-
+// cycle instructions) per visit and the record's colour read of visits
+// without a blend by a scalar branch.  That branch and its mask sit on the
+// walk's serial path, so it pays where the kernel is bound by its issue rate
+// (config 2 render 0.230 -> 0.223 ms, config 4 0.256 -> 0.252) and not where
+// a few long walks bound it (config 1: 12% slower); the host takes it under
+// the tile order's condition (tile_order_pays: lists of 192 pairs a tile or
+// more on average).  (Choosing per tile, selects for lists over four times
+// the mean, kept config 1 2.5% slower and config 4 1.3% slower.)
+template <bool kFlow, bool kDepth, int kPixPerLane, bool kStaged, bool kMasked>
+__device__ __forceinline__ void render_fwd_tile(const RenderFwdParams& p, float4* s_rec, int* s_id,
+                                                unsigned short* s_pos, int lane, int2 ts) {
   const int tile = ts.x;
   const int tx = tile % p.grid_x;
   const int ty = tile / p.grid_x;
@@ -245,28 +247,54 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
         const uint64_t fin_lanes = ok_lanes & __builtin_amdgcn_fcmpf(test_T, kTransmittanceMin, kCmpOLT);
         live_lanes[k] &= ~fin_lanes;
         const bool blend = __builtin_amdgcn_inverse_ballot_w64(ok_lanes & ~fin_lanes);
-        // A pixel that does not blend adds a contribution of exactly +0 (the
-        // sums are unchanged bit for bit), which replaces per-output selects.
-        const float contribution = blend ? alpha * T[k] : 0.0f;
-        c0[k] = fmaf(f.x, contribution, c0[k]);
-        c1[k] = fmaf(f.y, contribution, c1[k]);
-        c2[k] = fmaf(f.z, contribution, c2[k]);
-        ws[k] = ws[k] + contribution;
-        if (kDepth) da[k] = fmaf(b.z, contribution, da[k]);
-        if (staged) {
-          if (aux && blend && nsucc[k] < p.top_k)
-            s_pos[(nsucc[k] * kPixPerLane + k) * 64 + lane] = (unsigned short)(base + j);
-        } else if (aux && blend && nsucc[k] < p.top_k) {
-          const size_t pix = (size_t)(py0 + kRowStep * k) * p.W + px;
-          const size_t ai = (size_t)nsucc[k] * P + pix;
-          p.gs_per_pixel[ai] = s_id[j];
-          p.weight[ai] = contribution;
-          p.x_mu[ai] = dx;
-          p.x_mu[(size_t)p.top_k * P + ai] = dy[k];
+        if constexpr (kMasked) {
+          if (blend) {
+            const float contribution = alpha * T[k];
+            c0[k] = fmaf(f.x, contribution, c0[k]);
+            c1[k] = fmaf(f.y, contribution, c1[k]);
+            c2[k] = fmaf(f.z, contribution, c2[k]);
+            ws[k] = ws[k] + contribution;
+            if (kDepth) da[k] = fmaf(b.z, contribution, da[k]);
+            if (staged) {
+              if (aux && nsucc[k] < p.top_k)
+                s_pos[(nsucc[k] * kPixPerLane + k) * 64 + lane] = (unsigned short)(base + j);
+            } else if (aux && nsucc[k] < p.top_k) {
+              const size_t pix = (size_t)(py0 + kRowStep * k) * p.W + px;
+              const size_t ai = (size_t)nsucc[k] * P + pix;
+              p.gs_per_pixel[ai] = s_id[j];
+              p.weight[ai] = contribution;
+              p.x_mu[ai] = dx;
+              p.x_mu[(size_t)p.top_k * P + ai] = dy[k];
+            }
+            if (kFlow) nsucc[k] += 1;
+            T[k] = test_T;
+            last[k] = base + j + 1;
+          }
+        } else {
+          // A pixel that does not blend adds a contribution of exactly +0
+          // (the sums are unchanged bit for bit), which replaces per-output
+          // selects.
+          const float contribution = blend ? alpha * T[k] : 0.0f;
+          c0[k] = fmaf(f.x, contribution, c0[k]);
+          c1[k] = fmaf(f.y, contribution, c1[k]);
+          c2[k] = fmaf(f.z, contribution, c2[k]);
+          ws[k] = ws[k] + contribution;
+          if (kDepth) da[k] = fmaf(b.z, contribution, da[k]);
+          if (staged) {
+            if (aux && blend && nsucc[k] < p.top_k)
+              s_pos[(nsucc[k] * kPixPerLane + k) * 64 + lane] = (unsigned short)(base + j);
+          } else if (aux && blend && nsucc[k] < p.top_k) {
+            const size_t pix = (size_t)(py0 + kRowStep * k) * p.W + px;
+            const size_t ai = (size_t)nsucc[k] * P + pix;
+            p.gs_per_pixel[ai] = s_id[j];
+            p.weight[ai] = contribution;
+            p.x_mu[ai] = dx;
+            p.x_mu[(size_t)p.top_k * P + ai] = dy[k];
+          }
+          if (kFlow) nsucc[k] += blend ? 1 : 0;
+          T[k] = blend ? test_T : T[k];
+          last[k] = blend ? base + j + 1 : last[k];
         }
-        if (kFlow) nsucc[k] += blend ? 1 : 0;
-        T[k] = blend ? test_T : T[k];
-        last[k] = blend ? base + j + 1 : last[k];
       }
     }
   }
@@ -340,6 +368,20 @@ __global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
       }
     }
   }
+}
+
+template <bool kFlow, bool kDepth, int kPixPerLane, bool kStaged, bool kMasked>
+__global__ __launch_bounds__(64) void render_fwd_kernel(RenderFwdParams p) {
+  constexpr int kSubs = 4 / kPixPerLane;
+  __shared__ float4 s_rec[3 * 64];  // record j at s_rec[3 j .. 3 j + 2]
+  __shared__ int s_id[kFlow ? 64 : 1];
+  extern __shared__ unsigned short s_pos[];  // kStaged: slot s of pixel k at [(s kPix + k) 64 + lane]
+  const int lane = threadIdx.x;
+  const int unit = xcd_unit(blockIdx.x, p.num_tiles * kSubs);
+  if (unit < p.num_tiles * kSubs) {  // else grid padding
+    const int2 ts = make_int2(p.tile_order ? p.tile_order[unit / kSubs] : unit / kSubs, unit % kSubs);
+    render_fwd_tile<kFlow, kDepth, kPixPerLane, kStaged, kMasked>(p, s_rec, s_id, s_pos, lane, ts);
+  }
   clear_share(p, lane);
 }
 
@@ -381,24 +423,33 @@ __global__ __launch_bounds__(1024) void tile_order_kernel(int T, const int2* __r
   for (int t = t0; t < T; t += 1024) order[atomicAdd(&s_count[tile_length_class(ranges[t])], 1)] = t;
 }
 
+// One launch of render_fwd_kernel with the template arguments of p's flags.
+template <bool kFlow, bool kDepth, bool kStaged>
+static void launch_render_fwd_as(const RenderFwdParams& p, dim3 grid, size_t lds, hipStream_t s) {
+  if (p.masked)
+    hipLaunchKernelGGL((render_fwd_kernel<kFlow, kDepth, kFwdPix, kStaged, true>), grid, dim3(64), lds, s, p);
+  else
+    hipLaunchKernelGGL((render_fwd_kernel<kFlow, kDepth, kFwdPix, kStaged, false>), grid, dim3(64), lds, s, p);
+}
+
 static int launch_render_fwd(const RenderFwdParams& p, bool flow, hipStream_t s) {
   const dim3 grid(gs::xcd_grid(p.num_tiles * (4 / kFwdPix)));
   if (flow && p.write_aux && p.top_k <= kMaxStagedTopK) {
     const size_t lds = (size_t)p.top_k * kFwdPix * 64 * sizeof(unsigned short);
     if (p.compute_depth)
-      hipLaunchKernelGGL((render_fwd_kernel<true, true, kFwdPix, true>), grid, dim3(64), lds, s, p);
+      launch_render_fwd_as<true, true, true>(p, grid, lds, s);
     else
-      hipLaunchKernelGGL((render_fwd_kernel<true, false, kFwdPix, true>), grid, dim3(64), lds, s, p);
+      launch_render_fwd_as<true, false, true>(p, grid, lds, s);
   } else if (flow) {
     if (p.compute_depth)
-      hipLaunchKernelGGL((render_fwd_kernel<true, true, kFwdPix>), grid, dim3(64), 0, s, p);
+      launch_render_fwd_as<true, true, false>(p, grid, 0, s);
     else
-      hipLaunchKernelGGL((render_fwd_kernel<true, false, kFwdPix>), grid, dim3(64), 0, s, p);
+      launch_render_fwd_as<true, false, false>(p, grid, 0, s);
   } else {
     if (p.compute_depth)
-      hipLaunchKernelGGL((render_fwd_kernel<false, true, kFwdPix>), grid, dim3(64), 0, s, p);
+      launch_render_fwd_as<false, true, false>(p, grid, 0, s);
     else
-      hipLaunchKernelGGL((render_fwd_kernel<false, false, kFwdPix>), grid, dim3(64), 0, s, p);
+      launch_render_fwd_as<false, false, false>(p, grid, 0, s);
   }
   return gs_status_from_hip(hipGetLastError());
 }
@@ -443,6 +494,7 @@ static int gs_render_fwd_common(int32_t W, int32_t H, int32_t num_points, int64_
   p.x_mu = x_mu;
   p.clear = clear_floats > 0 ? clear : nullptr;
   p.clear_floats = clear_floats;
+  p.masked = gs::tile_order_pays(num_rendered, num_points, p.num_tiles) ? 1 : 0;
   p.tile_order = nullptr;
   if (tile_order && gs::tile_order_pays(num_rendered, num_points, p.num_tiles)) {
     const int st = gs_tile_order(p.num_tiles, ranges, tile_order, stream);
