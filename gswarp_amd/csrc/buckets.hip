@@ -60,23 +60,11 @@ __global__ __launch_bounds__(256) void bucket_depth_keys_kernel(int P, const int
   values[i] = i;
 }
 
-// The cover word of depth position j of the valid part of the order (zero
-// past V or for an out-of-range index), and the Gaussian's index.
-__device__ __forceinline__ int4 gather_word(int j, int V, int first, int P, const int* __restrict__ order,
-                                           const int4* __restrict__ coverage, int& idx) {
-  idx = 0;
-  if (j >= V) return make_int4(0, 0, 0, 0);
-  const int i = order[first + j];
-  if ((unsigned)i >= (unsigned)P) return make_int4(0, 0, 0, 0);  // never for a permutation
-  idx = i;
-  return coverage[i];
-}
-
 // Level-1 counts: chunk c (depth positions [c * kL1Chunk, ...) of the valid
 // part of the order) counts its entries per super-tile into
 // hist[bucket * nchunks + c], and stores its cover words and indices in
-// depth order for the ranking pass.  The next group's gathers are issued
-// before the current group is counted.
+// depth order for the ranking pass.  The chunk's indices are loaded in one
+// batch, then its cover words in one batch (addresses clamped, no branches).
 __global__ __launch_bounds__(64) void bucket_count_kernel(int V, int first, int P, const int* __restrict__ order,
                                                          const int4* __restrict__ coverage,
                                                          int4* __restrict__ cw_sorted, int* __restrict__ idx_sorted,
@@ -84,27 +72,30 @@ __global__ __launch_bounds__(64) void bucket_count_kernel(int V, int first, int 
   extern __shared__ int h[];  // B counters
   const int lane = threadIdx.x;
   const int c = blockIdx.x;
+  int idx[kL1Groups];
+#pragma unroll
+  for (int g = 0; g < kL1Groups; ++g) idx[g] = order[first + imin(c * kL1Chunk + g * 64 + lane, V - 1)];
   for (int b = lane; b < B; b += 64) h[b] = 0;
+  int4 cw[kL1Groups];
+#pragma unroll
+  for (int g = 0; g < kL1Groups; ++g) cw[g] = coverage[(unsigned)idx[g] < (unsigned)P ? idx[g] : 0];
   __syncthreads();
-  int idx;
-  int4 cw = gather_word(c * kL1Chunk + lane, V, first, P, order, coverage, idx);
+#pragma unroll
   for (int g = 0; g < kL1Groups; ++g) {
     const int j = c * kL1Chunk + g * 64 + lane;
-    int next_idx = 0;
-    int4 next = make_int4(0, 0, 0, 0);
-    if (g + 1 < kL1Groups) next = gather_word(j + 64, V, first, P, order, coverage, next_idx);
+    // past V, or an out-of-range index (never for a permutation): no word
+    const bool in = j < V && (unsigned)idx[g] < (unsigned)P;
+    const int4 w = in ? cw[g] : make_int4(0, 0, 0, 0);
     if (j < V) {
-      cw_sorted[j] = cw;
-      idx_sorted[j] = idx;
+      cw_sorted[j] = w;
+      idx_sorted[j] = in ? idx[g] : 0;
     }
-    const SuperRect r = super_rect(unpack_cover(cw));
+    const SuperRect r = super_rect(unpack_cover(w));
     for (int sy = r.sy0; sy < r.sy0 + r.ny; ++sy)
       for (int sx = r.sx0; sx < r.sx0 + r.nx; ++sx) {
         const int b = sy * nsx + sx;
         if (b < B) atomicAdd(&h[b], 1);
       }
-    cw = next;
-    idx = next_idx;
   }
   __syncthreads();
   for (int b = lane; b < B; b += 64) hist[(size_t)b * nchunks + c] = h[b];
@@ -231,16 +222,37 @@ __global__ __launch_bounds__(64) void bucket_scatter_kernel(int V, const int4* _
   const int lane = threadIdx.x;
   const int c = blockIdx.x;
   const int j0 = c * kL1Chunk;
-  // loads: words, indices, positions
+  // loads: words, indices, positions, all issued (addresses clamped, no
+  // branches) before the first LDS store, so the wave waits for memory once
+  // per batch
+  {
+    int4 cwv[kL1Groups];
+    int idv[kL1Groups];
 #pragma unroll
-  for (int q = 0; q < kL1Groups; ++q) {
-    const int j = j0 + q * 64 + lane;
-    s_cw[q * 64 + lane] = j < V ? cw_sorted[j] : make_int4(0, 0, 0, 0);
-    s_idx[q * 64 + lane] = j < V ? idx_sorted[j] : 0;
-  }
-  for (int b = lane; b < B; b += 64) {
-    const long long f = (long long)b * nchunks + c;
-    cnt[b] = f > 0 ? hist_incl[f - 1] : 0;
+    for (int q = 0; q < kL1Groups; ++q) {
+      const int j = imin(j0 + q * 64 + lane, V - 1);
+      cwv[q] = cw_sorted[j];
+      idv[q] = idx_sorted[j];
+    }
+    constexpr int kPosBatch = 4;
+    for (int b0 = 0; b0 < B; b0 += 64 * kPosBatch) {
+      int v[kPosBatch];
+#pragma unroll
+      for (int q = 0; q < kPosBatch; ++q) {
+        const long long f = (long long)imin(b0 + q * 64 + lane, B - 1) * nchunks + c;
+        v[q] = hist_incl[f > 0 ? f - 1 : 0];
+        v[q] = f > 0 ? v[q] : 0;
+      }
+#pragma unroll
+      for (int q = 0; q < kPosBatch; ++q)
+        if (b0 + q * 64 + lane < B) cnt[b0 + q * 64 + lane] = v[q];
+    }
+#pragma unroll
+    for (int q = 0; q < kL1Groups; ++q) {
+      const bool in = j0 + q * 64 + lane < V;
+      s_cw[q * 64 + lane] = in ? cwv[q] : make_int4(0, 0, 0, 0);
+      s_idx[q * 64 + lane] = in ? idv[q] : 0;
+    }
   }
   __syncthreads();
   // entries and coverage bands per Gaussian, scanned over the chunk
@@ -284,13 +296,34 @@ __global__ __launch_bounds__(64) void bucket_scatter_kernel(int V, const int4* _
     const int b1 = g1 < kL1Chunk ? s_bexcl[g1] : band_all;
     const int e_begin = s_excl[g0], e_end = g1 < kL1Chunk ? s_excl[g1] : total;
     __syncthreads();  // the previous segment's rounds are done with s_band
-    for (int t = b0 + lane; t < b1; t += 64) {
-      const int g = table_floor(s_bexcl, t);
-      const CoverWord w = unpack_cover(s_cw[g]);
-      const int b = t - s_bexcl[g];
-      if (w.band_off >= 0 && band_store != nullptr) {
-        s_band[t - b0] = band_store[w.band_off + b];
-      } else {
+    // batches of kBandBatch words per lane: the stored words' loads are all
+    // issued before the first of them is used; the words to recompute are
+    // handled after, one at a time
+    constexpr int kBandBatch = 4;
+    for (int tb = b0; tb < b1; tb += 64 * kBandBatch) {
+      unsigned word[kBandBatch];
+      unsigned recompute = 0;  // bit q: word q has no stored copy
+#pragma unroll
+      for (int q = 0; q < kBandBatch; ++q) {
+        const int t = imin(tb + q * 64 + lane, b1 - 1);
+        const int g = table_floor(s_bexcl, t);
+        const CoverWord w = unpack_cover(s_cw[g]);
+        const bool stored = w.band_off >= 0 && band_store != nullptr;
+        word[q] = stored ? band_store[w.band_off + (t - s_bexcl[g])] : 0u;
+        recompute |= stored || tb + q * 64 + lane >= b1 ? 0u : 1u << q;
+      }
+#pragma unroll
+      for (int q = 0; q < kBandBatch; ++q) {
+        const int t = tb + q * 64 + lane;
+        if (t < b1 && !((recompute >> q) & 1u)) s_band[t - b0] = word[q];
+      }
+#pragma unroll 1
+      for (int q = 0; q < kBandBatch; ++q) {
+        if (!((recompute >> q) & 1u)) continue;
+        const int t = tb + q * 64 + lane;
+        const int g = table_floor(s_bexcl, t);
+        const CoverWord w = unpack_cover(s_cw[g]);
+        const int b = t - s_bexcl[g];
         const int idx = s_idx[g];
         const float4 r0v = records[3 * (size_t)idx];
         const float4 r1v = records[3 * (size_t)idx + 1];
@@ -341,19 +374,23 @@ __global__ __launch_bounds__(64) void bucket_scatter_kernel(int V, const int4* _
 
 // Per super-tile: its entry list [list_start[s], list_start[s + 1]) from the
 // scanned level-1 counts, and its level-2 chunks [chunk_start[s],
-// chunk_start[s + 1]); chunk_start[B] is the number of level-2 chunks.
+// chunk_start[s + 1]); chunk_start[B] is the number of level-2 chunks.  Each
+// chunk g < nc2_max gets chunk_info[g] = (s, first entry, end entry), or
+// (-1, 0, 0) past the last chunk, so that a chunk's wave finds its entries
+// with one load.
 __global__ __launch_bounds__(256) void bucket_table_kernel(const int* __restrict__ hist_incl, int nchunks, int B,
-                                                          int* __restrict__ list_start,
-                                                          int* __restrict__ chunk_start) {
+                                                          int nc2_max, int* __restrict__ list_start,
+                                                          int* __restrict__ chunk_start,
+                                                          int4* __restrict__ chunk_info) {
   __shared__ int s_tot[256 / 64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int carry = 0;
   for (int s0 = 0; s0 < B; s0 += 256) {
     const int s = s0 + threadIdx.x;
-    int nch = 0;
+    int nch = 0, start = 0, end = 0;
     if (s < B) {
-      const int start = s > 0 ? hist_incl[(size_t)s * nchunks - 1] : 0;
-      const int end = hist_incl[(size_t)(s + 1) * nchunks - 1];
+      start = s > 0 ? hist_incl[(size_t)s * nchunks - 1] : 0;
+      end = hist_incl[(size_t)(s + 1) * nchunks - 1];
       list_start[s] = start;
       if (s == B - 1) list_start[B] = end;
       nch = (end - start + kL2Chunk - 1) / kL2Chunk;
@@ -366,22 +403,19 @@ __global__ __launch_bounds__(256) void bucket_table_kernel(const int* __restrict
       before += k < wave ? s_tot[k] : 0;
       all += s_tot[k];
     }
-    if (s < B) chunk_start[s] = carry + before + incl - nch;
+    if (s < B) {
+      const int first = carry + before + incl - nch;
+      chunk_start[s] = first;
+      for (int k = 0; k < nch && first + k < nc2_max; ++k) {
+        const int e0 = start + k * kL2Chunk;
+        chunk_info[first + k] = make_int4(s, e0, imin(e0 + kL2Chunk, end), 0);
+      }
+    }
     carry += all;
     __syncthreads();
   }
   if (threadIdx.x == 0) chunk_start[B] = carry;
-}
-
-// Super-tile of level-2 chunk g: the last s with chunk_start[s] <= g.
-__device__ __forceinline__ int chunk_super(const int* __restrict__ chunk_start, int B, int g) {
-  int lo = 0, hi = B;
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (chunk_start[mid] <= g) lo = mid;
-    else hi = mid;
-  }
-  return lo;
+  for (int g = carry + threadIdx.x; g < nc2_max; g += 256) chunk_info[g] = make_int4(-1, 0, 0, 0);
 }
 
 // Whether tile lane (bit `lane` of the super-tile's masks) is set in m: the
@@ -391,23 +425,53 @@ __device__ __forceinline__ unsigned mask_bit(unsigned long long m, int lane) {
   return (half >> (lane & 31)) & 1u;
 }
 
+// Copies the entries [e0, e0 + n) (1 <= n <= kL2Chunk) of a level-2 chunk
+// into LDS, zero past n up to the next multiple of 16.  Every load of the
+// lane is issued before its first LDS store (addresses clamped into the
+// chunk, no branches), so the wave waits for memory once.
+template <bool kIds>
+__device__ __forceinline__ void stage_chunk(int e0, int n, int lane, const unsigned long long* __restrict__ e_mask,
+                                            const int* __restrict__ e_idx, unsigned long long* s_m, int* s_id) {
+  constexpr int kQ = kL2Chunk / 64;
+  unsigned long long m[kQ];
+  int id[kQ];
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) {
+    const int e = e0 + imin(q * 64 + lane, n - 1);
+    m[q] = e_mask[e];
+    if (kIds) id[q] = e_idx[e];
+  }
+  const int n16 = (n + 15) & ~15;
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) {
+    const int i = q * 64 + lane;
+    if (i < n16) {
+      s_m[i] = i < n ? m[q] : 0ull;
+      if (kIds) s_id[i] = i < n ? id[q] : 0;
+    }
+  }
+}
+
 // Level-2 counts: lane k of chunk g counts the chunk's entries covering tile k
 // of its super-tile into cnt2[g * 64 + k].  The chunk's masks are copied into
 // LDS (coalesced) and every lane reads them all, 16 per batch of reads.
-__global__ __launch_bounds__(64) void bucket_tile_count_kernel(const int* __restrict__ list_start,
-                                                              const int* __restrict__ chunk_start, int B, int E,
+// chunk_info[g] = (super-tile, first entry, end entry), super-tile -1 past the
+// last chunk.
+__global__ __launch_bounds__(64) void bucket_tile_count_kernel(const int4* __restrict__ chunk_info, int E,
                                                               const unsigned long long* __restrict__ e_mask,
                                                               int* __restrict__ cnt2) {
   __shared__ __align__(16) unsigned long long s_m[kL2Chunk];
   const int g = blockIdx.x;
-  if (g >= chunk_start[B]) return;
-  const int s = chunk_super(chunk_start, B, g);
-  const int e0 = list_start[s] + (g - chunk_start[s]) * kL2Chunk;
-  const int e1 = imin(imin(e0 + kL2Chunk, list_start[s + 1]), E);
-  const int n16 = (e1 - e0 + 15) & ~15;  // entries past the chunk count nothing: zero masks
   const int lane = threadIdx.x;
-#pragma unroll 4
-  for (int i = lane; i < n16; i += 64) s_m[i] = e0 + i < e1 ? e_mask[e0 + i] : 0ull;
+  const int4 ci = chunk_info[g];
+  if (ci.x < 0) return;
+  const int e0 = ci.y, n = imin(ci.z, E) - e0;
+  if (n <= 0) {
+    cnt2[(size_t)g * 64 + lane] = 0;
+    return;
+  }
+  stage_chunk<false>(e0, n, lane, e_mask, nullptr, s_m, nullptr);
+  const int n16 = (n + 15) & ~15;
   __syncthreads();
   int count = 0;
   for (int i0 = 0; i0 < n16; i0 += 16) {
@@ -429,14 +493,22 @@ __global__ __launch_bounds__(64) void bucket_tile_count_kernel(const int* __rest
 __global__ __launch_bounds__(64) void bucket_tile_prefix_kernel(const int* __restrict__ chunk_start, int nsx,
                                                                int grid_x, int grid_y, int nc2,
                                                                int* __restrict__ cnt2, int* __restrict__ tile_count) {
+  constexpr int kBatch = 16;  // chunks whose counts are loaded together
   const int s = blockIdx.x;
   const int lane = threadIdx.x;
+  const int g0 = chunk_start[s], g1 = imin(chunk_start[s + 1], nc2);
   int run = 0;
-  for (int g = chunk_start[s]; g < imin(chunk_start[s + 1], nc2); ++g) {
-    int* p = cnt2 + (size_t)g * 64 + lane;
-    const int v = *p;
-    *p = run;
-    run += v;
+  for (int g = g0; g < g1; g += kBatch) {
+    int v[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) v[q] = cnt2[(size_t)imin(g + q, g1 - 1) * 64 + lane];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      if (g + q < g1) {
+        cnt2[(size_t)(g + q) * 64 + lane] = run;
+        run += v[q];
+      }
+    }
   }
   const int tx = (s % nsx) * kSuperTile + (lane & 7);
   const int ty = (s / nsx) * kSuperTile + (lane >> 3);
@@ -480,8 +552,7 @@ typedef int int4_dw __attribute__((ext_vector_type(4), aligned(4)));
 // up to the next 64-byte boundary of its tile's list once (the head), and
 // after that whole 64-byte blocks of 16 as four 16-byte stores, so the list
 // is written in full HBM sectors; the rest follows at the end.
-__global__ __launch_bounds__(64) void bucket_tile_scatter_kernel(const int* __restrict__ list_start,
-                                                                const int* __restrict__ chunk_start, int B, int E,
+__global__ __launch_bounds__(64) void bucket_tile_scatter_kernel(const int4* __restrict__ chunk_info, int E,
                                                                 int nsx, int grid_x, int grid_y,
                                                                 const int* __restrict__ e_idx,
                                                                 const unsigned long long* __restrict__ e_mask,
@@ -492,22 +563,22 @@ __global__ __launch_bounds__(64) void bucket_tile_scatter_kernel(const int* __re
   __shared__ __align__(16) int s_id[kL2Chunk];
   __shared__ int s_ring[kStageRing * 64];  // slot-major: slot q of tile k at q * 64 + k (conflict-free)
   const int g = blockIdx.x;
-  if (g >= chunk_start[B]) return;
-  const int s = chunk_super(chunk_start, B, g);
-  const int e0 = list_start[s] + (g - chunk_start[s]) * kL2Chunk;
-  const int e1 = imin(imin(e0 + kL2Chunk, list_start[s + 1]), E);
-  const int n = e1 - e0;
-  const int n16 = (n + 15) & ~15;  // entries past n have no tile: zero masks
   const int lane = threadIdx.x;
-#pragma unroll 4
-  for (int i = lane; i < n16; i += 64) {
-    s_m[i] = i < n ? e_mask[e0 + i] : 0ull;
-    s_id[i] = i < n ? e_idx[e0 + i] : 0;
-  }
+  const int4 ci = chunk_info[g];
+  const int s = ci.x;
+  if (s < 0) return;
+  const int e0 = ci.y;
+  const int n = imin(ci.z, E) - e0;
+  if (n <= 0) return;
+  const int n16 = (n + 15) & ~15;  // entries past n have no tile: zero masks
   const int tx = (s % nsx) * kSuperTile + (lane & 7);
   const int ty = (s / nsx) * kSuperTile + (lane >> 3);
   const bool tile_ok = tx < grid_x && ty < grid_y;
-  const long long out = tile_ok ? (long long)ranges[ty * grid_x + tx].x + cnt2[(size_t)g * 64 + lane] : 0;
+  // the tile's list start and the chunk's offset in it, loaded with the chunk
+  const int start = ranges[tile_ok ? ty * grid_x + tx : 0].x;
+  const int before = cnt2[(size_t)g * 64 + lane];
+  stage_chunk<true>(e0, n, lane, e_mask, e_idx, s_m, s_id);
+  const long long out = tile_ok ? (long long)start + before : 0;
   int head = (int)((16 - (out & 15)) & 15);  // pairs before the list's next 64-byte boundary
   // staged pairs [flushed, staged) in ring slots modulo kStageRing
   int staged = 0, flushed = 0;
@@ -575,7 +646,7 @@ namespace {
 struct BucketLayout {
   int grid_x, grid_y, num_tiles, nsx, nsy, B, nchunks, nc2_max;
   size_t off_keys, off_vals, off_keys_alt, off_vals_alt, off_sort, off_cw, off_idx, off_hist, off_hist_incl, off_scan,
-      off_info, off_eidx, off_emask, off_list, off_chunk, off_cnt2, off_tiles, total;
+      off_info, off_eidx, off_emask, off_list, off_chunk, off_cinfo, off_cnt2, off_tiles, total;
 };
 
 int bucket_layout(int32_t P, int32_t V, int64_t E, int32_t W, int32_t H, BucketLayout& L) {
@@ -612,6 +683,7 @@ int bucket_layout(int32_t P, int32_t V, int64_t E, int32_t W, int32_t H, BucketL
   L.off_emask = take((size_t)E * 8);
   L.off_list = take((size_t)(L.B + 1) * 4);
   L.off_chunk = take((size_t)(L.B + 1) * 4);
+  L.off_cinfo = take((size_t)L.nc2_max * 16);
   L.off_cnt2 = take((size_t)L.nc2_max * 64 * 4);
   L.off_tiles = take((size_t)L.num_tiles * 4);
   L.total = o;
@@ -674,6 +746,7 @@ extern "C" int gs_bin_buckets(int32_t P, int32_t num_valid, int64_t num_entries,
   unsigned long long* e_mask = reinterpret_cast<unsigned long long*>(ws + L.off_emask);
   int* list_start = reinterpret_cast<int*>(ws + L.off_list);
   int* chunk_start = reinterpret_cast<int*>(ws + L.off_chunk);
+  int4* chunk_info = reinterpret_cast<int4*>(ws + L.off_cinfo);
   int* cnt2 = reinterpret_cast<int*>(ws + L.off_cnt2);
   int* tile_count = reinterpret_cast<int*>(ws + L.off_tiles);
   const int4* cw = reinterpret_cast<const int4*>(coverage);
@@ -705,16 +778,15 @@ extern "C" int gs_bin_buckets(int32_t P, int32_t num_valid, int64_t num_entries,
   mark(2);
 
   // 3. level 2: per-tile lists
-  hipLaunchKernelGGL(gs::bucket_table_kernel, dim3(1), dim3(256), 0, s, hist_incl, L.nchunks, L.B, list_start,
-                     chunk_start);
-  hipLaunchKernelGGL(gs::bucket_tile_count_kernel, dim3(L.nc2_max), dim3(64), 0, s, list_start, chunk_start, L.B,
-                     (int)E, e_mask, cnt2);
+  hipLaunchKernelGGL(gs::bucket_table_kernel, dim3(1), dim3(256), 0, s, hist_incl, L.nchunks, L.B, L.nc2_max,
+                     list_start, chunk_start, chunk_info);
+  hipLaunchKernelGGL(gs::bucket_tile_count_kernel, dim3(L.nc2_max), dim3(64), 0, s, chunk_info, (int)E, e_mask, cnt2);
   hipLaunchKernelGGL(gs::bucket_tile_prefix_kernel, dim3(L.B), dim3(64), 0, s, chunk_start, L.nsx, L.grid_x,
                      L.grid_y, L.nc2_max, cnt2, tile_count);
   hipLaunchKernelGGL(gs::bucket_ranges_kernel, dim3(1), dim3(1024), 0, s, L.num_tiles, tile_count,
                      reinterpret_cast<int2*>(ranges));
-  hipLaunchKernelGGL(gs::bucket_tile_scatter_kernel, dim3(L.nc2_max), dim3(64), 0, s, list_start, chunk_start, L.B,
-                     (int)E, L.nsx, L.grid_x, L.grid_y, e_idx, e_mask, cnt2, reinterpret_cast<const int2*>(ranges),
+  hipLaunchKernelGGL(gs::bucket_tile_scatter_kernel, dim3(L.nc2_max), dim3(64), 0, s, chunk_info, (int)E, L.nsx,
+                     L.grid_x, L.grid_y, e_idx, e_mask, cnt2, reinterpret_cast<const int2*>(ranges),
                      (long long)num_rendered, point_list);
   mark(3);
   return gs_status_from_hip(hipGetLastError());

@@ -399,13 +399,27 @@ __device__ __forceinline__ int tile_length_class(int2 r) {
   return 255 - c;  // longest first
 }
 
+// Up to kOrderRegTiles tiles per thread keep their classes in registers
+// between the two passes (images of up to 16384 tiles); beyond, the second
+// pass reads the ranges again.
+constexpr int kOrderRegTiles = 16;
+
 __global__ __launch_bounds__(1024) void tile_order_kernel(int T, const int2* __restrict__ ranges,
                                                          int* __restrict__ order) {
   __shared__ __align__(16) int s_count[256];
   const int t0 = threadIdx.x;
   if (t0 < 256) s_count[t0] = 0;
+  int cls[kOrderRegTiles];
+#pragma unroll
+  for (int i = 0; i < kOrderRegTiles; ++i) {
+    const int t = t0 + 1024 * i;
+    cls[i] = t < T ? tile_length_class(ranges[t]) : 0;
+  }
   __syncthreads();
-  for (int t = t0; t < T; t += 1024) atomicAdd(&s_count[tile_length_class(ranges[t])], 1);
+#pragma unroll
+  for (int i = 0; i < kOrderRegTiles; ++i)
+    if (t0 + 1024 * i < T) atomicAdd(&s_count[cls[i]], 1);
+  for (int t = t0 + 1024 * kOrderRegTiles; t < T; t += 1024) atomicAdd(&s_count[tile_length_class(ranges[t])], 1);
   __syncthreads();
   if (t0 < 64) {  // exclusive prefix over the 256 classes, four per lane
     const int4 c = reinterpret_cast<const int4*>(s_count)[t0];
@@ -420,7 +434,13 @@ __global__ __launch_bounds__(1024) void tile_order_kernel(int T, const int2* __r
     reinterpret_cast<int4*>(s_count)[t0] = make_int4(e, e + c.x, e + c.x + c.y, e + c.x + c.y + c.z);
   }
   __syncthreads();
-  for (int t = t0; t < T; t += 1024) order[atomicAdd(&s_count[tile_length_class(ranges[t])], 1)] = t;
+#pragma unroll
+  for (int i = 0; i < kOrderRegTiles; ++i) {
+    const int t = t0 + 1024 * i;
+    if (t < T) order[atomicAdd(&s_count[cls[i]], 1)] = t;
+  }
+  for (int t = t0 + 1024 * kOrderRegTiles; t < T; t += 1024)
+    order[atomicAdd(&s_count[tile_length_class(ranges[t])], 1)] = t;
 }
 
 // One launch of render_fwd_kernel with the template arguments of p's flags.
