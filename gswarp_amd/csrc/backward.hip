@@ -294,38 +294,52 @@ __device__ __forceinline__ void render_bwd_slice(const RenderBwdParams& p, int t
 #pragma unroll
   for (int c = 0; c < kCols; ++c) pfx[c] = (float)(sx0 + 8 * c + (lane & 7));
   int2 rg = p.ranges[tile];
-  rg.x = imax(0, imin(rg.x, p.num_rendered));
-  rg.y = imax(rg.x, imin(rg.y, p.num_rendered));
-  const int n = rg.y - rg.x;
-
+  // The pixels' loads are issued with the range's, at addresses clamped into
+  // the image and with no branch between them, so the wave waits for memory
+  // once; pixels outside the image (or of an empty tile) then take the
+  // values of a pixel that blends nothing.
+  const float bg0 = p.bg[0], bg1 = p.bg[1], bg2 = p.bg[2];
   float pfy[kPix], Ti[kPix], S[kPix], gp0[kPix], gp1[kPix], gp2[kPix], gpd[kPix], gpa[kPix];
+  float a_out[kPix];
   int last[kPix];
-  int lmax = 0;
 #pragma unroll
   for (int k = 0; k < kPix; ++k) {
     const int px = sx0 + 8 * (k % kCols) + (lane & 7);
     const int py = sy0 + 8 * (k / kCols) + (lane >> 3);
     pfy[k] = (float)py;
-    last[k] = 0;
-    Ti[k] = 1.0f;
-    S[k] = gp0[k] = gp1[k] = gp2[k] = gpd[k] = gpa[k] = 0.0f;
-    if (px < p.W && py < p.H && n > 0) {
-      const int pix = py * p.W + px;
-      const float T0 = 1.0f - p.out_alpha[pix];
-      // With T = 0 every term of the pixel is an exact zero, as for a pixel
-      // that blends nothing (and 1/T would be infinite).
-      last[k] = T0 == 0.0f ? 0 : imax(0, imin(p.n_contrib[pix], n));
-      if (T0 != 0.0f) Ti[k] = 1.0f / T0;
-      // absent upstream gradients (null) are zero
-      if (p.grad_color) {
-        gp0[k] = p.grad_color[pix];
-        gp1[k] = p.grad_color[P + pix];
-        gp2[k] = p.grad_color[2 * P + pix];
-      }
-      if (kDepth && p.grad_depth) gpd[k] = p.grad_depth[pix];
-      if (p.grad_alpha) gpa[k] = p.grad_alpha[pix];
-      S[k] = fmaf(p.bg[2], gp2[k], fmaf(p.bg[1], gp1[k], p.bg[0] * gp0[k]));
+    const int pix = imin(py, p.H - 1) * p.W + imin(px, p.W - 1);
+    a_out[k] = p.out_alpha[pix];
+    last[k] = p.n_contrib[pix];
+    gp0[k] = gp1[k] = gp2[k] = gpd[k] = gpa[k] = 0.0f;
+    // absent upstream gradients (null) are zero
+    if (p.grad_color) {
+      gp0[k] = p.grad_color[pix];
+      gp1[k] = p.grad_color[P + pix];
+      gp2[k] = p.grad_color[2 * P + pix];
     }
+    if (kDepth && p.grad_depth) gpd[k] = p.grad_depth[pix];
+    if (p.grad_alpha) gpa[k] = p.grad_alpha[pix];
+  }
+  rg.x = imax(0, imin(rg.x, p.num_rendered));
+  rg.y = imax(rg.x, imin(rg.y, p.num_rendered));
+  const int n = rg.y - rg.x;
+  int lmax = 0;
+#pragma unroll
+  for (int k = 0; k < kPix; ++k) {
+    const int px = sx0 + 8 * (k % kCols) + (lane & 7);
+    const int py = sy0 + 8 * (k / kCols) + (lane >> 3);
+    const float T0 = 1.0f - a_out[k];
+    // With T = 0 every term of the pixel is an exact zero, as for a pixel
+    // that blends nothing (and 1/T would be infinite).
+    const bool live = px < p.W && py < p.H && n > 0;
+    last[k] = live && T0 != 0.0f ? imax(0, imin(last[k], n)) : 0;
+    Ti[k] = live && T0 != 0.0f ? 1.0f / T0 : 1.0f;
+    gp0[k] = live ? gp0[k] : 0.0f;
+    gp1[k] = live ? gp1[k] : 0.0f;
+    gp2[k] = live ? gp2[k] : 0.0f;
+    gpd[k] = live ? gpd[k] : 0.0f;
+    gpa[k] = live ? gpa[k] : 0.0f;
+    S[k] = live ? fmaf(bg2, gp2[k], fmaf(bg1, gp1[k], bg0 * gp0[k])) : 0.0f;
     lmax = imax(lmax, last[k]);
   }
   const int max_lc = __builtin_amdgcn_readfirstlane(wave_max_i32(lmax));
@@ -837,7 +851,11 @@ struct ShStage {
   int lane, w0, nvalid;  // w0: the wave's first Gaussian; nvalid: its Gaussians below P
 };
 
-// The wave's coefficient blocks into its LDS rows.
+// The wave's coefficient blocks into its LDS rows.  Each block's load is
+// followed by its guarded LDS store, so the wave waits for the loads one at a
+// time; issuing all twelve before the first store (clamped addresses,
+// unguarded stores) measured slower at configs 2 and 3, the kernel's other
+// loads then queueing behind 12 KB per wave.
 __device__ __forceinline__ void sh_stage_in(const ShStage& st, const float* shs) {
   const float4* src = reinterpret_cast<const float4*>(shs) + (size_t)st.w0 * 12;
 #pragma unroll
@@ -1026,10 +1044,43 @@ __device__ __forceinline__ void preprocess_bwd_one(const PreprocessBwdParams& p,
   // the reference's per-pixel terms (backward_kernels.py:678-685) summed.
   // A Gaussian that was never rendered has zero moments (its record is not
   // read).
+  // Every per-Gaussian word that a rendered Gaussian needs is loaded here,
+  // together, so that the wave waits for memory once rather than once per
+  // use below.
+  const bool precomp = p.cov3d != nullptr;
+  float4 r0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r1 = r0, q_in = r0;
+  float ax_in = 0.0f, ay_in = 0.0f, uc_in0 = 0.0f, uc_in1 = 0.0f, uc_in2 = 0.0f;
+  float ci_in0 = 0.0f, ci_in1 = 0.0f, ci_in2 = 0.0f;
+  float cv_in[6] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  if (rad > 0) {
+    r0 = p.records[3 * (size_t)tid];
+    r1 = p.records[3 * (size_t)tid + 1];
+    if (p.grad_proj_2d) {
+      ax_in = p.grad_proj_2d[2 * tid + 0];
+      ay_in = p.grad_proj_2d[2 * tid + 1];
+    }
+    if (precomp) {
+#pragma unroll
+      for (int k = 0; k < 6; ++k) cv_in[k] = p.cov3d[6 * (size_t)tid + k];
+    } else {
+      cv_in[0] = p.scales[3 * tid + 0];
+      cv_in[1] = p.scales[3 * tid + 1];
+      cv_in[2] = p.scales[3 * tid + 2];
+      q_in = reinterpret_cast<const float4*>(p.rotations)[tid];
+    }
+    if (p.grad_conic_2d) {
+      uc_in0 = p.grad_conic_2d[3 * tid + 0];
+      uc_in1 = p.grad_conic_2d[3 * tid + 1];
+      uc_in2 = p.grad_conic_2d[3 * tid + 2];
+    }
+    if (p.grad_conic_2d_inv) {
+      ci_in0 = p.grad_conic_2d_inv[3 * tid + 0];
+      ci_in1 = p.grad_conic_2d_inv[3 * tid + 1];
+      ci_in2 = p.grad_conic_2d_inv[3 * tid + 2];
+    }
+  }
   float rpx = 0.0f, rpy = 0.0f, rc0 = 0.0f, rc1 = 0.0f, rc2 = 0.0f;
   if (rad > 0) {
-    const float4 r0 = p.records[3 * (size_t)tid];
-    const float4 r1 = p.records[3 * (size_t)tid + 1];
     const float o = r1.y;
     rpx = -p.half_w * (o * (r0.z * gg[0] + r0.w * gg[1]));
     rpy = -p.half_h * (o * (r1.x * gg[1] + r0.w * gg[0]));
@@ -1051,8 +1102,8 @@ __device__ __forceinline__ void preprocess_bwd_one(const PreprocessBwdParams& p,
   const float inv_w2 = inv_w * inv_w;
   if (rad > 0) {
     // absent upstream gradients (null) are zero
-    float ax = p.grad_proj_2d ? p.grad_proj_2d[2 * tid + 0] : 0.0f;
-    float ay = p.grad_proj_2d ? p.grad_proj_2d[2 * tid + 1] : 0.0f;
+    float ax = ax_in;
+    float ay = ay_in;
     if (p.flow_double) {
       ax = ax + rpx;
       ay = ay + rpy;
@@ -1101,7 +1152,6 @@ __device__ __forceinline__ void preprocess_bwd_one(const PreprocessBwdParams& p,
     const float t11 = w11 * j11 + w12 * j12;
     const float t21 = w21 * j11 + w22 * j12;
 
-    const bool precomp = p.cov3d != nullptr;
     float ss0 = 0.0f, ss1 = 0.0f, ss2 = 0.0f, rr = 0.0f, xq = 0.0f, yq = 0.0f, zq = 0.0f;
     float r00 = 0.0f, r01 = 0.0f, r02 = 0.0f, r10 = 0.0f, r11 = 0.0f, r12 = 0.0f, r20 = 0.0f, r21 = 0.0f,
           r22 = 0.0f;
@@ -1109,14 +1159,12 @@ __device__ __forceinline__ void preprocess_bwd_one(const PreprocessBwdParams& p,
           mm22 = 0.0f;
     float v00, v01, v02, v11, v12, v22;
     if (precomp) {
-      const float* cv = p.cov3d + 6 * (size_t)tid;
-      v00 = cv[0]; v01 = cv[1]; v02 = cv[2]; v11 = cv[3]; v12 = cv[4]; v22 = cv[5];
+      v00 = cv_in[0]; v01 = cv_in[1]; v02 = cv_in[2]; v11 = cv_in[3]; v12 = cv_in[4]; v22 = cv_in[5];
     } else {
-      ss0 = p.scales[3 * tid + 0] * p.scale_modifier;
-      ss1 = p.scales[3 * tid + 1] * p.scale_modifier;
-      ss2 = p.scales[3 * tid + 2] * p.scale_modifier;
-      const float4 q = reinterpret_cast<const float4*>(p.rotations)[tid];
-      rr = q.x; xq = q.y; yq = q.z; zq = q.w;
+      ss0 = cv_in[0] * p.scale_modifier;
+      ss1 = cv_in[1] * p.scale_modifier;
+      ss2 = cv_in[2] * p.scale_modifier;
+      rr = q_in.x; xq = q_in.y; yq = q_in.z; zq = q_in.w;
       r00 = 1.0f - 2.0f * (yq * yq + zq * zq);
       r01 = 2.0f * (xq * yq + rr * zq);
       r02 = 2.0f * (xq * zq - rr * yq);
@@ -1150,9 +1198,9 @@ __device__ __forceinline__ void preprocess_bwd_one(const PreprocessBwdParams& p,
     const float denom = aa * cc - bb * bb;
     const float denom2inv = 1.0f / (denom * denom + 1.0e-7f);
 
-    float uc0 = p.grad_conic_2d ? p.grad_conic_2d[3 * tid + 0] : 0.0f;
-    float uc1 = p.grad_conic_2d ? p.grad_conic_2d[3 * tid + 1] : 0.0f;
-    float uc2 = p.grad_conic_2d ? p.grad_conic_2d[3 * tid + 2] : 0.0f;
+    float uc0 = uc_in0;
+    float uc1 = uc_in1;
+    float uc2 = uc_in2;
     if (p.flow_double) {
       uc0 = uc0 + rc0;
       uc1 = uc1 + rc1;
@@ -1165,9 +1213,9 @@ __device__ __forceinline__ void preprocess_bwd_one(const PreprocessBwdParams& p,
     float dL_dc = denom2inv * (-aa * aa * tc2 + 2.0f * aa * bb * tc1 - bb * bb * tc0);
     float dL_db = denom2inv * 2.0f * (bb * cc * tc0 - (aa * cc + bb * bb) * tc1 + aa * bb * tc2);
     if (p.grad_conic_2d_inv) {
-      dL_da = dL_da + p.grad_conic_2d_inv[3 * tid + 0];
-      dL_db = dL_db + p.grad_conic_2d_inv[3 * tid + 1];
-      dL_dc = dL_dc + p.grad_conic_2d_inv[3 * tid + 2];
+      dL_da = dL_da + ci_in0;
+      dL_db = dL_db + ci_in1;
+      dL_dc = dL_dc + ci_in2;
     }
 
     const float gc0 = t00 * t00 * dL_da + t00 * t01 * dL_db + t01 * t01 * dL_dc;

@@ -942,7 +942,15 @@ __global__ __launch_bounds__(256) void duplicate_keys_kernel(int P, const int* _
     if (depth_bits + value_bits + tile_bits > 64) limit = 0;
   }
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  const int radius = idx < P ? radii[idx] : 0;
+  // The Gaussian's radius, offsets and cover word are loaded together (index
+  // clamped, no branch between them), so the wave waits for memory once
+  // before the cover word decides which further words it needs.
+  const int ic = imin(idx, P - 1);
+  const int radius_in = radii[ic];
+  const int off_prev = offsets[imax(ic - 1, 0)];
+  const int off_cur = offsets[ic];
+  const int4 cover_in = coverage ? coverage[ic] : make_int4(0, 0, 0, 0);
+  const int radius = idx < P ? radius_in : 0;
   const bool active = radius > 0;
   long long off = 0;
   int count = 0;
@@ -951,9 +959,9 @@ __global__ __launch_bounds__(256) void duplicate_keys_kernel(int P, const int* _
   int4 cover_w = make_int4(0, 0, 0, 0);
   unsigned long long field = 0;
   if (active) {
-    off = idx > 0 ? (long long)offsets[idx - 1] : 0;
-    count = (int)((long long)offsets[idx] - off);
-    if (coverage) cover_w = coverage[idx];
+    off = idx > 0 ? (long long)off_prev : 0;
+    count = (int)((long long)off_cur - off);
+    cover_w = cover_in;
     float depth;
     if (!unpack_cover(cover_w).has_mask) {
       r0 = records[3 * (size_t)idx + 0];

@@ -409,12 +409,12 @@ __global__ __launch_bounds__(1024) void tile_order_kernel(int T, const int2* __r
   __shared__ __align__(16) int s_count[256];
   const int t0 = threadIdx.x;
   if (t0 < 256) s_count[t0] = 0;
+  int2 rr[kOrderRegTiles];
   int cls[kOrderRegTiles];
 #pragma unroll
-  for (int i = 0; i < kOrderRegTiles; ++i) {
-    const int t = t0 + 1024 * i;
-    cls[i] = t < T ? tile_length_class(ranges[t]) : 0;
-  }
+  for (int i = 0; i < kOrderRegTiles; ++i) rr[i] = ranges[imin(t0 + 1024 * i, T - 1)];
+#pragma unroll
+  for (int i = 0; i < kOrderRegTiles; ++i) cls[i] = tile_length_class(rr[i]);
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < kOrderRegTiles; ++i)
