@@ -12,8 +12,8 @@
 //   2. level 1, super-tiles (8 x 8 tiles): each Gaussian, in depth order,
 //      yields one entry per super-tile its tile rectangle meets, holding the
 //      point index and the 64-bit mask of the tiles it covers there;
-//      a stable partition (a counting pass per chunk of 1024 Gaussians, a
-//      scan, and a ranking pass) lists every super-tile's entries in depth
+//      a stable partition (a counting pass per chunk of kL1Chunk Gaussians,
+//      a scan, and a ranking pass) lists every super-tile's entries in depth
 //      order;
 //   3. level 2, tiles: per chunk of 1024 entries of one super-tile list, the
 //      number of entries covering each of its 64 tiles, a prefix over the
@@ -35,7 +35,7 @@
 
 namespace gs {
 
-constexpr int kL1Chunk = 128;            // depth positions per level-1 workgroup (one wave, 2 groups of 64)
+constexpr int kL1Chunk = 256;            // depth positions per level-1 workgroup (one wave, 4 groups of 64)
 constexpr int kL1Groups = kL1Chunk / 64;
 constexpr int kL2Chunk = 1024;           // entries per level-2 workgroup (one wave)
 constexpr int kStageRing = 32;           // level-2 staged pairs per tile (two flush blocks of 16)
