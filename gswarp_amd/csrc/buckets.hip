@@ -38,7 +38,8 @@ namespace gs {
 constexpr int kL1Chunk = 256;            // depth positions per level-1 workgroup (one wave, 4 groups of 64)
 constexpr int kL1Groups = kL1Chunk / 64;
 constexpr int kL2Chunk = 1024;           // entries per level-2 workgroup (one wave)
-constexpr int kStageRing = 32;           // level-2 staged pairs per tile (two flush blocks of 16)
+constexpr int kFlushPairs = 16;          // level-2 pairs per tile written out at once (64 bytes)
+constexpr int kStageRing = 2 * kFlushPairs;  // level-2 staged pairs per tile (two flush blocks)
 constexpr int kMaxGridTiles = 255;       // cover words hold spans below 2^8: at most 32 x 32 super-tiles
 
 __global__ __launch_bounds__(256) void bucket_zero_kernel(int n, int* __restrict__ p) {
@@ -579,7 +580,7 @@ __global__ __launch_bounds__(64) void bucket_tile_scatter_kernel(const int4* __r
   const int before = cnt2[(size_t)g * 64 + lane];
   stage_chunk<true>(e0, n, lane, e_mask, e_idx, s_m, s_id);
   const long long out = tile_ok ? (long long)start + before : 0;
-  int head = (int)((16 - (out & 15)) & 15);  // pairs before the list's next 64-byte boundary
+  int head = (int)((kFlushPairs - (out & (kFlushPairs - 1))) & (kFlushPairs - 1));  // pairs before the next block boundary
   // staged pairs [flushed, staged) in ring slots modulo kStageRing
   int staged = 0, flushed = 0;
   int* ring = s_ring + lane;
@@ -614,11 +615,11 @@ __global__ __launch_bounds__(64) void bucket_tile_scatter_kernel(const int4* __r
       flushed += head;
       head = 0;
     }
-    if (head == 0 && staged - flushed >= 16) {
-      if (out + flushed + 16 <= R) {
+    if (head == 0 && staged - flushed >= kFlushPairs) {
+      if (out + flushed + kFlushPairs <= R) {
         int4_dw* dst = reinterpret_cast<int4_dw*>(point_list + out + flushed);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < kFlushPairs / 4; ++q) {
           int4_dw v;
           v.x = ring[((flushed + 4 * q) & (kStageRing - 1)) * 64];
           v.y = ring[((flushed + 4 * q + 1) & (kStageRing - 1)) * 64];
@@ -627,7 +628,7 @@ __global__ __launch_bounds__(64) void bucket_tile_scatter_kernel(const int4* __r
           dst[q] = v;
         }
       }
-      flushed += 16;
+      flushed += kFlushPairs;
     }
   }
   for (int q = flushed; q < staged; ++q)
