@@ -66,17 +66,23 @@ __global__ __launch_bounds__(256) void bucket_depth_keys_kernel(int P, const int
 // hist[bucket * nchunks + c], and stores its cover words and indices in
 // depth order for the ranking pass.  The chunk's indices are loaded in one
 // batch, then its cover words in one batch (addresses clamped, no branches).
+// A Gaussian's entries are the super-tiles of its super-rectangle, so the
+// chunk counts them as a 2D difference array over the (nsx + 1) x (nsy + 1)
+// corners (four LDS adds per Gaussian, whatever its size) and takes the
+// counts as the array's 2D prefix sums.
 __global__ __launch_bounds__(64) void bucket_count_kernel(int V, int first, int P, const int* __restrict__ order,
                                                          const int4* __restrict__ coverage,
                                                          int4* __restrict__ cw_sorted, int* __restrict__ idx_sorted,
-                                                         int nsx, int B, int nchunks, int* __restrict__ hist) {
-  extern __shared__ int h[];  // B counters
+                                                         int nsx, int nsy, int nchunks, int* __restrict__ hist) {
+  extern __shared__ int h[];  // (nsy + 1) x (nsx + 1) difference counters
   const int lane = threadIdx.x;
   const int c = blockIdx.x;
+  const int stride = nsx + 1;
+  const int nd = (nsy + 1) * stride;
   int idx[kL1Groups];
 #pragma unroll
   for (int g = 0; g < kL1Groups; ++g) idx[g] = order[first + imin(c * kL1Chunk + g * 64 + lane, V - 1)];
-  for (int b = lane; b < B; b += 64) h[b] = 0;
+  for (int b = lane; b < nd; b += 64) h[b] = 0;
   int4 cw[kL1Groups];
 #pragma unroll
   for (int g = 0; g < kL1Groups; ++g) cw[g] = coverage[(unsigned)idx[g] < (unsigned)P ? idx[g] : 0];
@@ -92,14 +98,35 @@ __global__ __launch_bounds__(64) void bucket_count_kernel(int V, int first, int 
       idx_sorted[j] = in ? idx[g] : 0;
     }
     const SuperRect r = super_rect(unpack_cover(w));
-    for (int sy = r.sy0; sy < r.sy0 + r.ny; ++sy)
-      for (int sx = r.sx0; sx < r.sx0 + r.nx; ++sx) {
-        const int b = sy * nsx + sx;
-        if (b < B) atomicAdd(&h[b], 1);
-      }
+    const int x0 = imin(r.sx0, nsx), x1 = imin(r.sx0 + r.nx, nsx);
+    const int y0 = imin(r.sy0, nsy), y1 = imin(r.sy0 + r.ny, nsy);
+    if (x1 > x0 && y1 > y0) {
+      atomicAdd(&h[y0 * stride + x0], 1);
+      atomicAdd(&h[y0 * stride + x1], -1);
+      atomicAdd(&h[y1 * stride + x0], -1);
+      atomicAdd(&h[y1 * stride + x1], 1);
+    }
   }
   __syncthreads();
-  for (int b = lane; b < B; b += 64) hist[(size_t)b * nchunks + c] = h[b];
+  // prefix sums down the columns, then along the rows
+  for (int x = lane; x <= nsx; x += 64) {
+    int run = 0;
+    for (int y = 0; y <= nsy; ++y) {
+      run += h[y * stride + x];
+      h[y * stride + x] = run;
+    }
+  }
+  __syncthreads();
+  for (int y = lane; y <= nsy; y += 64) {
+    int run = 0;
+    for (int x = 0; x <= nsx; ++x) {
+      run += h[y * stride + x];
+      h[y * stride + x] = run;
+    }
+  }
+  __syncthreads();
+  const int B = nsx * nsy;
+  for (int b = lane; b < B; b += 64) hist[(size_t)b * nchunks + c] = h[(b / nsx) * stride + b % nsx];
 }
 
 // The clipped extent of a cover word's rectangle in super-tile (sx, sy):
@@ -350,7 +377,9 @@ __global__ __launch_bounds__(64) void bucket_scatter_kernel(int V, const int4* _
       const int ux = u - uy * r.nx;
       const int sx = r.sx0 + ux, sy = r.sy0 + uy;
       const int bucket = in_owner ? sy * nsx + sx : 0;
-      const bool live = in_owner && ux >= 0 && ux < r.nx && bucket >= 0 && bucket < B;
+      // (a rectangle inside the grid, as the preprocess writes them, meets only
+      // super-tiles with sx < nsx; the counts clip likewise)
+      const bool live = in_owner && ux >= 0 && ux < r.nx && sx < nsx && bucket >= 0 && bucket < B;
       const bool banded = w.valid && !w.has_mask && !w.full;
       // a banded Gaussian's words in this segment's buffer (kept in bounds
       // whatever the word says); other kinds read any words and ignore them
@@ -767,8 +796,9 @@ extern "C" int gs_bin_buckets(int32_t P, int32_t num_valid, int64_t num_entries,
   // 2. level 1: entries per super-tile in depth order
   const int nh = L.B * L.nchunks;
   const size_t lds_b = (size_t)L.B * sizeof(int);
-  hipLaunchKernelGGL(gs::bucket_count_kernel, dim3(L.nchunks), dim3(64), lds_b, s, V, first, P, order, cw,
-                     cw_sorted, idx_sorted, L.nsx, L.B, L.nchunks, hist);
+  const size_t lds_d = (size_t)(L.nsx + 1) * (L.nsy + 1) * sizeof(int);
+  hipLaunchKernelGGL(gs::bucket_count_kernel, dim3(L.nchunks), dim3(64), lds_d, s, V, first, P, order, cw,
+                     cw_sorted, idx_sorted, L.nsx, L.nsy, L.nchunks, hist);
   st = gs_scan_tiles(nh, hist, nullptr, nullptr, nullptr, hist_incl, info, ws + L.off_scan,
                      L.off_info - L.off_scan, stream);
   if (st != GS_OK) return st;
