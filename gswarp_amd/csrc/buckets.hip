@@ -126,7 +126,36 @@ __global__ __launch_bounds__(64) void bucket_count_kernel(int V, int first, int 
   }
   __syncthreads();
   const int B = nsx * nsy;
-  for (int b = lane; b < B; b += 64) hist[(size_t)b * nchunks + c] = h[(b / nsx) * stride + b % nsx];
+  for (int b = lane; b < B; b += 64) hist[(size_t)c * B + b] = h[(b / nsx) * stride + b % nsx];
+}
+
+// Transpose of an int matrix through LDS, 64 x 64 elements per workgroup:
+// out[c * rows + r] = flat[r * cols + c - shift] of the rows x cols input
+// (0 where that index is negative), so that both sides are read and written
+// in contiguous runs.  With shift 1 it turns an inclusive prefix into the
+// exclusive one of the transposed layout.
+__global__ __launch_bounds__(256) void bucket_transpose_kernel(const int* __restrict__ in, int rows, int cols,
+                                                              int shift, int* __restrict__ out) {
+  __shared__ int t[64][65];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  int v[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int r = r0 + ty + 4 * k, c = c0 + tx;
+    const long long f = (long long)r * cols + c - shift;
+    const bool ok = r < rows && c < cols && f >= 0;
+    v[k] = in[ok ? f : 0];
+    v[k] = ok ? v[k] : 0;
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) t[ty + 4 * k][tx] = v[k];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int c = c0 + ty + 4 * k, r = r0 + tx;
+    if (c < cols && r < rows) out[(size_t)c * rows + r] = t[tx][ty + 4 * k];
+  }
 }
 
 // The clipped extent of a cover word's rectangle in super-tile (sx, sy):
@@ -236,7 +265,7 @@ __global__ __launch_bounds__(64) void bucket_scatter_kernel(int V, const int4* _
                                                            const int* __restrict__ idx_sorted,
                                                            const unsigned* __restrict__ band_store,
                                                            const float4* __restrict__ records,
-                                                           const int* __restrict__ hist_incl, int nchunks, int nsx,
+                                                           const int* __restrict__ pos_cm, int nchunks, int nsx,
                                                            int B, int bucket_bits, long long E,
                                                            int* __restrict__ e_idx,
                                                            unsigned long long* __restrict__ e_mask) {
@@ -266,11 +295,7 @@ __global__ __launch_bounds__(64) void bucket_scatter_kernel(int V, const int4* _
     for (int b0 = 0; b0 < B; b0 += 64 * kPosBatch) {
       int v[kPosBatch];
 #pragma unroll
-      for (int q = 0; q < kPosBatch; ++q) {
-        const long long f = (long long)imin(b0 + q * 64 + lane, B - 1) * nchunks + c;
-        v[q] = hist_incl[f > 0 ? f - 1 : 0];
-        v[q] = f > 0 ? v[q] : 0;
-      }
+      for (int q = 0; q < kPosBatch; ++q) v[q] = pos_cm[(size_t)c * B + imin(b0 + q * 64 + lane, B - 1)];
 #pragma unroll
       for (int q = 0; q < kPosBatch; ++q)
         if (b0 + q * 64 + lane < B) cnt[b0 + q * 64 + lane] = v[q];
@@ -675,7 +700,8 @@ namespace {
 
 struct BucketLayout {
   int grid_x, grid_y, num_tiles, nsx, nsy, B, nchunks, nc2_max;
-  size_t off_keys, off_vals, off_keys_alt, off_vals_alt, off_sort, off_cw, off_idx, off_hist, off_hist_incl, off_scan,
+  size_t off_keys, off_vals, off_keys_alt, off_vals_alt, off_sort, off_cw, off_idx, off_hist, off_hist_incl, off_pos,
+      off_scan,
       off_info, off_eidx, off_emask, off_list, off_chunk, off_cinfo, off_cnt2, off_tiles, total;
 };
 
@@ -707,6 +733,7 @@ int bucket_layout(int32_t P, int32_t V, int64_t E, int32_t W, int32_t H, BucketL
   L.off_idx = take((size_t)V * 4);
   L.off_hist = take(nh * 4);
   L.off_hist_incl = take(nh * 4);
+  L.off_pos = take(nh * 4);
   L.off_scan = take(gs_scan_scratch_bytes((int32_t)nh));
   L.off_info = take(4 * sizeof(int64_t));
   L.off_eidx = take((size_t)E * 4);
@@ -771,6 +798,7 @@ extern "C" int gs_bin_buckets(int32_t P, int32_t num_valid, int64_t num_entries,
   int* idx_sorted = reinterpret_cast<int*>(ws + L.off_idx);
   int* hist = reinterpret_cast<int*>(ws + L.off_hist);
   int* hist_incl = reinterpret_cast<int*>(ws + L.off_hist_incl);
+  int* pos_cm = reinterpret_cast<int*>(ws + L.off_pos);
   int64_t* info = reinterpret_cast<int64_t*>(ws + L.off_info);
   int* e_idx = reinterpret_cast<int*>(ws + L.off_eidx);
   unsigned long long* e_mask = reinterpret_cast<unsigned long long*>(ws + L.off_emask);
@@ -797,15 +825,22 @@ extern "C" int gs_bin_buckets(int32_t P, int32_t num_valid, int64_t num_entries,
   const int nh = L.B * L.nchunks;
   const size_t lds_b = (size_t)L.B * sizeof(int);
   const size_t lds_d = (size_t)(L.nsx + 1) * (L.nsy + 1) * sizeof(int);
+  // counts chunk-major (each chunk writes one contiguous row), transposed to
+  // super-tile-major for the scan, and the scanned positions transposed back
+  // so that each ranking chunk reads one contiguous row
   hipLaunchKernelGGL(gs::bucket_count_kernel, dim3(L.nchunks), dim3(64), lds_d, s, V, first, P, order, cw,
-                     cw_sorted, idx_sorted, L.nsx, L.nsy, L.nchunks, hist);
+                     cw_sorted, idx_sorted, L.nsx, L.nsy, L.nchunks, pos_cm);
+  hipLaunchKernelGGL(gs::bucket_transpose_kernel, dim3((L.B + 63) / 64, (L.nchunks + 63) / 64), dim3(256), 0, s,
+                     pos_cm, L.nchunks, L.B, 0, hist);
   st = gs_scan_tiles(nh, hist, nullptr, nullptr, nullptr, hist_incl, info, ws + L.off_scan,
                      L.off_info - L.off_scan, stream);
   if (st != GS_OK) return st;
+  hipLaunchKernelGGL(gs::bucket_transpose_kernel, dim3((L.nchunks + 63) / 64, (L.B + 63) / 64), dim3(256), 0, s,
+                     hist_incl, L.B, L.nchunks, 1, pos_cm);
   const int bucket_bits = gs_bit_length((long long)L.B - 1);
   hipLaunchKernelGGL(gs::bucket_scatter_kernel, dim3(L.nchunks), dim3(64), lds_b, s, V, cw_sorted, idx_sorted,
                      reinterpret_cast<const unsigned*>(band_store), reinterpret_cast<const float4*>(records),
-                     hist_incl, L.nchunks, L.nsx, L.B, bucket_bits, E, e_idx, e_mask);
+                     pos_cm, L.nchunks, L.nsx, L.B, bucket_bits, E, e_idx, e_mask);
   mark(2);
 
   // 3. level 2: per-tile lists
