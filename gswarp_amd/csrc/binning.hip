@@ -1605,7 +1605,7 @@ static int bin_packed_impl(int32_t P, const int32_t* radii, const float* records
                            int32_t depth_bits, int32_t value_bits, void* workspace, size_t workspace_bytes,
                            int32_t* ranges, int32_t* point_list, uint64_t* sorted_keys_out,
                            void* const* stage_events, void* stream, bool ranges_cleared,
-                           bool keys_emitted = false) {
+                           bool keys_emitted = false, int32_t* tile_order = nullptr) {
   if (P < 0 || num_rendered < 0 || image_width <= 0 || image_height <= 0 || value_bits < 1 || value_bits > 31 ||
       depth_bits < 0 || depth_bits > 32)
     return GS_ERR_INVALID_ARGUMENT;
@@ -1650,8 +1650,16 @@ static int bin_packed_impl(int32_t P, const int32_t* radii, const float* records
   st = tile_ranges_impl(num_rendered, keys, tile_shift, 0, num_tiles, ranges, nullptr, ranges_cleared, s);
   if (st != GS_OK) return st;
   mark(3);
-  st = gs_sort_tile_segments(num_rendered, keys, keys_alt, num_tiles, ranges, value_bits, depth_bits, value_bits,
-                             point_list, sorted_keys_out != nullptr, stream);
+  // With a tile order buffer (when the order pays) the tiles are ordered
+  // longest list first here, for the segment sort and then the render.
+  const bool ordered = tile_order != nullptr && gs::tile_order_pays(num_rendered, P, num_tiles);
+  if (ordered) {
+    st = gs_tile_order(num_tiles, ranges, tile_order, stream);
+    if (st != GS_OK) return st;
+  }
+  st = gs_sort_tile_segments_ordered(num_rendered, keys, keys_alt, num_tiles, ranges, value_bits, depth_bits,
+                                     value_bits, point_list, sorted_keys_out != nullptr,
+                                     ordered ? tile_order : nullptr, stream);
   if (st != GS_OK) return st;
   mark(4);
   if (sorted_keys_out) {
@@ -1754,15 +1762,17 @@ extern "C" int gs_readback_bin_packed(const int64_t* info_dev, int64_t* slot, in
   if (R <= 0 || R > 0x7fffffffLL || R > capacity) return GS_OK;
   if (tile_bits + depth_bits + value_bits > 64 || value_bits > 31) return GS_OK;
   if (max_pairs_per_point > 0 && R > (int64_t)max_pairs_per_point * P) return GS_OK;
+  // the render's tile order is written by the binning (before its segment sort)
+  int32_t* order = out_color ? tile_order : nullptr;
   st = bin_packed_impl(P, radii, records, conic_2d_inv, coverage, depths, offsets, image_width, image_height,
                        coverage_mode, R, depth_min, depth_bits, value_bits, workspace, workspace_bytes, ranges,
-                       point_list, nullptr, stage_events, stream, clear_first, emitted);
+                       point_list, nullptr, stage_events, stream, clear_first, emitted, order);
   if (st != GS_OK) return st;
   result[4] = 1;
   if (out_color) {
-    st = gs_render_fwd_clear(image_width, image_height, P, R, ranges, point_list, records, background,
-                             compute_depth, out_color, out_depth, out_alpha, n_contrib, grad_clear,
-                             grad_clear_floats, tile_order, stream);
+    st = gs_render_fwd_clear_ordered(image_width, image_height, P, R, ranges, point_list, records, background,
+                                     compute_depth, out_color, out_depth, out_alpha, n_contrib, grad_clear,
+                                     grad_clear_floats, order, true, stream);
     if (st != GS_OK) return st;
     if (stage_events) (void)hipEventRecord((hipEvent_t)stage_events[5], (hipStream_t)stream);
     result[5] = 1;

@@ -481,7 +481,8 @@ static int gs_render_fwd_common(int32_t W, int32_t H, int32_t num_points, int64_
                                 const float* background, int32_t compute_depth, int32_t write_aux, int32_t top_k,
                                 float* out_color, float* out_depth, float* out_alpha, int32_t* n_contrib,
                                 int32_t* gs_per_pixel, float* weight, float* x_mu, bool flow, void* stream,
-                                int32_t* tile_order, float* clear = nullptr, int64_t clear_floats = 0) {
+                                int32_t* tile_order, float* clear = nullptr, int64_t clear_floats = 0,
+                                bool order_ready = false) {
   if (W <= 0 || H <= 0 || (long long)W * H > 0x7fffffffLL) return GS_ERR_INVALID_ARGUMENT;
   if (clear_floats < 0 || (clear_floats > 0 && !clear)) return GS_ERR_INVALID_ARGUMENT;
   if (reinterpret_cast<uintptr_t>(clear) & 15) return GS_ERR_MISALIGNED;
@@ -517,8 +518,10 @@ static int gs_render_fwd_common(int32_t W, int32_t H, int32_t num_points, int64_
   p.masked = gs::tile_order_pays(num_rendered, num_points, p.num_tiles) ? 1 : 0;
   p.tile_order = nullptr;
   if (tile_order && gs::tile_order_pays(num_rendered, num_points, p.num_tiles)) {
-    const int st = gs_tile_order(p.num_tiles, ranges, tile_order, stream);
-    if (st != GS_OK) return st;
+    if (!order_ready) {
+      const int st = gs_tile_order(p.num_tiles, ranges, tile_order, stream);
+      if (st != GS_OK) return st;
+    }
     p.tile_order = tile_order;
   }
   return gs::launch_render_fwd(p, flow, (hipStream_t)stream);
@@ -549,6 +552,16 @@ extern "C" int gs_render_fwd_clear(int32_t image_width, int32_t image_height, in
   return gs_render_fwd_common(image_width, image_height, num_points, num_rendered, ranges, point_list, records,
                               background, compute_depth, 0, 0, out_color, out_depth, out_alpha, n_contrib, nullptr,
                               nullptr, nullptr, false, stream, tile_order, clear, clear_floats);
+}
+
+int gs_render_fwd_clear_ordered(int32_t image_width, int32_t image_height, int32_t num_points, int64_t num_rendered,
+                                const int32_t* ranges, const int32_t* point_list, const float* records,
+                                const float* background, int32_t compute_depth, float* out_color, float* out_depth,
+                                float* out_alpha, int32_t* n_contrib, float* clear, int64_t clear_floats,
+                                int32_t* tile_order, bool order_ready, void* stream) {
+  return gs_render_fwd_common(image_width, image_height, num_points, num_rendered, ranges, point_list, records,
+                              background, compute_depth, 0, 0, out_color, out_depth, out_alpha, n_contrib, nullptr,
+                              nullptr, nullptr, false, stream, tile_order, clear, clear_floats, order_ready);
 }
 
 extern "C" int gs_render_fwd_flow(int32_t image_width, int32_t image_height, int32_t num_points,

@@ -369,8 +369,9 @@ extern "C" int gs_sort_pairs_u32(int64_t n, int32_t lo_bit, int32_t key_bits, ui
 // back in place).
 //
 // Segments of up to kSmallCap keys are sorted by one wave each
-// (segment_sort_small_kernel); longer ones by a 256-thread workgroup
-// (segment_sort_kernel).  There, segments of up to kCap keys are sorted on
+// (small_segment_sort); longer ones by a 256-thread workgroup
+// (long_segment_sort), both in one launch (segment_sort_kernel).  There,
+// segments of up to kCap keys are sorted on
 // chip: each thread holds up to
 // kSlots keys in registers, ranks them with the same ballot-matched stable
 // ranking as the downsweep above, scatters them into one LDS buffer and
@@ -464,15 +465,19 @@ __device__ __forceinline__ unsigned wave_inclusive_scan_u32(unsigned x) {
   return x + (row >= 1 ? r0 : 0u) + (row >= 2 ? r1 : 0u) + (row >= 3 ? r2 : 0u);
 }
 
-__global__ __launch_bounds__(64) void segment_sort_small_kernel(long long n, u64* __restrict__ keys,
-                                                               const int2* __restrict__ ranges, int lo_bit,
-                                                               int key_bits, int value_bits,
-                                                               int* __restrict__ point_list, int write_keys) {
-  __shared__ u64 s_buf[kSmallCap];
-  __shared__ uint4 s_wc4[kSmallRadix / 4];
+// The wave's LDS for one short segment.
+struct SmallShared {
+  u64 buf[kSmallCap];
+  uint4 wc4[kSmallRadix / 4];
+};
+
+__device__ __forceinline__ void small_segment_sort(long long n, u64* __restrict__ keys, int2 rg, int lo_bit,
+                                                   int key_bits, int value_bits, int* __restrict__ point_list,
+                                                   int write_keys, SmallShared& sh) {
+  u64* const s_buf = sh.buf;
+  uint4* const s_wc4 = sh.wc4;
   unsigned* s_wc = reinterpret_cast<unsigned*>(s_wc4);
-  const int lane = threadIdx.x;
-  int2 rg = ranges[blockIdx.x];
+  const int lane = threadIdx.x & 63;
   const long long start = rg.x < 0 ? 0 : (rg.x > n ? n : rg.x);
   const long long end = rg.y < start ? start : (rg.y > n ? n : rg.y);
   const int cnt = (int)(end - start);
@@ -554,21 +559,16 @@ __global__ __launch_bounds__(64) void segment_sort_small_kernel(long long n, u64
   }
 }
 
-__global__ __launch_bounds__(kThreads) void segment_sort_kernel(long long n, u64* __restrict__ keys,
-                                                               u64* __restrict__ keys_alt, int num_tiles,
-                                                               const int2* __restrict__ ranges, int lo_bit,
-                                                               int key_bits, int value_bits,
-                                                               int* __restrict__ point_list, int write_keys) {
-  __shared__ Shared s;
+__device__ __forceinline__ void long_segment_sort(long long n, u64* __restrict__ keys, u64* __restrict__ keys_alt,
+                                                  int2 rg, int lo_bit, int key_bits, int value_bits,
+                                                  int* __restrict__ point_list, int write_keys, Shared& s) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int tile = blockIdx.x;
-  int2 rg = ranges[tile];
   const long long start = rg.x < 0 ? 0 : (rg.x > n ? n : rg.x);
   const long long end = rg.y < start ? start : (rg.y > n ? n : rg.y);
   const int cnt_all = (int)(end - start);
-  if (cnt_all <= kSmallCap) return;  // segment_sort_small_kernel's
+  if (cnt_all <= kSmallCap) return;  // small_segment_sort's
   const u64 vmask = (1ull << value_bits) - 1ull;
   const int passes = (key_bits + 7) / 8;
 
@@ -695,23 +695,65 @@ __global__ __launch_bounds__(kThreads) void segment_sort_kernel(long long n, u64
   }
 }
 
+// One launch for every segment.  The grid's first min(num_tiles,
+// kLongWorkgroups) workgroups take the segments longer than kSmallCap, one
+// 256-thread workgroup at a time, tiles b, b + kLongWorkgroups, ... (the
+// others are skipped at once), so that the long sorts start first and run
+// beside the short ones; the rest of the grid takes the short segments four
+// at a time, one wave each (its path has no workgroup barrier).  With an order
+// (longest list first) the long segments come first and a workgroup's four
+// short ones are of about one length, so its waves finish together.
+constexpr int kLongWorkgroups = 1024;
+
+__global__ __launch_bounds__(kThreads) void segment_sort_kernel(long long n, u64* __restrict__ keys,
+                                                               u64* __restrict__ keys_alt, int num_tiles,
+                                                               const int2* __restrict__ ranges, int lo_bit,
+                                                               int key_bits, int value_bits,
+                                                               int* __restrict__ point_list, int write_keys,
+                                                               const int* __restrict__ order) {
+  __shared__ union Lds {
+    Shared big;
+    SmallShared small[kWaves];
+  } lds;
+  const int long_wgs = min(num_tiles, kLongWorkgroups);
+  if ((int)blockIdx.x < long_wgs) {
+    for (int b = blockIdx.x; b < num_tiles; b += long_wgs) {
+      const int tile = order ? max(0, min(order[b], num_tiles - 1)) : b;
+      long_segment_sort(n, keys, keys_alt, ranges[tile], lo_bit, key_bits, value_bits, point_list, write_keys,
+                        lds.big);
+      __syncthreads();  // the next segment reuses the LDS
+    }
+    return;
+  }
+  const int wave = threadIdx.x >> 6;
+  const int slot = ((int)blockIdx.x - long_wgs) * kWaves + wave;
+  if (slot >= num_tiles) return;
+  const int tile = order ? max(0, min(order[slot], num_tiles - 1)) : slot;
+  small_segment_sort(n, keys, ranges[tile], lo_bit, key_bits, value_bits, point_list, write_keys, lds.small[wave]);
+}
+
 }  // namespace gs_seg
 
-extern "C" int gs_sort_tile_segments(int64_t n, uint64_t* keys, uint64_t* keys_alt, int32_t num_tiles,
-                                     const int32_t* ranges, int32_t lo_bit, int32_t key_bits, int32_t value_bits,
-                                     int32_t* point_list, int32_t write_keys, void* stream) {
+int gs_sort_tile_segments_ordered(int64_t n, uint64_t* keys, uint64_t* keys_alt, int32_t num_tiles,
+                                  const int32_t* ranges, int32_t lo_bit, int32_t key_bits, int32_t value_bits,
+                                  int32_t* point_list, int32_t write_keys, const int32_t* order, void* stream) {
   if (n < 0 || num_tiles < 0 || key_bits < 0 || value_bits < 1 || value_bits > 31 || lo_bit < value_bits ||
       lo_bit + key_bits > 64)
     return GS_ERR_INVALID_ARGUMENT;
   if (n > 0x7fffffffLL) return GS_ERR_OVERFLOW;
   if (n == 0 || num_tiles == 0) return GS_OK;
   if (!keys || !keys_alt || !ranges || !point_list) return GS_ERR_INVALID_ARGUMENT;
-  hipLaunchKernelGGL(gs_seg::segment_sort_small_kernel, dim3(num_tiles), dim3(64), 0, (hipStream_t)stream,
-                     (long long)n, reinterpret_cast<gs_sort::u64*>(keys), reinterpret_cast<const int2*>(ranges),
-                     lo_bit, key_bits, value_bits, point_list, write_keys);
-  hipLaunchKernelGGL(gs_seg::segment_sort_kernel, dim3(num_tiles), dim3(gs_seg::kThreads), 0, (hipStream_t)stream,
+  const int grid = std::min(num_tiles, gs_seg::kLongWorkgroups) + (num_tiles + gs_seg::kWaves - 1) / gs_seg::kWaves;
+  hipLaunchKernelGGL(gs_seg::segment_sort_kernel, dim3(grid), dim3(gs_seg::kThreads), 0, (hipStream_t)stream,
                      (long long)n, reinterpret_cast<gs_sort::u64*>(keys), reinterpret_cast<gs_sort::u64*>(keys_alt),
                      num_tiles, reinterpret_cast<const int2*>(ranges), lo_bit, key_bits, value_bits, point_list,
-                     write_keys);
+                     write_keys, order);
   return gs_status_from_hip(hipGetLastError());
+}
+
+extern "C" int gs_sort_tile_segments(int64_t n, uint64_t* keys, uint64_t* keys_alt, int32_t num_tiles,
+                                     const int32_t* ranges, int32_t lo_bit, int32_t key_bits, int32_t value_bits,
+                                     int32_t* point_list, int32_t write_keys, void* stream) {
+  return gs_sort_tile_segments_ordered(n, keys, keys_alt, num_tiles, ranges, lo_bit, key_bits, value_bits, point_list,
+                                       write_keys, nullptr, stream);
 }
