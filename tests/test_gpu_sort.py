@@ -156,6 +156,9 @@ SEGMENT_CASES = [
     ([500, 3000, 1], 0, 20, False, True),
     ([777, 2500, 64], 1, 31, True, True),
     ([1024, 6000, 2000], 32, 20, False, False),
+    # more long segments than the launch's 1024 long-segment workgroups, so
+    # that each takes several (some through the chunked global path)
+    ([1025 + 150 * (i % 7) for i in range(1100)] + [3000] * 30 + [100] * 50, 26, 20, False, True),
 ]
 
 
@@ -163,8 +166,9 @@ SEGMENT_CASES = [
 def test_tile_segment_sort_matches_full_key_sort(sizes, depth_bits, value_bits, dup, write_keys, device):
     """gs_sort_tile_segments on tile-grouped keys gives the full (tile, depth,
     point) key order: tiles empty, tiny, ragged, exactly at and above the
-    2048-key on-chip capacity (the chunked global path), partial last digits,
-    no depth bits, and duplicate-heavy depths (stability)."""
+    2048-key on-chip capacity (the chunked global path), more long tiles than
+    long-segment workgroups, partial last digits, no depth bits, and
+    duplicate-heavy depths (stability)."""
     lib = _lib.load()
     rng = np.random.default_rng(sum(sizes) * 7 + depth_bits)
     keys, ranges = _tile_sorted_keys(rng, sizes, depth_bits, value_bits, dup)
