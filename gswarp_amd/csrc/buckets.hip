@@ -244,8 +244,8 @@ __device__ __forceinline__ int table_floor(const int* t, int v) {
   return lo;
 }
 
-constexpr int kL1BandCap = 2048;   // band words of a level-1 chunk held in LDS
-constexpr int kL1OwnerCap = 2048;  // entries of a level-1 chunk whose Gaussian is looked up in a table
+constexpr int kL1BandCap = 1024;   // band words of a level-1 chunk held in LDS
+constexpr int kL1OwnerCap = 1024;  // entries of a level-1 chunk whose Gaussian is looked up in a table
 
 // Level-1 ranking.  Chunk c (kL1Chunk Gaussians in depth order) first loads
 // the Gaussians' cover words and indices and the chunk's running
