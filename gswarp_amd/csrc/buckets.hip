@@ -617,6 +617,7 @@ __global__ __launch_bounds__(64) void bucket_tile_scatter_kernel(const int4* __r
   __shared__ __align__(16) unsigned long long s_m[kL2Chunk];
   __shared__ __align__(16) int s_id[kL2Chunk];
   __shared__ int s_ring[kStageRing * 64];  // slot-major: slot q of tile k at q * 64 + k (conflict-free)
+  static_assert(kFlushPairs == 16, "four lanes of four pairs per block");
   const int g = blockIdx.x;
   const int lane = threadIdx.x;
   const int4 ci = chunk_info[g];
@@ -669,20 +670,40 @@ __global__ __launch_bounds__(64) void bucket_tile_scatter_kernel(const int4* __r
       flushed += head;
       head = 0;
     }
-    if (head == 0 && staged - flushed >= kFlushPairs) {
-      if (out + flushed + kFlushPairs <= R) {
-        int4_dw* dst = reinterpret_cast<int4_dw*>(point_list + out + flushed);
-#pragma unroll
-        for (int q = 0; q < kFlushPairs / 4; ++q) {
+    // Whole blocks, written four lanes to a block: each lane with a block to
+    // write sends its tile (lane), the block's ring slot and its start (-1
+    // past R) to the first lane of a quad (a forward lane permute, then a
+    // quad broadcast), and lane 4 j + h stores part h (one 16-byte store) of
+    // the j-th block, so that one store instruction writes sixteen blocks'
+    // 64-byte sectors whole.
+    const bool fl = head == 0 && staged - flushed >= kFlushPairs;
+    const uint64_t fmask = __ballot(fl);
+    if (fmask != 0) {
+      const int rank = (int)__builtin_amdgcn_mbcnt_hi((unsigned)(fmask >> 32),
+                                                      __builtin_amdgcn_mbcnt_lo((unsigned)fmask, 0u));
+      const int nfl = __popcll(fmask);
+      const int info_x = lane | ((flushed & (kStageRing - 1)) << 8);
+      const int info_y = out + flushed + kFlushPairs <= R ? (int)(out + flushed) : -1;
+      for (int p0 = 0; p0 < nfl; p0 += 16) {
+        // this pass's blocks go to lanes 0, 4, ..., 60; every other lane
+        // sends to lane 1, whose value no lane reads
+        const bool mine = fl && rank >= p0 && rank < p0 + 16;
+        const int to = (mine ? 4 * (rank - p0) : 1) * 4;
+        int x = __builtin_amdgcn_ds_permute(to, info_x);
+        int y = __builtin_amdgcn_ds_permute(to, info_y);
+        x = __builtin_amdgcn_update_dpp(0, x, 0x00, 0xF, 0xF, false);  // quad_perm [0,0,0,0]
+        y = __builtin_amdgcn_update_dpp(0, y, 0x00, 0xF, 0xF, false);
+        if (p0 + (lane >> 2) < nfl) {
+          const int t = x & 63, slot = (x >> 8) + 4 * (lane & 3);
           int4_dw v;
-          v.x = ring[((flushed + 4 * q) & (kStageRing - 1)) * 64];
-          v.y = ring[((flushed + 4 * q + 1) & (kStageRing - 1)) * 64];
-          v.z = ring[((flushed + 4 * q + 2) & (kStageRing - 1)) * 64];
-          v.w = ring[((flushed + 4 * q + 3) & (kStageRing - 1)) * 64];
-          dst[q] = v;
+          v.x = s_ring[(slot & (kStageRing - 1)) * 64 + t];
+          v.y = s_ring[((slot + 1) & (kStageRing - 1)) * 64 + t];
+          v.z = s_ring[((slot + 2) & (kStageRing - 1)) * 64 + t];
+          v.w = s_ring[((slot + 3) & (kStageRing - 1)) * 64 + t];
+          if (y >= 0) *reinterpret_cast<int4_dw*>(point_list + y + 4 * (lane & 3)) = v;
         }
       }
-      flushed += kFlushPairs;
+      if (fl) flushed += kFlushPairs;
     }
   }
   for (int q = flushed; q < staged; ++q)
