@@ -123,8 +123,10 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p)
   static_assert(kScanAggGaussians == 256, "one workgroup's Gaussians per scan aggregate");
   __shared__ CoverCountLds s_cover[256 / 64];
   __shared__ ScanAggLds s_agg;
+  __shared__ float4 s_rec[256 / 64][3 * 64];  // each wave's records, written out whole-wave
   const int idx0 = blockIdx.x * blockDim.x + threadIdx.x;
   const bool in_range = idx0 < p.P;
+  bool rec_written = false;
   const int idx = in_range ? idx0 : p.P - 1;  // loads stay in bounds; nothing is stored for it
   // the next stage's one-pass scan starts from cleared status words (fewer
   // than this grid's threads)
@@ -285,14 +287,31 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(PreprocessParams p)
           if (col.y < 0.0f) { col.y = 0.0f; clamp_bits |= 2; }
           if (col.z < 0.0f) { col.z = 0.0f; clamp_bits |= 4; }
         }
-        float4* rec = p.records + 3 * (size_t)idx;
+        float4* rec = s_rec[threadIdx.x >> 6] + 3 * (threadIdx.x & 63);
         const float4 w0 = make_float4(ptx, pty, q0, q1);
         const float4 w1 = make_float4(q2, op, p_view_z, quad_cutoff(op));
         rec[0] = w0;
         rec[1] = w1;
         rec[2] = make_float4(col.x, col.y, col.z, __uint_as_float(record_extents(w0, w1)));
+        rec_written = in_range;
         if (p.clamped != nullptr) p.clamped[idx] = clamp_bits;
       }
+    }
+  }
+  {
+    // The wave's records go out as three whole-wave stores of consecutive
+    // float4 (lane l stores float4 64 q + l of the wave's 3 x 64, if its
+    // Gaussian wrote a record), not as three 48-byte-strided stores per lane:
+    // a third of the address-unit work.  The wave's LDS accesses complete in
+    // order.
+    const uint64_t written = __ballot(rec_written);
+    __builtin_amdgcn_wave_barrier();
+    const float4* rw = s_rec[threadIdx.x >> 6];
+    float4* out = p.records + 3 * (size_t)(idx0 - (threadIdx.x & 63));
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const int f = 64 * q + (threadIdx.x & 63);
+      if ((written >> (f / 3)) & 1) out[f] = rw[f];
     }
   }
   TileCover cover;
