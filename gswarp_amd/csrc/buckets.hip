@@ -41,6 +41,7 @@ constexpr int kL2Chunk = 1024;           // entries per level-2 workgroup (one w
 constexpr int kFlushPairs = 16;          // level-2 pairs per tile written out at once (64 bytes)
 constexpr int kStageRing = 2 * kFlushPairs;  // level-2 staged pairs per tile (two flush blocks)
 constexpr int kMaxGridTiles = 255;       // cover words hold spans below 2^8: at most 32 x 32 super-tiles
+constexpr int kMaxSuper = 32 * 32;       // super-tiles at most (kMaxGridTiles tiles a side)
 
 __global__ __launch_bounds__(256) void bucket_zero_kernel(int n, int* __restrict__ p) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -432,45 +433,68 @@ __global__ __launch_bounds__(64) void bucket_scatter_kernel(int V, const int4* _
 // chunk_start[s + 1]); chunk_start[B] is the number of level-2 chunks.  Each
 // chunk g < nc2_max gets chunk_info[g] = (s, first entry, end entry), or
 // (-1, 0, 0) past the last chunk, so that a chunk's wave finds its entries
-// with one load.
+// with one load.  Every workgroup scans the super-tiles itself (at most
+// kMaxSuper, four per thread) and fills 256 chunks, each finding its
+// super-tile by binary search; workgroup 0 also writes the two tables.
 __global__ __launch_bounds__(256) void bucket_table_kernel(const int* __restrict__ hist_incl, int nchunks, int B,
                                                           int nc2_max, int* __restrict__ list_start,
                                                           int* __restrict__ chunk_start,
                                                           int4* __restrict__ chunk_info) {
+  constexpr int kPer = kMaxSuper / 256;
+  __shared__ int s_ls[kMaxSuper + 1], s_cs[kMaxSuper + 1];
   __shared__ int s_tot[256 / 64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int start[kPer], end[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int s = k * 256 + threadIdx.x;
+    start[k] = s > 0 && s < B ? hist_incl[(size_t)s * nchunks - 1] : 0;
+    end[k] = s < B ? hist_incl[(size_t)(s + 1) * nchunks - 1] : 0;
+  }
   int carry = 0;
-  for (int s0 = 0; s0 < B; s0 += 256) {
-    const int s = s0 + threadIdx.x;
-    int nch = 0, start = 0, end = 0;
-    if (s < B) {
-      start = s > 0 ? hist_incl[(size_t)s * nchunks - 1] : 0;
-      end = hist_incl[(size_t)(s + 1) * nchunks - 1];
-      list_start[s] = start;
-      if (s == B - 1) list_start[B] = end;
-      nch = (end - start + kL2Chunk - 1) / kL2Chunk;
-    }
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    if (k * 256 >= B) break;
+    const int s = k * 256 + threadIdx.x;
+    const int nch = s < B ? (end[k] - start[k] + kL2Chunk - 1) / kL2Chunk : 0;
     const int incl = wave_inclusive_scan_i32(nch);
     if (lane == 63) s_tot[wave] = incl;
     __syncthreads();
     int before = 0, all = 0;
-    for (int k = 0; k < 256 / 64; ++k) {
-      before += k < wave ? s_tot[k] : 0;
-      all += s_tot[k];
+    for (int w = 0; w < 256 / 64; ++w) {
+      before += w < wave ? s_tot[w] : 0;
+      all += s_tot[w];
     }
     if (s < B) {
-      const int first = carry + before + incl - nch;
-      chunk_start[s] = first;
-      for (int k = 0; k < nch && first + k < nc2_max; ++k) {
-        const int e0 = start + k * kL2Chunk;
-        chunk_info[first + k] = make_int4(s, e0, imin(e0 + kL2Chunk, end), 0);
-      }
+      s_ls[s] = start[k];
+      s_cs[s] = carry + before + incl - nch;
+      if (s == B - 1) s_ls[B] = end[k];
     }
     carry += all;
     __syncthreads();
   }
-  if (threadIdx.x == 0) chunk_start[B] = carry;
-  for (int g = carry + threadIdx.x; g < nc2_max; g += 256) chunk_info[g] = make_int4(-1, 0, 0, 0);
+  if (threadIdx.x == 0) s_cs[B] = carry;
+  __syncthreads();
+  if (blockIdx.x == 0) {
+    for (int s = threadIdx.x; s <= B; s += 256) {
+      list_start[s] = s_ls[s];
+      chunk_start[s] = s_cs[s];
+    }
+  }
+  const int g = blockIdx.x * 256 + threadIdx.x;
+  if (g >= nc2_max) return;
+  if (g >= carry) {
+    chunk_info[g] = make_int4(-1, 0, 0, 0);
+    return;
+  }
+  int lo = 0, hi = B - 1;  // the last super-tile whose chunks start at or before g
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_cs[mid] <= g) lo = mid;
+    else hi = mid - 1;
+  }
+  const int e0 = s_ls[lo] + (g - s_cs[lo]) * kL2Chunk;
+  chunk_info[g] = make_int4(lo, e0, imin(e0 + kL2Chunk, s_ls[lo + 1]), 0);
 }
 
 // Whether tile lane (bit `lane` of the super-tile's masks) is set in m: the
@@ -544,22 +568,40 @@ __global__ __launch_bounds__(64) void bucket_tile_count_kernel(const int4* __res
 }
 
 // Per super-tile: each chunk's count becomes its exclusive prefix over the
-// super-tile's chunks, and the totals are the tiles' pair counts.
-__global__ __launch_bounds__(64) void bucket_tile_prefix_kernel(const int* __restrict__ chunk_start, int nsx,
-                                                               int grid_x, int grid_y, int nc2,
-                                                               int* __restrict__ cnt2, int* __restrict__ tile_count) {
+// super-tile's chunks, and the totals are the tiles' pair counts.  The
+// super-tile's chunks are split into 16 consecutive runs, one per wave: each
+// wave sums its run, the waves' sums are scanned in LDS, and each wave walks
+// its run again writing the prefixes (a sixteenth of the serial walk).
+__global__ __launch_bounds__(1024) void bucket_tile_prefix_kernel(const int* __restrict__ chunk_start, int nsx,
+                                                                 int grid_x, int grid_y, int nc2,
+                                                                 int* __restrict__ cnt2, int* __restrict__ tile_count) {
+  constexpr int kWaves = 1024 / 64;
   constexpr int kBatch = 16;  // chunks whose counts are loaded together
+  __shared__ int s_tot[kWaves][64];
   const int s = blockIdx.x;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g0 = chunk_start[s], g1 = imin(chunk_start[s + 1], nc2);
-  int run = 0;
-  for (int g = g0; g < g1; g += kBatch) {
+  const int per = imax(g1 - g0 + kWaves - 1, 0) / kWaves;
+  const int a = g0 + wave * per, b = imin(a + per, g1);
+  int sum = 0;
+  for (int g = a; g < b; g += kBatch) {
     int v[kBatch];
 #pragma unroll
-    for (int q = 0; q < kBatch; ++q) v[q] = cnt2[(size_t)imin(g + q, g1 - 1) * 64 + lane];
+    for (int q = 0; q < kBatch; ++q) v[q] = cnt2[(size_t)imin(g + q, b - 1) * 64 + lane];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) sum += g + q < b ? v[q] : 0;
+  }
+  s_tot[wave][lane] = sum;
+  __syncthreads();
+  int run = 0;
+  for (int w = 0; w < wave; ++w) run += s_tot[w][lane];
+  for (int g = a; g < b; g += kBatch) {
+    int v[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) v[q] = cnt2[(size_t)imin(g + q, b - 1) * 64 + lane];
 #pragma unroll
     for (int q = 0; q < kBatch; ++q) {
-      if (g + q < g1) {
+      if (g + q < b) {
         cnt2[(size_t)(g + q) * 64 + lane] = run;
         run += v[q];
       }
@@ -567,32 +609,43 @@ __global__ __launch_bounds__(64) void bucket_tile_prefix_kernel(const int* __res
   }
   const int tx = (s % nsx) * kSuperTile + (lane & 7);
   const int ty = (s / nsx) * kSuperTile + (lane >> 3);
-  if (tx < grid_x && ty < grid_y) tile_count[ty * grid_x + tx] = run;
+  if (wave == kWaves - 1 && tx < grid_x && ty < grid_y) tile_count[ty * grid_x + tx] = run;
 }
 
 // Tile ranges from the tile counts in tile order (one workgroup): [start,
 // start + count) for a tile with pairs, [0, 0] for an empty one (the
-// reference's cleared ranges).
+// reference's cleared ranges).  Eight rounds of 1024 tiles are loaded
+// together, then scanned round by round.
 __global__ __launch_bounds__(1024) void bucket_ranges_kernel(int T, const int* __restrict__ tile_count,
                                                             int2* __restrict__ ranges) {
+  constexpr int kRounds = 8;
   __shared__ int s_tot[1024 / 64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int carry = 0;
-  for (int t0 = 0; t0 < T; t0 += 1024) {
-    const int t = t0 + threadIdx.x;
-    const int v = t < T ? tile_count[t] : 0;
-    const int incl = wave_inclusive_scan_i32(v);
-    if (lane == 63) s_tot[wave] = incl;
-    __syncthreads();
-    int before = 0, all = 0;
-    for (int k = 0; k < 1024 / 64; ++k) {
-      before += k < wave ? s_tot[k] : 0;
-      all += s_tot[k];
+  for (int t0 = 0; t0 < T; t0 += 1024 * kRounds) {
+    int v[kRounds];
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      const int t = t0 + r * 1024 + threadIdx.x;
+      v[r] = t < T ? tile_count[t] : 0;
     }
-    const int start = carry + before + incl - v;
-    if (t < T) ranges[t] = v > 0 ? make_int2(start, start + v) : make_int2(0, 0);
-    carry += all;
-    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      if (t0 + r * 1024 >= T) break;
+      const int t = t0 + r * 1024 + threadIdx.x;
+      const int incl = wave_inclusive_scan_i32(v[r]);
+      if (lane == 63) s_tot[wave] = incl;
+      __syncthreads();
+      int before = 0, all = 0;
+      for (int k = 0; k < 1024 / 64; ++k) {
+        before += k < wave ? s_tot[k] : 0;
+        all += s_tot[k];
+      }
+      const int start = carry + before + incl - v[r];
+      if (t < T) ranges[t] = v[r] > 0 ? make_int2(start, start + v[r]) : make_int2(0, 0);
+      carry += all;
+      __syncthreads();
+    }
   }
 }
 
@@ -865,10 +918,10 @@ extern "C" int gs_bin_buckets(int32_t P, int32_t num_valid, int64_t num_entries,
   mark(2);
 
   // 3. level 2: per-tile lists
-  hipLaunchKernelGGL(gs::bucket_table_kernel, dim3(1), dim3(256), 0, s, hist_incl, L.nchunks, L.B, L.nc2_max,
-                     list_start, chunk_start, chunk_info);
+  hipLaunchKernelGGL(gs::bucket_table_kernel, dim3((L.nc2_max + 255) / 256), dim3(256), 0, s, hist_incl, L.nchunks,
+                     L.B, L.nc2_max, list_start, chunk_start, chunk_info);
   hipLaunchKernelGGL(gs::bucket_tile_count_kernel, dim3(L.nc2_max), dim3(64), 0, s, chunk_info, (int)E, e_mask, cnt2);
-  hipLaunchKernelGGL(gs::bucket_tile_prefix_kernel, dim3(L.B), dim3(64), 0, s, chunk_start, L.nsx, L.grid_x,
+  hipLaunchKernelGGL(gs::bucket_tile_prefix_kernel, dim3(L.B), dim3(1024), 0, s, chunk_start, L.nsx, L.grid_x,
                      L.grid_y, L.nc2_max, cnt2, tile_count);
   hipLaunchKernelGGL(gs::bucket_ranges_kernel, dim3(1), dim3(1024), 0, s, L.num_tiles, tile_count,
                      reinterpret_cast<int2*>(ranges));
