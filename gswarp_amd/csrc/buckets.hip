@@ -692,18 +692,22 @@ __global__ __launch_bounds__(64) void bucket_tile_scatter_kernel(const int4* __r
   // staged pairs [flushed, staged) in ring slots modulo kStageRing
   int staged = 0, flushed = 0;
   int* ring = s_ring + lane;
+  // Each lane reads only its half of the masks, and keeps its ring position
+  // as the byte offset of its slot row (staged << 8), so that an entry costs
+  // one bit extract, one add and one and-or for the ring address.
+  const unsigned* s_half = reinterpret_cast<const unsigned*>(s_m) + (lane >> 5);
+  const unsigned lbit = lane & 31;
+  const int lane4 = lane << 2;
+  char* ring_b = reinterpret_cast<char*>(s_ring);
+  int pos = 0;
   __syncthreads();
   for (int i0 = 0; i0 < n16; i0 += 16) {
     // 16 entries: all their LDS reads first, then the ring positions in
     // registers, then the ring writes, so no write waits on a read
-    unsigned long long mm[16];
+    unsigned h[16];
     int id[16];
 #pragma unroll
-    for (int q = 0; q < 16; q += 2) {
-      const ulonglong2 v = *reinterpret_cast<const ulonglong2*>(s_m + i0 + q);
-      mm[q] = v.x;
-      mm[q + 1] = v.y;
-    }
+    for (int q = 0; q < 16; ++q) h[q] = s_half[2 * (i0 + q)];
 #pragma unroll
     for (int q = 0; q < 16; q += 4) {
       const int4 v = *reinterpret_cast<const int4*>(s_id + i0 + q);
@@ -714,9 +718,10 @@ __global__ __launch_bounds__(64) void bucket_tile_scatter_kernel(const int4* __r
     }
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
-      ring[(staged & (kStageRing - 1)) * 64] = id[q];
-      staged += (int)mask_bit(mm[q], lane);
+      *reinterpret_cast<int*>(ring_b + ((pos & ((kStageRing - 1) << 8)) | lane4)) = id[q];
+      pos += (int)__builtin_amdgcn_ubfe(h[q], lbit, 1u) << 8;
     }
+    staged = pos >> 8;
     if (head > 0 && staged - flushed >= head) {
       for (int q = 0; q < head; ++q)
         if (out + flushed + q < R) point_list[out + flushed + q] = ring[((flushed + q) & (kStageRing - 1)) * 64];
