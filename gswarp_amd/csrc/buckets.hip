@@ -531,15 +531,59 @@ __device__ __forceinline__ void stage_chunk(int e0, int n, int lane, const unsig
   }
 }
 
+// Carry-save addition of three bit vectors: per bit, a + b + c = 2 hi + lo.
+__device__ __forceinline__ void csa(unsigned& hi, unsigned& lo, unsigned a, unsigned b, unsigned c) {
+  const unsigned u = a ^ b;
+  hi = (a & b) | (u & c);
+  lo = u ^ c;
+}
+
+// One step of the wave's bit transpose inside each 32-bit word: lane L and
+// lane L ^ S swap the bits k of L's word with (k & S) != 0 (L below its
+// partner) for the bits k - S of the partner's word, and so on mirrored.
+template <int S>
+__device__ __forceinline__ unsigned transpose_step(unsigned x, unsigned keep, unsigned rot) {
+  const unsigned p = (unsigned)__builtin_amdgcn_ds_swizzle((int)x, (S << 10) | 0x1f);  // lane ^ S
+  return (keep & x) | (~keep & __builtin_amdgcn_alignbit(p, p, rot));
+}
+
+// Transposes the 64 x 64 bit matrix whose row j is lane j's 64-bit word
+// (lo, hi): afterwards bit j of lane k's word is bit k of lane j's word.
+// Recursive block swap: halves across lanes L and L ^ 32 (one lane permute),
+// then quarters, ..., single bits inside each word (lane swizzles).
+__device__ __forceinline__ void wave_bit_transpose(unsigned& lo, unsigned& hi, int lane) {
+  const bool up = lane >= 32;
+  const unsigned recv = (unsigned)__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, (int)(up ? lo : hi));
+  if (up) lo = recv;
+  else hi = recv;
+#define GS_TRANSPOSE_STEP(S, MASK)                                   \
+  {                                                                  \
+    const bool u = (lane & (S)) != 0;                                \
+    const unsigned keep = u ? ~(unsigned)(MASK) : (unsigned)(MASK);  \
+    const unsigned rot = u ? (S) : 32 - (S);                         \
+    lo = transpose_step<S>(lo, keep, rot);                           \
+    hi = transpose_step<S>(hi, keep, rot);                           \
+  }
+  GS_TRANSPOSE_STEP(16, 0x0000ffffu)
+  GS_TRANSPOSE_STEP(8, 0x00ff00ffu)
+  GS_TRANSPOSE_STEP(4, 0x0f0f0f0fu)
+  GS_TRANSPOSE_STEP(2, 0x33333333u)
+  GS_TRANSPOSE_STEP(1, 0x55555555u)
+#undef GS_TRANSPOSE_STEP
+}
+
 // Level-2 counts: lane k of chunk g counts the chunk's entries covering tile k
-// of its super-tile into cnt2[g * 64 + k].  The chunk's masks are copied into
-// LDS (coalesced) and every lane reads them all, 16 per batch of reads.
+// of its super-tile into cnt2[g * 64 + k].  Lane j loads the masks of entries
+// j, 64 + j, ..., adds its 16 masks bit-sliced (carry-save adders: five bit
+// planes of the per-tile counts 0..16), and the wave transposes each plane,
+// so that lane k's popcounts of the planes are tile k's count.
 // chunk_info[g] = (super-tile, first entry, end entry), super-tile -1 past the
 // last chunk.
 __global__ __launch_bounds__(64) void bucket_tile_count_kernel(const int4* __restrict__ chunk_info, int E,
                                                               const unsigned long long* __restrict__ e_mask,
                                                               int* __restrict__ cnt2) {
-  __shared__ __align__(16) unsigned long long s_m[kL2Chunk];
+  constexpr int kQ = kL2Chunk / 64;
+  static_assert(kQ == 16, "sixteen masks per lane");
   const int g = blockIdx.x;
   const int lane = threadIdx.x;
   const int4 ci = chunk_info[g];
@@ -549,20 +593,47 @@ __global__ __launch_bounds__(64) void bucket_tile_count_kernel(const int4* __res
     cnt2[(size_t)g * 64 + lane] = 0;
     return;
   }
-  stage_chunk<false>(e0, n, lane, e_mask, nullptr, s_m, nullptr);
-  const int n16 = (n + 15) & ~15;
-  __syncthreads();
+  unsigned long long m[kQ];
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) m[q] = e_mask[e0 + imin(q * 64 + lane, n - 1)];
+#pragma unroll
+  for (int q = 0; q < kQ; ++q)
+    if (q * 64 + lane >= n) m[q] = 0ull;
+  unsigned plane_lo[5], plane_hi[5];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    unsigned a[kQ];
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) a[q] = h ? (unsigned)(m[q] >> 32) : (unsigned)m[q];
+    unsigned ones = 0, twos = 0, fours = 0, eights = 0, sixteens, tA, tB, fA, fB, eA, eB;
+    csa(tA, ones, ones, a[0], a[1]);
+    csa(tB, ones, ones, a[2], a[3]);
+    csa(fA, twos, twos, tA, tB);
+    csa(tA, ones, ones, a[4], a[5]);
+    csa(tB, ones, ones, a[6], a[7]);
+    csa(fB, twos, twos, tA, tB);
+    csa(eA, fours, fours, fA, fB);
+    csa(tA, ones, ones, a[8], a[9]);
+    csa(tB, ones, ones, a[10], a[11]);
+    csa(fA, twos, twos, tA, tB);
+    csa(tA, ones, ones, a[12], a[13]);
+    csa(tB, ones, ones, a[14], a[15]);
+    csa(fB, twos, twos, tA, tB);
+    csa(eB, fours, fours, fA, fB);
+    csa(sixteens, eights, eights, eA, eB);
+    unsigned* pl = h ? plane_hi : plane_lo;
+    pl[0] = ones;
+    pl[1] = twos;
+    pl[2] = fours;
+    pl[3] = eights;
+    pl[4] = sixteens;
+  }
   int count = 0;
-  for (int i0 = 0; i0 < n16; i0 += 16) {
-    unsigned long long mm[16];
 #pragma unroll
-    for (int q = 0; q < 16; q += 2) {
-      const ulonglong2 v = *reinterpret_cast<const ulonglong2*>(s_m + i0 + q);
-      mm[q] = v.x;
-      mm[q + 1] = v.y;
-    }
-#pragma unroll
-    for (int q = 0; q < 16; ++q) count += mask_bit(mm[q], lane);
+  for (int pidx = 0; pidx < 5; ++pidx) {
+    unsigned lo = plane_lo[pidx], hi = plane_hi[pidx];
+    wave_bit_transpose(lo, hi, lane);
+    count += (__popc(lo) + __popc(hi)) << pidx;
   }
   cnt2[(size_t)g * 64 + lane] = count;
 }
