@@ -497,18 +497,10 @@ __global__ __launch_bounds__(256) void bucket_table_kernel(const int* __restrict
   chunk_info[g] = make_int4(lo, e0, imin(e0 + kL2Chunk, s_ls[lo + 1]), 0);
 }
 
-// Whether tile lane (bit `lane` of the super-tile's masks) is set in m: the
-// lane's half of the mask, shifted.
-__device__ __forceinline__ unsigned mask_bit(unsigned long long m, int lane) {
-  const unsigned half = lane < 32 ? (unsigned)m : (unsigned)(m >> 32);
-  return (half >> (lane & 31)) & 1u;
-}
-
 // Copies the entries [e0, e0 + n) (1 <= n <= kL2Chunk) of a level-2 chunk
 // into LDS, zero past n up to the next multiple of 16.  Every load of the
 // lane is issued before its first LDS store (addresses clamped into the
 // chunk, no branches), so the wave waits for memory once.
-template <bool kIds>
 __device__ __forceinline__ void stage_chunk(int e0, int n, int lane, const unsigned long long* __restrict__ e_mask,
                                             const int* __restrict__ e_idx, unsigned long long* s_m, int* s_id) {
   constexpr int kQ = kL2Chunk / 64;
@@ -518,7 +510,7 @@ __device__ __forceinline__ void stage_chunk(int e0, int n, int lane, const unsig
   for (int q = 0; q < kQ; ++q) {
     const int e = e0 + imin(q * 64 + lane, n - 1);
     m[q] = e_mask[e];
-    if (kIds) id[q] = e_idx[e];
+    id[q] = e_idx[e];
   }
   const int n16 = (n + 15) & ~15;
 #pragma unroll
@@ -526,7 +518,7 @@ __device__ __forceinline__ void stage_chunk(int e0, int n, int lane, const unsig
     const int i = q * 64 + lane;
     if (i < n16) {
       s_m[i] = i < n ? m[q] : 0ull;
-      if (kIds) s_id[i] = i < n ? id[q] : 0;
+      s_id[i] = i < n ? id[q] : 0;
     }
   }
 }
@@ -757,7 +749,7 @@ __global__ __launch_bounds__(64) void bucket_tile_scatter_kernel(const int4* __r
   // the tile's list start and the chunk's offset in it, loaded with the chunk
   const int start = ranges[tile_ok ? ty * grid_x + tx : 0].x;
   const int before = cnt2[(size_t)g * 64 + lane];
-  stage_chunk<true>(e0, n, lane, e_mask, e_idx, s_m, s_id);
+  stage_chunk(e0, n, lane, e_mask, e_idx, s_m, s_id);
   const long long out = tile_ok ? (long long)start + before : 0;
   int head = (int)((kFlushPairs - (out & (kFlushPairs - 1))) & (kFlushPairs - 1));  // pairs before the next block boundary
   // staged pairs [flushed, staged) in ring slots modulo kStageRing
