@@ -245,6 +245,21 @@ __device__ __forceinline__ int table_floor(const int* t, int v) {
   return lo;
 }
 
+// Workgroups go round-robin to the eight XCDs (each with its own L2).  The
+// level-1 ranking maps workgroup b to a chunk so that runs of kXcdRun
+// consecutive chunks run on one XCD: consecutive chunks write adjacent pieces
+// of every super-tile's list, which then meet in one L2 before they are
+// written back; the runs still take turns over the XCDs, so the heavy chunks
+// at the front of the depth order are spread over all of them.  Bijective on
+// [0, n): workgroups past the last whole round of 8 runs keep their index.
+constexpr int kXcdRun = 16;
+__device__ __forceinline__ int xcd_run_chunk(int b, int n) {
+  const int full = n / (8 * kXcdRun) * (8 * kXcdRun);
+  if (b >= full) return b;
+  const int k = b >> 3;  // the k-th workgroup on XCD b & 7
+  return ((k / kXcdRun) * 8 + (b & 7)) * kXcdRun + k % kXcdRun;
+}
+
 constexpr int kL1BandCap = 1024;   // band words of a level-1 chunk held in LDS
 constexpr int kL1OwnerCap = 1024;  // entries of a level-1 chunk whose Gaussian is looked up in a table
 
@@ -278,7 +293,7 @@ __global__ __launch_bounds__(64) void bucket_scatter_kernel(int V, const int4* _
   __shared__ unsigned s_band[kL1BandCap];
   __shared__ unsigned char s_owner[kL1OwnerCap];  // Gaussian of each entry, for chunks of few entries
   const int lane = threadIdx.x;
-  const int c = blockIdx.x;
+  const int c = xcd_run_chunk(blockIdx.x, nchunks);
   const int j0 = c * kL1Chunk;
   // loads: words, indices, positions, all issued (addresses clamped, no
   // branches) before the first LDS store, so the wave waits for memory once
